@@ -1,0 +1,169 @@
+// Shared device/host helpers for the gfx950 hot-tier kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <math.h>
+
+#include "hotcold_hip.h"
+
+namespace hc {
+
+typedef _Float16 half_t;
+typedef __bf16 bf16_t;
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// ---------------------------------------------------------------------------
+// Host-side error reporting (defined in hc_runtime.hip).
+// ---------------------------------------------------------------------------
+int set_error(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int check_launch(const char* what);
+int dtype_size(int dtype);
+
+#define HC_REQUIRE(cond, ...)                                        \
+  do {                                                               \
+    if (!(cond)) return ::hc::set_error(HC_ERR_INVALID, __VA_ARGS__); \
+  } while (0)
+
+// ---------------------------------------------------------------------------
+// Element conversions.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(half_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x);
+template <>
+__device__ __forceinline__ float from_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ half_t from_f32<half_t>(float x) { return (half_t)x; }
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float x) { return (bf16_t)x; }
+
+__device__ __forceinline__ double to_f64(float x) { return (double)x; }
+__device__ __forceinline__ double to_f64(half_t x) { return (double)(float)x; }
+__device__ __forceinline__ double to_f64(bf16_t x) { return (double)(float)x; }
+
+// ---------------------------------------------------------------------------
+// Vectorised 16-byte loads/stores (global_load_dwordx4).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ u32x4 ld16(const void* p) {
+  return *reinterpret_cast<const u32x4*>(p);
+}
+__device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// Unpack n contiguous elements of T from raw 32-bit words into floats.
+template <typename T>
+struct Unpack;
+template <>
+struct Unpack<half_t> {
+  __device__ __forceinline__ static float get(const uint32_t* w, int i) {
+    uint32_t word = w[i >> 1];
+    uint16_t bits = (i & 1) ? (uint16_t)(word >> 16) : (uint16_t)(word & 0xffffu);
+    return (float)__builtin_bit_cast(half_t, bits);
+  }
+};
+template <>
+struct Unpack<bf16_t> {
+  __device__ __forceinline__ static float get(const uint32_t* w, int i) {
+    uint32_t word = w[i >> 1];
+    uint32_t bits = (i & 1) ? (word & 0xffff0000u) : (word << 16);
+    return __builtin_bit_cast(float, bits);
+  }
+};
+template <>
+struct Unpack<float> {
+  __device__ __forceinline__ static float get(const uint32_t* w, int i) {
+    return __builtin_bit_cast(float, w[i]);
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (ds_swizzle / bpermute through __shfl_xor).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
+    lo = __shfl_xor(lo, o, 64);
+    hi = __shfl_xor(hi, o, 64);
+    v += ((uint64_t)hi << 32) | lo;
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Deterministic exp for x <= 0 (the softmax numerators of the window scores).
+//
+// Cody-Waite argument reduction x = k*ln2 + r with the two-part ln2 split of
+// fdlibm (ln2_hi has 32 significant bits so k*ln2_hi is exact for |k| < 2^21),
+// then the degree-12 Taylor polynomial of exp(r) on |r| <= ln2/2 in Horner
+// form, then scaling by 2^k built from the exponent bits.  Every step is an
+// IEEE-754 binary64 fma/mul/rint, so any conforming implementation (this
+// kernel, the C restatement used for testing) produces identical bits.
+// Inputs below -708 return 0 (their fixed-point contribution is 0 anyway).
+// ---------------------------------------------------------------------------
+#define HC_LN2_HI 6.93147180369123816490e-01
+#define HC_LN2_LO 1.90821492927058770002e-10
+#define HC_INV_LN2 1.44269504088896338700e+00
+
+__device__ __forceinline__ double det_exp_nonpos(double x) {
+  if (!(x >= -708.0)) return 0.0;  // also catches -inf and NaN
+  const double kf = __builtin_rint(x * HC_INV_LN2);
+  double r = __builtin_fma(-kf, HC_LN2_HI, x);
+  r = __builtin_fma(-kf, HC_LN2_LO, r);
+  double p = 2.08767569878680989792e-09;        // 1/12!
+  p = __builtin_fma(p, r, 2.50521083854417187751e-08);   // 1/11!
+  p = __builtin_fma(p, r, 2.75573192239858906526e-07);   // 1/10!
+  p = __builtin_fma(p, r, 2.75573192239858906526e-06);   // 1/9!
+  p = __builtin_fma(p, r, 2.48015873015873015873e-05);   // 1/8!
+  p = __builtin_fma(p, r, 1.98412698412698412698e-04);   // 1/7!
+  p = __builtin_fma(p, r, 1.38888888888888888889e-03);   // 1/6!
+  p = __builtin_fma(p, r, 8.33333333333333333333e-03);   // 1/5!
+  p = __builtin_fma(p, r, 4.16666666666666666667e-02);   // 1/4!
+  p = __builtin_fma(p, r, 1.66666666666666666667e-01);   // 1/3!
+  p = __builtin_fma(p, r, 5.00000000000000000000e-01);   // 1/2!
+  p = __builtin_fma(p, r, 1.0);
+  p = __builtin_fma(p, r, 1.0);
+  const int64_t k = (int64_t)kf;  // in [-1022, 0]
+  const double scale = __builtin_bit_cast(double, (uint64_t)(k + 1023) << 52);
+  return p * scale;
+}
+
+// Fixed-point quantum of the softmax normaliser: e in [0,1] -> round(e * 2^44).
+#define HC_FIX_SHIFT 44
+__device__ __forceinline__ uint64_t det_fix(double e) {
+  const double t = __builtin_rint(e * 17592186044416.0);  // 2^44, exact scaling
+  const uint32_t hi = (uint32_t)(t * (1.0 / 4294967296.0));
+  const double lo = t - (double)hi * 4294967296.0;
+  return ((uint64_t)hi << 32) | (uint64_t)(uint32_t)lo;
+}
+
+// Total order key for fp32 scores: larger score -> larger key; -0 == +0;
+// NaN above everything (torch.topk ranks NaN highest).
+__device__ __forceinline__ uint32_t order_key(float x) {
+  if (x != x) return 0xffffffffu;
+  if (x == 0.0f) x = 0.0f;
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  return (b & 0x80000000u) ? ~b : (b | 0x80000000u);
+}
+
+__host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace hc

@@ -1,0 +1,127 @@
+// Error reporting and the stream/event/copy primitives of the inject feed.
+//
+// The staging path mirrors KVController.maybe_prefetch_to_gpu /
+// poll_staged_gpu (src/hotcold_kv/controller.py:344-442): pinned host
+// buffers are copied to the device on a non-blocking side stream, an event is
+// recorded behind the copy, the consumer polls the event (never blocks on it,
+// controller.py:401) and, once it has completed, orders its own stream after
+// the copy with hipStreamWaitEvent before the inject kernel reads the data.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "hc_common.h"
+
+namespace hc {
+
+static thread_local char g_err[1024] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(HC_ERR_HIP, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return HC_OK;
+}
+
+int dtype_size(int dtype) {
+  switch (dtype) {
+    case HC_DTYPE_F32: return 4;
+    case HC_DTYPE_F16: return 2;
+    case HC_DTYPE_BF16: return 2;
+    default: return 0;
+  }
+}
+
+static int hip_rc(hipError_t e, const char* what) {
+  if (e == hipSuccess) return HC_OK;
+  return set_error(HC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+}  // namespace hc
+
+using namespace hc;
+
+extern "C" int hc_abi_version(void) { return 1; }
+
+extern "C" const char* hc_last_error(void) { return g_err; }
+
+extern "C" int hc_stream_create(void** stream_out) {
+  HC_REQUIRE(stream_out != nullptr, "hc_stream_create: null output");
+  hipStream_t s = nullptr;
+  // Default priority on purpose: no hipStreamCreateWithPriority.
+  int rc = hip_rc(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+  if (rc != HC_OK) return rc;
+  *stream_out = reinterpret_cast<void*>(s);
+  return HC_OK;
+}
+
+extern "C" int hc_stream_destroy(void* stream) {
+  if (!stream) return HC_OK;
+  return hip_rc(hipStreamDestroy(reinterpret_cast<hipStream_t>(stream)), "hipStreamDestroy");
+}
+
+extern "C" int hc_event_create(void** event_out, int timing) {
+  HC_REQUIRE(event_out != nullptr, "hc_event_create: null output");
+  hipEvent_t e = nullptr;
+  int rc = hip_rc(hipEventCreateWithFlags(&e, timing ? hipEventDefault : hipEventDisableTiming),
+                  "hipEventCreateWithFlags");
+  if (rc != HC_OK) return rc;
+  *event_out = reinterpret_cast<void*>(e);
+  return HC_OK;
+}
+
+extern "C" int hc_event_destroy(void* event) {
+  if (!event) return HC_OK;
+  return hip_rc(hipEventDestroy(reinterpret_cast<hipEvent_t>(event)), "hipEventDestroy");
+}
+
+extern "C" int hc_event_record(void* event, void* stream) {
+  HC_REQUIRE(event != nullptr, "hc_event_record: null event");
+  return hip_rc(hipEventRecord(reinterpret_cast<hipEvent_t>(event), reinterpret_cast<hipStream_t>(stream)),
+                "hipEventRecord");
+}
+
+extern "C" int hc_event_query(void* event) {
+  HC_REQUIRE(event != nullptr, "hc_event_query: null event");
+  hipError_t e = hipEventQuery(reinterpret_cast<hipEvent_t>(event));
+  if (e == hipSuccess) return 1;
+  if (e == hipErrorNotReady) {
+    (void)hipGetLastError();  // not-ready is a status, not a sticky error
+    return 0;
+  }
+  return hip_rc(e, "hipEventQuery");
+}
+
+extern "C" int hc_event_elapsed_ms(void* start, void* end, float* ms_out) {
+  HC_REQUIRE(start && end && ms_out, "hc_event_elapsed_ms: null argument");
+  return hip_rc(hipEventElapsedTime(ms_out, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(end)),
+                "hipEventElapsedTime");
+}
+
+extern "C" int hc_stream_wait_event(void* stream, void* event) {
+  HC_REQUIRE(event != nullptr, "hc_stream_wait_event: null event");
+  return hip_rc(hipStreamWaitEvent(reinterpret_cast<hipStream_t>(stream), reinterpret_cast<hipEvent_t>(event), 0),
+                "hipStreamWaitEvent");
+}
+
+extern "C" int hc_memcpy_h2d_async(void* dst, const void* src, int64_t bytes, void* stream) {
+  HC_REQUIRE(bytes >= 0, "hc_memcpy_h2d_async: negative size");
+  if (bytes == 0) return HC_OK;
+  HC_REQUIRE(dst && src, "hc_memcpy_h2d_async: null pointer");
+  return hip_rc(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyHostToDevice, reinterpret_cast<hipStream_t>(stream)),
+                "hipMemcpyAsync(H2D)");
+}
+
+extern "C" int hc_memcpy_d2h_async(void* dst, const void* src, int64_t bytes, void* stream) {
+  HC_REQUIRE(bytes >= 0, "hc_memcpy_d2h_async: negative size");
+  if (bytes == 0) return HC_OK;
+  HC_REQUIRE(dst && src, "hc_memcpy_d2h_async: null pointer");
+  return hip_rc(hipMemcpyAsync(dst, src, (size_t)bytes, hipMemcpyDeviceToHost, reinterpret_cast<hipStream_t>(stream)),
+                "hipMemcpyAsync(D2H)");
+}

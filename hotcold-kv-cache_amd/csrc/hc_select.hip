@@ -1,0 +1,289 @@
+// Kept-index selection and row movement into the hot buffer.
+//
+// hc_topk_keep replaces keep_index (src/hotcold_kv/baselines/scoring.py:110-132)
+// and the top-k of HotColdLayer._compress_if_needed (src/hotcold_kv/cache.py:47-95).
+// One workgroup per (batch, head): an MSB-first radix select over 32-bit
+// order keys finds the threshold key T of the keep_prefix-th largest prefix
+// score, then one ordered pass emits every index with key > T plus the
+// lowest-index ties with key == T.  Emitting in index order gives the
+// ascending sort of scoring.py:130 for free, and the result is the exact
+// "value descending, ties to the lower index" set (no nth_element ambiguity).
+//
+// hc_gather_rows / hc_append_rows replace gather_kv (scoring.py:135-139),
+// the gathers of cache.py:79-84 and the torch.cat appends of cache.py:145-148
+// and layer_state.py:99-100: 16-byte vector copies of whole rows into the
+// fixed-capacity hot buffer, no re-copy of the resident cache.
+#include "hc_common.h"
+
+namespace hc {
+
+constexpr int kTopkThreads = 1024;
+constexpr int kTopkWaves = kTopkThreads / 64;
+
+// Block-wide exclusive prefix count of `flag` in thread order; returns the
+// rank and writes the block total to *total.  Uses one ballot per wave.
+__device__ __forceinline__ int block_rank(bool flag, int* sm_wave, int* total) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint64_t bal = __ballot(flag);
+  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+  const int in_wave = __popcll(bal & lt);
+  if (lane == 0) sm_wave[wave] = __popcll(bal);
+  __syncthreads();
+  int before = 0, tot = 0;
+  for (int w = 0; w < kTopkWaves; ++w) {
+    const int c = sm_wave[w];
+    if (w < wave) before += c;
+    tot += c;
+  }
+  __syncthreads();
+  *total = tot;
+  return before + in_wave;
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __restrict__ scores, int64_t s_sb,
+                                                                 int64_t s_sh, int H, int prefix, int keep_prefix,
+                                                                 int window, int64_t* __restrict__ keep,
+                                                                 int64_t* __restrict__ evicted) {
+  const int h = blockIdx.x, b = blockIdx.y;
+  const float* sc = scores + b * s_sb + h * s_sh;
+  const int n_keep = keep_prefix + window;
+  int64_t* out = keep + ((int64_t)b * H + h) * n_keep;
+  const int n_ev = prefix - keep_prefix;
+  int64_t* ev = evicted ? evicted + ((int64_t)b * H + h) * n_ev : nullptr;
+
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t sm_digit, sm_krem;
+  __shared__ int sm_wave[kTopkWaves];
+
+  uint32_t tkey = 0;
+  int need_eq = 0;
+  if (keep_prefix > 0) {
+    uint32_t pbits = 0, pmask = 0;
+    uint32_t krem = (uint32_t)keep_prefix;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      for (int i = threadIdx.x; i < 256; i += kTopkThreads) hist[i] = 0;
+      __syncthreads();
+      for (int i = threadIdx.x; i < prefix; i += kTopkThreads) {
+        const uint32_t key = order_key(sc[i]);
+        if ((key & pmask) == pbits) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (threadIdx.x == 0) {
+        uint32_t cum = 0;
+        int d = 255;
+        for (; d > 0; --d) {
+          if (cum + hist[d] >= krem) break;
+          cum += hist[d];
+        }
+        sm_digit = (uint32_t)d;
+        sm_krem = krem - cum;
+      }
+      __syncthreads();
+      pbits |= sm_digit << shift;
+      pmask |= 255u << shift;
+      krem = sm_krem;
+      __syncthreads();
+    }
+    tkey = pbits;
+    need_eq = (int)krem;
+  }
+
+  int base_sel = 0, base_eq = 0, base_ev = 0;
+  for (int t0 = 0; t0 < prefix; t0 += kTopkThreads) {
+    const int i = t0 + threadIdx.x;
+    const bool in = i < prefix;
+    uint32_t key = 0;
+    if (in && keep_prefix > 0) key = order_key(sc[i]);
+    const bool gt = in && keep_prefix > 0 && key > tkey;
+    const bool eq = in && keep_prefix > 0 && key == tkey;
+    int tot_eq;
+    const int eq_rank = base_eq + block_rank(eq, sm_wave, &tot_eq);
+    const bool sel = gt || (eq && eq_rank < need_eq);
+    int tot_sel;
+    const int pos = base_sel + block_rank(sel, sm_wave, &tot_sel);
+    if (sel) out[pos] = i;
+    int tot_ev;
+    const int epos = base_ev + block_rank(in && !sel, sm_wave, &tot_ev);
+    if (ev && in && !sel) ev[epos] = i;
+    base_sel += tot_sel;
+    base_eq += tot_eq;
+    base_ev += tot_ev;
+  }
+  for (int j = threadIdx.x; j < window; j += kTopkThreads) out[keep_prefix + j] = prefix + j;
+}
+
+// Row copy: thread copies one VW-byte vector of one row of each tensor.
+struct RowCopy {
+  const char* src[3];
+  char* dst[3];
+  int64_t s_sb[3], s_sh[3], s_ss[3];
+  int64_t d_sb[3], d_sh[3], d_ss[3];
+  int ntensor;
+  const int64_t* idx;
+  int64_t i_sb, i_sh;
+  int64_t src_rows, src_row0, dst_row0;
+  const int64_t* pos_src;
+  int64_t ps_sb;
+  int64_t* pos_dst;
+  int64_t pd_sb;
+  int B, H, n;
+  int row_bytes, elem_bytes;
+};
+
+template <int VW>
+__global__ __launch_bounds__(256) void row_copy_kernel(RowCopy c) {
+  const int vpr = c.row_bytes / VW;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t total = (int64_t)c.B * c.H * c.n * vpr;
+  if (gid >= total) return;
+  const int v = (int)(gid % vpr);
+  const int64_t row = gid / vpr;
+  const int j = (int)(row % c.n);
+  const int64_t bh = row / c.n;
+  const int h = (int)(bh % c.H);
+  const int b = (int)(bh / c.H);
+  int64_t si;
+  if (c.idx) {
+    si = c.idx[b * c.i_sb + h * c.i_sh + j];
+    if (si < 0 || si >= c.src_rows) return;
+  } else {
+    si = c.src_row0 + j;
+  }
+  const int64_t di = c.dst_row0 + j;
+  const int eb = c.elem_bytes;
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    if (t < c.ntensor && c.src[t]) {
+      const char* sp = c.src[t] + (b * c.s_sb[t] + h * c.s_sh[t] + si * c.s_ss[t]) * eb + (int64_t)v * VW;
+      char* dp = c.dst[t] + (b * c.d_sb[t] + h * c.d_sh[t] + di * c.d_ss[t]) * eb + (int64_t)v * VW;
+      if constexpr (VW == 16) {
+        st16(dp, ld16(sp));
+      } else if constexpr (VW == 8) {
+        *reinterpret_cast<uint64_t*>(dp) = *reinterpret_cast<const uint64_t*>(sp);
+      } else if constexpr (VW == 4) {
+        *reinterpret_cast<uint32_t*>(dp) = *reinterpret_cast<const uint32_t*>(sp);
+      } else {
+        *reinterpret_cast<uint16_t*>(dp) = *reinterpret_cast<const uint16_t*>(sp);
+      }
+    }
+  }
+  if (c.pos_dst && h == 0 && v == 0) c.pos_dst[b * c.pd_sb + di] = c.pos_src[b * c.ps_sb + si];
+}
+
+static int pick_vw(const RowCopy& c) {
+  for (int vw = 16; vw >= 2; vw >>= 1) {
+    if (c.row_bytes % vw) continue;
+    bool ok = true;
+    for (int t = 0; t < c.ntensor; ++t) {
+      if (!c.src[t]) continue;
+      const int64_t eb = c.elem_bytes;
+      if (((uintptr_t)c.src[t] % vw) || ((uintptr_t)c.dst[t] % vw)) ok = false;
+      if ((c.s_sb[t] * eb) % vw || (c.s_sh[t] * eb) % vw || (c.s_ss[t] * eb) % vw) ok = false;
+      if ((c.d_sb[t] * eb) % vw || (c.d_sh[t] * eb) % vw || (c.d_ss[t] * eb) % vw) ok = false;
+    }
+    if (ok) return vw;
+  }
+  return 0;
+}
+
+static int launch_row_copy(RowCopy& c, hipStream_t st, const char* what) {
+  const int vw = pick_vw(c);
+  if (vw == 0) return set_error(HC_ERR_INVALID, "%s: rows are not 2-byte aligned", what);
+  const int64_t total = (int64_t)c.B * c.H * c.n * (c.row_bytes / vw);
+  if (total == 0) return HC_OK;
+  const dim3 grid((unsigned)cdiv(total, 256));
+  switch (vw) {
+    case 16: hipLaunchKernelGGL(row_copy_kernel<16>, grid, dim3(256), 0, st, c); break;
+    case 8: hipLaunchKernelGGL(row_copy_kernel<8>, grid, dim3(256), 0, st, c); break;
+    case 4: hipLaunchKernelGGL(row_copy_kernel<4>, grid, dim3(256), 0, st, c); break;
+    default: hipLaunchKernelGGL(row_copy_kernel<2>, grid, dim3(256), 0, st, c); break;
+  }
+  return check_launch(what);
+}
+
+}  // namespace hc
+
+using namespace hc;
+
+extern "C" int hc_topk_keep(int64_t B, int64_t H, int64_t S, const float* scores, int64_t s_sb, int64_t s_sh,
+                            int64_t window, int64_t budget, int64_t* keep, int64_t* evicted, void* stream) {
+  HC_REQUIRE(B > 0 && H > 0 && S > 0, "topk: empty shape");
+  HC_REQUIRE(window >= 0 && budget >= 0, "topk: negative window/budget");
+  HC_REQUIRE(S < ((int64_t)1 << 31), "topk: S too large");
+  HC_REQUIRE(B <= 65535 && H <= 65535, "topk: grid too large");
+  HC_REQUIRE(scores && keep, "topk: null pointer");
+  const int64_t win = window < S ? window : S;
+  const int64_t prefix = S - win;
+  int64_t kp = budget - win;
+  if (kp > prefix) kp = prefix;
+  if (kp < 0) kp = 0;
+  hipLaunchKernelGGL(topk_keep_kernel, dim3((unsigned)H, (unsigned)B), dim3(kTopkThreads), 0,
+                     reinterpret_cast<hipStream_t>(stream), scores, s_sb, s_sh, (int)H, (int)prefix, (int)kp,
+                     (int)win, keep, evicted);
+  return check_launch("topk_keep");
+}
+
+extern "C" int hc_gather_rows(int64_t B, int64_t H, int64_t n, int64_t D, int64_t elem_bytes, const int64_t* idx,
+                              int64_t i_sb, int64_t i_sh, int64_t src_rows, int64_t dst_row0, const void* src1,
+                              int64_t s1_sb, int64_t s1_sh, int64_t s1_ss, void* dst1, int64_t d1_sb, int64_t d1_sh,
+                              int64_t d1_ss, const void* src2, int64_t s2_sb, int64_t s2_sh, int64_t s2_ss,
+                              void* dst2, int64_t d2_sb, int64_t d2_sh, int64_t d2_ss, const void* src3,
+                              int64_t s3_sb, int64_t s3_sh, int64_t s3_ss, void* dst3, int64_t d3_sb, int64_t d3_sh,
+                              int64_t d3_ss, const int64_t* pos_src, int64_t ps_sb, int64_t* pos_dst, int64_t pd_sb,
+                              void* stream) {
+  HC_REQUIRE(B > 0 && H > 0 && n >= 0 && D > 0, "gather: bad shape");
+  HC_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8, "gather: bad elem_bytes");
+  HC_REQUIRE(idx != nullptr, "gather: null index");
+  HC_REQUIRE(src1 && dst1, "gather: first tensor required");
+  HC_REQUIRE((src2 == nullptr) == (dst2 == nullptr) && (src3 == nullptr) == (dst3 == nullptr),
+             "gather: src/dst pairs must both be set");
+  HC_REQUIRE((pos_src == nullptr) == (pos_dst == nullptr), "gather: pos_src/pos_dst must both be set");
+  HC_REQUIRE(D * elem_bytes % 2 == 0, "gather: odd row size");
+  if (n == 0) return HC_OK;
+  RowCopy c{};
+  c.src[0] = (const char*)src1; c.dst[0] = (char*)dst1;
+  c.src[1] = (const char*)src2; c.dst[1] = (char*)dst2;
+  c.src[2] = (const char*)src3; c.dst[2] = (char*)dst3;
+  c.s_sb[0] = s1_sb; c.s_sh[0] = s1_sh; c.s_ss[0] = s1_ss; c.d_sb[0] = d1_sb; c.d_sh[0] = d1_sh; c.d_ss[0] = d1_ss;
+  c.s_sb[1] = s2_sb; c.s_sh[1] = s2_sh; c.s_ss[1] = s2_ss; c.d_sb[1] = d2_sb; c.d_sh[1] = d2_sh; c.d_ss[1] = d2_ss;
+  c.s_sb[2] = s3_sb; c.s_sh[2] = s3_sh; c.s_ss[2] = s3_ss; c.d_sb[2] = d3_sb; c.d_sh[2] = d3_sh; c.d_ss[2] = d3_ss;
+  c.ntensor = 3;
+  c.idx = idx; c.i_sb = i_sb; c.i_sh = i_sh;
+  c.src_rows = src_rows; c.src_row0 = 0; c.dst_row0 = dst_row0;
+  c.pos_src = pos_src; c.ps_sb = ps_sb; c.pos_dst = pos_dst; c.pd_sb = pd_sb;
+  c.B = (int)B; c.H = (int)H; c.n = (int)n;
+  c.row_bytes = (int)(D * elem_bytes);
+  c.elem_bytes = (int)elem_bytes;
+  return launch_row_copy(c, reinterpret_cast<hipStream_t>(stream), "gather_rows");
+}
+
+extern "C" int hc_append_rows(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t row, const void* k_src,
+                              int64_t ks_sb, int64_t ks_sh, int64_t ks_ss, void* k_dst, int64_t kd_sb, int64_t kd_sh,
+                              int64_t kd_ss, const void* v_src, int64_t vs_sb, int64_t vs_sh, int64_t vs_ss,
+                              void* v_dst, int64_t vd_sb, int64_t vd_sh, int64_t vd_ss, const void* p_src,
+                              int64_t ps_sb, int64_t ps_sh, int64_t ps_ss, void* p_dst, int64_t pd_sb, int64_t pd_sh,
+                              int64_t pd_ss, const int64_t* pos_src, int64_t pos_s_sb, int64_t* pos_dst,
+                              int64_t pos_d_sb, void* stream) {
+  const int es = dtype_size(dtype);
+  HC_REQUIRE(es > 0, "append: bad dtype %d", dtype);
+  HC_REQUIRE(B > 0 && H > 0 && T >= 0 && D > 0 && row >= 0, "append: bad shape");
+  HC_REQUIRE(k_src && k_dst, "append: key tensors required");
+  HC_REQUIRE((v_src == nullptr) == (v_dst == nullptr) && (p_src == nullptr) == (p_dst == nullptr),
+             "append: src/dst pairs must both be set");
+  HC_REQUIRE((pos_src == nullptr) == (pos_dst == nullptr), "append: pos_src/pos_dst must both be set");
+  if (T == 0) return HC_OK;
+  RowCopy c{};
+  c.src[0] = (const char*)k_src; c.dst[0] = (char*)k_dst;
+  c.src[1] = (const char*)v_src; c.dst[1] = (char*)v_dst;
+  c.src[2] = (const char*)p_src; c.dst[2] = (char*)p_dst;
+  c.s_sb[0] = ks_sb; c.s_sh[0] = ks_sh; c.s_ss[0] = ks_ss; c.d_sb[0] = kd_sb; c.d_sh[0] = kd_sh; c.d_ss[0] = kd_ss;
+  c.s_sb[1] = vs_sb; c.s_sh[1] = vs_sh; c.s_ss[1] = vs_ss; c.d_sb[1] = vd_sb; c.d_sh[1] = vd_sh; c.d_ss[1] = vd_ss;
+  c.s_sb[2] = ps_sb; c.s_sh[2] = ps_sh; c.s_ss[2] = ps_ss; c.d_sb[2] = pd_sb; c.d_sh[2] = pd_sh; c.d_ss[2] = pd_ss;
+  c.ntensor = 3;
+  c.idx = nullptr; c.src_rows = T; c.src_row0 = 0; c.dst_row0 = row;
+  c.pos_src = pos_src; c.ps_sb = pos_s_sb; c.pos_dst = pos_dst; c.pd_sb = pos_d_sb;
+  c.B = (int)B; c.H = (int)H; c.n = (int)T;
+  c.row_bytes = (int)(D * es);
+  c.elem_bytes = es;
+  return launch_row_copy(c, reinterpret_cast<hipStream_t>(stream), "append_rows");
+}

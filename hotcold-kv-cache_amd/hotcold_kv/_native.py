@@ -1,0 +1,155 @@
+"""Loader for the gfx950 hot-tier library (libhotcold_hip.so, C ABI in
+include/hotcold_hip.h).
+
+The library is the only compute path of this package: if it is missing or the
+tensors are not on a ROCm device, the ops raise instead of falling back to
+another implementation.
+"""
+
+import ctypes
+import os
+import threading
+
+import torch  # noqa: F401  (loads the HIP runtime the library binds to)
+
+_LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libhotcold_hip.so")
+_lock = threading.Lock()
+_lib = None
+
+HC_OK = 0
+HC_ERR_INVALID = -1
+HC_ERR_HIP = -2
+HC_ERR_UNSUPPORTED = -3
+HC_ERR_WORKSPACE = -4
+HC_ERR_GROUP = -5
+HC_ERR_DROPOUT = -6
+
+HC_DTYPE_F32 = 0
+HC_DTYPE_F16 = 1
+HC_DTYPE_BF16 = 2
+
+HC_POOL_MAX = 0
+HC_POOL_AVG = 1
+
+HC_SCORE_SNAPKV = 0
+HC_SCORE_RAWSUM = 1
+
+_i64 = ctypes.c_int64
+_int = ctypes.c_int
+_vp = ctypes.c_void_p
+_dbl = ctypes.c_double
+
+# name -> (restype, argtypes)
+SIGNATURES = {
+    "hc_abi_version": (_int, []),
+    "hc_last_error": (ctypes.c_char_p, []),
+    "hc_decode_attn_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _int]),
+    "hc_decode_attn": (_int, [
+        _int, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64,
+        _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp,
+        _dbl, _dbl,
+        _vp, _i64, _i64,
+        _vp, _vp,
+        _vp, _i64, _i64,
+        _vp]),
+    "hc_snapkv_score_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "hc_snapkv_score": (_int, [
+        _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _dbl, _i64, _int,
+        _vp,
+        _vp, _i64, _vp]),
+    "hc_head_mean": (_int, [_i64, _i64, _i64, _vp, _vp, _vp]),
+    "hc_topk_keep": (_int, [_i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "hc_gather_rows": (_int, [
+        _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+        _vp, _i64, _vp, _i64,
+        _vp]),
+    "hc_append_rows": (_int, [
+        _int, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
+        _vp, _i64, _vp, _i64,
+        _vp]),
+    "hc_inject_rerope": (_int, [
+        _int, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _dbl,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp]),
+    "hc_stream_create": (_int, [ctypes.POINTER(_vp)]),
+    "hc_stream_destroy": (_int, [_vp]),
+    "hc_event_create": (_int, [ctypes.POINTER(_vp), _int]),
+    "hc_event_destroy": (_int, [_vp]),
+    "hc_event_record": (_int, [_vp, _vp]),
+    "hc_event_query": (_int, [_vp]),
+    "hc_event_elapsed_ms": (_int, [_vp, _vp, ctypes.POINTER(ctypes.c_float)]),
+    "hc_stream_wait_event": (_int, [_vp, _vp]),
+    "hc_memcpy_h2d_async": (_int, [_vp, _vp, _i64, _vp]),
+    "hc_memcpy_d2h_async": (_int, [_vp, _vp, _i64, _vp]),
+}
+
+
+def library_path():
+    return _LIB_PATH
+
+
+def lib():
+    """Return the loaded library, loading it on first use; raise if absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not os.path.exists(_LIB_PATH):
+            raise RuntimeError(
+                f"hotcold_kv: native library not built ({_LIB_PATH}); "
+                "run `python hotcold-kv-cache_amd/build_native.py`")
+        handle = ctypes.CDLL(_LIB_PATH, mode=ctypes.RTLD_GLOBAL)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(handle, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = handle
+    return _lib
+
+
+class HotColdError(RuntimeError):
+    pass
+
+
+def check(rc, what):
+    """Map a C-ABI status to the reference's exception types."""
+    if rc == HC_OK:
+        return
+    msg = lib().hc_last_error().decode(errors="replace")
+    if rc in (HC_ERR_GROUP, HC_ERR_DROPOUT):
+        raise ValueError(msg)
+    raise HotColdError(f"{what}: {msg} (status {rc})")
+
+
+def dtype_code(dtype):
+    if dtype == torch.float16:
+        return HC_DTYPE_F16
+    if dtype == torch.bfloat16:
+        return HC_DTYPE_BF16
+    if dtype == torch.float32:
+        return HC_DTYPE_F32
+    raise TypeError(f"hotcold_kv: unsupported dtype {dtype}")

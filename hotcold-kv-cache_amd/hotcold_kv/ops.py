@@ -1,0 +1,388 @@
+"""Torch-tensor front end of the gfx950 hot-tier kernels.
+
+Every function here launches HIP kernels from libhotcold_hip.so on the current
+torch stream of the tensors' device.  Tensors must live on a ROCm device;
+there is no CPU path.  Workspaces are cached per (device, stream) and grown on
+demand; torch's caching allocator owns all memory.
+"""
+
+import math
+import threading
+
+import torch
+
+from . import _native as N
+
+_ws_lock = threading.Lock()
+_ws_cache = {}
+
+
+def _require_device(*tensors):
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise RuntimeError(
+                "hotcold_kv: the hot-tier kernels run on ROCm device tensors only "
+                f"(got a tensor on {t.device})")
+
+
+def _stream_handle(device):
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t):
+    return None if t is None else t.data_ptr()
+
+
+def _workspace(kind, device, nbytes):
+    """A zero-initialised uint8 workspace of at least nbytes for this stream."""
+    key = (kind, device.index if device.index is not None else torch.cuda.current_device(),
+           _stream_handle(device))
+    with _ws_lock:
+        ws = _ws_cache.get(key)
+        if ws is None or ws.numel() < nbytes:
+            size = max(nbytes, 256)
+            if ws is not None:
+                size = max(size, int(ws.numel() * 1.5))
+            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            _ws_cache[key] = ws
+        return ws
+
+
+def _rows4(x, name):
+    if x.dim() != 4:
+        raise RuntimeError(f"{name} must be 4D (B,H,S,D); got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    return x
+
+
+# ---------------------------------------------------------------------------
+# Decode attention
+# ---------------------------------------------------------------------------
+def decode_attention(q, k, v, scaling, mask=None, held_len=0, held_pos=None, held_valid=None,
+                     cur_pos=None, out=None, num_splits=0, with_evict=False, dropout=0.0):
+    """Single-token GQA attention of q (B,Hq,D) or (B,Hq,1,D) over k/v (B,Hk,S,D).
+
+    mask: optional (B,S) bool/uint8, True = attend.  held_len > 0 additionally
+    masks the first held_len rows with held_valid & (held_pos <= cur_pos);
+    held_pos/held_valid are (B,R) or (B,Hk,R), cur_pos a 1-element int64 device
+    tensor (or None).  Returns out (B,Hq,D) in q's dtype, plus
+    (evict_loss (B,S) float32, evict_idx (B,) int64) when with_evict.
+    """
+    _require_device(q, k, v, mask, held_pos, held_valid, cur_pos)
+    lib = N.lib()
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise RuntimeError(f"decode_attention: expected one query token, got q {tuple(q.shape)}")
+        q3 = q[:, :, 0, :]
+    else:
+        q3 = q
+    if q3.stride(-1) != 1:
+        q3 = q3.contiguous()
+    k = _rows4(k, "key")
+    v = _rows4(v, "value")
+    B, Hq, D = q3.shape
+    Bk, Hk, S, Dk = k.shape
+    if Bk != B or Dk != D or tuple(v.shape) != tuple(k.shape):
+        raise RuntimeError(f"decode_attention: shape mismatch q {tuple(q3.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
+    if k.dtype != q3.dtype or v.dtype != q3.dtype:
+        raise RuntimeError("decode_attention: q, k, v must share a dtype")
+    if mask is not None:
+        if mask.dim() != 2 or mask.shape[0] != B or mask.shape[1] != S:
+            raise RuntimeError(f"decode_attention: mask must be (B,S)=({B},{S}); got {tuple(mask.shape)}")
+        if mask.dtype == torch.bool:
+            mask = mask.view(torch.uint8) if mask.is_contiguous() else mask.contiguous().view(torch.uint8)
+        elif mask.dtype != torch.uint8:
+            mask = (mask != 0).to(torch.uint8)
+        if mask.stride(1) != 1:
+            mask = mask.contiguous()
+    hp_sb = hp_sh = hv_sb = hv_sh = 0
+    if held_len:
+        if held_pos is None or held_valid is None:
+            raise RuntimeError("decode_attention: held_len needs held_pos and held_valid")
+        if held_valid.dtype == torch.bool:
+            held_valid = held_valid.contiguous().view(torch.uint8)
+        held_pos = held_pos.contiguous()
+        held_valid = held_valid.contiguous()
+        for t, name in ((held_pos, "held_pos"), (held_valid, "held_valid")):
+            if t.dim() not in (2, 3) or t.shape[0] != B or t.shape[-1] < held_len or held_len > S \
+                    or (t.dim() == 3 and t.shape[1] != Hk):
+                raise RuntimeError(f"decode_attention: {name} {tuple(t.shape)} does not cover {held_len} "
+                                   f"held rows of (B,Hk)=({B},{Hk})")
+        if held_pos.dtype != torch.int64:
+            raise RuntimeError("decode_attention: held_pos must be int64")
+    if cur_pos is not None and (cur_pos.dtype != torch.int64 or cur_pos.numel() < 1):
+        raise RuntimeError("decode_attention: cur_pos must be a non-empty int64 tensor")
+    if held_len:
+        if held_pos.dim() == 2:
+            hp_sb, hp_sh = held_pos.stride(0), 0
+        else:
+            hp_sb, hp_sh = held_pos.stride(0), held_pos.stride(1)
+        if held_valid.dim() == 2:
+            hv_sb, hv_sh = held_valid.stride(0), 0
+        else:
+            hv_sb, hv_sh = held_valid.stride(0), held_valid.stride(1)
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=q3.dtype, device=q3.device)
+    if out.stride(-1) != 1:
+        raise RuntimeError("decode_attention: out must have a unit last stride")
+    ev_loss = ev_idx = None
+    if with_evict:
+        ev_loss = torch.empty((B, S), dtype=torch.float32, device=q3.device)
+        ev_idx = torch.empty((B,), dtype=torch.int64, device=q3.device)
+    nbytes = lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, int(with_evict))
+    ws = _workspace("decode", q3.device, nbytes)
+    rc = lib.hc_decode_attn(
+        N.dtype_code(q3.dtype), B, Hq, Hk, D, S,
+        _ptr(q3), q3.stride(0), q3.stride(1),
+        _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        _ptr(mask), mask.stride(0) if mask is not None else 0,
+        int(held_len),
+        _ptr(held_pos), hp_sb, hp_sh,
+        _ptr(held_valid), hv_sb, hv_sh,
+        _ptr(cur_pos),
+        float(scaling), float(dropout),
+        _ptr(out), out.stride(0), out.stride(1),
+        _ptr(ev_loss), _ptr(ev_idx),
+        _ptr(ws), ws.numel(), int(num_splits),
+        _stream_handle(q3.device))
+    N.check(rc, "hc_decode_attn")
+    if with_evict:
+        return out, ev_loss, ev_idx
+    return out
+
+
+# ---------------------------------------------------------------------------
+# SnapKV compaction
+# ---------------------------------------------------------------------------
+def snapkv_scores(q_post, keys, window_size, scaling, kernel_size=7, pooling="maxpool",
+                  mode="snapkv", q_rows=None):
+    """Per-KV-head importance (B,Hk,S) float32.
+
+    mode "snapkv": scoring.py:50-79 (window = last min(window_size,S) rows of
+    q_post, causal mask, softmax, window sum, pooling).  mode "rawsum":
+    cache.py:55-69 before the head mean (q_post holds the stashed queries; the
+    last `window_size` of its rows are used; no mask, no softmax, no pooling).
+    """
+    _require_device(q_post, keys)
+    lib = N.lib()
+    keys = _rows4(keys, "keys")
+    if q_post.dim() != 4:
+        raise RuntimeError(f"q_post must be 4D (B,Hq,T,D); got {tuple(q_post.shape)}")
+    if q_post.stride(-1) != 1:
+        q_post = q_post.contiguous()
+    B, Hq, T, D = q_post.shape
+    _, Hk, S, _ = keys.shape
+    if keys.dtype != q_post.dtype:
+        raise RuntimeError("snapkv_scores: q and keys must share a dtype")
+    if mode == "snapkv":
+        W = min(int(window_size), S)
+        if T != S:
+            raise RuntimeError("snapkv_scores: q_post must cover the whole prompt (T == S)")
+        q_row0 = S - W
+        mcode = N.HC_SCORE_SNAPKV
+    elif mode == "rawsum":
+        W = min(int(window_size), T)
+        q_row0 = T - W
+        mcode = N.HC_SCORE_RAWSUM
+        kernel_size = 1
+    else:
+        raise ValueError(f"unknown score mode {mode}")
+    if kernel_size is None:
+        kernel_size = 1
+    pool = N.HC_POOL_AVG if pooling == "avgpool" else N.HC_POOL_MAX
+    scores = torch.empty((B, Hk, S), dtype=torch.float32, device=keys.device)
+    nbytes = lib.hc_snapkv_score_workspace_size(B, Hk, S, D, W)
+    ws = _workspace("score", keys.device, nbytes)
+    rc = lib.hc_snapkv_score(
+        N.dtype_code(keys.dtype), mcode, B, Hq, Hk, S, D, W,
+        _ptr(q_post), q_post.stride(0), q_post.stride(1), q_post.stride(2), q_row0,
+        _ptr(keys), keys.stride(0), keys.stride(1), keys.stride(2),
+        float(scaling), int(kernel_size), pool,
+        _ptr(scores), _ptr(ws), ws.numel(), _stream_handle(keys.device))
+    N.check(rc, "hc_snapkv_score")
+    return scores
+
+
+def head_mean(scores):
+    """(B,H,S) float32 -> (B,S): mean over heads in fp64, rounded to fp32."""
+    _require_device(scores)
+    scores = scores.contiguous()
+    B, H, S = scores.shape
+    out = torch.empty((B, S), dtype=torch.float32, device=scores.device)
+    N.check(N.lib().hc_head_mean(B, H, S, _ptr(scores), _ptr(out), _stream_handle(scores.device)), "hc_head_mean")
+    return out
+
+
+def keep_counts(S, window_size, budget):
+    window = min(int(window_size), int(S))
+    prefix = int(S) - window
+    keep_prefix = max(0, min(int(budget) - window, prefix))
+    return window, prefix, keep_prefix
+
+
+def keep_index(scores, window_size, budget, return_evicted=False):
+    """scoring.py:110-132 on the device: (B,H,S) float32 -> (B,H,keep) int64.
+
+    Top keep_prefix prefix positions by (score desc, index asc), ascending,
+    then the recent window.  With return_evicted also the ascending prefix
+    positions not kept, (B,H,prefix-keep_prefix).
+    """
+    _require_device(scores)
+    squeeze = False
+    if scores.dim() == 2:
+        scores = scores.unsqueeze(1)
+        squeeze = True
+    if scores.dtype != torch.float32:
+        scores = scores.float()
+    if scores.stride(-1) != 1:
+        scores = scores.contiguous()
+    B, H, S = scores.shape
+    window, prefix, kp = keep_counts(S, window_size, budget)
+    keep = torch.empty((B, H, kp + window), dtype=torch.int64, device=scores.device)
+    ev = torch.empty((B, H, prefix - kp), dtype=torch.int64, device=scores.device) if return_evicted else None
+    rc = N.lib().hc_topk_keep(B, H, S, _ptr(scores), scores.stride(0), scores.stride(1), int(window_size),
+                              int(budget), _ptr(keep), _ptr(ev), _stream_handle(scores.device))
+    N.check(rc, "hc_topk_keep")
+    if squeeze:
+        keep = keep[:, 0]
+        ev = ev[:, 0] if ev is not None else None
+    return (keep, ev) if return_evicted else keep
+
+
+def _strides3(t):
+    """(sb, sh, ss) element strides of a (B,H,S,D) tensor."""
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def gather_rows(idx, pairs, dst_row0=0, pos_src=None, pos_dst=None, src_rows=None):
+    """dst[b,h,dst_row0+j] = src[b,h,idx[b,h,j]] for up to three (src, dst) pairs.
+
+    idx is (B,H,n) or (B,n) (one set shared by all heads).  pos_src (B,S) and
+    pos_dst (B,*) gather int64 positions with the head-0 index set.
+    """
+    if not 1 <= len(pairs) <= 3:
+        raise ValueError("gather_rows takes one to three (src, dst) pairs")
+    src0, dst0 = pairs[0]
+    _require_device(idx, src0, dst0, pos_src, pos_dst)
+    B, H, S, D = src0.shape
+    if idx.dim() == 2:
+        i_sb, i_sh, n = idx.stride(0), 0, idx.shape[1]
+    else:
+        i_sb, i_sh, n = idx.stride(0), idx.stride(1), idx.shape[2]
+    if idx.stride(-1) != 1:
+        idx = idx.contiguous()
+        return gather_rows(idx, pairs, dst_row0, pos_src, pos_dst, src_rows)
+    es = src0.element_size()
+    args = []
+    for i in range(3):
+        if i < len(pairs):
+            s, d = pairs[i]
+            if s.dtype != src0.dtype or d.dtype != src0.dtype:
+                raise RuntimeError("gather_rows: all tensors must share a dtype")
+            if s.dim() != 4 or d.dim() != 4 or s.shape[0] != B or d.shape[0] != B or s.shape[1] != H \
+                    or d.shape[1] != H or s.shape[3] != D or d.shape[3] != D or s.shape[2] < S:
+                raise RuntimeError(f"gather_rows: shape mismatch src {tuple(s.shape)} dst {tuple(d.shape)}")
+            if d.shape[2] < dst_row0 + n:
+                raise RuntimeError(f"gather_rows: destination holds {d.shape[2]} rows, needs {dst_row0 + n}")
+            if s.stride(-1) != 1 or d.stride(-1) != 1:
+                raise RuntimeError("gather_rows: rows must be contiguous")
+            args += [_ptr(s), *_strides3(s), _ptr(d), *_strides3(d)]
+        else:
+            args += [None, 0, 0, 0, None, 0, 0, 0]
+    if idx.shape[0] != B or (idx.dim() == 3 and idx.shape[1] != H):
+        raise RuntimeError(f"gather_rows: index shape {tuple(idx.shape)} does not match (B,H)=({B},{H})")
+    if pos_src is not None:
+        if pos_src.dim() != 2 or pos_src.shape[0] != B or pos_src.shape[1] < S or pos_dst.dim() != 2 \
+                or pos_dst.shape[0] != B or pos_dst.shape[1] < dst_row0 + n or pos_src.stride(1) != 1 \
+                or pos_dst.stride(1) != 1:
+            raise RuntimeError("gather_rows: bad position tensors")
+    rc = N.lib().hc_gather_rows(
+        B, H, n, D, es, _ptr(idx), i_sb, i_sh, int(src_rows if src_rows is not None else S), int(dst_row0),
+        *args,
+        _ptr(pos_src), pos_src.stride(0) if pos_src is not None else 0,
+        _ptr(pos_dst), pos_dst.stride(0) if pos_dst is not None else 0,
+        _stream_handle(src0.device))
+    N.check(rc, "hc_gather_rows")
+
+
+def gather_kv(t, keep):
+    """scoring.py:135-139: gather (B,H,S,D) along S with per-head keep (B,H,k)."""
+    B, H, S, D = t.shape
+    n = keep.shape[-1]
+    out = torch.empty((B, H, n, D), dtype=t.dtype, device=t.device)
+    gather_rows(keep, [(t, out)])
+    return out
+
+
+def append_rows(row, k_src, k_dst, v_src=None, v_dst=None, p_src=None, p_dst=None, pos_src=None, pos_dst=None):
+    """Write T new rows (B,H,T,D) at row `row` of the hot buffers."""
+    _require_device(k_src, k_dst, v_src, v_dst, p_src, p_dst, pos_src, pos_dst)
+    B, H, T, D = k_src.shape
+    args = []
+    for s, d in ((k_src, k_dst), (v_src, v_dst), (p_src, p_dst)):
+        if s is None:
+            args += [None, 0, 0, 0, None, 0, 0, 0]
+        else:
+            if tuple(s.shape) != (B, H, T, D) or d.dim() != 4 or tuple(d.shape[:2]) != (B, H) \
+                    or d.shape[3] != D or d.shape[2] < row + T or d.dtype != s.dtype or d.stride(-1) != 1:
+                raise RuntimeError(f"append_rows: bad shapes src {tuple(s.shape)} dst {tuple(d.shape)} row {row}")
+            if s.stride(-1) != 1:
+                s = s.contiguous()
+            args += [_ptr(s), *_strides3(s), _ptr(d), *_strides3(d)]
+    if pos_src is not None:
+        if pos_src.stride(-1) != 1:
+            pos_src = pos_src.contiguous()
+        if pos_src.shape != (B, T) or pos_dst.dim() != 2 or pos_dst.shape[0] != B \
+                or pos_dst.shape[1] < row + T or pos_dst.stride(1) != 1:
+            raise RuntimeError("append_rows: bad position tensors")
+    rc = N.lib().hc_append_rows(
+        N.dtype_code(k_src.dtype), B, H, T, D, int(row), *args,
+        _ptr(pos_src), pos_src.stride(0) if pos_src is not None else 0,
+        _ptr(pos_dst), pos_dst.stride(0) if pos_dst is not None else 0,
+        _stream_handle(k_src.device))
+    N.check(rc, "hc_append_rows")
+
+
+def inject_rerope(k_pre_f32, v_f32, pos, inv_freq, attention_scaling, k_dst, v_dst):
+    """Re-RoPE staged fp32 pre-RoPE keys (B,Hk,R,D) to positions pos (B,R) or
+    (B,Hk,R) and write them with their values into rows 0..R-1 of k_dst/v_dst
+    (B,Hk,cap,D) in the cache dtype."""
+    _require_device(k_pre_f32, v_f32, pos, inv_freq, k_dst, v_dst)
+    B, Hk, R, D = k_pre_f32.shape
+    if k_pre_f32.dtype != torch.float32 or v_f32.dtype != torch.float32:
+        raise RuntimeError("inject_rerope: staged k_pre/v must be float32")
+    if pos.dtype != torch.int64:
+        raise RuntimeError("inject_rerope: positions must be int64")
+    if inv_freq.dtype != torch.float32 or inv_freq.numel() != D // 2:
+        raise RuntimeError("inject_rerope: inv_freq must be float32 of length D/2")
+    inv_freq = inv_freq.contiguous()
+    for d, name in ((k_dst, "k_dst"), (v_dst, "v_dst")):
+        if d.dim() != 4 or d.shape[0] != B or d.shape[1] != Hk or d.shape[2] < R or d.shape[3] != D \
+                or d.stride(-1) != 1:
+            raise RuntimeError(f"inject_rerope: {name} {tuple(d.shape)} cannot hold {R} rows of ({B},{Hk},*,{D})")
+    if tuple(v_f32.shape) != (B, Hk, R, D) or k_pre_f32.stride(-1) != 1 or v_f32.stride(-1) != 1:
+        raise RuntimeError("inject_rerope: staged k_pre/v must be (B,Hk,R,D) with unit last stride")
+    if not ((pos.dim() == 2 and tuple(pos.shape) == (B, R)) or (pos.dim() == 3 and tuple(pos.shape) == (B, Hk, R))):
+        raise RuntimeError(f"inject_rerope: positions {tuple(pos.shape)} must be (B,R) or (B,Hk,R)")
+    if pos.stride(-1) != 1:
+        pos = pos.contiguous()
+    if pos.dim() == 2:
+        pos_sb, pos_sh = pos.stride(0), 0
+    else:
+        pos_sb, pos_sh = pos.stride(0), pos.stride(1)
+    rc = N.lib().hc_inject_rerope(
+        N.dtype_code(k_dst.dtype), B, Hk, R, D,
+        _ptr(k_pre_f32), *_strides3(k_pre_f32),
+        _ptr(v_f32), *_strides3(v_f32),
+        _ptr(pos), pos_sb, pos_sh,
+        _ptr(inv_freq), float(attention_scaling),
+        _ptr(k_dst), *_strides3(k_dst),
+        _ptr(v_dst), *_strides3(v_dst),
+        _stream_handle(k_dst.device))
+    N.check(rc, "hc_inject_rerope")
+
+
+def default_scaling(head_dim):
+    return 1.0 / math.sqrt(head_dim)

@@ -1,0 +1,210 @@
+/*
+ * hotcold_hip.h -- C ABI of the MI355X (gfx950) hot tier of hotcold-kv-cache.
+ *
+ * Every entry point takes plain device pointers, int64 sizes and element
+ * strides, a dtype code and a hipStream_t (passed as void*), and returns an
+ * int status: HC_OK (0) or a negative HC_ERR_* code.  hc_last_error() returns
+ * a message for the last failure on the calling thread.  Nothing here
+ * allocates device memory: scratch space is a caller-owned workspace whose
+ * size the matching *_workspace_size() function reports.
+ *
+ * Strides are in ELEMENTS of the tensor they describe.  The innermost (head
+ * dimension) stride is always 1.  A stride of 0 broadcasts (for example one
+ * index set shared by every KV head).
+ *
+ * Citations name the reference interface (tarun931/hotcold-kv-cache,
+ * src/hotcold_kv/...) each entry point replaces.
+ */
+#ifndef HOTCOLD_HIP_H
+#define HOTCOLD_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define HC_OK 0
+#define HC_ERR_INVALID (-1)     /* bad argument (shape, stride, dtype, size) */
+#define HC_ERR_HIP (-2)         /* a HIP runtime call failed */
+#define HC_ERR_UNSUPPORTED (-3) /* valid but unsupported configuration */
+#define HC_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+#define HC_ERR_GROUP (-5)       /* Hq / n_rep != Hk (kernels.py:99-100) */
+#define HC_ERR_DROPOUT (-6)     /* dropout != 0 (kernels.py:88-89) */
+
+#define HC_DTYPE_F32 0
+#define HC_DTYPE_F16 1
+#define HC_DTYPE_BF16 2
+
+#define HC_POOL_MAX 0 /* F.max_pool1d, scoring.py:47 */
+#define HC_POOL_AVG 1 /* F.avg_pool1d(count_include_pad=True), scoring.py:45-46 */
+
+/* Score modes for hc_snapkv_score. */
+#define HC_SCORE_SNAPKV 0 /* causal-masked softmax over keys, summed over the window (scoring.py:50-79) */
+#define HC_SCORE_RAWSUM 1 /* raw q.k / sqrt(D) summed over the window, no mask (cache.py:68-69) */
+
+/* Library identity and errors. */
+int hc_abi_version(void);
+const char* hc_last_error(void);
+
+/*
+ * GQA decode attention over the hot buffer (+ held retrieved slot), split-K.
+ * Replaces evict_fwd_kernel + triton_evict_attention_forward
+ * (kernels.py:9-74, 77-137) and the call site at patch.py:295-305.
+ *
+ *   q    [B][Hq][D]       q[b*q_sb + h*q_sh + d]
+ *   k, v [B][Hk][S][D]    k[b*k_sb + h*k_sh + s*k_ss + d]
+ *   mask [B][S] uint8 (1 = attend) or NULL; kernels.py:53-55, patch.py:280-291
+ *   held_len > 0 masks the first held_len rows of every (b,hk) with
+ *     held_valid[b*hv_sb + hk*hv_sh + r] && held_pos[b*hp_sb + hk*hp_sh + r] <= *cur_pos
+ *     (patch.py:288; cur_pos may be NULL = no position test).
+ *   out  [B][Hq][D] in dtype: out[b*o_sb + h*o_sh + d]
+ *   evict_loss / evict_idx (may be NULL): the per-token eviction score
+ *     mean_h(mean_d|p v| / l) rounded to dtype, [B][S] float, and its
+ *     first-index argmin [B] int64 (kernels.py:66-67, 134-136).
+ *   num_splits <= 0 picks a split count; the workspace must hold
+ *     hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, with_evict)
+ *     bytes and be zero-filled once before its first use (the kernels leave
+ *     it zeroed again).  One workspace must not be used by two launches that
+ *     may overlap.
+ *   dropout must be 0.0.
+ */
+int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hk, int64_t D,
+                                      int64_t S, int64_t num_splits, int with_evict);
+int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                   const void* q, int64_t q_sb, int64_t q_sh,
+                   const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                   const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                   const uint8_t* mask, int64_t mask_sb,
+                   int64_t held_len,
+                   const int64_t* held_pos, int64_t hp_sb, int64_t hp_sh,
+                   const uint8_t* held_valid, int64_t hv_sb, int64_t hv_sh,
+                   const int64_t* cur_pos,
+                   double scaling, double dropout,
+                   void* out, int64_t o_sb, int64_t o_sh,
+                   float* evict_loss, int64_t* evict_idx,
+                   void* workspace, int64_t workspace_bytes, int64_t num_splits,
+                   void* stream);
+
+/*
+ * Window importance scores per KV head, fp32 [B][Hk][S] (row stride S).
+ * Replaces snapkv_importance (scoring.py:50-79) with _group_query_to_kv
+ * (scoring.py:17-26) and pool1d (scoring.py:40-47) in HC_SCORE_SNAPKV mode,
+ * and the scoring of HotColdLayer._compress_if_needed (cache.py:55-69) in
+ * HC_SCORE_RAWSUM mode (pooling off; the head mean is hc_head_mean).
+ *
+ *   q [B][Hq][*][D]: the W window query rows are q rows q_row0 .. q_row0+W-1
+ *     (q[b*q_sb + h*q_sh + (q_row0+w)*q_ss + d]); in SNAPKV mode window row w
+ *     sits at absolute position S-W+w for the causal mask.
+ *   k [B][Hk][S][D].
+ *   kernel_size <= 1 disables pooling; otherwise it must be odd.
+ * Scores are defined bit-for-bit (fp64 exact-product dot chains, integer
+ * fixed-point softmax normaliser, fixed-order window sum, fp32 result) so the
+ * selected indices are reproducible on any conforming implementation.
+ */
+int64_t hc_snapkv_score_workspace_size(int64_t B, int64_t Hk, int64_t S, int64_t D, int64_t W);
+int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64_t Hk, int64_t S,
+                    int64_t D, int64_t W,
+                    const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_row0,
+                    const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                    double scaling, int64_t kernel_size, int pooling,
+                    float* scores,
+                    void* workspace, int64_t workspace_bytes, void* stream);
+
+/* Mean over KV heads of fp32 scores [B][H][S] -> [B][S] (cache.py:69 ".mean(dim=1)"). */
+int hc_head_mean(int64_t B, int64_t H, int64_t S, const float* scores, float* out, void* stream);
+
+/*
+ * Kept-index selection: the keep_prefix highest-scoring prefix positions
+ * (value descending, ties to the lower index), ascending, followed by the
+ * recent window.  Replaces keep_index (scoring.py:110-132) and the top-k of
+ * cache.py:47-76 (window = recent, budget = topk + recent).
+ *   window_eff = min(window, S); prefix = S - window_eff;
+ *   keep_prefix = max(0, min(budget - window_eff, prefix)); n_keep = keep_prefix + window_eff
+ *   scores [B][H][S] fp32 (s[b*s_sb + h*s_sh + s]) -> keep [B][H][n_keep] int64
+ *   evicted [B][H][prefix-keep_prefix] int64 (prefix positions not kept,
+ *   ascending), or NULL (cache.py:86-95).
+ */
+int hc_topk_keep(int64_t B, int64_t H, int64_t S, const float* scores, int64_t s_sb, int64_t s_sh,
+                 int64_t window, int64_t budget, int64_t* keep, int64_t* evicted, void* stream);
+
+/*
+ * Row gather into the hot buffer: dst_i[b][h][j] = src_i[b][h][idx[b][h][j]] for
+ * j < n, for up to three tensors that share the index set (K, V, pre-RoPE K).
+ * Replaces gather_kv (scoring.py:135-139), _compress (layer_state.py:76-77) and
+ * the gathers of cache.py:79-84.  idx[b*i_sb + h*i_sh + j] (i_sh = 0 shares one
+ * set across heads); an index outside [0, src_rows) leaves its destination row
+ * untouched.  Rows are D elements of elem_bytes bytes; dst row j is written at
+ * row dst_row0 + j.  src2/dst2 and src3/dst3 may be NULL.  pos_src [B][*] /
+ * pos_dst [B][*] int64 positions (cache.py:84) may be NULL.
+ */
+int hc_gather_rows(int64_t B, int64_t H, int64_t n, int64_t D, int64_t elem_bytes,
+                   const int64_t* idx, int64_t i_sb, int64_t i_sh, int64_t src_rows,
+                   int64_t dst_row0,
+                   const void* src1, int64_t s1_sb, int64_t s1_sh, int64_t s1_ss,
+                   void* dst1, int64_t d1_sb, int64_t d1_sh, int64_t d1_ss,
+                   const void* src2, int64_t s2_sb, int64_t s2_sh, int64_t s2_ss,
+                   void* dst2, int64_t d2_sb, int64_t d2_sh, int64_t d2_ss,
+                   const void* src3, int64_t s3_sb, int64_t s3_sh, int64_t s3_ss,
+                   void* dst3, int64_t d3_sb, int64_t d3_sh, int64_t d3_ss,
+                   const int64_t* pos_src, int64_t ps_sb, int64_t* pos_dst, int64_t pd_sb,
+                   void* stream);
+
+/*
+ * Append T new token rows at row `row` of the hot buffer (replaces the torch.cat
+ * appends of cache.py:145-148 and layer_state.py:99-100).  src rows
+ * [B][H][T][D]; k_pre/pos may be NULL.  pos_src [B][T] int64 -> pos_dst[b][row+t].
+ */
+int hc_append_rows(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t row,
+                   const void* k_src, int64_t ks_sb, int64_t ks_sh, int64_t ks_ss,
+                   void* k_dst, int64_t kd_sb, int64_t kd_sh, int64_t kd_ss,
+                   const void* v_src, int64_t vs_sb, int64_t vs_sh, int64_t vs_ss,
+                   void* v_dst, int64_t vd_sb, int64_t vd_sh, int64_t vd_ss,
+                   const void* p_src, int64_t ps_sb, int64_t ps_sh, int64_t ps_ss,
+                   void* p_dst, int64_t pd_sb, int64_t pd_sh, int64_t pd_ss,
+                   const int64_t* pos_src, int64_t pos_s_sb, int64_t* pos_dst, int64_t pos_d_sb,
+                   void* stream);
+
+/*
+ * Inject: re-RoPE staged pre-RoPE keys to their original positions and write
+ * them, with their values, into the held slot (rows 0..R-1) of the hot buffer.
+ * Replaces _rotate_k_with_pos / _rope_cos_sin_for_positions (patch.py:76-102)
+ * and the held-slot replacement of patch.py:241-270.
+ *   k_pre, v: staged fp32 [B][Hk][R][D] (element strides kp_*, vp_*)
+ *   pos [B][Hk?][R] int64 with strides (pos_sh = 0: one position set per batch)
+ *   inv_freq fp32 [D/2] on the device; attention_scaling as in the rotary module.
+ *   k_dst/v_dst rows r of [B][Hk][*][D] in dtype.
+ * The rotation follows the model's per-op rounding in dtype:
+ *   k*cos + rotate_half(k)*sin with cos/sin = dtype(fp32(cos(fp32(pos*inv_freq)))*scaling).
+ */
+int hc_inject_rerope(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D,
+                     const float* k_pre, int64_t kp_sb, int64_t kp_sh, int64_t kp_ss,
+                     const float* v, int64_t vp_sb, int64_t vp_sh, int64_t vp_ss,
+                     const int64_t* pos, int64_t pos_sb, int64_t pos_sh,
+                     const float* inv_freq, double attention_scaling,
+                     void* k_dst, int64_t kd_sb, int64_t kd_sh, int64_t kd_ss,
+                     void* v_dst, int64_t vd_sb, int64_t vd_sh, int64_t vd_ss,
+                     void* stream);
+
+/*
+ * Staging primitives for the inject feed (controller.py:344-442): a library
+ * side stream created hipStreamNonBlocking at default priority, pinned
+ * host->device copies on it, and events that the consumer polls (never waits
+ * on) before ordering its stream after the copy.
+ */
+int hc_stream_create(void** stream_out);
+int hc_stream_destroy(void* stream);
+int hc_event_create(void** event_out, int timing);
+int hc_event_destroy(void* event);
+int hc_event_record(void* event, void* stream);
+int hc_event_query(void* event);            /* 1 = complete, 0 = pending, <0 = error */
+int hc_event_elapsed_ms(void* start, void* end, float* ms_out);
+int hc_stream_wait_event(void* stream, void* event);
+int hc_memcpy_h2d_async(void* dst, const void* src, int64_t bytes, void* stream);
+int hc_memcpy_d2h_async(void* dst, const void* src, int64_t bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HOTCOLD_HIP_H */

@@ -1,0 +1,409 @@
+"""CPU restatement of the reference hot-tier algorithms -- TEST INFRASTRUCTURE.
+
+Used only by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg,
+as the checker (never as the product path).  Every function cites the
+reference file:line it follows (tarun931/hotcold-kv-cache, src/hotcold_kv/...).
+
+Parity pins (what checks each function; see tests/test_oracle.py):
+  window_scores (C, bit-defined contract)   -- fp64 closed-form softmax, the
+      literal fp32 torch restatement below, brute force on tiny shapes, golden
+      fixtures, exp_det vs libm
+  snapkv_importance_torch (literal fp32)    -- fp64 closed form
+  keep_index                                -- brute force over all subsets on
+      tiny S, test_baselines.py:89-100 invariants, hand-made tie cases
+  gather_kv                                 -- identity / permutation checks
+  decode_attention                          -- closed forms (single key, equal
+      keys), torch SDPA fp32
+  evict_scores                              -- closed form on a hand-made case
+  rerope                                    -- HF apply_rotary_pos_emb on CPU;
+      orthogonality (norm) and rot(p) then rot(-p) = identity in fp64
+  hotcold_compress                          -- cache.py invariants (kept count,
+      recent window, evicted = complement)
+  ColdStore                                 -- test_cold_store.py self-retrieval
+      and ring-wrap cases
+"""
+
+import ctypes
+import math
+import os
+import subprocess
+
+import numpy as np
+import torch
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "_build", "libhc_oracle.so")
+_lib = None
+
+
+def build():
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def _clib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        lib = ctypes.CDLL(_LIB_PATH)
+        i64, vp, dbl = ctypes.c_int64, ctypes.c_void_p, ctypes.c_double
+        lib.hco_exp_det.restype = dbl
+        lib.hco_exp_det.argtypes = [dbl]
+        lib.hco_window_scores.restype = ctypes.c_int
+        lib.hco_window_scores.argtypes = [ctypes.c_int, i64, i64, i64, i64, i64, i64,
+                                          vp, i64, i64, i64, i64,
+                                          vp, i64, i64, i64, dbl, i64, ctypes.c_int, vp]
+        lib.hco_head_mean.restype = None
+        lib.hco_head_mean.argtypes = [i64, i64, i64, vp, vp]
+        _lib = lib
+    return _lib
+
+
+def exp_det(x):
+    return _clib().hco_exp_det(float(x))
+
+
+def _f64(t):
+    """Exact fp64 numpy copy of a CPU/GPU tensor of any float dtype."""
+    return np.ascontiguousarray(t.detach().to("cpu", torch.float64).numpy())
+
+
+# ---------------------------------------------------------------------------
+# Window scores: the bit-defined contract (C)
+# ---------------------------------------------------------------------------
+def window_scores(q, k, window, scaling, kernel_size=7, pooling="maxpool", mode="snapkv"):
+    """Importance (B,Hk,S) float32 under the bit-defined contract.
+
+    mode "snapkv" follows snapkv_importance (scoring.py:50-79): window rows are
+    the last min(window,S) rows of q (T == S).  mode "rawsum" follows
+    cache.py:55-69 before the head mean: the last min(window,T) rows of q, no
+    mask, no softmax, no pooling.
+    """
+    qn, kn = _f64(q), _f64(k)
+    B, Hq, T, D = qn.shape
+    _, Hk, S, _ = kn.shape
+    if mode == "snapkv":
+        W = min(int(window), S)
+        q_row0 = S - W
+        m = 0
+    else:
+        W = min(int(window), T)
+        q_row0 = T - W
+        m = 1
+        kernel_size = 1
+    out = np.empty((B, Hk, S), dtype=np.float32)
+    rc = _clib().hco_window_scores(
+        m, B, Hq, Hk, S, D, W,
+        qn.ctypes.data, Hq * T * D, T * D, D, q_row0,
+        kn.ctypes.data, Hk * S * D, S * D, D,
+        float(scaling), int(kernel_size or 1), 1 if pooling == "avgpool" else 0,
+        out.ctypes.data)
+    if rc != 0:
+        raise ValueError("hco_window_scores: bad arguments")
+    return torch.from_numpy(out)
+
+
+def head_mean(x):
+    xn = np.ascontiguousarray(x.detach().cpu().float().numpy())
+    B, H, S = xn.shape
+    out = np.empty((B, S), dtype=np.float32)
+    _clib().hco_head_mean(B, H, S, xn.ctypes.data, out.ctypes.data)
+    return torch.from_numpy(out)
+
+
+# ---------------------------------------------------------------------------
+# Literal fp32 restatements of the reference scoring (scoring.py)
+# ---------------------------------------------------------------------------
+def repeat_kv(x, n_rep):
+    """scoring.py:9-14."""
+    if n_rep == 1:
+        return x
+    B, Hk, S, D = x.shape
+    return x[:, :, None].expand(B, Hk, n_rep, S, D).reshape(B, Hk * n_rep, S, D)
+
+
+def group_query_to_kv(q, Hk):
+    """scoring.py:17-26: mean of each GQA group (or of all heads)."""
+    B, Hq, T, D = q.shape
+    if Hq == Hk:
+        return q
+    if Hq % Hk == 0:
+        return q.view(B, Hk, Hq // Hk, T, D).mean(dim=2)
+    return q.mean(dim=1, keepdim=True).expand(B, Hk, T, D)
+
+
+def pool1d(x, kernel_size, pooling):
+    """scoring.py:40-47."""
+    if kernel_size is None or kernel_size <= 1:
+        return x
+    pad = kernel_size // 2
+    if pooling == "avgpool":
+        return torch.nn.functional.avg_pool1d(x, kernel_size=kernel_size, stride=1, padding=pad)
+    return torch.nn.functional.max_pool1d(x, kernel_size=kernel_size, stride=1, padding=pad)
+
+
+def snapkv_importance_torch(q_post, keys, window_size, scaling, kernel_size, pooling, dtype=torch.float32):
+    """scoring.py:50-79 on CPU with inputs upcast to `dtype` (the reference's
+    own op sequence: GQA mean, matmul, causal masked_fill, fp32 softmax, sum
+    over the window, pooling)."""
+    q_post = q_post.detach().cpu().to(dtype)
+    keys = keys.detach().cpu().to(dtype)
+    B, Hq, S, D = q_post.shape
+    Hk = keys.shape[1]
+    W = min(window_size, S)
+    q_for = group_query_to_kv(q_post[:, :, S - W:, :], Hk)
+    logits = torch.matmul(q_for, keys.transpose(2, 3)) * scaling
+    qpos = torch.arange(S - W, S).view(1, 1, W, 1)
+    kpos = torch.arange(S).view(1, 1, 1, S)
+    logits = logits.masked_fill(kpos > qpos, float("-inf"))
+    probs = torch.softmax(logits.float(), dim=-1)
+    imp = probs.sum(dim=2)
+    return pool1d(imp, kernel_size, pooling)
+
+
+def snapkv_importance_f64(q_post, keys, window_size, scaling, kernel_size, pooling):
+    """Closed-form fp64 version of scoring.py:50-79 (numpy)."""
+    qn, kn = _f64(q_post), _f64(keys)
+    B, Hq, S, D = qn.shape
+    Hk = kn.shape[1]
+    W = min(window_size, S)
+    qt = qn[:, :, S - W:, :]
+    if Hq % Hk == 0:
+        qf = qt.reshape(B, Hk, Hq // Hk, W, D).mean(axis=2)
+    else:
+        qf = np.broadcast_to(qt.mean(axis=1, keepdims=True), (B, Hk, W, D))
+    logits = np.einsum("bhwd,bhsd->bhws", qf, kn) * scaling
+    qpos = np.arange(S - W, S).reshape(1, 1, W, 1)
+    kpos = np.arange(S).reshape(1, 1, 1, S)
+    logits = np.where(kpos > qpos, -np.inf, logits)
+    m = logits.max(axis=-1, keepdims=True)
+    e = np.exp(logits - m)
+    probs = e / e.sum(axis=-1, keepdims=True)
+    imp = probs.sum(axis=2)
+    if kernel_size and kernel_size > 1:
+        P = kernel_size // 2
+        padv = -np.inf if pooling != "avgpool" else 0.0
+        padded = np.pad(imp, ((0, 0), (0, 0), (P, P)), constant_values=padv)
+        win = np.lib.stride_tricks.sliding_window_view(padded, kernel_size, axis=-1)
+        imp = win.max(axis=-1) if pooling != "avgpool" else win.sum(axis=-1) / kernel_size
+    return imp
+
+
+# ---------------------------------------------------------------------------
+# Selection and gather (scoring.py:110-139)
+# ---------------------------------------------------------------------------
+def keep_counts(S, window_size, budget):
+    """scoring.py:118-120."""
+    window = min(window_size, S)
+    prefix = S - window
+    keep_prefix = max(0, min(budget - window, prefix))
+    return window, prefix, keep_prefix
+
+
+def keep_index(scores, window_size, budget, return_evicted=False):
+    """scoring.py:110-132 with the deterministic tie rule: the keep_prefix
+    prefix positions of highest score, ties to the lower index (a stable sort
+    on -score), sorted ascending, then arange(prefix, S)."""
+    sc = scores.detach().cpu().float().numpy()
+    squeeze = sc.ndim == 2
+    if squeeze:
+        sc = sc[:, None, :]
+    B, H, S = sc.shape
+    window, prefix, kp = keep_counts(S, window_size, budget)
+    keep = np.empty((B, H, kp + window), dtype=np.int64)
+    ev = np.empty((B, H, prefix - kp), dtype=np.int64)
+    recent = np.arange(prefix, S, dtype=np.int64)
+    for b in range(B):
+        for h in range(H):
+            pre = sc[b, h, :prefix].astype(np.float64)
+            key = np.where(np.isnan(pre), -np.inf, -pre)  # NaN ranks highest, like torch.topk
+            order = np.argsort(key, kind="stable")
+            top = np.sort(order[:kp])
+            keep[b, h, :kp] = top
+            keep[b, h, kp:] = recent
+            mask = np.ones(prefix, dtype=bool)
+            mask[top] = False
+            ev[b, h] = np.nonzero(mask)[0]
+    keep_t = torch.from_numpy(keep)
+    ev_t = torch.from_numpy(ev)
+    if squeeze:
+        keep_t, ev_t = keep_t[:, 0], ev_t[:, 0]
+    return (keep_t, ev_t) if return_evicted else keep_t
+
+
+def gather_kv(t, keep):
+    """scoring.py:135-139."""
+    t = t.detach().cpu()
+    keep = keep.detach().cpu()
+    if keep.dim() == 2:
+        keep = keep.unsqueeze(1).expand(t.shape[0], t.shape[1], keep.shape[-1])
+    B, H, S, D = t.shape
+    return t.gather(2, keep.unsqueeze(-1).expand(B, H, keep.shape[-1], D))
+
+
+# ---------------------------------------------------------------------------
+# Decode attention (kernels.py:9-137, patch.py:280-305)
+# ---------------------------------------------------------------------------
+def decode_attention(q, k, v, scaling, mask=None):
+    """softmax(q.K^T * scaling, masked) . V per query head in fp64, with the GQA
+    map kv = h // (Hq/Hk) (kernels.py:35).  q (B,Hq,D) or (B,Hq,1,D); returns
+    (B,Hq,D) float64 numpy.  Rows with every key masked give NaN, as the
+    reference's 0/0 does."""
+    qn = _f64(q)
+    if qn.ndim == 4:
+        qn = qn[:, :, 0, :]
+    kn, vn = _f64(k), _f64(v)
+    B, Hq, D = qn.shape
+    Hk = kn.shape[1]
+    G = Hq // Hk
+    kr = np.repeat(kn, G, axis=1)
+    vr = np.repeat(vn, G, axis=1)
+    s = np.einsum("bhd,bhsd->bhs", qn, kr) * scaling
+    if mask is not None:
+        mk = mask.detach().cpu().numpy().astype(bool)
+        s = np.where(mk[:, None, :], s, -np.inf)
+    m = s.max(axis=-1, keepdims=True)
+    with np.errstate(invalid="ignore", divide="ignore"):
+        e = np.where(np.isfinite(m), np.exp(s - m), 0.0)
+        out = np.einsum("bhs,bhsd->bhd", e, vr) / e.sum(axis=-1)[..., None]
+    return out
+
+
+def evict_scores(q, k, v, scaling, mask=None):
+    """Eviction score of kernels.py:66-67 and 134-136 in fp64:
+    final_loss[b,s] = mean_h( p[b,h,s]/l[b,h] * mean_d|v[b,kv(h),s,d]| ).
+    Returns (final_loss (B,S) float64, argmin (B,) over the loss rounded to
+    q's dtype, first index on ties)."""
+    qn = _f64(q)
+    if qn.ndim == 4:
+        qn = qn[:, :, 0, :]
+    kn, vn = _f64(k), _f64(v)
+    B, Hq, D = qn.shape
+    Hk = kn.shape[1]
+    G = Hq // Hk
+    s = np.einsum("bhd,bhsd->bhs", qn, np.repeat(kn, G, axis=1)) * scaling
+    if mask is not None:
+        mk = mask.detach().cpu().numpy().astype(bool)
+        s = np.where(mk[:, None, :], s, -np.inf)
+    m = s.max(axis=-1, keepdims=True)
+    p = np.exp(s - m)
+    p = p / p.sum(axis=-1, keepdims=True)
+    av = np.abs(np.repeat(vn, G, axis=1)).mean(axis=-1)
+    loss = (p * av).mean(axis=1)
+    rounded = torch.from_numpy(loss).to(q.dtype).float().numpy()
+    return loss, np.argmin(rounded, axis=-1)
+
+
+# ---------------------------------------------------------------------------
+# Re-RoPE (patch.py:76-102; transformers LlamaRotaryEmbedding.forward and
+# apply_rotary_pos_emb of the installed modeling_llama.py)
+# ---------------------------------------------------------------------------
+def default_inv_freq(head_dim, theta):
+    """compute_default_rope_parameters: 1 / theta^(arange(0, D, 2) / D), fp32."""
+    return 1.0 / (theta ** (torch.arange(0, head_dim, 2, dtype=torch.float) / head_dim))
+
+
+def rotary_cos_sin(inv_freq, attention_scaling, pos, dtype):
+    """LlamaRotaryEmbedding.forward on CPU: cos/sin (B,S,D) in `dtype`."""
+    pos = pos.detach().cpu().long()
+    if pos.dim() == 1:
+        pos = pos.unsqueeze(0)
+    inv = inv_freq.detach().cpu().float()
+    inv_exp = inv[None, :, None].expand(pos.shape[0], -1, 1)
+    freqs = (inv_exp @ pos[:, None, :].float()).transpose(1, 2)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    cos = emb.cos() * attention_scaling
+    sin = emb.sin() * attention_scaling
+    return cos.to(dtype), sin.to(dtype)
+
+
+def rotate_half(x):
+    x1 = x[..., : x.shape[-1] // 2]
+    x2 = x[..., x.shape[-1] // 2:]
+    return torch.cat((-x2, x1), dim=-1)
+
+
+def rerope(k_pre, pos, inv_freq, attention_scaling, dtype):
+    """_rotate_k_with_pos (patch.py:94-102): staged k_pre (B,Hk,R,D) fp32 cast
+    to the cache dtype (controller.py:365-373), rotated to positions pos (B,R)
+    (one set per batch) or (B,Hk,R) (one per KV head) with the model's per-op
+    rounding k*cos + rotate_half(k)*sin."""
+    k16 = k_pre.detach().cpu().to(dtype)
+    B, Hk, R, D = k16.shape
+    pos = pos.detach().cpu().long()
+    if pos.dim() == 2:
+        cos, sin = rotary_cos_sin(inv_freq, attention_scaling, pos, dtype)   # (B,R,D)
+        cos, sin = cos[:, None], sin[:, None]
+    else:
+        cos, sin = rotary_cos_sin(inv_freq, attention_scaling, pos.reshape(B * Hk, R), dtype)
+        cos, sin = cos.view(B, Hk, R, D), sin.view(B, Hk, R, D)
+    return (k16 * cos) + (rotate_half(k16) * sin)
+
+
+# ---------------------------------------------------------------------------
+# Hot/cold compression (cache.py:37-128)
+# ---------------------------------------------------------------------------
+def hotcold_compress(keys, values, pre_keys, positions, q_last, max_capacity, recent_size, topk_ratio):
+    """HotColdLayer._compress_if_needed with contract scoring.  Returns None if
+    no compression happens, else dict(keep (B,n), keys, values, pre_keys,
+    positions, evicted_idx (B,Te) ascending)."""
+    B, Hk, S, D = keys.shape
+    if S <= max_capacity:
+        return None
+    recent = min(recent_size, max_capacity, S)
+    prefix = S - recent
+    if prefix <= 0:
+        return None
+    topk = max(1, min(int(max_capacity * topk_ratio), prefix))
+    tq = min(recent, q_last.shape[2])
+    per_head = window_scores(q_last, keys, tq, 1.0, kernel_size=1, mode="rawsum")
+    scores = head_mean(per_head)                       # (B,S)
+    keep, ev = keep_index(scores, recent, topk + recent, return_evicted=True)
+    return dict(keep=keep, evicted_idx=ev,
+                keys=gather_kv(keys, keep), values=gather_kv(values, keep),
+                pre_keys=gather_kv(pre_keys, keep),
+                positions=positions.detach().cpu().gather(1, keep))
+
+
+# ---------------------------------------------------------------------------
+# Cold store (controller.py:166-293), exact inner-product search
+# ---------------------------------------------------------------------------
+class ColdStore:
+    """Ring of evicted tokens per batch with exact IP search over the
+    head-mean, pad/crop, L2-normalised pre-RoPE key (controller.py:166-188,
+    190-238, 250-293).  Ties rank the lower ring slot first."""
+
+    def __init__(self, capacity, dim, normalize=True):
+        self.capacity, self.dim, self.normalize = capacity, dim, normalize
+        self.kpre, self.v, self.pos = [], [], []
+
+    def _vec(self, x):
+        x = np.asarray(x, dtype=np.float64)
+        if x.shape[-1] > self.dim:
+            x = x[..., : self.dim]
+        elif x.shape[-1] < self.dim:
+            x = np.pad(x, [(0, 0)] * (x.ndim - 1) + [(0, self.dim - x.shape[-1])])
+        if self.normalize:
+            n = np.linalg.norm(x, axis=-1, keepdims=True)
+            x = x / np.maximum(n, 1e-12)
+        return x
+
+    def add(self, kpre_tokens, v_tokens, positions):
+        for kp, vv, p in zip(kpre_tokens, v_tokens, positions):
+            self.kpre.append(np.asarray(kp, dtype=np.float32))
+            self.v.append(np.asarray(vv, dtype=np.float32))
+            self.pos.append(int(p))
+        over = len(self.kpre) - self.capacity
+        if over > 0:
+            del self.kpre[:over], self.v[:over], self.pos[:over]
+
+    def search(self, q_vec, r):
+        n = len(self.kpre)
+        if n == 0:
+            return []
+        keys = self._vec(np.stack([k.mean(axis=0) for k in self.kpre]))
+        q = self._vec(np.asarray(q_vec, dtype=np.float64)[None])[0]
+        ip = keys @ q
+        order = np.argsort(-ip, kind="stable")[: min(r, n)]
+        return [int(i) for i in order]

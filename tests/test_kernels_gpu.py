@@ -1,0 +1,288 @@
+"""GPU parity of each hot-tier kernel against the CPU oracle (same seeded inputs).
+
+Bars: kept indices and gathered rows bit-exact; window scores bit-exact under
+the bit-defined contract; attention outputs within max-abs 2e-3 (fp16),
+1e-2 (bf16), 1e-4 (fp32) of the fp64 oracle; re-RoPE keys within one ulp of
+the model's own rotation (and equal in at least 99.9% of elements).
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from hotcold_kv import ops, synthetic
+from oracle import reference as ref
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+TOL = {torch.float16: 2e-3, torch.bfloat16: 1e-2, torch.float32: 1e-4}
+
+
+def _randn(shape, seed, dtype, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(dtype)
+
+
+# ---------------------------------------------------------------------------
+# Decode attention
+# ---------------------------------------------------------------------------
+DECODE_CASES = [
+    # B, Hq, Hk, S, D, dtype
+    (2, 8, 2, 200, 16, torch.float32),      # reference test geometry (test_baselines.py:46)
+    (2, 8, 2, 200, 16, torch.float16),
+    (1, 32, 8, 574, 128, torch.float16),    # 8k/budget-512 hot buffer after 62 appends
+    (1, 32, 8, 574, 128, torch.bfloat16),
+    (1, 32, 8, 544, 128, torch.float32),
+    (3, 16, 4, 1, 64, torch.float16),       # a single key
+    (2, 8, 8, 37, 32, torch.bfloat16),      # no grouping, ragged length
+    (4, 32, 8, 2431, 128, torch.float16),   # batched long hot buffer
+    (1, 64, 8, 300, 128, torch.float16),    # group of 8
+    (1, 8, 1, 1000, 256, torch.bfloat16),   # one KV head, wide head_dim
+    (1, 32, 2, 333, 128, torch.float16),    # group of 16
+]
+
+
+def test_decode_unsupported_group_raises():
+    q = torch.zeros((1, 16, 1, 256), dtype=torch.float16, device=DEV)
+    k = torch.zeros((1, 1, 8, 256), dtype=torch.float16, device=DEV)
+    with pytest.raises(RuntimeError, match="group size 16"):
+        ops.decode_attention(q, k, k, 0.1)
+    with pytest.raises(ValueError, match="dropout"):
+        ops.decode_attention(q, k, k, 0.1, dropout=0.1)
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S,D,dtype", DECODE_CASES)
+@pytest.mark.parametrize("splits", [0, 1])
+def test_decode_matches_oracle(B, Hq, Hk, S, D, dtype, splits):
+    q = _randn((B, Hq, 1, D), 1, dtype)
+    k = _randn((B, Hk, S, D), 2, dtype)
+    v = _randn((B, Hk, S, D), 3, dtype)
+    sc = 1.0 / math.sqrt(D)
+    out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), sc, num_splits=splits)
+    want = ref.decode_attention(q, k, v, sc)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert np.abs(got - want).max() <= TOL[dtype], np.abs(got - want).max()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_decode_mask_and_held_slot(dtype):
+    B, Hq, Hk, R, n, D = 2, 32, 8, 64, 300, 128
+    S = R + n
+    q = _randn((B, Hq, 1, D), 4, dtype)
+    k = _randn((B, Hk, S, D), 5, dtype)
+    v = _randn((B, Hk, S, D), 6, dtype)
+    g = torch.Generator().manual_seed(7)
+    valid = torch.rand((B, R), generator=g) < 0.7
+    pos = torch.randint(0, 2000, (B, R), generator=g)
+    cur = torch.tensor([1500], dtype=torch.int64)
+    keep_mem = valid & (pos <= cur)
+    mask = torch.cat([keep_mem, torch.ones((B, n), dtype=torch.bool)], dim=1)
+    sc = 1.0 / math.sqrt(D)
+    want = ref.decode_attention(q, k, v, sc, mask)
+    # explicit (B,S) mask, as triton_evict_attention_forward takes it
+    out1 = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), sc, mask=mask.to(DEV))
+    # held-slot form: the kernel evaluates valid & pos <= cur_pos itself
+    out2 = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), sc, held_len=R, held_pos=pos.to(DEV),
+                                held_valid=valid.to(DEV), cur_pos=cur.to(DEV))
+    for out in (out1, out2):
+        assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype]
+
+
+def test_decode_per_head_held_positions():
+    B, Hq, Hk, R, n, D = 1, 32, 8, 16, 100, 128
+    S = R + n
+    dtype = torch.float16
+    q, k, v = _randn((B, Hq, 1, D), 8, dtype), _randn((B, Hk, S, D), 9, dtype), _randn((B, Hk, S, D), 10, dtype)
+    g = torch.Generator().manual_seed(11)
+    valid = torch.rand((B, Hk, R), generator=g) < 0.5
+    pos = torch.randint(0, 100, (B, Hk, R), generator=g)
+    cur = torch.tensor([60], dtype=torch.int64)
+    out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), 0.1, held_len=R, held_pos=pos.to(DEV),
+                               held_valid=valid.to(DEV), cur_pos=cur.to(DEV)).float().cpu().numpy()
+    for h in range(Hk):
+        m = torch.cat([valid[:, h] & (pos[:, h] <= 60), torch.ones((B, n), dtype=torch.bool)], 1)
+        want = ref.decode_attention(q[:, h * 4:(h + 1) * 4], k[:, h:h + 1], v[:, h:h + 1], 0.1, m)
+        assert np.abs(out[:, h * 4:(h + 1) * 4] - want).max() <= 2e-3
+
+
+def test_decode_all_masked_is_nan_like_reference():
+    # kernels.py:55-69: every score -1e35 -> l = 0 -> 0/0.
+    B, Hq, Hk, S, D = 1, 4, 1, 10, 16
+    q, k, v = _randn((B, Hq, 1, D), 1, torch.float16), _randn((B, Hk, S, D), 2, torch.float16), \
+        _randn((B, Hk, S, D), 3, torch.float16)
+    mask = torch.zeros((B, S), dtype=torch.bool)
+    out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), 0.25, mask=mask.to(DEV))
+    assert torch.isnan(out.float()).all()
+
+
+def test_decode_single_unmasked_key_returns_its_value():
+    B, Hq, Hk, S, D = 1, 8, 2, 77, 128
+    q, k, v = _randn((B, Hq, 1, D), 1, torch.float16), _randn((B, Hk, S, D), 2, torch.float16), \
+        _randn((B, Hk, S, D), 3, torch.float16)
+    mask = torch.zeros((B, S), dtype=torch.bool)
+    mask[0, 41] = True
+    out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), 0.1, mask=mask.to(DEV)).cpu()
+    for h in range(Hq):
+        assert torch.equal(out[0, h], v[0, h // 4, 41])
+
+
+def test_decode_strided_views_and_evict_score():
+    # hot buffer view: (B,Hk,cap,D) storage, attended prefix of n rows
+    B, Hq, Hk, cap, n, D = 2, 32, 8, 700, 531, 128
+    dtype = torch.float16
+    kbuf, vbuf = _randn((B, Hk, cap, D), 12, dtype), _randn((B, Hk, cap, D), 13, dtype)
+    q = _randn((B, Hq, 1, D), 14, dtype)
+    k, v = kbuf[:, :, :n], vbuf[:, :, :n]
+    out, loss, idx = ops.decode_attention(q.to(DEV), kbuf.to(DEV)[:, :, :n], vbuf.to(DEV)[:, :, :n], 0.088,
+                                          with_evict=True)
+    want = ref.decode_attention(q, k, v, 0.088)
+    assert np.abs(out.float().cpu().numpy() - want).max() <= 2e-3
+    want_loss, _ = ref.evict_scores(q, k, v, 0.088)
+    got_loss = loss.cpu().numpy()
+    assert np.allclose(got_loss, want_loss, rtol=2e-3, atol=1e-6)
+    for b in range(B):
+        # the chosen index is a minimiser of the oracle loss up to fp16 rounding
+        assert want_loss[b, int(idx[b])] <= want_loss[b].min() * (1 + 2e-3) + 1e-7
+
+
+# ---------------------------------------------------------------------------
+# SnapKV compaction
+# ---------------------------------------------------------------------------
+SCORE_CASES = [
+    # B, Hq, Hk, S, D, W, dtype, pool, pooling
+    (2, 8, 2, 200, 16, 16, torch.float32, 7, "maxpool"),   # test_baselines.py geometry
+    (2, 8, 2, 200, 16, 16, torch.float32, 7, "avgpool"),
+    (1, 32, 8, 2048, 128, 32, torch.float32, 7, "maxpool"),  # plumbing config
+    (1, 32, 8, 1000, 128, 32, torch.float16, 7, "maxpool"),
+    (1, 32, 8, 1000, 128, 64, torch.bfloat16, 7, "maxpool"),
+    (2, 12, 4, 333, 64, 40, torch.float16, 5, "maxpool"),    # ragged window row block
+    (1, 6, 4, 150, 32, 8, torch.float16, 1, "maxpool"),      # Hq % Hk != 0, no pooling
+    (1, 4, 4, 20, 16, 32, torch.float32, 7, "maxpool"),      # window longer than the prompt
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S,D,W,dtype,pool,pooling", SCORE_CASES)
+def test_snapkv_scores_bit_exact(B, Hq, Hk, S, D, W, dtype, pool, pooling):
+    q = _randn((B, Hq, S, D), 21, dtype)
+    k = _randn((B, Hk, S, D), 22, dtype)
+    sc = 1.0 / math.sqrt(D)
+    got = ops.snapkv_scores(q.to(DEV), k.to(DEV), W, sc, pool, pooling).cpu()
+    want = ref.window_scores(q, k, W, sc, pool, pooling)
+    assert torch.equal(got, want), (got - want).abs().max()
+
+
+def test_snapkv_scores_and_keep_c1_layer():
+    """One layer of the 8k fp16 workload with needles: scores, kept indices
+    and the compacted K/V are bit-exact."""
+    w = synthetic.WORKLOADS["c1_llama8b_8k_b512"]
+    p = synthetic.make_prompt(w, layer=3, seed=0, device="cpu")
+    qd, kd, vd = p["q_post"].to(DEV), p["k_post"].to(DEV), p["v"].to(DEV)
+    got = ops.snapkv_scores(qd, kd, w.window, w.scaling, w.pool, "maxpool")
+    want = ref.window_scores(p["q_post"], p["k_post"], w.window, w.scaling, w.pool, "maxpool")
+    assert torch.equal(got.cpu(), want)
+    keep = ops.keep_index(got, w.window, w.budget)
+    want_keep = ref.keep_index(want, w.window, w.budget)
+    assert torch.equal(keep.cpu(), want_keep)
+    # the needles are selected
+    needles = p["needles"][0]
+    for h in range(w.hk):
+        assert set(needles[h].tolist()) <= set(want_keep[0, h].tolist())
+    kk = ops.gather_kv(kd, keep)
+    vv = ops.gather_kv(vd, keep)
+    assert torch.equal(kk.cpu(), ref.gather_kv(p["k_post"], want_keep))
+    assert torch.equal(vv.cpu(), ref.gather_kv(p["v"], want_keep))
+
+
+def test_rawsum_scores_and_head_mean():
+    B, Hq, Hk, S, T, D = 2, 32, 8, 700, 40, 128
+    q = _randn((B, Hq, T, D), 31, torch.float16)
+    k = _randn((B, Hk, S, D), 32, torch.float16)
+    got = ops.snapkv_scores(q.to(DEV), k.to(DEV), 32, 0.0, mode="rawsum")
+    want = ref.window_scores(q, k, 32, 0.0, mode="rawsum")
+    assert torch.equal(got.cpu(), want)
+    assert torch.equal(ops.head_mean(got).cpu(), ref.head_mean(want))
+
+
+@pytest.mark.parametrize("S,window,budget", [(200, 16, 64), (100, 8, 30), (50, 32, 20), (10, 32, 512),
+                                             (8192, 32, 512), (5000, 64, 5000), (4097, 1, 2)])
+def test_keep_index_matches_oracle(S, window, budget):
+    B, H = 2, 3
+    g = torch.Generator().manual_seed(S)
+    # coarse values: many exact ties, like max-pool plateaus
+    sc = torch.randint(0, 50, (B, H, S), generator=g).float() / 7.0
+    got, gev = ops.keep_index(sc.to(DEV), window, budget, return_evicted=True)
+    want, wev = ref.keep_index(sc, window, budget, return_evicted=True)
+    assert torch.equal(got.cpu(), want)
+    assert torch.equal(gev.cpu(), wev)
+
+
+def test_keep_index_special_values():
+    sc = torch.tensor([[[0.0, -0.0, 1.0, float("inf"), -float("inf"), 0.5, -0.0, 0.0, 2.0, 2.0, 0.1, 0.2]]])
+    for budget in range(1, 12):
+        got = ops.keep_index(sc.to(DEV), 2, budget).cpu()
+        assert torch.equal(got, ref.keep_index(sc, 2, budget)), budget
+
+
+def test_gather_shared_index_with_positions():
+    B, Hk, S, D, n = 2, 8, 300, 128, 77
+    dtype = torch.float16
+    k, v, kp = (_randn((B, Hk, S, D), s, dtype) for s in (41, 42, 43))
+    pos = torch.arange(S).unsqueeze(0).expand(B, S) * 3 + 5
+    g = torch.Generator().manual_seed(44)
+    idx = torch.stack([torch.sort(torch.randperm(S, generator=g)[:n]).values for _ in range(B)])
+    cap = 128
+    dk, dv, dp = (torch.zeros((B, Hk, cap, D), dtype=dtype, device=DEV) for _ in range(3))
+    dpos = torch.zeros((B, cap), dtype=torch.int64, device=DEV)
+    ops.gather_rows(idx.to(DEV), [(k.to(DEV), dk), (v.to(DEV), dv), (kp.to(DEV), dp)], dst_row0=10,
+                    pos_src=pos.contiguous().to(DEV), pos_dst=dpos)
+    for src, dst in ((k, dk), (v, dv), (kp, dp)):
+        assert torch.equal(dst[:, :, 10:10 + n].cpu(), ref.gather_kv(src, idx))
+        assert torch.count_nonzero(dst[:, :, :10]) == 0 and torch.count_nonzero(dst[:, :, 10 + n:]) == 0
+    assert torch.equal(dpos[:, 10:10 + n].cpu(), pos.gather(1, idx))
+
+
+def test_append_rows():
+    B, Hk, D, cap = 2, 8, 128, 40
+    dtype = torch.bfloat16
+    dk = torch.zeros((B, Hk, cap, D), dtype=dtype, device=DEV)
+    dv = torch.zeros_like(dk)
+    dpos = torch.zeros((B, cap), dtype=torch.int64, device=DEV)
+    k1, v1 = _randn((B, Hk, 1, D), 51, dtype), _randn((B, Hk, 1, D), 52, dtype)
+    ops.append_rows(17, k1.to(DEV), dk, v1.to(DEV), dv, pos_src=torch.full((B, 1), 999).to(DEV), pos_dst=dpos)
+    assert torch.equal(dk[:, :, 17:18].cpu(), k1) and torch.equal(dv[:, :, 17:18].cpu(), v1)
+    assert int(dpos[0, 17]) == 999 and torch.count_nonzero(dk[:, :, :17]) == 0
+
+
+# ---------------------------------------------------------------------------
+# Inject (re-RoPE into the held slot)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("per_head", [False, True])
+def test_inject_rerope_matches_model_rotation(dtype, per_head):
+    B, Hk, R, D, cap = 2, 8, 64, 128, 100
+    k_pre = _randn((B, Hk, R, D), 61, torch.float32)
+    v = _randn((B, Hk, R, D), 62, torch.float32)
+    g = torch.Generator().manual_seed(63)
+    pos = torch.randint(0, 65536, (B, Hk, R) if per_head else (B, R), generator=g)
+    inv = ref.default_inv_freq(D, 500000.0)
+    kd = torch.zeros((B, Hk, cap, D), dtype=dtype, device=DEV)
+    vd = torch.zeros_like(kd)
+    ops.inject_rerope(k_pre.to(DEV), v.to(DEV), pos.to(DEV), inv.to(DEV), 1.0, kd, vd)
+    want = ref.rerope(k_pre, pos, inv, 1.0, dtype)
+    got = kd[:, :, :R].cpu()
+    assert torch.equal(vd[:, :, :R].cpu(), v.to(dtype))
+    exact = (got == want).float().mean().item()
+    # fp16/bf16 rounding absorbs the last-bit differences between the device's
+    # cos/sin of the fp32 angle and torch's CPU cos/sin; fp32 output shows them.
+    assert exact >= (0.999 if dtype != torch.float32 else 0.9), exact
+    # any difference is a few rounding steps of the two rotated terms
+    # |k_i cos| + |k_(i+-D/2) sin| (the result itself may cancel)
+    k16 = k_pre.to(dtype).float()
+    partner = torch.cat((k16[..., D // 2:], k16[..., : D // 2]), dim=-1)
+    bound = 4 * torch.finfo(dtype).eps * (k16.abs() + partner.abs())
+    diff = (got.float() - want.float()).abs()
+    assert (diff <= bound).all(), (diff - bound).max()
