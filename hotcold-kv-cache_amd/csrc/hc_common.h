@@ -79,9 +79,10 @@ struct Unpack<bf16_t> {
 };
 template <>
 struct Unpack<float> {
-  __device__ __forceinline__ static float get(const uint32_t* w, int i) {
-    return __builtin_bit_cast(float, w[i]);
-  }
+  // __uint_as_float takes the word by value: __builtin_bit_cast of an
+  // element of a register-resident array miscompiles with this toolchain
+  // (it reads element 0).
+  __device__ __forceinline__ static float get(const uint32_t* w, int i) { return __uint_as_float(w[i]); }
 };
 
 // ---------------------------------------------------------------------------

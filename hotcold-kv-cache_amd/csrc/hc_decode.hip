@@ -35,8 +35,7 @@ struct DecodeArgs {
   int64_t held_len;
   void* out;
   int64_t o_sb, o_sh;
-  float* part;         // [units][splits][G*D + 2*G]
-  uint32_t* counters;  // [units], zero between launches
+  float* part;         // [units][splits][G*D + 2*G] split partials (splits > 1)
   float* scores;       // optional [B][Hq][S] log2-domain logits (eviction score)
   float* ml;           // optional [B][Hq][2] final (max, sum)
   int B, Hq, Hk, G, S, splits, keys_per_split;
@@ -44,45 +43,115 @@ struct DecodeArgs {
 };
 
 // ---------------------------------------------------------------------------
-// Q.K^T tile on MFMA.  Output lane layout of every 16x16 fp32 MFMA block:
-// lane l holds C[4*(l/16)+i][l%16], i = 0..3  (row = key, column = head).
+// Per-lane registers of one 16-key tile, loaded one tile ahead of use.
+//   K (MFMA A operand): lane l holds key row tile + l%16, 16-byte pieces at
+//     dims 32t + 8*(l/16) (f16/bf16) or 16t + 4*(l/16) (f32).
+//   V (P.V layout): lane l holds rows tile + 4*(l/16) + i, i = 0..3, dims
+//     (l%16)*DPL .. +DPL.
 // ---------------------------------------------------------------------------
 template <typename T, int D>
-struct QKTile;
+struct TileRegs {
+  static constexpr int KW = (sizeof(T) == 4) ? D / 16 : (D + 31) / 32;  // 16-byte K pieces
+  static constexpr int DPL = D / 16;
+  static constexpr int VB = DPL * (int)sizeof(T);                        // V bytes per row per lane
+  static constexpr int VWORDS = VB >= 4 ? VB / 4 : 1;
+  u32x4 k[KW];
+  uint32_t v[4][VWORDS];
+  uint32_t keep;  // bit i: key tile + 4*(l/16) + i is attended
+};
 
-template <int D>
-struct QKTile<half_t, D> {
-  static constexpr int NK = (D + 31) / 32;  // k-steps of 32 dims
-  half8 qb[NK];
-  // B operand: lane l supplies q[head l%16][32t + 8*(l/16) + j].
-  __device__ void load_q(const half_t* q0, int64_t q_sh, int col, int grp, int G) {
+template <typename T, int D>
+__device__ __forceinline__ void load_tile(TileRegs<T, D>& r, const T* kbase, const T* vbase, int64_t k_ss,
+                                          int64_t v_ss, int tile, int key_end, int col, int grp,
+                                          const DecodeArgs& a, int b, int hk, int64_t cur, const uint8_t* mrow) {
+  using R = TileRegs<T, D>;
+  // Key mask of this lane's four rows, evaluated here (one tile ahead) so
+  // that the MFMA, the reads of its result and the score selects of
+  // process_tile form one straight-line block.
+  uint32_t keep = 0;
 #pragma unroll
-    for (int t = 0; t < NK; ++t) {
-      const int d0 = 32 * t + 8 * grp;
-      half8 f = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (col < G && d0 < D) f = *reinterpret_cast<const half8*>(q0 + col * q_sh + d0);
-      qb[t] = f;
+  for (int i = 0; i < 4; ++i) {
+    const int key = tile + 4 * grp + i;
+    bool kp = key < key_end;
+    if (kp && mrow) kp = mrow[key] != 0;
+    if (kp && key < a.held_len)
+      kp = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key] != 0 && a.held_pos[b * a.hp_sb + hk * a.hp_sh + key] <= cur;
+    keep |= (kp ? 1u : 0u) << i;
+  }
+  r.keep = keep;
+  const int arow = tile + col;
+  const bool kok = arow < key_end;
+  const T* krow = kbase + (int64_t)arow * k_ss;
+#pragma unroll
+  for (int t = 0; t < R::KW; ++t) {
+    const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (kok && d0 < D) w = ld16(krow + d0);
+    r.k[t] = w;
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int key = tile + 4 * grp + i;
+    const char* p = reinterpret_cast<const char*>(vbase + (int64_t)key * v_ss + col * R::DPL);
+    if (key < key_end) {
+      if constexpr (R::VB >= 16) {
+#pragma unroll
+        for (int c = 0; c < R::VB / 16; ++c) {
+          const u32x4 x = ld16(p + 16 * c);
+          r.v[i][4 * c + 0] = x[0];
+          r.v[i][4 * c + 1] = x[1];
+          r.v[i][4 * c + 2] = x[2];
+          r.v[i][4 * c + 3] = x[3];
+        }
+      } else if constexpr (R::VB == 8) {
+        const u32x2 x = *reinterpret_cast<const u32x2*>(p);
+        r.v[i][0] = x[0];
+        r.v[i][1] = x[1];
+      } else if constexpr (R::VB == 4) {
+        r.v[i][0] = *reinterpret_cast<const uint32_t*>(p);
+      } else {
+        r.v[i][0] = (uint32_t)(*reinterpret_cast<const uint16_t*>(p));
+      }
+    } else {
+#pragma unroll
+      for (int c = 0; c < R::VWORDS; ++c) r.v[i][c] = 0u;
     }
   }
-  // A operand: lane l supplies key row (tile + l%16), dims 32t + 8*(l/16) + j.
-  __device__ floatx4 dot(const half_t* krow, bool ok, int grp) const {
-    floatx4 c = {0.f, 0.f, 0.f, 0.f};
+}
+
+// Q.K^T of one tile.  Output lane layout of every 16x16 fp32 MFMA block:
+// lane l holds C[4*(l/16)+i][l%16], i = 0..3  (row = key, column = head).
+template <typename T, int D>
+struct QFrag;
+
+template <int D>
+struct QFrag<half_t, D> {
+  static constexpr int NK = (D + 31) / 32;
+  half8 qb[NK];
+  // B operand: lane l supplies q[head l%16][32t + 8*(l/16) + j].
+  __device__ void load(const half_t* q0, int64_t q_sh, int col, int grp, int G) {
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
       const int d0 = 32 * t + 8 * grp;
-      half8 a = {0, 0, 0, 0, 0, 0, 0, 0};
-      if (ok && d0 < D) a = *reinterpret_cast<const half8*>(krow + d0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, qb[t], c, 0, 0, 0);
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (col < G && d0 < D) w = ld16(q0 + col * q_sh + d0);
+      qb[t] = __builtin_bit_cast(half8, w);
     }
+  }
+  __device__ floatx4 dot(const TileRegs<half_t, D>& r) const {
+    floatx4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int t = 0; t < NK; ++t)
+      c = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(half8, r.k[t]), qb[t], c, 0, 0, 0);
     return c;
   }
 };
 
 template <int D>
-struct QKTile<bf16_t, D> {
+struct QFrag<bf16_t, D> {
   static constexpr int NK = (D + 31) / 32;
   bf16x8 qb[NK];
-  __device__ void load_q(const bf16_t* q0, int64_t q_sh, int col, int grp, int G) {
+  __device__ void load(const bf16_t* q0, int64_t q_sh, int col, int grp, int G) {
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
       const int d0 = 32 * t + 8 * grp;
@@ -91,83 +160,133 @@ struct QKTile<bf16_t, D> {
       qb[t] = __builtin_bit_cast(bf16x8, w);
     }
   }
-  __device__ floatx4 dot(const bf16_t* krow, bool ok, int grp) const {
+  __device__ floatx4 dot(const TileRegs<bf16_t, D>& r) const {
     floatx4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int t = 0; t < NK; ++t) {
-      const int d0 = 32 * t + 8 * grp;
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (ok && d0 < D) w = ld16(krow + d0);
-      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, w), qb[t], c, 0, 0, 0);
-    }
+    for (int t = 0; t < NK; ++t)
+      c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, r.k[t]), qb[t], c, 0, 0, 0);
     return c;
   }
 };
 
 template <int D>
-struct QKTile<float, D> {
+struct QFrag<float, D> {
   // v_mfma_f32_16x16x4f32: lane l supplies A[l%16][l/16] and B[l/16][l%16].
-  // One 16-byte load per lane covers four MFMA steps: step j of block t uses
+  // One 16-byte piece per lane covers four MFMA steps: step j of block t uses
   // dim 16t + 4*(l/16) + j (a permutation of the block's 16 dims).
   static constexpr int NB = D / 16;
-  floatx4 qb[NB];
-  __device__ void load_q(const float* q0, int64_t q_sh, int col, int grp, int G) {
+  float qb[NB][4];
+  __device__ void load(const float* q0, int64_t q_sh, int col, int grp, int G) {
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
-      floatx4 f = {0.f, 0.f, 0.f, 0.f};
-      if (col < G) f = *reinterpret_cast<const floatx4*>(q0 + col * q_sh + 16 * t + 4 * grp);
-      qb[t] = f;
+      u32x4 w = {0u, 0u, 0u, 0u};
+      if (col < G) w = ld16(q0 + col * q_sh + 16 * t + 4 * grp);
+      // Whole-vector bit cast, then element reads: a bit cast of a single
+      // vector element miscompiles to element 0 with this toolchain.
+      const floatx4 f = __builtin_bit_cast(floatx4, w);
+      qb[t][0] = f[0];
+      qb[t][1] = f[1];
+      qb[t][2] = f[2];
+      qb[t][3] = f[3];
     }
   }
-  __device__ floatx4 dot(const float* krow, bool ok, int grp) const {
+  __device__ floatx4 dot(const TileRegs<float, D>& r) const {
     floatx4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
-      floatx4 a = {0.f, 0.f, 0.f, 0.f};
-      if (ok) a = *reinterpret_cast<const floatx4*>(krow + 16 * t + 4 * grp);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], qb[t][j], c, 0, 0, 0);
+      const floatx4 f = __builtin_bit_cast(floatx4, r.k[t]);
+      const float a0 = f[0];
+      const float a1 = f[1];
+      const float a2 = f[2];
+      const float a3 = f[3];
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(a0, qb[t][0], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(a1, qb[t][1], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(a2, qb[t][2], c, 0, 0, 0);
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(a3, qb[t][3], c, 0, 0, 0);
     }
     return c;
   }
 };
 
-// Load N contiguous elements of T starting at p (N*sizeof(T) is 2..64 bytes,
-// p aligned to that size up to 16 bytes) and widen to fp32.
-template <typename T, int N>
-__device__ __forceinline__ void load_row_f32(const T* p, float (&out)[N]) {
-  constexpr int BYTES = N * (int)sizeof(T);
-  constexpr int WORDS = BYTES >= 4 ? BYTES / 4 : 1;
-  uint32_t w[WORDS];
-  if constexpr (BYTES >= 16) {
-#pragma unroll
-    for (int i = 0; i < BYTES / 16; ++i) {
-      u32x4 x = ld16(reinterpret_cast<const char*>(p) + 16 * i);
-      w[4 * i + 0] = x[0];
-      w[4 * i + 1] = x[1];
-      w[4 * i + 2] = x[2];
-      w[4 * i + 3] = x[3];
-    }
-  } else if constexpr (BYTES == 8) {
-    u32x2 x = *reinterpret_cast<const u32x2*>(p);
-    w[0] = x[0];
-    w[1] = x[1];
-  } else if constexpr (BYTES == 4) {
-    w[0] = *reinterpret_cast<const uint32_t*>(p);
-  } else {  // 2 bytes: one half/bf16
-    w[0] = (uint32_t)(*reinterpret_cast<const uint16_t*>(p));
-  }
-#pragma unroll
-  for (int i = 0; i < N; ++i) out[i] = Unpack<T>::get(w, i);
-}
+// Online-softmax state of one lane: running max / partial sum of head `col`
+// and the P.V accumulators of the lane's dim slice for every head.
+template <int GM, int DPL>
+struct SoftmaxState {
+  float m_run;
+  float l_run;
+  float acc[GM][DPL];
+};
 
 template <typename T, int D, int GM>
+__device__ __forceinline__ void process_tile(const TileRegs<T, D>& r, const QFrag<T, D>& qf,
+                                             SoftmaxState<GM, D / 16>& st, const DecodeArgs& a, int b, int hk,
+                                             int tile, int key_end, int col, int grp, int64_t cur,
+                                             const uint8_t* mrow, float* srow) {
+  constexpr int DPL = D / 16;
+  const int G = a.G;
+  const floatx4 c = qf.dot(r);
+  const float c4[4] = {c[0], c[1], c[2], c[3]};
+  const uint32_t keep = (col < G) ? r.keep : 0u;
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = ((keep >> i) & 1u) ? c4[i] * a.scale_log2 : -INFINITY;
+  if (srow && col < G) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int key = tile + 4 * grp + i;
+      if (key < key_end) srow[key] = s[i];
+    }
+  }
+  float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+  tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+  const float m_new = fmaxf(st.m_run, tm);
+  const bool dead = (m_new == -INFINITY);
+  const float alpha = dead ? 1.f : exp2f(st.m_run - m_new);
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : exp2f(s[i] - m_new);
+  st.l_run = st.l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
+  st.m_run = m_new;
+
+  // P.V: lane (grp, col) handles keys tile + 4*grp + i, dims col*DPL ..
+  const int src = 16 * grp;
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+      if (g < G) {
+        const float ag = __shfl(alpha, src + g, 64);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) st.acc[g][j] *= ag;
+      }
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    float vv[DPL];
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) vv[j] = Unpack<T>::get(r.v[i], j);
+#pragma unroll
+    for (int g = 0; g < GM; ++g) {
+      if (g < G) {
+        const float pg = __shfl(p[i], src + g, 64);
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) st.acc[g][j] = fmaf(pg, vv[j], st.acc[g][j]);
+      }
+    }
+  }
+}
+
+// grid (splits, Hk, B), block 256 (4 waves).  Each wave takes every fourth
+// 16-key tile of the workgroup's key range, with the next tile's K/V loads in
+// flight while the current one is processed.
+template <typename T, int D, int GM>
 __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
-  constexpr int DPL = D / 16;  // dims per lane in the P.V layout
+  constexpr int DPL = D / 16;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
-  const int col = lane & 15;  // MFMA column (head) / P.V dim slice
-  const int grp = lane >> 4;  // MFMA row group / P.V row group
+  const int col = lane & 15;
+  const int grp = lane >> 4;
   const int split = blockIdx.x;
   const int hk = blockIdx.y;
   const int b = blockIdx.z;
@@ -178,115 +297,66 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
   const T* kbase = reinterpret_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const T* vbase = reinterpret_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
 
-  QKTile<T, D> qk;
-  qk.load_q(reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh, a.q_sh, col, grp, G);
+  QFrag<T, D> qf;
+  qf.load(reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh, a.q_sh, col, grp, G);
 
   const int64_t cur = a.cur_pos ? *a.cur_pos : INT64_MAX;
   const uint8_t* mrow = a.mask ? a.mask + b * a.mask_sb : nullptr;
   float* srow = a.scores ? a.scores + ((int64_t)b * a.Hq + hk * G + col) * a.S : nullptr;
 
-  float m_run = -INFINITY;  // running max (log2 domain) of head `col`
-  float l_run = 0.f;        // partial sum of head `col` over this row group's keys
-  float acc[GM][DPL];
+  SoftmaxState<GM, DPL> st;
+  st.m_run = -INFINITY;
+  st.l_run = 0.f;
 #pragma unroll
   for (int g = 0; g < GM; ++g)
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) acc[g][j] = 0.f;
+    for (int j = 0; j < DPL; ++j) st.acc[g][j] = 0.f;
 
-  for (int tile = key_begin + wave * 16; tile < key_end; tile += 64) {
-    // ---- scores: C[key = tile + 4*grp + i][head = col] ----
-    const int arow = tile + col;
-    const floatx4 c = qk.dot(kbase + (int64_t)arow * a.k_ss, arow < key_end, grp);
-    float s[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = tile + 4 * grp + i;
-      bool keep = key < key_end && col < G;
-      if (keep && mrow) keep = mrow[key] != 0;
-      if (keep && key < a.held_len)
-        keep = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key] != 0 &&
-               a.held_pos[b * a.hp_sb + hk * a.hp_sh + key] <= cur;
-      s[i] = keep ? c[i] * a.scale_log2 : -INFINITY;
-      if (srow && col < G && key < key_end) srow[key] = s[i];
-    }
-    float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-    tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-    tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
-    const float m_new = fmaxf(m_run, tm);
-    const bool dead = (m_new == -INFINITY);
-    const float alpha = dead ? 1.f : exp2f(m_run - m_new);
-    float p[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : exp2f(s[i] - m_new);
-    l_run = l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
-    m_run = m_new;
-
-    // ---- P.V: lane (grp, col) handles keys tile + 4*grp + i, dims col*DPL.. ----
-    const int src = 16 * grp;
-    const bool rescale = __any(alpha != 1.f);
-#pragma unroll
-    for (int g = 0; g < GM; ++g) {
-      if (g < G && rescale) {
-        const float ag = __shfl(alpha, src + g, 64);
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) acc[g][j] *= ag;
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = tile + 4 * grp + i;
-      float vv[DPL];
-      if (key < key_end) {
-        load_row_f32<T, DPL>(vbase + (int64_t)key * a.v_ss + col * DPL, vv);
-      } else {
-#pragma unroll
-        for (int j = 0; j < DPL; ++j) vv[j] = 0.f;
-      }
-#pragma unroll
-      for (int g = 0; g < GM; ++g) {
-        if (g < G) {
-          const float pg = __shfl(p[i], src + g, 64);
-#pragma unroll
-          for (int j = 0; j < DPL; ++j) acc[g][j] = fmaf(pg, vv[j], acc[g][j]);
-        }
-      }
-    }
+  TileRegs<T, D> ra, rb;
+  int tile = key_begin + wave * 16;
+  if (tile < key_end) load_tile<T, D>(ra, kbase, vbase, a.k_ss, a.v_ss, tile, key_end, col, grp, a, b, hk, cur, mrow);
+  while (tile < key_end) {
+    if (tile + 64 < key_end) load_tile<T, D>(rb, kbase, vbase, a.k_ss, a.v_ss, tile + 64, key_end, col, grp, a, b, hk, cur, mrow);
+    process_tile<T, D, GM>(ra, qf, st, a, b, hk, tile, key_end, col, grp, cur, mrow, srow);
+    tile += 64;
+    if (tile >= key_end) break;
+    if (tile + 64 < key_end) load_tile<T, D>(ra, kbase, vbase, a.k_ss, a.v_ss, tile + 64, key_end, col, grp, a, b, hk, cur, mrow);
+    process_tile<T, D, GM>(rb, qf, st, a, b, hk, tile, key_end, col, grp, cur, mrow, srow);
+    tile += 64;
   }
 
   // ---- reduce the four row groups of the wave (they share m_run) ----
+  float l_run = st.l_run;
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
 #pragma unroll
   for (int g = 0; g < GM; ++g)
 #pragma unroll
     for (int j = 0; j < DPL; ++j) {
-      float x = acc[g][j];
+      float x = st.acc[g][j];
       x += __shfl_xor(x, 16, 64);
       x += __shfl_xor(x, 32, 64);
-      acc[g][j] = x;
+      st.acc[g][j] = x;
     }
 
   __shared__ float sm_m[4][GM];
   __shared__ float sm_l[4][GM];
   __shared__ float sm_acc[4][GM][D];
-  __shared__ int sm_last;
   if (grp == 0) {
     if (col < GM) {
-      sm_m[wave][col] = m_run;
+      sm_m[wave][col] = st.m_run;
       sm_l[wave][col] = l_run;
     }
 #pragma unroll
     for (int g = 0; g < GM; ++g)
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) sm_acc[wave][g][col * DPL + j] = acc[g][j];
+      for (int j = 0; j < DPL; ++j) sm_acc[wave][g][col * DPL + j] = st.acc[g][j];
   }
   __syncthreads();
 
   const int unit = b * a.Hk + hk;
   const int stride_part = G * D + 2 * G;
   T* obase = reinterpret_cast<T*>(a.out) + b * a.o_sb + (int64_t)(hk * G) * a.o_sh;
-
-  // combine the four waves; element e = g*D + d
   for (int e = threadIdx.x; e < G * D; e += 256) {
     const int g = e / D, d = e - g * D;
     float M = -INFINITY;
@@ -316,31 +386,28 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
       }
     }
   }
-  if (a.splits == 1) return;
+}
 
-  // ---- last-arriving split combines ----
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const uint32_t ticket = atomicAdd(&a.counters[unit], 1u);
-    sm_last = (ticket == (uint32_t)(a.splits - 1));
-  }
-  __syncthreads();
-  if (!sm_last) return;
-  __threadfence();
-
+// Merge the split partials of every (b, kv head).  grid (Hk, B), block 256.
+template <typename T>
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int D) {
+  const int hk = blockIdx.x, b = blockIdx.y;
+  const int G = a.G;
+  const int unit = b * a.Hk + hk;
+  const int stride_part = G * D + 2 * G;
   const float* pu = a.part + (int64_t)unit * a.splits * stride_part;
-  for (int e = threadIdx.x; e < G * D; e += 256) {
+  T* obase = reinterpret_cast<T*>(a.out) + b * a.o_sb + (int64_t)(hk * G) * a.o_sh;
+  for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
     const int g = e / D, d = e - g * D;
     float M = -INFINITY;
-    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, __builtin_nontemporal_load(pu + s * stride_part + G * D + g));
+    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, pu[s * stride_part + G * D + g]);
     float A = 0.f, L = 0.f;
     if (M != -INFINITY) {
       for (int s = 0; s < a.splits; ++s) {
         const float* ps = pu + s * stride_part;
-        const float sc = exp2f(__builtin_nontemporal_load(ps + G * D + g) - M);
-        A = fmaf(__builtin_nontemporal_load(ps + e), sc, A);
-        L = fmaf(__builtin_nontemporal_load(ps + G * D + G + g), sc, L);
+        const float sc = exp2f(ps[G * D + g] - M);
+        A = fmaf(ps[e], sc, A);
+        L = fmaf(ps[G * D + G + g], sc, L);
       }
     }
     obase[g * a.o_sh + d] = from_f32<T>(A / L);
@@ -349,7 +416,6 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
       a.ml[((int64_t)b * a.Hq + hk * G + g) * 2 + 1] = L;
     }
   }
-  if (threadIdx.x == 0) a.counters[unit] = 0u;
 }
 
 // Per-token eviction score of the reference kernel (kernels.py:66-67, 134-136):
@@ -414,7 +480,9 @@ __global__ __launch_bounds__(256) void evict_score_kernel(const float* scores, c
 static int pick_splits(int64_t units, int64_t S, int64_t requested) {
   int64_t splits = requested;
   if (splits <= 0) {
-    const int64_t target_blocks = 1024;  // ~4 workgroups per CU on 256 CUs
+    // Enough workgroups to cover the 256 CUs about twice; a split smaller
+    // than 64 keys leaves waves of the workgroup idle.
+    const int64_t target_blocks = 512;
     splits = cdiv(target_blocks, units);
   }
   const int64_t max_splits = cdiv(S, 64);
@@ -427,7 +495,7 @@ static int pick_splits(int64_t units, int64_t S, int64_t requested) {
 static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 struct DecodeLayout {
-  int64_t counters_off, part_off, scores_off, ml_off, total;
+  int64_t part_off, scores_off, ml_off, total;
 };
 
 static DecodeLayout decode_layout(int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
@@ -435,8 +503,7 @@ static DecodeLayout decode_layout(int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
   DecodeLayout L;
   const int64_t units = B * Hk;
   const int64_t G = Hq / (Hk > 0 ? Hk : 1);
-  L.counters_off = 0;
-  L.part_off = align256(units * 4);
+  L.part_off = 0;
   const int64_t part_bytes = splits > 1 ? units * splits * (G * D + 2 * G) * 4 : 0;
   L.scores_off = align256(L.part_off + part_bytes);
   const int64_t scores_bytes = with_evict ? B * Hq * S * 4 : 0;
@@ -450,6 +517,8 @@ template <typename T, int D, int GM>
 static void launch_decode(const DecodeArgs& a, hipStream_t st) {
   dim3 grid(a.splits, a.Hk, a.B);
   hipLaunchKernelGGL((decode_attn_kernel<T, D, GM>), grid, dim3(256), 0, st, a);
+  if (a.splits > 1)
+    hipLaunchKernelGGL(decode_combine_kernel<T>, dim3(a.Hk, a.B), dim3(256), 0, st, a, D);
 }
 
 template <typename T, int D>
@@ -545,7 +614,6 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
   a.cur_pos = cur_pos; a.held_len = held_len;
   a.out = out; a.o_sb = o_sb; a.o_sh = o_sh;
   char* ws = reinterpret_cast<char*>(workspace);
-  a.counters = reinterpret_cast<uint32_t*>(ws + lay.counters_off);
   a.part = reinterpret_cast<float*>(ws + lay.part_off);
   a.scores = with_evict ? reinterpret_cast<float*>(ws + lay.scores_off) : nullptr;
   a.ml = with_evict ? reinterpret_cast<float*>(ws + lay.ml_off) : nullptr;

@@ -26,14 +26,15 @@
 
 namespace hc {
 
-constexpr int kChunk = 256;   // keys per logits/imp workgroup (one per lane)
+constexpr int kChunk = 256;   // keys per imp workgroup
+constexpr int kChunkM = 128;  // keys per logits workgroup (4 waves x 32 keys)
 constexpr int kRowBlk = 32;   // window rows per logits workgroup (fp64 accumulators)
 constexpr int kSumChunk = 512;  // keys per rowsum workgroup
 constexpr int kMaxW = 256;
 constexpr int kMaxPool = 64;  // max half-width of the pooling window
 
 struct ScoreLayout {
-  int64_t wpad, nchunk, qf_off, logits_off, cmax_off, lsum_off, total;
+  int64_t wpad, nchunk, nchunk_m, qf_off, logits_off, cmax_off, lsum_off, total;
 };
 
 static int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -42,10 +43,11 @@ static ScoreLayout score_layout(int64_t B, int64_t Hk, int64_t S, int64_t D, int
   ScoreLayout L;
   L.wpad = cdiv(W, kRowBlk) * kRowBlk;
   L.nchunk = cdiv(S, kChunk);
+  L.nchunk_m = cdiv(S, kChunkM);
   L.qf_off = 0;
   L.logits_off = al256(L.qf_off + B * Hk * L.wpad * D * 8);
   L.cmax_off = al256(L.logits_off + B * Hk * W * S * 4);
-  L.lsum_off = al256(L.cmax_off + B * Hk * L.nchunk * W * 4);
+  L.lsum_off = al256(L.cmax_off + B * Hk * L.nchunk_m * W * 4);
   L.total = al256(L.lsum_off + B * Hk * W * 8);
   return L;
 }
@@ -76,87 +78,154 @@ __global__ void qmean_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh
   *dst = sum / (double)G;
 }
 
-// Load 8 contiguous elements (d0..d0+7) of a key row as doubles.
+// Raw 16-byte pieces of one 8-dim chunk of a key row (16-bit types: one
+// piece; fp32: two).
 template <typename T>
-__device__ __forceinline__ void load8_f64(const T* p, double (&kd)[8]);
-template <>
-__device__ __forceinline__ void load8_f64<half_t>(const half_t* p, double (&kd)[8]) {
-  const u32x4 w = ld16(p);
-  const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
+struct KChunk {
+  static constexpr int N = (sizeof(T) == 4) ? 2 : 1;
+  uint32_t w[4 * N];
+};
+
+template <typename T>
+__device__ __forceinline__ void load_kchunk(KChunk<T>& c, const T* p, bool ok) {
 #pragma unroll
-  for (int j = 0; j < 8; ++j) kd[j] = (double)Unpack<half_t>::get(ww, j);
-}
-template <>
-__device__ __forceinline__ void load8_f64<bf16_t>(const bf16_t* p, double (&kd)[8]) {
-  const u32x4 w = ld16(p);
-  const uint32_t ww[4] = {w[0], w[1], w[2], w[3]};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kd[j] = (double)Unpack<bf16_t>::get(ww, j);
-}
-template <>
-__device__ __forceinline__ void load8_f64<float>(const float* p, double (&kd)[8]) {
-  const u32x4 w0 = ld16(p);
-  const u32x4 w1 = ld16(p + 4);
-  const uint32_t ww[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
-#pragma unroll
-  for (int j = 0; j < 8; ++j) kd[j] = (double)__builtin_bit_cast(float, ww[j]);
+  for (int i = 0; i < KChunk<T>::N; ++i) {
+    u32x4 x = {0u, 0u, 0u, 0u};
+    if (ok) x = ld16(reinterpret_cast<const char*>(p) + 16 * i);
+    c.w[4 * i + 0] = x[0];
+    c.w[4 * i + 1] = x[1];
+    c.w[4 * i + 2] = x[2];
+    c.w[4 * i + 3] = x[3];
+  }
 }
 
-// grid (nchunk, Hk * nrb, B), block 256: one key per lane, 32 window rows per
-// workgroup held as fp64 accumulators; qf is wave-uniform (scalar loads).
+// Element j (0..7) of the chunk as an exact double, j chosen per lane.
+template <typename T>
+__device__ __forceinline__ double kchunk_elem(const KChunk<T>& c, int j);
+template <>
+__device__ __forceinline__ double kchunk_elem<half_t>(const KChunk<half_t>& c, int j) {
+  const uint32_t word = (j & 4) ? ((j & 2) ? c.w[3] : c.w[2]) : ((j & 2) ? c.w[1] : c.w[0]);
+  const uint16_t bits = (uint16_t)((j & 1) ? (word >> 16) : (word & 0xffffu));
+  return (double)(float)__builtin_bit_cast(half_t, bits);
+}
+template <>
+__device__ __forceinline__ double kchunk_elem<bf16_t>(const KChunk<bf16_t>& c, int j) {
+  const uint32_t word = (j & 4) ? ((j & 2) ? c.w[3] : c.w[2]) : ((j & 2) ? c.w[1] : c.w[0]);
+  const uint32_t bits = (j & 1) ? (word & 0xffff0000u) : (word << 16);
+  return (double)__uint_as_float(bits);
+}
+template <>
+__device__ __forceinline__ double kchunk_elem<float>(const KChunk<float>& c, int j) {
+  const uint32_t lo = (j & 2) ? ((j & 1) ? c.w[3] : c.w[2]) : ((j & 1) ? c.w[1] : c.w[0]);
+  const uint32_t hi = (j & 2) ? ((j & 1) ? c.w[7] : c.w[6]) : ((j & 1) ? c.w[5] : c.w[4]);
+  return (double)__uint_as_float((j & 4) ? hi : lo);
+}
+
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+
+// Window logits on the fp64 matrix cores.  v_mfma_f64_16x16x4f64 computes
+// every output as a sequential IEEE fma chain over its four k terms in
+// ascending k, so chaining the k-steps over d = 4t + k reproduces exactly the
+// fma chain over ascending d that defines the scores.
+//   A (16 rows x 4): lane l supplies qf[w0 + 16*nb + l%16][4t + l/16]
+//   B (4 x 16 keys): lane l supplies k[key0 + 16*mb + l%16][4t + l/16]
+//   D: lane l holds rows w0 + 16*nb + l/16 + 4i, key key0 + 16*mb + l%16
+// grid (ceil(S/128), Hk * nrb, B), block 256: each wave covers 32 keys
+// (two 16-key blocks) x 32 window rows (two 16-row blocks).
 template <typename T>
 __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, int64_t k_sb, int64_t k_sh,
-                                                     int64_t k_ss, const double* __restrict__ qf, int Hk,
-                                                     int S, int D, int W, int wpad, int mode, double scaling,
+                                                     int64_t k_ss, const double* __restrict__ qf, int Hk, int S,
+                                                     int D, int W, int wpad, int mode, double scaling,
                                                      float* __restrict__ logits, float* __restrict__ cmax,
                                                      uint64_t* __restrict__ lsum) {
+  extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
   const int nrb = wpad / kRowBlk;
   const int rb = blockIdx.y % nrb;
   const int h = blockIdx.y / nrb;
   const int b = blockIdx.z;
   const int chunk = blockIdx.x;
-  const int s = chunk * kChunk + threadIdx.x;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int col = lane & 15, kk = lane >> 4;
   const int w0 = rb * kRowBlk;
   const int nw = min(kRowBlk, W - w0);
   const int64_t bh = (int64_t)b * Hk + h;
-  const double* qrow = qf + (bh * wpad + w0) * D;
+  const int ld = D + 1;
+  const double* qsrc = qf + (bh * wpad + w0) * D;
+  for (int i = threadIdx.x; i < kRowBlk * D; i += 256) sq[(i / D) * ld + (i % D)] = qsrc[i];
+  __syncthreads();
 
-  double acc[kRowBlk];
-#pragma unroll
-  for (int w = 0; w < kRowBlk; ++w) acc[w] = 0.0;
+  const int key0 = chunk * kChunkM + wave * 32;
+  const T* kb = k + b * k_sb + h * k_sh;
+  const int r0 = key0 + col, r1 = key0 + 16 + col;
+  const T* kr0 = kb + (int64_t)min(r0, S - 1) * k_ss;
+  const T* kr1 = kb + (int64_t)min(r1, S - 1) * k_ss;
+  const bool ok0 = r0 < S, ok1 = r1 < S;
+  const double* q0 = sq + col * ld + kk;         // rows 0..15 of the block
+  const double* q1 = sq + (16 + col) * ld + kk;  // rows 16..31
 
-  if (s < S) {
-    const T* krow = k + b * k_sb + h * k_sh + (int64_t)s * k_ss;
-    for (int d0 = 0; d0 < D; d0 += 8) {
-      double kd[8];
-      load8_f64<T>(krow + d0, kd);
+  doublex4 acc00 = {0.0, 0.0, 0.0, 0.0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
+  KChunk<T> ca, cb;
+  load_kchunk<T>(ca, kr0, ok0);
+  load_kchunk<T>(cb, kr1, ok1);
+  for (int d0 = 0; d0 < D; d0 += 8) {
+    KChunk<T> na, nb;
+    const bool more = d0 + 8 < D;
+    if (more) {
+      load_kchunk<T>(na, kr0 + d0 + 8, ok0);
+      load_kchunk<T>(nb, kr1 + d0 + 8, ok1);
+    }
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-#pragma unroll
-        for (int w = 0; w < kRowBlk; ++w) acc[w] = __builtin_fma(qrow[w * D + d0 + j], kd[j], acc[w]);
-      }
+    for (int half = 0; half < 2; ++half) {  // k-steps t = d0/4 + half
+      const int d = d0 + 4 * half;
+      const double a0 = q0[d], a1 = q1[d];
+      const double b0 = kchunk_elem<T>(ca, 4 * half + kk);
+      const double b1 = kchunk_elem<T>(cb, 4 * half + kk);
+      acc00 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc00, 0, 0, 0);
+      acc01 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc01, 0, 0, 0);
+      acc10 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc10, 0, 0, 0);
+      acc11 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc11, 0, 0, 0);
+    }
+    if (more) {
+      ca = na;
+      cb = nb;
     }
   }
 
+  // Epilogue: lane holds rows w0 + 16*nb + kk + 4i for key key0 + 16*mb + col.
+  const double r00[4] = {acc00[0], acc00[1], acc00[2], acc00[3]};
+  const double r01[4] = {acc01[0], acc01[1], acc01[2], acc01[3]};
+  const double r10[4] = {acc10[0], acc10[1], acc10[2], acc10[3]};
+  const double r11[4] = {acc11[0], acc11[1], acc11[2], acc11[3]};
   __shared__ float red[4][kRowBlk];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int qpos0 = S - W + w0;  // absolute position of window row w0
+  const int qpos0 = S - W + w0;
 #pragma unroll
-  for (int w = 0; w < kRowBlk; ++w) {
-    if (w < nw) {
-      float L = -INFINITY;
-      if (s < S) {
+  for (int nbk = 0; nbk < 2; ++nbk) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int w = 16 * nbk + kk + 4 * i;  // row within the block
+      float m = -INFINITY;
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
+        const double v = nbk == 0 ? (mb == 0 ? r00[i] : r10[i]) : (mb == 0 ? r01[i] : r11[i]);
+        const int key = key0 + 16 * mb + col;
+        float L;
         if (mode == HC_SCORE_SNAPKV) {
-          L = (float)(acc[w] * scaling);
-          if (s > qpos0 + w) L = -INFINITY;
+          L = (key > qpos0 + w) ? -INFINITY : (float)(v * scaling);
         } else {
-          L = (float)(acc[w] / scaling);
+          L = (float)(v / scaling);
         }
-        logits[(bh * W + w0 + w) * S + s] = L;
+        if (key < S && w < nw) {
+          logits[(bh * W + w0 + w) * S + key] = L;
+          m = fmaxf(m, L);
+        }
       }
       if (mode == HC_SCORE_SNAPKV) {
-        const float m = wave_max(L);
-        if (lane == 0) red[wave][w] = m;
+        // max over the 16 lanes that share this row (same kk)
+        m = fmaxf(m, __shfl_xor(m, 1, 64));
+        m = fmaxf(m, __shfl_xor(m, 2, 64));
+        m = fmaxf(m, __shfl_xor(m, 4, 64));
+        m = fmaxf(m, __shfl_xor(m, 8, 64));
+        if (col == 0) red[wave][w] = m;
       }
     }
   }
@@ -289,16 +358,19 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
   hipLaunchKernelGGL(qmean_kernel<T>, dim3((unsigned)lay.wpad, (unsigned)Hk, (unsigned)B),
                      dim3((unsigned)(D < 64 ? 64 : D)), 0, st, (const T*)q, q_sb, q_sh, q_ss, q_row0, (int)Hq,
                      (int)Hk, (int)W, (int)lay.wpad, (int)D, qf);
-  hipLaunchKernelGGL(logits_kernel<T>, dim3((unsigned)lay.nchunk, (unsigned)(Hk * nrb), (unsigned)B), dim3(256),
-                     0, st, (const T*)k, k_sb, k_sh, k_ss, (const double*)qf, (int)Hk, (int)S, (int)D, (int)W,
-                     (int)lay.wpad, mode, scal, logits, cmax, lsum);
+  const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
+  if (lds > 65536)
+    (void)hipFuncSetAttribute((const void*)logits_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+  hipLaunchKernelGGL(logits_kernel<T>, dim3((unsigned)lay.nchunk_m, (unsigned)(Hk * nrb), (unsigned)B), dim3(256),
+                     lds, st, (const T*)k, k_sb, k_sh, k_ss, (const double*)qf, (int)Hk,
+                     (int)S, (int)D, (int)W, (int)lay.wpad, mode, scal, logits, cmax, lsum);
   if (mode == HC_SCORE_SNAPKV)
     hipLaunchKernelGGL(rowsum_kernel, dim3((unsigned)cdiv(S, kSumChunk), (unsigned)Hk, (unsigned)B), dim3(256), 0,
-                       st, (const float*)logits, (const float*)cmax, (int)Hk, (int)S, (int)W, (int)lay.nchunk,
+                       st, (const float*)logits, (const float*)cmax, (int)Hk, (int)S, (int)W, (int)lay.nchunk_m,
                        lsum);
   hipLaunchKernelGGL(imp_pool_kernel, dim3((unsigned)lay.nchunk, (unsigned)Hk, (unsigned)B), dim3(256), 0, st,
                      (const float*)logits, (const float*)cmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W,
-                     (int)lay.nchunk, mode, P, pooling, ksize, scores);
+                     (int)lay.nchunk_m, mode, P, pooling, ksize, scores);
 }
 
 }  // namespace hc
@@ -321,7 +393,7 @@ extern "C" int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64
   HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && S > 0 && D > 0 && W > 0, "score: empty shape");
   HC_REQUIRE(W <= S, "score: window %lld exceeds S %lld", (long long)W, (long long)S);
   HC_REQUIRE(W <= kMaxW, "score: window %lld above the supported %d rows", (long long)W, kMaxW);
-  HC_REQUIRE(D % 8 == 0 && D <= 1024, "score: head_dim %lld must be a multiple of 8 and <= 1024", (long long)D);
+  HC_REQUIRE(D % 8 == 0 && D <= 512, "score: head_dim %lld must be a multiple of 8 and <= 512", (long long)D);
   HC_REQUIRE(S <= ((int64_t)1 << 19), "score: S %lld above 2^19 (fixed-point normaliser range)", (long long)S);
   HC_REQUIRE(B <= 65535 && Hk * cdiv(W, kRowBlk) <= 65535, "score: grid too large");
   HC_REQUIRE(q_row0 >= 0, "score: negative q_row0");

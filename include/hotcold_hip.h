@@ -62,11 +62,10 @@ const char* hc_last_error(void);
  *   evict_loss / evict_idx (may be NULL): the per-token eviction score
  *     mean_h(mean_d|p v| / l) rounded to dtype, [B][S] float, and its
  *     first-index argmin [B] int64 (kernels.py:66-67, 134-136).
- *   num_splits <= 0 picks a split count; the workspace must hold
+ *   num_splits <= 0 picks a split count; with more than one split the
+ *     partial results are merged by a second kernel.  The workspace must hold
  *     hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, with_evict)
- *     bytes and be zero-filled once before its first use (the kernels leave
- *     it zeroed again).  One workspace must not be used by two launches that
- *     may overlap.
+ *     bytes; one workspace must not be used by two launches that may overlap.
  *   dropout must be 0.0.
  */
 int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hk, int64_t D,

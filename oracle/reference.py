@@ -407,3 +407,41 @@ class ColdStore:
         ip = keys @ q
         order = np.argsort(-ip, kind="stable")[: min(r, n)]
         return [int(i) for i in order]
+
+
+# ---------------------------------------------------------------------------
+# Literal torch-CPU reference path, timed as the CPU baseline by bench.py
+# ---------------------------------------------------------------------------
+def keep_index_torch(scores, window_size, budget):
+    """scoring.py:110-132 verbatim in torch (topk + sort + cat)."""
+    B, Hk, S = scores.shape
+    window = min(window_size, S)
+    prefix_len = S - window
+    keep_prefix = max(0, min(budget - window, prefix_len))
+    recent = torch.arange(prefix_len, S).view(1, 1, window).expand(B, Hk, window)
+    if keep_prefix <= 0:
+        return recent.contiguous()
+    top = torch.topk(scores[:, :, :prefix_len], k=keep_prefix, dim=-1).indices
+    top, _ = torch.sort(top, dim=-1)
+    return torch.cat([top, recent], dim=-1)
+
+
+def press_compress_torch(q_post, keys, values, window_size, budget, scaling, kernel_size=7, pooling="maxpool"):
+    """PressLayerState._compress after prefill scoring (layer_state.py:68-94)
+    on the CPU: snapkv_importance -> keep_index -> gather_kv x2."""
+    imp = snapkv_importance_torch(q_post, keys, window_size, scaling, kernel_size, pooling, dtype=keys.dtype)
+    keep = keep_index_torch(imp, window_size, budget)
+    B, H, _, D = keys.shape
+    idx = keep.unsqueeze(-1).expand(B, H, keep.shape[-1], D)
+    return keys.gather(2, idx).contiguous(), values.gather(2, idx).contiguous()
+
+
+def press_decode_torch(q_post, keys, values, k_new, v_new, scaling):
+    """PressLayerState.decode for SnapKV (layer_state.py:96-100, 115-116, 49-53):
+    cat the new token, repeat_kv, SDPA."""
+    keys = torch.cat([keys, k_new], dim=2)
+    values = torch.cat([values, v_new], dim=2)
+    n_rep = q_post.shape[1] // keys.shape[1]
+    out = torch.nn.functional.scaled_dot_product_attention(
+        q_post, repeat_kv(keys, n_rep), repeat_kv(values, n_rep), is_causal=False, scale=scaling)
+    return out.to(q_post.dtype), keys, values
