@@ -142,18 +142,19 @@ __device__ __forceinline__ double det_exp_nonpos(double x) {
   p = __builtin_fma(p, r, 5.00000000000000000000e-01);   // 1/2!
   p = __builtin_fma(p, r, 1.0);
   p = __builtin_fma(p, r, 1.0);
-  const int64_t k = (int64_t)kf;  // in [-1022, 0]
-  const double scale = __builtin_bit_cast(double, (uint64_t)(k + 1023) << 52);
-  return p * scale;
+  // p * 2^k with k in [-1022, 0]: exact scaling, as multiplying by the
+  // double 2^k would be.
+  return __builtin_ldexp(p, (int)kf);
 }
 
-// Fixed-point quantum of the softmax normaliser: e in [0,1] -> round(e * 2^44).
+// Fixed-point quantum of the softmax normaliser: e in [0,1] -> rint(e * 2^44).
+// fma(e, 2^44, 2^52) lands in [2^52, 2^53) where the spacing of doubles is 1,
+// so its single rounding is round-to-nearest-even of e * 2^44 and the low
+// mantissa bits are that integer.
 #define HC_FIX_SHIFT 44
 __device__ __forceinline__ uint64_t det_fix(double e) {
-  const double t = __builtin_rint(e * 17592186044416.0);  // 2^44, exact scaling
-  const uint32_t hi = (uint32_t)(t * (1.0 / 4294967296.0));
-  const double lo = t - (double)hi * 4294967296.0;
-  return ((uint64_t)hi << 32) | (uint64_t)(uint32_t)lo;
+  const double t = __builtin_fma(e, 17592186044416.0, 4503599627370496.0);  // e * 2^44 + 2^52
+  return __builtin_bit_cast(uint64_t, t) - 0x4330000000000000ull;
 }
 
 // Total order key for fp32 scores: larger score -> larger key; -0 == +0;

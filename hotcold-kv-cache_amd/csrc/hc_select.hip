@@ -19,15 +19,19 @@ namespace hc {
 
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / 64;
+constexpr int kTopkCache = 32768;  // prefix keys cached in LDS (128 KiB)
 
-// Block-wide exclusive prefix count of `flag` in thread order; returns the
-// rank and writes the block total to *total.  Uses one ballot per wave.
-__device__ __forceinline__ int block_rank(bool flag, int* sm_wave, int* total) {
+// Block-wide exclusive prefix sum of v in thread order (wave scans plus one
+// pass over the wave totals); writes the block total to *total.
+__device__ __forceinline__ int block_excl_scan(int v, int* sm_wave, int* total) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint64_t bal = __ballot(flag);
-  const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-  const int in_wave = __popcll(bal & lt);
-  if (lane == 0) sm_wave[wave] = __popcll(bal);
+  int incl = v;
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const int y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
+  }
+  if (lane == 63) sm_wave[wave] = incl;
   __syncthreads();
   int before = 0, tot = 0;
   for (int w = 0; w < kTopkWaves; ++w) {
@@ -37,23 +41,63 @@ __device__ __forceinline__ int block_rank(bool flag, int* sm_wave, int* total) {
   }
   __syncthreads();
   *total = tot;
-  return before + in_wave;
+  return before + incl - v;
 }
 
+// Digit search of one radix pass: the largest digit d with
+// count(digits > d) < krem <= count(digits >= d), by a scan over the 256
+// bins in descending order on threads 0..255.
+__device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, uint32_t* sm_scan,
+                                           uint32_t* sm_digit, uint32_t* sm_krem) {
+  const int t = threadIdx.x;
+  const int lane = t & 63, wave = t >> 6;
+  uint32_t cnt = 0, incl = 0;
+  if (t < 256) {
+    cnt = hist[255 - t];
+    incl = cnt;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+      const uint32_t y = __shfl_up(incl, o, 64);
+      if (lane >= o) incl += y;
+    }
+    if (lane == 63) sm_scan[wave] = incl;
+  }
+  __syncthreads();
+  if (t < 256) {
+    for (int w = 0; w < wave; ++w) incl += sm_scan[w];
+    const uint32_t excl = incl - cnt;
+    if (excl < krem && incl >= krem) {
+      *sm_digit = (uint32_t)(255 - t);
+      *sm_krem = krem - excl;
+    }
+  }
+  __syncthreads();
+}
+
+// One workgroup per (batch, head).  The prefix's order keys are cached in
+// LDS when they fit (prefix <= kTopkCache), otherwise re-read from global.
 __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __restrict__ scores, int64_t s_sb,
                                                                  int64_t s_sh, int H, int prefix, int keep_prefix,
                                                                  int window, int64_t* __restrict__ keep,
                                                                  int64_t* __restrict__ evicted) {
+  extern __shared__ uint32_t skey[];
   const int h = blockIdx.x, b = blockIdx.y;
   const float* sc = scores + b * s_sb + h * s_sh;
   const int n_keep = keep_prefix + window;
   int64_t* out = keep + ((int64_t)b * H + h) * n_keep;
   const int n_ev = prefix - keep_prefix;
   int64_t* ev = evicted ? evicted + ((int64_t)b * H + h) * n_ev : nullptr;
+  const bool cached = prefix <= kTopkCache;
 
   __shared__ uint32_t hist[256];
+  __shared__ uint32_t sm_scan[4];
   __shared__ uint32_t sm_digit, sm_krem;
   __shared__ int sm_wave[kTopkWaves];
+
+  if (cached && keep_prefix > 0) {
+    for (int i = threadIdx.x; i < prefix; i += kTopkThreads) skey[i] = order_key(sc[i]);
+    __syncthreads();
+  }
 
   uint32_t tkey = 0;
   int need_eq = 0;
@@ -64,21 +108,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
       for (int i = threadIdx.x; i < 256; i += kTopkThreads) hist[i] = 0;
       __syncthreads();
       for (int i = threadIdx.x; i < prefix; i += kTopkThreads) {
-        const uint32_t key = order_key(sc[i]);
+        const uint32_t key = cached ? skey[i] : order_key(sc[i]);
         if ((key & pmask) == pbits) atomicAdd(&hist[(key >> shift) & 255u], 1u);
       }
       __syncthreads();
-      if (threadIdx.x == 0) {
-        uint32_t cum = 0;
-        int d = 255;
-        for (; d > 0; --d) {
-          if (cum + hist[d] >= krem) break;
-          cum += hist[d];
-        }
-        sm_digit = (uint32_t)d;
-        sm_krem = krem - cum;
-      }
-      __syncthreads();
+      find_digit(hist, krem, sm_scan, &sm_digit, &sm_krem);
       pbits |= sm_digit << shift;
       pmask |= 255u << shift;
       krem = sm_krem;
@@ -88,26 +122,39 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
     need_eq = (int)krem;
   }
 
-  int base_sel = 0, base_eq = 0, base_ev = 0;
-  for (int t0 = 0; t0 < prefix; t0 += kTopkThreads) {
-    const int i = t0 + threadIdx.x;
-    const bool in = i < prefix;
-    uint32_t key = 0;
-    if (in && keep_prefix > 0) key = order_key(sc[i]);
-    const bool gt = in && keep_prefix > 0 && key > tkey;
-    const bool eq = in && keep_prefix > 0 && key == tkey;
-    int tot_eq;
-    const int eq_rank = base_eq + block_rank(eq, sm_wave, &tot_eq);
-    const bool sel = gt || (eq && eq_rank < need_eq);
-    int tot_sel;
-    const int pos = base_sel + block_rank(sel, sm_wave, &tot_sel);
-    if (sel) out[pos] = i;
-    int tot_ev;
-    const int epos = base_ev + block_rank(in && !sel, sm_wave, &tot_ev);
-    if (ev && in && !sel) ev[epos] = i;
-    base_sel += tot_sel;
-    base_eq += tot_eq;
-    base_ev += tot_ev;
+  // Each thread owns a contiguous run of the prefix; two block scans give
+  // every run its first output slot, so the kept indices come out ascending.
+  const int run = (prefix + kTopkThreads - 1) / kTopkThreads;
+  const int i0 = min(prefix, (int)threadIdx.x * run);
+  const int i1 = min(prefix, i0 + run);
+  int n_gt = 0, n_eq = 0;
+  if (keep_prefix > 0) {
+    for (int i = i0; i < i1; ++i) {
+      const uint32_t key = cached ? skey[i] : order_key(sc[i]);
+      n_gt += key > tkey;
+      n_eq += key == tkey;
+    }
+  }
+  int tot;
+  const int eq_before = block_excl_scan(n_eq, sm_wave, &tot);
+  const int take_eq = max(0, min(need_eq - eq_before, n_eq));
+  const int sel_before = block_excl_scan(n_gt + take_eq, sm_wave, &tot);
+  int pos = sel_before;
+  int epos = i0 - sel_before;
+  int eq_seen = 0;
+  for (int i = i0; i < i1; ++i) {
+    bool sel = false;
+    if (keep_prefix > 0) {
+      const uint32_t key = cached ? skey[i] : order_key(sc[i]);
+      if (key > tkey) {
+        sel = true;
+      } else if (key == tkey) {
+        sel = eq_seen < take_eq;
+        ++eq_seen;
+      }
+    }
+    if (sel) out[pos++] = i;
+    else if (ev) ev[epos++] = i;
   }
   for (int j = threadIdx.x; j < window; j += kTopkThreads) out[keep_prefix + j] = prefix + j;
 }
@@ -217,7 +264,16 @@ extern "C" int hc_topk_keep(int64_t B, int64_t H, int64_t S, const float* scores
   int64_t kp = budget - win;
   if (kp > prefix) kp = prefix;
   if (kp < 0) kp = 0;
-  hipLaunchKernelGGL(topk_keep_kernel, dim3((unsigned)H, (unsigned)B), dim3(kTopkThreads), 0,
+  const size_t lds = (kp > 0 && prefix <= kTopkCache) ? (size_t)prefix * 4 : 0;
+  if (lds > 65536) {
+    static bool attr_set = false;
+    if (!attr_set) {
+      (void)hipFuncSetAttribute((const void*)topk_keep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                kTopkCache * 4);
+      attr_set = true;
+    }
+  }
+  hipLaunchKernelGGL(topk_keep_kernel, dim3((unsigned)H, (unsigned)B), dim3(kTopkThreads), lds,
                      reinterpret_cast<hipStream_t>(stream), scores, s_sb, s_sh, (int)H, (int)prefix, (int)kp,
                      (int)win, keep, evicted);
   return check_launch("topk_keep");

@@ -19,22 +19,21 @@
 //
 // Kernels (one stream, in order):
 //   qmean   -> qf (fp64 [B][Hk][Wpad][D], rows >= W zeroed)
-//   logits  -> L (fp32 [B][Hk][W][S]) + per-256-key-chunk row max
+//   logits  -> L (fp32 [B][Hk][W][S]) + row max (atomicMax on order keys)
 //   rowsum  -> l_w (uint64, 64-bit atomics)            [SNAPKV only]
 //   imp     -> pooled fp32 scores [B][Hk][S]
 #include "hc_common.h"
 
 namespace hc {
 
-constexpr int kChunk = 256;   // keys per imp workgroup
 constexpr int kChunkM = 128;  // keys per logits workgroup (4 waves x 32 keys)
 constexpr int kRowBlk = 32;   // window rows per logits workgroup (fp64 accumulators)
-constexpr int kSumChunk = 512;  // keys per rowsum workgroup
+constexpr int kSumChunk = 512;  // keys per rowsum workgroup (two per lane)
 constexpr int kMaxW = 256;
-constexpr int kMaxPool = 64;  // max half-width of the pooling window
+constexpr int kMaxPool = 32;  // max half-width of the pooling window
 
 struct ScoreLayout {
-  int64_t wpad, nchunk, nchunk_m, qf_off, logits_off, cmax_off, lsum_off, total;
+  int64_t wpad, nchunk_m, qf_off, logits_off, rmax_off, lsum_off, total;
 };
 
 static int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -42,22 +41,28 @@ static int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 static ScoreLayout score_layout(int64_t B, int64_t Hk, int64_t S, int64_t D, int64_t W) {
   ScoreLayout L;
   L.wpad = cdiv(W, kRowBlk) * kRowBlk;
-  L.nchunk = cdiv(S, kChunk);
   L.nchunk_m = cdiv(S, kChunkM);
   L.qf_off = 0;
   L.logits_off = al256(L.qf_off + B * Hk * L.wpad * D * 8);
-  L.cmax_off = al256(L.logits_off + B * Hk * W * S * 4);
-  L.lsum_off = al256(L.cmax_off + B * Hk * L.nchunk_m * W * 4);
+  L.rmax_off = al256(L.logits_off + B * Hk * W * S * 4);
+  L.lsum_off = al256(L.rmax_off + B * Hk * W * 4);
   L.total = al256(L.lsum_off + B * Hk * W * 8);
   return L;
 }
 
 // qf[b][h][w][d] for w < wpad (zero rows past W).  grid (wpad, Hk, B), block D.
+// Also resets the row-max keys (to the key of -inf) and the fixed-point
+// row sums that the following kernels accumulate into.
 template <typename T>
 __global__ void qmean_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_row0,
-                             int Hq, int Hk, int W, int wpad, int D, double* __restrict__ qf) {
+                             int Hq, int Hk, int W, int wpad, int D, double* __restrict__ qf,
+                             uint32_t* __restrict__ rmax, uint64_t* __restrict__ lsum) {
   const int w = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int d = threadIdx.x;
+  if (d == 0 && w < W) {
+    rmax[((int64_t)b * Hk + h) * W + w] = order_key(-INFINITY);
+    lsum[((int64_t)b * Hk + h) * W + w] = 0ull;
+  }
   if (d >= D) return;
   double* dst = qf + (((int64_t)b * Hk + h) * wpad + w) * D + d;
   if (w >= W) {
@@ -136,8 +141,7 @@ template <typename T>
 __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, int64_t k_sb, int64_t k_sh,
                                                      int64_t k_ss, const double* __restrict__ qf, int Hk, int S,
                                                      int D, int W, int wpad, int mode, double scaling,
-                                                     float* __restrict__ logits, float* __restrict__ cmax,
-                                                     uint64_t* __restrict__ lsum) {
+                                                     float* __restrict__ logits, uint32_t* __restrict__ rmax) {
   extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
   const int nrb = wpad / kRowBlk;
   const int rb = blockIdx.y % nrb;
@@ -234,101 +238,152 @@ __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, in
   if (threadIdx.x < nw) {
     const int w = threadIdx.x;
     const float m = fmaxf(fmaxf(red[0][w], red[1][w]), fmaxf(red[2][w], red[3][w]));
-    cmax[(bh * gridDim.x + chunk) * W + w0 + w] = m;
-    if (chunk == 0) lsum[bh * W + w0 + w] = 0ull;
+    atomicMax(&rmax[bh * W + w0 + w], order_key(m));
   }
 }
 
-// Row maxima from the per-chunk maxima.  m[w] for w < W into shared memory.
-__device__ __forceinline__ void load_row_max(const float* cmax, int64_t bh, int nchunk, int W, float* sm_m) {
-  for (int w = threadIdx.x; w < W; w += blockDim.x) {
-    float m = -INFINITY;
-    for (int c = 0; c < nchunk; ++c) m = fmaxf(m, cmax[(bh * nchunk + c) * W + w]);
-    sm_m[w] = m;
-  }
+// Inverse of order_key for non-NaN keys.
+__device__ __forceinline__ float key_to_float(uint32_t k) {
+  return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// grid (ceil(S/512), Hk, B), block 256: exact fixed-point softmax denominators.
+// grid (ceil(S/kSumChunk), Hk, B), block 256: exact fixed-point softmax
+// denominators.  Each lane accumulates its keys for 16 rows at a time; a
+// butterfly reduce-scatter then leaves the wave sum of row (lane >> 2) in
+// lanes 4r .. 4r+3 (16 exchanges per row block instead of a full reduction
+// per row).
+constexpr int kSumRows = 16;
 __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ logits,
-                                                     const float* __restrict__ cmax, int Hk, int S, int W,
-                                                     int nchunk, uint64_t* __restrict__ lsum) {
+                                                     const uint32_t* __restrict__ rmax, int Hk, int S, int W,
+                                                     uint64_t* __restrict__ lsum) {
   const int h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * Hk + h;
   __shared__ float sm_m[kMaxW];
-  load_row_max(cmax, bh, nchunk, W, sm_m);
+  __shared__ uint64_t sm_red[4][kSumRows];
+  for (int w = threadIdx.x; w < W; w += blockDim.x) sm_m[w] = key_to_float(rmax[bh * W + w]);
   __syncthreads();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int s0 = blockIdx.x * kSumChunk + threadIdx.x;
-  const int lane = threadIdx.x & 63;
-  for (int w = 0; w < W; ++w) {
-    const double m = (double)sm_m[w];
-    const float* row = logits + (bh * W + w) * S;
-    uint64_t part = 0;
+  for (int w0 = 0; w0 < W; w0 += kSumRows) {
+    const int nw = min(kSumRows, W - w0);
+    uint64_t acc[kSumRows];
 #pragma unroll
+    for (int w = 0; w < kSumRows; ++w) acc[w] = 0;
+#pragma unroll 1
     for (int i = 0; i < kSumChunk / 256; ++i) {
       const int s = s0 + 256 * i;
-      if (s < S) part += det_fix(det_exp_nonpos((double)row[s] - m));
+      if (s < S) {
+        float L[kSumRows];
+        const float* pr = logits + (bh * W + w0) * S + s;
+#pragma unroll
+        for (int w = 0; w < kSumRows; ++w) {
+          L[w] = (w < nw) ? *pr : -INFINITY;
+          pr += S;
+        }
+#pragma unroll
+        for (int w = 0; w < kSumRows; ++w)
+          if (w < nw) acc[w] += det_fix(det_exp_nonpos((double)L[w] - (double)sm_m[w0 + w]));
+      }
     }
-    part = wave_sum_u64(part);
-    if (lane == 0 && part) atomicAdd((unsigned long long*)&lsum[bh * W + w], (unsigned long long)part);
+    // reduce-scatter over lanes: 16 -> 8 -> 4 -> 2 -> 1 rows per lane
+#pragma unroll
+    for (int n = kSumRows / 2, o = 32; n >= 1; n >>= 1, o >>= 1) {
+      const bool up = (lane & o) != 0;
+#pragma unroll
+      for (int i = 0; i < n; ++i) {
+        const uint64_t lo = acc[i], hi = acc[i + n];
+        const uint64_t send = up ? lo : hi;
+        const uint64_t keep = up ? hi : lo;
+        const uint32_t rl = __shfl_xor((uint32_t)send, o, 64);
+        const uint32_t rh = __shfl_xor((uint32_t)(send >> 32), o, 64);
+        acc[i] = keep + (((uint64_t)rh << 32) | rl);
+      }
+    }
+#pragma unroll
+    for (int o = 2; o >= 1; o >>= 1) {
+      const uint32_t rl = __shfl_xor((uint32_t)acc[0], o, 64);
+      const uint32_t rh = __shfl_xor((uint32_t)(acc[0] >> 32), o, 64);
+      acc[0] += ((uint64_t)rh << 32) | rl;
+    }
+    // step o kept the half of the rows selected by lane bit o, so lanes
+    // 4r .. 4r+3 now hold the wave sum of row r
+    if ((lane & 3) == 0) sm_red[wave][lane >> 2] = acc[0];
+    __syncthreads();
+    if (threadIdx.x < nw) {
+      const int w = threadIdx.x;
+      const uint64_t tot = sm_red[0][w] + sm_red[1][w] + sm_red[2][w] + sm_red[3][w];
+      if (tot) atomicAdd((unsigned long long*)&lsum[bh * W + w0 + w], (unsigned long long)tot);
+    }
+    __syncthreads();
   }
 }
 
-// grid (nchunk, Hk, B), block 256: importance of keys [c0-P, c0+256+P), then
-// pooling of keys [c0, c0+256).
+// grid (ceil(S / (256 - 2P)), Hk, B), block 256: thread t computes the
+// importance of key c0 - P + t; threads P .. 255-P pool and write keys
+// c0 .. c0 + 255 - 2P.
 __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__ logits,
-                                                       const float* __restrict__ cmax,
+                                                       const uint32_t* __restrict__ rmax,
                                                        const uint64_t* __restrict__ lsum, int Hk, int S,
-                                                       int W, int nchunk, int mode, int P, int pooling,
-                                                       int ksize, float* __restrict__ scores) {
+                                                       int W, int mode, int P, int pooling, int ksize,
+                                                       float* __restrict__ scores) {
   const int h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * Hk + h;
-  const int c0 = blockIdx.x * kChunk;
+  const int out_per_block = 256 - 2 * P;
+  const int c0 = blockIdx.x * out_per_block;
   __shared__ float sm_m[kMaxW];
   __shared__ double sm_inv[kMaxW];
-  __shared__ float sm_imp[kChunk + 2 * kMaxPool];
+  __shared__ float sm_imp[256];
   if (mode == HC_SCORE_SNAPKV) {
-    load_row_max(cmax, bh, nchunk, W, sm_m);
     for (int w = threadIdx.x; w < W; w += blockDim.x) {
+      sm_m[w] = key_to_float(rmax[bh * W + w]);
       const double l = (double)lsum[bh * W + w] * 0x1p-44;
       sm_inv[w] = 1.0 / l;
     }
   }
   __syncthreads();
-  const int span = kChunk + 2 * P;
-  for (int t = threadIdx.x; t < span; t += blockDim.x) {
-    const int s = c0 - P + t;
-    float v = 0.f;
-    if (s >= 0 && s < S) {
-      double acc = 0.0;
-      if (mode == HC_SCORE_SNAPKV) {
-        for (int w = 0; w < W; ++w) {
-          const double e = det_exp_nonpos((double)logits[(bh * W + w) * S + s] - (double)sm_m[w]);
-          acc = __builtin_fma(e, sm_inv[w], acc);
-        }
-      } else {
-        for (int w = 0; w < W; ++w) acc = acc + (double)logits[(bh * W + w) * S + s];
+  const int s = c0 - P + (int)threadIdx.x;
+  float v = 0.f;
+  if (s >= 0 && s < S) {
+    double acc = 0.0;
+    for (int w0 = 0; w0 < W; w0 += kSumRows) {
+      const int nw = min(kSumRows, W - w0);
+      float L[kSumRows];
+      const float* pr = logits + (bh * W + w0) * S + s;
+#pragma unroll
+      for (int w = 0; w < kSumRows; ++w) {
+        L[w] = (w < nw) ? *pr : 0.f;
+        pr += S;
       }
-      v = (float)acc;
+      if (mode == HC_SCORE_SNAPKV) {
+#pragma unroll
+        for (int w = 0; w < kSumRows; ++w)
+          if (w < nw) acc = __builtin_fma(det_exp_nonpos((double)L[w] - (double)sm_m[w0 + w]), sm_inv[w0 + w], acc);
+      } else {
+#pragma unroll
+        for (int w = 0; w < kSumRows; ++w)
+          if (w < nw) acc = acc + (double)L[w];
+      }
     }
-    sm_imp[t] = v;
+    v = (float)acc;
   }
+  sm_imp[threadIdx.x] = v;
   __syncthreads();
-  const int s = c0 + threadIdx.x;
-  if (s >= S) return;
+  const int t = threadIdx.x;
+  if (t < P || t >= 256 - P || s >= S) return;
   float out;
   if (P == 0) {
-    out = sm_imp[threadIdx.x];
+    out = sm_imp[t];
   } else if (pooling == HC_POOL_MAX) {
     out = -INFINITY;
     for (int j = -P; j <= P; ++j) {
       const int sj = s + j;
-      if (sj >= 0 && sj < S) out = fmaxf(out, sm_imp[threadIdx.x + P + j]);
+      if (sj >= 0 && sj < S) out = fmaxf(out, sm_imp[t + j]);
     }
   } else {
     double sum = 0.0;
     for (int j = -P; j <= P; ++j) {
       const int sj = s + j;
-      if (sj >= 0 && sj < S) sum = sum + (double)sm_imp[threadIdx.x + P + j];
+      if (sj >= 0 && sj < S) sum = sum + (double)sm_imp[t + j];
     }
     out = (float)(sum / (double)ksize);
   }
@@ -352,25 +407,24 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
                          int P, int pooling, int ksize, float* scores, hipStream_t st) {
   double* qf = reinterpret_cast<double*>(ws + lay.qf_off);
   float* logits = reinterpret_cast<float*>(ws + lay.logits_off);
-  float* cmax = reinterpret_cast<float*>(ws + lay.cmax_off);
+  uint32_t* rmax = reinterpret_cast<uint32_t*>(ws + lay.rmax_off);
   uint64_t* lsum = reinterpret_cast<uint64_t*>(ws + lay.lsum_off);
   const int nrb = (int)(lay.wpad / kRowBlk);
   hipLaunchKernelGGL(qmean_kernel<T>, dim3((unsigned)lay.wpad, (unsigned)Hk, (unsigned)B),
                      dim3((unsigned)(D < 64 ? 64 : D)), 0, st, (const T*)q, q_sb, q_sh, q_ss, q_row0, (int)Hq,
-                     (int)Hk, (int)W, (int)lay.wpad, (int)D, qf);
+                     (int)Hk, (int)W, (int)lay.wpad, (int)D, qf, rmax, lsum);
   const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
   if (lds > 65536)
     (void)hipFuncSetAttribute((const void*)logits_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
   hipLaunchKernelGGL(logits_kernel<T>, dim3((unsigned)lay.nchunk_m, (unsigned)(Hk * nrb), (unsigned)B), dim3(256),
-                     lds, st, (const T*)k, k_sb, k_sh, k_ss, (const double*)qf, (int)Hk,
-                     (int)S, (int)D, (int)W, (int)lay.wpad, mode, scal, logits, cmax, lsum);
+                     lds, st, (const T*)k, k_sb, k_sh, k_ss, (const double*)qf, (int)Hk, (int)S, (int)D, (int)W,
+                     (int)lay.wpad, mode, scal, logits, rmax);
   if (mode == HC_SCORE_SNAPKV)
     hipLaunchKernelGGL(rowsum_kernel, dim3((unsigned)cdiv(S, kSumChunk), (unsigned)Hk, (unsigned)B), dim3(256), 0,
-                       st, (const float*)logits, (const float*)cmax, (int)Hk, (int)S, (int)W, (int)lay.nchunk_m,
-                       lsum);
-  hipLaunchKernelGGL(imp_pool_kernel, dim3((unsigned)lay.nchunk, (unsigned)Hk, (unsigned)B), dim3(256), 0, st,
-                     (const float*)logits, (const float*)cmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W,
-                     (int)lay.nchunk_m, mode, P, pooling, ksize, scores);
+                       st, (const float*)logits, (const uint32_t*)rmax, (int)Hk, (int)S, (int)W, lsum);
+  hipLaunchKernelGGL(imp_pool_kernel, dim3((unsigned)cdiv(S, 256 - 2 * P), (unsigned)Hk, (unsigned)B), dim3(256), 0,
+                     st, (const float*)logits, (const uint32_t*)rmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W,
+                     mode, P, pooling, ksize, scores);
 }
 
 }  // namespace hc

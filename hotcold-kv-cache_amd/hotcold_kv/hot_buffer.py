@@ -1,0 +1,141 @@
+"""Fixed-capacity device storage of one layer's hot tier.
+
+Layout (per layer): keys / values (and optionally pre-RoPE keys) as
+[B][H][cap][D] in the cache dtype, positions as [B][cap] int64.  Rows
+0 .. held-1 are the held retrieved slot (written by the inject kernel), rows
+held .. held+n-1 the resident hot tokens.  Appends write one row in place
+(replacing the per-step torch.cat of cache.py:145-148 and
+layer_state.py:99-100); compaction gathers into a second buffer and swaps,
+so no row is read after it was overwritten.  Capacity grows geometrically
+when an append would overflow.
+"""
+
+import torch
+
+from . import ops
+
+
+class HotBuffer:
+    def __init__(self, batch, heads, head_dim, dtype, device, capacity, held=0, with_pre=False, with_pos=False):
+        self.B, self.H, self.D = int(batch), int(heads), int(head_dim)
+        self.dtype, self.device = dtype, torch.device(device)
+        self.held = int(held)
+        self.with_pre, self.with_pos = with_pre, with_pos
+        self.n = 0
+        self._alloc(max(1, int(capacity)))
+        self._spare = None
+
+    # -- storage --------------------------------------------------------------
+    def _new_storage(self, cap):
+        shape = (self.B, self.H, self.held + cap, self.D)
+        st = {
+            "k": torch.zeros(shape, dtype=self.dtype, device=self.device),
+            "v": torch.zeros(shape, dtype=self.dtype, device=self.device),
+        }
+        if self.with_pre:
+            st["p"] = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        if self.with_pos:
+            st["pos"] = torch.zeros((self.B, self.held + cap), dtype=torch.int64, device=self.device)
+        return st
+
+    def _alloc(self, cap):
+        self.cap = cap
+        self.st = self._new_storage(cap)
+
+    @property
+    def capacity(self):
+        return self.cap
+
+    def ensure(self, rows):
+        """Make room for `rows` hot rows, keeping the current contents."""
+        if rows <= self.cap:
+            return
+        new_cap = max(rows, 2 * self.cap)
+        old = self.st
+        self.st = self._new_storage(new_cap)
+        self.cap = new_cap
+        self._spare = None
+        total = self.held + self.n
+        if total:
+            ops.append_rows(0, old["k"][:, :, :total], self.st["k"], old["v"][:, :, :total], self.st["v"],
+                            old["p"][:, :, :total] if self.with_pre else None,
+                            self.st["p"] if self.with_pre else None,
+                            pos_src=old["pos"][:, :total] if self.with_pos else None,
+                            pos_dst=self.st["pos"] if self.with_pos else None)
+
+    # -- views ------------------------------------------------------------------
+    def _rows(self, name, start, stop):
+        t = self.st[name]
+        return t[:, start:stop] if name == "pos" else t[:, :, start:stop]
+
+    @property
+    def keys(self):
+        return self._rows("k", self.held, self.held + self.n)
+
+    @property
+    def values(self):
+        return self._rows("v", self.held, self.held + self.n)
+
+    @property
+    def pre_keys(self):
+        return self._rows("p", self.held, self.held + self.n) if self.with_pre else None
+
+    @property
+    def positions(self):
+        return self._rows("pos", self.held, self.held + self.n) if self.with_pos else None
+
+    def attended(self, with_held):
+        """(keys, values) of the rows decode attends: held slot + hot rows, or
+        the hot rows only."""
+        start = 0 if with_held else self.held
+        return self._rows("k", start, self.held + self.n), self._rows("v", start, self.held + self.n)
+
+    def held_storage(self):
+        """Full-width k/v tensors whose rows 0..held-1 are the held slot."""
+        return self.st["k"], self.st["v"]
+
+    # -- mutation ----------------------------------------------------------------
+    def append(self, k, v, pre=None, pos=None):
+        """Append T tokens: k, v, pre (B,H,T,D) and pos (B,T) int64."""
+        T = int(k.shape[2])
+        self.ensure(self.n + T)
+        row = self.held + self.n
+        ops.append_rows(row, k, self.st["k"], v, self.st["v"],
+                        pre if self.with_pre else None, self.st["p"] if self.with_pre else None,
+                        pos_src=pos if self.with_pos else None, pos_dst=self.st["pos"] if self.with_pos else None)
+        self.n += T
+
+    def set_from(self, k, v, pre=None, pos=None):
+        """Replace the hot rows with the given tokens."""
+        self.n = 0
+        self.append(k, v, pre, pos)
+
+    def compact(self, keep):
+        """Keep rows keep (B,H,n) per head or (B,n) shared, in that order."""
+        n_keep = int(keep.shape[-1])
+        if self._spare is None or self._spare["k"].shape[2] != self.held + self.cap:
+            self._spare = self._new_storage(self.cap)
+        dst = self._spare
+        pairs = [(self.keys, dst["k"]), (self.values, dst["v"])]
+        if self.with_pre:
+            pairs.append((self.pre_keys, dst["p"]))
+        ops.gather_rows(keep, pairs, dst_row0=self.held,
+                        pos_src=self.positions if self.with_pos else None,
+                        pos_dst=dst["pos"] if self.with_pos else None)
+        if self.held:
+            # the held slot travels with the buffer
+            ops.append_rows(0, self.st["k"][:, :, :self.held], dst["k"], self.st["v"][:, :, :self.held], dst["v"])
+        self._spare, self.st = self.st, dst
+        self.n = n_keep
+
+    def gather_from(self, k, v, keep, pre=None, pos=None):
+        """Fill the hot rows with rows keep of external tensors (B,H,S,D)."""
+        n_keep = int(keep.shape[-1])
+        self.ensure(n_keep)
+        pairs = [(k, self.st["k"]), (v, self.st["v"])]
+        if self.with_pre and pre is not None:
+            pairs.append((pre, self.st["p"]))
+        ops.gather_rows(keep, pairs, dst_row0=self.held,
+                        pos_src=pos if (self.with_pos and pos is not None) else None,
+                        pos_dst=self.st["pos"] if (self.with_pos and pos is not None) else None)
+        self.n = n_keep
