@@ -75,7 +75,9 @@ class HotColdLayer(CacheLayerMixin):
     def lazy_initialization(self, key_states, value_states=None):
         B, Hk, T, D = key_states.shape
         held = max(0, self.kvctrl.lookahead_k)
-        cap = max(self.kvctrl.max_capacity_prompt, T) + self.decode_reserve
+        # the resident length is T after the first update and at most
+        # max(max_capacity_prompt, T) + steps later; HotBuffer grows on demand
+        cap = T + self.decode_reserve
         self.buf = HotBuffer(B, Hk, D, key_states.dtype, key_states.device, cap, held=held, with_pre=True,
                              with_pos=True)
         self.is_initialized = True

@@ -197,6 +197,16 @@ def test_snapkv_scores_and_keep_c1_layer():
     assert torch.equal(vv.cpu(), ref.gather_kv(p["v"], want_keep))
 
 
+def test_snapkv_scores_and_keep_golden_fixtures():
+    """Kernels reproduce the committed fixtures (tests/golden) bit for bit."""
+    from test_oracle import load_golden
+
+    for case, (q, k, W, pool, budget, sc, want_scores, want_keep) in load_golden().items():
+        scores = ops.snapkv_scores(q.to(DEV), k.to(DEV), W, sc, pool, "maxpool")
+        assert torch.equal(scores.cpu(), want_scores), case
+        assert torch.equal(ops.keep_index(scores, W, budget).cpu(), want_keep), case
+
+
 def test_rawsum_scores_and_head_mean():
     B, Hq, Hk, S, T, D = 2, 32, 8, 700, 40, 128
     q = _randn((B, Hq, T, D), 31, torch.float16)
