@@ -1,30 +1,39 @@
 #!/usr/bin/env python3
 """Hot-tier benchmark on one MI355X.
 
-Workload (default): the full 32-layer Llama-3.1-8B KV geometry (32 query / 8 KV
+Workload (default): the 32-layer Llama-3.1-8B KV geometry (32 query / 8 KV
 heads, head_dim 128), fp16, batch 1, 8192-token synthetic prompt with 16
-needles, SnapKV compaction (window 32, max-pool 7, budget 512), then 63 decode
-steps of GQA decode attention over the hot buffer.  Inputs are generated on
-the device before the timed region.
+needles; SnapKV compaction (window 32, max-pool 7, budget 512) of all 32
+layers, then 63 decode steps, each appending one token per layer and running
+GQA decode attention over the hot buffer.  Inputs are generated on the device
+before the timed region.
 
-One step = compaction of all 32 layers (one batched launch set: scores,
-kept indices, gather into the fixed-capacity hot buffer) + 63 decode steps,
-each appending one token per layer and attending all 32 layers in one launch.
+One step = one such job.  The 32 layers are independent in this synthetic
+workload, so each kernel covers all of them in one launch (layer l is batch
+row l): compaction is one launch set (scores, kept indices, gather into the
+hot buffer), recorded once as a HIP graph and replayed, and each decode step
+is an append launch plus one decode launch over the 32 layers' hot buffers
+(72 MB).
+
+Before each decode launch a read sweep over 512 MiB evicts the 256 MB Infinity
+Cache (in a model, the weights streamed between two visits of a layer do
+that), so decode reads its K/V from HBM; the sweep is outside the decode
+events.  It only reads, so no dirty lines are left for decode to write back.
 
 Reported:
-  value                      decode us per layer-step (32-layer launches)
-  compact_ms_32_layers       SnapKV compaction of all 32 layers, ms
-  decode_us_per_layer_launch decode us per layer with one launch per layer
-  roofline                   decode kernel, cold-MALL launches timed with HIP
-                             events on the launch stream
-  cpu_baseline               the reference's torch-CPU path on a bounded sample
+  value              decode us per layer-step: mean decode-launch time of the
+                     timed steps (HIP events on the launch stream) / 32
+  compact_ms_32_layers  compaction of all 32 layers per step, ms
+  roofline           decode launch: algorithmic bytes / mean launch time
+  roofline_compaction, scoring MFMA rate, a per-layer-launch variant (one
+  decode launch per layer, as a model's layer loop issues them), warm-cache
+  figures, and the reference's torch-CPU path on a bounded sample.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
 
 import argparse
 import json
-import math
 import os
 import statistics
 import sys
@@ -38,15 +47,54 @@ for _p in (ROOT, PKG):
 
 METRIC = "decode µs/layer & SnapKV compact ms (8k→512); % of HBM peak GB/s on 1 MI355X"
 HBM_PEAK_GBS = 8000.0
+FP64_MFMA_PEAK_TFLOPS = 78.6
+FLUSH_BYTES = 512 << 20
+
+
+class CacheSweep:
+    """Evicts the Infinity Cache by reading FLUSH_BYTES (a max reduction)."""
+
+    def __init__(self, dev):
+        import torch
+        self.buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
+
+    def __call__(self):
+        import torch
+        torch.amax(self.buf)
 
 
 def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
+def elem_size(dtype):
+    import torch
+    return torch.tensor([], dtype=dtype).element_size()
+
+
+def decode_bytes(w, rows, n_keys):
+    """Algorithmic HBM bytes of one decode launch over `rows` (layer, batch)
+    rows: each hot K and V row read once, q read, output written."""
+    es = elem_size(w.dtype)
+    return rows * (2 * w.hk * n_keys * w.head_dim + 2 * w.hq * w.head_dim) * es
+
+
+def compaction_bytes(w, rows):
+    """Algorithmic HBM bytes of one compaction over `rows` layer rows: the
+    window queries and every key read once, fp32 scores written and read,
+    kept K and V rows read and written."""
+    es = elem_size(w.dtype)
+    S, D, W = w.seq_len, w.head_dim, min(w.window, w.seq_len)
+    q = w.hq * W * D * es
+    k = w.hk * S * D * es
+    scores = 2 * w.hk * S * 4
+    gather = 2 * 2 * w.hk * w.budget * D * es
+    return rows * (q + k + scores + gather)
+
+
 class Setup:
-    """Device-resident inputs and hot buffers of one workload (all layers
-    stacked along the batch axis: row l*B + b is layer l, sequence b)."""
+    """Device-resident inputs, hot buffers and captured graphs of one
+    workload (all layers stacked along the batch axis)."""
 
     def __init__(self, w, dev):
         import torch
@@ -54,9 +102,8 @@ class Setup:
 
         self.w = w
         L, B, S, D = w.layers, w.batch, w.seq_len, w.head_dim
-        LB = L * B
+        self.LB = LB = L * B
         dt = w.dtype
-        self.LB = LB
         self.q_post = torch.empty((LB, w.hq, S, D), dtype=dt, device=dev)
         self.k_post = torch.empty((LB, w.hk, S, D), dtype=dt, device=dev)
         self.v = torch.empty((LB, w.hk, S, D), dtype=dt, device=dev)
@@ -80,74 +127,128 @@ class Setup:
             self.k_new.append(torch.cat(ks, 0))
             self.v_new.append(torch.cat(vs, 0))
         self.out = torch.empty((LB, w.hq, D), dtype=dt, device=dev)
-        self.n_hot = 0
+        self.stream = torch.cuda.Stream(dev)
+        self.g_comp = None
+        self.g_pl = None
 
+    # -- eager launch sets -----------------------------------------------------------
     def compaction(self):
         from hotcold_kv import ops
         w = self.w
         scores = ops.snapkv_scores(self.q_post, self.k_post, w.window, w.scaling, w.pool, "maxpool")
         keep = ops.keep_index(scores, w.window, w.budget)
         ops.gather_rows(keep, [(self.k_post, self.k_hot), (self.v, self.v_hot)])
-        self.n_hot = keep.shape[-1]
         return keep
 
-    def decode_step(self, t):
+    def append(self, t):
         from hotcold_kv import ops
-        n = self.n_hot
-        ops.append_rows(n, self.k_new[t], self.k_hot, self.v_new[t], self.v_hot)
-        self.n_hot = n + 1
-        ops.decode_attention(self.q_new[t], self.k_hot[:, :, :n + 1], self.v_hot[:, :, :n + 1],
-                             self.w.scaling, out=self.out)
+        ops.append_rows(self.w.budget + t, self.k_new[t], self.k_hot, self.v_new[t], self.v_hot)
 
-    def step(self):
-        self.compaction()
-        for t in range(self.w.decode_steps):
-            self.decode_step(t)
+    def decode(self, t, num_splits=0):
+        from hotcold_kv import ops
+        n = self.w.budget + t + 1
+        ops.decode_attention(self.q_new[t], self.k_hot[:, :, :n], self.v_hot[:, :, :n], self.w.scaling,
+                             out=self.out, num_splits=num_splits)
+
+    def decode_per_layer(self, t):
+        """One decode launch per layer, as a model's layer loop issues them."""
+        from hotcold_kv import ops
+        B, n = self.w.batch, self.w.budget + t + 1
+        for l in range(self.w.layers):
+            sl = slice(l * B, (l + 1) * B)
+            ops.decode_attention(self.q_new[t][sl], self.k_hot[sl, :, :n], self.v_hot[sl, :, :n], self.w.scaling,
+                                 out=self.out[sl])
+
+    # -- graphs --------------------------------------------------------------------------
+    def capture(self):
+        """Record compaction and the per-layer decode loop as HIP graphs on a
+        side stream (warmed up eagerly on that stream first)."""
+        import torch
+        w = self.w
+        s = self.stream
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            self.compaction()
+            for t in range(w.decode_steps):
+                self.append(t)
+                self.decode(t)
+            self.decode_per_layer(w.decode_steps - 1)
+        s.synchronize()
+
+        def cap(fn):
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, stream=s):
+                fn()
+            return g
+
+        self.g_comp = cap(self.compaction)
+        self.g_pl = cap(lambda: self.decode_per_layer(w.decode_steps - 1))
+        # 20 back-to-back launches of the last step's decode (warm-cache rate)
+        self.g_dec20 = cap(lambda: [self.decode(w.decode_steps - 1) for _ in range(20)])
+        torch.cuda.synchronize()
 
 
-def decode_bytes(w, LB, n_rows):
-    """Algorithmic HBM bytes of one decode launch: K and V rows read once,
-    q read, output written."""
-    es = {"torch.float16": 2, "torch.bfloat16": 2, "torch.float32": 4}[str(w.dtype)]
-    return LB * (2 * w.hk * n_rows * w.head_dim + 2 * w.hq * w.head_dim) * es
-
-
-def compaction_bytes(w, LB):
-    """Algorithmic bytes of one compaction (per all LB layer-rows): window
-    queries and all keys read once, fp32 scores written and read, kept K/V
-    rows read and written."""
-    es = 2 if w.dtype != __import__("torch").float32 else 4
-    S, D, W = w.seq_len, w.head_dim, min(w.window, w.seq_len)
-    q = w.hq * W * D * es
-    k = w.hk * S * D * es
-    scores = 2 * w.hk * S * 4
-    gather = 2 * 2 * w.hk * w.budget * D * es
-    return LB * (q + k + scores + gather)
-
-
-def time_events(fn, iters, flush=None):
-    """Mean ms of fn() over iters, bracketed by HIP events on the current
-    stream; flush() (if given) runs before each start event."""
+def run_steps(s, steps, flush):
+    """Run `steps` whole jobs; return (wall ms/step, compaction ms per step,
+    decode-launch ms list).  Compaction replays its graph; append and decode
+    are launched directly: the cache sweep before each decode keeps the GPU
+    busy long enough for the host to stay ahead, so the decode events see no
+    host gap (a one-kernel graph replay adds several microseconds of its own
+    on this stack)."""
     import torch
-    st = torch.cuda.current_stream()
-    times = []
-    for _ in range(iters):
-        if flush is not None:
-            flush()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        e0.record(st)
-        fn()
-        e1.record(st)
-        e1.synchronize()
-        times.append(e0.elapsed_time(e1))
-    return statistics.mean(times), times
+    w = s.w
+    st = s.stream
+    comp_ev, dec_ev = [], []
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    with torch.cuda.stream(st):
+        for _ in range(steps):
+            c0 = torch.cuda.Event(enable_timing=True)
+            c1 = torch.cuda.Event(enable_timing=True)
+            c0.record(st)
+            s.g_comp.replay()
+            c1.record(st)
+            comp_ev.append((c0, c1))
+            for t in range(w.decode_steps):
+                s.append(t)
+                if flush is not None:
+                    flush()
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record(st)
+                s.decode(t)
+                e1.record(st)
+                dec_ev.append((e0, e1))
+    torch.cuda.synchronize()
+    wall_ms = (time.perf_counter() - t0) * 1e3 / max(1, steps)
+    comp = [a.elapsed_time(b) for a, b in comp_ev]
+    dec = [a.elapsed_time(b) for a, b in dec_ev]
+    return wall_ms, comp, dec
+
+
+def time_graph(g, st, iters, flush=None):
+    """Mean ms of replays of g on st, events around each replay; the optional
+    flush runs before each start event."""
+    import torch
+    evs = []
+    with torch.cuda.stream(st):
+        for i in range(iters):
+            if flush is not None:
+                flush()
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record(st)
+            g.replay()
+            e1.record(st)
+            evs.append((e0, e1))
+    torch.cuda.synchronize()
+    return statistics.mean(a.elapsed_time(b) for a, b in evs)
 
 
 def cpu_baseline(w, sample_seconds):
     """The reference's torch-CPU path (snapkv_importance -> keep_index ->
     gather_kv, then cat + repeat_kv + SDPA decode) on a bounded sample of the
-    same workload, fp32-upcast inputs, on this host's cores."""
+    same workload -- layer 0's prompt, fp32-upcast -- on this host's cores."""
     import torch
     from hotcold_kv import synthetic
     from oracle import reference as ref
@@ -155,9 +256,7 @@ def cpu_baseline(w, sample_seconds):
     threads = max(1, min(16, os.cpu_count() or 1))
     torch.set_num_threads(threads)
     p = synthetic.make_prompt(w, layer=0, seed=0, device="cpu")
-    q = p["q_post"].float()
-    k = p["k_post"].float()
-    v = p["v"].float()
+    q, k, v = p["q_post"].float(), p["k_post"].float(), p["v"].float()
     ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)  # warm-up
     comp = []
     t_end = time.perf_counter() + sample_seconds / 2
@@ -185,7 +284,7 @@ def cpu_baseline(w, sample_seconds):
         "kind": "port",
         "sample": (f"layer 0 of {w.name}: {len(comp)} compactions ({comp_ms_layer:.1f} ms/layer, "
                    f"x{w.layers} = {comp_ms_layer * w.layers:.1f} ms for all layers) and {len(dec)} decode "
-                   f"steps, fp32-upcast torch CPU (scoring.py / layer_state.py op sequence)"),
+                   f"steps (append + SDPA), fp32-upcast torch CPU restating scoring.py / layer_state.py"),
         "compact_ms_32_layers": round(comp_ms_layer * w.layers, 2),
     }
 
@@ -193,91 +292,58 @@ def cpu_baseline(w, sample_seconds):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3)
-    ap.add_argument("--warmup", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=5)
+    ap.add_argument("--warmup", type=int, default=2)
     ap.add_argument("--workload", default="c1_llama8b_8k_b512")
-    ap.add_argument("--roofline-iters", type=int, default=30)
     ap.add_argument("--cpu-sample-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; --gpus must be 1 "
-                                   "(the hot tier shards by batch and KV head, see the design notes)"}))
+        print("bench.py: this build measures one GPU only; the hot tier shards by batch and KV head "
+              "across GPUs with no exchange inside the path, and no multi-GPU figure is produced. "
+              "Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     import torch
-    from hotcold_kv import ops, synthetic
+    from hotcold_kv import synthetic
 
     w = synthetic.WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"workload {w.name}: generating inputs on {torch.cuda.get_device_name(dev)}")
     s = Setup(w, dev)
+    flush = CacheSweep(dev)
     torch.cuda.synchronize()
+    s.capture()
+    log("captured the compaction and per-layer decode graphs")
 
-    for i in range(args.warmup):
-        s.step()
-    torch.cuda.synchronize()
+    run_steps(s, args.warmup, flush)
     log(f"warmup done ({args.warmup} steps)")
+    wall_ms, comp, dec = run_steps(s, args.steps, flush)
+    comp_ms = statistics.mean(comp)
+    dec_ms = statistics.mean(dec)                      # one decode launch, all layers
+    dec_us_layer = dec_ms * 1e3 / w.layers
+    log(f"timed {args.steps} steps: {wall_ms:.3f} ms/step wall (incl. cache flushes), compaction "
+        f"{comp_ms:.3f} ms, decode launch {dec_ms * 1e3:.2f} us = {dec_us_layer:.3f} us/layer-step")
 
-    st = torch.cuda.current_stream()
-    comp_ms, dec_ms = [], []
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    for i in range(args.steps):
-        e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
-        e0.record(st)
-        s.compaction()
-        e1.record(st)
-        for t in range(w.decode_steps):
-            s.decode_step(t)
-        e2.record(st)
-        comp_ms.append((e0, e1))
-        dec_ms.append((e1, e2))
-    torch.cuda.synchronize()
-    t1 = time.perf_counter()
-    ms_per_step = (t1 - t0) * 1e3 / args.steps
-    comp = statistics.mean(a.elapsed_time(b) for a, b in comp_ms)
-    dec = statistics.mean(a.elapsed_time(b) for a, b in dec_ms)
-    dec_us_layer = dec * 1e3 / (w.decode_steps * w.layers)
-    log(f"timed {args.steps} steps: {ms_per_step:.3f} ms/step, compaction {comp:.3f} ms, "
-        f"decode {dec:.3f} ms ({dec_us_layer:.3f} us/layer-step)")
-
-    # decode kernel alone, cold MALL: a 512 MiB fill between launches.
-    n_rows = w.budget + w.decode_steps
-    flush_buf = torch.empty(512 << 20, dtype=torch.uint8, device=dev)
-    kv_k, kv_v = s.k_hot[:, :, :n_rows], s.v_hot[:, :, :n_rows]
-
-    def dec_launch():
-        ops.decode_attention(s.q_new[-1], kv_k, kv_v, w.scaling, out=s.out)
-
-    dec_launch()
-    cold_ms, _ = time_events(dec_launch, args.roofline_iters, flush=lambda: flush_buf.fill_(1))
-    warm_ms, _ = time_events(dec_launch, args.roofline_iters)
-    nbytes = decode_bytes(w, s.LB, n_rows)
-    achieved = nbytes / (cold_ms * 1e-3) / 1e9
-    log(f"decode kernel: {nbytes / 1e6:.1f} MB/launch, cold {cold_ms * 1e3:.2f} us ({achieved:.0f} GB/s), "
-        f"warm {warm_ms * 1e3:.2f} us ({nbytes / (warm_ms * 1e-3) / 1e9:.0f} GB/s)")
-
-    # one launch per layer, as the model's layer loop issues them
-    B = w.batch
-
-    def per_layer():
-        for l in range(w.layers):
-            sl = slice(l * B, (l + 1) * B)
-            ops.decode_attention(s.q_new[-1][sl], kv_k[sl], kv_v[sl], w.scaling, out=s.out[sl])
-
-    per_layer()
-    pl_ms, _ = time_events(per_layer, 10)
-    dec_us_launch = pl_ms * 1e3 / w.layers
-
-    # compaction alone, cold
-    comp_cold_ms, _ = time_events(s.compaction, 5, flush=lambda: flush_buf.fill_(1))
+    # algorithmic rates
+    mean_keys = w.budget + (w.decode_steps + 1) / 2.0
+    nbytes = decode_bytes(w, s.LB, mean_keys)
+    achieved = nbytes / (dec_ms * 1e-3) / 1e9
     cbytes = compaction_bytes(w, s.LB)
+    c_achieved = cbytes / (comp_ms * 1e-3) / 1e9
     sflops = 2.0 * s.LB * w.hk * min(w.window, w.seq_len) * w.seq_len * w.head_dim
-    log(f"compaction cold {comp_cold_ms:.3f} ms: {cbytes / (comp_cold_ms * 1e-3) / 1e9:.0f} GB/s algorithmic, "
-        f"{sflops / (comp_cold_ms * 1e-3) / 1e12:.1f} TFLOP/s fp64 scoring")
-    del flush_buf
+    log(f"decode {nbytes / 1e6:.1f} MB/launch -> {achieved:.0f} GB/s; compaction {cbytes / 1e6:.0f} MB -> "
+        f"{c_achieved:.0f} GB/s, scoring {sflops / (comp_ms * 1e-3) / 1e12:.2f} TFLOP/s fp64")
+
+    # warm-cache decode and the per-layer-launch schedule (last decode step)
+    warm_dec_ms = time_graph(s.g_dec20, s.stream, 5) / 20
+    pl_cold_ms = time_graph(s.g_pl, s.stream, 20, flush)
+    pl_warm_ms = time_graph(s.g_pl, s.stream, 20)
+    n_last = w.budget + w.decode_steps
+    log(f"last-step decode launch warm {warm_dec_ms * 1e3:.2f} us; per-layer launches cold "
+        f"{pl_cold_ms * 1e3 / w.layers:.2f} us/layer, warm {pl_warm_ms * 1e3 / w.layers:.2f} us/layer")
+    del flush
 
     cpu = None
     if not args.no_cpu_baseline:
@@ -292,7 +358,7 @@ def main():
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms_per_step, 4),
+        "ms_per_step": round(wall_ms, 4),
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
@@ -300,15 +366,23 @@ def main():
         "data": "synthetic",
         "config": {"workload": w.name, "layers": w.layers, "batch": w.batch, "seq_len": w.seq_len,
                    "budget": w.budget, "window": w.window, "pool": w.pool, "decode_steps": w.decode_steps,
-                   "q_heads": w.hq, "kv_heads": w.hk, "head_dim": w.head_dim, "parallelism": "single-gpu"},
-        "compact_ms_32_layers": round(comp, 4),
-        "compact_ms_cold": round(comp_cold_ms, 4),
-        "decode_us_per_layer_launch": round(dec_us_launch, 3),
-        "decode_kernel_us_cold": round(cold_ms * 1e3, 3),
-        "decode_kernel_us_warm": round(warm_ms * 1e3, 3),
+                   "q_heads": w.hq, "kv_heads": w.hk, "head_dim": w.head_dim,
+                   "schedule": "32 layers per launch, HIP graphs, Infinity Cache flushed before decode"},
+        "compact_ms_32_layers": round(comp_ms, 4),
+        "decode_us_per_layer_step": round(dec_us_layer, 4),
+        "decode_us_per_layer_launch_cold": round(pl_cold_ms * 1e3 / w.layers, 3),
+        "decode_us_per_layer_launch_warm": round(pl_warm_ms * 1e3 / w.layers, 3),
+        "decode_launch_us_warm_last_step": round(warm_dec_ms * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                     "kernel": "decode_attn_kernel", "bytes_per_launch": nbytes},
+                     "kernel": "decode_attn_kernel (+ decode_combine_kernel)",
+                     "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3)},
+        "roofline_compaction": {"bound": "hbm", "achieved": round(c_achieved, 1), "peak": HBM_PEAK_GBS,
+                                "unit": "GB/s", "frac": round(c_achieved / HBM_PEAK_GBS, 4),
+                                "bytes_per_job": int(cbytes),
+                                "scoring_tflops_fp64": round(sflops / (comp_ms * 1e-3) / 1e12, 3),
+                                "scoring_mfma_frac": round(sflops / (comp_ms * 1e-3) / 1e12
+                                                           / FP64_MFMA_PEAK_TFLOPS, 4)},
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

@@ -6,14 +6,24 @@
 // times, with an unstabilised exp (kernels.py:57).  Here one workgroup owns
 // (batch, KV head, key split) and serves all G query heads of the group from
 // a single K/V read:
+//   * K/V stream through a per-wave ring of register tiles filled by raw
+//     buffer loads (128-bit per lane).  Rows outside the workgroup's key range
+//     are addressed past the buffer's end, so the hardware returns zeros
+//     without touching memory; every load is unconditional, which lets the
+//     compiler keep the whole ring in flight (exact vmcnt waits);
 //   * Q.K^T on MFMA: v_mfma_f32_16x16x32_{f16,bf16} with the 16 key rows of a
 //     tile as the A operand and the G (<=16) query heads as the B operand;
-//     fp32 inputs use v_mfma_f32_16x16x4f32.
+//     fp32 inputs use v_mfma_f32_16x16x4f32;
 //   * online max-stabilised softmax in the log2 domain (exp2), fp32;
-//   * P.V on the VALU: 16 lanes cover one 2*D-byte V row (128-bit loads),
-//     4 rows per wave instruction, fp32 accumulators;
-//   * split partials (m, l, acc) combined by the last-arriving workgroup of
-//     each (b, kv-head) through an atomic ticket (no second launch).
+//   * P.V on MFMA for f16/bf16 (v_mfma_f32_16x16x16_{f16,bf16}): the Q.K^T
+//     output leaves lane (r, c) holding p for keys 4r..4r+3 of head c, which
+//     is exactly its B-operand share, and its four V rows give the A operand
+//     (a byte permute per register), so no lane exchanges data; P is rounded
+//     to the input type and the softmax sum uses the same rounded values.
+//     fp32 inputs use the VALU (16 lanes per V row, fp32 FMAs);
+//   * the attention mask and the held slot's valid & (pos <= cur) test are
+//     evaluated once per workgroup into an LDS bitmap;
+//   * split partials (m, l, acc) are merged by a second, one-pass kernel.
 #include "hc_common.h"
 
 namespace hc {
@@ -38,12 +48,37 @@ struct DecodeArgs {
   float* part;         // [units][splits][G*D + 2*G] split partials (splits > 1)
   float* scores;       // optional [B][Hq][S] log2-domain logits (eviction score)
   float* ml;           // optional [B][Hq][2] final (max, sum)
+  uint32_t k_bytes, v_bytes, q_bytes;  // buffer extents of one (b, kv head)
   int B, Hq, Hk, G, S, splits, keys_per_split;
   float scale_log2;
 };
 
+// Keys of one split when the keep bitmap is needed (mask or held slot).
+constexpr int kMaxBitmapKeys = 16384;
+// Buffer offset past every extent: the load returns zeros, no memory access.
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int BYTES>
+__device__ __forceinline__ void bload(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t* w) {
+  if constexpr (BYTES == 16) {
+    const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
+  } else if constexpr (BYTES == 8) {
+    const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+    w[0] = x[0]; w[1] = x[1];
+  } else if constexpr (BYTES == 4) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+  } else {
+    w[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+  }
+}
+
 // ---------------------------------------------------------------------------
-// Per-lane registers of one 16-key tile, loaded one tile ahead of use.
+// Per-lane registers of one 16-key tile.
 //   K (MFMA A operand): lane l holds key row tile + l%16, 16-byte pieces at
 //     dims 32t + 8*(l/16) (f16/bf16) or 16t + 4*(l/16) (f32).
 //   V (P.V layout): lane l holds rows tile + 4*(l/16) + i, i = 0..3, dims
@@ -60,63 +95,41 @@ struct TileRegs {
   uint32_t keep;  // bit i: key tile + 4*(l/16) + i is attended
 };
 
+// Issue the loads of one tile (all unconditional) and read its keep bits.
 template <typename T, int D>
-__device__ __forceinline__ void load_tile(TileRegs<T, D>& r, const T* kbase, const T* vbase, int64_t k_ss,
-                                          int64_t v_ss, int tile, int key_end, int col, int grp,
-                                          const DecodeArgs& a, int b, int hk, int64_t cur, const uint8_t* mrow) {
+__device__ __forceinline__ void load_tile(TileRegs<T, D>& r, __amdgpu_buffer_rsrc_t krs, __amdgpu_buffer_rsrc_t vrs,
+                                          uint32_t k_rowb, uint32_t v_rowb, int tile, int key_begin, int key_end,
+                                          int col, int grp, const uint32_t* bits) {
   using R = TileRegs<T, D>;
-  // Key mask of this lane's four rows, evaluated here (one tile ahead) so
-  // that the MFMA, the reads of its result and the score selects of
-  // process_tile form one straight-line block.
+  const int arow = tile + col;
+  const bool kok = arow < key_end;
+#pragma unroll
+  for (int t = 0; t < R::KW; ++t) {
+    const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
+    const uint32_t off = (kok && d0 < D) ? (uint32_t)arow * k_rowb + (uint32_t)(d0 * sizeof(T)) : kOob;
+    uint32_t w[4];
+    bload<16>(krs, off, w);
+    r.k[t] = u32x4{w[0], w[1], w[2], w[3]};
+  }
   uint32_t keep = 0;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int key = tile + 4 * grp + i;
-    bool kp = key < key_end;
-    if (kp && mrow) kp = mrow[key] != 0;
-    if (kp && key < a.held_len)
-      kp = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key] != 0 && a.held_pos[b * a.hp_sb + hk * a.hp_sh + key] <= cur;
+    const bool ok = key < key_end;
+    const uint32_t off = ok ? (uint32_t)key * v_rowb + (uint32_t)(col * R::DPL * sizeof(T)) : kOob;
+    bload<(R::VB >= 16 ? 16 : R::VB)>(vrs, off, r.v[i]);
+    if constexpr (R::VB > 16) {
+#pragma unroll
+      for (int c = 1; c < R::VB / 16; ++c) bload<16>(vrs, off == kOob ? kOob : off + 16 * c, &r.v[i][4 * c]);
+    }
+    bool kp = ok;
+    if (bits) {
+      const int rel = min(key - key_begin, kMaxBitmapKeys - 1);
+      kp = ok && ((bits[rel >> 5] >> (rel & 31)) & 1u);
+    }
     keep |= (kp ? 1u : 0u) << i;
   }
   r.keep = keep;
-  const int arow = tile + col;
-  const bool kok = arow < key_end;
-  const T* krow = kbase + (int64_t)arow * k_ss;
-#pragma unroll
-  for (int t = 0; t < R::KW; ++t) {
-    const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
-    u32x4 w = {0u, 0u, 0u, 0u};
-    if (kok && d0 < D) w = ld16(krow + d0);
-    r.k[t] = w;
-  }
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int key = tile + 4 * grp + i;
-    const char* p = reinterpret_cast<const char*>(vbase + (int64_t)key * v_ss + col * R::DPL);
-    if (key < key_end) {
-      if constexpr (R::VB >= 16) {
-#pragma unroll
-        for (int c = 0; c < R::VB / 16; ++c) {
-          const u32x4 x = ld16(p + 16 * c);
-          r.v[i][4 * c + 0] = x[0];
-          r.v[i][4 * c + 1] = x[1];
-          r.v[i][4 * c + 2] = x[2];
-          r.v[i][4 * c + 3] = x[3];
-        }
-      } else if constexpr (R::VB == 8) {
-        const u32x2 x = *reinterpret_cast<const u32x2*>(p);
-        r.v[i][0] = x[0];
-        r.v[i][1] = x[1];
-      } else if constexpr (R::VB == 4) {
-        r.v[i][0] = *reinterpret_cast<const uint32_t*>(p);
-      } else {
-        r.v[i][0] = (uint32_t)(*reinterpret_cast<const uint16_t*>(p));
-      }
-    } else {
-#pragma unroll
-      for (int c = 0; c < R::VWORDS; ++c) r.v[i][c] = 0u;
-    }
-  }
 }
 
 // Q.K^T of one tile.  Output lane layout of every 16x16 fp32 MFMA block:
@@ -129,13 +142,14 @@ struct QFrag<half_t, D> {
   static constexpr int NK = (D + 31) / 32;
   half8 qb[NK];
   // B operand: lane l supplies q[head l%16][32t + 8*(l/16) + j].
-  __device__ void load(const half_t* q0, int64_t q_sh, int col, int grp, int G) {
+  __device__ void load(__amdgpu_buffer_rsrc_t qrs, uint32_t q_rowb, int col, int grp, int G) {
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
       const int d0 = 32 * t + 8 * grp;
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (col < G && d0 < D) w = ld16(q0 + col * q_sh + d0);
-      qb[t] = __builtin_bit_cast(half8, w);
+      const uint32_t off = (col < G && d0 < D) ? (uint32_t)col * q_rowb + (uint32_t)(d0 * 2) : kOob;
+      uint32_t w[4];
+      bload<16>(qrs, off, w);
+      qb[t] = __builtin_bit_cast(half8, u32x4{w[0], w[1], w[2], w[3]});
     }
   }
   __device__ floatx4 dot(const TileRegs<half_t, D>& r) const {
@@ -151,13 +165,14 @@ template <int D>
 struct QFrag<bf16_t, D> {
   static constexpr int NK = (D + 31) / 32;
   bf16x8 qb[NK];
-  __device__ void load(const bf16_t* q0, int64_t q_sh, int col, int grp, int G) {
+  __device__ void load(__amdgpu_buffer_rsrc_t qrs, uint32_t q_rowb, int col, int grp, int G) {
 #pragma unroll
     for (int t = 0; t < NK; ++t) {
       const int d0 = 32 * t + 8 * grp;
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (col < G && d0 < D) w = ld16(q0 + col * q_sh + d0);
-      qb[t] = __builtin_bit_cast(bf16x8, w);
+      const uint32_t off = (col < G && d0 < D) ? (uint32_t)col * q_rowb + (uint32_t)(d0 * 2) : kOob;
+      uint32_t w[4];
+      bload<16>(qrs, off, w);
+      qb[t] = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
     }
   }
   __device__ floatx4 dot(const TileRegs<bf16_t, D>& r) const {
@@ -176,14 +191,15 @@ struct QFrag<float, D> {
   // dim 16t + 4*(l/16) + j (a permutation of the block's 16 dims).
   static constexpr int NB = D / 16;
   float qb[NB][4];
-  __device__ void load(const float* q0, int64_t q_sh, int col, int grp, int G) {
+  __device__ void load(__amdgpu_buffer_rsrc_t qrs, uint32_t q_rowb, int col, int grp, int G) {
 #pragma unroll
     for (int t = 0; t < NB; ++t) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (col < G) w = ld16(q0 + col * q_sh + 16 * t + 4 * grp);
+      const uint32_t off = (col < G) ? (uint32_t)col * q_rowb + (uint32_t)((16 * t + 4 * grp) * 4) : kOob;
+      uint32_t w[4];
+      bload<16>(qrs, off, w);
       // Whole-vector bit cast, then element reads: a bit cast of a single
       // vector element miscompiles to element 0 with this toolchain.
-      const floatx4 f = __builtin_bit_cast(floatx4, w);
+      const floatx4 f = __builtin_bit_cast(floatx4, u32x4{w[0], w[1], w[2], w[3]});
       qb[t][0] = f[0];
       qb[t][1] = f[1];
       qb[t][2] = f[2];
@@ -217,24 +233,24 @@ struct SoftmaxState {
   float acc[GM][DPL];
 };
 
-template <typename T, int D, int GM>
+template <typename T, int D, int GM, bool EVICT>
 __device__ __forceinline__ void process_tile(const TileRegs<T, D>& r, const QFrag<T, D>& qf,
-                                             SoftmaxState<GM, D / 16>& st, const DecodeArgs& a, int b, int hk,
-                                             int tile, int key_end, int col, int grp, int64_t cur,
-                                             const uint8_t* mrow, float* srow) {
+                                             SoftmaxState<GM, D / 16>& st, int G, float scale_log2, int tile,
+                                             int key_end, int col, int grp, float* srow) {
   constexpr int DPL = D / 16;
-  const int G = a.G;
   const floatx4 c = qf.dot(r);
   const float c4[4] = {c[0], c[1], c[2], c[3]};
   const uint32_t keep = (col < G) ? r.keep : 0u;
   float s[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) s[i] = ((keep >> i) & 1u) ? c4[i] * a.scale_log2 : -INFINITY;
-  if (srow && col < G) {
+  for (int i = 0; i < 4; ++i) s[i] = ((keep >> i) & 1u) ? c4[i] * scale_log2 : -INFINITY;
+  if constexpr (EVICT) {
+    if (col < G) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int key = tile + 4 * grp + i;
-      if (key < key_end) srow[key] = s[i];
+      for (int i = 0; i < 4; ++i) {
+        const int key = tile + 4 * grp + i;
+        if (key < key_end) srow[key] = s[i];
+      }
     }
   }
   float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
@@ -277,12 +293,119 @@ __device__ __forceinline__ void process_tile(const TileRegs<T, D>& r, const QFra
   }
 }
 
-// grid (splits, Hk, B), block 256 (4 waves).  Each wave takes every fourth
-// 16-key tile of the workgroup's key range, with the next tile's K/V loads in
-// flight while the current one is processed.
-template <typename T, int D, int GM>
-__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
+// P.V on MFMA (2-byte types).  Accumulator block j holds, in lane (r, c),
+// out[dim (4r + i) * (D/16) + j][head c] for i = 0..3.
+template <int D>
+struct MxState {
+  float m_run;
+  float l_run;
+  floatx4 acc[D / 16];
+};
+
+template <typename T>
+struct MxOps;
+
+template <>
+struct MxOps<half_t> {
+  typedef _Float16 vec4 __attribute__((ext_vector_type(4)));
+  __device__ static floatx4 mma(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(vec4, u32x2{a0, a1}),
+                                                __builtin_bit_cast(vec4, u32x2{b0, b1}), c, 0, 0, 0);
+  }
+  // Round two probabilities to f16; return the packed pair and the rounded values.
+  __device__ static uint32_t pack2(float x, float y, float& rx, float& ry) {
+    const half_t hx = (half_t)x, hy = (half_t)y;
+    rx = (float)hx;
+    ry = (float)hy;
+    return (uint32_t)__builtin_bit_cast(uint16_t, hx) | ((uint32_t)__builtin_bit_cast(uint16_t, hy) << 16);
+  }
+};
+
+template <>
+struct MxOps<bf16_t> {
+  typedef short vec4 __attribute__((ext_vector_type(4)));
+  __device__ static floatx4 mma(uint32_t a0, uint32_t a1, uint32_t b0, uint32_t b1, floatx4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(vec4, u32x2{a0, a1}),
+                                                    __builtin_bit_cast(vec4, u32x2{b0, b1}), c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack2(float x, float y, float& rx, float& ry) {
+    const bf16_t hx = (bf16_t)x, hy = (bf16_t)y;
+    rx = (float)hx;
+    ry = (float)hy;
+    return (uint32_t)__builtin_bit_cast(uint16_t, hx) | ((uint32_t)__builtin_bit_cast(uint16_t, hy) << 16);
+  }
+};
+
+template <typename T, int D, bool EVICT>
+__device__ __forceinline__ void process_tile_mx(const TileRegs<T, D>& r, const QFrag<T, D>& qf, MxState<D>& st,
+                                                int G, float scale_log2, int tile, int key_end, int col, int grp,
+                                                float* srow) {
   constexpr int DPL = D / 16;
+  const floatx4 c = qf.dot(r);
+  const float c4[4] = {c[0], c[1], c[2], c[3]};
+  const uint32_t keep = (col < G) ? r.keep : 0u;
+  float s[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) s[i] = ((keep >> i) & 1u) ? c4[i] * scale_log2 : -INFINITY;
+  if constexpr (EVICT) {
+    if (col < G) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = tile + 4 * grp + i;
+        if (key < key_end) srow[key] = s[i];
+      }
+    }
+  }
+  float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+  tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
+  tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
+  const float m_new = fmaxf(st.m_run, tm);
+  const bool dead = (m_new == -INFINITY);
+  const float alpha = dead ? 1.f : exp2f(st.m_run - m_new);
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : exp2f(s[i] - m_new);
+  float pr[4];
+  const uint32_t b0 = MxOps<T>::pack2(p[0], p[1], pr[0], pr[1]);
+  const uint32_t b1 = MxOps<T>::pack2(p[2], p[3], pr[2], pr[3]);
+  st.l_run = st.l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
+  st.m_run = m_new;
+  if (__any(alpha != 1.f)) {
+#pragma unroll
+    for (int j = 0; j < DPL; ++j) st.acc[j] *= alpha;
+  }
+  // A operand of block j: the lane's four V rows at dim col*DPL + j.
+#pragma unroll
+  for (int j = 0; j < DPL; ++j) {
+    const uint32_t sel = (j & 1) ? 0x07060302u : 0x05040100u;
+    const int w = j >> 1;
+    const uint32_t a0 = __builtin_amdgcn_perm(r.v[1][w], r.v[0][w], sel);
+    const uint32_t a1 = __builtin_amdgcn_perm(r.v[3][w], r.v[2][w], sel);
+    st.acc[j] = MxOps<T>::mma(a0, a1, b0, b1, st.acc[j]);
+  }
+}
+
+template <typename T, int D, int GM>
+struct DecodeState {
+  typedef SoftmaxState<GM, D / 16> type;
+};
+template <int D, int GM>
+struct DecodeState<half_t, D, GM> {
+  typedef MxState<D> type;
+};
+template <int D, int GM>
+struct DecodeState<bf16_t, D, GM> {
+  typedef MxState<D> type;
+};
+
+// grid (splits, Hk, B), block 64*NW (NW waves).  Wave w takes the tiles
+// key_begin + 16*(w + NW*i), i = 0 .. nt-1, through a ring of NBUF register
+// tiles: step i issues the loads of tile i + NBUF - 1 (past the range: no
+// memory traffic) and then processes tile i, so NBUF-1 tiles stay in flight.
+template <typename T, int D, int GM, int NW, int NBUF, int MINW, bool EVICT>
+__global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a) {
+  constexpr int DPL = D / 16;
+  constexpr int STEP = 16 * NW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -296,76 +419,128 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
 
   const T* kbase = reinterpret_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const T* vbase = reinterpret_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(kbase, a.k_bytes);
+  const __amdgpu_buffer_rsrc_t vrs = make_rsrc(vbase, a.v_bytes);
+  const uint32_t k_rowb = (uint32_t)(a.k_ss * (int64_t)sizeof(T));
+  const uint32_t v_rowb = (uint32_t)(a.v_ss * (int64_t)sizeof(T));
 
-  QFrag<T, D> qf;
-  qf.load(reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh, a.q_sh, col, grp, G);
+  // Keep bitmap of the split's keys: attention mask and held-slot test.
+  __shared__ uint32_t sm_bits[kMaxBitmapKeys / 32];
+  const bool use_bits = (a.mask != nullptr) || (a.held_len > key_begin);
+  if (use_bits) {
+    const int64_t cur = a.cur_pos ? *a.cur_pos : INT64_MAX;
+    const uint8_t* mrow = a.mask ? a.mask + b * a.mask_sb : nullptr;
+    const int nwords = (key_end - key_begin + 31) >> 5;
+    for (int wd = threadIdx.x; wd < nwords; wd += 64 * NW) {
+      uint32_t bits = 0;
+      for (int j = 0; j < 32; ++j) {
+        const int key = key_begin + 32 * wd + j;
+        bool kp = key < key_end;
+        if (kp && mrow) kp = mrow[key] != 0;
+        if (kp && key < a.held_len)
+          kp = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key] != 0 &&
+               a.held_pos[b * a.hp_sb + hk * a.hp_sh + key] <= cur;
+        bits |= (kp ? 1u : 0u) << j;
+      }
+      sm_bits[wd] = bits;
+    }
+    __syncthreads();
+  }
+  const uint32_t* bits = use_bits ? sm_bits : nullptr;
 
-  const int64_t cur = a.cur_pos ? *a.cur_pos : INT64_MAX;
-  const uint8_t* mrow = a.mask ? a.mask + b * a.mask_sb : nullptr;
-  float* srow = a.scores ? a.scores + ((int64_t)b * a.Hq + hk * G + col) * a.S : nullptr;
-
-  SoftmaxState<GM, DPL> st;
+  constexpr bool MX = sizeof(T) == 2;
+  typename DecodeState<T, D, GM>::type st;
   st.m_run = -INFINITY;
   st.l_run = 0.f;
+  if constexpr (MX) {
 #pragma unroll
-  for (int g = 0; g < GM; ++g)
+    for (int j = 0; j < DPL; ++j) st.acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  } else {
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) st.acc[g][j] = 0.f;
+    for (int g = 0; g < GM; ++g)
+#pragma unroll
+      for (int j = 0; j < DPL; ++j) st.acc[g][j] = 0.f;
+  }
 
-  TileRegs<T, D> ra, rb;
-  int tile = key_begin + wave * 16;
-  if (tile < key_end) load_tile<T, D>(ra, kbase, vbase, a.k_ss, a.v_ss, tile, key_end, col, grp, a, b, hk, cur, mrow);
-  while (tile < key_end) {
-    if (tile + 64 < key_end) load_tile<T, D>(rb, kbase, vbase, a.k_ss, a.v_ss, tile + 64, key_end, col, grp, a, b, hk, cur, mrow);
-    process_tile<T, D, GM>(ra, qf, st, a, b, hk, tile, key_end, col, grp, cur, mrow, srow);
-    tile += 64;
-    if (tile >= key_end) break;
-    if (tile + 64 < key_end) load_tile<T, D>(ra, kbase, vbase, a.k_ss, a.v_ss, tile + 64, key_end, col, grp, a, b, hk, cur, mrow);
-    process_tile<T, D, GM>(rb, qf, st, a, b, hk, tile, key_end, col, grp, cur, mrow, srow);
-    tile += 64;
+  const int first = key_begin + wave * 16;
+  const int nt = first < key_end ? (key_end - first + STEP - 1) / STEP : 0;
+  if (nt > 0) {
+    TileRegs<T, D> r[NBUF];
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i)
+      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * STEP, key_begin, key_end, col, grp, bits);
+
+    QFrag<T, D> qf;
+    const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
+    qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
+    float* srow = EVICT ? a.scores + ((int64_t)b * a.Hq + hk * G + min(col, G - 1)) * a.S : nullptr;
+
+    for (int g0 = 0; g0 < nt; g0 += NBUF) {
+#pragma unroll
+      for (int j = 0; j < NBUF; ++j) {
+        const int t = g0 + j;
+        load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * STEP,
+                        key_begin, key_end, col, grp, bits);
+        if (t < nt) {
+          if constexpr (MX)
+            process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * STEP, key_end, col, grp, srow);
+          else
+            process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * STEP, key_end, col, grp, srow);
+        }
+      }
+    }
   }
 
   // ---- reduce the four row groups of the wave (they share m_run) ----
   float l_run = st.l_run;
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
+  __shared__ float sm_m[NW][GM];
+  __shared__ float sm_l[NW][GM];
+  __shared__ float sm_acc[NW][GM][D];
+  if (grp == 0 && col < GM) {
+    sm_m[wave][col] = st.m_run;
+    sm_l[wave][col] = l_run;
+  }
+  if constexpr (MX) {
+    // lane (grp, col) holds dims (4*grp + i) * DPL + j of head col
+    if (col < G) {
 #pragma unroll
-  for (int g = 0; g < GM; ++g)
+      for (int j = 0; j < DPL; ++j)
 #pragma unroll
-    for (int j = 0; j < DPL; ++j) {
-      float x = st.acc[g][j];
-      x += __shfl_xor(x, 16, 64);
-      x += __shfl_xor(x, 32, 64);
-      st.acc[g][j] = x;
+        for (int i = 0; i < 4; ++i) sm_acc[wave][col][(4 * grp + i) * DPL + j] = st.acc[j][i];
     }
-
-  __shared__ float sm_m[4][GM];
-  __shared__ float sm_l[4][GM];
-  __shared__ float sm_acc[4][GM][D];
-  if (grp == 0) {
-    if (col < GM) {
-      sm_m[wave][col] = st.m_run;
-      sm_l[wave][col] = l_run;
-    }
+  } else {
 #pragma unroll
     for (int g = 0; g < GM; ++g)
 #pragma unroll
-      for (int j = 0; j < DPL; ++j) sm_acc[wave][g][col * DPL + j] = st.acc[g][j];
+      for (int j = 0; j < DPL; ++j) {
+        float x = st.acc[g][j];
+        x += __shfl_xor(x, 16, 64);
+        x += __shfl_xor(x, 32, 64);
+        st.acc[g][j] = x;
+      }
+    if (grp == 0) {
+#pragma unroll
+      for (int g = 0; g < GM; ++g)
+#pragma unroll
+        for (int j = 0; j < DPL; ++j) sm_acc[wave][g][col * DPL + j] = st.acc[g][j];
+    }
   }
   __syncthreads();
 
   const int unit = b * a.Hk + hk;
   const int stride_part = G * D + 2 * G;
   T* obase = reinterpret_cast<T*>(a.out) + b * a.o_sb + (int64_t)(hk * G) * a.o_sh;
-  for (int e = threadIdx.x; e < G * D; e += 256) {
+  for (int e = threadIdx.x; e < G * D; e += 64 * NW) {
     const int g = e / D, d = e - g * D;
     float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) M = fmaxf(M, sm_m[w][g]);
+    for (int w = 0; w < NW; ++w) M = fmaxf(M, sm_m[w][g]);
     float A = 0.f, L = 0.f;
     if (M != -INFINITY) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < NW; ++w) {
         const float sc = exp2f(sm_m[w][g] - M);
         A = fmaf(sm_acc[w][g][d], sc, A);
         L = fmaf(sm_l[w][g], sc, L);
@@ -388,7 +563,9 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
   }
 }
 
-// Merge the split partials of every (b, kv head).  grid (Hk, B), block 256.
+// Merge the split partials of every (b, kv head) in one pass over the splits
+// (online rescaling, loads independent of the running values).
+// grid (Hk, B), block 256.
 template <typename T>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int D) {
   const int hk = blockIdx.x, b = blockIdx.y;
@@ -399,15 +576,19 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int D
   T* obase = reinterpret_cast<T*>(a.out) + b * a.o_sb + (int64_t)(hk * G) * a.o_sh;
   for (int e = threadIdx.x; e < G * D; e += blockDim.x) {
     const int g = e / D, d = e - g * D;
-    float M = -INFINITY;
-    for (int s = 0; s < a.splits; ++s) M = fmaxf(M, pu[s * stride_part + G * D + g]);
-    float A = 0.f, L = 0.f;
-    if (M != -INFINITY) {
-      for (int s = 0; s < a.splits; ++s) {
-        const float* ps = pu + s * stride_part;
-        const float sc = exp2f(ps[G * D + g] - M);
-        A = fmaf(ps[e], sc, A);
-        L = fmaf(ps[G * D + G + g], sc, L);
+    float M = -INFINITY, A = 0.f, L = 0.f;
+#pragma unroll 8
+    for (int s = 0; s < a.splits; ++s) {
+      const float* ps = pu + s * stride_part;
+      const float ms = ps[G * D + g];
+      const float as = ps[e];
+      const float ls = ps[G * D + G + g];
+      const float Mn = fmaxf(M, ms);
+      if (Mn != -INFINITY) {
+        const float c0 = exp2f(M - Mn), c1 = exp2f(ms - Mn);
+        A = A * c0 + as * c1;
+        L = L * c0 + ls * c1;
+        M = Mn;
       }
     }
     obase[g * a.o_sh + d] = from_f32<T>(A / L);
@@ -477,19 +658,53 @@ __global__ __launch_bounds__(256) void evict_score_kernel(const float* scores, c
   if (threadIdx.x == 0) idx[b] = si[0];
 }
 
-static int pick_splits(int64_t units, int64_t S, int64_t requested) {
-  int64_t splits = requested;
-  if (splits <= 0) {
-    // Enough workgroups to cover the 256 CUs about twice; a split smaller
-    // than 64 keys leaves waves of the workgroup idle.
-    const int64_t target_blocks = 512;
-    splits = cdiv(target_blocks, units);
+// Launch shape of one (element size, head_dim, group bucket) instance:
+//   nbuf  depth of the per-wave K/V register ring (tiles in flight + 1);
+//   minw  waves per SIMD the register budget is sized for (2: <= 256 VGPRs,
+//         1: up to 512 with the accumulation registers);
+//   nw    waves per workgroup (8 needs minw 2 and an epilogue of at most
+//         32 KB LDS, nw*gm*D floats).
+// Chosen so that no instance spills (checked with the compiler's
+// kernel-resource-usage report).
+struct DecodeCfg {
+  int nbuf, minw, nw;
+};
+
+constexpr DecodeCfg decode_cfg(int es, int D, int gm) {
+  int nbuf = 2, minw = 1;
+  if (es == 2) {
+    // MFMA P.V: the accumulators do not grow with the group.
+    if (D <= 128) { nbuf = 4; minw = 2; }
+  } else if (D <= 32) {
+    nbuf = 4; minw = 2;
+  } else if (D == 64) {
+    nbuf = gm >= 16 ? 2 : 4; minw = 2;
   }
-  const int64_t max_splits = cdiv(S, 64);
+  const int nw = (minw == 2 && gm * D <= 1024) ? 8 : 4;
+  return DecodeCfg{nbuf, minw, nw};
+}
+
+static int group_bucket(int64_t G) { return G <= 4 ? 4 : (G <= 8 ? 8 : 16); }
+
+// Key splits per (batch, kv head): enough workgroups to give every CU one
+// 8-wave (or two 4-wave) workgroups, no split shorter than one tile per wave,
+// and, when the keep bitmap is used (mask or held slot), no split longer
+// than the bitmap.
+static int pick_splits(int64_t units, int64_t S, int64_t requested, int nw, bool bitmap) {
+  int64_t splits = requested;
+  if (splits <= 0) splits = cdiv((int64_t)256 * 8 / nw, units);
+  const int64_t step = 16 * nw;
+  const int64_t max_splits = cdiv(S, step);
   if (splits > max_splits) splits = max_splits;
+  if (bitmap && splits < cdiv(S, kMaxBitmapKeys)) splits = cdiv(S, kMaxBitmapKeys);
   if (splits < 1) splits = 1;
-  const int64_t kps = cdiv(cdiv(S, splits), 64) * 64;
+  const int64_t kps = cdiv(cdiv(S, splits), step) * step;
   return (int)cdiv(S, kps);
+}
+
+static int64_t keys_per_split(int64_t S, int splits, int nw) {
+  const int64_t step = 16 * nw;
+  return cdiv(cdiv(S, splits), step) * step;
 }
 
 static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
@@ -513,24 +728,34 @@ static DecodeLayout decode_layout(int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
   return L;
 }
 
-template <typename T, int D, int GM>
+template <typename T, int D, int GM, int NW, int NBUF, int MINW>
 static void launch_decode(const DecodeArgs& a, hipStream_t st) {
   dim3 grid(a.splits, a.Hk, a.B);
-  hipLaunchKernelGGL((decode_attn_kernel<T, D, GM>), grid, dim3(256), 0, st, a);
+  if (a.scores)
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, true>), grid, dim3(64 * NW), 0, st, a);
+  else
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, false>), grid, dim3(64 * NW), 0, st, a);
   if (a.splits > 1)
     hipLaunchKernelGGL(decode_combine_kernel<T>, dim3(a.Hk, a.B), dim3(256), 0, st, a, D);
 }
 
+template <typename T, int D, int GM>
+static void launch_nw(const DecodeArgs& a, int nw, hipStream_t st) {
+  constexpr DecodeCfg c = decode_cfg((int)sizeof(T), D, GM);
+  (void)nw;  // equals c.nw: the host picked the splits for it
+  launch_decode<T, D, GM, c.nw, c.nbuf, c.minw>(a, st);
+}
+
 template <typename T, int D>
-static int dispatch_g(const DecodeArgs& a, hipStream_t st) {
+static int dispatch_g(const DecodeArgs& a, int nw, hipStream_t st) {
   if (a.G <= 4) {
-    launch_decode<T, D, 4>(a, st);
+    launch_nw<T, D, 4>(a, nw, st);
   } else if (a.G <= 8) {
-    launch_decode<T, D, 8>(a, st);
+    launch_nw<T, D, 8>(a, nw, st);
   } else {
     if constexpr (D <= 128) {
       if (a.G <= 16) {
-        launch_decode<T, D, 16>(a, st);
+        launch_nw<T, D, 16>(a, nw, st);
         return HC_OK;
       }
     }
@@ -540,13 +765,13 @@ static int dispatch_g(const DecodeArgs& a, hipStream_t st) {
 }
 
 template <typename T>
-static int dispatch_d(int64_t D, const DecodeArgs& a, hipStream_t st) {
+static int dispatch_d(int64_t D, const DecodeArgs& a, int nw, hipStream_t st) {
   switch (D) {
-    case 16: return dispatch_g<T, 16>(a, st);
-    case 32: return dispatch_g<T, 32>(a, st);
-    case 64: return dispatch_g<T, 64>(a, st);
-    case 128: return dispatch_g<T, 128>(a, st);
-    case 256: return dispatch_g<T, 256>(a, st);
+    case 16: return dispatch_g<T, 16>(a, nw, st);
+    case 32: return dispatch_g<T, 32>(a, nw, st);
+    case 64: return dispatch_g<T, 64>(a, nw, st);
+    case 128: return dispatch_g<T, 128>(a, nw, st);
+    case 256: return dispatch_g<T, 256>(a, nw, st);
     default: return set_error(HC_ERR_UNSUPPORTED, "decode: head_dim %lld unsupported (16/32/64/128/256)", (long long)D);
   }
 }
@@ -558,8 +783,15 @@ using namespace hc;
 extern "C" int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hk, int64_t D,
                                                  int64_t S, int64_t num_splits, int with_evict) {
   if (B <= 0 || Hq <= 0 || Hk <= 0 || D <= 0 || S <= 0) return 256;
-  const int splits = pick_splits(B * Hk, S, num_splits);
-  return decode_layout(B, Hq, Hk, D, S, splits, with_evict).total;
+  // The element size is not an argument: size for both workgroup shapes.
+  int64_t need = 0;
+  for (int nw : {4, 8})
+    for (bool bitmap : {false, true}) {
+      const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap);
+      const int64_t t = decode_layout(B, Hq, Hk, D, S, splits, with_evict).total;
+      if (t > need) need = t;
+    }
+  return need;
 }
 
 extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
@@ -595,7 +827,15 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
                  (k_ss * es) % 16 == 0 && (v_sb * es) % 16 == 0 && (v_sh * es) % 16 == 0 && (v_ss * es) % 16 == 0,
              "decode: q/k/v strides must be multiples of 16 bytes (row bytes %lld)", (long long)rowb);
   const int G = (int)(Hq / Hk);
-  const int splits = pick_splits(B * Hk, S, num_splits);
+  const int nw = decode_cfg(es, (int)D, group_bucket(G)).nw;
+  const bool bitmap = mask != nullptr || held_len > 0;
+  const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap);
+  // Buffer extents of one (b, kv head) must fit the 31-bit load offsets.
+  const int64_t k_bytes = ((S - 1) * k_ss + D) * es, v_bytes = ((S - 1) * v_ss + D) * es;
+  const int64_t q_bytes = ((Hq / Hk - 1) * q_sh + D) * es;
+  HC_REQUIRE(k_ss >= D && v_ss >= D && k_bytes < ((int64_t)1 << 31) && v_bytes < ((int64_t)1 << 31) &&
+                 q_bytes < ((int64_t)1 << 31),
+             "decode: one (batch, kv head) K/V/Q extent must be below 2 GiB with row stride >= D");
   const int with_evict = (evict_loss != nullptr || evict_idx != nullptr);
   const DecodeLayout lay = decode_layout(B, Hq, Hk, D, S, splits, with_evict);
   if (!workspace || workspace_bytes < lay.total)
@@ -619,14 +859,17 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
   a.ml = with_evict ? reinterpret_cast<float*>(ws + lay.ml_off) : nullptr;
   a.B = (int)B; a.Hq = (int)Hq; a.Hk = (int)Hk; a.G = G; a.S = (int)S;
   a.splits = splits;
-  a.keys_per_split = (int)(cdiv(cdiv(S, splits), 64) * 64);
+  a.keys_per_split = (int)keys_per_split(S, splits, nw);
   a.scale_log2 = (float)(scaling * 1.4426950408889634);
+  a.k_bytes = (uint32_t)k_bytes;
+  a.v_bytes = (uint32_t)v_bytes;
+  a.q_bytes = (uint32_t)q_bytes;
 
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int rc;
-  if (dtype == HC_DTYPE_F16) rc = dispatch_d<half_t>(D, a, st);
-  else if (dtype == HC_DTYPE_BF16) rc = dispatch_d<bf16_t>(D, a, st);
-  else rc = dispatch_d<float>(D, a, st);
+  if (dtype == HC_DTYPE_F16) rc = dispatch_d<half_t>(D, a, nw, st);
+  else if (dtype == HC_DTYPE_BF16) rc = dispatch_d<bf16_t>(D, a, nw, st);
+  else rc = dispatch_d<float>(D, a, nw, st);
   if (rc != HC_OK) return rc;
   if ((rc = check_launch("decode_attn")) != HC_OK) return rc;
 
