@@ -245,46 +245,90 @@ def time_graph(g, st, iters, flush=None):
     return statistics.mean(a.elapsed_time(b) for a, b in evs)
 
 
-def cpu_baseline(w, sample_seconds):
+def stream_rates(dev, nbytes=1 << 30, iters=10):
+    """Measured device bandwidth for context: a read sweep (max reduction)
+    over nbytes and a device copy of nbytes/2 -> nbytes/2.  The copy is also
+    the known-size kernel the FETCH_SIZE / WRITE_SIZE counters are scaled by."""
+    import torch
+    src = torch.ones(nbytes // 4, dtype=torch.float32, device=dev)
+    half = src.numel() // 2
+    dst = torch.empty(half, dtype=torch.float32, device=dev)
+    torch.amax(src)
+    dst.copy_(src[:half])
+    torch.cuda.synchronize()
+    e = [torch.cuda.Event(enable_timing=True) for _ in range(4)]
+    e[0].record()
+    for _ in range(iters):
+        torch.amax(src)
+    e[1].record()
+    for _ in range(iters):
+        dst.copy_(src[:half])
+    e[2].record()
+    torch.cuda.synchronize()
+    read = nbytes * iters / (e[0].elapsed_time(e[1]) * 1e-3) / 1e9
+    copy = 2 * half * 4 * iters / (e[1].elapsed_time(e[2]) * 1e-3) / 1e9
+    del src, dst
+    return {"read_GBps": round(read, 1), "copy_GBps": round(copy, 1), "copy_bytes_each_way": half * 4}
+
+
+def profiled_traffic(workload):
+    """HBM bytes per decode launch from the committed FETCH_SIZE / WRITE_SIZE
+    summary of this workload (rocprofv3 --pmc runs, scaled by a known-size
+    copy), or None if there is none."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"decode_attn_compaction_{workload}_pmc_traffic.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)", open(path).read(), re.M)
+    return int(m.group(1)) if m else None
+
+
+def cpu_baseline(w, sample_seconds, n_layers=4):
     """The reference's torch-CPU path (snapkv_importance -> keep_index ->
-    gather_kv, then cat + repeat_kv + SDPA decode) on a bounded sample of the
-    same workload -- layer 0's prompt, fp32-upcast -- on this host's cores."""
+    gather_kv, then per decode step cat + repeat_kv + SDPA) on a bounded
+    sample of the same workload: whole single-layer jobs (compaction of the
+    8k prompt + the decode steps) over the first n_layers layers' inputs,
+    fp32-upcast, repeated until sample_seconds of CPU time have been spent."""
     import torch
     from hotcold_kv import synthetic
     from oracle import reference as ref
 
     threads = max(1, min(16, os.cpu_count() or 1))
     torch.set_num_threads(threads)
-    p = synthetic.make_prompt(w, layer=0, seed=0, device="cpu")
-    q, k, v = p["q_post"].float(), p["k_post"].float(), p["v"].float()
+    layers = []
+    for l in range(min(n_layers, w.layers)):
+        p = synthetic.make_prompt(w, layer=l, seed=0, device="cpu")
+        toks = [synthetic.make_decode_token(w, l, t, seed=0, device="cpu") for t in range(w.decode_steps)]
+        layers.append((p["q_post"].float(), p["k_post"].float(), p["v"].float(),
+                       [(t["q_post"].float(), t["k_post"].float(), t["v"].float()) for t in toks]))
+    q, k, v, _ = layers[0]
     ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)  # warm-up
-    comp = []
-    t_end = time.perf_counter() + sample_seconds / 2
-    while len(comp) < 3 or (time.perf_counter() < t_end and len(comp) < 20):
+    comp, dec = [], []
+    jobs = 0
+    t_end = time.perf_counter() + sample_seconds
+    while jobs < 2 or time.perf_counter() < t_end:
+        q, k, v, toks = layers[jobs % len(layers)]
         t0 = time.perf_counter()
-        kk, vv = ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)
+        keys, vals = ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)
         comp.append(time.perf_counter() - t0)
+        for qt, kt, vt in toks:
+            t0 = time.perf_counter()
+            _, keys, vals = ref.press_decode_torch(qt, keys, vals, kt, vt, w.scaling)
+            dec.append(time.perf_counter() - t0)
+        jobs += 1
     comp_ms_layer = statistics.median(comp) * 1e3
-    dec = []
-    keys, vals = kk, vv
-    t_end = time.perf_counter() + sample_seconds / 2
-    t = 0
-    while t < w.decode_steps and (len(dec) < 3 or time.perf_counter() < t_end):
-        tok = synthetic.make_decode_token(w, 0, t, seed=0, device="cpu")
-        t0 = time.perf_counter()
-        _, keys, vals = ref.press_decode_torch(tok["q_post"].float(), keys, vals, tok["k_post"].float(),
-                                               tok["v"].float(), w.scaling)
-        dec.append(time.perf_counter() - t0)
-        t += 1
-    dec_us = statistics.median(dec[1:] if len(dec) > 1 else dec) * 1e6
+    dec_us = statistics.median(dec) * 1e6
+    spent = sum(comp) + sum(dec)
     return {
         "value": round(dec_us, 2),
         "unit": "us/layer-step",
         "cores": threads,
         "kind": "port",
-        "sample": (f"layer 0 of {w.name}: {len(comp)} compactions ({comp_ms_layer:.1f} ms/layer, "
-                   f"x{w.layers} = {comp_ms_layer * w.layers:.1f} ms for all layers) and {len(dec)} decode "
-                   f"steps (append + SDPA), fp32-upcast torch CPU restating scoring.py / layer_state.py"),
+        "sample": (f"{jobs} single-layer jobs of {w.name} cycling over layers 0-{len(layers) - 1} "
+                   f"({spent:.1f} s of CPU time): each an {w.seq_len}-token SnapKV compaction "
+                   f"(median {comp_ms_layer:.2f} ms; x{w.layers} layers = {comp_ms_layer * w.layers:.1f} ms) and "
+                   f"{w.decode_steps} decode steps (append + SDPA, median value above); fp32-upcast torch CPU "
+                   f"restating scoring.py / layer_state.py"),
         "compact_ms_32_layers": round(comp_ms_layer * w.layers, 2),
     }
 
@@ -294,7 +338,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=5)
     ap.add_argument("--warmup", type=int, default=2)
-    ap.add_argument("--workload", default="c1_llama8b_8k_b512")
+    ap.add_argument("--workload", default="llama8b_8k_b512")
     ap.add_argument("--cpu-sample-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     args = ap.parse_args()
@@ -311,6 +355,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     log(f"workload {w.name}: generating inputs on {torch.cuda.get_device_name(dev)}")
+    stream = stream_rates(dev)
+    log(f"device read sweep {stream['read_GBps']:.0f} GB/s, copy {stream['copy_GBps']:.0f} GB/s")
     s = Setup(w, dev)
     flush = CacheSweep(dev)
     torch.cuda.synchronize()
@@ -374,7 +420,7 @@ def main():
         "decode_us_per_layer_launch_warm": round(pl_warm_ms * 1e3 / w.layers, 3),
         "decode_launch_us_warm_last_step": round(warm_dec_ms * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(w.name),
                      "kernel": "decode_attn_kernel (+ decode_combine_kernel)",
                      "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3)},
         "roofline_compaction": {"bound": "hbm", "achieved": round(c_achieved, 1), "peak": HBM_PEAK_GBS,
@@ -383,6 +429,7 @@ def main():
                                 "scoring_tflops_fp64": round(sflops / (comp_ms * 1e-3) / 1e12, 3),
                                 "scoring_mfma_frac": round(sflops / (comp_ms * 1e-3) / 1e12
                                                            / FP64_MFMA_PEAK_TFLOPS, 4)},
+        "device_stream": stream,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

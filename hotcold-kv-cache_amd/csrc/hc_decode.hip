@@ -673,8 +673,9 @@ struct DecodeCfg {
 constexpr DecodeCfg decode_cfg(int es, int D, int gm) {
   int nbuf = 2, minw = 1;
   if (es == 2) {
-    // MFMA P.V: the accumulators do not grow with the group.
-    if (D <= 128) { nbuf = 4; minw = 2; }
+    // MFMA P.V: the accumulators do not grow with the group.  One tile in
+    // flight per wave measured fastest (deeper rings add VGPRs, no speed).
+    if (D <= 128) { nbuf = 2; minw = 2; }
   } else if (D <= 32) {
     nbuf = 4; minw = 2;
   } else if (D == 64) {
@@ -686,13 +687,18 @@ constexpr DecodeCfg decode_cfg(int es, int D, int gm) {
 
 static int group_bucket(int64_t G) { return G <= 4 ? 4 : (G <= 8 ? 8 : 16); }
 
-// Key splits per (batch, kv head): enough workgroups to give every CU one
-// 8-wave (or two 4-wave) workgroups, no split shorter than one tile per wave,
-// and, when the keep bitmap is used (mask or held slot), no split longer
-// than the bitmap.
-static int pick_splits(int64_t units, int64_t S, int64_t requested, int nw, bool bitmap) {
+// Key splits per (batch, kv head).  Every split beyond one costs a second
+// (merge) launch, a few microseconds of latency, so few units with short key
+// ranges (up to 512 KB of K and V per unit, e.g. one layer at batch 1) run
+// unsplit.  Otherwise: enough workgroups to give every CU one 8-wave (or two
+// 4-wave) workgroups, no split shorter than one tile per wave, and, when the
+// keep bitmap is used (mask or held slot), no split longer than the bitmap.
+static int pick_splits(int64_t units, int64_t S, int64_t requested, int nw, bool bitmap, int64_t row_bytes) {
   int64_t splits = requested;
-  if (splits <= 0) splits = cdiv((int64_t)256 * 8 / nw, units);
+  if (splits <= 0) {
+    splits = cdiv((int64_t)256 * 8 / nw, units);
+    if (units < 128 && S * 2 * row_bytes <= ((int64_t)512 << 10)) splits = 1;
+  }
   const int64_t step = 16 * nw;
   const int64_t max_splits = cdiv(S, step);
   if (splits > max_splits) splits = max_splits;
@@ -783,14 +789,15 @@ using namespace hc;
 extern "C" int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hk, int64_t D,
                                                  int64_t S, int64_t num_splits, int with_evict) {
   if (B <= 0 || Hq <= 0 || Hk <= 0 || D <= 0 || S <= 0) return 256;
-  // The element size is not an argument: size for both workgroup shapes.
+  // The element size is not an argument: size for every launch shape.
   int64_t need = 0;
-  for (int nw : {4, 8})
-    for (bool bitmap : {false, true}) {
-      const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap);
-      const int64_t t = decode_layout(B, Hq, Hk, D, S, splits, with_evict).total;
-      if (t > need) need = t;
-    }
+  for (int es : {2, 4})
+    for (int nw : {4, 8})
+      for (bool bitmap : {false, true}) {
+        const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap, D * es);
+        const int64_t t = decode_layout(B, Hq, Hk, D, S, splits, with_evict).total;
+        if (t > need) need = t;
+      }
   return need;
 }
 
@@ -829,7 +836,7 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
   const int G = (int)(Hq / Hk);
   const int nw = decode_cfg(es, (int)D, group_bucket(G)).nw;
   const bool bitmap = mask != nullptr || held_len > 0;
-  const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap);
+  const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap, D * es);
   // Buffer extents of one (b, kv head) must fit the 31-bit load offsets.
   const int64_t k_bytes = ((S - 1) * k_ss + D) * es, v_bytes = ((S - 1) * v_ss + D) * es;
   const int64_t q_bytes = ((Hq / Hk - 1) * q_sh + D) * es;

@@ -59,17 +59,17 @@ class Workload:
 
 
 WORKLOADS = {
-    "c0_plumbing_fp32": Workload("c0_plumbing_fp32", layers=1, batch=1, seq_len=2048, dtype=torch.float32,
+    "plumbing_fp32_2k_b512": Workload("plumbing_fp32_2k_b512", layers=1, batch=1, seq_len=2048, dtype=torch.float32,
                                  budget=512, window=32, pool=7, decode_steps=64),
-    "c1_llama8b_8k_b512": Workload("c1_llama8b_8k_b512", layers=32, batch=1, seq_len=8192, dtype=torch.float16,
+    "llama8b_8k_b512": Workload("llama8b_8k_b512", layers=32, batch=1, seq_len=8192, dtype=torch.float16,
                                    budget=512, window=32, pool=7, decode_steps=63, needles=16),
-    "c2_llama8b_16k_b1024_held64": Workload("c2_llama8b_16k_b1024_held64", layers=32, batch=1, seq_len=16384,
+    "llama8b_16k_b1024_held64": Workload("llama8b_16k_b1024_held64", layers=32, batch=1, seq_len=16384,
                                             dtype=torch.float16, budget=1024, window=32, pool=7, decode_steps=128,
                                             held=64, retrieve_every=16, needles=16),
-    "c3_b16_32k_b2048_held128": Workload("c3_b16_32k_b2048_held128", layers=32, batch=16, seq_len=32768,
+    "b16_32k_b2048_held128": Workload("b16_32k_b2048_held128", layers=32, batch=16, seq_len=32768,
                                          dtype=torch.float16, budget=2048, window=64, pool=7, decode_steps=256,
                                          held=128, retrieve_every=16, needles=16, per_sequence_seeds=True),
-    "c4_bf16_b4_64k_b4096_held256": Workload("c4_bf16_b4_64k_b4096_held256", layers=32, batch=4, seq_len=65536,
+    "bf16_b4_64k_b4096_held256": Workload("bf16_b4_64k_b4096_held256", layers=32, batch=4, seq_len=65536,
                                              dtype=torch.bfloat16, budget=4096, window=64, pool=7,
                                              decode_steps=128, held=256, retrieve_every=8, prefill_retrieval=256,
                                              needles=16, outliers=4, per_sequence_seeds=True),

@@ -175,10 +175,10 @@ def test_snapkv_scores_bit_exact(B, Hq, Hk, S, D, W, dtype, pool, pooling):
     assert torch.equal(got, want), (got - want).abs().max()
 
 
-def test_snapkv_scores_and_keep_c1_layer():
+def test_snapkv_scores_and_keep_llama8b_8k_layer():
     """One layer of the 8k fp16 workload with needles: scores, kept indices
     and the compacted K/V are bit-exact."""
-    w = synthetic.WORKLOADS["c1_llama8b_8k_b512"]
+    w = synthetic.WORKLOADS["llama8b_8k_b512"]
     p = synthetic.make_prompt(w, layer=3, seed=0, device="cpu")
     qd, kd, vd = p["q_post"].to(DEV), p["k_post"].to(DEV), p["v"].to(DEV)
     got = ops.snapkv_scores(qd, kd, w.window, w.scaling, w.pool, "maxpool")
