@@ -38,6 +38,14 @@ HIPCC_FLAGS = [
 ]
 
 
+# Per-file extra flags.  The window-scoring kernels keep their fp64 MFMA
+# accumulators in VGPRs: with the default AGPR form the compiler copies all 32
+# accumulator registers between the two files on every loop iteration.
+FILE_FLAGS = {
+    "hc_snapkv.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def hipcc():
     exe = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
     if not os.path.exists(exe):
@@ -46,9 +54,9 @@ def hipcc():
 
 
 def _compile(src, obj):
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", src, "-o", obj]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
-    errs = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l)
+    errs = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and "--hip-link" not in l)
     if r.returncode != 0:
         raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{errs}")
     return errs

@@ -168,4 +168,31 @@ __device__ __forceinline__ uint32_t order_key(float x) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------------------
+// Raw buffer loads.  A load whose offset is past the resource's extent returns
+// zeros without a memory access, so kernels can issue every load
+// unconditionally (which keeps the compiler's vmcnt waits exact) and steer
+// out-of-range lanes to kOob.
+// ---------------------------------------------------------------------------
+constexpr uint32_t kOob = 0x80000000u;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+template <int BYTES>
+__device__ __forceinline__ void bload(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t* w) {
+  if constexpr (BYTES == 16) {
+    const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+    w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
+  } else if constexpr (BYTES == 8) {
+    const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+    w[0] = x[0]; w[1] = x[1];
+  } else if constexpr (BYTES == 4) {
+    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
+  } else {
+    w[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+  }
+}
+
 }  // namespace hc

@@ -55,28 +55,6 @@ struct DecodeArgs {
 
 // Keys of one split when the keep bitmap is needed (mask or held slot).
 constexpr int kMaxBitmapKeys = 16384;
-// Buffer offset past every extent: the load returns zeros, no memory access.
-constexpr uint32_t kOob = 0x80000000u;
-
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
-
-template <int BYTES>
-__device__ __forceinline__ void bload(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t* w) {
-  if constexpr (BYTES == 16) {
-    const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
-    w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
-  } else if constexpr (BYTES == 8) {
-    const u32x2 x = __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
-    w[0] = x[0]; w[1] = x[1];
-  } else if constexpr (BYTES == 4) {
-    w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
-  } else {
-    w[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
-  }
-}
-
 // ---------------------------------------------------------------------------
 // Per-lane registers of one 16-key tile.
 //   K (MFMA A operand): lane l holds key row tile + l%16, 16-byte pieces at

@@ -28,7 +28,6 @@ namespace hc {
 
 constexpr int kChunkM = 128;  // keys per logits workgroup (4 waves x 32 keys)
 constexpr int kRowBlk = 32;   // window rows per logits workgroup (fp64 accumulators)
-constexpr int kSumChunk = 512;  // keys per rowsum workgroup (two per lane)
 constexpr int kMaxW = 256;
 constexpr int kMaxPool = 32;  // max half-width of the pooling window
 
@@ -83,50 +82,57 @@ __global__ void qmean_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh
   *dst = sum / (double)G;
 }
 
-// Raw 16-byte pieces of one 8-dim chunk of a key row (16-bit types: one
-// piece; fp32: two).
+typedef double doublex4 __attribute__((ext_vector_type(4)));
+
+// K operand of the fp64 MFMA.  Lane (kk, col) needs, for k-step t, the key
+// element at dim 4t + kk.  2-byte types: a 16-byte load brings dims d0..d0+7
+// of the lane's key row, and one byte permute with a per-lane selector
+// extracts dim d0 + kk (dwords 0,1) or d0 + 4 + kk (dwords 2,3): no lane
+// exchange, no dynamic register indexing.  fp32: a 4-byte load per k-step.
 template <typename T>
-struct KChunk {
-  static constexpr int N = (sizeof(T) == 4) ? 2 : 1;
-  uint32_t w[4 * N];
+struct KOperand;
+
+template <>
+struct KOperand<half_t> {
+  static constexpr int DSTEP = 8;  // dims per load
+  uint32_t w[4];
+  __device__ static uint32_t sel(int kk) { return 0x0c0c0000u | ((uint32_t)(2 * kk + 1) << 8) | (uint32_t)(2 * kk); }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int d0, int kk) {
+    (void)kk;
+    bload<16>(r, row_off == kOob ? kOob : row_off + (uint32_t)(d0 * 2), w);
+  }
+  __device__ double elem(int half, uint32_t sl) const {
+    const uint32_t bits = half ? __builtin_amdgcn_perm(w[3], w[2], sl) : __builtin_amdgcn_perm(w[1], w[0], sl);
+    return (double)(float)__builtin_bit_cast(half_t, (uint16_t)bits);
+  }
 };
 
-template <typename T>
-__device__ __forceinline__ void load_kchunk(KChunk<T>& c, const T* p, bool ok) {
-#pragma unroll
-  for (int i = 0; i < KChunk<T>::N; ++i) {
-    u32x4 x = {0u, 0u, 0u, 0u};
-    if (ok) x = ld16(reinterpret_cast<const char*>(p) + 16 * i);
-    c.w[4 * i + 0] = x[0];
-    c.w[4 * i + 1] = x[1];
-    c.w[4 * i + 2] = x[2];
-    c.w[4 * i + 3] = x[3];
+template <>
+struct KOperand<bf16_t> {
+  static constexpr int DSTEP = 8;
+  uint32_t w[4];
+  // the element's two bytes land in the high half: the fp32 of the bf16
+  __device__ static uint32_t sel(int kk) { return ((uint32_t)(2 * kk + 1) << 24) | ((uint32_t)(2 * kk) << 16) | 0x0c0cu; }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int d0, int kk) {
+    (void)kk;
+    bload<16>(r, row_off == kOob ? kOob : row_off + (uint32_t)(d0 * 2), w);
   }
-}
+  __device__ double elem(int half, uint32_t sl) const {
+    const uint32_t bits = half ? __builtin_amdgcn_perm(w[3], w[2], sl) : __builtin_amdgcn_perm(w[1], w[0], sl);
+    return (double)__uint_as_float(bits);
+  }
+};
 
-// Element j (0..7) of the chunk as an exact double, j chosen per lane.
-template <typename T>
-__device__ __forceinline__ double kchunk_elem(const KChunk<T>& c, int j);
 template <>
-__device__ __forceinline__ double kchunk_elem<half_t>(const KChunk<half_t>& c, int j) {
-  const uint32_t word = (j & 4) ? ((j & 2) ? c.w[3] : c.w[2]) : ((j & 2) ? c.w[1] : c.w[0]);
-  const uint16_t bits = (uint16_t)((j & 1) ? (word >> 16) : (word & 0xffffu));
-  return (double)(float)__builtin_bit_cast(half_t, bits);
-}
-template <>
-__device__ __forceinline__ double kchunk_elem<bf16_t>(const KChunk<bf16_t>& c, int j) {
-  const uint32_t word = (j & 4) ? ((j & 2) ? c.w[3] : c.w[2]) : ((j & 2) ? c.w[1] : c.w[0]);
-  const uint32_t bits = (j & 1) ? (word & 0xffff0000u) : (word << 16);
-  return (double)__uint_as_float(bits);
-}
-template <>
-__device__ __forceinline__ double kchunk_elem<float>(const KChunk<float>& c, int j) {
-  const uint32_t lo = (j & 2) ? ((j & 1) ? c.w[3] : c.w[2]) : ((j & 1) ? c.w[1] : c.w[0]);
-  const uint32_t hi = (j & 2) ? ((j & 1) ? c.w[7] : c.w[6]) : ((j & 1) ? c.w[5] : c.w[4]);
-  return (double)__uint_as_float((j & 4) ? hi : lo);
-}
-
-typedef double doublex4 __attribute__((ext_vector_type(4)));
+struct KOperand<float> {
+  static constexpr int DSTEP = 4;
+  uint32_t w[1];
+  __device__ static uint32_t sel(int) { return 0u; }
+  __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int d0, int kk) {
+    bload<4>(r, row_off == kOob ? kOob : row_off + (uint32_t)((d0 + kk) * 4), w);
+  }
+  __device__ double elem(int, uint32_t) const { return (double)__uint_as_float(w[0]); }
+};
 
 // Window logits on the fp64 matrix cores.  v_mfma_f64_16x16x4f64 computes
 // every output as a sequential IEEE fma chain over its four k terms in
@@ -135,105 +141,141 @@ typedef double doublex4 __attribute__((ext_vector_type(4)));
 //   A (16 rows x 4): lane l supplies qf[w0 + 16*nb + l%16][4t + l/16]
 //   B (4 x 16 keys): lane l supplies k[key0 + 16*mb + l%16][4t + l/16]
 //   D: lane l holds rows w0 + 16*nb + l/16 + 4i, key key0 + 16*mb + l%16
-// grid (ceil(S/128), Hk * nrb, B), block 256: each wave covers 32 keys
-// (two 16-key blocks) x 32 window rows (two 16-row blocks).
-template <typename T>
+// grid (ceil(S / (128*kLogitChunks)), Hk * nrb, B), block 256.  The 32 x D
+// fp64 query block is staged in LDS once and reused for kLogitChunks chunks
+// of 128 keys; per chunk each wave covers 32 keys (two 16-key blocks) x 32
+// window rows (two 16-row blocks).  K loads are unconditional buffer loads
+// one chunk of dims ahead (rows past S read zeros).  Each 32x32 fp32 tile is
+// staged in LDS and written as full 128-byte row segments.
+constexpr int kLogitChunks = 4;
+
+template <typename T, int MODE>
 __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, int64_t k_sb, int64_t k_sh,
-                                                     int64_t k_ss, const double* __restrict__ qf, int Hk, int S,
-                                                     int D, int W, int wpad, int mode, double scaling,
+                                                     int64_t k_ss, uint32_t k_bytes, const double* __restrict__ qf,
+                                                     int Hk, int S, int D, int W, int wpad, double scaling,
                                                      float* __restrict__ logits, uint32_t* __restrict__ rmax) {
   extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
+  __shared__ float tile[4][kRowBlk][33];
+  __shared__ float red[4][kRowBlk];
   const int nrb = wpad / kRowBlk;
   const int rb = blockIdx.y % nrb;
   const int h = blockIdx.y / nrb;
   const int b = blockIdx.z;
-  const int chunk = blockIdx.x;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, kk = lane >> 4;
   const int w0 = rb * kRowBlk;
   const int nw = min(kRowBlk, W - w0);
   const int64_t bh = (int64_t)b * Hk + h;
   const int ld = D + 1;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + b * k_sb + h * k_sh, k_bytes);
+  const uint32_t rowb = (uint32_t)(k_ss * (int64_t)sizeof(T));
+  constexpr int DS = KOperand<T>::DSTEP;
+  const int qpos0 = S - W + w0;
+  const uint32_t sl = KOperand<T>::sel(kk);
+  const double* q0 = sq + col * ld + kk;         // rows 0..15 of the block
+  const double* q1 = sq + (16 + col) * ld + kk;  // rows 16..31
+  const int rr = lane >> 3, kq = 4 * (lane & 7);
+  float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+
+  KOperand<T> ca, cb, na, nb;
+  int key0 = blockIdx.x * (kChunkM * kLogitChunks) + wave * 32;
+  uint32_t off0 = key0 + col < S ? (uint32_t)(key0 + col) * rowb : kOob;
+  uint32_t off1 = key0 + 16 + col < S ? (uint32_t)(key0 + 16 + col) * rowb : kOob;
+  // first K chunk in flight before the q block is staged
+  ca.load(krs, off0, 0, kk);
+  cb.load(krs, off1, 0, kk);
   const double* qsrc = qf + (bh * wpad + w0) * D;
   for (int i = threadIdx.x; i < kRowBlk * D; i += 256) sq[(i / D) * ld + (i % D)] = qsrc[i];
   __syncthreads();
 
-  const int key0 = chunk * kChunkM + wave * 32;
-  const T* kb = k + b * k_sb + h * k_sh;
-  const int r0 = key0 + col, r1 = key0 + 16 + col;
-  const T* kr0 = kb + (int64_t)min(r0, S - 1) * k_ss;
-  const T* kr1 = kb + (int64_t)min(r1, S - 1) * k_ss;
-  const bool ok0 = r0 < S, ok1 = r1 < S;
-  const double* q0 = sq + col * ld + kk;         // rows 0..15 of the block
-  const double* q1 = sq + (16 + col) * ld + kk;  // rows 16..31
-
-  doublex4 acc00 = {0.0, 0.0, 0.0, 0.0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
-  KChunk<T> ca, cb;
-  load_kchunk<T>(ca, kr0, ok0);
-  load_kchunk<T>(cb, kr1, ok1);
-  for (int d0 = 0; d0 < D; d0 += 8) {
-    KChunk<T> na, nb;
-    const bool more = d0 + 8 < D;
-    if (more) {
-      load_kchunk<T>(na, kr0 + d0 + 8, ok0);
-      load_kchunk<T>(nb, kr1 + d0 + 8, ok1);
-    }
+  for (int c = 0; c < kLogitChunks; ++c) {
+    doublex4 acc00 = {0.0, 0.0, 0.0, 0.0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
+    auto steps = [&](const KOperand<T>& xa, const KOperand<T>& xb, int d0) {
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {  // k-steps t = d0/4 + half
-      const int d = d0 + 4 * half;
-      const double a0 = q0[d], a1 = q1[d];
-      const double b0 = kchunk_elem<T>(ca, 4 * half + kk);
-      const double b1 = kchunk_elem<T>(cb, 4 * half + kk);
-      acc00 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc00, 0, 0, 0);
-      acc01 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc01, 0, 0, 0);
-      acc10 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc10, 0, 0, 0);
-      acc11 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc11, 0, 0, 0);
+      for (int hf = 0; hf < DS / 4; ++hf) {  // k-steps t = d0/4 + hf
+        const int d = d0 + 4 * hf;
+        const double a0 = q0[d], a1 = q1[d];
+        const double b0 = xa.elem(hf, sl);
+        const double b1 = xb.elem(hf, sl);
+        acc00 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc00, 0, 0, 0);
+        acc01 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc01, 0, 0, 0);
+        acc10 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc10, 0, 0, 0);
+        acc11 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc11, 0, 0, 0);
+      }
+    };
+    // ping-pong over pairs of dim chunks (D % 16 == 0); the final pair of
+    // loads targets dim 0 of this wave's rows in the next chunk
+    const int nkey0 = key0 + kChunkM;
+    const uint32_t noff0 = nkey0 + col < S ? (uint32_t)(nkey0 + col) * rowb : kOob;
+    const uint32_t noff1 = nkey0 + 16 + col < S ? (uint32_t)(nkey0 + 16 + col) * rowb : kOob;
+    for (int d0 = 0; d0 < D; d0 += 2 * DS) {
+      na.load(krs, off0, d0 + DS, kk);
+      nb.load(krs, off1, d0 + DS, kk);
+      steps(ca, cb, d0);
+      const bool last = d0 + 2 * DS >= D;
+      ca.load(krs, last ? noff0 : off0, last ? 0 : d0 + 2 * DS, kk);
+      cb.load(krs, last ? noff1 : off1, last ? 0 : d0 + 2 * DS, kk);
+      steps(na, nb, d0 + DS);
     }
-    if (more) {
-      ca = na;
-      cb = nb;
-    }
-  }
 
-  // Epilogue: lane holds rows w0 + 16*nb + kk + 4i for key key0 + 16*mb + col.
-  const double r00[4] = {acc00[0], acc00[1], acc00[2], acc00[3]};
-  const double r01[4] = {acc01[0], acc01[1], acc01[2], acc01[3]};
-  const double r10[4] = {acc10[0], acc10[1], acc10[2], acc10[3]};
-  const double r11[4] = {acc11[0], acc11[1], acc11[2], acc11[3]};
-  __shared__ float red[4][kRowBlk];
-  const int qpos0 = S - W + w0;
-#pragma unroll
-  for (int nbk = 0; nbk < 2; ++nbk) {
+    // Epilogue: lane holds rows 16*nbk + kk + 4i for keys 16*mb + col.
+    const double r00[4] = {acc00[0], acc00[1], acc00[2], acc00[3]};
+    const double r01[4] = {acc01[0], acc01[1], acc01[2], acc01[3]};
+    const double r10[4] = {acc10[0], acc10[1], acc10[2], acc10[3]};
+    const double r11[4] = {acc11[0], acc11[1], acc11[2], acc11[3]};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int w = 16 * nbk + kk + 4 * i;  // row within the block
-      float m = -INFINITY;
 #pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        const double v = nbk == 0 ? (mb == 0 ? r00[i] : r10[i]) : (mb == 0 ? r01[i] : r11[i]);
-        const int key = key0 + 16 * mb + col;
-        float L;
-        if (mode == HC_SCORE_SNAPKV) {
-          L = (key > qpos0 + w) ? -INFINITY : (float)(v * scaling);
-        } else {
-          L = (float)(v / scaling);
+      for (int nbk = 0; nbk < 2; ++nbk) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          const double v = nbk == 0 ? (mb == 0 ? r00[i] : r10[i]) : (mb == 0 ? r01[i] : r11[i]);
+          const int w = 16 * nbk + kk + 4 * i;
+          const int kc = 16 * mb + col;
+          const int key = key0 + kc;
+          float L;
+          if constexpr (MODE == HC_SCORE_SNAPKV) L = (key > qpos0 + w) ? -INFINITY : (float)(v * scaling);
+          else L = (float)(v / scaling);
+          tile[wave][w][kc] = (key < S && w < nw) ? L : -INFINITY;
         }
-        if (key < S && w < nw) {
-          logits[(bh * W + w0 + w) * S + key] = L;
-          m = fmaxf(m, L);
-        }
-      }
-      if (mode == HC_SCORE_SNAPKV) {
-        // max over the 16 lanes that share this row (same kk)
-        m = fmaxf(m, __shfl_xor(m, 1, 64));
-        m = fmaxf(m, __shfl_xor(m, 2, 64));
-        m = fmaxf(m, __shfl_xor(m, 4, 64));
-        m = fmaxf(m, __shfl_xor(m, 8, 64));
-        if (col == 0) red[wave][w] = m;
       }
     }
+    // the tile is private to this wave: its LDS accesses complete in order
+    __builtin_amdgcn_wave_barrier();
+    const bool vec = ((S & 3) == 0) && (key0 + 32 <= S);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int w = 8 * j + rr;
+      const float x0 = tile[wave][w][kq], x1 = tile[wave][w][kq + 1];
+      const float x2 = tile[wave][w][kq + 2], x3 = tile[wave][w][kq + 3];
+      if (w < nw && key0 < S) {
+        float* dst = logits + (bh * W + w0 + w) * S + key0 + kq;
+        if (vec) {
+          *reinterpret_cast<floatx4*>(dst) = floatx4{x0, x1, x2, x3};
+        } else {
+          const float xs[4] = {x0, x1, x2, x3};
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (key0 + kq + e < S) dst[e] = xs[e];
+        }
+      }
+      if constexpr (MODE == HC_SCORE_SNAPKV) mrow[j] = fmaxf(mrow[j], fmaxf(fmaxf(x0, x1), fmaxf(x2, x3)));
+    }
+    __builtin_amdgcn_wave_barrier();
+    key0 = nkey0;
+    off0 = noff0;
+    off1 = noff1;
   }
-  if (mode != HC_SCORE_SNAPKV) return;
+
+  if constexpr (MODE != HC_SCORE_SNAPKV) return;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    float m = mrow[j];
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    m = fmaxf(m, __shfl_xor(m, 4, 64));
+    if ((lane & 7) == 0) red[wave][8 * j + rr] = m;
+  }
   __syncthreads();
   if (threadIdx.x < nw) {
     const int w = threadIdx.x;
@@ -247,84 +289,69 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// grid (ceil(S/kSumChunk), Hk, B), block 256: exact fixed-point softmax
-// denominators.  Each lane accumulates its keys for 16 rows at a time; a
-// butterfly reduce-scatter then leaves the wave sum of row (lane >> 2) in
-// lanes 4r .. 4r+3 (16 exchanges per row block instead of a full reduction
-// per row).
-constexpr int kSumRows = 16;
+// Exact fixed-point softmax denominators.  grid (ceil(W/4), Hk, B), block
+// 256: each wave streams one window row of the logits (4 keys per lane per
+// step, kSumRing steps in flight), sums rint(e * 2^44) exactly in uint64 and
+// writes the row's total (no atomics: one wave owns the row).
+constexpr int kSumRing = 4;
+
+template <bool VEC>
 __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ logits,
                                                      const uint32_t* __restrict__ rmax, int Hk, int S, int W,
                                                      uint64_t* __restrict__ lsum) {
-  const int h = blockIdx.y, b = blockIdx.z;
-  const int64_t bh = (int64_t)b * Hk + h;
-  __shared__ float sm_m[kMaxW];
-  __shared__ uint64_t sm_red[4][kSumRows];
-  for (int w = threadIdx.x; w < W; w += blockDim.x) sm_m[w] = key_to_float(rmax[bh * W + w]);
-  __syncthreads();
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int s0 = blockIdx.x * kSumChunk + threadIdx.x;
-  for (int w0 = 0; w0 < W; w0 += kSumRows) {
-    const int nw = min(kSumRows, W - w0);
-    uint64_t acc[kSumRows];
+  const int w = blockIdx.x * 4 + wave;
+  if (w >= W) return;
+  const int64_t bh = (int64_t)blockIdx.z * Hk + blockIdx.y;
+  const float m = key_to_float(rmax[bh * W + w]);
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + (bh * W + w) * S, (uint32_t)S * 4u);
+  const int nstep = (S + 255) / 256;
+  uint64_t acc[4] = {0, 0, 0, 0};
+  uint32_t x[kSumRing][4];
+  auto load = [&](uint32_t (&dst)[4], int step) {
+    const int key = step * 256 + lane * 4;
+    if constexpr (VEC) {
+      bload<16>(rs, key < S ? (uint32_t)key * 4u : kOob, dst);
+    } else {
 #pragma unroll
-    for (int w = 0; w < kSumRows; ++w) acc[w] = 0;
-#pragma unroll 1
-    for (int i = 0; i < kSumChunk / 256; ++i) {
-      const int s = s0 + 256 * i;
-      if (s < S) {
-        float L[kSumRows];
-        const float* pr = logits + (bh * W + w0) * S + s;
+      for (int e = 0; e < 4; ++e) bload<4>(rs, key + e < S ? (uint32_t)(key + e) * 4u : kOob, &dst[e]);
+    }
+  };
 #pragma unroll
-        for (int w = 0; w < kSumRows; ++w) {
-          L[w] = (w < nw) ? *pr : -INFINITY;
-          pr += S;
-        }
+  for (int i = 0; i < kSumRing - 1; ++i) load(x[i], i);
+  for (int s0 = 0; s0 < nstep; s0 += kSumRing) {
 #pragma unroll
-        for (int w = 0; w < kSumRows; ++w)
-          if (w < nw) acc[w] += det_fix(det_exp_nonpos((double)L[w] - (double)sm_m[w0 + w]));
+    for (int j = 0; j < kSumRing; ++j) {
+      load(x[(j + kSumRing - 1) % kSumRing], s0 + j + kSumRing - 1);
+      const int key = (s0 + j) * 256 + lane * 4;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float L = key + e < S ? __uint_as_float(x[j][e]) : -INFINITY;
+        acc[e] += det_fix(det_exp_nonpos((double)L - (double)m));
       }
     }
-    // reduce-scatter over lanes: 16 -> 8 -> 4 -> 2 -> 1 rows per lane
-#pragma unroll
-    for (int n = kSumRows / 2, o = 32; n >= 1; n >>= 1, o >>= 1) {
-      const bool up = (lane & o) != 0;
-#pragma unroll
-      for (int i = 0; i < n; ++i) {
-        const uint64_t lo = acc[i], hi = acc[i + n];
-        const uint64_t send = up ? lo : hi;
-        const uint64_t keep = up ? hi : lo;
-        const uint32_t rl = __shfl_xor((uint32_t)send, o, 64);
-        const uint32_t rh = __shfl_xor((uint32_t)(send >> 32), o, 64);
-        acc[i] = keep + (((uint64_t)rh << 32) | rl);
-      }
-    }
-#pragma unroll
-    for (int o = 2; o >= 1; o >>= 1) {
-      const uint32_t rl = __shfl_xor((uint32_t)acc[0], o, 64);
-      const uint32_t rh = __shfl_xor((uint32_t)(acc[0] >> 32), o, 64);
-      acc[0] += ((uint64_t)rh << 32) | rl;
-    }
-    // step o kept the half of the rows selected by lane bit o, so lanes
-    // 4r .. 4r+3 now hold the wave sum of row r
-    if ((lane & 3) == 0) sm_red[wave][lane >> 2] = acc[0];
-    __syncthreads();
-    if (threadIdx.x < nw) {
-      const int w = threadIdx.x;
-      const uint64_t tot = sm_red[0][w] + sm_red[1][w] + sm_red[2][w] + sm_red[3][w];
-      if (tot) atomicAdd((unsigned long long*)&lsum[bh * W + w0 + w], (unsigned long long)tot);
-    }
-    __syncthreads();
   }
+  uint64_t t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    const uint32_t rl = __shfl_xor((uint32_t)t, o, 64);
+    const uint32_t rh = __shfl_xor((uint32_t)(t >> 32), o, 64);
+    t += ((uint64_t)rh << 32) | rl;
+  }
+  if (lane == 0) lsum[bh * W + w] = t;
 }
 
-// grid (ceil(S / (256 - 2P)), Hk, B), block 256: thread t computes the
-// importance of key c0 - P + t; threads P .. 255-P pool and write keys
-// c0 .. c0 + 255 - 2P.
+// Importance and pooling.  grid (ceil(S / (256 - 2P)), Hk, B), block 256:
+// thread t computes imp for key c0 - P + t as the fma chain over the window
+// rows in ascending order (rows streamed 8 at a time, the next 8 in flight),
+// then the inner 256 - 2P threads pool over their neighbours in LDS.
+constexpr int kImpRows = 8;
+
+template <int MODE>
 __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__ logits,
                                                        const uint32_t* __restrict__ rmax,
                                                        const uint64_t* __restrict__ lsum, int Hk, int S,
-                                                       int W, int mode, int P, int pooling, int ksize,
+                                                       int W, int P, int pooling, int ksize,
                                                        float* __restrict__ scores) {
   const int h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * Hk + h;
@@ -333,7 +360,7 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
   __shared__ float sm_m[kMaxW];
   __shared__ double sm_inv[kMaxW];
   __shared__ float sm_imp[256];
-  if (mode == HC_SCORE_SNAPKV) {
+  if constexpr (MODE == HC_SCORE_SNAPKV) {
     for (int w = threadIdx.x; w < W; w += blockDim.x) {
       sm_m[w] = key_to_float(rmax[bh * W + w]);
       const double l = (double)lsum[bh * W + w] * 0x1p-44;
@@ -342,31 +369,38 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
   }
   __syncthreads();
   const int s = c0 - P + (int)threadIdx.x;
-  float v = 0.f;
-  if (s >= 0 && s < S) {
-    double acc = 0.0;
-    for (int w0 = 0; w0 < W; w0 += kSumRows) {
-      const int nw = min(kSumRows, W - w0);
-      float L[kSumRows];
-      const float* pr = logits + (bh * W + w0) * S + s;
+  const bool sv = s >= 0 && s < S;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + bh * W * S, (uint32_t)((int64_t)W * S * 4));
+  const uint32_t base = sv ? (uint32_t)s * 4u : kOob;
+  const uint32_t rowb = (uint32_t)S * 4u;
+  auto load = [&](uint32_t (&dst)[kImpRows], int w0) {
 #pragma unroll
-      for (int w = 0; w < kSumRows; ++w) {
-        L[w] = (w < nw) ? *pr : 0.f;
-        pr += S;
-      }
-      if (mode == HC_SCORE_SNAPKV) {
+    for (int r = 0; r < kImpRows; ++r)
+      bload<4>(rs, (base == kOob || w0 + r >= W) ? kOob : base + (uint32_t)(w0 + r) * rowb, &dst[r]);
+  };
+  double acc = 0.0;
+  auto chain = [&](const uint32_t (&x)[kImpRows], int w0) {
 #pragma unroll
-        for (int w = 0; w < kSumRows; ++w)
-          if (w < nw) acc = __builtin_fma(det_exp_nonpos((double)L[w] - (double)sm_m[w0 + w]), sm_inv[w0 + w], acc);
-      } else {
-#pragma unroll
-        for (int w = 0; w < kSumRows; ++w)
-          if (w < nw) acc = acc + (double)L[w];
+    for (int r = 0; r < kImpRows; ++r) {
+      const int w = w0 + r;
+      if (w < W) {
+        const float L = __uint_as_float(x[r]);
+        if constexpr (MODE == HC_SCORE_SNAPKV)
+          acc = __builtin_fma(det_exp_nonpos((double)L - (double)sm_m[w]), sm_inv[w], acc);
+        else
+          acc = acc + (double)L;
       }
     }
-    v = (float)acc;
+  };
+  uint32_t xa[kImpRows], xb[kImpRows];
+  load(xa, 0);
+  for (int w0 = 0; w0 < W; w0 += 2 * kImpRows) {
+    load(xb, w0 + kImpRows);
+    chain(xa, w0);
+    load(xa, w0 + 2 * kImpRows);
+    chain(xb, w0 + kImpRows);
   }
-  sm_imp[threadIdx.x] = v;
+  sm_imp[threadIdx.x] = sv ? (float)acc : 0.f;
   __syncthreads();
   const int t = threadIdx.x;
   if (t < P || t >= 256 - P || s >= S) return;
@@ -414,17 +448,39 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
                      dim3((unsigned)(D < 64 ? 64 : D)), 0, st, (const T*)q, q_sb, q_sh, q_ss, q_row0, (int)Hq,
                      (int)Hk, (int)W, (int)lay.wpad, (int)D, qf, rmax, lsum);
   const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
-  if (lds > 65536)
-    (void)hipFuncSetAttribute((const void*)logits_kernel<T>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-  hipLaunchKernelGGL(logits_kernel<T>, dim3((unsigned)lay.nchunk_m, (unsigned)(Hk * nrb), (unsigned)B), dim3(256),
-                     lds, st, (const T*)k, k_sb, k_sh, k_ss, (const double*)qf, (int)Hk, (int)S, (int)D, (int)W,
-                     (int)lay.wpad, mode, scal, logits, rmax);
+  const uint32_t k_bytes = (uint32_t)(((S - 1) * k_ss + D) * (int64_t)sizeof(T));
+  const dim3 grid((unsigned)cdiv(S, (int64_t)kChunkM * kLogitChunks), (unsigned)(Hk * nrb), (unsigned)B);
+  if (mode == HC_SCORE_SNAPKV) {
+    if (lds > 48 * 1024)
+      (void)hipFuncSetAttribute((const void*)logits_kernel<T, HC_SCORE_SNAPKV>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((logits_kernel<T, HC_SCORE_SNAPKV>), grid, dim3(256), lds, st, (const T*)k, k_sb, k_sh, k_ss,
+                       k_bytes, (const double*)qf, (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, logits, rmax);
+  } else {
+    if (lds > 48 * 1024)
+      (void)hipFuncSetAttribute((const void*)logits_kernel<T, HC_SCORE_RAWSUM>,
+                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL((logits_kernel<T, HC_SCORE_RAWSUM>), grid, dim3(256), lds, st, (const T*)k, k_sb, k_sh, k_ss,
+                       k_bytes, (const double*)qf, (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, logits, rmax);
+  }
+  if (mode == HC_SCORE_SNAPKV) {
+    const dim3 g((unsigned)cdiv(W, 4), (unsigned)Hk, (unsigned)B);
+    if (S % 4 == 0)
+      hipLaunchKernelGGL(rowsum_kernel<true>, g, dim3(256), 0, st, (const float*)logits, (const uint32_t*)rmax,
+                         (int)Hk, (int)S, (int)W, lsum);
+    else
+      hipLaunchKernelGGL(rowsum_kernel<false>, g, dim3(256), 0, st, (const float*)logits, (const uint32_t*)rmax,
+                         (int)Hk, (int)S, (int)W, lsum);
+  }
+  const dim3 gi((unsigned)cdiv(S, 256 - 2 * P), (unsigned)Hk, (unsigned)B);
   if (mode == HC_SCORE_SNAPKV)
-    hipLaunchKernelGGL(rowsum_kernel, dim3((unsigned)cdiv(S, kSumChunk), (unsigned)Hk, (unsigned)B), dim3(256), 0,
-                       st, (const float*)logits, (const uint32_t*)rmax, (int)Hk, (int)S, (int)W, lsum);
-  hipLaunchKernelGGL(imp_pool_kernel, dim3((unsigned)cdiv(S, 256 - 2 * P), (unsigned)Hk, (unsigned)B), dim3(256), 0,
-                     st, (const float*)logits, (const uint32_t*)rmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W,
-                     mode, P, pooling, ksize, scores);
+    hipLaunchKernelGGL(imp_pool_kernel<HC_SCORE_SNAPKV>, gi, dim3(256), 0, st, (const float*)logits,
+                       (const uint32_t*)rmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W, P, pooling, ksize,
+                       scores);
+  else
+    hipLaunchKernelGGL(imp_pool_kernel<HC_SCORE_RAWSUM>, gi, dim3(256), 0, st, (const float*)logits,
+                       (const uint32_t*)rmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W, P, pooling, ksize,
+                       scores);
 }
 
 }  // namespace hc
@@ -447,12 +503,14 @@ extern "C" int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64
   HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && S > 0 && D > 0 && W > 0, "score: empty shape");
   HC_REQUIRE(W <= S, "score: window %lld exceeds S %lld", (long long)W, (long long)S);
   HC_REQUIRE(W <= kMaxW, "score: window %lld above the supported %d rows", (long long)W, kMaxW);
-  HC_REQUIRE(D % 8 == 0 && D <= 512, "score: head_dim %lld must be a multiple of 8 and <= 512", (long long)D);
+  HC_REQUIRE(D % 16 == 0 && D <= 512, "score: head_dim %lld must be a multiple of 16 and <= 512", (long long)D);
   HC_REQUIRE(S <= ((int64_t)1 << 19), "score: S %lld above 2^19 (fixed-point normaliser range)", (long long)S);
   HC_REQUIRE(B <= 65535 && Hk * cdiv(W, kRowBlk) <= 65535, "score: grid too large");
   HC_REQUIRE(q_row0 >= 0, "score: negative q_row0");
   HC_REQUIRE(q && k && scores, "score: null pointer");
   const int es = dtype_size(dtype);
+  HC_REQUIRE(k_ss >= D && ((S - 1) * k_ss + D) * es < ((int64_t)1 << 31),
+             "score: one (batch, kv head) key extent must be below 2 GiB with row stride >= D");
   HC_REQUIRE((uintptr_t)k % 16 == 0 && (k_sb * es) % 16 == 0 && (k_sh * es) % 16 == 0 && (k_ss * es) % 16 == 0,
              "score: keys must be 16-byte aligned rows");
   int P = 0;
