@@ -383,7 +383,6 @@ struct DecodeState<bf16_t, D, GM> {
 template <typename T, int D, int GM, int NW, int NBUF, int MINW, bool EVICT>
 __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a) {
   constexpr int DPL = D / 16;
-  constexpr int STEP = 16 * NW;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int col = lane & 15;
@@ -440,13 +439,18 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       for (int j = 0; j < DPL; ++j) st.acc[g][j] = 0.f;
   }
 
-  const int first = key_begin + wave * 16;
-  const int nt = first < key_end ? (key_end - first + STEP - 1) / STEP : 0;
+  // Wave w streams the contiguous keys [wbeg, wend): equal counts per wave,
+  // so no wave of the workgroup waits on a longer one at the final barrier.
+  const int kpw = (key_end - key_begin + NW - 1) / NW;
+  const int wbeg = key_begin + wave * kpw;
+  const int wend = min(key_end, wbeg + kpw);
+  const int first = wbeg;
+  const int nt = wbeg < wend ? (wend - wbeg + 15) / 16 : 0;
   if (nt > 0) {
     TileRegs<T, D> r[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i)
-      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * STEP, key_begin, key_end, col, grp, bits);
+      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * 16, key_begin, wend, col, grp, bits);
 
     QFrag<T, D> qf;
     const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
@@ -457,13 +461,13 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
 #pragma unroll
       for (int j = 0; j < NBUF; ++j) {
         const int t = g0 + j;
-        load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * STEP,
-                        key_begin, key_end, col, grp, bits);
+        load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * 16,
+                        key_begin, wend, col, grp, bits);
         if (t < nt) {
           if constexpr (MX)
-            process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * STEP, key_end, col, grp, srow);
+            process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow);
           else
-            process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * STEP, key_end, col, grp, srow);
+            process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow);
         }
       }
     }
@@ -473,9 +477,12 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
   float l_run = st.l_run;
   l_run += __shfl_xor(l_run, 16, 64);
   l_run += __shfl_xor(l_run, 32, 64);
+  // Partials in LDS, one padding float per 32 (bank-conflict-free writes of
+  // the MFMA layout, where the four row groups sit 32 floats apart).
+  constexpr int RS = D + D / 32 + 1;
   __shared__ float sm_m[NW][GM];
   __shared__ float sm_l[NW][GM];
-  __shared__ float sm_acc[NW][GM][D];
+  __shared__ float sm_acc[NW][GM][RS];
   if (grp == 0 && col < GM) {
     sm_m[wave][col] = st.m_run;
     sm_l[wave][col] = l_run;
@@ -486,7 +493,10 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
 #pragma unroll
       for (int j = 0; j < DPL; ++j)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) sm_acc[wave][col][(4 * grp + i) * DPL + j] = st.acc[j][i];
+        for (int i = 0; i < 4; ++i) {
+          const int d = (4 * grp + i) * DPL + j;
+          sm_acc[wave][col][d + (d >> 5)] = st.acc[j][i];
+        }
     }
   } else {
 #pragma unroll
@@ -502,7 +512,10 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
 #pragma unroll
       for (int g = 0; g < GM; ++g)
 #pragma unroll
-        for (int j = 0; j < DPL; ++j) sm_acc[wave][g][col * DPL + j] = st.acc[g][j];
+        for (int j = 0; j < DPL; ++j) {
+          const int d = col * DPL + j;
+          sm_acc[wave][g][d + (d >> 5)] = st.acc[g][j];
+        }
     }
   }
   __syncthreads();
@@ -520,7 +533,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
         const float sc = exp2f(sm_m[w][g] - M);
-        A = fmaf(sm_acc[w][g][d], sc, A);
+        A = fmaf(sm_acc[w][g][d + (d >> 5)], sc, A);
         L = fmaf(sm_l[w][g], sc, L);
       }
     }
