@@ -12,8 +12,8 @@ One step = one such job.  The 32 layers are independent in this synthetic
 workload, so each kernel covers all of them in one launch (layer l is batch
 row l): compaction is one launch set (scores, kept indices, gather into the
 hot buffer), recorded once as a HIP graph and replayed, and each decode step
-is an append launch plus one decode launch over the 32 layers' hot buffers
-(72 MB).
+is one fused launch over the 32 layers' hot buffers (72 MB) that writes the
+new token's K/V row and attends over the buffer plus that token.
 
 Before each decode launch a read sweep over 512 MiB evicts the 256 MB Infinity
 Cache (in a model, the weights streamed between two visits of a layer do
@@ -21,8 +21,8 @@ that), so decode reads its K/V from HBM; the sweep is outside the decode
 events.  It only reads, so no dirty lines are left for decode to write back.
 
 Reported:
-  value              decode us per layer-step: mean decode-launch time of the
-                     timed steps (HIP events on the launch stream) / 32
+  value              decode us per layer-step: mean append+decode launch time
+                     of the timed steps (HIP events on the launch stream) / 32
   compact_ms_32_layers  compaction of all 32 layers per step, ms
   roofline           decode launch: algorithmic bytes / mean launch time
   roofline_compaction, scoring MFMA rate, a per-layer-launch variant (one
@@ -73,10 +73,12 @@ def elem_size(dtype):
 
 
 def decode_bytes(w, rows, n_keys):
-    """Algorithmic HBM bytes of one decode launch over `rows` (layer, batch)
-    rows: each hot K and V row read once, q read, output written."""
+    """Algorithmic HBM bytes of one append+decode launch over `rows` (layer,
+    batch) rows attending n_keys keys: the n_keys - 1 cached K and V rows
+    read once, the new token's K and V read and written into the hot
+    buffer, q read, output written."""
     es = elem_size(w.dtype)
-    return rows * (2 * w.hk * n_keys * w.head_dim + 2 * w.hq * w.head_dim) * es
+    return rows * (2 * w.hk * (n_keys + 1) * w.head_dim + 2 * w.hq * w.head_dim) * es
 
 
 def compaction_bytes(w, rows):
@@ -140,24 +142,22 @@ class Setup:
         ops.gather_rows(keep, [(self.k_post, self.k_hot), (self.v, self.v_hot)])
         return keep
 
-    def append(self, t):
-        from hotcold_kv import ops
-        ops.append_rows(self.w.budget + t, self.k_new[t], self.k_hot, self.v_new[t], self.v_hot)
-
     def decode(self, t, num_splits=0):
+        """Decode step t: append token t into row budget+t of every layer's
+        hot buffer and attend over rows 0..budget+t, one fused launch."""
         from hotcold_kv import ops
         n = self.w.budget + t + 1
-        ops.decode_attention(self.q_new[t], self.k_hot[:, :, :n], self.v_hot[:, :, :n], self.w.scaling,
-                             out=self.out, num_splits=num_splits)
+        ops.decode_attention_append(self.q_new[t], self.k_hot[:, :, :n], self.v_hot[:, :, :n], self.k_new[t],
+                                    self.v_new[t], self.w.scaling, out=self.out, num_splits=num_splits)
 
     def decode_per_layer(self, t):
-        """One decode launch per layer, as a model's layer loop issues them."""
+        """One append+decode launch per layer, as a model's layer loop issues them."""
         from hotcold_kv import ops
         B, n = self.w.batch, self.w.budget + t + 1
         for l in range(self.w.layers):
             sl = slice(l * B, (l + 1) * B)
-            ops.decode_attention(self.q_new[t][sl], self.k_hot[sl, :, :n], self.v_hot[sl, :, :n], self.w.scaling,
-                                 out=self.out[sl])
+            ops.decode_attention_append(self.q_new[t][sl], self.k_hot[sl, :, :n], self.v_hot[sl, :, :n],
+                                        self.k_new[t][sl], self.v_new[t][sl], self.w.scaling, out=self.out[sl])
 
     # -- graphs --------------------------------------------------------------------------
     def capture(self):
@@ -170,7 +170,6 @@ class Setup:
         with torch.cuda.stream(s):
             self.compaction()
             for t in range(w.decode_steps):
-                self.append(t)
                 self.decode(t)
             self.decode_per_layer(w.decode_steps - 1)
         s.synchronize()
@@ -190,8 +189,8 @@ class Setup:
 
 def run_steps(s, steps, flush):
     """Run `steps` whole jobs; return (wall ms/step, compaction ms per step,
-    decode-launch ms list).  Compaction replays its graph; append and decode
-    are launched directly: the cache sweep before each decode keeps the GPU
+    decode-launch ms list).  Compaction replays its graph; the append+decode
+    launches are issued directly: the cache sweep before each keeps the GPU
     busy long enough for the host to stay ahead, so the decode events see no
     host gap (a one-kernel graph replay adds several microseconds of its own
     on this stack)."""
@@ -210,7 +209,6 @@ def run_steps(s, steps, flush):
             c1.record(st)
             comp_ev.append((c0, c1))
             for t in range(w.decode_steps):
-                s.append(t)
                 if flush is not None:
                     flush()
                 e0 = torch.cuda.Event(enable_timing=True)
@@ -413,7 +411,8 @@ def main():
         "config": {"workload": w.name, "layers": w.layers, "batch": w.batch, "seq_len": w.seq_len,
                    "budget": w.budget, "window": w.window, "pool": w.pool, "decode_steps": w.decode_steps,
                    "q_heads": w.hq, "kv_heads": w.hk, "head_dim": w.head_dim,
-                   "schedule": "32 layers per launch, HIP graphs, Infinity Cache flushed before decode"},
+                   "schedule": "32 layers per launch, fused append+decode, compaction as a HIP graph, "
+                               "Infinity Cache flushed before decode"},
         "compact_ms_32_layers": round(comp_ms, 4),
         "decode_us_per_layer_step": round(dec_us_layer, 4),
         "decode_us_per_layer_launch_cold": round(pl_cold_ms * 1e3 / w.layers, 3),
@@ -421,7 +420,7 @@ def main():
         "decode_launch_us_warm_last_step": round(warm_dec_ms * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(w.name),
-                     "kernel": "decode_attn_kernel (+ decode_combine_kernel)",
+                     "kernel": "decode_attn_kernel (fused append, + decode_combine_kernel)",
                      "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3)},
         "roofline_compaction": {"bound": "hbm", "achieved": round(c_achieved, 1), "peak": HBM_PEAK_GBS,
                                 "unit": "GB/s", "frac": round(c_achieved / HBM_PEAK_GBS, 4),

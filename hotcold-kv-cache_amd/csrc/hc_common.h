@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <math.h>
+#include <utility>
 
 #include "hotcold_hip.h"
 
@@ -168,6 +169,17 @@ __device__ __forceinline__ uint32_t order_key(float x) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// f(std::integral_constant<int, i>) for i = 0 .. N-1, unrolled at compile time
+// (register arrays indexed by i stay in registers).
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
 // ---------------------------------------------------------------------------
 // Raw buffer loads.  A load whose offset is past the resource's extent returns
 // zeros without a memory access, so kernels can issue every load
@@ -192,6 +204,20 @@ __device__ __forceinline__ void bload(__amdgpu_buffer_rsrc_t r, uint32_t off, ui
     w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0);
   } else {
     w[0] = (uint32_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0);
+  }
+}
+
+// Raw buffer stores: a store whose offset is past the extent is dropped.
+template <int BYTES>
+__device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, uint32_t off, const uint32_t* w) {
+  if constexpr (BYTES == 16) {
+    __builtin_amdgcn_raw_buffer_store_b128(u32x4{w[0], w[1], w[2], w[3]}, r, (int)off, 0, 0);
+  } else if constexpr (BYTES == 8) {
+    __builtin_amdgcn_raw_buffer_store_b64(u32x2{w[0], w[1]}, r, (int)off, 0, 0);
+  } else if constexpr (BYTES == 4) {
+    __builtin_amdgcn_raw_buffer_store_b32(w[0], r, (int)off, 0, 0);
+  } else {
+    __builtin_amdgcn_raw_buffer_store_b16((unsigned short)w[0], r, (int)off, 0, 0);
   }
 }
 

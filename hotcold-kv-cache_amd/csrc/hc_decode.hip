@@ -50,7 +50,24 @@ struct DecodeArgs {
   float* ml;           // optional [B][Hq][2] final (max, sum)
   uint32_t k_bytes, v_bytes, q_bytes;  // buffer extents of one (b, kv head)
   int B, Hq, Hk, G, S, splits, keys_per_split;
+  int S_cache;  // rows read from k/v: S, or S-1 with a fused append
   float scale_log2;
+  // Fused append (hc_decode_attn_append): the token at row S-1 comes from
+  // k_new / v_new ([B][Hk][D]); the last split's workgroup attends it and
+  // writes it (and optionally its pre-RoPE key and position) into row S-1.
+  // Last in the struct: only the append kernels read these.
+  const void* k_new;
+  int64_t kn_sb, kn_sh;
+  const void* v_new;
+  int64_t vn_sb, vn_sh;
+  const void* p_new;
+  int64_t pn_sb, pn_sh;
+  void* p_dst;
+  int64_t pd_sb, pd_sh, pd_ss;
+  const int64_t* pos_new;
+  int64_t posn_sb;
+  int64_t* pos_dst;
+  int64_t posd_sb;
 };
 
 // Keys of one split when the keep bitmap is needed (mask or held slot).
@@ -112,6 +129,58 @@ __device__ __forceinline__ void load_tile(TileRegs<T, D>& r, __amdgpu_buffer_rsr
 
 // Q.K^T of one tile.  Output lane layout of every 16x16 fp32 MFMA block:
 // lane l holds C[4*(l/16)+i][l%16], i = 0..3  (row = key, column = head).
+// The appended token as a one-key tile: key row 0 of the K (MFMA A operand)
+// and V (P.V) layouts, read from k_new / v_new; every other row is zero and
+// not attended.  Resources of extent 0 (waves that do not own the token)
+// make every load return zeros without a memory access.
+template <typename T, int D>
+__device__ __forceinline__ void load_token(TileRegs<T, D>& r, __amdgpu_buffer_rsrc_t knrs,
+                                           __amdgpu_buffer_rsrc_t vnrs, int col, int grp, bool tok) {
+  using R = TileRegs<T, D>;
+#pragma unroll
+  for (int t = 0; t < R::KW; ++t) {
+    const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
+    const uint32_t off = (col == 0 && d0 < D) ? (uint32_t)(d0 * sizeof(T)) : kOob;
+    uint32_t w[4];
+    bload<16>(knrs, off, w);
+    r.k[t] = u32x4{w[0], w[1], w[2], w[3]};
+  }
+  const uint32_t off = (grp == 0) ? (uint32_t)(col * R::DPL * sizeof(T)) : kOob;
+  bload<(R::VB >= 16 ? 16 : R::VB)>(vnrs, off, r.v[0]);
+  if constexpr (R::VB > 16) {
+#pragma unroll
+    for (int c = 1; c < R::VB / 16; ++c) bload<16>(vnrs, off == kOob ? kOob : off + 16 * c, &r.v[0][4 * c]);
+  }
+#pragma unroll
+  for (int i = 1; i < 4; ++i)
+#pragma unroll
+    for (int w = 0; w < R::VWORDS; ++w) r.v[i][w] = 0u;
+  r.keep = (tok && grp == 0) ? 1u : 0u;
+}
+
+// Write the token tile's K and V rows at byte offsets k_row / v_row of the
+// hot buffer (dropped unless tok).
+template <typename T, int D>
+__device__ __forceinline__ void store_token(const TileRegs<T, D>& r, __amdgpu_buffer_rsrc_t krs,
+                                            __amdgpu_buffer_rsrc_t vrs, uint32_t k_row, uint32_t v_row, int col,
+                                            int grp, bool tok) {
+  using R = TileRegs<T, D>;
+#pragma unroll
+  for (int t = 0; t < R::KW; ++t) {
+    const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
+    const uint32_t off = (tok && col == 0 && d0 < D) ? k_row + (uint32_t)(d0 * sizeof(T)) : kOob;
+    const u32x4 x = r.k[t];
+    const uint32_t w[4] = {x[0], x[1], x[2], x[3]};
+    bstore<16>(krs, off, w);
+  }
+  const uint32_t off = (tok && grp == 0) ? v_row + (uint32_t)(col * R::DPL * sizeof(T)) : kOob;
+  bstore<(R::VB >= 16 ? 16 : R::VB)>(vrs, off, r.v[0]);
+  if constexpr (R::VB > 16) {
+#pragma unroll
+    for (int c = 1; c < R::VB / 16; ++c) bstore<16>(vrs, off == kOob ? kOob : off + 16 * c, &r.v[0][4 * c]);
+  }
+}
+
 template <typename T, int D>
 struct QFrag;
 
@@ -376,12 +445,14 @@ struct DecodeState<bf16_t, D, GM> {
   typedef MxState<D> type;
 };
 
-// grid (splits, Hk, B), block 64*NW (NW waves).  Wave w takes the tiles
-// key_begin + 16*(w + NW*i), i = 0 .. nt-1, through a ring of NBUF register
-// tiles: step i issues the loads of tile i + NBUF - 1 (past the range: no
-// memory traffic) and then processes tile i, so NBUF-1 tiles stay in flight.
-template <typename T, int D, int GM, int NW, int NBUF, int MINW, bool EVICT>
+// grid (splits, Hk, B), block 64*NW (NW waves).  Wave w streams a
+// contiguous key range through a ring of NBUF register tiles.
+enum DecodeMode { kPlain = 0, kEvict = 1, kAppend = 2 };
+
+template <typename T, int D, int GM, int NW, int NBUF, int MINW, int MODE>
 __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a) {
+  constexpr bool EVICT = MODE == kEvict;
+  constexpr bool APPEND = MODE == kAppend;
   constexpr int DPL = D / 16;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -392,7 +463,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
   const int b = blockIdx.z;
   const int G = a.G;
   const int key_begin = split * a.keys_per_split;
-  const int key_end = min(a.S, key_begin + a.keys_per_split);
+  const int key_end = min(a.S_cache, key_begin + a.keys_per_split);
 
   const T* kbase = reinterpret_cast<const T*>(a.k) + b * a.k_sb + hk * a.k_sh;
   const T* vbase = reinterpret_cast<const T*>(a.v) + b * a.v_sb + hk * a.v_sh;
@@ -446,7 +517,37 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
   const int wend = min(key_end, wbeg + kpw);
   const int first = wbeg;
   const int nt = wbeg < wend ? (wend - wbeg + 15) / 16 : 0;
-  if (nt > 0) {
+  if (APPEND || nt > 0) {
+    // Fused append: the last wave of the last split attends the new token as
+    // a one-key tile and copies the token's K/V (and pre-RoPE key and
+    // position) into row S-1.  Its loads are issued first and it is processed
+    // after the wave's first NBUF tiles, by when they have landed, so it adds
+    // no wait; the copies are stored after the last tile.  Every wave runs this code with resources of extent 0 where it
+    // does not own the token: no branch around memory operations, so the
+    // compiler's load counting stays exact.
+    TileRegs<T, D> rn;
+    uint32_t pw[TileRegs<T, D>::KW][4];
+    uint32_t pos_w[2];
+    bool tok = false;
+    if constexpr (APPEND) {
+      tok = split == a.splits - 1 && __builtin_amdgcn_readfirstlane(wave) == NW - 1;
+      constexpr uint32_t rowb = D * sizeof(T);
+      const T* kn = tok ? reinterpret_cast<const T*>(a.k_new) + b * a.kn_sb + hk * a.kn_sh : kbase;
+      const T* vn = tok ? reinterpret_cast<const T*>(a.v_new) + b * a.vn_sb + hk * a.vn_sh : vbase;
+      load_token<T, D>(rn, make_rsrc(kn, tok ? rowb : 0u), make_rsrc(vn, tok ? rowb : 0u), col, grp, tok);
+      const bool tp = tok && a.p_new != nullptr;
+      const T* pn = tp ? reinterpret_cast<const T*>(a.p_new) + b * a.pn_sb + hk * a.pn_sh : kbase;
+      const __amdgpu_buffer_rsrc_t pnrs = make_rsrc(pn, tp ? rowb : 0u);
+#pragma unroll
+      for (int t = 0; t < TileRegs<T, D>::KW; ++t) {
+        const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
+        bload<16>(pnrs, (col == 0 && d0 < D) ? (uint32_t)(d0 * sizeof(T)) : kOob, pw[t]);
+      }
+      const bool tq = tok && a.pos_new != nullptr && hk == 0;
+      const int64_t* psrc = tq ? a.pos_new + b * a.posn_sb : reinterpret_cast<const int64_t*>(kbase);
+      bload<8>(make_rsrc(psrc, tq ? 8u : 0u), lane == 0 ? 0u : kOob, pos_w);
+    }
+
     TileRegs<T, D> r[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i)
@@ -457,19 +558,50 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
     float* srow = EVICT ? a.scores + ((int64_t)b * a.Hq + hk * G + min(col, G - 1)) * a.S : nullptr;
 
-    for (int g0 = 0; g0 < nt; g0 += NBUF) {
+    // Step t issues the loads of tile t + NBUF - 1 (past the range: no memory
+    // traffic) and then processes tile t, so NBUF-1 tiles stay in flight.
+#define HC_RING_GROUP(g0)                                                                                  \
+  _Pragma("unroll") for (int j = 0; j < NBUF; ++j) {                                                       \
+    const int t = (g0) + j;                                                                                \
+    load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * 16,       \
+                    key_begin, wend, col, grp, bits);                                                      \
+    if (t < nt) {                                                                                          \
+      if constexpr (MX)                                                                                    \
+        process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow); \
+      else                                                                                                 \
+        process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow); \
+    }                                                                                                      \
+  }
+    int g_start = 0;
+    if constexpr (APPEND) {
+      HC_RING_GROUP(0)
+      g_start = NBUF;
+      if constexpr (MX)
+        process_tile_mx<T, D, false>(rn, qf, st, G, a.scale_log2, 0, 0, col, grp, nullptr);
+      else
+        process_tile<T, D, GM, false>(rn, qf, st, G, a.scale_log2, 0, 0, col, grp, nullptr);
+    }
+    for (int g0 = g_start; g0 < nt; g0 += NBUF) {
+      HC_RING_GROUP(g0)
+    }
+#undef HC_RING_GROUP
+    if constexpr (APPEND) {
+      // The token's rows.  Stored after the last tile: issued before the
+      // loop instead, they measured slower.
+      const uint32_t row = (uint32_t)(a.S - 1);
+      store_token<T, D>(rn, krs, vrs, row * k_rowb, row * v_rowb, col, grp, tok);
+      const bool tp = tok && a.p_new != nullptr;
+      T* pd = tp ? reinterpret_cast<T*>(a.p_dst) + b * a.pd_sb + hk * a.pd_sh + (int64_t)row * a.pd_ss
+                 : const_cast<T*>(kbase);
+      const __amdgpu_buffer_rsrc_t pdrs = make_rsrc(pd, tp ? (uint32_t)(D * sizeof(T)) : 0u);
 #pragma unroll
-      for (int j = 0; j < NBUF; ++j) {
-        const int t = g0 + j;
-        load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * 16,
-                        key_begin, wend, col, grp, bits);
-        if (t < nt) {
-          if constexpr (MX)
-            process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow);
-          else
-            process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow);
-        }
+      for (int t = 0; t < TileRegs<T, D>::KW; ++t) {
+        const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
+        bstore<16>(pdrs, (col == 0 && d0 < D) ? (uint32_t)(d0 * sizeof(T)) : kOob, pw[t]);
       }
+      const bool tq = tok && a.pos_new != nullptr && hk == 0;
+      int64_t* pdst = tq ? a.pos_dst + b * a.posd_sb + row : reinterpret_cast<int64_t*>(const_cast<T*>(kbase));
+      bstore<8>(make_rsrc(pdst, tq ? 8u : 0u), lane == 0 ? 0u : kOob, pos_w);
     }
   }
 
@@ -523,6 +655,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
   const int unit = b * a.Hk + hk;
   const int stride_part = G * D + 2 * G;
   T* obase = reinterpret_cast<T*>(a.out) + b * a.o_sb + (int64_t)(hk * G) * a.o_sh;
+
   for (int e = threadIdx.x; e < G * D; e += 64 * NW) {
     const int g = e / D, d = e - g * D;
     float M = -INFINITY;
@@ -729,9 +862,11 @@ template <typename T, int D, int GM, int NW, int NBUF, int MINW>
 static void launch_decode(const DecodeArgs& a, hipStream_t st) {
   dim3 grid(a.splits, a.Hk, a.B);
   if (a.scores)
-    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, true>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, kEvict>), grid, dim3(64 * NW), 0, st, a);
+  else if (a.k_new)
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, kAppend>), grid, dim3(64 * NW), 0, st, a);
   else
-    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, false>), grid, dim3(64 * NW), 0, st, a);
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, kPlain>), grid, dim3(64 * NW), 0, st, a);
   if (a.splits > 1)
     hipLaunchKernelGGL(decode_combine_kernel<T>, dim3(a.Hk, a.B), dim3(256), 0, st, a, D);
 }
@@ -784,15 +919,16 @@ extern "C" int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t 
   int64_t need = 0;
   for (int es : {2, 4})
     for (int nw : {4, 8})
-      for (bool bitmap : {false, true}) {
-        const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap, D * es);
+      for (bool bitmap : {false, true})
+        for (int64_t Sc : {S, S > 1 ? S - 1 : S}) {
+        const int splits = pick_splits(B * Hk, Sc, num_splits, nw, bitmap, D * es);
         const int64_t t = decode_layout(B, Hq, Hk, D, S, splits, with_evict).total;
         if (t > need) need = t;
-      }
+        }
   return need;
 }
 
-extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
                               const void* q, int64_t q_sb, int64_t q_sh,
                               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
                               const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
@@ -805,7 +941,7 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
                               void* out, int64_t o_sb, int64_t o_sh,
                               float* evict_loss, int64_t* evict_idx,
                               void* workspace, int64_t workspace_bytes, int64_t num_splits,
-                              void* stream) {
+                              void* stream, const DecodeArgs* ap) {
   if (dropout != 0.0) return set_error(HC_ERR_DROPOUT, "dropout must be 0.0 , because we are not in training");
   HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16, "decode: bad dtype %d", dtype);
   HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && D > 0 && S > 0, "decode: empty shape B=%lld Hq=%lld Hk=%lld D=%lld S=%lld",
@@ -827,13 +963,25 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
   const int G = (int)(Hq / Hk);
   const int nw = decode_cfg(es, (int)D, group_bucket(G)).nw;
   const bool bitmap = mask != nullptr || held_len > 0;
-  const int splits = pick_splits(B * Hk, S, num_splits, nw, bitmap, D * es);
+  const int64_t S_cache = ap ? S - 1 : S;  // a fused append's token is not read from k/v
+  HC_REQUIRE(held_len <= S_cache, "decode: held_len %lld beyond the cached rows", (long long)held_len);
+  const int splits = pick_splits(B * Hk, S_cache > 0 ? S_cache : 1, num_splits, nw, bitmap, D * es);
   // Buffer extents of one (b, kv head) must fit the 31-bit load offsets.
   const int64_t k_bytes = ((S - 1) * k_ss + D) * es, v_bytes = ((S - 1) * v_ss + D) * es;
   const int64_t q_bytes = ((Hq / Hk - 1) * q_sh + D) * es;
   HC_REQUIRE(k_ss >= D && v_ss >= D && k_bytes < ((int64_t)1 << 31) && v_bytes < ((int64_t)1 << 31) &&
                  q_bytes < ((int64_t)1 << 31),
              "decode: one (batch, kv head) K/V/Q extent must be below 2 GiB with row stride >= D");
+  if (ap) {
+    const auto al16 = [](const void* p) { return ((uintptr_t)p % 16) == 0; };
+    HC_REQUIRE(al16(ap->k_new) && al16(ap->v_new) && (ap->kn_sb * es) % 16 == 0 && (ap->kn_sh * es) % 16 == 0 &&
+                   (ap->vn_sb * es) % 16 == 0 && (ap->vn_sh * es) % 16 == 0,
+               "decode_append: k_new / v_new rows must be 16-byte aligned");
+    HC_REQUIRE(!ap->p_new || (al16(ap->p_new) && al16(ap->p_dst) && (ap->pn_sb * es) % 16 == 0 &&
+                              (ap->pn_sh * es) % 16 == 0 && (ap->pd_sb * es) % 16 == 0 &&
+                              (ap->pd_sh * es) % 16 == 0 && (ap->pd_ss * es) % 16 == 0 && ap->pd_ss >= D),
+               "decode_append: p_new / p_dst rows must be 16-byte aligned with row stride >= D");
+  }
   const int with_evict = (evict_loss != nullptr || evict_idx != nullptr);
   const DecodeLayout lay = decode_layout(B, Hq, Hk, D, S, splits, with_evict);
   if (!workspace || workspace_bytes < lay.total)
@@ -857,7 +1005,20 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
   a.ml = with_evict ? reinterpret_cast<float*>(ws + lay.ml_off) : nullptr;
   a.B = (int)B; a.Hq = (int)Hq; a.Hk = (int)Hk; a.G = G; a.S = (int)S;
   a.splits = splits;
-  a.keys_per_split = (int)keys_per_split(S, splits, nw);
+  a.keys_per_split = (int)keys_per_split(S_cache > 0 ? S_cache : 1, splits, nw);
+  a.S_cache = (int)S_cache;
+  if (ap) {
+    a.k_new = ap->k_new; a.kn_sb = ap->kn_sb; a.kn_sh = ap->kn_sh;
+    a.v_new = ap->v_new; a.vn_sb = ap->vn_sb; a.vn_sh = ap->vn_sh;
+    a.p_new = ap->p_new; a.pn_sb = ap->pn_sb; a.pn_sh = ap->pn_sh;
+    a.p_dst = ap->p_dst; a.pd_sb = ap->pd_sb; a.pd_sh = ap->pd_sh; a.pd_ss = ap->pd_ss;
+    a.pos_new = ap->pos_new; a.posn_sb = ap->posn_sb; a.pos_dst = ap->pos_dst; a.posd_sb = ap->posd_sb;
+  } else {
+    a.k_new = a.v_new = a.p_new = nullptr;
+    a.p_dst = nullptr;
+    a.pos_new = nullptr;
+    a.pos_dst = nullptr;
+  }
   a.scale_log2 = (float)(scaling * 1.4426950408889634);
   a.k_bytes = (uint32_t)k_bytes;
   a.v_bytes = (uint32_t)v_bytes;
@@ -884,4 +1045,55 @@ extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int6
     if ((rc = check_launch("evict_score")) != HC_OK) return rc;
   }
   return HC_OK;
+}
+
+extern "C" int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                              const void* q, int64_t q_sb, int64_t q_sh,
+                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                              const uint8_t* mask, int64_t mask_sb,
+                              int64_t held_len,
+                              const int64_t* held_pos, int64_t hp_sb, int64_t hp_sh,
+                              const uint8_t* held_valid, int64_t hv_sb, int64_t hv_sh,
+                              const int64_t* cur_pos,
+                              double scaling, double dropout,
+                              void* out, int64_t o_sb, int64_t o_sh,
+                              float* evict_loss, int64_t* evict_idx,
+                              void* workspace, int64_t workspace_bytes, int64_t num_splits,
+                              void* stream) {
+  return decode_impl(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss, mask, mask_sb,
+                     held_len, held_pos, hp_sb, hp_sh, held_valid, hv_sb, hv_sh, cur_pos, scaling, dropout, out, o_sb,
+                     o_sh, evict_loss, evict_idx, workspace, workspace_bytes, num_splits, stream, nullptr);
+}
+
+extern "C" int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                                     const void* q, int64_t q_sb, int64_t q_sh,
+                                     void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                                     void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                     const void* k_new, int64_t kn_sb, int64_t kn_sh,
+                                     const void* v_new, int64_t vn_sb, int64_t vn_sh,
+                                     const void* p_new, int64_t pn_sb, int64_t pn_sh,
+                                     void* p_dst, int64_t pd_sb, int64_t pd_sh, int64_t pd_ss,
+                                     const int64_t* pos_new, int64_t posn_sb, int64_t* pos_dst, int64_t posd_sb,
+                                     const uint8_t* mask, int64_t mask_sb,
+                                     int64_t held_len,
+                                     const int64_t* held_pos, int64_t hp_sb, int64_t hp_sh,
+                                     const uint8_t* held_valid, int64_t hv_sb, int64_t hv_sh,
+                                     const int64_t* cur_pos,
+                                     double scaling,
+                                     void* out, int64_t o_sb, int64_t o_sh,
+                                     void* workspace, int64_t workspace_bytes, int64_t num_splits,
+                                     void* stream) {
+  HC_REQUIRE(k_new && v_new, "decode_append: k_new and v_new are required");
+  HC_REQUIRE((p_new == nullptr) == (p_dst == nullptr), "decode_append: p_new and p_dst go together");
+  HC_REQUIRE((pos_new == nullptr) == (pos_dst == nullptr), "decode_append: pos_new and pos_dst go together");
+  DecodeArgs ap{};
+  ap.k_new = k_new; ap.kn_sb = kn_sb; ap.kn_sh = kn_sh;
+  ap.v_new = v_new; ap.vn_sb = vn_sb; ap.vn_sh = vn_sh;
+  ap.p_new = p_new; ap.pn_sb = pn_sb; ap.pn_sh = pn_sh;
+  ap.p_dst = p_dst; ap.pd_sb = pd_sb; ap.pd_sh = pd_sh; ap.pd_ss = pd_ss;
+  ap.pos_new = pos_new; ap.posn_sb = posn_sb; ap.pos_dst = pos_dst; ap.posd_sb = posd_sb;
+  return decode_impl(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss, mask, mask_sb,
+                     held_len, held_pos, hp_sb, hp_sh, held_valid, hv_sb, hv_sh, cur_pos, scaling, 0.0, out, o_sb,
+                     o_sh, nullptr, nullptr, workspace, workspace_bytes, num_splits, stream, &ap);
 }

@@ -73,9 +73,13 @@ class PressLayerState:
         return out
 
     def decode(self, q_post, k_post, v, n_rep, scaling):
-        """Single-token decode: append, then attend over the compressed cache."""
+        """Single-token decode: append, then attend over the compressed cache
+        (one fused launch for one token)."""
         if self.buf is None:
             raise RuntimeError("decode before prefill")
-        self.buf.append(k_post, v)
-        out = ops.decode_attention(q_post, self.buf.keys, self.buf.values, scaling)
+        if k_post.shape[2] == 1:
+            out = self.buf.append_attend(q_post, k_post, v, scaling)
+        else:
+            self.buf.append(k_post, v)
+            out = ops.decode_attention(q_post, self.buf.keys, self.buf.values, scaling)
         return out.unsqueeze(2)  # (B,Hq,1,D)

@@ -105,6 +105,18 @@ class HotBuffer:
                         pos_src=pos if self.with_pos else None, pos_dst=self.st["pos"] if self.with_pos else None)
         self.n += T
 
+    def append_attend(self, q, k, v, scaling, pre=None, pos=None):
+        """Append one token (k, v, pre (B,H,1,D), pos (B,1)) and attend q over
+        the hot rows plus the token, in one launch.  Returns (B,Hq,D)."""
+        self.ensure(self.n + 1)
+        lo, hi = self.held, self.held + self.n + 1
+        out = ops.decode_attention_append(
+            q, self._rows("k", lo, hi), self._rows("v", lo, hi), k, v, scaling,
+            pre=(pre, self._rows("p", lo, hi)) if self.with_pre and pre is not None else None,
+            pos=(pos, self._rows("pos", lo, hi)) if self.with_pos and pos is not None else None)
+        self.n += 1
+        return out
+
     def set_from(self, k, v, pre=None, pos=None):
         """Replace the hot rows with the given tokens."""
         self.n = 0

@@ -59,6 +59,40 @@ def _rows4(x, name):
 # ---------------------------------------------------------------------------
 # Decode attention
 # ---------------------------------------------------------------------------
+def _held_mask_args(B, Hk, S, mask, held_len, held_pos, held_valid, cur_pos, what):
+    """Validate / normalise the mask and held-slot arguments over S cached rows."""
+    if mask is not None:
+        if mask.dim() != 2 or mask.shape[0] != B or mask.shape[1] < S:
+            raise RuntimeError(f"{what}: mask must be (B,S)=({B},{S}); got {tuple(mask.shape)}")
+        if mask.dtype == torch.bool:
+            mask = mask.view(torch.uint8) if mask.is_contiguous() else mask.contiguous().view(torch.uint8)
+        elif mask.dtype != torch.uint8:
+            mask = (mask != 0).to(torch.uint8)
+        if mask.stride(1) != 1:
+            mask = mask.contiguous()
+    hp_sb = hp_sh = hv_sb = hv_sh = 0
+    if held_len:
+        if held_pos is None or held_valid is None:
+            raise RuntimeError(f"{what}: held_len needs held_pos and held_valid")
+        if held_valid.dtype == torch.bool:
+            held_valid = held_valid.contiguous().view(torch.uint8)
+        held_pos = held_pos.contiguous()
+        held_valid = held_valid.contiguous()
+        for t, name in ((held_pos, "held_pos"), (held_valid, "held_valid")):
+            if t.dim() not in (2, 3) or t.shape[0] != B or t.shape[-1] < held_len or held_len > S \
+                    or (t.dim() == 3 and t.shape[1] != Hk):
+                raise RuntimeError(f"{what}: {name} {tuple(t.shape)} does not cover {held_len} "
+                                   f"held rows of (B,Hk)=({B},{Hk})")
+        if held_pos.dtype != torch.int64:
+            raise RuntimeError(f"{what}: held_pos must be int64")
+        hp_sb, hp_sh = (held_pos.stride(0), 0) if held_pos.dim() == 2 else (held_pos.stride(0), held_pos.stride(1))
+        hv_sb, hv_sh = (held_valid.stride(0), 0) if held_valid.dim() == 2 else \
+            (held_valid.stride(0), held_valid.stride(1))
+    if cur_pos is not None and (cur_pos.dtype != torch.int64 or cur_pos.numel() < 1):
+        raise RuntimeError(f"{what}: cur_pos must be a non-empty int64 tensor")
+    return mask, hp_sb, hp_sh, hv_sb, hv_sh, held_pos, held_valid
+
+
 def decode_attention(q, k, v, scaling, mask=None, held_len=0, held_pos=None, held_valid=None,
                      cur_pos=None, out=None, num_splits=0, with_evict=False, dropout=0.0):
     """Single-token GQA attention of q (B,Hq,D) or (B,Hq,1,D) over k/v (B,Hk,S,D).
@@ -87,41 +121,8 @@ def decode_attention(q, k, v, scaling, mask=None, held_len=0, held_pos=None, hel
         raise RuntimeError(f"decode_attention: shape mismatch q {tuple(q3.shape)} k {tuple(k.shape)} v {tuple(v.shape)}")
     if k.dtype != q3.dtype or v.dtype != q3.dtype:
         raise RuntimeError("decode_attention: q, k, v must share a dtype")
-    if mask is not None:
-        if mask.dim() != 2 or mask.shape[0] != B or mask.shape[1] != S:
-            raise RuntimeError(f"decode_attention: mask must be (B,S)=({B},{S}); got {tuple(mask.shape)}")
-        if mask.dtype == torch.bool:
-            mask = mask.view(torch.uint8) if mask.is_contiguous() else mask.contiguous().view(torch.uint8)
-        elif mask.dtype != torch.uint8:
-            mask = (mask != 0).to(torch.uint8)
-        if mask.stride(1) != 1:
-            mask = mask.contiguous()
-    hp_sb = hp_sh = hv_sb = hv_sh = 0
-    if held_len:
-        if held_pos is None or held_valid is None:
-            raise RuntimeError("decode_attention: held_len needs held_pos and held_valid")
-        if held_valid.dtype == torch.bool:
-            held_valid = held_valid.contiguous().view(torch.uint8)
-        held_pos = held_pos.contiguous()
-        held_valid = held_valid.contiguous()
-        for t, name in ((held_pos, "held_pos"), (held_valid, "held_valid")):
-            if t.dim() not in (2, 3) or t.shape[0] != B or t.shape[-1] < held_len or held_len > S \
-                    or (t.dim() == 3 and t.shape[1] != Hk):
-                raise RuntimeError(f"decode_attention: {name} {tuple(t.shape)} does not cover {held_len} "
-                                   f"held rows of (B,Hk)=({B},{Hk})")
-        if held_pos.dtype != torch.int64:
-            raise RuntimeError("decode_attention: held_pos must be int64")
-    if cur_pos is not None and (cur_pos.dtype != torch.int64 or cur_pos.numel() < 1):
-        raise RuntimeError("decode_attention: cur_pos must be a non-empty int64 tensor")
-    if held_len:
-        if held_pos.dim() == 2:
-            hp_sb, hp_sh = held_pos.stride(0), 0
-        else:
-            hp_sb, hp_sh = held_pos.stride(0), held_pos.stride(1)
-        if held_valid.dim() == 2:
-            hv_sb, hv_sh = held_valid.stride(0), 0
-        else:
-            hv_sb, hv_sh = held_valid.stride(0), held_valid.stride(1)
+    mask, hp_sb, hp_sh, hv_sb, hv_sh, held_pos, held_valid = _held_mask_args(
+        B, Hk, S, mask, held_len, held_pos, held_valid, cur_pos, "decode_attention")
     if out is None:
         out = torch.empty((B, Hq, D), dtype=q3.dtype, device=q3.device)
     if out.stride(-1) != 1:
@@ -150,6 +151,93 @@ def decode_attention(q, k, v, scaling, mask=None, held_len=0, held_pos=None, hel
     N.check(rc, "hc_decode_attn")
     if with_evict:
         return out, ev_loss, ev_idx
+    return out
+
+
+def decode_attention_append(q, k, v, k_new, v_new, scaling, pre=None, pos=None, mask=None, held_len=0,
+                            held_pos=None, held_valid=None, cur_pos=None, out=None, num_splits=0):
+    """Append one token and attend, in one launch.
+
+    k, v are (B,Hk,S,D) views of the hot buffer whose last row S-1 is the
+    free row for the new token; k_new, v_new (B,Hk,D) or (B,Hk,1,D) are the
+    token's key and value.  The kernel attends over rows 0..S-2 of k/v plus
+    the new token and writes k_new/v_new into row S-1 -- the torch.cat append
+    followed by attention of cache.py:145-148 / layer_state.py:96-100 and
+    kernels.py:77-137.  pre = (p_new, p_dst) and pos = (pos_new (B,1),
+    pos_dst (B,>=S)) optionally write the pre-RoPE key row and the position as
+    well.  mask / held_* apply to the cached rows as in decode_attention; the
+    new token is always attended.  Returns out (B,Hq,D).
+    """
+    _require_device(q, k, v, k_new, v_new, mask, held_pos, held_valid, cur_pos)
+    lib = N.lib()
+    if q.dim() == 4 and q.shape[2] != 1:
+        raise RuntimeError(f"decode_attention_append: expected one query token, got q {tuple(q.shape)}")
+    q3 = q[:, :, 0, :] if q.dim() == 4 else q
+    if q3.stride(-1) != 1:
+        q3 = q3.contiguous()
+    if k.dim() != 4 or v.dim() != 4 or k.stride(-1) != 1 or v.stride(-1) != 1:
+        raise RuntimeError("decode_attention_append: k, v must be 4D views with a unit last stride "
+                           "(they are written in place)")
+    kn = k_new[:, :, 0, :] if k_new.dim() == 4 else k_new
+    vn = v_new[:, :, 0, :] if v_new.dim() == 4 else v_new
+    B, Hq, D = q3.shape
+    Bk, Hk, S, Dk = k.shape
+    if Bk != B or Dk != D or S < 1 or tuple(kn.shape) != (B, Hk, D) or tuple(vn.shape) != (B, Hk, D) \
+            or tuple(v.shape) != tuple(k.shape):
+        raise RuntimeError(f"decode_attention_append: shape mismatch k {tuple(k.shape)} k_new {tuple(k_new.shape)} "
+                           f"v_new {tuple(v_new.shape)}")
+    if kn.stride(-1) != 1:
+        kn = kn.contiguous()
+    if vn.stride(-1) != 1:
+        vn = vn.contiguous()
+    for t in (k, v, kn, vn):
+        if t.dtype != q3.dtype:
+            raise RuntimeError("decode_attention_append: q, k, v, k_new, v_new must share a dtype")
+    pn = pd = None
+    if pre is not None:
+        pn, pd = pre
+        pn = pn[:, :, 0, :] if pn.dim() == 4 else pn
+        if pn.stride(-1) != 1:
+            pn = pn.contiguous()
+        if tuple(pn.shape) != (B, Hk, D) or pd.dim() != 4 or pd.shape[2] < S or pd.stride(-1) != 1 \
+                or pd.dtype != q3.dtype or pn.dtype != q3.dtype:
+            raise RuntimeError("decode_attention_append: pre=(p_new (B,Hk,D), p_dst (B,Hk,>=S,D)) in q's dtype")
+    posn = posd = None
+    if pos is not None:
+        posn, posd = pos
+        if posn.dtype != torch.int64 or posd.dtype != torch.int64 or posn.shape[0] != B or posd.shape[0] != B \
+                or posd.dim() != 2 or posd.shape[1] < S or posd.stride(1) != 1:
+            raise RuntimeError("decode_attention_append: pos=(pos_new (B,1) int64, pos_dst (B,>=S) int64)")
+        posn = posn.reshape(B, -1)
+    mask, hp_sb, hp_sh, hv_sb, hv_sh, held_pos, held_valid = _held_mask_args(
+        B, Hk, S - 1, mask, held_len, held_pos, held_valid, cur_pos, "decode_attention_append")
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=q3.dtype, device=q3.device)
+    if out.stride(-1) != 1:
+        raise RuntimeError("decode_attention_append: out must have a unit last stride")
+    nbytes = lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, 0)
+    ws = _workspace("decode", q3.device, nbytes)
+    rc = lib.hc_decode_attn_append(
+        N.dtype_code(q3.dtype), B, Hq, Hk, D, S,
+        _ptr(q3), q3.stride(0), q3.stride(1),
+        _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        _ptr(kn), kn.stride(0), kn.stride(1),
+        _ptr(vn), vn.stride(0), vn.stride(1),
+        _ptr(pn), pn.stride(0) if pn is not None else 0, pn.stride(1) if pn is not None else 0,
+        _ptr(pd), *(pd.stride()[:3] if pd is not None else (0, 0, 0)),
+        _ptr(posn), posn.stride(0) if posn is not None else 0,
+        _ptr(posd), posd.stride(0) if posd is not None else 0,
+        _ptr(mask), mask.stride(0) if mask is not None else 0,
+        int(held_len),
+        _ptr(held_pos), hp_sb, hp_sh,
+        _ptr(held_valid), hv_sb, hv_sh,
+        _ptr(cur_pos),
+        float(scaling),
+        _ptr(out), out.stride(0), out.stride(1),
+        _ptr(ws), ws.numel(), int(num_splits),
+        _stream_handle(q3.device))
+    N.check(rc, "hc_decode_attn_append")
     return out
 
 

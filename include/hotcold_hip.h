@@ -86,6 +86,41 @@ int hc_decode_attn(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int6
                    void* stream);
 
 /*
+ * Append one token per (b, kv head) and attend, in one launch.  Replaces the
+ * torch.cat append of cache.py:145-148 / layer_state.py:96-100 followed by
+ * the decode attention of kernels.py:77-137 (call site patch.py:295-305).
+ *
+ *   k, v [B][Hk][S][D]: rows 0..S-2 are the cache; row S-1 receives the new
+ *     token.  k_new / v_new [B][Hk][D] are the token's key and value,
+ *     attended as key S-1 and written into row S-1 by the launch.
+ *   p_new / p_dst (may both be NULL): the token's pre-RoPE key, written into
+ *     row S-1 of p_dst [B][Hk][*][D] (cache.py:145-148 keeps pre-RoPE keys).
+ *   pos_new [B] (stride posn_sb) / pos_dst [B][*] (may both be NULL): its
+ *     absolute position, written at pos_dst[b][S-1].
+ *   mask / held_* apply to the cached rows (held_len <= S-1) exactly as in
+ *     hc_decode_attn; the new token is always attended.  No eviction score.
+ *   The workspace is sized by hc_decode_attn_workspace_size(.., S, .., 0).
+ */
+int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                          const void* q, int64_t q_sb, int64_t q_sh,
+                          void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                          void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                          const void* k_new, int64_t kn_sb, int64_t kn_sh,
+                          const void* v_new, int64_t vn_sb, int64_t vn_sh,
+                          const void* p_new, int64_t pn_sb, int64_t pn_sh,
+                          void* p_dst, int64_t pd_sb, int64_t pd_sh, int64_t pd_ss,
+                          const int64_t* pos_new, int64_t posn_sb, int64_t* pos_dst, int64_t posd_sb,
+                          const uint8_t* mask, int64_t mask_sb,
+                          int64_t held_len,
+                          const int64_t* held_pos, int64_t hp_sb, int64_t hp_sh,
+                          const uint8_t* held_valid, int64_t hv_sb, int64_t hv_sh,
+                          const int64_t* cur_pos,
+                          double scaling,
+                          void* out, int64_t o_sb, int64_t o_sh,
+                          void* workspace, int64_t workspace_bytes, int64_t num_splits,
+                          void* stream);
+
+/*
  * Window importance scores per KV head, fp32 [B][Hk][S] (row stride S).
  * Replaces snapkv_importance (scoring.py:50-79) with _group_query_to_kv
  * (scoring.py:17-26) and pool1d (scoring.py:40-47) in HC_SCORE_SNAPKV mode,

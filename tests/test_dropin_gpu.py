@@ -246,6 +246,8 @@ def _press_cycle(method, dtype, B=2, Hq=8, Hk=2, S=200, D=16, budget=64, window=
         kk, vv = torch.cat([kk, k1], 2), torch.cat([vv, v1], 2)
         want = ref.decode_attention(q1, kk, vv, scaling)
         assert (out1[:, :, 0].double().cpu().numpy() - want).__abs__().max() < tol
+    # the fused append left the token rows in the buffer
+    assert torch.equal(st.keys.cpu(), kk) and torch.equal(st.values.cpu(), vv)
     return st
 
 

@@ -149,6 +149,101 @@ def test_decode_strided_views_and_evict_score():
         assert want_loss[b, int(idx[b])] <= want_loss[b].min() * (1 + 2e-3) + 1e-7
 
 
+APPEND_CASES = [
+    # B, Hq, Hk, cap, n (cached rows), D, dtype, splits
+    (1, 32, 8, 700, 573, 128, torch.float16, 0),    # 8k/budget-512 hot buffer, mid-decode
+    (1, 32, 8, 700, 573, 128, torch.bfloat16, 0),
+    (1, 32, 8, 600, 543, 128, torch.float32, 0),
+    (2, 8, 2, 300, 199, 16, torch.float32, 0),      # reference test geometry
+    (4, 32, 8, 2500, 2430, 128, torch.float16, 0),  # batched, several splits
+    (1, 32, 8, 700, 573, 128, torch.float16, 1),    # forced single split
+    (1, 32, 8, 700, 573, 128, torch.float16, 7),    # forced ragged splits
+    (3, 16, 4, 8, 0, 64, torch.float16, 0),         # empty cache: the new token alone
+    (1, 64, 8, 300, 250, 128, torch.float16, 0),    # group of 8
+    (1, 8, 1, 1000, 900, 256, torch.bfloat16, 0),   # one KV head, wide head_dim
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hk,cap,n,D,dtype,splits", APPEND_CASES)
+def test_decode_append_matches_append_then_decode(B, Hq, Hk, cap, n, D, dtype, splits):
+    """The fused launch writes the token into row n of the hot buffer and
+    attends over rows 0..n: same buffer as append_rows, same output as the
+    oracle on the concatenated cache."""
+    kbuf, vbuf = _randn((B, Hk, cap, D), 21, dtype), _randn((B, Hk, cap, D), 22, dtype)
+    q = _randn((B, Hq, 1, D), 23, dtype)
+    kn, vn = _randn((B, Hk, 1, D), 24, dtype), _randn((B, Hk, 1, D), 25, dtype)
+    sc = 1.0 / math.sqrt(D)
+    kd, vd = kbuf.to(DEV), vbuf.to(DEV)
+    out = ops.decode_attention_append(q.to(DEV), kd[:, :, :n + 1], vd[:, :, :n + 1], kn.to(DEV), vn.to(DEV), sc,
+                                      num_splits=splits)
+    kw, vw = kbuf.clone(), vbuf.clone()
+    kw[:, :, n:n + 1], vw[:, :, n:n + 1] = kn, vn
+    assert torch.equal(kd.cpu(), kw) and torch.equal(vd.cpu(), vw)
+    want = ref.decode_attention(q, kw[:, :, :n + 1], vw[:, :, :n + 1], sc)
+    got = out.float().cpu().numpy()
+    assert np.isfinite(got).all()
+    assert np.abs(got - want).max() <= TOL[dtype], np.abs(got - want).max()
+    # the two-launch path on a second copy of the buffer agrees within the tolerance
+    k2, v2 = kbuf.to(DEV), vbuf.to(DEV)
+    ops.append_rows(n, kn.to(DEV), k2, vn.to(DEV), v2)
+    out2 = ops.decode_attention(q.to(DEV), k2[:, :, :n + 1], v2[:, :, :n + 1], sc, num_splits=splits)
+    assert np.abs(out2.float().cpu().numpy() - got).max() <= TOL[dtype]
+    if n == 0:
+        for h in range(Hq):
+            assert torch.equal(out[:, h].cpu(), vn[:, h // (Hq // Hk), 0])
+
+
+@pytest.mark.parametrize("per_head", [False, True])
+def test_decode_append_held_slot_mask_pre_and_pos(per_head):
+    """Held-slot masking and an explicit mask apply to the cached rows; the
+    new token is always attended; its pre-RoPE key and position land in row n."""
+    B, Hq, Hk, R, n0, cap, D = 2, 32, 8, 64, 400, 600, 128
+    n = R + n0
+    dtype = torch.float16
+    kbuf, vbuf, pbuf = (_randn((B, Hk, cap, D), s, dtype) for s in (31, 32, 33))
+    posbuf = torch.randint(0, 5000, (B, cap), generator=torch.Generator().manual_seed(34))
+    q = _randn((B, Hq, 1, D), 35, dtype)
+    kn, vn, pn = (_randn((B, Hk, 1, D), s, dtype) for s in (36, 37, 38))
+    posn = torch.tensor([[4321], [4322]], dtype=torch.int64)
+    g = torch.Generator().manual_seed(39)
+    shape = (B, Hk, R) if per_head else (B, R)
+    valid = torch.rand(shape, generator=g) < 0.7
+    hpos = torch.randint(0, 2000, shape, generator=g)
+    cur = torch.tensor([1500], dtype=torch.int64)
+    mask = torch.rand((B, n), generator=g) < 0.9
+    kd, vd, pd, posd = kbuf.to(DEV), vbuf.to(DEV), pbuf.to(DEV), posbuf.to(DEV)
+    out = ops.decode_attention_append(q.to(DEV), kd[:, :, :n + 1], vd[:, :, :n + 1], kn.to(DEV), vn.to(DEV), 0.088,
+                                      pre=(pn.to(DEV), pd), pos=(posn.to(DEV), posd), mask=mask.to(DEV),
+                                      held_len=R, held_pos=hpos.to(DEV), held_valid=valid.to(DEV),
+                                      cur_pos=cur.to(DEV)).float().cpu().numpy()
+    kw, vw, pw, posw = kbuf.clone(), vbuf.clone(), pbuf.clone(), posbuf.clone()
+    kw[:, :, n:n + 1], vw[:, :, n:n + 1], pw[:, :, n:n + 1] = kn, vn, pn
+    posw[:, n] = posn[:, 0]
+    for got, want in ((kd, kw), (vd, vw), (pd, pw), (posd, posw)):
+        assert torch.equal(got.cpu(), want)
+    G = Hq // Hk
+    for h in range(Hk):
+        vh = valid[:, h] if per_head else valid
+        ph = hpos[:, h] if per_head else hpos
+        held = torch.cat([vh & (ph <= cur), torch.ones((B, n0), dtype=torch.bool)], 1)
+        m = torch.cat([held & mask, torch.ones((B, 1), dtype=torch.bool)], 1)
+        want = ref.decode_attention(q[:, h * G:(h + 1) * G], kw[:, h:h + 1, :n + 1], vw[:, h:h + 1, :n + 1], 0.088, m)
+        assert np.abs(out[:, h * G:(h + 1) * G] - want).max() <= 2e-3, h
+
+
+def test_decode_append_argument_errors():
+    q = torch.zeros((1, 8, 1, 64), dtype=torch.float16, device=DEV)
+    k = torch.zeros((1, 2, 10, 64), dtype=torch.float16, device=DEV)
+    kn = torch.zeros((1, 2, 64), dtype=torch.float16, device=DEV)
+    hp = torch.zeros((1, 10), dtype=torch.int64, device=DEV)
+    hv = torch.ones((1, 10), dtype=torch.bool, device=DEV)
+    # the held slot may not reach the row the token is written to
+    with pytest.raises(RuntimeError, match="held"):
+        ops.decode_attention_append(q, k, k.clone(), kn, kn, 0.1, held_len=10, held_pos=hp, held_valid=hv)
+    with pytest.raises(RuntimeError, match="shape mismatch"):
+        ops.decode_attention_append(q, k, k.clone(), kn[:, :1], kn, 0.1)
+
+
 # ---------------------------------------------------------------------------
 # SnapKV compaction
 # ---------------------------------------------------------------------------
