@@ -17,12 +17,16 @@ new token's K/V row and attends over the buffer plus that token.
 
 Before each decode launch a read sweep over 512 MiB evicts the 256 MB Infinity
 Cache (in a model, the weights streamed between two visits of a layer do
-that), so decode reads its K/V from HBM; the sweep is outside the decode
-events.  It only reads, so no dirty lines are left for decode to write back.
+that), so decode reads its K/V from HBM; the sweep's own time is measured
+separately and subtracted.  It only reads, so no dirty lines are left for
+decode to write back.
 
 Reported:
   value              decode us per layer-step: mean append+decode launch time
-                     of the timed steps (HIP events on the launch stream) / 32
+                     of the timed steps / 32, timed with HIP events on the
+                     launch stream as [sweep; decode] minus [sweep] alone
+                     (run_steps explains; the event-bracketed time is also
+                     reported)
   compact_ms_32_layers  compaction of all 32 layers per step, ms
   roofline           decode launch: algorithmic bytes / mean launch time
   roofline_compaction, scoring MFMA rate, a per-layer-launch variant (one
@@ -188,40 +192,61 @@ class Setup:
 
 
 def run_steps(s, steps, flush):
-    """Run `steps` whole jobs; return (wall ms/step, compaction ms per step,
-    decode-launch ms list).  Compaction replays its graph; the append+decode
-    launches are issued directly: the cache sweep before each keeps the GPU
-    busy long enough for the host to stay ahead, so the decode events see no
-    host gap (a one-kernel graph replay adds several microseconds of its own
-    on this stack)."""
+    """Run `steps` whole jobs; return (wall ms/step, compaction ms list,
+    decode ms (differential), decode ms (event-bracketed)).
+
+    Compaction replays its graph between two events.  Each decode step t is
+    timed two ways, both after a cache sweep:
+      differential  events around [sweep; decode] minus events around
+                    [sweep] alone: the decode kernel plus the ordinary gap
+                    between two dependent kernels, as in a model's stream;
+      bracketed     events directly around the decode launch: this adds the
+                    3-4 us an event marker between two kernels costs here.
+    The fused launch is idempotent (it rewrites row budget+t with the same
+    token), so running step t twice leaves the same buffer."""
     import torch
     w = s.w
     st = s.stream
-    comp_ev, dec_ev = [], []
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    comp_ev, sweep_ev, pair_ev, br_ev = [], [], [], []
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     with torch.cuda.stream(st):
         for _ in range(steps):
-            c0 = torch.cuda.Event(enable_timing=True)
-            c1 = torch.cuda.Event(enable_timing=True)
+            c0, c1 = ev(), ev()
             c0.record(st)
             s.g_comp.replay()
             c1.record(st)
             comp_ev.append((c0, c1))
             for t in range(w.decode_steps):
-                if flush is not None:
-                    flush()
-                e0 = torch.cuda.Event(enable_timing=True)
-                e1 = torch.cuda.Event(enable_timing=True)
+                a0, a1, b0, b1, e0, e1 = ev(), ev(), ev(), ev(), ev(), ev()
+                a0.record(st)
+                flush()
+                a1.record(st)
+                b0.record(st)
+                flush()
+                s.decode(t)
+                b1.record(st)
+                flush()
                 e0.record(st)
                 s.decode(t)
                 e1.record(st)
-                dec_ev.append((e0, e1))
+                sweep_ev.append((a0, a1))
+                pair_ev.append((b0, b1))
+                br_ev.append((e0, e1))
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / max(1, steps)
-    comp = [a.elapsed_time(b) for a, b in comp_ev]
-    dec = [a.elapsed_time(b) for a, b in dec_ev]
-    return wall_ms, comp, dec
+
+    def ms(evs):
+        return [a.elapsed_time(b) for a, b in evs]
+
+    comp = ms(comp_ev)
+    dec_diff = statistics.mean(ms(pair_ev)) - statistics.mean(ms(sweep_ev))
+    dec_br = statistics.mean(ms(br_ev))
+    return wall_ms, comp, dec_diff, dec_br
 
 
 def time_graph(g, st, iters, flush=None):
@@ -363,12 +388,12 @@ def main():
 
     run_steps(s, args.warmup, flush)
     log(f"warmup done ({args.warmup} steps)")
-    wall_ms, comp, dec = run_steps(s, args.steps, flush)
+    wall_ms, comp, dec_ms, dec_br_ms = run_steps(s, args.steps, flush)
     comp_ms = statistics.mean(comp)
-    dec_ms = statistics.mean(dec)                      # one decode launch, all layers
-    dec_us_layer = dec_ms * 1e3 / w.layers
-    log(f"timed {args.steps} steps: {wall_ms:.3f} ms/step wall (incl. cache flushes), compaction "
-        f"{comp_ms:.3f} ms, decode launch {dec_ms * 1e3:.2f} us = {dec_us_layer:.3f} us/layer-step")
+    dec_us_layer = dec_ms * 1e3 / w.layers            # one append+decode launch covers all layers
+    log(f"timed {args.steps} steps: {wall_ms:.3f} ms/step wall (incl. cache sweeps), compaction "
+        f"{comp_ms:.3f} ms, append+decode launch {dec_ms * 1e3:.2f} us (differential; "
+        f"event-bracketed {dec_br_ms * 1e3:.2f} us) = {dec_us_layer:.3f} us/layer-step")
 
     # algorithmic rates
     mean_keys = w.budget + (w.decode_steps + 1) / 2.0
@@ -415,13 +440,16 @@ def main():
                                "Infinity Cache flushed before decode"},
         "compact_ms_32_layers": round(comp_ms, 4),
         "decode_us_per_layer_step": round(dec_us_layer, 4),
+        "decode_launch_us_differential": round(dec_ms * 1e3, 3),
+        "decode_launch_us_event_bracketed": round(dec_br_ms * 1e3, 3),
         "decode_us_per_layer_launch_cold": round(pl_cold_ms * 1e3 / w.layers, 3),
         "decode_us_per_layer_launch_warm": round(pl_warm_ms * 1e3 / w.layers, 3),
         "decode_launch_us_warm_last_step": round(warm_dec_ms * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(w.name),
                      "kernel": "decode_attn_kernel (fused append, + decode_combine_kernel)",
-                     "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3)},
+                     "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3),
+                     "launch_timing": "events around [cache sweep; decode] minus events around [cache sweep]"},
         "roofline_compaction": {"bound": "hbm", "achieved": round(c_achieved, 1), "peak": HBM_PEAK_GBS,
                                 "unit": "GB/s", "frac": round(c_achieved / HBM_PEAK_GBS, 4),
                                 "bytes_per_job": int(cbytes),
