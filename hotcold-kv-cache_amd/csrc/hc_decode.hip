@@ -25,16 +25,27 @@
 //     evaluated once per workgroup into an LDS bitmap;
 //   * split partials (m, l, acc) are merged by a second, one-pass kernel.
 #include "hc_common.h"
+#include <stddef.h>
 
 namespace hc {
 
 struct DecodeArgs {
+  // Fields the kernel's prologue reads come first: they fit the first 128
+  // bytes, two scalar loads issued together, so the first K/V loads wait on
+  // one round trip to the argument memory.
   const void* q;
   int64_t q_sb, q_sh;
   const void* k;
   int64_t k_sb, k_sh, k_ss;
   const void* v;
   int64_t v_sb, v_sh, v_ss;
+  uint32_t k_bytes, v_bytes, q_bytes;  // buffer extents of one (b, kv head)
+  int G;
+  int keys_per_split;
+  int S_cache;  // rows read from k/v: S, or S-1 with a fused append
+  float scale_log2;
+  int splits, S, Hq;
+  int B, Hk;
   const uint8_t* mask;
   int64_t mask_sb;
   const int64_t* held_pos;
@@ -48,10 +59,6 @@ struct DecodeArgs {
   float* part;         // [units][splits][G*D + 2*G] split partials (splits > 1)
   float* scores;       // optional [B][Hq][S] log2-domain logits (eviction score)
   float* ml;           // optional [B][Hq][2] final (max, sum)
-  uint32_t k_bytes, v_bytes, q_bytes;  // buffer extents of one (b, kv head)
-  int B, Hq, Hk, G, S, splits, keys_per_split;
-  int S_cache;  // rows read from k/v: S, or S-1 with a fused append
-  float scale_log2;
   // Fused append (hc_decode_attn_append): the token at row S-1 comes from
   // k_new / v_new ([B][Hk][D]); the last split's workgroup attends it and
   // writes it (and optionally its pre-RoPE key and position) into row S-1.
@@ -69,6 +76,7 @@ struct DecodeArgs {
   int64_t* pos_dst;
   int64_t posd_sb;
 };
+static_assert(offsetof(DecodeArgs, Hq) + sizeof(int) <= 128, "prologue fields must fit the first 128 bytes");
 
 // Keys of one split when the keep bitmap is needed (mask or held slot).
 constexpr int kMaxBitmapKeys = 16384;
@@ -89,6 +97,20 @@ struct TileRegs {
   uint32_t v[4][VWORDS];
   uint32_t keep;  // bit i: key tile + 4*(l/16) + i is attended
 };
+
+// Keep bit of key `key` in the split's bitmap (bit key - key_begin).
+__device__ __forceinline__ uint32_t bitmap_bit(const uint32_t* bits, int key, int key_begin) {
+  const int rel = min(key - key_begin, kMaxBitmapKeys - 1);
+  return (bits[rel >> 5] >> (rel & 31)) & 1u;
+}
+
+// Keep bits (bit i: key tile + 4*grp + i) of a tile from the bitmap.
+__device__ __forceinline__ uint32_t tile_keep_bits(int tile, int key_begin, int grp, const uint32_t* bits) {
+  uint32_t keep = 0;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) keep |= bitmap_bit(bits, tile + 4 * grp + i, key_begin) << i;
+  return keep;
+}
 
 // Issue the loads of one tile (all unconditional) and read its keep bits.
 template <typename T, int D>
@@ -117,11 +139,7 @@ __device__ __forceinline__ void load_tile(TileRegs<T, D>& r, __amdgpu_buffer_rsr
 #pragma unroll
       for (int c = 1; c < R::VB / 16; ++c) bload<16>(vrs, off == kOob ? kOob : off + 16 * c, &r.v[i][4 * c]);
     }
-    bool kp = ok;
-    if (bits) {
-      const int rel = min(key - key_begin, kMaxBitmapKeys - 1);
-      kp = ok && ((bits[rel >> 5] >> (rel & 31)) & 1u);
-    }
+    const bool kp = ok && (!bits || bitmap_bit(bits, key, key_begin));
     keep |= (kp ? 1u : 0u) << i;
   }
   r.keep = keep;
@@ -472,29 +490,6 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
   const uint32_t k_rowb = (uint32_t)(a.k_ss * (int64_t)sizeof(T));
   const uint32_t v_rowb = (uint32_t)(a.v_ss * (int64_t)sizeof(T));
 
-  // Keep bitmap of the split's keys: attention mask and held-slot test.
-  __shared__ uint32_t sm_bits[kMaxBitmapKeys / 32];
-  const bool use_bits = (a.mask != nullptr) || (a.held_len > key_begin);
-  if (use_bits) {
-    const int64_t cur = a.cur_pos ? *a.cur_pos : INT64_MAX;
-    const uint8_t* mrow = a.mask ? a.mask + b * a.mask_sb : nullptr;
-    const int nwords = (key_end - key_begin + 31) >> 5;
-    for (int wd = threadIdx.x; wd < nwords; wd += 64 * NW) {
-      uint32_t bits = 0;
-      for (int j = 0; j < 32; ++j) {
-        const int key = key_begin + 32 * wd + j;
-        bool kp = key < key_end;
-        if (kp && mrow) kp = mrow[key] != 0;
-        if (kp && key < a.held_len)
-          kp = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key] != 0 &&
-               a.held_pos[b * a.hp_sb + hk * a.hp_sh + key] <= cur;
-        bits |= (kp ? 1u : 0u) << j;
-      }
-      sm_bits[wd] = bits;
-    }
-    __syncthreads();
-  }
-  const uint32_t* bits = use_bits ? sm_bits : nullptr;
 
   constexpr bool MX = sizeof(T) == 2;
   typename DecodeState<T, D, GM>::type st;
@@ -517,14 +512,28 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
   const int wend = min(key_end, wbeg + kpw);
   const int first = wbeg;
   const int nt = wbeg < wend ? (wend - wbeg + 15) / 16 : 0;
-  if (APPEND || nt > 0) {
+  {
+    QFrag<T, D> qf;
+    const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
+    qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
+
+    // The ring's first NBUF-1 tiles are issued before the keep bitmap is
+    // built, so the bitmap's own loads overlap them; their keep bits are
+    // applied once the bitmap is complete.
+    TileRegs<T, D> r[NBUF];
+#pragma unroll
+    for (int i = 0; i < NBUF - 1; ++i)
+      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * 16, key_begin, wend, col, grp, nullptr);
+
     // Fused append: the last wave of the last split attends the new token as
     // a one-key tile and copies the token's K/V (and pre-RoPE key and
-    // position) into row S-1.  Its loads are issued first and it is processed
-    // after the wave's first NBUF tiles, by when they have landed, so it adds
-    // no wait; the copies are stored after the last tile.  Every wave runs this code with resources of extent 0 where it
-    // does not own the token: no branch around memory operations, so the
-    // compiler's load counting stays exact.
+    // position) into row S-1.  Its loads are issued right after the ring's
+    // first tiles and it is processed after the wave's first NBUF tiles, by
+    // when they have landed, so it adds no wait; the copies are stored after
+    // the last tile.  Every wave runs
+    // this code with resources of extent 0 where it does not own the token:
+    // no branch around memory operations, so the compiler's load counting
+    // stays exact.
     TileRegs<T, D> rn;
     uint32_t pw[TileRegs<T, D>::KW][4];
     uint32_t pos_w[2];
@@ -548,14 +557,33 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       bload<8>(make_rsrc(psrc, tq ? 8u : 0u), lane == 0 ? 0u : kOob, pos_w);
     }
 
-    TileRegs<T, D> r[NBUF];
+    // Keep bitmap of the split's keys (attention mask and held-slot test
+    // valid & pos <= cur), one key per thread, packed by wave ballots.
+    __shared__ uint32_t sm_bits[kMaxBitmapKeys / 32];
+    const bool use_bits = (a.mask != nullptr) || (a.held_len > key_begin);
+    if (use_bits) {
+      const int64_t cur = a.cur_pos ? *a.cur_pos : INT64_MAX;
+      const uint8_t* mrow = a.mask ? a.mask + b * a.mask_sb : nullptr;
+      const int nkeys = key_end - key_begin;
+      for (int base = 0; base < nkeys; base += 64 * NW) {
+        const int rel = base + (int)threadIdx.x;
+        const int key = key_begin + rel;
+        bool kp = rel < nkeys;
+        if (kp && mrow) kp = mrow[key] != 0;
+        if (kp && key < a.held_len)
+          kp = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key] != 0 &&
+               a.held_pos[b * a.hp_sb + hk * a.hp_sh + key] <= cur;
+        const unsigned long long m = __ballot(kp);
+        if (lane < 2) sm_bits[((base + 64 * wave) >> 5) + lane] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
+      }
+      // LDS-only fences: the barrier does not wait for the ring's K/V loads.
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
-    for (int i = 0; i < NBUF - 1; ++i)
-      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * 16, key_begin, wend, col, grp, bits);
-
-    QFrag<T, D> qf;
-    const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
-    qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
+      for (int i = 0; i < NBUF - 1; ++i) r[i].keep &= tile_keep_bits(first + i * 16, key_begin, grp, sm_bits);
+    }
+    const uint32_t* bits = use_bits ? sm_bits : nullptr;
     float* srow = EVICT ? a.scores + ((int64_t)b * a.Hq + hk * G + min(col, G - 1)) * a.S : nullptr;
 
     // Step t issues the loads of tile t + NBUF - 1 (past the range: no memory
