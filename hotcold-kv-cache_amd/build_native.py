@@ -2,9 +2,10 @@
 
     python hotcold-kv-cache_amd/build_native.py [--jobs N]
 
-Compiles every csrc/*.hip for gfx950 with hipcc (one object per file, in
-parallel) and links hotcold_kv/_lib/libhotcold_hip.so.  No torch involvement:
-the library's ABI is plain C (include/hotcold_hip.h).
+Compiles every csrc/*.hip for gfx950 with hipcc and every csrc/*.cpp (host
+code: the cold store) with g++, one object per file, in parallel, and links
+hotcold_kv/_lib/libhotcold_hip.so.  No torch involvement: the library's ABI
+is plain C (include/hotcold_hip.h).
 """
 
 import argparse
@@ -53,20 +54,29 @@ def hipcc():
     return exe
 
 
+# Host C++ (no device code).  AVX2 for the cold-store scans; floating-point
+# contraction off so the fp64 search arithmetic is the written sequence.
+CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-mavx2", "-ffp-contract=off", "-Wall", f"-I{INCLUDE}",
+             f"-I{CSRC}"]
+
+
 def _compile(src, obj):
-    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
+    if src.endswith(".cpp"):
+        cmd = [shutil.which("g++") or "g++", *CXX_FLAGS, "-c", src, "-o", obj]
+    else:
+        cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in r.stderr.splitlines() if "packed-fp32-ops" not in l and "--hip-link" not in l)
     if r.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {os.path.basename(src)}:\n{errs}")
+        raise RuntimeError(f"compile failed for {os.path.basename(src)}:\n{errs}")
     return errs
 
 
 def build(jobs=None, verbose=True):
     os.makedirs(OUT_DIR, exist_ok=True)
     os.makedirs(OBJ_DIR, exist_ok=True)
-    srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip"))
-    objs = [os.path.join(OBJ_DIR, s[:-4] + ".o") for s in srcs]
+    srcs = sorted(f for f in os.listdir(CSRC) if f.endswith(".hip") or f.endswith(".cpp"))
+    objs = [os.path.join(OBJ_DIR, os.path.splitext(s)[0] + ".o") for s in srcs]
     jobs = jobs or min(8, os.cpu_count() or 4, len(srcs))
     with cf.ThreadPoolExecutor(max_workers=jobs) as ex:
         futs = {ex.submit(_compile, os.path.join(CSRC, s), o): s for s, o in zip(srcs, objs)}
@@ -76,7 +86,7 @@ def build(jobs=None, verbose=True):
                 print(f"[build] {futs[f]}:\n{warn}", file=sys.stderr)
     out = os.path.join(OUT_DIR, LIB_NAME)
     tmp = out + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp,
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp,
            "-Wl,-rpath,/opt/rocm/lib"]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:

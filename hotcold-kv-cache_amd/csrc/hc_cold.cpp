@@ -1,0 +1,328 @@
+// Host cold store: one ring of evicted tokens per (layer, batch row) with an
+// exact inner-product search (src/hotcold_kv/controller.py:166-293, which
+// keeps Python deques of tensors and a faiss.IndexFlatIP per ring).
+//
+// Contract (the oracle in oracle/reference.py restates it):
+//   * A token carries its pre-RoPE key and value ([heads][head_dim] fp32),
+//     its absolute position, and vec_heads search vectors of vec_dim fp32:
+//     the mean over the heads of the pre-RoPE key (vec_heads == 1,
+//     controller.py:190-194) or each head's key (vec_heads == heads), padded
+//     with zeros or cropped to vec_dim, then divided by max(||x||, 1e-12).
+//     The mean and the norm accumulate in fp64 in index order; the quotient
+//     is rounded to fp32.
+//   * Inner products accumulate in fp64 in dimension order.  fp32 x fp32
+//     products are exact in fp64, so every implementation that adds them in
+//     that order gets the same bits.
+//   * Ranking: larger inner product first, ties to the older token (lower
+//     logical index; logical index 0 is the oldest live token).
+//   * A full ring overwrites its oldest token; a batch larger than the ring
+//     keeps its last `capacity` tokens (controller.py:219-232).
+//
+// Storage is one uninitialised allocation per array at full capacity, so host
+// pages are touched only as tokens arrive and never copied on growth.  Search
+// vectors are kept dimension-major ([vec_head][dim][slot]) so the scan over
+// slots is a contiguous, vectorisable loop per dimension.  Large adds fill
+// their (distinct) slots on host threads.  Each store has a reader/writer
+// lock: adds exclude searches, searches run concurrently.
+
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include <algorithm>
+#include <atomic>
+#include <cmath>
+#include <mutex>
+#include <shared_mutex>
+#include <thread>
+#include <vector>
+
+#include "hotcold_hip.h"
+
+namespace hc {
+int set_error(int code, const char* fmt, ...);
+}
+
+namespace {
+
+// Uninitialised host array: pages are touched only when tokens land in them.
+template <typename T>
+struct RawArray {
+  T* p = nullptr;
+  void reset(size_t n) {
+    free(p);
+    p = static_cast<T*>(malloc(n * sizeof(T)));
+  }
+  ~RawArray() { free(p); }
+  T& operator[](size_t i) { return p[i]; }
+  const T& operator[](size_t i) const { return p[i]; }
+};
+
+struct ColdStore {
+  int64_t cap, H, D, VD, VH;
+  bool normalize;
+  int64_t size = 0;  // live tokens
+  int64_t head = 0;  // physical slot of the next write once full
+  RawArray<float> kpre, v;  // [slot][H][D]
+  RawArray<int64_t> pos;    // [slot]
+  RawArray<float> vec;      // [VH][VD][cap]
+  mutable std::shared_mutex mu;
+
+  bool allocate() {
+    kpre.reset((size_t)cap * H * D);
+    v.reset((size_t)cap * H * D);
+    pos.reset((size_t)cap);
+    vec.reset((size_t)VH * VD * cap);
+    return kpre.p && v.p && pos.p && vec.p;
+  }
+
+  int64_t physical(int64_t logical) const {
+    return size < cap ? logical : (head + logical) % cap;
+  }
+
+  // Search vector(s) of the token in `slot` (its key already stored).
+  void set_vec(int64_t slot) {
+    const float* kp = &kpre[(size_t)slot * H * D];
+    double x[4096];
+    const int64_t n = std::min(D, VD);
+    for (int64_t vh = 0; vh < VH; ++vh) {
+      if (VH == 1) {
+        // head mean: fp64, heads added in order (vectorised across dims)
+        for (int64_t d = 0; d < n; ++d) x[d] = 0.0;
+        for (int64_t h = 0; h < H; ++h)
+          for (int64_t d = 0; d < n; ++d) x[d] += (double)kp[h * D + d];
+        for (int64_t d = 0; d < n; ++d) x[d] = x[d] / (double)H;
+      } else {
+        for (int64_t d = 0; d < n; ++d) x[d] = (double)kp[vh * D + d];
+      }
+      for (int64_t d = n; d < VD; ++d) x[d] = 0.0;
+      double den = 1.0;
+      if (normalize) {
+        double ss = 0.0;
+        for (int64_t d = 0; d < VD; ++d) ss += x[d] * x[d];
+        den = std::max(std::sqrt(ss), 1e-12);
+      }
+      float* col = &vec[(size_t)vh * VD * cap + slot];
+      for (int64_t d = 0; d < VD; ++d) col[(size_t)d * cap] = (float)(x[d] / den);
+    }
+  }
+
+  void copy_in(int64_t slot, const float* kp, int64_t k_sh, const float* vv, int64_t v_sh, int64_t p) {
+    float* kd = &kpre[(size_t)slot * H * D];
+    float* vd = &v[(size_t)slot * H * D];
+    for (int64_t h = 0; h < H; ++h) {
+      memcpy(kd + h * D, kp + h * k_sh, sizeof(float) * D);
+      memcpy(vd + h * D, vv + h * v_sh, sizeof(float) * D);
+    }
+    pos[slot] = p;
+    set_vec(slot);
+  }
+
+  // Slot for the next token (advances the ring).
+  int64_t next_slot() {
+    if (size < cap) return size++;
+    const int64_t s = head;
+    head = (head + 1) % cap;
+    return s;
+  }
+
+  // Inner products of query q with the vectors of head vh over physical
+  // slots [s0, s1): fp64, dimensions in order.
+  void scan(const float* q, int64_t vh, int64_t s0, int64_t s1, double* ip) const {
+    for (int64_t s = s0; s < s1; ++s) ip[s] = 0.0;
+    for (int64_t d = 0; d < VD; ++d) {
+      const double qd = (double)q[d];
+      const float* col = &vec[((size_t)vh * VD + d) * cap];
+      for (int64_t s = s0; s < s1; ++s) ip[s] += (double)col[s] * qd;
+    }
+  }
+
+  // Top-r logical indices by (ip desc, logical asc).
+  int64_t select(const double* ip, int64_t r, int64_t* out) const {
+    const int64_t n = size;
+    r = std::min(r, n);
+    if (r <= 0) return 0;
+    std::vector<int64_t> idx((size_t)n);
+    for (int64_t i = 0; i < n; ++i) idx[i] = i;
+    const auto better = [&](int64_t a, int64_t b) {
+      const double x = ip[physical(a)], y = ip[physical(b)];
+      return x > y || (x == y && a < b);
+    };
+    if (r < n) std::nth_element(idx.begin(), idx.begin() + r, idx.end(), better);
+    std::sort(idx.begin(), idx.begin() + r, better);
+    memcpy(out, idx.data(), sizeof(int64_t) * r);
+    return r;
+  }
+};
+
+ColdStore* as_store(void* p) { return reinterpret_cast<ColdStore*>(p); }
+
+int threads_for(int64_t requested, int64_t tasks) {
+  int64_t hw = (int64_t)std::thread::hardware_concurrency();
+  if (hw <= 0) hw = 1;
+  int64_t n = requested > 0 ? requested : std::min<int64_t>(hw, 16);
+  return (int)std::max<int64_t>(1, std::min(n, tasks));
+}
+
+// Run f(i) for i in [0, n) on up to `nthreads` threads.
+template <typename F>
+void parallel_for(int64_t n, int nthreads, F f) {
+  if (nthreads <= 1 || n <= 1) {
+    for (int64_t i = 0; i < n; ++i) f(i);
+    return;
+  }
+  std::atomic<int64_t> next{0};
+  std::vector<std::thread> pool;
+  pool.reserve(nthreads - 1);
+  const auto work = [&]() {
+    for (int64_t i = next.fetch_add(1); i < n; i = next.fetch_add(1)) f(i);
+  };
+  for (int t = 1; t < nthreads; ++t) pool.emplace_back(work);
+  work();
+  for (auto& th : pool) th.join();
+}
+
+}  // namespace
+
+using hc::set_error;
+
+extern "C" void* hc_cold_create(int64_t capacity, int64_t heads, int64_t head_dim, int64_t vec_dim,
+                                int64_t vec_heads, int normalize) {
+  if (capacity <= 0 || heads <= 0 || head_dim <= 0 || vec_dim <= 0 || (vec_heads != 1 && vec_heads != heads)) {
+    set_error(HC_ERR_INVALID, "cold_create: bad sizes capacity=%lld heads=%lld head_dim=%lld vec_dim=%lld "
+              "vec_heads=%lld", (long long)capacity, (long long)heads, (long long)head_dim, (long long)vec_dim,
+              (long long)vec_heads);
+    return nullptr;
+  }
+  if (vec_dim > 4096) {
+    set_error(HC_ERR_INVALID, "cold_create: vec_dim %lld above 4096", (long long)vec_dim);
+    return nullptr;
+  }
+  ColdStore* s = new ColdStore();
+  s->cap = capacity;
+  s->H = heads;
+  s->D = head_dim;
+  s->VD = vec_dim;
+  s->VH = vec_heads;
+  s->normalize = normalize != 0;
+  if (!s->allocate()) {
+    delete s;
+    set_error(HC_ERR_INVALID, "cold_create: out of host memory for %lld tokens", (long long)capacity);
+    return nullptr;
+  }
+  return s;
+}
+
+extern "C" void hc_cold_destroy(void* store) { delete as_store(store); }
+
+extern "C" int64_t hc_cold_size(const void* store) {
+  const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
+  if (!s) return 0;
+  std::shared_lock<std::shared_mutex> lk(s->mu);
+  return s->size;
+}
+
+extern "C" int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
+                           const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos,
+                           const int64_t* evicted_idx) {
+  ColdStore* s = as_store(store);
+  if (!s) return set_error(HC_ERR_INVALID, "cold_add: null store");
+  if (te < 0 || (te > 0 && (!kpre || !v || !pos))) return set_error(HC_ERR_INVALID, "cold_add: bad arguments");
+  // tokens kept: evicted_idx[t] >= 0 (datatypes.py:58-63 pads with -1)
+  std::vector<int64_t> sel;
+  sel.reserve((size_t)te);
+  for (int64_t t = 0; t < te; ++t)
+    if (!evicted_idx || evicted_idx[t] >= 0) sel.push_back(t);
+  const int64_t m = (int64_t)sel.size();
+  const int64_t first = m > s->cap ? m - s->cap : 0;  // only the last cap tokens survive
+  std::unique_lock<std::shared_mutex> lk(s->mu);
+  std::vector<int64_t> slot((size_t)(m - first));
+  for (int64_t i = first; i < m; ++i) slot[i - first] = s->next_slot();
+  // distinct slots: the copies and search vectors run on host threads
+  constexpr int64_t kChunk = 256;
+  const int64_t nchunks = (m - first + kChunk - 1) / kChunk;
+  parallel_for(nchunks, threads_for(0, nchunks), [&](int64_t c) {
+    const int64_t i1 = std::min(m, first + (c + 1) * kChunk);
+    for (int64_t i = first + c * kChunk; i < i1; ++i) {
+      const int64_t t = sel[i];
+      s->copy_in(slot[i - first], kpre + t * k_st, k_sh, v + t * v_st, v_sh, pos[t]);
+    }
+  });
+  return HC_OK;
+}
+
+extern "C" int hc_cold_search(const void* store, const float* q, int64_t r, int64_t head, int64_t* out,
+                              int64_t* n_out) {
+  const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
+  if (!s || !q || !out || !n_out) return set_error(HC_ERR_INVALID, "cold_search: null argument");
+  if (head < 0 || head >= s->VH) return set_error(HC_ERR_INVALID, "cold_search: head %lld out of range", (long long)head);
+  std::shared_lock<std::shared_mutex> lk(s->mu);
+  std::vector<double> ip((size_t)std::max<int64_t>(s->size, 1));
+  s->scan(q, head, 0, s->size, ip.data());
+  *n_out = s->select(ip.data(), r, out);
+  return HC_OK;
+}
+
+extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t* pos, float* vec) {
+  const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
+  if (!s) return set_error(HC_ERR_INVALID, "cold_export: null store");
+  std::shared_lock<std::shared_mutex> lk(s->mu);
+  const int64_t HD = s->H * s->D;
+  for (int64_t i = 0; i < s->size; ++i) {
+    const int64_t p = s->physical(i);
+    if (kpre) memcpy(kpre + i * HD, &s->kpre[(size_t)p * HD], sizeof(float) * HD);
+    if (v) memcpy(v + i * HD, &s->v[(size_t)p * HD], sizeof(float) * HD);
+    if (pos) pos[i] = s->pos[p];
+    if (vec)
+      for (int64_t h = 0; h < s->VH; ++h)
+        for (int64_t d = 0; d < s->VD; ++d)
+          vec[(i * s->VH + h) * s->VD + d] = s->vec[((size_t)h * s->VD + d) * s->cap + p];
+  }
+  return HC_OK;
+}
+
+extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
+                                int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
+                                uint8_t* valid_out, int64_t nthreads) {
+  if (B <= 0 || R <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out)
+    return set_error(HC_ERR_INVALID, "cold_retrieve: bad arguments");
+  const ColdStore* s0 = reinterpret_cast<const ColdStore*>(stores[0]);
+  if (!s0) return set_error(HC_ERR_INVALID, "cold_retrieve: null store");
+  const int64_t H = s0->H, D = s0->D;
+  for (int64_t b = 0; b < B; ++b) {
+    const ColdStore* s = reinterpret_cast<const ColdStore*>(stores[b]);
+    if (!s || s->H != H || s->D != D || s->VD != s0->VD || s->VH != (per_head ? H : 1))
+      return set_error(HC_ERR_INVALID, "cold_retrieve: store %lld does not match (per_head=%d)", (long long)b,
+                       per_head);
+  }
+  const int64_t VH = per_head ? H : 1;
+  // outputs: kpre/v [B][H][R][D]; pos/valid [B][R] or [B][H][R]; zero-filled
+  memset(kpre_out, 0, sizeof(float) * B * H * R * D);
+  memset(v_out, 0, sizeof(float) * B * H * R * D);
+  memset(pos_out, 0, sizeof(int64_t) * B * VH * R);
+  memset(valid_out, 0, (size_t)(B * VH * R));
+  const int64_t tasks = B * VH;
+  parallel_for(tasks, threads_for(nthreads, tasks), [&](int64_t task) {
+    const int64_t b = task / VH, h = task % VH;
+    const ColdStore* s = reinterpret_cast<const ColdStore*>(stores[b]);
+    std::shared_lock<std::shared_mutex> lk(s->mu);
+    if (s->size == 0) return;
+    std::vector<double> ip((size_t)s->size);
+    std::vector<int64_t> hits((size_t)R);
+    s->scan(q + b * q_sb + h * q_sh, h, 0, s->size, ip.data());
+    const int64_t m = s->select(ip.data(), R, hits.data());
+    for (int64_t j = 0; j < m; ++j) {
+      const int64_t p = s->physical(hits[j]);
+      const float* kp = &s->kpre[(size_t)p * H * D];
+      const float* vp = &s->v[(size_t)p * H * D];
+      const int64_t h0 = per_head ? h : 0, h1 = per_head ? h + 1 : H;
+      for (int64_t hh = h0; hh < h1; ++hh) {
+        memcpy(kpre_out + ((b * H + hh) * R + j) * D, kp + hh * D, sizeof(float) * D);
+        memcpy(v_out + ((b * H + hh) * R + j) * D, vp + hh * D, sizeof(float) * D);
+      }
+      pos_out[(b * VH + h) * R + j] = s->pos[p];
+      valid_out[(b * VH + h) * R + j] = 1;
+    }
+  });
+  return HC_OK;
+}

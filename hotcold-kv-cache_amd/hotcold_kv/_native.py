@@ -122,6 +122,14 @@ SIGNATURES = {
     "hc_stream_wait_event": (_int, [_vp, _vp]),
     "hc_memcpy_h2d_async": (_int, [_vp, _vp, _i64, _vp]),
     "hc_memcpy_d2h_async": (_int, [_vp, _vp, _i64, _vp]),
+    # host cold store
+    "hc_cold_create": (_vp, [_i64, _i64, _i64, _i64, _i64, _int]),
+    "hc_cold_destroy": (None, [_vp]),
+    "hc_cold_size": (_i64, [_vp]),
+    "hc_cold_add": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp]),
+    "hc_cold_search": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
+    "hc_cold_export": (_int, [_vp, _vp, _vp, _vp, _vp]),
+    "hc_cold_retrieve": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _vp, _vp, _vp, _vp, _i64]),
 }
 
 

@@ -1,14 +1,17 @@
 """KVController: cold store, look-ahead retrieval scheduling and the staged
 host-to-device feed of the inject path (src/hotcold_kv/controller.py).
 
-Cold store (controller.py:121-293).  One ring per (layer, batch row) of
-cpu_buffer_size evicted tokens (pre-RoPE keys and values in fp32, absolute
-positions) with an exact inner-product search over the head-mean,
+Cold store (controller.py:121-293).  One native store per (layer, batch
+row) of cpu_buffer_size evicted tokens (pre-RoPE keys and values in fp32,
+absolute positions) with an exact inner-product search over the head-mean,
 pad/crop-to-faiss_dim, L2-normalised pre-RoPE key -- the same vectors the
-reference puts in a faiss.IndexFlatIP.  Ring slot order is the index order
-(oldest first); the search ranks by inner product, ties to the older slot.
-With per_head_retrieval=True the search runs per KV head (one vector per
-token and head) and positions become (B,Hk,R).
+reference puts in a faiss.IndexFlatIP.  The store, its search and the
+retrieval gather are host C++ in the library (hc_cold_*): adds and searches
+run without the GIL, a retrieval runs all batch rows (and heads) on host
+threads.  Logical order is oldest first; the search ranks by inner product
+(fp64, accumulated in dimension order), ties to the older token.  With
+per_head_retrieval=True the search runs per KV head (one vector per token
+and head) and positions become (B,Hk,R).
 
 Staging (controller.py:344-442).  A retrieval result lives in pinned host
 buffers; maybe_prefetch_to_gpu copies them with hipMemcpyAsync on a
@@ -20,6 +23,7 @@ referenced until their copy is known complete.
 """
 
 import ctypes
+import math
 import threading
 from collections import deque
 
@@ -31,57 +35,61 @@ from .datatypes import EvictedKV, RetrievedKV, _canon_br_2d, _canon_kv_4d
 
 
 class _Ring:
-    """Fixed-capacity ring of evicted tokens of one (layer, batch row)."""
+    """Native cold store of one (layer, batch row) (hc_cold_*)."""
 
-    def __init__(self, capacity, heads, head_dim, vec_dim, vec_heads):
-        self.cap = int(capacity)
-        self.kpre = np.zeros((self.cap, heads, head_dim), dtype=np.float32)
-        self.v = np.zeros((self.cap, heads, head_dim), dtype=np.float32)
-        self.pos = np.zeros((self.cap,), dtype=np.int64)
-        self.vec = np.zeros((self.cap, vec_heads, vec_dim), dtype=np.float32)
-        self.count = 0
-        self.head = 0  # next physical slot to write
+    def __init__(self, capacity, heads, head_dim, vec_dim, vec_heads, normalize=True):
+        self.cap, self.H, self.D = int(capacity), int(heads), int(head_dim)
+        self.vec_dim, self.vec_heads = int(vec_dim), int(vec_heads)
+        self._lib = N.lib()
+        self.handle = self._lib.hc_cold_create(self.cap, self.H, self.D, self.vec_dim, self.vec_heads,
+                                               int(bool(normalize)))
+        if not self.handle:
+            N.check(N.HC_ERR_INVALID, "hc_cold_create")
+
+    def __del__(self):
+        h, self.handle = getattr(self, "handle", None), None
+        if h:
+            self._lib.hc_cold_destroy(h)
 
     def __len__(self):
-        return self.count
+        return int(self._lib.hc_cold_size(self.handle))
 
     @property
     def ntotal(self):
         """Vectors in the search index (faiss.Index.ntotal of the reference)."""
-        return self.count
+        return len(self)
 
-    def append(self, kpre, v, pos, vec):
-        m = kpre.shape[0]
-        if m > self.cap:  # only the last cap tokens survive
-            kpre, v, pos, vec = kpre[-self.cap:], v[-self.cap:], pos[-self.cap:], vec[-self.cap:]
-            m = self.cap
-        first = min(m, self.cap - self.head)
-        for dst, src in ((self.kpre, kpre), (self.v, v), (self.pos, pos), (self.vec, vec)):
-            dst[self.head:self.head + first] = src[:first]
-            if m > first:
-                dst[:m - first] = src[first:]
-        self.head = (self.head + m) % self.cap
-        self.count = min(self.cap, self.count + m)
-
-    def logical_to_physical(self, idx):
-        start = (self.head - self.count) % self.cap
-        return (start + np.asarray(idx)) % self.cap
-
-    def ordered(self, arr):
-        """arr rows in logical order (oldest first)."""
-        return arr[self.logical_to_physical(np.arange(self.count))]
+    def add(self, kpre, v, pos, evicted_idx=None):
+        """Tokens t with evicted_idx[t] >= 0 of kpre/v (H,Te,D) fp32, pos (Te,)."""
+        kpre = np.ascontiguousarray(kpre, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        pos = np.ascontiguousarray(pos, dtype=np.int64)
+        te = int(kpre.shape[1])
+        idx = None if evicted_idx is None else np.ascontiguousarray(evicted_idx, dtype=np.int64)
+        rc = self._lib.hc_cold_add(self.handle, te, kpre.ctypes.data, te * self.D, self.D,
+                                   v.ctypes.data, te * self.D, self.D, pos.ctypes.data,
+                                   None if idx is None else idx.ctypes.data)
+        N.check(rc, "hc_cold_add")
 
     def search(self, q, r, head=0):
         """Logical indices of the top-r inner products with q (descending,
-        ties to the older slot)."""
-        n = self.count
-        if n == 0 or r <= 0:
-            return np.zeros((0,), dtype=np.int64)
-        keys = self.ordered(self.vec[:, head, :])
-        ip = keys @ q.astype(np.float32)
-        r = min(r, n)
-        order = np.argsort(-ip.astype(np.float64), kind="stable")
-        return order[:r]
+        ties to the older token)."""
+        q = np.ascontiguousarray(q, dtype=np.float32)
+        out = np.zeros((max(int(r), 0),), dtype=np.int64)
+        n = ctypes.c_int64()
+        N.check(self._lib.hc_cold_search(self.handle, q.ctypes.data, int(r), int(head), out.ctypes.data,
+                                         ctypes.byref(n)), "hc_cold_search")
+        return out[: n.value]
+
+    def export(self):
+        """The store in logical order (oldest first): kpre/v (n,H,D), pos (n,),
+        vec (n,vec_heads,vec_dim)."""
+        n = len(self)
+        d = {"kpre": np.zeros((n, self.H, self.D), np.float32), "v": np.zeros((n, self.H, self.D), np.float32),
+             "pos": np.zeros((n,), np.int64), "vec": np.zeros((n, self.vec_heads, self.vec_dim), np.float32)}
+        N.check(self._lib.hc_cold_export(self.handle, d["kpre"].ctypes.data, d["v"].ctypes.data,
+                                         d["pos"].ctypes.data, d["vec"].ctypes.data), "hc_cold_export")
+        return d
 
 
 class KVController:
@@ -126,7 +134,6 @@ class KVController:
         self._inited = False
         self.B = self.Hk = self.D = self.n_layers = None
         self.rings = []
-        self.ring_lock = []
         self.step_count = []
         self.query_window = []
         self._retrieval_thread = []
@@ -169,9 +176,8 @@ class KVController:
         self.B, self.Hk, self.D = int(B), int(Hk), int(D)
         self.n_layers = L = int(n_layers)
         vec_heads = self.Hk if self.per_head_retrieval else 1
-        self.rings = [[_Ring(self.cpu_buffer_size, self.Hk, self.D, self.faiss_dim, vec_heads) for _ in range(B)]
-                      for _ in range(L)]
-        self.ring_lock = [[threading.RLock() for _ in range(B)] for _ in range(L)]
+        self.rings = [[_Ring(self.cpu_buffer_size, self.Hk, self.D, self.faiss_dim, vec_heads,
+                             self.normalize_for_ip) for _ in range(B)] for _ in range(L)]
         self.step_count = [0] * L
         self.query_window = [deque(maxlen=self.query_pool_size) for _ in range(L)]
         self._retrieval_thread = [None] * L
@@ -225,11 +231,30 @@ class KVController:
         return (x / np.maximum(n, 1e-12)).astype(np.float32)
 
     def _k_token_to_vec_np(self, kpre_token):
-        """(Hk,D) pre-RoPE key of one token -> its search vector(s)."""
+        """(Hk,D) pre-RoPE key of one token -> its search vector(s), computed
+        as the native store computes them: head mean (or each head) in fp64
+        accumulated in head order, pad/crop, norm accumulated in dimension
+        order, quotient rounded to fp32 -- bit-equal to the stored vector."""
         k = np.asarray(kpre_token.detach().cpu().float() if isinstance(kpre_token, torch.Tensor) else kpre_token,
                        dtype=np.float32)
-        v = k if self.per_head_retrieval else k.mean(axis=0)
-        return self._normalize(self._pad_or_crop(v))
+        if self.per_head_retrieval:
+            rows = [k[h].astype(np.float64) for h in range(k.shape[0])]
+        else:
+            acc = np.zeros(k.shape[-1], dtype=np.float64)
+            for h in range(k.shape[0]):
+                acc = acc + k[h].astype(np.float64)
+            rows = [acc / float(k.shape[0])]
+        out = []
+        for x in rows:
+            x = self._pad_or_crop(x)
+            den = 1.0
+            if self.normalize_for_ip:
+                ss = 0.0
+                for t in x.tolist():
+                    ss += t * t
+                den = max(math.sqrt(ss), 1e-12)
+            out.append((x / den).astype(np.float32))
+        return out[0] if not self.per_head_retrieval else np.stack(out)
 
     def _q_to_vecs_np(self, q_pre):
         """(B,Hq,T,D) pre-RoPE queries -> (B,faiss_dim), or (B,Hk,faiss_dim)
@@ -248,25 +273,18 @@ class KVController:
         if not self._inited:
             raise RuntimeError("KVController not initialized")
         li = int(layer_idx)
-        kpre = ev.k_pre_cpu.detach().cpu().float().numpy()
-        vv = ev.v_cpu.detach().cpu().float().numpy()
-        pos = ev.pos_cpu.detach().cpu().numpy().astype(np.int64)
-        idx = ev.evicted_idx.detach().cpu().numpy()
-        B = kpre.shape[0]
-        for b in range(B):
-            sel = np.nonzero(idx[b] >= 0)[0]
-            if sel.size == 0:
+        kpre = ev.k_pre_cpu.detach().cpu().float().contiguous().numpy()      # (B,Hk,Te,D)
+        vv = ev.v_cpu.detach().cpu().float().contiguous().numpy()
+        pos = ev.pos_cpu.detach().cpu().contiguous().numpy().astype(np.int64)
+        idx = ev.evicted_idx.detach().cpu().contiguous().numpy().astype(np.int64)
+        for b in range(kpre.shape[0]):
+            kept = int((idx[b] >= 0).sum())
+            if kept == 0:
                 continue
-            k_tok = np.ascontiguousarray(kpre[b][:, sel, :].transpose(1, 0, 2))   # (m,Hk,D)
-            v_tok = np.ascontiguousarray(vv[b][:, sel, :].transpose(1, 0, 2))
-            p_tok = pos[b][sel]
-            src = k_tok if self.per_head_retrieval else k_tok.mean(axis=1, keepdims=True)
-            vec = self._normalize(self._pad_or_crop(src))                           # (m,vh,faiss_dim)
-            with self.ring_lock[li][b]:
-                self.rings[li][b].append(k_tok, v_tok, p_tok, vec)
-                self.dbg["faiss_add"] += min(int(sel.size), self.cpu_buffer_size)
-                if self.enable_asserts:
-                    assert len(self.rings[li][b]) <= self.cpu_buffer_size
+            self.rings[li][b].add(kpre[b], vv[b], pos[b], idx[b])
+            self.dbg["faiss_add"] += min(kept, self.cpu_buffer_size)
+            if self.enable_asserts:
+                assert len(self.rings[li][b]) <= self.cpu_buffer_size
 
     # -- query pooling / retrieval -----------------------------------------------------
     def update_query_window(self, layer_idx, q_pre):
@@ -279,44 +297,25 @@ class KVController:
         return self._q_to_vecs_np(torch.cat(list(qwin), dim=2))
 
     def _retrieval_worker(self, layer_idx, q_vecs):
+        """Top-lookahead_k tokens per batch row (or per KV head) into pinned
+        host buffers (controller.py:250-293), one native call over all rows."""
         li = int(layer_idx)
         if not self._inited:
             return
         B, Hk, D, R = self.B, self.Hk, self.D, self.lookahead_k
         pin = torch.cuda.is_available()
-        kpre = torch.zeros((B, Hk, R, D), dtype=torch.float32, pin_memory=pin)
-        vv = torch.zeros((B, Hk, R, D), dtype=torch.float32, pin_memory=pin)
+        kpre = torch.empty((B, Hk, R, D), dtype=torch.float32, pin_memory=pin)
+        vv = torch.empty((B, Hk, R, D), dtype=torch.float32, pin_memory=pin)
         pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
-        pos = torch.zeros(pshape, dtype=torch.int64, pin_memory=pin)
-        valid = torch.zeros(pshape, dtype=torch.bool, pin_memory=pin)
-        kn, vn, pn, valn = kpre.numpy(), vv.numpy(), pos.numpy(), valid.numpy()
-        any_valid = False
-        for b in range(B):
-            with self.ring_lock[li][b]:
-                ring = self.rings[li][b]
-                if len(ring) == 0:
-                    continue
-                if self.per_head_retrieval:
-                    for h in range(Hk):
-                        hits = ring.search(q_vecs[b, h], R, head=h)
-                        phys = ring.logical_to_physical(hits)
-                        m = hits.size
-                        kn[b, h, :m] = ring.kpre[phys, h]
-                        vn[b, h, :m] = ring.v[phys, h]
-                        pn[b, h, :m] = ring.pos[phys]
-                        valn[b, h, :m] = True
-                        any_valid |= m > 0
-                else:
-                    hits = ring.search(q_vecs[b], R)
-                    phys = ring.logical_to_physical(hits)
-                    m = hits.size
-                    kn[b, :, :m] = ring.kpre[phys].transpose(1, 0, 2)
-                    vn[b, :, :m] = ring.v[phys].transpose(1, 0, 2)
-                    pn[b, :m] = ring.pos[phys]
-                    valn[b, :m] = True
-                    any_valid |= m > 0
+        pos = torch.empty(pshape, dtype=torch.int64, pin_memory=pin)
+        valid = torch.empty(pshape, dtype=torch.bool, pin_memory=pin)
+        q = np.ascontiguousarray(q_vecs, dtype=np.float32).reshape(B, -1, self.faiss_dim)
+        stores = (ctypes.c_void_p * B)(*[self.rings[li][b].handle for b in range(B)])
+        N.check(N.lib().hc_cold_retrieve(stores, B, q.ctypes.data, q.shape[1] * self.faiss_dim, self.faiss_dim, R,
+                                         int(self.per_head_retrieval), kpre.data_ptr(), vv.data_ptr(),
+                                         pos.data_ptr(), valid.data_ptr(), 0), "hc_cold_retrieve")
         with self._retrieval_lock[li]:
-            if not any_valid:
+            if not bool(valid.any()):
                 self._retrieval_ready_cpu[li] = None
                 self.dbg["retrieval_ready_empty"] += 1
                 return

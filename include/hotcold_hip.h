@@ -237,6 +237,49 @@ int hc_stream_wait_event(void* stream, void* event);
 int hc_memcpy_h2d_async(void* dst, const void* src, int64_t bytes, void* stream);
 int hc_memcpy_d2h_async(void* dst, const void* src, int64_t bytes, void* stream);
 
+/*
+ * Host cold store (host memory, host threads; no device calls).  One store
+ * per (layer, batch row) replaces the reference's ring of token tensors plus
+ * faiss.IndexFlatIP (controller.py:121-293):
+ *   - hc_cold_add        add_evicted_to_cold_store (controller.py:199-238)
+ *   - hc_cold_retrieve   one layer's retrieval over B stores (_retrieval_worker,
+ *                        controller.py:250-293), run on host threads
+ *   - hc_cold_search     index.search for one query (controller.py:274)
+ *   - hc_cold_size       len(cpu_kpre_ring[l][b]) == index.ntotal
+ *   - hc_cold_export     the ring in logical order (oldest first), for checks
+ * Tokens hold fp32 pre-RoPE key and value [heads][head_dim], an int64
+ * position, and vec_heads search vectors of vec_dim floats: the head mean
+ * (vec_heads == 1) or each head's key (vec_heads == heads), padded/cropped to
+ * vec_dim and divided by max(||x||, 1e-12) (normalize != 0), accumulated in
+ * fp64 in index order.  Inner products accumulate in fp64 in dimension order;
+ * ranking is descending, ties to the older token.  A full store overwrites its
+ * oldest token; an add larger than the store keeps its last tokens.  Adds
+ * exclude searches; searches run concurrently.  Returns 0 / HC_ERR_INVALID.
+ */
+void* hc_cold_create(int64_t capacity, int64_t heads, int64_t head_dim, int64_t vec_dim, int64_t vec_heads,
+                     int normalize);
+void hc_cold_destroy(void* store);
+int64_t hc_cold_size(const void* store);
+/* Tokens t < te with evicted_idx[t] >= 0 (evicted_idx may be NULL: all), from
+ * kpre/v [heads][te][head_dim] with element strides (k_sh, k_st), (v_sh, v_st)
+ * and pos[te] -- one batch row of EvictedKV (datatypes.py:58-63). */
+int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
+                const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos, const int64_t* evicted_idx);
+/* Top-r logical indices for query q [vec_dim] against search vector `head`;
+ * *n_out = min(r, size). */
+int hc_cold_search(const void* store, const float* q, int64_t r, int64_t head, int64_t* out, int64_t* n_out);
+/* Logical-order copies: kpre/v [size][heads][head_dim], pos [size],
+ * vec [size][vec_heads][vec_dim]; any pointer may be NULL. */
+int hc_cold_export(const void* store, float* kpre, float* v, int64_t* pos, float* vec);
+/* Retrieval of R tokens per batch row (per_head = 0: query q[b] of store b's
+ * head-mean vectors; outputs pos/valid [B][R]) or per (batch row, head)
+ * (per_head = 1: q[b][h]; pos/valid [B][heads][R]).  kpre/v out are
+ * [B][heads][R][head_dim]; rows past the hits are zero with valid = 0.  q has
+ * element strides (q_sb, q_sh).  nthreads <= 0 picks min(cores, 16). */
+int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh, int64_t R,
+                     int per_head, float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out,
+                     int64_t nthreads);
+
 #ifdef __cplusplus
 }
 #endif

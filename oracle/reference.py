@@ -370,41 +370,75 @@ def hotcold_compress(keys, values, pre_keys, positions, q_last, max_capacity, re
 # Cold store (controller.py:166-293), exact inner-product search
 # ---------------------------------------------------------------------------
 class ColdStore:
-    """Ring of evicted tokens per batch with exact IP search over the
-    head-mean, pad/crop, L2-normalised pre-RoPE key (controller.py:166-188,
-    190-238, 250-293).  Ties rank the lower ring slot first."""
+    """Ring of evicted tokens of one (layer, batch row) with exact inner-product
+    search (controller.py:166-188, 190-238, 250-293; the reference indexes the
+    vectors in a faiss.IndexFlatIP, whose last-bit arithmetic and tie order are
+    not pinned).  The contract the native store follows:
+      vector  head mean of the pre-RoPE key (or each head's key with
+              per_head=True), fp64 accumulated in head order, padded/cropped
+              to `dim`, divided by max(norm, 1e-12) with the norm's squares
+              accumulated in dimension order; rounded to fp32
+      search  inner product of the fp32 vector and fp32 query, fp64,
+              accumulated in dimension order; larger first, ties to the older
+              token; a full ring drops its oldest token."""
 
-    def __init__(self, capacity, dim, normalize=True):
-        self.capacity, self.dim, self.normalize = capacity, dim, normalize
-        self.kpre, self.v, self.pos = [], [], []
+    def __init__(self, capacity, dim, normalize=True, per_head=False):
+        self.capacity, self.dim, self.normalize, self.per_head = capacity, dim, normalize, per_head
+        self.kpre, self.v, self.pos, self.vec = [], [], [], []
 
-    def _vec(self, x):
-        x = np.asarray(x, dtype=np.float64)
-        if x.shape[-1] > self.dim:
-            x = x[..., : self.dim]
-        elif x.shape[-1] < self.dim:
-            x = np.pad(x, [(0, 0)] * (x.ndim - 1) + [(0, self.dim - x.shape[-1])])
-        if self.normalize:
-            n = np.linalg.norm(x, axis=-1, keepdims=True)
-            x = x / np.maximum(n, 1e-12)
-        return x
+    def token_vecs(self, kp):
+        """(H,D) fp32 pre-RoPE key -> (vec_heads, dim) fp32 search vectors."""
+        kp = np.asarray(kp, dtype=np.float32)
+        H = kp.shape[0]
+        if self.per_head:
+            rows = [kp[h].astype(np.float64) for h in range(H)]
+        else:
+            acc = np.zeros(kp.shape[1], dtype=np.float64)
+            for h in range(H):
+                acc = acc + kp[h].astype(np.float64)
+            rows = [acc / float(H)]
+        out = []
+        for x in rows:
+            if x.shape[0] > self.dim:
+                x = x[: self.dim]
+            elif x.shape[0] < self.dim:
+                x = np.concatenate([x, np.zeros(self.dim - x.shape[0])])
+            den = 1.0
+            if self.normalize:
+                ss = 0.0
+                for t in x.tolist():
+                    ss += t * t
+                den = max(math.sqrt(ss), 1e-12)
+            out.append((x / den).astype(np.float32))
+        return np.stack(out)
 
-    def add(self, kpre_tokens, v_tokens, positions):
-        for kp, vv, p in zip(kpre_tokens, v_tokens, positions):
+    def add(self, kpre_tokens, v_tokens, positions, evicted_idx=None):
+        """Tokens (n,H,D); those with evicted_idx < 0 are padding and skipped."""
+        for t, (kp, vv, p) in enumerate(zip(kpre_tokens, v_tokens, positions)):
+            if evicted_idx is not None and int(evicted_idx[t]) < 0:
+                continue
             self.kpre.append(np.asarray(kp, dtype=np.float32))
             self.v.append(np.asarray(vv, dtype=np.float32))
             self.pos.append(int(p))
+            self.vec.append(self.token_vecs(kp))
         over = len(self.kpre) - self.capacity
         if over > 0:
-            del self.kpre[:over], self.v[:over], self.pos[:over]
+            del self.kpre[:over], self.v[:over], self.pos[:over], self.vec[:over]
 
-    def search(self, q_vec, r):
+    def inner_products(self, q_vec, head=0):
         n = len(self.kpre)
-        if n == 0:
+        keys = np.stack([v[head] for v in self.vec]).astype(np.float64) if n else np.zeros((0, self.dim))
+        q = np.asarray(q_vec, dtype=np.float32).astype(np.float64)
+        ip = np.zeros(n)
+        for d in range(self.dim):
+            ip = ip + keys[:, d] * q[d]
+        return ip
+
+    def search(self, q_vec, r, head=0):
+        n = len(self.kpre)
+        if n == 0 or r <= 0:
             return []
-        keys = self._vec(np.stack([k.mean(axis=0) for k in self.kpre]))
-        q = self._vec(np.asarray(q_vec, dtype=np.float64)[None])[0]
-        ip = keys @ q
+        ip = self.inner_products(q_vec, head)
         order = np.argsort(-ip, kind="stable")[: min(r, n)]
         return [int(i) for i in order]
 

@@ -169,9 +169,9 @@ def test_hotcold_retrieval_injects_rerotated_keys():
         pos, valid, r = kv.held_mem[li]
         assert r == R and bool(valid.all())
         pos_cpu = pos.cpu()
-        ring = kv.rings[li][0]
-        ring_pos = ring.ordered(ring.pos)
-        ring_k = ring.ordered(ring.kpre)                                   # (n,Hk,D) fp32
+        snap = kv.rings[li][0].export()
+        ring_pos = snap["pos"]
+        ring_k = snap["kpre"]                                              # (n,Hk,D) fp32
         rows = [int((ring_pos == p).nonzero()[0][0]) for p in pos_cpu[0].tolist()]
         k_pre = torch.from_numpy(ring_k[rows]).permute(1, 0, 2).unsqueeze(0)  # (1,Hk,R,D)
         want = ref.rerope(k_pre, pos_cpu, rot.inv_freq.float().cpu(), float(rot.attention_scaling), dtype)
@@ -184,7 +184,7 @@ def test_hotcold_retrieval_injects_rerotated_keys():
         partner = torch.cat((k16[..., D // 2:], k16[..., :D // 2]), dim=-1)
         bound = 4 * torch.finfo(dtype).eps * (k16.abs() + partner.abs())
         assert ((got.float() - want.float()).abs() <= bound).all()
-        ring_v = torch.from_numpy(ring.ordered(ring.v)[rows]).permute(1, 0, 2).unsqueeze(0)
+        ring_v = torch.from_numpy(snap["v"][rows]).permute(1, 0, 2).unsqueeze(0)
         assert torch.equal(vbuf[:, :, layer.buf.held - R:layer.buf.held].cpu(), ring_v.to(dtype))
 
 
@@ -217,8 +217,9 @@ def test_hotcold_layer_compression_matches_oracle(dtype):
         ev = want["evicted_idx"][b]
         ring = kv.rings[0][b]
         assert len(ring) == ev.numel()
-        assert ring.ordered(ring.pos).tolist() == pos[b, ev].tolist()
-        assert torch.equal(torch.from_numpy(ring.ordered(ring.kpre)), pre[b][:, ev].permute(1, 0, 2).float())
+        snap = ring.export()
+        assert snap["pos"].tolist() == pos[b, ev].tolist()
+        assert torch.equal(torch.from_numpy(snap["kpre"]), pre[b][:, ev].permute(1, 0, 2).float())
     assert kv.dbg["compress_calls"] == 1
 
 

@@ -17,6 +17,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADER = os.path.join(ROOT, "include", "hotcold_hip.h")
 
 from hotcold_kv import _native as N  # noqa: E402
+from oracle import reference as ref  # noqa: E402
 from hotcold_kv import ops  # noqa: E402
 from hotcold_kv.baselines import PressConfig, PressLayerState, pyramid_layer_budget  # noqa: E402
 from hotcold_kv.baselines import scoring  # noqa: E402
@@ -198,10 +199,11 @@ def test_cold_store_skips_padding_and_ranks_by_inner_product():
     ctrl._retrieval_worker(0, q[None, :])
     _, _, pos, valid = ctrl._retrieval_ready_cpu[0]
     got = pos[0][valid[0]].tolist()
-    ring = ctrl.rings[0][0]
-    vecs = ring.ordered(ring.vec[:, 0, :])
-    ip = vecs @ q
-    want_order = [int(ring.ordered(ring.pos)[i]) for i in np.argsort(-ip, kind="stable")[:3]]
+    snap = ctrl.rings[0][0].export()
+    ip = np.zeros(len(snap["pos"]))
+    for d in range(D):                       # fp64, accumulated in dimension order
+        ip = ip + snap["vec"][:, 0, d].astype(np.float64) * float(q[d])
+    want_order = [int(snap["pos"][i]) for i in np.argsort(-ip, kind="stable")[:3]]
     assert got == want_order and got[0] == 3
 
 
@@ -227,6 +229,89 @@ def test_cold_store_per_head_retrieval():
     assert pos.shape == (1, HK, 2) and valid.dtype == torch.bool
     assert int(pos[0, 0, 0]) == 52 and int(pos[0, 1, 0]) == 57
     assert torch.equal(kpre[0, 0, 0], keys[2, 0]) and torch.equal(kpre[0, 1, 0], keys[7, 1])
+
+
+def _native_store(cap, H, Dm, dim, per_head):
+    from hotcold_kv.controller import _Ring
+    return _Ring(cap, H, Dm, dim, H if per_head else 1)
+
+
+@pytest.mark.parametrize("per_head", [False, True])
+@pytest.mark.parametrize("dim", [24, 32, 48])
+def test_native_cold_store_bit_exact_against_oracle(per_head, dim):
+    """Vectors, search order and ring wrap of the native store equal the
+    oracle's bit for bit: random tokens, padding indices, exact ties from
+    power-of-two multiples, near-ties from one-ulp perturbations, and adds
+    that wrap the ring and overflow it."""
+    H, Dm, cap = 4, 32, 40
+    g = torch.Generator().manual_seed(7 + dim + per_head)
+    nat = _native_store(cap, H, Dm, dim, per_head)
+    orc = ref.ColdStore(capacity=cap, dim=dim, per_head=per_head)
+    pos0 = 0
+    for n in (13, 25, 7, 61):
+        k = torch.randn(n, H, Dm, generator=g)
+        k[3] = 2 * k[1]                                   # exact tie with token 1
+        k[5] = torch.nextafter(k[4], torch.full_like(k[4], 1e9))   # near tie with token 4
+        v = torch.randn(n, H, Dm, generator=g)
+        idx = torch.arange(n)
+        idx[torch.randperm(n, generator=g)[: n // 5]] = -1        # padding
+        pos = torch.arange(pos0, pos0 + n)
+        pos0 += n
+        nat.add(k.permute(1, 0, 2).numpy(), v.permute(1, 0, 2).numpy(), pos.numpy(), idx.numpy())
+        orc.add(k.numpy(), v.numpy(), pos.numpy(), idx.numpy())
+        snap = nat.export()
+        assert snap["pos"].tolist() == orc.pos
+        assert np.array_equal(snap["kpre"], np.stack(orc.kpre)) and np.array_equal(snap["v"], np.stack(orc.v))
+        assert np.array_equal(snap["vec"], np.stack(orc.vec))             # bit-equal vectors
+        for trial in range(6):
+            head = trial % (H if per_head else 1)
+            if trial < 3:   # a stored token's own vector: itself and its exact tie lead
+                q = snap["vec"][int(torch.randint(len(orc.pos), (1,), generator=g))][head]
+            else:
+                q = orc.token_vecs(torch.randn(H, Dm, generator=g).numpy())[head]
+            for r in (1, 5, 64):
+                assert nat.search(q, r, head).tolist() == orc.search(q, r, head)
+
+
+@pytest.mark.parametrize("per_head", [False, True])
+def test_native_retrieve_matches_per_row_search(per_head):
+    """hc_cold_retrieve over B stores equals per-store oracle searches and
+    gathers; rows past the hits are zero and invalid."""
+    B, H, Dm, dim, cap, R = 3, 4, 16, 16, 32, 6
+    g = torch.Generator().manual_seed(11)
+    ctrl = KVController(cpu_buffer_size=cap, faiss_dim=dim, lookahead_k=R, enable_asserts=True,
+                        profile_overlap=False, per_head_retrieval=per_head)
+    ctrl._lazy_init(torch.zeros(B, H, 1, Dm), n_layers=1)
+    orcs = [ref.ColdStore(capacity=cap, dim=dim, per_head=per_head) for _ in range(B)]
+    counts = (20, 3, 0)                                  # batch row 2 stays empty
+    te = max(counts)
+    k = torch.randn(B, H, te, Dm, generator=g)
+    v = torch.randn(B, H, te, Dm, generator=g)
+    pos = torch.arange(B * te).view(B, te) + 100
+    idx = torch.stack([torch.where(torch.arange(te) < c, torch.arange(te), torch.full((te,), -1)) for c in counts])
+    ctrl.add_evicted_to_cold_store(0, EvictedKV(k_pre_cpu=k, v_cpu=v, pos_cpu=pos, evicted_idx=idx))
+    for b in range(B):
+        orcs[b].add(k[b].permute(1, 0, 2).numpy(), v[b].permute(1, 0, 2).numpy(), pos[b].numpy(), idx[b].numpy())
+    vh = H if per_head else 1
+    q = np.stack([np.stack([orcs[0].token_vecs(torch.randn(H, Dm, generator=g).numpy())[h % vh]
+                            for h in range(vh)]) for _ in range(B)])
+    ctrl._retrieval_worker(0, q if per_head else q[:, 0])
+    kpre, vv, p, valid = ctrl._retrieval_ready_cpu[0]
+    for b in range(B):
+        for h in range(vh):
+            hits = orcs[b].search(q[b, h], R, h)
+            pv = p[b, h] if per_head else p[b]
+            ok = valid[b, h] if per_head else valid[b]
+            assert ok.tolist() == [True] * len(hits) + [False] * (R - len(hits))
+            assert pv[: len(hits)].tolist() == [orcs[b].pos[i] for i in hits]
+            assert (pv[len(hits):] == 0).all()
+            heads = [h] if per_head else range(H)
+            for hh in heads:
+                want_k = np.zeros((R, Dm), np.float32)
+                want_v = np.zeros((R, Dm), np.float32)
+                for j, i in enumerate(hits):
+                    want_k[j], want_v[j] = orcs[b].kpre[i][hh], orcs[b].v[i][hh]
+                assert np.array_equal(kpre[b, hh].numpy(), want_k) and np.array_equal(vv[b, hh].numpy(), want_v)
 
 
 def test_query_pooling_matches_reference_definition():

@@ -296,6 +296,48 @@ def test_cold_store_self_retrieval_and_wrap():
         assert store.pos[hit] == t and np.array_equal(store.kpre[hit], keys[t].numpy())
 
 
+def test_cold_store_vectors_are_unit_head_means():
+    # the search vector is the L2-normalised head mean (controller.py:190-194),
+    # or each head's key per KV head; padded / cropped to the index width
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(8, 128, generator=g)
+    for dim in (64, 128, 160):
+        store = ref.ColdStore(capacity=4, dim=dim)
+        vec = store.token_vecs(k.numpy())[0].astype(np.float64)
+        m = k.double().mean(0)
+        m = torch.nn.functional.pad(m, (0, max(0, dim - 128)))[:dim]
+        assert abs(np.linalg.norm(vec) - 1.0) < 1e-6
+        assert np.allclose(vec, (m / m.norm()).numpy(), atol=1e-7)
+    per = ref.ColdStore(capacity=4, dim=64, per_head=True).token_vecs(k.numpy())
+    for h in range(8):
+        want = k[h, :64].double() / k[h, :64].double().norm()
+        assert np.allclose(per[h], want.numpy(), atol=1e-7)
+
+
+def test_cold_store_search_ranks_like_a_float64_matmul():
+    # with clear gaps the order is the one of an ordinary fp64 inner product
+    g = torch.Generator().manual_seed(4)
+    store = ref.ColdStore(capacity=300, dim=32)
+    keys = torch.randn(300, 2, 32, generator=g)
+    store.add(keys.numpy(), keys.numpy(), range(300))
+    q = store.token_vecs(torch.randn(2, 32, generator=g).numpy())[0]
+    ip = np.stack([v[0] for v in store.vec]).astype(np.float64) @ q.astype(np.float64)
+    want = np.argsort(-ip, kind="stable")[:20]
+    gaps = np.diff(np.sort(ip)[::-1][:21])
+    assert (np.abs(gaps) > 1e-9).all()
+    assert store.search(q, 20) == [int(i) for i in want]
+
+
+def test_cold_store_exact_ties_go_to_the_older_token():
+    # power-of-two multiples normalise to the same bits: exact ties
+    g = torch.Generator().manual_seed(5)
+    k = torch.randn(2, 16, generator=g)
+    store = ref.ColdStore(capacity=8, dim=16)
+    store.add(torch.stack([4 * k, k, 2 * k, -k]).numpy(), np.zeros((4, 2, 16)), [40, 10, 20, 30])
+    assert np.array_equal(store.vec[0], store.vec[1]) and np.array_equal(store.vec[1], store.vec[2])
+    assert store.search(store.vec[1][0], 4) == [0, 1, 2, 3]
+
+
 # ---------------------------------------------------------------------------
 # Golden fixtures (tests/golden/make_golden.py)
 # ---------------------------------------------------------------------------
