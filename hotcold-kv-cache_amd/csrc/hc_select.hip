@@ -248,6 +248,61 @@ static int launch_row_copy(RowCopy& c, hipStream_t st, const char* what) {
   return check_launch(what);
 }
 
+// Eviction gather with upcast (cache.py:86-125).  Output block:
+//   [k fp32 B][H][te][D] | [v fp32 B][H][te][D] | [pos int64 B][te]
+// Thread g < 2*B*H*te*D/4 converts four elements of one (tensor, b, h, j)
+// row; the next B*te threads copy the positions.  An index outside
+// [0, src_rows) writes a zero row and position -1.
+struct EvictGather {
+  const void* k;
+  const void* v;
+  int64_t k_sb, k_sh, k_ss, v_sb, v_sh, v_ss;
+  const int64_t* idx;
+  int64_t i_sb;
+  const int64_t* pos;
+  int64_t ps_sb;
+  float* out;
+  int64_t src_rows;
+  int B, H, te, D;
+};
+
+template <typename T>
+__global__ __launch_bounds__(256) void gather_evict_kernel(EvictGather a) {
+  const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int q = a.D / 4;
+  const int64_t per = (int64_t)a.B * a.H * a.te * q;
+  if (g < 2 * per) {
+    const int t = g >= per;
+    const int64_t r = g - t * per;
+    const int c = (int)(r % q);
+    const int64_t row = r / q;
+    const int j = (int)(row % a.te);
+    const int64_t bh = row / a.te;
+    const int h = (int)(bh % a.H);
+    const int b = (int)(bh / a.H);
+    const int64_t si = a.idx[b * a.i_sb + j];
+    floatx4 f = {0.f, 0.f, 0.f, 0.f};
+    if (si >= 0 && si < a.src_rows) {
+      const T* src = reinterpret_cast<const T*>(t ? a.v : a.k) +
+                     b * (t ? a.v_sb : a.k_sb) + h * (t ? a.v_sh : a.k_sh) + si * (t ? a.v_ss : a.k_ss) + 4 * c;
+      if constexpr (sizeof(T) == 4) {
+        f = *reinterpret_cast<const floatx4*>(src);
+      } else {
+        const u32x2 w = *reinterpret_cast<const u32x2*>(src);
+        const uint32_t ww[2] = {w[0], w[1]};
+        f = floatx4{Unpack<T>::get(ww, 0), Unpack<T>::get(ww, 1), Unpack<T>::get(ww, 2), Unpack<T>::get(ww, 3)};
+      }
+    }
+    *reinterpret_cast<floatx4*>(a.out + t * per * 4 + row * a.D + 4 * c) = f;
+  } else if (g < 2 * per + (int64_t)a.B * a.te) {
+    const int64_t r = g - 2 * per;
+    const int j = (int)(r % a.te), b = (int)(r / a.te);
+    const int64_t si = a.idx[b * a.i_sb + j];
+    int64_t* pos_out = reinterpret_cast<int64_t*>(a.out + 2 * per * 4);
+    pos_out[r] = (si >= 0 && si < a.src_rows) ? a.pos[b * a.ps_sb + si] : -1;
+  }
+}
+
 }  // namespace hc
 
 using namespace hc;
@@ -342,4 +397,49 @@ extern "C" int hc_append_rows(int dtype, int64_t B, int64_t H, int64_t T, int64_
   c.row_bytes = (int)(D * es);
   c.elem_bytes = es;
   return launch_row_copy(c, reinterpret_cast<hipStream_t>(stream), "append_rows");
+}
+
+extern "C" int64_t hc_gather_evict_bytes(int64_t B, int64_t H, int64_t te, int64_t D) {
+  if (B <= 0 || H <= 0 || te < 0 || D <= 0) return 0;
+  return 2 * B * H * te * D * (int64_t)sizeof(float) + B * te * (int64_t)sizeof(int64_t);
+}
+
+extern "C" int hc_gather_evict(int dtype, int64_t B, int64_t H, int64_t te, int64_t D, const int64_t* idx,
+                               int64_t i_sb, int64_t src_rows, const void* k_src, int64_t k_sb, int64_t k_sh,
+                               int64_t k_ss, const void* v_src, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                               const int64_t* pos_src, int64_t ps_sb, void* dev_out, void* host_out,
+                               void* stream) {
+  HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16, "gather_evict: bad dtype %d",
+             dtype);
+  HC_REQUIRE(B > 0 && H > 0 && te >= 0 && D > 0 && D % 4 == 0, "gather_evict: bad shape (D %% 4 == 0)");
+  HC_REQUIRE(B * H * te * (D / 4) < ((int64_t)1 << 38), "gather_evict: too large for one launch");
+  HC_REQUIRE(idx && k_src && v_src && pos_src && dev_out, "gather_evict: null pointer");
+  const int es = dtype_size(dtype);
+  const int64_t al = 4 * es;  // four elements per load
+  HC_REQUIRE((uintptr_t)k_src % al == 0 && (uintptr_t)v_src % al == 0 && (k_sb * es) % al == 0 &&
+                 (k_sh * es) % al == 0 && (k_ss * es) % al == 0 && (v_sb * es) % al == 0 && (v_sh * es) % al == 0 &&
+                 (v_ss * es) % al == 0 && (uintptr_t)dev_out % 16 == 0,
+             "gather_evict: rows must be %lld-byte aligned", (long long)al);
+  if (te == 0) return HC_OK;
+  EvictGather a{};
+  a.k = k_src; a.v = v_src;
+  a.k_sb = k_sb; a.k_sh = k_sh; a.k_ss = k_ss; a.v_sb = v_sb; a.v_sh = v_sh; a.v_ss = v_ss;
+  a.idx = idx; a.i_sb = i_sb; a.pos = pos_src; a.ps_sb = ps_sb;
+  a.out = reinterpret_cast<float*>(dev_out);
+  a.src_rows = src_rows;
+  a.B = (int)B; a.H = (int)H; a.te = (int)te; a.D = (int)D;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const int64_t threads = 2 * B * H * te * (D / 4) + B * te;
+  const dim3 grid((unsigned)cdiv(threads, 256));
+  if (dtype == HC_DTYPE_F16) hipLaunchKernelGGL(gather_evict_kernel<half_t>, grid, dim3(256), 0, st, a);
+  else if (dtype == HC_DTYPE_BF16) hipLaunchKernelGGL(gather_evict_kernel<bf16_t>, grid, dim3(256), 0, st, a);
+  else hipLaunchKernelGGL(gather_evict_kernel<float>, grid, dim3(256), 0, st, a);
+  int rc = check_launch("gather_evict");
+  if (rc != HC_OK) return rc;
+  if (host_out) {
+    const hipError_t e = hipMemcpyAsync(host_out, dev_out, (size_t)hc_gather_evict_bytes(B, H, te, D),
+                                        hipMemcpyDeviceToHost, st);
+    if (e != hipSuccess) return set_error(HC_ERR_HIP, "gather_evict: hipMemcpyAsync: %s", hipGetErrorString(e));
+  }
+  return HC_OK;
 }

@@ -122,6 +122,9 @@ SIGNATURES = {
     "hc_stream_wait_event": (_int, [_vp, _vp]),
     "hc_memcpy_h2d_async": (_int, [_vp, _vp, _i64, _vp]),
     "hc_memcpy_d2h_async": (_int, [_vp, _vp, _i64, _vp]),
+    "hc_gather_evict_bytes": (_i64, [_i64, _i64, _i64, _i64]),
+    "hc_gather_evict": (_int, [_int, _i64, _i64, _i64, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _i64,
+                               _vp, _i64, _i64, _i64, _vp, _i64, _vp, _vp, _vp]),
     # host cold store
     "hc_cold_create": (_vp, [_i64, _i64, _i64, _i64, _i64, _int]),
     "hc_cold_destroy": (None, [_vp]),

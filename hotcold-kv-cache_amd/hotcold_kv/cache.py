@@ -8,9 +8,9 @@ compressed like cache.py:37-128: the last min(recent, stashed) post-RoPE
 queries score every key (raw q.k/sqrt(D) summed over the queries, mean over
 KV heads), the top int(max_capacity_prompt * topk_ratio) prefix tokens plus
 the recent window are kept (one index set for every head, ties to the lower
-index), and the evicted prefix tokens go to the cold store as pinned fp32
-copies.  Scoring, selection, the gathers and the eviction gather run on the
-gfx950 kernels.
+index), and the evicted prefix tokens go to the cold store as fp32 copies
+staged through reusable pinned memory.  Scoring, selection, the gathers and
+the eviction gather (with its fp32 upcast) run on the gfx950 kernels.
 
 get_seq_length() reports the number of tokens processed (the absolute
 position of the next token) so that transformers' default position ids stay
@@ -124,27 +124,20 @@ class HotColdLayer(CacheLayerMixin):
         self.buf.compact(keep)
 
     def _evict(self, layer_idx, evicted):
-        """Copy the evicted prefix tokens to pinned fp32 host buffers and hand
-        them to the cold store (cache.py:86-125)."""
+        """Gather the evicted prefix tokens' pre-RoPE keys, values (upcast to
+        fp32) and positions in one kernel, copy the packed block to reusable
+        pinned host memory in one hipMemcpyAsync, and hand it to the cold
+        store (cache.py:86-125)."""
         ctrl = self.kvctrl
         B, Hk, D = self.buf.B, self.buf.H, self.buf.D
         te = int(evicted.shape[-1])
-        dev = self.buf.keys.device
-        kp = torch.empty((B, Hk, te, D), dtype=self.buf.dtype, device=dev)
-        vv = torch.empty_like(kp)
-        pos = torch.empty((B, te), dtype=torch.int64, device=dev)
-        ops.gather_rows(evicted, [(self.buf.pre_keys, kp), (self.buf.values, vv)], pos_src=self.buf.positions,
-                        pos_dst=pos)
-        pin = torch.cuda.is_available()
-        kp_cpu = torch.empty((B, Hk, te, D), dtype=torch.float32, pin_memory=pin)
-        v_cpu = torch.empty_like(kp_cpu, pin_memory=pin)
-        pos_cpu = torch.empty((B, te), dtype=torch.int64, pin_memory=pin)
-        kp_cpu.copy_(kp.float(), non_blocking=True)
-        v_cpu.copy_(vv.float(), non_blocking=True)
-        pos_cpu.copy_(pos, non_blocking=True)
-        idx_cpu = evicted.to("cpu")  # synchronising copy: the pinned copies above are complete after it
+        dev_buf, host_buf = ctrl.evict_staging(self.buf.keys.device, B, Hk, te, D)
+        kp_cpu, v_cpu, pos_cpu = ops.gather_evict(evicted, self.buf.pre_keys, self.buf.values, self.buf.positions,
+                                                  dev_out=dev_buf, host_out=host_buf)
+        idx_cpu = evicted.to("cpu")  # synchronising copy: the staged block is complete after it
         ctrl.dbg["compress_calls"] += 1
         ctrl.dbg["evicted_tokens"] += int(B * te)
+        # the cold store copies the tokens before returning; the staging is reused
         ctrl.add_evicted_to_cold_store(layer_idx, EvictedKV(k_pre_cpu=kp_cpu, v_cpu=v_cpu, pos_cpu=pos_cpu,
                                                             evicted_idx=idx_cpu))
 

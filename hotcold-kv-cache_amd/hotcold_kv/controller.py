@@ -142,6 +142,8 @@ class KVController:
         self._stage_lock = []
         self._staged = []
         self._stream = None
+        self._evict_dev = None
+        self._evict_host = None
         self.last_injected_len = 0
         self.held_mem = []
 
@@ -198,6 +200,17 @@ class KVController:
                 N.lib().hc_stream_destroy(self._stream)
         except Exception:
             pass
+
+    def evict_staging(self, device, B, H, te, D):
+        """Device and pinned host staging blocks of at least
+        hc_gather_evict_bytes(B, H, te, D) bytes for one eviction; grown on
+        demand and reused (evictions run one at a time on the main thread)."""
+        nbytes = int(N.lib().hc_gather_evict_bytes(B, H, te, D))
+        if self._evict_dev is None or self._evict_dev.numel() < nbytes or self._evict_dev.device != device:
+            size = max(nbytes, 2 * (self._evict_dev.numel() if self._evict_dev is not None else 0))
+            self._evict_dev = torch.empty((size,), dtype=torch.uint8, device=device)
+            self._evict_host = torch.empty((size,), dtype=torch.uint8, pin_memory=True)
+        return self._evict_dev, self._evict_host
 
     @property
     def cpu_kpre_ring(self):

@@ -404,6 +404,43 @@ def gather_kv(t, keep):
     return out
 
 
+def gather_evict(idx, k, v, pos, dev_out=None, host_out=None):
+    """Evicted rows idx (B,te) (shared by the heads) of k/v (B,H,S,D) upcast
+    to fp32 plus their positions from pos (B,S), in one packed block
+    (cache.py:86-125).  dev_out / host_out are uint8 tensors of at least
+    gather_evict_bytes() bytes (host_out pinned: one hipMemcpyAsync D2H on the
+    current stream; the caller synchronises before reading it).  Returns
+    (k (B,H,te,D) f32, v, pos (B,te) int64) views of host_out if given, else
+    of dev_out."""
+    _require_device(idx, k, v, pos)
+    B, H, S, D = k.shape
+    te = int(idx.shape[-1])
+    if idx.dim() != 2 or idx.shape[0] != B or idx.dtype != torch.int64 or tuple(v.shape) != tuple(k.shape) \
+            or v.dtype != k.dtype or pos.dim() != 2 or pos.shape[0] != B or pos.dtype != torch.int64:
+        raise RuntimeError("gather_evict: idx (B,te) int64, k/v (B,H,S,D) of one dtype, pos (B,S) int64")
+    if idx.stride(1) != 1:
+        idx = idx.contiguous()
+    if pos.stride(1) != 1:
+        pos = pos.contiguous()
+    nbytes = int(N.lib().hc_gather_evict_bytes(B, H, te, D))
+    if dev_out is None:
+        dev_out = torch.empty((nbytes,), dtype=torch.uint8, device=k.device)
+    if dev_out.numel() < nbytes or (host_out is not None and host_out.numel() < nbytes):
+        raise RuntimeError(f"gather_evict: staging buffers need {nbytes} bytes")
+    rc = N.lib().hc_gather_evict(
+        N.dtype_code(k.dtype), B, H, te, D, _ptr(idx), idx.stride(0), S,
+        _ptr(k), *k.stride()[:3], _ptr(v), *v.stride()[:3], _ptr(pos), pos.stride(0),
+        _ptr(dev_out), _ptr(host_out), _stream_handle(k.device))
+    N.check(rc, "hc_gather_evict")
+    blk = host_out if host_out is not None else dev_out
+    kv_elems = B * H * te * D
+    f = blk[: 8 * kv_elems].view(torch.float32)
+    kk = f[:kv_elems].view(B, H, te, D)
+    vv = f[kv_elems:].view(B, H, te, D)
+    pp = blk[8 * kv_elems: nbytes].view(torch.int64).view(B, te)
+    return kk, vv, pp
+
+
 def append_rows(row, k_src, k_dst, v_src=None, v_dst=None, p_src=None, p_dst=None, pos_src=None, pos_dst=None):
     """Write T new rows (B,H,T,D) at row `row` of the hot buffers."""
     _require_device(k_src, k_dst, v_src, v_dst, p_src, p_dst, pos_src, pos_dst)

@@ -185,6 +185,24 @@ int hc_gather_rows(int64_t B, int64_t H, int64_t n, int64_t D, int64_t elem_byte
                    void* stream);
 
 /*
+ * Eviction gather with fp32 upcast (replaces the per-batch gather, .float()
+ * and pinned copies of cache.py:86-125).  For the te evicted token indices
+ * idx[b*i_sb + j] (one set shared by the heads) the pre-RoPE keys and values
+ * [B][H][*][D] (dtype, element strides) and positions pos_src[b*ps_sb + i]
+ * are written into one packed device block dev_out of
+ * hc_gather_evict_bytes(B, H, te, D) bytes (16-byte aligned):
+ *   [k fp32 B][H][te][D] | [v fp32 B][H][te][D] | [pos int64 B][te]
+ * An index outside [0, src_rows) gives a zero row and position -1.  With
+ * host_out (pinned, same size) the block is then copied to it by one
+ * hipMemcpyAsync on the stream.  D % 4 == 0; K/V rows aligned to 4 elements.
+ */
+int64_t hc_gather_evict_bytes(int64_t B, int64_t H, int64_t te, int64_t D);
+int hc_gather_evict(int dtype, int64_t B, int64_t H, int64_t te, int64_t D, const int64_t* idx, int64_t i_sb,
+                    int64_t src_rows, const void* k_src, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                    const void* v_src, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                    const int64_t* pos_src, int64_t ps_sb, void* dev_out, void* host_out, void* stream);
+
+/*
  * Append T new token rows at row `row` of the hot buffer (replaces the torch.cat
  * appends of cache.py:145-148 and layer_state.py:99-100).  src rows
  * [B][H][T][D]; k_pre/pos may be NULL.  pos_src [B][T] int64 -> pos_dst[b][row+t].

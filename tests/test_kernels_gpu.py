@@ -366,6 +366,39 @@ def test_append_rows():
 # Inject (re-RoPE into the held slot)
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("to_host", [False, True])
+def test_gather_evict_upcast_and_stage(dtype, to_host):
+    """Evicted rows of strided hot-buffer views (held slot in front) upcast to
+    fp32, with positions, in one packed block; out-of-range indices give zero
+    rows and position -1; the pinned copy equals the device block."""
+    B, H, held, cap, D = 2, 4, 8, 300, 128
+    g = torch.Generator().manual_seed(21)
+    kbuf = _randn((B, H, held + cap, D), 22, dtype).to(DEV)
+    vbuf = _randn((B, H, held + cap, D), 23, dtype).to(DEV)
+    posbuf = torch.randint(0, 10 ** 6, (B, held + cap), generator=g).to(DEV)
+    S = 250
+    k, v, pos = kbuf[:, :, held:held + S], vbuf[:, :, held:held + S], posbuf[:, held:held + S]
+    te = 97
+    idx = torch.stack([torch.randperm(S, generator=g)[:te] for _ in range(B)])
+    idx[1, 5], idx[0, 9] = -1, S + 3
+    dev_out = torch.empty((ops_bytes := 2 * B * H * te * D * 4 + B * te * 8,), dtype=torch.uint8, device=DEV)
+    host_out = torch.empty((ops_bytes,), dtype=torch.uint8, pin_memory=True) if to_host else None
+    kk, vv, pp = ops.gather_evict(idx.to(DEV), k, v, pos, dev_out=dev_out, host_out=host_out)
+    torch.cuda.synchronize()
+    kc, vc, pc = k.float().cpu(), v.float().cpu(), pos.cpu()
+    for b in range(B):
+        for j in range(te):
+            i = int(idx[b, j])
+            if 0 <= i < S:
+                assert torch.equal(kk[b, :, j].cpu(), kc[b, :, i]) and torch.equal(vv[b, :, j].cpu(), vc[b, :, i])
+                assert int(pp[b, j]) == int(pc[b, i])
+            else:
+                assert not kk[b, :, j].cpu().any() and not vv[b, :, j].cpu().any() and int(pp[b, j]) == -1
+    if to_host:
+        assert not kk.is_cuda and torch.equal(host_out, dev_out.cpu())
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("per_head", [False, True])
 def test_inject_rerope_matches_model_rotation(dtype, per_head):
     B, Hk, R, D, cap = 2, 8, 64, 128, 100
