@@ -22,8 +22,8 @@ separately and subtracted.  It only reads, so no dirty lines are left for
 decode to write back.
 
 Reported:
-  value              decode us per layer-step: mean append+decode launch time
-                     of the timed steps / 32, timed with HIP events on the
+  value              decode us per layer-step: median append+decode launch
+                     time of the timed steps / 32, timed with HIP events on the
                      launch stream as [sweep; decode] minus [sweep] alone
                      (run_steps explains; the event-bracketed time is also
                      reported)
@@ -31,7 +31,9 @@ Reported:
   roofline           decode launch: algorithmic bytes / mean launch time
   roofline_compaction, scoring MFMA rate, a per-layer-launch variant (one
   decode launch per layer, as a model's layer loop issues them), warm-cache
-  figures, and the reference's torch-CPU path on a bounded sample.
+  figures, the reference's torch-CPU path on a bounded sample, and
+  other_workloads: decode / compaction / inject figures of the 16k, 32k and
+  64k workloads (secondary; --no-other-configs skips them).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 """
@@ -196,7 +198,7 @@ def run_steps(s, steps, flush):
     decode ms (differential), decode ms (event-bracketed)).
 
     Compaction replays its graph between two events.  Each decode step t is
-    timed two ways, both after a cache sweep:
+    timed two ways, both after a cache sweep (medians over the timed steps):
       differential  events around [sweep; decode] minus events around
                     [sweep] alone: the decode kernel plus the ordinary gap
                     between two dependent kernels, as in a model's stream;
@@ -244,8 +246,8 @@ def run_steps(s, steps, flush):
         return [a.elapsed_time(b) for a, b in evs]
 
     comp = ms(comp_ev)
-    dec_diff = statistics.mean(ms(pair_ev)) - statistics.mean(ms(sweep_ev))
-    dec_br = statistics.mean(ms(br_ev))
+    dec_diff = statistics.median(ms(pair_ev)) - statistics.median(ms(sweep_ev))
+    dec_br = statistics.median(ms(br_ev))
     return wall_ms, comp, dec_diff, dec_br
 
 
@@ -306,6 +308,154 @@ def profiled_traffic(workload):
     return int(m.group(1)) if m else None
 
 
+def differential_ms(st, flush, fn, reps, warmup=3):
+    """ms of fn() measured as events around [sweep; fn] minus events around
+    [sweep] alone (see run_steps), as the difference of the two medians
+    after `warmup` discarded rounds."""
+    import torch
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    sw, pr = [], []
+    with torch.cuda.stream(st):
+        for i in range(warmup + reps):
+            a0, a1, b0, b1 = ev(), ev(), ev(), ev()
+            a0.record(st)
+            flush()
+            a1.record(st)
+            b0.record(st)
+            flush()
+            fn(i)
+            b1.record(st)
+            if i >= warmup:
+                sw.append((a0, a1))
+                pr.append((b0, b1))
+    torch.cuda.synchronize()
+    return statistics.median(a.elapsed_time(b) for a, b in pr) - statistics.median(a.elapsed_time(b) for a, b in sw)
+
+
+def measure_config(w, dev, flush, reps=24):
+    """Secondary figures of a larger workload (not the headline): the fused
+    append+decode over all layers' hot buffers with the held slot active, one
+    layer's compaction at the full batch, and the inject path (re-RoPE of a
+    full held slot, its pinned H2D copy, and decode with that copy running
+    concurrently on a side stream).  Inputs are N(0,1) of the workload's
+    shapes, generated on the device."""
+    import torch
+    from hotcold_kv import ops, synthetic
+
+    g = torch.Generator(device=dev).manual_seed(5)
+    dt, D, Hk, Hq = w.dtype, w.head_dim, w.hk, w.hq
+    es = elem_size(dt)
+    LB = w.layers * w.batch
+    R = w.held
+    cap = w.hot_capacity
+    st = torch.cuda.Stream(dev)
+    out = {"workload": w.name, "layers": w.layers, "batch": w.batch, "seq_len": w.seq_len, "budget": w.budget,
+           "held": R, "dtype": {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}[dt]}
+
+    # -- decode: hot buffers of every layer, held slot in rows 0..R-1 ------------------------
+    k_hot = torch.randn((LB, Hk, cap, D), generator=g, device=dev, dtype=dt)
+    v_hot = torch.randn((LB, Hk, cap, D), generator=g, device=dev, dtype=dt)
+    q = torch.randn((LB, Hq, D), generator=g, device=dev, dtype=dt)
+    k_new = torch.randn((LB, Hk, 1, D), generator=g, device=dev, dtype=dt)
+    v_new = torch.randn((LB, Hk, 1, D), generator=g, device=dev, dtype=dt)
+    held_pos = torch.randint(0, w.seq_len, (LB, Hk, R), generator=g, device=dev)
+    held_valid = torch.rand((LB, Hk, R), generator=g, device=dev) < 0.9
+    cur = torch.tensor([w.seq_len], dtype=torch.int64, device=dev)
+    o = torch.empty((LB, Hq, D), dtype=dt, device=dev)
+    steps = [int(x) for x in torch.linspace(0, w.decode_steps - 1, reps)]
+
+    def decode(i):
+        n = R + w.budget + steps[i % len(steps)] + 1
+        ops.decode_attention_append(q, k_hot[:, :, :n], v_hot[:, :, :n], k_new, v_new, w.scaling, held_len=R,
+                                    held_pos=held_pos, held_valid=held_valid, cur_pos=cur, out=o)
+
+    with torch.cuda.stream(st):
+        decode(0)
+    dec_ms = differential_ms(st, flush, decode, reps)
+    mean_keys = R + w.budget + (w.decode_steps + 1) / 2.0
+    nbytes = decode_bytes(w, LB, mean_keys)
+    gbps = nbytes / (dec_ms * 1e-3) / 1e9
+    out["decode"] = {"us_per_layer_step": round(dec_ms * 1e3 / w.layers, 3), "launch_us": round(dec_ms * 1e3, 2),
+                     "bytes_per_launch": int(nbytes), "achieved_GBps": round(gbps, 1),
+                     "frac": round(gbps / HBM_PEAK_GBS, 4), "layers_per_launch": w.layers}
+
+    # -- inject: staged fp32 held slot of every layer -> re-RoPE into the hot buffers --------
+    inv = synthetic.inv_freq(D, w.theta).to(dev)
+    kp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).pin_memory()
+    vp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).pin_memory()
+    kp_dev = torch.empty_like(kp_host, device=dev)
+    vp_dev = torch.empty_like(vp_host, device=dev)
+    kp_dev.copy_(kp_host)
+    vp_dev.copy_(vp_host)
+
+    def inject(i):
+        ops.inject_rerope(kp_dev, vp_dev, held_pos, inv, 1.0, k_hot, v_hot)
+
+    with torch.cuda.stream(st):
+        inject(0)
+    inj_ms = differential_ms(st, flush, inject, reps)
+    inj_bytes = 2 * LB * Hk * R * D * (4 + es) + LB * Hk * R * 8
+    side = torch.cuda.Stream(dev)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    with torch.cuda.stream(side):
+        e0.record(side)
+        kp_dev.copy_(kp_host, non_blocking=True)
+        vp_dev.copy_(vp_host, non_blocking=True)
+        e1.record(side)
+    torch.cuda.synchronize()
+    h2d_ms = e0.elapsed_time(e1)
+    h2d_bytes = 2 * LB * Hk * R * D * 4
+
+    # decode while the side stream copies the staged slot (the inject feed's overlap)
+    def decode_overlapped(i):
+        with torch.cuda.stream(side):
+            kp_dev.copy_(kp_host, non_blocking=True)
+            vp_dev.copy_(vp_host, non_blocking=True)
+        decode(i)
+
+    ov_ms = differential_ms(st, flush, decode_overlapped, reps)
+    torch.cuda.synchronize()
+    out["inject"] = {"rerope_us_all_layers": round(inj_ms * 1e3, 2), "rerope_bytes": int(inj_bytes),
+                     "rerope_GBps": round(inj_bytes / (inj_ms * 1e-3) / 1e9, 1),
+                     "h2d_us_all_layers": round(h2d_ms * 1e3, 1), "h2d_bytes": int(h2d_bytes),
+                     "h2d_GBps": round(h2d_bytes / (h2d_ms * 1e-3) / 1e9, 1),
+                     "decode_launch_us_with_concurrent_h2d": round(ov_ms * 1e3, 2)}
+    del k_hot, v_hot, kp_dev, vp_dev
+
+    # -- compaction of one layer at the full batch ------------------------------------------
+    B, S, W = w.batch, w.seq_len, min(w.window, w.seq_len)
+    q_post = torch.randn((B, Hq, S, D), generator=g, device=dev, dtype=dt)
+    k_post = torch.randn((B, Hk, S, D), generator=g, device=dev, dtype=dt)
+    v = torch.randn((B, Hk, S, D), generator=g, device=dev, dtype=dt)
+    kb = torch.empty((B, Hk, w.budget, D), dtype=dt, device=dev)
+    vb = torch.empty_like(kb)
+
+    def compact(i):
+        sc = ops.snapkv_scores(q_post, k_post, W, w.scaling, w.pool, "maxpool")
+        keep = ops.keep_index(sc, W, w.budget)
+        ops.gather_rows(keep, [(k_post, kb), (v, vb)])
+
+    with torch.cuda.stream(st):
+        compact(0)
+    comp_ms = differential_ms(st, flush, compact, 6)
+    cbytes = compaction_bytes(w, B)
+    cg = cbytes / (comp_ms * 1e-3) / 1e9
+    sflops = 2.0 * B * Hk * W * S * D      # fp64 window logits (the exact-score contract)
+    out["compaction"] = {"ms_per_layer": round(comp_ms, 4), "ms_32_layers": round(comp_ms * w.layers, 3),
+                         "bytes_per_layer": int(cbytes), "achieved_GBps": round(cg, 1),
+                         "frac": round(cg / HBM_PEAK_GBS, 4),
+                         "scoring_tflops_fp64": round(sflops / (comp_ms * 1e-3) / 1e12, 2),
+                         "scoring_mfma_frac": round(sflops / (comp_ms * 1e-3) / 1e12 / FP64_MFMA_PEAK_TFLOPS, 4)}
+    del q_post, k_post, v
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(w, sample_seconds, n_layers=4):
     """The reference's torch-CPU path (snapkv_importance -> keep_index ->
     gather_kv, then per decode step cat + repeat_kv + SDPA) on a bounded
@@ -364,6 +514,8 @@ def main():
     ap.add_argument("--workload", default="llama8b_8k_b512")
     ap.add_argument("--cpu-sample-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-other-configs", action="store_true",
+                    help="skip the secondary figures of the 16k/32k/64k workloads")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; the hot tier shards by batch and KV head "
@@ -414,6 +566,18 @@ def main():
         f"{pl_cold_ms * 1e3 / w.layers:.2f} us/layer, warm {pl_warm_ms * 1e3 / w.layers:.2f} us/layer")
     del flush
 
+    others = []
+    if not args.no_other_configs and args.workload == "llama8b_8k_b512":
+        flush = CacheSweep(dev)
+        for name in ("llama8b_16k_b1024_held64", "b16_32k_b2048_held128", "bf16_b4_64k_b4096_held256"):
+            log(f"secondary figures: {name} ...")
+            r = measure_config(synthetic.WORKLOADS[name], dev, flush)
+            log(f"  decode {r['decode']['us_per_layer_step']} us/layer-step ({r['decode']['frac'] * 100:.1f}% of "
+                f"HBM peak), compaction {r['compaction']['ms_per_layer']} ms/layer, re-RoPE "
+                f"{r['inject']['rerope_us_all_layers']} us, H2D {r['inject']['h2d_GBps']} GB/s")
+            others.append(r)
+        del flush
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
@@ -457,6 +621,7 @@ def main():
                                 "scoring_mfma_frac": round(sflops / (comp_ms * 1e-3) / 1e12
                                                            / FP64_MFMA_PEAK_TFLOPS, 4)},
         "device_stream": stream,
+        "other_workloads": others,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
