@@ -751,6 +751,31 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int D
   }
 }
 
+// H2O accumulated attention (layer_state.py:55-65, 102-114): for every key
+// s of (b, kv head hk), the attention probability averaged over the G query
+// heads of the group (_reduce_probs_to_kv, scoring.py:29-37),
+//   col = (1/G) sum_g exp2(score[h][s] - M[h]) / L[h],   h = hk*G + g,
+// is added to acc[b][hk][s]; key S-1 (the token appended this step) starts
+// from zero (the torch.cat of a zero column, layer_state.py:108-111).
+// grid (cdiv(S, 256), Hk, B), block 256.
+__global__ __launch_bounds__(256) void h2o_accum_kernel(const float* scores, const float* ml, int Hq, int G, int S,
+                                                        float* acc, int64_t a_sb, int64_t a_sh) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  const int hk = blockIdx.y, b = blockIdx.z;
+  if (s >= S) return;
+  float col = 0.f;
+  for (int g = 0; g < G; ++g) {
+    const int h = hk * G + g;
+    const float M = ml[((int64_t)b * Hq + h) * 2 + 0];
+    const float L = ml[((int64_t)b * Hq + h) * 2 + 1];
+    const float sc = scores[((int64_t)b * Hq + h) * S + s];
+    col += (sc == -INFINITY) ? 0.f : exp2f(sc - M) / L;
+  }
+  col /= (float)G;
+  float* a = acc + b * a_sb + hk * a_sh;
+  a[s] = (s == S - 1 ? 0.f : a[s]) + col;
+}
+
 // Per-token eviction score of the reference kernel (kernels.py:66-67, 134-136):
 //   loss[b,s] = dtype( mean_h( p[b,h,s] / l[b,h] * mean_d |v[b,hk(h),s,d]| ) )
 // with p = exp(logit - max) (the max cancels), and evict_idx[b] = first argmin.
@@ -969,7 +994,8 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
                               void* out, int64_t o_sb, int64_t o_sh,
                               float* evict_loss, int64_t* evict_idx,
                               void* workspace, int64_t workspace_bytes, int64_t num_splits,
-                              void* stream, const DecodeArgs* ap) {
+                              void* stream, const DecodeArgs* ap, float* h2o_acc = nullptr,
+                              int64_t h2o_sb = 0, int64_t h2o_sh = 0) {
   if (dropout != 0.0) return set_error(HC_ERR_DROPOUT, "dropout must be 0.0 , because we are not in training");
   HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16, "decode: bad dtype %d", dtype);
   HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && D > 0 && S > 0, "decode: empty shape B=%lld Hq=%lld Hk=%lld D=%lld S=%lld",
@@ -1010,13 +1036,15 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
                               (ap->pd_sh * es) % 16 == 0 && (ap->pd_ss * es) % 16 == 0 && ap->pd_ss >= D),
                "decode_append: p_new / p_dst rows must be 16-byte aligned with row stride >= D");
   }
-  const int with_evict = (evict_loss != nullptr || evict_idx != nullptr);
+  // per-head logits and (max, sum) are kept for the eviction score or H2O
+  const int with_evict = (evict_loss != nullptr || evict_idx != nullptr || h2o_acc != nullptr);
   const DecodeLayout lay = decode_layout(B, Hq, Hk, D, S, splits, with_evict);
   if (!workspace || workspace_bytes < lay.total)
     return set_error(HC_ERR_WORKSPACE, "decode: workspace of %lld bytes needed, got %lld", (long long)lay.total,
                      (long long)workspace_bytes);
   HC_REQUIRE(((uintptr_t)workspace % 256) == 0, "decode: workspace must be 256-byte aligned");
-  HC_REQUIRE(!with_evict || (evict_loss && evict_idx), "decode: evict_loss and evict_idx go together");
+  HC_REQUIRE((evict_loss == nullptr) == (evict_idx == nullptr), "decode: evict_loss and evict_idx go together");
+  HC_REQUIRE(!(h2o_acc && (evict_loss || ap)), "decode: H2O accumulation runs alone");
 
   DecodeArgs a;
   a.q = q; a.q_sb = q_sb; a.q_sh = q_sh;
@@ -1060,7 +1088,12 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
   if (rc != HC_OK) return rc;
   if ((rc = check_launch("decode_attn")) != HC_OK) return rc;
 
-  if (with_evict) {
+  if (h2o_acc) {
+    const dim3 grid((unsigned)cdiv(S, 256), (unsigned)Hk, (unsigned)B);
+    hipLaunchKernelGGL(h2o_accum_kernel, grid, dim3(256), 0, st, a.scores, a.ml, (int)Hq, G, (int)S, h2o_acc,
+                       h2o_sb, h2o_sh);
+    if ((rc = check_launch("h2o_accum")) != HC_OK) return rc;
+  } else if (with_evict) {
     if (dtype == HC_DTYPE_F16)
       hipLaunchKernelGGL(evict_score_kernel<half_t>, dim3((unsigned)B), dim3(256), 0, st, a.scores, a.ml,
                          (const half_t*)v, v_sb, v_sh, v_ss, (int)Hq, G, (int)S, (int)D, evict_loss, evict_idx);
@@ -1124,4 +1157,18 @@ extern "C" int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t H
   return decode_impl(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss, mask, mask_sb,
                      held_len, held_pos, hp_sb, hp_sh, held_valid, hv_sb, hv_sh, cur_pos, scaling, 0.0, out, o_sb,
                      o_sh, nullptr, nullptr, workspace, workspace_bytes, num_splits, stream, &ap);
+}
+
+extern "C" int hc_decode_attn_h2o(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                                  const void* q, int64_t q_sb, int64_t q_sh,
+                                  const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                                  const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                  double scaling,
+                                  void* out, int64_t o_sb, int64_t o_sh,
+                                  float* acc, int64_t a_sb, int64_t a_sh,
+                                  void* workspace, int64_t workspace_bytes, int64_t num_splits, void* stream) {
+  HC_REQUIRE(acc != nullptr, "decode_h2o: acc is required");
+  return decode_impl(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss, nullptr, 0, 0,
+                     nullptr, 0, 0, nullptr, 0, 0, nullptr, scaling, 0.0, out, o_sb, o_sh, nullptr, nullptr, workspace,
+                     workspace_bytes, num_splits, stream, nullptr, acc, a_sb, a_sh);
 }

@@ -343,8 +343,9 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ l
 
 // Importance and pooling.  grid (ceil(S / (256 - 2P)), Hk, B), block 256:
 // thread t computes imp for key c0 - P + t as the fma chain over the window
-// rows in ascending order (rows streamed 8 at a time, the next 8 in flight),
-// then the inner 256 - 2P threads pool over their neighbours in LDS.
+// rows in ascending order (rows streamed 8 at a time, the next 8 in flight;
+// the rows' max and 1/sum staged in LDS kMaxW rows at a time), then the inner
+// 256 - 2P threads pool over their neighbours in LDS.
 constexpr int kImpRows = 8;
 
 template <int MODE>
@@ -360,14 +361,6 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
   __shared__ float sm_m[kMaxW];
   __shared__ double sm_inv[kMaxW];
   __shared__ float sm_imp[256];
-  if constexpr (MODE == HC_SCORE_SNAPKV) {
-    for (int w = threadIdx.x; w < W; w += blockDim.x) {
-      sm_m[w] = key_to_float(rmax[bh * W + w]);
-      const double l = (double)lsum[bh * W + w] * 0x1p-44;
-      sm_inv[w] = 1.0 / l;
-    }
-  }
-  __syncthreads();
   const int s = c0 - P + (int)threadIdx.x;
   const bool sv = s >= 0 && s < S;
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + bh * W * S, (uint32_t)((int64_t)W * S * 4));
@@ -379,26 +372,39 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
       bload<4>(rs, (base == kOob || w0 + r >= W) ? kOob : base + (uint32_t)(w0 + r) * rowb, &dst[r]);
   };
   double acc = 0.0;
-  auto chain = [&](const uint32_t (&x)[kImpRows], int w0) {
+  // rows [w0, w0 + kImpRows) of the chunk starting at wc (rows past we skipped)
+  auto chain = [&](const uint32_t (&x)[kImpRows], int w0, int wc, int we) {
 #pragma unroll
     for (int r = 0; r < kImpRows; ++r) {
       const int w = w0 + r;
-      if (w < W) {
+      if (w < we) {
         const float L = __uint_as_float(x[r]);
         if constexpr (MODE == HC_SCORE_SNAPKV)
-          acc = __builtin_fma(det_exp_nonpos((double)L - (double)sm_m[w]), sm_inv[w], acc);
+          acc = __builtin_fma(det_exp_nonpos((double)L - (double)sm_m[w - wc]), sm_inv[w - wc], acc);
         else
           acc = acc + (double)L;
       }
     }
   };
-  uint32_t xa[kImpRows], xb[kImpRows];
-  load(xa, 0);
-  for (int w0 = 0; w0 < W; w0 += 2 * kImpRows) {
-    load(xb, w0 + kImpRows);
-    chain(xa, w0);
-    load(xa, w0 + 2 * kImpRows);
-    chain(xb, w0 + kImpRows);
+  for (int wc = 0; wc < W; wc += kMaxW) {
+    const int we = min(W, wc + kMaxW);
+    if constexpr (MODE == HC_SCORE_SNAPKV) {
+      __syncthreads();  // the previous chunk's statistics are no longer read
+      for (int w = wc + (int)threadIdx.x; w < we; w += blockDim.x) {
+        sm_m[w - wc] = key_to_float(rmax[bh * W + w]);
+        const double l = (double)lsum[bh * W + w] * 0x1p-44;
+        sm_inv[w - wc] = 1.0 / l;
+      }
+      __syncthreads();
+    }
+    uint32_t xa[kImpRows], xb[kImpRows];
+    load(xa, wc);
+    for (int w0 = wc; w0 < we; w0 += 2 * kImpRows) {
+      load(xb, w0 + kImpRows);
+      chain(xa, w0, wc, we);
+      load(xa, w0 + 2 * kImpRows);
+      chain(xb, w0 + kImpRows, wc, we);
+    }
   }
   sm_imp[threadIdx.x] = sv ? (float)acc : 0.f;
   __syncthreads();
@@ -502,7 +508,8 @@ extern "C" int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64
   HC_REQUIRE(mode == HC_SCORE_SNAPKV || mode == HC_SCORE_RAWSUM, "score: bad mode %d", mode);
   HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && S > 0 && D > 0 && W > 0, "score: empty shape");
   HC_REQUIRE(W <= S, "score: window %lld exceeds S %lld", (long long)W, (long long)S);
-  HC_REQUIRE(W <= kMaxW, "score: window %lld above the supported %d rows", (long long)W, kMaxW);
+  HC_REQUIRE(W * S * 4 < ((int64_t)1 << 31), "score: window x keys (%lld x %lld) logits above 2 GiB per head",
+             (long long)W, (long long)S);
   HC_REQUIRE(D % 16 == 0 && D <= 512, "score: head_dim %lld must be a multiple of 16 and <= 512", (long long)D);
   HC_REQUIRE(S <= ((int64_t)1 << 19), "score: S %lld above 2^19 (fixed-point normaliser range)", (long long)S);
   HC_REQUIRE(B <= 65535 && Hk * cdiv(W, kRowBlk) <= 65535, "score: grid too large");

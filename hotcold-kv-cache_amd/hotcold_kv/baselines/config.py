@@ -8,9 +8,8 @@ class PressConfig:
     """KV-cache compression settings.
 
     method: "snapkv" (observation-window importance + pooling, compressed at
-        prefill) or "pyramidkv" (SnapKV importance, per-layer pyramidal budget).
-        "h2o" is accepted by the reference but is not part of the MI355X hot
-        tier; PressLayerState rejects it.
+        prefill), "pyramidkv" (SnapKV importance, per-layer pyramidal budget)
+        or "h2o" (accumulated attention, re-evicted every decode step).
     max_capacity: KV budget per layer including the recent window (the mean
         budget for PyramidKV).
     window_size: observation window; also the recent window that is kept.

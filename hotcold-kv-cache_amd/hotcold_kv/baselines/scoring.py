@@ -1,8 +1,8 @@
-"""SnapKV scoring and selection with the reference's function names
+"""SnapKV / H2O scoring and selection with the reference's function names
 (src/hotcold_kv/baselines/scoring.py).
 
-snapkv_importance, keep_index and gather_kv run on the gfx950 kernels
-(device tensors only).  The small layout helpers (repeat_kv, the GQA
+snapkv_importance, h2o_prefill_scores, keep_index and gather_kv run on the
+gfx950 kernels (device tensors only).  The small layout helpers (repeat_kv, the GQA
 reductions, pool1d, gather_scores) are plain tensor ops that the kernels
 fuse; they are kept for API compatibility.
 """
@@ -56,6 +56,14 @@ def snapkv_importance(q_post, keys, window_size, scaling, kernel_size, pooling):
     GQA-mean window queries, causal window logits, softmax over keys, sum over
     the window, pooling -- one fused pipeline on the device."""
     return ops.snapkv_scores(q_post, keys, window_size, scaling, kernel_size, pooling)
+
+
+def h2o_prefill_scores(q_post, keys, scaling, chunk=512):
+    """H2O accumulated attention over the whole prefill per KV head (B,Hk,S)
+    float32 (scoring.py:82-107): causal softmax of every query row summed per
+    query head, then averaged over the query heads of each KV head.  `chunk`
+    is the reference's query-row chunking; the device pipeline needs none."""
+    return ops.h2o_prefill_scores(q_post, keys, scaling)
 
 
 def keep_index(scores, window_size, budget):

@@ -241,6 +241,49 @@ def decode_attention_append(q, k, v, k_new, v_new, scaling, pre=None, pos=None, 
     return out
 
 
+def decode_attention_h2o(q, k, v, scaling, acc, out=None, num_splits=0):
+    """Decode attention of q (B,Hq,D) or (B,Hq,1,D) over k/v (B,Hk,S,D) that
+    adds each key's attention probability, averaged over the query heads of
+    its KV head, to acc (B,Hk,>=S) fp32; key S-1 (this step's token) starts
+    from zero -- H2O's accumulated attention (layer_state.py:102-114).
+    Returns out (B,Hq,D)."""
+    _require_device(q, k, v, acc)
+    lib = N.lib()
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise RuntimeError(f"decode_attention_h2o: expected one query token, got q {tuple(q.shape)}")
+        q = q[:, :, 0, :]
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    k = _rows4(k, "key")
+    v = _rows4(v, "value")
+    B, Hq, D = q.shape
+    _, Hk, S, _ = k.shape
+    if tuple(v.shape) != tuple(k.shape) or k.shape[0] != B or k.shape[3] != D or k.dtype != q.dtype \
+            or v.dtype != q.dtype:
+        raise RuntimeError("decode_attention_h2o: q, k, v shapes / dtypes do not match")
+    if acc.dtype != torch.float32 or acc.dim() != 3 or tuple(acc.shape[:2]) != (B, Hk) or acc.shape[2] < S \
+            or acc.stride(2) != 1:
+        raise RuntimeError(f"decode_attention_h2o: acc must be (B,Hk,>=S) fp32 with unit last stride; "
+                           f"got {tuple(acc.shape)} {acc.dtype}")
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+    nbytes = lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, 1)
+    ws = _workspace("decode", q.device, nbytes)
+    rc = lib.hc_decode_attn_h2o(
+        N.dtype_code(q.dtype), B, Hq, Hk, D, S,
+        _ptr(q), q.stride(0), q.stride(1),
+        _ptr(k), k.stride(0), k.stride(1), k.stride(2),
+        _ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        float(scaling),
+        _ptr(out), out.stride(0), out.stride(1),
+        _ptr(acc), acc.stride(0), acc.stride(1),
+        _ptr(ws), ws.numel(), int(num_splits),
+        _stream_handle(q.device))
+    N.check(rc, "hc_decode_attn_h2o")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # SnapKV compaction
 # ---------------------------------------------------------------------------
@@ -291,6 +334,31 @@ def snapkv_scores(q_post, keys, window_size, scaling, kernel_size=7, pooling="ma
         _ptr(scores), _ptr(ws), ws.numel(), _stream_handle(keys.device))
     N.check(rc, "hc_snapkv_score")
     return scores
+
+
+def h2o_prefill_scores(q_post, keys, scaling, max_workspace_bytes=2 << 30):
+    """H2O accumulated attention of the whole prompt per KV head, fp32
+    (B,Hk,S) (scoring.py:82-107): for every key, the causal softmax
+    probabilities of all query rows summed, per query head, then averaged over
+    the query heads of its KV head.  It is the window score with the window
+    covering the prompt, one query head per "KV head" and no pooling, so it
+    runs on the exact window-score kernels (bit-defined like SnapKV's) over
+    keys repeated per query head, followed by the group mean.  Query heads go
+    in chunks whose logits workspace fits max_workspace_bytes."""
+    _require_device(q_post, keys)
+    B, Hq, S, D = q_post.shape
+    Hk = keys.shape[1]
+    if Hq % Hk != 0:
+        raise ValueError(f"h2o_prefill_scores: Hq ({Hq}) must be a multiple of Hk ({Hk})")
+    G = Hq // Hk
+    per_group = G * int(N.lib().hc_snapkv_score_workspace_size(B, 1, S, D, S))
+    groups = max(1, min(Hk, max_workspace_bytes // max(per_group, 1)))     # KV groups per chunk
+    per_q = torch.empty((B, Hq, S), dtype=torch.float32, device=keys.device)
+    for g0 in range(0, Hk, groups):
+        g1 = min(Hk, g0 + groups)
+        k_rep = keys[:, g0:g1].repeat_interleave(G, dim=1).contiguous()   # one key head per query head
+        per_q[:, g0 * G:g1 * G] = snapkv_scores(q_post[:, g0 * G:g1 * G], k_rep, S, scaling, 1, "maxpool")
+    return head_mean(per_q.view(B * Hk, G, S)).view(B, Hk, S)
 
 
 def head_mean(scores):

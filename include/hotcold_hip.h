@@ -121,6 +121,24 @@ int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t 
                           void* stream);
 
 /*
+ * Decode attention that also accumulates H2O scores (layer_state.py:55-65,
+ * 102-114): after attending (as hc_decode_attn, no mask), for every key s the
+ * attention probability averaged over the G query heads of each KV head
+ * (_reduce_probs_to_kv, scoring.py:29-37) is added to acc[b*a_sb + hk*a_sh + s]
+ * (fp32).  Key S-1 is the token appended this step: its score starts from zero
+ * (the zero column of layer_state.py:108-111).  The workspace is
+ * hc_decode_attn_workspace_size(.., S, .., with_evict = 1).
+ */
+int hc_decode_attn_h2o(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                       const void* q, int64_t q_sb, int64_t q_sh,
+                       const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                       const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                       double scaling,
+                       void* out, int64_t o_sb, int64_t o_sh,
+                       float* acc, int64_t a_sb, int64_t a_sh,
+                       void* workspace, int64_t workspace_bytes, int64_t num_splits, void* stream);
+
+/*
  * Window importance scores per KV head, fp32 [B][Hk][S] (row stride S).
  * Replaces snapkv_importance (scoring.py:50-79) with _group_query_to_kv
  * (scoring.py:17-26) and pool1d (scoring.py:40-47) in HC_SCORE_SNAPKV mode,

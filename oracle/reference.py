@@ -113,6 +113,46 @@ def head_mean(x):
 
 
 # ---------------------------------------------------------------------------
+# H2O (scoring.py:82-107, layer_state.py:55-65, 102-114)
+# ---------------------------------------------------------------------------
+def h2o_prefill_scores(q, k, scaling):
+    """H2O prefill scores (B,Hk,S) float32 under the bit-defined contract: the
+    window score of every query head with the window covering the whole
+    prompt (causal rows 0..S-1, exact-sum softmax, fp64 row sum, no pooling)
+    against its own KV head's keys, then the head mean over each group."""
+    B, Hq, S, D = q.shape
+    Hk = k.shape[1]
+    G = Hq // Hk
+    per_q = window_scores(q, repeat_kv(k, G), S, scaling, 1, "maxpool")        # (B,Hq,S)
+    return head_mean(per_q.reshape(B * Hk, G, S)).reshape(B, Hk, S)
+
+
+def h2o_prefill_scores_f64(q, k, scaling):
+    """The same quantity in plain fp64 (closed form, no rounding contract)."""
+    qd, kd = q.double(), k.double()
+    B, Hq, S, D = qd.shape
+    G = Hq // k.shape[1]
+    logits = torch.matmul(qd, repeat_kv(kd, G).transpose(2, 3)) * scaling
+    causal = torch.ones(S, S, dtype=torch.bool).triu(1)
+    probs = torch.softmax(logits.masked_fill(causal, float("-inf")), dim=-1)
+    acc = probs.sum(dim=2)                                                    # (B,Hq,S)
+    return acc.view(B, Hq // G, G, S).mean(dim=2)
+
+
+def h2o_decode_probs(q, k, scaling):
+    """Attention probabilities of one query token (B,Hq,1,D) over k (B,Hk,S,D),
+    fp64, averaged over the query heads of each KV head -> (B,Hk,S)
+    (_attn_with_probs + _reduce_probs_to_kv, layer_state.py:55-65,
+    scoring.py:29-37)."""
+    qd, kd = q.double(), k.double()
+    B, Hq = qd.shape[:2]
+    G = Hq // kd.shape[1]
+    logits = torch.matmul(qd, repeat_kv(kd, G).transpose(2, 3)) * scaling     # (B,Hq,1,S)
+    probs = torch.softmax(logits, dim=-1)[:, :, 0]
+    return probs.view(B, Hq // G, G, -1).mean(dim=2)
+
+
+# ---------------------------------------------------------------------------
 # Literal fp32 restatements of the reference scoring (scoring.py)
 # ---------------------------------------------------------------------------
 def repeat_kv(x, n_rep):

@@ -11,6 +11,8 @@ range 0.1 so that attention is far from uniform.
 
 import math
 
+import numpy as np
+
 import pytest
 import torch
 from transformers import LlamaConfig, LlamaForCausalLM
@@ -252,6 +254,62 @@ def _press_cycle(method, dtype, B=2, Hq=8, Hk=2, S=200, D=16, budget=64, window=
     return st
 
 
+def _rows_to_index(buf, full):
+    """Per (b, head) indices into full (B,H,n,D) of the rows of buf (B,H,m,D)."""
+    B, H, m, _ = buf.shape
+    idx = torch.empty((B, H, m), dtype=torch.long)
+    for b in range(B):
+        for h in range(H):
+            eq = (buf[b, h][:, None, :] == full[b, h][None, :, :]).all(-1)     # (m, n)
+            assert (eq.sum(1) == 1).all()
+            idx[b, h] = eq.float().argmax(1)
+    return idx
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_h2o_cycle_holds_budget_and_tracks_oracle(dtype):
+    """tests/test_baselines.py:82-87 (the length stays at the budget, scores
+    are (B,Hk,budget)) with every step checked against the oracle: prefill
+    keeps and scores bit-exact; then each decode step's output within the
+    dtype tolerance, the accumulated scores within a few fp32/fp16 rounding
+    steps, and the kept set equal to the oracle's except at near-ties (where
+    the oracle follows the kernel's choice)."""
+    B, Hq, Hk, S, D, budget, window, steps = 2, 8, 2, 200, 16, 64, 16, 60
+    n_rep, scaling = Hq // Hk, 1.0 / math.sqrt(D)
+    g = torch.Generator().manual_seed(51)
+    st = PressLayerState(method="h2o", budget=budget, window_size=window, kernel_size=7, pooling="maxpool")
+    q, k, v = (torch.randn(B, h, S, D, generator=g).to(dtype) for h in (Hq, Hk, Hk))
+    st.prefill(q.to(DEV), k.to(DEV), v.to(DEV), n_rep, scaling)
+    sc = ref.h2o_prefill_scores(q, k, scaling)
+    keep = ref.keep_index(sc, window, budget)
+    kk, vv = ref.gather_kv(k, keep), ref.gather_kv(v, keep)
+    assert torch.equal(st.keys.cpu(), kk) and torch.equal(st.values.cpu(), vv)
+    assert torch.equal(st.scores.cpu(), sc.gather(2, keep))
+    sc = sc.gather(2, keep).double()
+    tol_out = 2e-3 if dtype == torch.float16 else 1e-5
+    tol_sc = 3e-3 if dtype == torch.float16 else 2e-5
+    for t in range(steps):
+        q1, k1, v1 = (torch.randn(B, h, 1, D, generator=g).to(dtype) for h in (Hq, Hk, Hk))
+        out1 = st.decode(q1.to(DEV), k1.to(DEV), v1.to(DEV), n_rep, scaling)
+        kk, vv = torch.cat([kk, k1], 2), torch.cat([vv, v1], 2)
+        want = ref.decode_attention(q1, kk, vv, scaling)
+        assert np.abs(out1[:, :, 0].float().cpu().numpy() - want).max() <= tol_out, t
+        sc = torch.cat([sc, torch.zeros(B, Hk, 1, dtype=torch.float64)], 2) + ref.h2o_decode_probs(q1, kk, scaling)
+        assert st.get_seq_length() == budget and st.scores.shape == (B, Hk, budget)
+        got_keep = _rows_to_index(st.keys.cpu(), kk)
+        want_keep = ref.keep_index(sc.float(), window, budget)
+        for b in range(B):
+            for h in range(Hk):
+                a, w_ = set(got_keep[b, h].tolist()), set(want_keep[b, h].tolist())
+                if a != w_:   # only near-ties may differ
+                    n = sc.shape[2]       # the recent window is always kept: ties are among the prefix
+                    kth = sc[b, h, :n - window].sort(descending=True).values[budget - window - 1]
+                    for i in a ^ w_:
+                        assert abs(float(sc[b, h, i]) - float(kth)) <= 4 * tol_sc * max(1.0, float(kth)), (t, b, h)
+        kk, vv, sc = ref.gather_kv(kk, got_keep), ref.gather_kv(vv, got_keep), sc.gather(2, got_keep)
+        assert torch.allclose(st.scores.cpu().double(), sc, rtol=tol_sc, atol=tol_sc * 1e-2), t
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_snapkv_cycle(dtype):
     st = _press_cycle("snapkv", dtype, budget=64, steps=40)
@@ -262,7 +320,7 @@ def test_pyramidkv_cycle():
     _press_cycle("pyramidkv", torch.float16, budget=80, steps=20)
 
 
-@pytest.mark.parametrize("method", ["snapkv", "pyramidkv"])
+@pytest.mark.parametrize("method", ["snapkv", "pyramidkv", "h2o"])
 def test_press_patch_matches_stock_without_compression(model_and_ref, method):
     model, ids, (ref_prefill, ref_logits, fed), dtype = model_and_ref
     install_press_patch()
@@ -295,5 +353,26 @@ def test_press_patch_compresses_to_budget(model_and_ref):
     assert (prefill - ref_prefill).abs().max().item() < TOL[dtype]
     for layer in cache.layers:
         assert layer.state.get_seq_length() == 64 + 5
+        assert layer.get_seq_length() == ids.shape[1] + 5
+    assert all(torch.isfinite(lg).all() for lg in logits)
+
+
+def test_press_patch_h2o_holds_budget_in_the_model(model_and_ref):
+    """H2O inside the patched model: prompt compressed to the budget, then
+    re-evicted every decode step (test_baselines.py:82-87 at model level)."""
+    model, ids, (ref_prefill, _, fed), dtype = model_and_ref
+    install_press_patch()
+    try:
+        cache = build_press_cache(model, PressConfig(method="h2o", max_capacity=64, window_size=16))
+        set_active_press_cache(cache)
+        with torch.inference_mode():
+            prefill, logits, _ = decode_trace(model, ids, cache, 5, forced=fed[:5])
+    finally:
+        uninstall_press_patch()
+        set_active_press_cache(None)
+    assert (prefill - ref_prefill).abs().max().item() < TOL[dtype]
+    for layer in cache.layers:
+        assert layer.state.get_seq_length() == 64
+        assert layer.state.scores.shape[-1] == 64
         assert layer.get_seq_length() == ids.shape[1] + 5
     assert all(torch.isfinite(lg).all() for lg in logits)

@@ -356,8 +356,11 @@ def test_press_config_checks():
         PressConfig(method="streaming")
     with pytest.raises(AssertionError):
         PressConfig(window_size=512, max_capacity=512)
-    with pytest.raises(NotImplementedError):
-        PressLayerState("h2o", 64, 16, 7, "maxpool")
+    PressConfig(method="h2o")
+    st = PressLayerState("h2o", 64, 16, 7, "maxpool")
+    assert st.scores is None and st.get_seq_length() == 0
+    with pytest.raises(ValueError):
+        PressLayerState("streaming", 64, 16, 7, "maxpool")
 
 
 def test_gqa_reduction_shapes():

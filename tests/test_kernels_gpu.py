@@ -365,6 +365,48 @@ def test_append_rows():
 # ---------------------------------------------------------------------------
 # Inject (re-RoPE into the held slot)
 # ---------------------------------------------------------------------------
+H2O_CASES = [
+    # B, Hq, Hk, S, D, dtype
+    (2, 8, 2, 200, 16, torch.float32),      # reference test geometry (test_baselines.py:46)
+    (2, 8, 2, 200, 16, torch.float16),
+    (1, 32, 8, 333, 64, torch.float16),
+    (1, 8, 8, 97, 128, torch.bfloat16),
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S,D,dtype", H2O_CASES)
+def test_h2o_prefill_scores_bit_exact(B, Hq, Hk, S, D, dtype):
+    q, k = _randn((B, Hq, S, D), 41, dtype), _randn((B, Hk, S, D), 42, dtype)
+    want = ref.h2o_prefill_scores(q, k, 0.125)
+    got = ops.h2o_prefill_scores(q.to(DEV), k.to(DEV), 0.125)
+    assert torch.equal(got.cpu(), want)
+    # query heads in chunks of one KV group: the same bits
+    small = ops.h2o_prefill_scores(q.to(DEV), k.to(DEV), 0.125, max_workspace_bytes=1)
+    assert torch.equal(small.cpu(), want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("splits", [0, 1, 5])
+def test_decode_attention_h2o_accumulates_group_mean_probs(dtype, splits):
+    """out as decode attention; acc[:S-1] += mean-over-group probabilities,
+    acc[S-1] = its probability (this step's token starts from zero)."""
+    B, Hq, Hk, S, D, cap = 2, 32, 8, 430, 128, 500
+    q, k, v = _randn((B, Hq, 1, D), 43, dtype), _randn((B, Hk, S, D), 44, dtype), _randn((B, Hk, S, D), 45, dtype)
+    acc0 = torch.rand((B, Hk, cap), generator=torch.Generator().manual_seed(46)) * 10
+    acc = acc0.to(DEV)
+    out = ops.decode_attention_h2o(q.to(DEV), k.to(DEV), v.to(DEV), 0.088, acc[:, :, :S], num_splits=splits)
+    want_out = ref.decode_attention(q, k, v, 0.088)
+    assert np.abs(out.float().cpu().numpy() - want_out).max() <= TOL[dtype]
+    probs = ref.h2o_decode_probs(q, k, 0.088)
+    want = acc0.double().clone()
+    want[:, :, S - 1] = 0
+    want[:, :, :S] += probs
+    got = acc.cpu().double()
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    assert torch.allclose(got[:, :, :S], want[:, :, :S], rtol=tol, atol=tol * 1e-2)
+    assert torch.equal(got[:, :, S:], acc0[:, :, S:].double())   # rows past S untouched
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("to_host", [False, True])
 def test_gather_evict_upcast_and_stage(dtype, to_host):

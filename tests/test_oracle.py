@@ -370,3 +370,42 @@ def test_golden_fixtures_reproduce():
         # the frozen vectors also satisfy the closed form they were pinned by
         f64 = ref.snapkv_importance_f64(q, k, W, sc, pool, "maxpool")
         assert np.allclose(want_scores.double().numpy(), f64, rtol=2e-7, atol=1e-9), case
+
+
+# ---------------------------------------------------------------------------
+# H2O scores (scoring.py:82-107)
+# ---------------------------------------------------------------------------
+def test_h2o_prefill_scores_against_fp64_closed_form():
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(2, 8, 40, 16, generator=g)
+    k = torch.randn(2, 2, 40, 16, generator=g)
+    got = ref.h2o_prefill_scores(q, k, 0.25)
+    want = ref.h2o_prefill_scores_f64(q, k, 0.25)
+    assert got.dtype == torch.float32 and got.shape == (2, 2, 40)
+    assert torch.allclose(got.double(), want, rtol=1e-6, atol=1e-7)
+    # every causal row's probabilities sum to one: the scores of a head sum to S
+    assert torch.allclose(got.double().sum(-1), torch.full((2, 2), 40.0, dtype=torch.float64), rtol=1e-6)
+    # key 0 is the only key row 0 sees
+    assert (got[..., 0] >= 1.0 - 1e-6).all()
+
+
+def test_h2o_prefill_scores_equal_keys_harmonic_tail():
+    # equal keys: row i spreads 1/(i+1) over keys 0..i, so key j scores
+    # sum_{i>=j} 1/(i+1) in every head
+    S = 24
+    q = torch.randn(1, 4, S, 8, generator=torch.Generator().manual_seed(32))
+    k = torch.ones(1, 1, S, 8).mul(0.5)
+    got = ref.h2o_prefill_scores(q, k, 0.3)[0, 0].double()
+    want = torch.tensor([sum(1.0 / (i + 1) for i in range(j, S)) for j in range(S)], dtype=torch.float64)
+    assert torch.allclose(got, want, rtol=1e-6)
+
+
+def test_h2o_decode_probs_sum_to_one_and_match_attention():
+    g = torch.Generator().manual_seed(33)
+    q, k = torch.randn(2, 8, 1, 16, generator=g), torch.randn(2, 2, 30, 16, generator=g)
+    p = ref.h2o_decode_probs(q, k, 0.25)
+    assert torch.allclose(p.sum(-1), torch.ones(2, 2, dtype=torch.float64))
+    v = torch.randn(2, 2, 30, 16, generator=g)
+    out = ref.decode_attention(q, k, v, 0.25)                 # (B,Hq,D) fp64 numpy
+    probs = torch.softmax(torch.matmul(q.double(), ref.repeat_kv(k, 4).double().transpose(2, 3)) * 0.25, -1)
+    assert np.allclose(out, torch.matmul(probs, ref.repeat_kv(v, 4).double())[:, :, 0].numpy(), atol=1e-12)
