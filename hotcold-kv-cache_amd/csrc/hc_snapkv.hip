@@ -145,17 +145,27 @@ struct KOperand<float> {
 // fp64 query block is staged in LDS once and reused for kLogitChunks chunks
 // of 128 keys; per chunk each wave covers 32 keys (two 16-key blocks) x 32
 // window rows (two 16-row blocks).  K loads are unconditional buffer loads
-// one chunk of dims ahead (rows past S read zeros).  Each 32x32 fp32 tile is
-// staged in LDS and written as full 128-byte row segments.
-constexpr int kLogitChunks = 4;
+// ahead of use (rows past S read zeros).  With the head dim known at compile
+// time (DC > 0) the dim loop is unrolled over a register ring of kKRing
+// slices, kKRing - 1 of them in flight while one is multiplied, and the ring
+// runs on into the next chunk; for any other head dim (DC == 0) it is a
+// two-slot ping-pong over a runtime loop.  Logits are stored straight from
+// the accumulators with unconditional buffer stores (masked lanes address
+// kOob), so the compiler's vmcnt waits for the ring never have to drain the
+// stores.  The LDS q block (33 KB at D = 128) allows four workgroups per CU;
+// the occupancy ceiling of 4 tells the scheduler not to trade the ring's
+// registers for occupancy it cannot get.  16 chunks per workgroup make the
+// 8k, 32-layer grid exactly one round of 4 workgroups per CU.
+constexpr int kLogitChunks = 16;
+constexpr int kKRing = 4;
 
-template <typename T, int MODE>
-__global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, int64_t k_sb, int64_t k_sh,
-                                                     int64_t k_ss, uint32_t k_bytes, const double* __restrict__ qf,
-                                                     int Hk, int S, int D, int W, int wpad, double scaling,
-                                                     float* __restrict__ logits, uint32_t* __restrict__ rmax) {
+template <typename T, int MODE, int DC>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void logits_kernel(
+    const T* __restrict__ k, int64_t k_sb, int64_t k_sh, int64_t k_ss, uint32_t k_bytes,
+    const double* __restrict__ qf, int Hk, int S, int Drt, int W, int wpad, double scaling,
+    float* __restrict__ logits, uint32_t* __restrict__ rmax) {
+  const int D = DC > 0 ? DC : Drt;
   extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
-  __shared__ float tile[4][kRowBlk][33];
   __shared__ float red[4][kRowBlk];
   const int nrb = wpad / kRowBlk;
   const int rb = blockIdx.y % nrb;
@@ -174,21 +184,41 @@ __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, in
   const uint32_t sl = KOperand<T>::sel(kk);
   const double* q0 = sq + col * ld + kk;         // rows 0..15 of the block
   const double* q1 = sq + (16 + col) * ld + kk;  // rows 16..31
-  const int rr = lane >> 3, kq = 4 * (lane & 7);
-  float mrow[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+  // this (b, h)'s W x S logits; W * S * 4 < 2^31 is checked by the host
+  const __amdgpu_buffer_rsrc_t lrs = make_rsrc(logits + bh * W * S, (uint32_t)((int64_t)W * S * 4));
+  float mrow[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) mrow[j] = -INFINITY;
 
-  KOperand<T> ca, cb, na, nb;
+  constexpr int NS = DC / DS;  // dim slices per key chunk (compile-time D)
+  // the ring runs on into the next chunk: slice s of every chunk must land in
+  // slot s % kKRing, so the slices per chunk are a multiple of the ring
+  static_assert(DC == 0 || (DC % (2 * DS) == 0 && NS % kKRing == 0), "ring must tile the slices of a chunk");
+  KOperand<T> ka[kKRing], kb[kKRing];
   int key0 = blockIdx.x * (kChunkM * kLogitChunks) + wave * 32;
   uint32_t off0 = key0 + col < S ? (uint32_t)(key0 + col) * rowb : kOob;
   uint32_t off1 = key0 + 16 + col < S ? (uint32_t)(key0 + 16 + col) * rowb : kOob;
-  // first K chunk in flight before the q block is staged
-  ca.load(krs, off0, 0, kk);
-  cb.load(krs, off1, 0, kk);
+  // first K slices in flight before the q block is staged
+  if constexpr (DC > 0) {
+#pragma unroll
+    for (int j = 0; j < kKRing - 1; ++j) {
+      ka[j].load(krs, off0, j * DS, kk);
+      kb[j].load(krs, off1, j * DS, kk);
+    }
+  } else {
+    ka[0].load(krs, off0, 0, kk);
+    kb[0].load(krs, off1, 0, kk);
+  }
   const double* qsrc = qf + (bh * wpad + w0) * D;
   for (int i = threadIdx.x; i < kRowBlk * D; i += 256) sq[(i / D) * ld + (i % D)] = qsrc[i];
   __syncthreads();
 
-  for (int c = 0; c < kLogitChunks; ++c) {
+  // wave-uniform chunk count: short prompts stop at their last chunk
+  const int nch = key0 < S ? min(kLogitChunks, (S - key0 + kChunkM - 1) / kChunkM) : 0;
+  for (int c = 0; c < nch; ++c) {
+    // the q reads repeat for every chunk; keep them inside the loop (hoisted,
+    // all D/2 of them would hold 2*D registers for the kernel's lifetime)
+    __asm__ volatile("" ::: "memory");
     doublex4 acc00 = {0.0, 0.0, 0.0, 0.0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
     auto steps = [&](const KOperand<T>& xa, const KOperand<T>& xb, int d0) {
 #pragma unroll
@@ -208,17 +238,36 @@ __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, in
     const int nkey0 = key0 + kChunkM;
     const uint32_t noff0 = nkey0 + col < S ? (uint32_t)(nkey0 + col) * rowb : kOob;
     const uint32_t noff1 = nkey0 + 16 + col < S ? (uint32_t)(nkey0 + 16 + col) * rowb : kOob;
-    for (int d0 = 0; d0 < D; d0 += 2 * DS) {
-      na.load(krs, off0, d0 + DS, kk);
-      nb.load(krs, off1, d0 + DS, kk);
-      steps(ca, cb, d0);
-      const bool last = d0 + 2 * DS >= D;
-      ca.load(krs, last ? noff0 : off0, last ? 0 : d0 + 2 * DS, kk);
-      cb.load(krs, last ? noff1 : off1, last ? 0 : d0 + 2 * DS, kk);
-      steps(na, nb, d0 + DS);
+    if constexpr (DC > 0) {
+      // slice j is multiplied while slices j+1 .. j+kKRing-1 are in flight;
+      // the loads past the last slice start the next chunk's rows
+#pragma unroll
+      for (int j = 0; j < NS; ++j) {
+        const int jl = j + kKRing - 1;
+        if (jl < NS) {
+          ka[jl % kKRing].load(krs, off0, jl * DS, kk);
+          kb[jl % kKRing].load(krs, off1, jl * DS, kk);
+        } else {
+          ka[jl % kKRing].load(krs, noff0, (jl - NS) * DS, kk);
+          kb[jl % kKRing].load(krs, noff1, (jl - NS) * DS, kk);
+        }
+        steps(ka[j % kKRing], kb[j % kKRing], j * DS);
+      }
+    } else {
+      for (int d0 = 0; d0 < D; d0 += 2 * DS) {
+        ka[1].load(krs, off0, d0 + DS, kk);
+        kb[1].load(krs, off1, d0 + DS, kk);
+        steps(ka[0], kb[0], d0);
+        const bool last = d0 + 2 * DS >= D;
+        ka[0].load(krs, last ? noff0 : off0, last ? 0 : d0 + 2 * DS, kk);
+        kb[0].load(krs, last ? noff1 : off1, last ? 0 : d0 + 2 * DS, kk);
+        steps(ka[1], kb[1], d0 + DS);
+      }
     }
 
-    // Epilogue: lane holds rows 16*nbk + kk + 4i for keys 16*mb + col.
+    // Epilogue: lane holds rows 16*nbk + kk + 4i for keys 16*mb + col.  The
+    // 16 lanes of one row store 64 contiguous bytes and the two key blocks
+    // complete the row's 128-byte segment; masked lanes store to kOob.
     const double r00[4] = {acc00[0], acc00[1], acc00[2], acc00[3]};
     const double r01[4] = {acc01[0], acc01[1], acc01[2], acc01[3]};
     const double r10[4] = {acc10[0], acc10[1], acc10[2], acc10[3]};
@@ -231,37 +280,17 @@ __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, in
         for (int mb = 0; mb < 2; ++mb) {
           const double v = nbk == 0 ? (mb == 0 ? r00[i] : r10[i]) : (mb == 0 ? r01[i] : r11[i]);
           const int w = 16 * nbk + kk + 4 * i;
-          const int kc = 16 * mb + col;
-          const int key = key0 + kc;
+          const int key = key0 + 16 * mb + col;
           float L;
           if constexpr (MODE == HC_SCORE_SNAPKV) L = (key > qpos0 + w) ? -INFINITY : (float)(v * scaling);
           else L = (float)(v / scaling);
-          tile[wave][w][kc] = (key < S && w < nw) ? L : -INFINITY;
+          const bool ok = key < S && w < nw;
+          const uint32_t bits = __float_as_uint(L);
+          bstore<4>(lrs, ok ? (uint32_t)((w0 + w) * S + key) * 4u : kOob, &bits);
+          if constexpr (MODE == HC_SCORE_SNAPKV) mrow[4 * nbk + i] = fmaxf(mrow[4 * nbk + i], ok ? L : -INFINITY);
         }
       }
     }
-    // the tile is private to this wave: its LDS accesses complete in order
-    __builtin_amdgcn_wave_barrier();
-    const bool vec = ((S & 3) == 0) && (key0 + 32 <= S);
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int w = 8 * j + rr;
-      const float x0 = tile[wave][w][kq], x1 = tile[wave][w][kq + 1];
-      const float x2 = tile[wave][w][kq + 2], x3 = tile[wave][w][kq + 3];
-      if (w < nw && key0 < S) {
-        float* dst = logits + (bh * W + w0 + w) * S + key0 + kq;
-        if (vec) {
-          *reinterpret_cast<floatx4*>(dst) = floatx4{x0, x1, x2, x3};
-        } else {
-          const float xs[4] = {x0, x1, x2, x3};
-#pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (key0 + kq + e < S) dst[e] = xs[e];
-        }
-      }
-      if constexpr (MODE == HC_SCORE_SNAPKV) mrow[j] = fmaxf(mrow[j], fmaxf(fmaxf(x0, x1), fmaxf(x2, x3)));
-    }
-    __builtin_amdgcn_wave_barrier();
     key0 = nkey0;
     off0 = noff0;
     off1 = noff1;
@@ -269,12 +298,13 @@ __global__ __launch_bounds__(256) void logits_kernel(const T* __restrict__ k, in
 
   if constexpr (MODE != HC_SCORE_SNAPKV) return;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
+  for (int j = 0; j < 8; ++j) {  // row 16*(j/4) + kk + 4*(j%4), max over the 16 key lanes
     float m = mrow[j];
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
     m = fmaxf(m, __shfl_xor(m, 4, 64));
-    if ((lane & 7) == 0) red[wave][8 * j + rr] = m;
+    m = fmaxf(m, __shfl_xor(m, 8, 64));
+    if (col == 0) red[wave][16 * (j >> 2) + kk + 4 * (j & 3)] = m;
   }
   __syncthreads();
   if (threadIdx.x < nw) {
@@ -456,18 +486,19 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
   const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
   const uint32_t k_bytes = (uint32_t)(((S - 1) * k_ss + D) * (int64_t)sizeof(T));
   const dim3 grid((unsigned)cdiv(S, (int64_t)kChunkM * kLogitChunks), (unsigned)(Hk * nrb), (unsigned)B);
+  auto launch = [&](auto kern) {
+    if (lds > 48 * 1024)
+      (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const T*)k, k_sb, k_sh, k_ss, k_bytes, (const double*)qf,
+                       (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, logits, rmax);
+  };
   if (mode == HC_SCORE_SNAPKV) {
-    if (lds > 48 * 1024)
-      (void)hipFuncSetAttribute((const void*)logits_kernel<T, HC_SCORE_SNAPKV>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((logits_kernel<T, HC_SCORE_SNAPKV>), grid, dim3(256), lds, st, (const T*)k, k_sb, k_sh, k_ss,
-                       k_bytes, (const double*)qf, (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, logits, rmax);
+    if (D == 128) launch(logits_kernel<T, HC_SCORE_SNAPKV, 128>);
+    else if (D == 64) launch(logits_kernel<T, HC_SCORE_SNAPKV, 64>);
+    else launch(logits_kernel<T, HC_SCORE_SNAPKV, 0>);
   } else {
-    if (lds > 48 * 1024)
-      (void)hipFuncSetAttribute((const void*)logits_kernel<T, HC_SCORE_RAWSUM>,
-                                hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL((logits_kernel<T, HC_SCORE_RAWSUM>), grid, dim3(256), lds, st, (const T*)k, k_sb, k_sh, k_ss,
-                       k_bytes, (const double*)qf, (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, logits, rmax);
+    // the raw sums' fp64 divides leave no registers for the unrolled ring
+    launch(logits_kernel<T, HC_SCORE_RAWSUM, 0>);
   }
   if (mode == HC_SCORE_SNAPKV) {
     const dim3 g((unsigned)cdiv(W, 4), (unsigned)Hk, (unsigned)B);
