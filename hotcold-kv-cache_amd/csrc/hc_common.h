@@ -125,28 +125,63 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 #define HC_LN2_LO 1.90821492927058770002e-10
 #define HC_INV_LN2 1.44269504088896338700e+00
 
-__device__ __forceinline__ double det_exp_nonpos(double x) {
-  if (!(x >= -708.0)) return 0.0;  // also catches -inf and NaN
-  const double kf = __builtin_rint(x * HC_INV_LN2);
-  double r = __builtin_fma(-kf, HC_LN2_HI, x);
-  r = __builtin_fma(-kf, HC_LN2_LO, r);
-  double p = 2.08767569878680989792e-09;        // 1/12!
-  p = __builtin_fma(p, r, 2.50521083854417187751e-08);   // 1/11!
-  p = __builtin_fma(p, r, 2.75573192239858906526e-07);   // 1/10!
-  p = __builtin_fma(p, r, 2.75573192239858906526e-06);   // 1/9!
-  p = __builtin_fma(p, r, 2.48015873015873015873e-05);   // 1/8!
-  p = __builtin_fma(p, r, 1.98412698412698412698e-04);   // 1/7!
-  p = __builtin_fma(p, r, 1.38888888888888888889e-03);   // 1/6!
-  p = __builtin_fma(p, r, 8.33333333333333333333e-03);   // 1/5!
-  p = __builtin_fma(p, r, 4.16666666666666666667e-02);   // 1/4!
-  p = __builtin_fma(p, r, 1.66666666666666666667e-01);   // 1/3!
-  p = __builtin_fma(p, r, 5.00000000000000000000e-01);   // 1/2!
-  p = __builtin_fma(p, r, 1.0);
-  p = __builtin_fma(p, r, 1.0);
-  // p * 2^k with k in [-1022, 0]: exact scaling, as multiplying by the
-  // double 2^k would be.
-  return __builtin_ldexp(p, (int)kf);
-}
+// The constants (ln2 split, 1/ln2, the 13 Taylor coefficients 1/12! .. 1/0!
+// highest degree first) are read once per kernel from constant memory into
+// SGPRs (DetExp::load), so each Horner step is one v_fma_f64 with an SGPR
+// operand instead of a 64-bit constant move plus v_fmac.  The out-of-range
+// test is a select, not a branch: the polynomial runs on a clamped argument
+// and the result is replaced by 0.
+static __constant__ double kDetExpConst[16] = {
+    HC_INV_LN2,
+    HC_LN2_HI,
+    HC_LN2_LO,
+    2.08767569878680989792e-09,  // 1/12!
+    2.50521083854417187751e-08,  // 1/11!
+    2.75573192239858906526e-07,  // 1/10!
+    2.75573192239858906526e-06,  // 1/9!
+    2.48015873015873015873e-05,  // 1/8!
+    1.98412698412698412698e-04,  // 1/7!
+    1.38888888888888888889e-03,  // 1/6!
+    8.33333333333333333333e-03,  // 1/5!
+    4.16666666666666666667e-02,  // 1/4!
+    1.66666666666666666667e-01,  // 1/3!
+    5.00000000000000000000e-01,  // 1/2!
+    1.0,                         // 1/1!
+    1.0,                         // 1/0!
+};
+
+struct DetExp {
+  double c[16];
+  __device__ static DetExp load() {
+    DetExp d;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) d.c[i] = kDetExpConst[i];
+    return d;
+  }
+  __device__ __forceinline__ double operator()(double x) const {
+#pragma clang fp contract(off)
+    const bool ok = x >= -708.0;  // false for -inf and NaN
+    const double xc = ok ? x : 0.0;
+    // rint(xc / ln2) by the 1.5 * 2^52 shifter: the sum's ulp is 1, so its
+    // one rounding is round-to-nearest-even of the (separately rounded)
+    // product, and the integer k sits in the low mantissa bits.
+    const double t = xc * c[0];
+    const double sh = t + 6755399441055744.0;
+    const double kf = sh - 6755399441055744.0;
+    const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
+    double r = __builtin_fma(-kf, c[1], xc);
+    r = __builtin_fma(-kf, c[2], r);
+    double p = c[3];
+#pragma unroll
+    for (int i = 4; i < 16; ++i) p = __builtin_fma(p, r, c[i]);
+    // p * 2^k with k in [-1021, 0] and p in [0.7, 1.5): the product is a
+    // normal double, so multiplying by 2^k (built from its exponent bits) is
+    // exact, as ldexp would be.
+    const double two_k = __builtin_bit_cast(double, (uint64_t)(uint32_t)((k + 1023) << 20) << 32);
+    const double e = p * two_k;
+    return ok ? e : 0.0;
+  }
+};
 
 // Fixed-point quantum of the softmax normaliser: e in [0,1] -> rint(e * 2^44).
 // fma(e, 2^44, 2^52) lands in [2^52, 2^53) where the spacing of doubles is 1,

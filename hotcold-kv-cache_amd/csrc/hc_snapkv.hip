@@ -329,11 +329,14 @@ template <bool VEC>
 __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ logits,
                                                      const uint32_t* __restrict__ rmax, int Hk, int S, int W,
                                                      uint64_t* __restrict__ lsum) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  // the wave index through readfirstlane: the row's buffer resource is then
+  // known to be wave-uniform and lives in SGPRs (no waterfall per load)
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int w = blockIdx.x * 4 + wave;
   if (w >= W) return;
   const int64_t bh = (int64_t)blockIdx.z * Hk + blockIdx.y;
-  const float m = key_to_float(rmax[bh * W + w]);
+  const double md = (double)key_to_float(rmax[bh * W + w]);
+  const DetExp dexp = DetExp::load();
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + (bh * W + w) * S, (uint32_t)S * 4u);
   const int nstep = (S + 255) / 256;
   uint64_t acc[4] = {0, 0, 0, 0};
@@ -357,7 +360,7 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ l
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float L = key + e < S ? __uint_as_float(x[j][e]) : -INFINITY;
-        acc[e] += det_fix(det_exp_nonpos((double)L - (double)m));
+        acc[e] += det_fix(dexp((double)L - md));
       }
     }
   }
@@ -402,17 +405,22 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
       bload<4>(rs, (base == kOob || w0 + r >= W) ? kOob : base + (uint32_t)(w0 + r) * rowb, &dst[r]);
   };
   double acc = 0.0;
-  // rows [w0, w0 + kImpRows) of the chunk starting at wc (rows past we skipped)
+  const DetExp dexp = DetExp::load();
+  // rows [w0, w0 + kImpRows) of the chunk starting at wc.  Rows past we add
+  // an exact zero without a branch: their exponent argument is -inf, so
+  // e = 0 and fma(0, inv, acc) = acc (acc >= +0, inv finite: a staged row).
   auto chain = [&](const uint32_t (&x)[kImpRows], int w0, int wc, int we) {
 #pragma unroll
     for (int r = 0; r < kImpRows; ++r) {
       const int w = w0 + r;
-      if (w < we) {
-        const float L = __uint_as_float(x[r]);
-        if constexpr (MODE == HC_SCORE_SNAPKV)
-          acc = __builtin_fma(det_exp_nonpos((double)L - (double)sm_m[w - wc]), sm_inv[w - wc], acc);
-        else
-          acc = acc + (double)L;
+      const bool in = w < we;  // wave-uniform
+      const int wi = in ? w - wc : 0;
+      const float L = __uint_as_float(x[r]);
+      if constexpr (MODE == HC_SCORE_SNAPKV) {
+        const double xe = in ? (double)L - (double)sm_m[wi] : -INFINITY;
+        acc = __builtin_fma(dexp(xe), sm_inv[wi], acc);
+      } else {
+        acc = acc + (in ? (double)L : 0.0);
       }
     }
   };
