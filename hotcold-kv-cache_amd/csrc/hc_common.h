@@ -116,9 +116,9 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 // Cody-Waite argument reduction x = k*ln2 + r with the two-part ln2 split of
 // fdlibm (ln2_hi has 32 significant bits so k*ln2_hi is exact for |k| < 2^21),
 // then the degree-12 Taylor polynomial of exp(r) on |r| <= ln2/2 in Horner
-// form, then scaling by 2^k built from the exponent bits.  Every step is an
-// IEEE-754 binary64 fma/mul/rint, so any conforming implementation (this
-// kernel, the C restatement used for testing) produces identical bits.
+// form, then the exact scaling by 2^k.  Every step is an IEEE-754 binary64
+// fma/mul/add with round-to-nearest-even, so any conforming implementation
+// (this kernel, the C restatement used for testing) produces identical bits.
 // Inputs below -708 return 0 (their fixed-point contribution is 0 anyway).
 // ---------------------------------------------------------------------------
 #define HC_LN2_HI 6.93147180369123816490e-01
@@ -131,7 +131,7 @@ __device__ __forceinline__ uint64_t wave_sum_u64(uint64_t v) {
 // operand instead of a 64-bit constant move plus v_fmac.  The out-of-range
 // test is a select, not a branch: the polynomial runs on a clamped argument
 // and the result is replaced by 0.
-static __constant__ double kDetExpConst[16] = {
+static __constant__ double kDetExpConst[18] = {
     HC_INV_LN2,
     HC_LN2_HI,
     HC_LN2_LO,
@@ -148,50 +148,70 @@ static __constant__ double kDetExpConst[16] = {
     5.00000000000000000000e-01,  // 1/2!
     1.0,                         // 1/1!
     1.0,                         // 1/0!
+    17592186044416.0,            // 2^44, the fixed-point quantum's inverse
+    4503599627370496.0,          // 2^52
 };
 
 struct DetExp {
-  double c[16];
+  double c[18];
   __device__ static DetExp load() {
     DetExp d;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) d.c[i] = kDetExpConst[i];
+    for (int i = 0; i < 18; ++i) d.c[i] = kDetExpConst[i];
     return d;
   }
-  __device__ __forceinline__ double operator()(double x) const {
+  // Polynomial part for max(x, -708): returns p in [0.7, 1.5) and k + BIAS,
+  // k in [-1021, 0], with exp = p * 2^k.
+  // The shifter is 1.5 * 2^52 + bias for an even bias: RNE(t + bias) =
+  // RNE(t) + bias, so the low mantissa bits hold k + bias while kf is exactly
+  // rint(t).
+  template <int BIAS>
+  __device__ __forceinline__ double poly(double x, uint32_t& kb) const {
 #pragma clang fp contract(off)
-    const bool ok = x >= -708.0;  // false for -inf and NaN
-    const double xc = ok ? x : 0.0;
+    static_assert(BIAS % 2 == 0 && BIAS >= 0 && BIAS < 1024, "even exponent bias");
+    constexpr double kShift = 6755399441055744.0 + BIAS;
+    const double xc = __builtin_fmax(x, -708.0);  // -inf and NaN -> -708
     // rint(xc / ln2) by the 1.5 * 2^52 shifter: the sum's ulp is 1, so its
     // one rounding is round-to-nearest-even of the (separately rounded)
     // product, and the integer k sits in the low mantissa bits.
     const double t = xc * c[0];
-    const double sh = t + 6755399441055744.0;
-    const double kf = sh - 6755399441055744.0;
-    const int k = (int)(uint32_t)__builtin_bit_cast(uint64_t, sh);
+    const double sh = t + kShift;
+    const double kf = sh - kShift;
+    kb = (uint32_t)__builtin_bit_cast(uint64_t, sh);
     double r = __builtin_fma(-kf, c[1], xc);
     r = __builtin_fma(-kf, c[2], r);
     double p = c[3];
 #pragma unroll
     for (int i = 4; i < 16; ++i) p = __builtin_fma(p, r, c[i]);
-    // p * 2^k with k in [-1021, 0] and p in [0.7, 1.5): the product is a
-    // normal double, so multiplying by 2^k (built from its exponent bits) is
-    // exact, as ldexp would be.
-    const double two_k = __builtin_bit_cast(double, (uint64_t)(uint32_t)((k + 1023) << 20) << 32);
-    const double e = p * two_k;
-    return ok ? e : 0.0;
+    return p;
+  }
+  // p * 2^j for p in [0.7, 1.5) and j in [-1021, 44]: the result is a normal
+  // double, so the scaling is exact (v_ldexp_f64, one instruction; building
+  // the factor from exponent bits measured slower).
+  __device__ __forceinline__ static double scale(double p, uint32_t j) { return __builtin_ldexp(p, (int)j); }
+  // The contract's value: exp(x) for x >= -708, else +0.
+  __device__ __forceinline__ double operator()(double x) const {
+    uint32_t k;
+    const double p = poly<0>(x, k);
+    return x >= -708.0 ? scale(p, k) : 0.0;  // false for -inf and NaN
+  }
+  // The bits of rint(e * 2^44) + 2^52 for the contract's value e.  e * 2^44 = p * 2^(k+44) exactly, so one add of
+  // 2^52 rounds it as fma(e, 2^44, 2^52) would.  Below -708 it uses
+  // exp(-708) (~3.3e-308) instead of 0: rint(e * 2^44) is 0 for both.
+  __device__ __forceinline__ uint64_t fixed_biased(double x) const {
+#pragma clang fp contract(off)
+    uint32_t k44;
+    const double p = poly<44>(x, k44);
+    return __builtin_bit_cast(uint64_t, scale(p, k44) + c[17]);
   }
 };
 
 // Fixed-point quantum of the softmax normaliser: e in [0,1] -> rint(e * 2^44).
-// fma(e, 2^44, 2^52) lands in [2^52, 2^53) where the spacing of doubles is 1,
-// so its single rounding is round-to-nearest-even of e * 2^44 and the low
-// mantissa bits are that integer.
-#define HC_FIX_SHIFT 44
-__device__ __forceinline__ uint64_t det_fix(double e) {
-  const double t = __builtin_fma(e, 17592186044416.0, 4503599627370496.0);  // e * 2^44 + 2^52
-  return __builtin_bit_cast(uint64_t, t) - 0x4330000000000000ull;
-}
+// e * 2^44 + 2^52 lands in [2^52, 2^53) where the spacing of doubles is 1, so
+// its single rounding is round-to-nearest-even of e * 2^44 and the low
+// mantissa bits are that integer; HC_FIX_BIAS is the bit pattern of 2^52,
+// which DetExp::fixed_biased leaves in and sums take off once.
+#define HC_FIX_BIAS 0x4330000000000000ull
 
 // Total order key for fp32 scores: larger score -> larger key; -0 == +0;
 // NaN above everything (torch.topk ranks NaN highest).

@@ -352,19 +352,30 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ l
   };
 #pragma unroll
   for (int i = 0; i < kSumRing - 1; ++i) load(x[i], i);
+  // each term is added with its 2^52 bias left in (keys past S add the
+  // bias alone); the 4 * nadd biases come off once, in wrapping uint64
+  const int nadd = (nstep + kSumRing - 1) / kSumRing * kSumRing;
   for (int s0 = 0; s0 < nstep; s0 += kSumRing) {
 #pragma unroll
     for (int j = 0; j < kSumRing; ++j) {
       load(x[(j + kSumRing - 1) % kSumRing], s0 + j + kSumRing - 1);
       const int key = (s0 + j) * 256 + lane * 4;
+      if constexpr (VEC) {
+        // S % 4 == 0: the lane's four keys are all in range or all past S;
+        // past S the max becomes +inf, so x = -inf and the term is the bias
+        const double mk = key < S ? md : INFINITY;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float L = key + e < S ? __uint_as_float(x[j][e]) : -INFINITY;
-        acc[e] += det_fix(dexp((double)L - md));
+        for (int e = 0; e < 4; ++e) acc[e] += dexp.fixed_biased((double)__uint_as_float(x[j][e]) - mk);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float L = key + e < S ? __uint_as_float(x[j][e]) : -INFINITY;
+          acc[e] += dexp.fixed_biased((double)L - md);
+        }
       }
     }
   }
-  uint64_t t = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  uint64_t t = (acc[0] + acc[1]) + (acc[2] + acc[3]) - (uint64_t)(4 * nadd) * HC_FIX_BIAS;
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     const uint32_t rl = __shfl_xor((uint32_t)t, o, 64);
