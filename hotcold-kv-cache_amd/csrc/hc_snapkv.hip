@@ -28,12 +28,19 @@ namespace hc {
 
 constexpr int kChunkM = 128;  // keys per logits workgroup (4 waves x 32 keys)
 constexpr int kRowBlk = 32;   // window rows per logits workgroup (fp64 accumulators)
-constexpr int kMaxW = 256;
 constexpr int kMaxPool = 32;  // max half-width of the pooling window
 
 struct ScoreLayout {
-  int64_t wpad, nchunk_m, qf_off, logits_off, rmax_off, lsum_off, total;
+  int64_t wpad, nchunk_m, qf_off, logits_off, rmax_off, rstat_off, total;
 };
+
+// Per window row, for the importance pass: the row max and 1/l_w in fp64.
+// Rows are padded to a multiple of kStatPad per (b, h); the padding rows hold
+// {+inf, 0}, so they add an exact zero to the importance chain.
+struct RowStat {
+  double m, inv;
+};
+constexpr int kStatPad = 16;
 
 static int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
@@ -44,24 +51,23 @@ static ScoreLayout score_layout(int64_t B, int64_t Hk, int64_t S, int64_t D, int
   L.qf_off = 0;
   L.logits_off = al256(L.qf_off + B * Hk * L.wpad * D * 8);
   L.rmax_off = al256(L.logits_off + B * Hk * W * S * 4);
-  L.lsum_off = al256(L.rmax_off + B * Hk * W * 4);
-  L.total = al256(L.lsum_off + B * Hk * W * 8);
+  L.rstat_off = al256(L.rmax_off + B * Hk * W * 4);
+  L.total = al256(L.rstat_off + B * Hk * cdiv(W, kStatPad) * kStatPad * (int64_t)sizeof(RowStat));
   return L;
 }
 
 // qf[b][h][w][d] for w < wpad (zero rows past W).  grid (wpad, Hk, B), block D.
-// Also resets the row-max keys (to the key of -inf) and the fixed-point
-// row sums that the following kernels accumulate into.
+// Also resets the row-max keys (to the key of -inf) that the logits kernel
+// accumulates into, and writes the padding rows of the row statistics.
 template <typename T>
 __global__ void qmean_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_row0,
                              int Hq, int Hk, int W, int wpad, int D, double* __restrict__ qf,
-                             uint32_t* __restrict__ rmax, uint64_t* __restrict__ lsum) {
+                             uint32_t* __restrict__ rmax, RowStat* __restrict__ rstat) {
   const int w = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int d = threadIdx.x;
-  if (d == 0 && w < W) {
-    rmax[((int64_t)b * Hk + h) * W + w] = order_key(-INFINITY);
-    lsum[((int64_t)b * Hk + h) * W + w] = 0ull;
-  }
+  const int wst = (int)cdiv(W, kStatPad) * kStatPad;  // wst <= wpad
+  if (d == 0 && w < W) rmax[((int64_t)b * Hk + h) * W + w] = order_key(-INFINITY);
+  if (d == 0 && w >= W && w < wst) rstat[((int64_t)b * Hk + h) * wst + w] = RowStat{INFINITY, 0.0};
   if (d >= D) return;
   double* dst = qf + (((int64_t)b * Hk + h) * wpad + w) * D + d;
   if (w >= W) {
@@ -322,13 +328,14 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
 // Exact fixed-point softmax denominators.  grid (ceil(W/4), Hk, B), block
 // 256: each wave streams one window row of the logits (4 keys per lane per
 // step, kSumRing steps in flight), sums rint(e * 2^44) exactly in uint64 and
-// writes the row's total (no atomics: one wave owns the row).
+// writes the row's max and 1/l_w, l_w = (double)sum * 2^-44 (no atomics: one
+// wave owns the row).
 constexpr int kSumRing = 4;
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ logits,
                                                      const uint32_t* __restrict__ rmax, int Hk, int S, int W,
-                                                     uint64_t* __restrict__ lsum) {
+                                                     RowStat* __restrict__ rstat) {
   // the wave index through readfirstlane: the row's buffer resource is then
   // known to be wave-uniform and lives in SGPRs (no waterfall per load)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -382,78 +389,81 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ l
     const uint32_t rh = __shfl_xor((uint32_t)(t >> 32), o, 64);
     t += ((uint64_t)rh << 32) | rl;
   }
-  if (lane == 0) lsum[bh * W + w] = t;
+  if (lane == 0) rstat[bh * (cdiv(W, kStatPad) * kStatPad) + w] = RowStat{md, 1.0 / ((double)t * 0x1p-44)};
 }
 
 // Importance and pooling.  grid (ceil(S / (256 - 2P)), Hk, B), block 256:
 // thread t computes imp for key c0 - P + t as the fma chain over the window
-// rows in ascending order (rows streamed 8 at a time, the next 8 in flight;
-// the rows' max and 1/sum staged in LDS kMaxW rows at a time), then the inner
-// 256 - 2P threads pool over their neighbours in LDS.
+// rows in ascending order (rows streamed 8 at a time, the next 8 in flight),
+// then the inner 256 - 2P threads pool over their neighbours in LDS.  Each
+// row's max and 1/l_w are wave-uniform: they come through scalar loads into
+// SGPRs, with no LDS staging and no per-row branch.
 constexpr int kImpRows = 8;
 
 template <int MODE>
 __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__ logits,
-                                                       const uint32_t* __restrict__ rmax,
-                                                       const uint64_t* __restrict__ lsum, int Hk, int S,
-                                                       int W, int P, int pooling, int ksize,
+                                                       const RowStat* __restrict__ rstat, int Hk, int S, int W,
+                                                       int P, int pooling, int ksize,
                                                        float* __restrict__ scores) {
   const int h = blockIdx.y, b = blockIdx.z;
   const int64_t bh = (int64_t)b * Hk + h;
   const int out_per_block = 256 - 2 * P;
   const int c0 = blockIdx.x * out_per_block;
-  __shared__ float sm_m[kMaxW];
-  __shared__ double sm_inv[kMaxW];
   __shared__ float sm_imp[256];
   const int s = c0 - P + (int)threadIdx.x;
   const bool sv = s >= 0 && s < S;
+  // W * S * 4 < 2^31 (checked by the host), so every in-range offset is below
+  // 2^31.  A lane outside [0, S) starts at kOob = 2^31: plus a row offset
+  // (< 2^31) it stays out of range; rows past W use the row offset kOob, out
+  // of range for in-range lanes (and wrapping to offset 0, a harmless read, for
+  // the others, whose result is discarded).
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + bh * W * S, (uint32_t)((int64_t)W * S * 4));
   const uint32_t base = sv ? (uint32_t)s * 4u : kOob;
   const uint32_t rowb = (uint32_t)S * 4u;
-  auto load = [&](uint32_t (&dst)[kImpRows], int w0) {
-#pragma unroll
-    for (int r = 0; r < kImpRows; ++r)
-      bload<4>(rs, (base == kOob || w0 + r >= W) ? kOob : base + (uint32_t)(w0 + r) * rowb, &dst[r]);
-  };
-  double acc = 0.0;
-  const DetExp dexp = DetExp::load();
-  // rows [w0, w0 + kImpRows) of the chunk starting at wc.  Rows past we add
-  // an exact zero without a branch: their exponent argument is -inf, so
-  // e = 0 and fma(0, inv, acc) = acc (acc >= +0, inv finite: a staged row).
-  auto chain = [&](const uint32_t (&x)[kImpRows], int w0, int wc, int we) {
+  const int wst = (int)cdiv(W, kStatPad) * kStatPad;
+  const RowStat* st = rstat + bh * wst;
+  // a group's logits and (scalar) row statistics are issued one group ahead;
+  // groups start at multiples of kImpRows, and the statistics are padded to
+  // kStatPad (a multiple of 2 * kImpRows) rows
+  static_assert(kStatPad % (2 * kImpRows) == 0, "statistics padding covers whole row pairs");
+  auto load = [&](uint32_t (&dst)[kImpRows], RowStat (&sdst)[kImpRows], int w0) {
 #pragma unroll
     for (int r = 0; r < kImpRows; ++r) {
       const int w = w0 + r;
-      const bool in = w < we;  // wave-uniform
-      const int wi = in ? w - wc : 0;
+      bload<4>(rs, base + (w < W ? (uint32_t)w * rowb : kOob), &dst[r]);
+    }
+    if constexpr (MODE == HC_SCORE_SNAPKV) {
+      // the look-ahead past the last group re-reads the last group (unused)
+      const RowStat* g = st + min(w0, wst - kImpRows);
+#pragma unroll
+      for (int r = 0; r < kImpRows; ++r) sdst[r] = g[r];
+    }
+  };
+  double acc = 0.0;
+  const DetExp dexp = DetExp::load();
+  // rows [w0, w0 + kImpRows); rows past W add an exact zero: their padding
+  // statistics are {+inf, 0}, so x = -inf, e = 0 and fma(0, 0, acc) = acc
+  // (acc >= +0)
+  auto chain = [&](const uint32_t (&x)[kImpRows], const RowStat (&sx)[kImpRows], int w0) {
+#pragma unroll
+    for (int r = 0; r < kImpRows; ++r) {
+      const int w = w0 + r;
       const float L = __uint_as_float(x[r]);
       if constexpr (MODE == HC_SCORE_SNAPKV) {
-        const double xe = in ? (double)L - (double)sm_m[wi] : -INFINITY;
-        acc = __builtin_fma(dexp(xe), sm_inv[wi], acc);
+        acc = __builtin_fma(dexp((double)L - sx[r].m), sx[r].inv, acc);
       } else {
-        acc = acc + (in ? (double)L : 0.0);
+        acc = acc + (w < W ? (double)L : 0.0);
       }
     }
   };
-  for (int wc = 0; wc < W; wc += kMaxW) {
-    const int we = min(W, wc + kMaxW);
-    if constexpr (MODE == HC_SCORE_SNAPKV) {
-      __syncthreads();  // the previous chunk's statistics are no longer read
-      for (int w = wc + (int)threadIdx.x; w < we; w += blockDim.x) {
-        sm_m[w - wc] = key_to_float(rmax[bh * W + w]);
-        const double l = (double)lsum[bh * W + w] * 0x1p-44;
-        sm_inv[w - wc] = 1.0 / l;
-      }
-      __syncthreads();
-    }
-    uint32_t xa[kImpRows], xb[kImpRows];
-    load(xa, wc);
-    for (int w0 = wc; w0 < we; w0 += 2 * kImpRows) {
-      load(xb, w0 + kImpRows);
-      chain(xa, w0, wc, we);
-      load(xa, w0 + 2 * kImpRows);
-      chain(xb, w0 + kImpRows, wc, we);
-    }
+  uint32_t xa[kImpRows], xb[kImpRows];
+  RowStat sa[kImpRows], sb[kImpRows];
+  load(xa, sa, 0);
+  for (int w0 = 0; w0 < W; w0 += 2 * kImpRows) {
+    load(xb, sb, w0 + kImpRows);
+    chain(xa, sa, w0);
+    load(xa, sa, w0 + 2 * kImpRows);
+    chain(xb, sb, w0 + kImpRows);
   }
   sm_imp[threadIdx.x] = sv ? (float)acc : 0.f;
   __syncthreads();
@@ -497,11 +507,11 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
   double* qf = reinterpret_cast<double*>(ws + lay.qf_off);
   float* logits = reinterpret_cast<float*>(ws + lay.logits_off);
   uint32_t* rmax = reinterpret_cast<uint32_t*>(ws + lay.rmax_off);
-  uint64_t* lsum = reinterpret_cast<uint64_t*>(ws + lay.lsum_off);
+  RowStat* rstat = reinterpret_cast<RowStat*>(ws + lay.rstat_off);
   const int nrb = (int)(lay.wpad / kRowBlk);
   hipLaunchKernelGGL(qmean_kernel<T>, dim3((unsigned)lay.wpad, (unsigned)Hk, (unsigned)B),
                      dim3((unsigned)(D < 64 ? 64 : D)), 0, st, (const T*)q, q_sb, q_sh, q_ss, q_row0, (int)Hq,
-                     (int)Hk, (int)W, (int)lay.wpad, (int)D, qf, rmax, lsum);
+                     (int)Hk, (int)W, (int)lay.wpad, (int)D, qf, rmax, rstat);
   const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
   const uint32_t k_bytes = (uint32_t)(((S - 1) * k_ss + D) * (int64_t)sizeof(T));
   const dim3 grid((unsigned)cdiv(S, (int64_t)kChunkM * kLogitChunks), (unsigned)(Hk * nrb), (unsigned)B);
@@ -523,19 +533,19 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
     const dim3 g((unsigned)cdiv(W, 4), (unsigned)Hk, (unsigned)B);
     if (S % 4 == 0)
       hipLaunchKernelGGL(rowsum_kernel<true>, g, dim3(256), 0, st, (const float*)logits, (const uint32_t*)rmax,
-                         (int)Hk, (int)S, (int)W, lsum);
+                         (int)Hk, (int)S, (int)W, rstat);
     else
       hipLaunchKernelGGL(rowsum_kernel<false>, g, dim3(256), 0, st, (const float*)logits, (const uint32_t*)rmax,
-                         (int)Hk, (int)S, (int)W, lsum);
+                         (int)Hk, (int)S, (int)W, rstat);
   }
   const dim3 gi((unsigned)cdiv(S, 256 - 2 * P), (unsigned)Hk, (unsigned)B);
   if (mode == HC_SCORE_SNAPKV)
     hipLaunchKernelGGL(imp_pool_kernel<HC_SCORE_SNAPKV>, gi, dim3(256), 0, st, (const float*)logits,
-                       (const uint32_t*)rmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W, P, pooling, ksize,
+                       (const RowStat*)rstat, (int)Hk, (int)S, (int)W, P, pooling, ksize,
                        scores);
   else
     hipLaunchKernelGGL(imp_pool_kernel<HC_SCORE_RAWSUM>, gi, dim3(256), 0, st, (const float*)logits,
-                       (const uint32_t*)rmax, (const uint64_t*)lsum, (int)Hk, (int)S, (int)W, P, pooling, ksize,
+                       (const RowStat*)rstat, (int)Hk, (int)S, (int)W, P, pooling, ksize,
                        scores);
 }
 
