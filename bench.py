@@ -245,6 +245,8 @@ def run_steps(s, steps, flush):
     def ms(evs):
         return [a.elapsed_time(b) for a, b in evs]
 
+    if not steps:  # warm-up with --warmup 0: nothing timed
+        return 0.0, [], float("nan"), float("nan")
     comp = ms(comp_ev)
     dec_diff = statistics.median(ms(pair_ev)) - statistics.median(ms(sweep_ev))
     dec_br = statistics.median(ms(br_ev))
@@ -521,6 +523,9 @@ def main():
         print("bench.py: this build measures one GPU only; the hot tier shards by batch and KV head "
               "across GPUs with no exchange inside the path, and no multi-GPU figure is produced. "
               "Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+    if args.steps < 1 or args.warmup < 0:
+        print("bench.py: --steps must be at least 1 and --warmup at least 0", file=sys.stderr)
         sys.exit(2)
 
     import torch

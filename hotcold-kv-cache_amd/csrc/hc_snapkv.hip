@@ -147,8 +147,8 @@ struct KOperand<float> {
 //   A (16 rows x 4): lane l supplies qf[w0 + 16*nb + l%16][4t + l/16]
 //   B (4 x 16 keys): lane l supplies k[key0 + 16*mb + l%16][4t + l/16]
 //   D: lane l holds rows w0 + 16*nb + l/16 + 4i, key key0 + 16*mb + l%16
-// grid (ceil(S / (128*kLogitChunks)), Hk * nrb, B), block 256.  The 32 x D
-// fp64 query block is staged in LDS once and reused for kLogitChunks chunks
+// grid (ceil(S / (128*cpw)), Hk * nrb, B), block 256.  The 32 x D
+// fp64 query block is staged in LDS once and reused for cpw chunks
 // of 128 keys; per chunk each wave covers 32 keys (two 16-key blocks) x 32
 // window rows (two 16-row blocks).  K loads are unconditional buffer loads
 // ahead of use (rows past S read zeros).  With the head dim known at compile
@@ -160,15 +160,18 @@ struct KOperand<float> {
 // kOob), so the compiler's vmcnt waits for the ring never have to drain the
 // stores.  The LDS q block (33 KB at D = 128) allows four workgroups per CU;
 // the occupancy ceiling of 4 tells the scheduler not to trade the ring's
-// registers for occupancy it cannot get.  16 chunks per workgroup make the
-// 8k, 32-layer grid exactly one round of 4 workgroups per CU.
+// registers for occupancy it cannot get.  The host sets the chunks per
+// workgroup (cpw, up to kLogitChunks) to leave about four workgroups per CU:
+// 16 at the 8k, 32-layer batch (one round of 1024 workgroups), 1 for one
+// 8k layer.
 constexpr int kLogitChunks = 16;
+constexpr int kLogitTargetWg = 1024;
 constexpr int kKRing = 4;
 
 template <typename T, int MODE, int DC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void logits_kernel(
     const T* __restrict__ k, int64_t k_sb, int64_t k_sh, int64_t k_ss, uint32_t k_bytes,
-    const double* __restrict__ qf, int Hk, int S, int Drt, int W, int wpad, double scaling,
+    const double* __restrict__ qf, int Hk, int S, int Drt, int W, int wpad, double scaling, int cpw,
     float* __restrict__ logits, uint32_t* __restrict__ rmax) {
   const int D = DC > 0 ? DC : Drt;
   extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
@@ -201,7 +204,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   // slot s % kKRing, so the slices per chunk are a multiple of the ring
   static_assert(DC == 0 || (DC % (2 * DS) == 0 && NS % kKRing == 0), "ring must tile the slices of a chunk");
   KOperand<T> ka[kKRing], kb[kKRing];
-  int key0 = blockIdx.x * (kChunkM * kLogitChunks) + wave * 32;
+  int key0 = blockIdx.x * (kChunkM * cpw) + wave * 32;
   uint32_t off0 = key0 + col < S ? (uint32_t)(key0 + col) * rowb : kOob;
   uint32_t off1 = key0 + 16 + col < S ? (uint32_t)(key0 + 16 + col) * rowb : kOob;
   // first K slices in flight before the q block is staged
@@ -220,7 +223,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   __syncthreads();
 
   // wave-uniform chunk count: short prompts stop at their last chunk
-  const int nch = key0 < S ? min(kLogitChunks, (S - key0 + kChunkM - 1) / kChunkM) : 0;
+  const int nch = key0 < S ? min(cpw, (S - key0 + kChunkM - 1) / kChunkM) : 0;
   for (int c = 0; c < nch; ++c) {
     // the q reads repeat for every chunk; keep them inside the loop (hoisted,
     // all D/2 of them would hold 2*D registers for the kernel's lifetime)
@@ -514,12 +517,14 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
                      (int)Hk, (int)W, (int)lay.wpad, (int)D, qf, rmax, rstat);
   const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
   const uint32_t k_bytes = (uint32_t)(((S - 1) * k_ss + D) * (int64_t)sizeof(T));
-  const dim3 grid((unsigned)cdiv(S, (int64_t)kChunkM * kLogitChunks), (unsigned)(Hk * nrb), (unsigned)B);
+  const int64_t wg1 = cdiv(S, (int64_t)kChunkM) * Hk * nrb * B;  // workgroups at one chunk each
+  const int cpw = (int)std::max<int64_t>(1, std::min<int64_t>(kLogitChunks, wg1 / kLogitTargetWg));
+  const dim3 grid((unsigned)cdiv(S, (int64_t)kChunkM * cpw), (unsigned)(Hk * nrb), (unsigned)B);
   auto launch = [&](auto kern) {
     if (lds > 48 * 1024)
       (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const T*)k, k_sb, k_sh, k_ss, k_bytes, (const double*)qf,
-                       (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, logits, rmax);
+                       (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, cpw, logits, rmax);
   };
   if (mode == HC_SCORE_SNAPKV) {
     if (D == 128) launch(logits_kernel<T, HC_SCORE_SNAPKV, 128>);
