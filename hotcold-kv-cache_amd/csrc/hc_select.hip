@@ -3,7 +3,8 @@
 // hc_topk_keep replaces keep_index (src/hotcold_kv/baselines/scoring.py:110-132)
 // and the top-k of HotColdLayer._compress_if_needed (src/hotcold_kv/cache.py:47-95).
 // One workgroup per (batch, head): an MSB-first radix select over 32-bit
-// order keys finds the threshold key T of the keep_prefix-th largest prefix
+// order keys (three passes: 11, 11, 10 bits) finds the threshold key T of
+// the keep_prefix-th largest prefix
 // score, then one ordered pass emits every index with key > T plus the
 // lowest-index ties with key == T.  Emitting in index order gives the
 // ascending sort of scoring.py:130 for free, and the result is the exact
@@ -20,6 +21,7 @@ namespace hc {
 constexpr int kTopkThreads = 1024;
 constexpr int kTopkWaves = kTopkThreads / 64;
 constexpr int kTopkCache = 32768;  // prefix keys cached in LDS (128 KiB)
+constexpr int kTopkU = 8;          // keys loaded together per thread (one wait per batch)
 
 // Block-wide exclusive prefix sum of v in thread order (wave scans plus one
 // pass over the wave totals); writes the block total to *total.
@@ -44,32 +46,34 @@ __device__ __forceinline__ int block_excl_scan(int v, int* sm_wave, int* total) 
   return before + incl - v;
 }
 
-// Digit search of one radix pass: the largest digit d with
-// count(digits > d) < krem <= count(digits >= d), by a scan over the 256
-// bins in descending order on threads 0..255.
+// Digit search of one radix pass over kDigitBins bins: the largest digit d
+// with count(digits > d) < krem <= count(digits >= d).  Thread t holds the
+// bin pair kDigitBins-1-2t, kDigitBins-2-2t, so thread order is descending
+// digit order and one block scan finds d.
+constexpr int kDigitBins = 2048;
+static_assert(kDigitBins == 2 * kTopkThreads, "two bins per thread");
 __device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, uint32_t* sm_scan,
                                            uint32_t* sm_digit, uint32_t* sm_krem) {
   const int t = threadIdx.x;
   const int lane = t & 63, wave = t >> 6;
-  uint32_t cnt = 0, incl = 0;
-  if (t < 256) {
-    cnt = hist[255 - t];
-    incl = cnt;
+  const uint32_t c0 = hist[kDigitBins - 1 - 2 * t], c1 = hist[kDigitBins - 2 - 2 * t];
+  const uint32_t v = c0 + c1;
+  uint32_t incl = v;
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-      const uint32_t y = __shfl_up(incl, o, 64);
-      if (lane >= o) incl += y;
-    }
-    if (lane == 63) sm_scan[wave] = incl;
+  for (int o = 1; o < 64; o <<= 1) {
+    const uint32_t y = __shfl_up(incl, o, 64);
+    if (lane >= o) incl += y;
   }
+  if (lane == 63) sm_scan[wave] = incl;
   __syncthreads();
-  if (t < 256) {
-    for (int w = 0; w < wave; ++w) incl += sm_scan[w];
-    const uint32_t excl = incl - cnt;
-    if (excl < krem && incl >= krem) {
-      *sm_digit = (uint32_t)(255 - t);
-      *sm_krem = krem - excl;
-    }
+  for (int w = 0; w < wave; ++w) incl += sm_scan[w];
+  const uint32_t excl = incl - v;
+  if (excl < krem && excl + c0 >= krem) {
+    *sm_digit = (uint32_t)(kDigitBins - 1 - 2 * t);
+    *sm_krem = krem - excl;
+  } else if (excl + c0 < krem && incl >= krem) {
+    *sm_digit = (uint32_t)(kDigitBins - 2 - 2 * t);
+    *sm_krem = krem - excl - c0;
   }
   __syncthreads();
 }
@@ -89,13 +93,37 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
   int64_t* ev = evicted ? evicted + ((int64_t)b * H + h) * n_ev : nullptr;
   const bool cached = prefix <= kTopkCache;
 
-  __shared__ uint32_t hist[256];
-  __shared__ uint32_t sm_scan[4];
+  __shared__ uint32_t hist[kDigitBins];
+  __shared__ uint32_t sm_scan[kTopkWaves];
   __shared__ uint32_t sm_digit, sm_krem;
   __shared__ int sm_wave[kTopkWaves];
 
+  // Global reads go kTopkU at a time with clamped (in-range) indices, so a
+  // batch costs one memory round trip instead of one per key.
+  // kTopkU order keys at idx(u), from LDS or (one batch of loads) global
+  auto keys_of = [&](uint32_t (&ks)[kTopkU], auto idx) {
+    if (cached) {
+#pragma unroll
+      for (int u = 0; u < kTopkU; ++u) ks[u] = skey[idx(u)];
+    } else {
+      float v[kTopkU];
+#pragma unroll
+      for (int u = 0; u < kTopkU; ++u) v[u] = sc[idx(u)];
+#pragma unroll
+      for (int u = 0; u < kTopkU; ++u) ks[u] = order_key(v[u]);
+    }
+  };
   if (cached && keep_prefix > 0) {
-    for (int i = threadIdx.x; i < prefix; i += kTopkThreads) skey[i] = order_key(sc[i]);
+    for (int base = 0; base < prefix; base += kTopkThreads * kTopkU) {
+      float v[kTopkU];
+#pragma unroll
+      for (int u = 0; u < kTopkU; ++u) v[u] = sc[min(base + u * kTopkThreads + (int)threadIdx.x, prefix - 1)];
+#pragma unroll
+      for (int u = 0; u < kTopkU; ++u) {
+        const int i = base + u * kTopkThreads + (int)threadIdx.x;
+        if (i < prefix) skey[i] = order_key(v[u]);
+      }
+    }
     __syncthreads();
   }
 
@@ -104,17 +132,27 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
   if (keep_prefix > 0) {
     uint32_t pbits = 0, pmask = 0;
     uint32_t krem = (uint32_t)keep_prefix;
-    for (int shift = 24; shift >= 0; shift -= 8) {
-      for (int i = threadIdx.x; i < 256; i += kTopkThreads) hist[i] = 0;
+    // three passes of 11, 11 and 10 bits: scores crowd a few exponents, and
+    // wide digits spread them over many bins (LDS atomics to one address
+    // serialise)
+    for (int ps = 0; ps < 3; ++ps) {
+      const int shift = ps == 0 ? 21 : ps == 1 ? 10 : 0;
+      const uint32_t dmask = ps == 2 ? 1023u : 2047u;
+      for (int i = threadIdx.x; i < kDigitBins; i += kTopkThreads) hist[i] = 0;
       __syncthreads();
-      for (int i = threadIdx.x; i < prefix; i += kTopkThreads) {
-        const uint32_t key = cached ? skey[i] : order_key(sc[i]);
-        if ((key & pmask) == pbits) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      for (int base = 0; base < prefix; base += kTopkThreads * kTopkU) {
+        uint32_t ks[kTopkU];
+        keys_of(ks, [&](int u) { return min(base + u * kTopkThreads + (int)threadIdx.x, prefix - 1); });
+#pragma unroll
+        for (int u = 0; u < kTopkU; ++u) {
+          const int i = base + u * kTopkThreads + (int)threadIdx.x;
+          if (i < prefix && (ks[u] & pmask) == pbits) atomicAdd(&hist[(ks[u] >> shift) & dmask], 1u);
+        }
       }
       __syncthreads();
       find_digit(hist, krem, sm_scan, &sm_digit, &sm_krem);
       pbits |= sm_digit << shift;
-      pmask |= 255u << shift;
+      pmask |= dmask << shift;
       krem = sm_krem;
       __syncthreads();
     }
@@ -129,10 +167,16 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
   const int i1 = min(prefix, i0 + run);
   int n_gt = 0, n_eq = 0;
   if (keep_prefix > 0) {
-    for (int i = i0; i < i1; ++i) {
-      const uint32_t key = cached ? skey[i] : order_key(sc[i]);
-      n_gt += key > tkey;
-      n_eq += key == tkey;
+    for (int c = i0; c < i1; c += kTopkU) {
+      uint32_t ks[kTopkU];
+      keys_of(ks, [&](int u) { return min(c + u, i1 - 1); });
+#pragma unroll
+      for (int u = 0; u < kTopkU; ++u) {
+        if (c + u < i1) {
+          n_gt += ks[u] > tkey;
+          n_eq += ks[u] == tkey;
+        }
+      }
     }
   }
   int tot;
@@ -142,19 +186,25 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
   int pos = sel_before;
   int epos = i0 - sel_before;
   int eq_seen = 0;
-  for (int i = i0; i < i1; ++i) {
-    bool sel = false;
-    if (keep_prefix > 0) {
-      const uint32_t key = cached ? skey[i] : order_key(sc[i]);
-      if (key > tkey) {
-        sel = true;
-      } else if (key == tkey) {
-        sel = eq_seen < take_eq;
-        ++eq_seen;
+  for (int c = i0; c < i1; c += kTopkU) {
+    uint32_t ks[kTopkU] = {};
+    if (keep_prefix > 0) keys_of(ks, [&](int u) { return min(c + u, i1 - 1); });
+#pragma unroll
+    for (int u = 0; u < kTopkU; ++u) {
+      const int i = c + u;
+      if (i >= i1) break;
+      bool sel = false;
+      if (keep_prefix > 0) {
+        if (ks[u] > tkey) {
+          sel = true;
+        } else if (ks[u] == tkey) {
+          sel = eq_seen < take_eq;
+          ++eq_seen;
+        }
       }
+      if (sel) out[pos++] = i;
+      else if (ev) ev[epos++] = i;
     }
-    if (sel) out[pos++] = i;
-    else if (ev) ev[epos++] = i;
   }
   for (int j = threadIdx.x; j < window; j += kTopkThreads) out[keep_prefix + j] = prefix + j;
 }
