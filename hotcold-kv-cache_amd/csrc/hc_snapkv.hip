@@ -328,58 +328,72 @@ __device__ __forceinline__ float key_to_float(uint32_t k) {
   return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
 }
 
-// Exact fixed-point softmax denominators.  grid (ceil(W/4), Hk, B), block
-// 256: each wave streams one window row of the logits (4 keys per lane per
-// step, kSumRing steps in flight), sums rint(e * 2^44) exactly in uint64 and
-// writes the row's max and 1/l_w, l_w = (double)sum * 2^-44 (no atomics: one
-// wave owns the row).
+// Exact fixed-point softmax denominators.  grid (ceil(W / (4 / nsplit)), Hk,
+// B), block 256: the workgroup's 4 waves cover 4 / nsplit window rows, nsplit
+// waves per row, each streaming its split of the row's logits (4 keys per
+// lane per step, kSumRing steps in flight) and summing rint(e * 2^44)
+// exactly in uint64.  The splits of a row combine in LDS (integer addition:
+// the total does not depend on the order), and the row's first wave writes
+// its max and 1/l_w, l_w = (double)sum * 2^-44.  nsplit > 1 serves grids with
+// too few rows to fill the GPU (one layer at batch 1).
 constexpr int kSumRing = 4;
+constexpr int kSumTargetWaves = 2048;
 
 template <bool VEC>
 __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ logits,
                                                      const uint32_t* __restrict__ rmax, int Hk, int S, int W,
-                                                     RowStat* __restrict__ rstat) {
+                                                     int nsplit, RowStat* __restrict__ rstat) {
+  __shared__ uint64_t sm_part[4];
   // the wave index through readfirstlane: the row's buffer resource is then
   // known to be wave-uniform and lives in SGPRs (no waterfall per load)
   const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int w = blockIdx.x * 4 + wave;
-  if (w >= W) return;
+  const int sp = wave % nsplit;
+  const int w = blockIdx.x * (4 / nsplit) + wave / nsplit;
+  const bool live = w < W;  // wave-uniform; every wave reaches the barrier
+  const int wr = live ? w : W - 1;
   const int64_t bh = (int64_t)blockIdx.z * Hk + blockIdx.y;
-  const double md = (double)key_to_float(rmax[bh * W + w]);
+  const double md = (double)key_to_float(rmax[bh * W + wr]);
   const DetExp dexp = DetExp::load();
-  const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + (bh * W + w) * S, (uint32_t)S * 4u);
-  const int nstep = (S + 255) / 256;
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + (bh * W + wr) * S, (uint32_t)S * 4u);
+  // this split's steps [st0, st0 + nstep) and keys [st0 * 256, kend); a wave
+  // past W streams nothing (kend = 0)
+  const int nstep_all = (S + 255) / 256;
+  const int sps = (nstep_all + nsplit - 1) / nsplit;
+  const int st0 = min(nstep_all, sp * sps);
+  const int nstep = live ? min(nstep_all, st0 + sps) - st0 : 0;
+  const int kend = min(S, (st0 + nstep) * 256);
   uint64_t acc[4] = {0, 0, 0, 0};
   uint32_t x[kSumRing][4];
   auto load = [&](uint32_t (&dst)[4], int step) {
-    const int key = step * 256 + lane * 4;
+    const int key = (st0 + step) * 256 + lane * 4;
     if constexpr (VEC) {
-      bload<16>(rs, key < S ? (uint32_t)key * 4u : kOob, dst);
+      bload<16>(rs, key < kend ? (uint32_t)key * 4u : kOob, dst);
     } else {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) bload<4>(rs, key + e < S ? (uint32_t)(key + e) * 4u : kOob, &dst[e]);
+      for (int e = 0; e < 4; ++e) bload<4>(rs, key + e < kend ? (uint32_t)(key + e) * 4u : kOob, &dst[e]);
     }
   };
 #pragma unroll
   for (int i = 0; i < kSumRing - 1; ++i) load(x[i], i);
-  // each term is added with its 2^52 bias left in (keys past S add the
+  // each term is added with its 2^52 bias left in (keys past kend add the
   // bias alone); the 4 * nadd biases come off once, in wrapping uint64
   const int nadd = (nstep + kSumRing - 1) / kSumRing * kSumRing;
   for (int s0 = 0; s0 < nstep; s0 += kSumRing) {
 #pragma unroll
     for (int j = 0; j < kSumRing; ++j) {
       load(x[(j + kSumRing - 1) % kSumRing], s0 + j + kSumRing - 1);
-      const int key = (s0 + j) * 256 + lane * 4;
+      const int key = (st0 + s0 + j) * 256 + lane * 4;
       if constexpr (VEC) {
-        // S % 4 == 0: the lane's four keys are all in range or all past S;
-        // past S the max becomes +inf, so x = -inf and the term is the bias
-        const double mk = key < S ? md : INFINITY;
+        // S % 4 == 0 and kend % 4 == 0: the lane's four keys are all in range
+        // or all past kend; past it the max becomes +inf, so x = -inf and the
+        // term is the bias
+        const double mk = key < kend ? md : INFINITY;
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[e] += dexp.fixed_biased((double)__uint_as_float(x[j][e]) - mk);
       } else {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float L = key + e < S ? __uint_as_float(x[j][e]) : -INFINITY;
+          const float L = key + e < kend ? __uint_as_float(x[j][e]) : -INFINITY;
           acc[e] += dexp.fixed_biased((double)L - md);
         }
       }
@@ -392,7 +406,18 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ l
     const uint32_t rh = __shfl_xor((uint32_t)(t >> 32), o, 64);
     t += ((uint64_t)rh << 32) | rl;
   }
-  if (lane == 0) rstat[bh * (cdiv(W, kStatPad) * kStatPad) + w] = RowStat{md, 1.0 / ((double)t * 0x1p-44)};
+  RowStat* out = rstat + bh * (cdiv(W, kStatPad) * kStatPad) + w;
+  if (nsplit == 1) {  // uniform: no barrier
+    if (live && lane == 0) *out = RowStat{md, 1.0 / ((double)t * 0x1p-44)};
+    return;
+  }
+  if (lane == 0) sm_part[wave] = t;
+  __syncthreads();
+  if (live && sp == 0 && lane == 0) {
+    uint64_t tot = 0;
+    for (int j = 0; j < nsplit; ++j) tot += sm_part[wave + j];
+    *out = RowStat{md, 1.0 / ((double)tot * 0x1p-44)};
+  }
 }
 
 // Importance and pooling.  grid (ceil(S / (256 - 2P)), Hk, B), block 256:
@@ -535,13 +560,18 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
     launch(logits_kernel<T, HC_SCORE_RAWSUM, 0>);
   }
   if (mode == HC_SCORE_SNAPKV) {
-    const dim3 g((unsigned)cdiv(W, 4), (unsigned)Hk, (unsigned)B);
+    // rows split across the waves of a workgroup (1, 2 or 4 per row) when
+    // there are too few rows to fill the GPU (about kSumTargetWaves waves)
+    const int64_t rows = W * Hk * B;
+    int nsplit = 1;
+    while (nsplit < 4 && rows * nsplit * 2 <= kSumTargetWaves && cdiv(S, 256) >= 2 * nsplit) nsplit *= 2;
+    const dim3 g((unsigned)cdiv(W, 4 / nsplit), (unsigned)Hk, (unsigned)B);
     if (S % 4 == 0)
       hipLaunchKernelGGL(rowsum_kernel<true>, g, dim3(256), 0, st, (const float*)logits, (const uint32_t*)rmax,
-                         (int)Hk, (int)S, (int)W, rstat);
+                         (int)Hk, (int)S, (int)W, nsplit, rstat);
     else
       hipLaunchKernelGGL(rowsum_kernel<false>, g, dim3(256), 0, st, (const float*)logits, (const uint32_t*)rmax,
-                         (int)Hk, (int)S, (int)W, rstat);
+                         (int)Hk, (int)S, (int)W, nsplit, rstat);
   }
   const dim3 gi((unsigned)cdiv(S, 256 - 2 * P), (unsigned)Hk, (unsigned)B);
   if (mode == HC_SCORE_SNAPKV)
