@@ -27,7 +27,10 @@ Reported:
                      launch stream as [sweep; decode] minus [sweep] alone
                      (run_steps explains; the event-bracketed time is also
                      reported)
-  compact_ms_32_layers  compaction of all 32 layers per step, ms
+  compact_ms_32_layers  compaction of all 32 layers per step, ms (the 32
+                     layers stacked along the batch axis, one launch set;
+                     compact_ms_32_layers_per_layer_launches is the same work
+                     as one launch set per layer, as a model's prefill runs it)
   roofline           decode launch: algorithmic bytes / mean launch time
   roofline_compaction, scoring MFMA rate, a per-layer-launch variant (one
   decode launch per layer, as a model's layer loop issues them), warm-cache
@@ -148,6 +151,17 @@ class Setup:
         ops.gather_rows(keep, [(self.k_post, self.k_hot), (self.v, self.v_hot)])
         return keep
 
+    def compaction_per_layer(self):
+        """The same compaction as one launch set per layer, as a model's
+        prefill issues it (each layer compacts after its attention)."""
+        from hotcold_kv import ops
+        w, B = self.w, self.w.batch
+        for l in range(w.layers):
+            sl = slice(l * B, (l + 1) * B)
+            scores = ops.snapkv_scores(self.q_post[sl], self.k_post[sl], w.window, w.scaling, w.pool, "maxpool")
+            keep = ops.keep_index(scores, w.window, w.budget)
+            ops.gather_rows(keep, [(self.k_post[sl], self.k_hot[sl]), (self.v[sl], self.v_hot[sl])])
+
     def decode(self, t, num_splits=0):
         """Decode step t: append token t into row budget+t of every layer's
         hot buffer and attend over rows 0..budget+t, one fused launch."""
@@ -175,6 +189,7 @@ class Setup:
         s.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(s):
             self.compaction()
+            self.compaction_per_layer()
             for t in range(w.decode_steps):
                 self.decode(t)
             self.decode_per_layer(w.decode_steps - 1)
@@ -187,6 +202,7 @@ class Setup:
             return g
 
         self.g_comp = cap(self.compaction)
+        self.g_cpl = cap(self.compaction_per_layer)
         self.g_pl = cap(lambda: self.decode_per_layer(w.decode_steps - 1))
         # 20 back-to-back launches of the last step's decode (warm-cache rate)
         self.g_dec20 = cap(lambda: [self.decode(w.decode_steps - 1) for _ in range(20)])
@@ -569,6 +585,8 @@ def main():
     n_last = w.budget + w.decode_steps
     log(f"last-step decode launch warm {warm_dec_ms * 1e3:.2f} us; per-layer launches cold "
         f"{pl_cold_ms * 1e3 / w.layers:.2f} us/layer, warm {pl_warm_ms * 1e3 / w.layers:.2f} us/layer")
+    cpl_ms = time_graph(s.g_cpl, s.stream, 10, flush)
+    log(f"compaction as one launch set per layer: {cpl_ms:.3f} ms for {w.layers} layers")
     del flush
 
     others = []
@@ -608,6 +626,7 @@ def main():
                    "schedule": "32 layers per launch, fused append+decode, compaction as a HIP graph, "
                                "Infinity Cache flushed before decode"},
         "compact_ms_32_layers": round(comp_ms, 4),
+        "compact_ms_32_layers_per_layer_launches": round(cpl_ms, 4),
         "decode_us_per_layer_step": round(dec_us_layer, 4),
         "decode_launch_us_differential": round(dec_ms * 1e3, 3),
         "decode_launch_us_event_bracketed": round(dec_br_ms * 1e3, 3),
