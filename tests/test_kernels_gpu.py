@@ -257,6 +257,11 @@ SCORE_CASES = [
     (2, 12, 4, 333, 64, 40, torch.float16, 5, "maxpool"),    # ragged window row block
     (1, 6, 4, 150, 32, 8, torch.float16, 1, "maxpool"),      # Hq % Hk != 0, no pooling
     (1, 4, 4, 20, 16, 32, torch.float32, 7, "maxpool"),      # window longer than the prompt
+    # few rows: each row sum split across 4 waves, S not a multiple of 256
+    (1, 8, 2, 3000, 64, 7, torch.float16, 7, "maxpool"),     # S % 4 == 0 (vector row loads)
+    (1, 8, 2, 3001, 128, 7, torch.bfloat16, 5, "avgpool"),   # S % 4 != 0 (scalar row loads)
+    # enough rows and keys for several 128-key chunks per logits workgroup
+    (8, 32, 8, 4160, 128, 32, torch.float16, 7, "maxpool"),
 ]
 
 
