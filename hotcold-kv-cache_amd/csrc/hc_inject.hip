@@ -34,8 +34,10 @@ __global__ void inject_rerope_kernel(const float* __restrict__ kp, int64_t kp_sb
   const float fpos = (float)pos[b * pos_sb + h * pos_sh + r];
   for (int i = threadIdx.x; i < half; i += blockDim.x) {
     const float f = fpos * inv_freq[i];
-    const float cf = (float)cos((double)f) * scaling;
-    const float sf = (float)sin((double)f) * scaling;
+    double sd, cd;
+    sincos((double)f, &sd, &cd);  // one shared argument reduction
+    const float cf = (float)cd * scaling;
+    const float sf = (float)sd * scaling;
     const float c = to_f32(from_f32<T>(cf));
     const float s = to_f32(from_f32<T>(sf));
     const float ka = to_f32(from_f32<T>(krow[i]));
