@@ -165,6 +165,7 @@ struct KOperand<float> {
 // 16 at the 8k, 32-layer batch (one round of 1024 workgroups), 1 for one
 // 8k layer.
 constexpr int kLogitChunks = 16;
+constexpr int kNeverRead = 512;  // > the 256 (rowsum) and 270 (imp_pool) read margins
 constexpr int kLogitTargetWg = 1024;
 constexpr int kKRing = 4;
 
@@ -177,7 +178,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
   __shared__ float red[4][kRowBlk];
   const int nrb = wpad / kRowBlk;
-  const int rb = blockIdx.y % nrb;
+  // last row block first: with a window as long as the prompt, later rows
+  // attend more keys, and dispatching the heavy workgroups first keeps the
+  // last round from being all heavy ones
+  const int rb = nrb - 1 - (int)(blockIdx.y % nrb);
   const int h = blockIdx.y / nrb;
   const int b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -203,8 +207,17 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   // the ring runs on into the next chunk: slice s of every chunk must land in
   // slot s % kKRing, so the slices per chunk are a multiple of the ring
   static_assert(DC == 0 || (DC % (2 * DS) == 0 && NS % kKRing == 0), "ring must tile the slices of a chunk");
+  // Logits more than kNeverRead keys past their row's position are never read
+  // (rowsum reads row w up to key S - W + w + 256, imp_pool reads key s from
+  // rows whose position is at least s - 270): a workgroup wholly past that
+  // line has nothing to do, and one wholly past its rows' positions has
+  // nothing to multiply (no q block to stage).
+  const int wg_key0 = blockIdx.x * (kChunkM * cpw);
+  if constexpr (MODE == HC_SCORE_SNAPKV)
+    if (wg_key0 > qpos0 + nw - 1 + kNeverRead) return;  // workgroup-uniform
+  const bool stage = MODE != HC_SCORE_SNAPKV || wg_key0 <= qpos0 + nw - 1;
   KOperand<T> ka[kKRing], kb[kKRing];
-  int key0 = blockIdx.x * (kChunkM * cpw) + wave * 32;
+  int key0 = wg_key0 + wave * 32;
   uint32_t off0 = key0 + col < S ? (uint32_t)(key0 + col) * rowb : kOob;
   uint32_t off1 = key0 + 16 + col < S ? (uint32_t)(key0 + 16 + col) * rowb : kOob;
   // first K slices in flight before the q block is staged
@@ -219,12 +232,21 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     kb[0].load(krs, off1, 0, kk);
   }
   const double* qsrc = qf + (bh * wpad + w0) * D;
-  for (int i = threadIdx.x; i < kRowBlk * D; i += 256) sq[(i / D) * ld + (i % D)] = qsrc[i];
+  if (stage)
+    for (int i = threadIdx.x; i < kRowBlk * D; i += 256) sq[(i / D) * ld + (i % D)] = qsrc[i];
   __syncthreads();
 
   // wave-uniform chunk count: short prompts stop at their last chunk
   const int nch = key0 < S ? min(cpw, (S - key0 + kChunkM - 1) / kChunkM) : 0;
-  for (int c = 0; c < nch; ++c) {
+  // Chunks whose 32 keys all lie after every row's position are wholly masked
+  // (a window as long as the prompt, H2O); keys only grow, so they are the
+  // last nch - nmul chunks: stored as -inf below, no MFMA.
+  int nmul = nch;
+  if constexpr (MODE == HC_SCORE_SNAPKV) {
+    const int last = qpos0 + nw - 1;  // the last row's position
+    nmul = key0 > last ? 0 : min(nch, (last - key0) / kChunkM + 1);
+  }
+  for (int c = 0; c < nmul; ++c) {
     // the q reads repeat for every chunk; keep them inside the loop (hoisted,
     // all D/2 of them would hold 2*D registers for the kernel's lifetime)
     __asm__ volatile("" ::: "memory");
@@ -306,6 +328,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   }
 
   if constexpr (MODE != HC_SCORE_SNAPKV) return;
+  for (int c = nmul; c < nch && key0 <= qpos0 + nw - 1 + kNeverRead; ++c) {  // wholly masked chunks
+    const uint32_t ninf = __float_as_uint(-INFINITY);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int nbk = 0; nbk < 2; ++nbk) {
+#pragma unroll
+        for (int mb = 0; mb < 2; ++mb) {
+          const int w = 16 * nbk + kk + 4 * i;
+          const int key = key0 + 16 * mb + col;
+          bstore<4>(lrs, (key < S && w < nw) ? (uint32_t)((w0 + w) * S + key) * 4u : kOob, &ninf);
+        }
+      }
+    }
+    key0 += kChunkM;
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {  // row 16*(j/4) + kk + 4*(j%4), max over the 16 key lanes
     float m = mrow[j];
@@ -356,8 +394,10 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ l
   const DetExp dexp = DetExp::load();
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + (bh * W + wr) * S, (uint32_t)S * 4u);
   // this split's steps [st0, st0 + nstep) and keys [st0 * 256, kend); a wave
-  // past W streams nothing (kend = 0)
-  const int nstep_all = (S + 255) / 256;
+  // past W streams nothing (kend = 0).  The row attends keys up to its own
+  // position S - W + w; later keys are -inf and add only the bias, so the
+  // row's steps stop there (half the keys when the window is the prompt).
+  const int nstep_all = (min(S, S - W + wr + 1) + 255) / 256;
   const int sps = (nstep_all + nsplit - 1) / nsplit;
   const int st0 = min(nstep_all, sp * sps);
   const int nstep = live ? min(nstep_all, st0 + sps) - st0 : 0;
@@ -484,10 +524,16 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
       }
     }
   };
+  // Key s is masked in the rows w < s - (S - W) (their position precedes s),
+  // which add exact zeros to acc (starting at +0): the chain starts at the
+  // first row the workgroup's smallest key attends, rounded down to a row
+  // pair (every row for a short window).
+  int wbeg = 0;
+  if constexpr (MODE == HC_SCORE_SNAPKV) wbeg = max(0, c0 - P - (S - W)) / (2 * kImpRows) * (2 * kImpRows);
   uint32_t xa[kImpRows], xb[kImpRows];
   RowStat sa[kImpRows], sb[kImpRows];
-  load(xa, sa, 0);
-  for (int w0 = 0; w0 < W; w0 += 2 * kImpRows) {
+  load(xa, sa, wbeg);
+  for (int w0 = wbeg; w0 < W; w0 += 2 * kImpRows) {
     load(xb, sb, w0 + kImpRows);
     chain(xa, sa, w0);
     load(xa, sa, w0 + 2 * kImpRows);

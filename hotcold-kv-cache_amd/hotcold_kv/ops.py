@@ -336,7 +336,7 @@ def snapkv_scores(q_post, keys, window_size, scaling, kernel_size=7, pooling="ma
     return scores
 
 
-def h2o_prefill_scores(q_post, keys, scaling, max_workspace_bytes=2 << 30):
+def h2o_prefill_scores(q_post, keys, scaling, max_workspace_bytes=10 << 30):
     """H2O accumulated attention of the whole prompt per KV head, fp32
     (B,Hk,S) (scoring.py:82-107): for every key, the causal softmax
     probabilities of all query rows summed, per query head, then averaged over
@@ -344,7 +344,9 @@ def h2o_prefill_scores(q_post, keys, scaling, max_workspace_bytes=2 << 30):
     covering the prompt, one query head per "KV head" and no pooling, so it
     runs on the exact window-score kernels (bit-defined like SnapKV's) over
     keys repeated per query head, followed by the group mean.  Query heads go
-    in chunks whose logits workspace fits max_workspace_bytes."""
+    in chunks whose logits workspace fits max_workspace_bytes (the 32 heads of
+    an 8k prompt fit one: the importance kernel needs their keys together to
+    fill the GPU, one chain per key)."""
     _require_device(q_post, keys)
     B, Hq, S, D = q_post.shape
     Hk = keys.shape[1]
