@@ -26,6 +26,7 @@
 //   * split partials (m, l, acc) are merged by a second, one-pass kernel.
 #include "hc_common.h"
 #include <stddef.h>
+#include <algorithm>
 
 namespace hc {
 
@@ -757,12 +758,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int D
 //   col = (1/G) sum_g exp2(score[h][s] - M[h]) / L[h],   h = hk*G + g,
 // is added to acc[b][hk][s]; key S-1 (the token appended this step) starts
 // from zero (the torch.cat of a zero column, layer_state.py:108-111).
-// grid (cdiv(S, 256), Hk, B), block 256.
-__global__ __launch_bounds__(256) void h2o_accum_kernel(const float* scores, const float* ml, int Hq, int G, int S,
-                                                        float* acc, int64_t a_sb, int64_t a_sh) {
-  const int s = blockIdx.x * 256 + threadIdx.x;
-  const int hk = blockIdx.y, b = blockIdx.z;
-  if (s >= S) return;
+// The one expression both H2O kernels use, so the fused eviction writes the
+// same bits as accumulation followed by a separate selection.
+__device__ __forceinline__ float h2o_updated(const float* scores, const float* ml, int Hq, int G, int S, int b,
+                                             int hk, int s, const float* acc_row) {
   float col = 0.f;
   for (int g = 0; g < G; ++g) {
     const int h = hk * G + g;
@@ -772,8 +771,111 @@ __global__ __launch_bounds__(256) void h2o_accum_kernel(const float* scores, con
     col += (sc == -INFINITY) ? 0.f : exp2f(sc - M) / L;
   }
   col /= (float)G;
+  return (s == S - 1 ? 0.f : acc_row[s]) + col;
+}
+
+// grid (cdiv(S, 256), Hk, B), block 256.
+__global__ __launch_bounds__(256) void h2o_accum_kernel(const float* scores, const float* ml, int Hq, int G, int S,
+                                                        float* acc, int64_t a_sb, int64_t a_sh) {
+  const int s = blockIdx.x * 256 + threadIdx.x;
+  const int hk = blockIdx.y, b = blockIdx.z;
+  if (s >= S) return;
   float* a = acc + b * a_sb + hk * a_sh;
-  a[s] = (s == S - 1 ? 0.f : a[s]) + col;
+  a[s] = h2o_updated(scores, ml, Hq, G, S, b, hk, s, a);
+}
+
+// H2O re-eviction of a cache one token over its budget, fused with the
+// accumulation above (layer_state.py:102-114 then _compress, :68-79).  With
+// keep_prefix = prefix - 1, keep_index (scoring.py:110-132) drops exactly one
+// prefix row: the last in (score desc, index asc) order, i.e. the lowest
+// order key and, among equal keys, the highest index.  Every other row keeps
+// its order, so row r goes to r - (r > e).  K, V and the updated scores are
+// written out of place into the destination buffers (S-1 rows).
+//
+// Every workgroup recomputes the updated scores of all S keys into LDS and
+// finds e itself (a few KB of logits from L2), so the row copy needs no
+// second launch; its own rows' loads are issued first and overlap that work.
+// grid (cdiv(S, rows_per_wg), Hk, B), block 256; rows are rowb bytes
+// (a multiple of 16), rows_per_wg <= 256 and rows_per_wg * rowb / 16 <= 2 * 256.
+constexpr int kEvictMaxKeys = 8192;
+struct H2OEvictArgs {
+  const char* k;
+  int64_t k_sb, k_sh, k_ss;  // byte strides
+  const char* v;
+  int64_t v_sb, v_sh, v_ss;
+  char* kd;
+  int64_t kd_sb, kd_sh, kd_ss;
+  char* vd;
+  int64_t vd_sb, vd_sh, vd_ss;
+  float* acc_dst;
+  int64_t ad_sb, ad_sh;
+  int prefix, rowb, rows_per_wg;
+};
+
+__global__ __launch_bounds__(256) void h2o_evict_one_kernel(const float* scores, const float* ml, int Hq, int G,
+                                                            int S, const float* acc, int64_t a_sb, int64_t a_sh,
+                                                            H2OEvictArgs e) {
+  __shared__ float sm_sc[kEvictMaxKeys];
+  __shared__ uint32_t sm_best[2][4];
+  const int hk = blockIdx.y, b = blockIdx.z;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int r0 = blockIdx.x * e.rows_per_wg;
+  const int cpr = e.rowb >> 4;
+  const char* ks = e.k + b * e.k_sb + hk * e.k_sh;
+  const char* vs = e.v + b * e.v_sb + hk * e.v_sh;
+
+  u32x4 kr[2], vr[2];
+  int row[2], part[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int c = tid + 256 * i;
+    row[i] = r0 + c / cpr;
+    part[i] = c - (c / cpr) * cpr;
+    if (c >= e.rows_per_wg * cpr || row[i] >= S) row[i] = -1;
+    if (row[i] >= 0) {
+      kr[i] = ld16(ks + row[i] * e.k_ss + part[i] * 16);
+      vr[i] = ld16(vs + row[i] * e.v_ss + part[i] * 16);
+    }
+  }
+
+  const float* arow = acc + b * a_sb + hk * a_sh;
+  for (int s = tid; s < S; s += 256) sm_sc[s] = h2o_updated(scores, ml, Hq, G, S, b, hk, s, arow);
+  __syncthreads();
+
+  // lowest (order key, ~index) over the prefix
+  uint32_t bk = 0xffffffffu, bi = 0xffffffffu;
+  for (int s = tid; s < e.prefix; s += 256) {
+    const uint32_t key = order_key(sm_sc[s]), inv = ~(uint32_t)s;
+    if (key < bk || (key == bk && inv < bi)) { bk = key; bi = inv; }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    const uint32_t ok = __shfl_xor(bk, off, 64), oi = __shfl_xor(bi, off, 64);
+    if (ok < bk || (ok == bk && oi < bi)) { bk = ok; bi = oi; }
+  }
+  if (lane == 0) { sm_best[0][wave] = bk; sm_best[1][wave] = bi; }
+  __syncthreads();
+  bk = sm_best[0][0]; bi = sm_best[1][0];
+#pragma unroll
+  for (int w = 1; w < 4; ++w) {
+    const uint32_t ok = sm_best[0][w], oi = sm_best[1][w];
+    if (ok < bk || (ok == bk && oi < bi)) { bk = ok; bi = oi; }
+  }
+  const int ev = (int)~bi;
+
+  char* kd = e.kd + b * e.kd_sb + hk * e.kd_sh;
+  char* vd = e.vd + b * e.vd_sb + hk * e.vd_sh;
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    if (row[i] >= 0 && row[i] != ev) {
+      const int d = row[i] - (row[i] > ev);
+      st16(kd + d * e.kd_ss + part[i] * 16, kr[i]);
+      st16(vd + d * e.vd_ss + part[i] * 16, vr[i]);
+    }
+  }
+  const int r = r0 + tid;
+  if (tid < e.rows_per_wg && r < S && r != ev)
+    e.acc_dst[b * e.ad_sb + hk * e.ad_sh + (r - (r > ev))] = sm_sc[r];
 }
 
 // Per-token eviction score of the reference kernel (kernels.py:66-67, 134-136):
@@ -995,7 +1097,7 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
                               float* evict_loss, int64_t* evict_idx,
                               void* workspace, int64_t workspace_bytes, int64_t num_splits,
                               void* stream, const DecodeArgs* ap, float* h2o_acc = nullptr,
-                              int64_t h2o_sb = 0, int64_t h2o_sh = 0) {
+                              int64_t h2o_sb = 0, int64_t h2o_sh = 0, const H2OEvictArgs* h2o_ev = nullptr) {
   if (dropout != 0.0) return set_error(HC_ERR_DROPOUT, "dropout must be 0.0 , because we are not in training");
   HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16, "decode: bad dtype %d", dtype);
   HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && D > 0 && S > 0, "decode: empty shape B=%lld Hq=%lld Hk=%lld D=%lld S=%lld",
@@ -1088,7 +1190,12 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
   if (rc != HC_OK) return rc;
   if ((rc = check_launch("decode_attn")) != HC_OK) return rc;
 
-  if (h2o_acc) {
+  if (h2o_acc && h2o_ev) {
+    const dim3 grid((unsigned)cdiv(S, h2o_ev->rows_per_wg), (unsigned)Hk, (unsigned)B);
+    hipLaunchKernelGGL(h2o_evict_one_kernel, grid, dim3(256), 0, st, a.scores, a.ml, (int)Hq, G, (int)S, h2o_acc,
+                       h2o_sb, h2o_sh, *h2o_ev);
+    if ((rc = check_launch("h2o_evict_one")) != HC_OK) return rc;
+  } else if (h2o_acc) {
     const dim3 grid((unsigned)cdiv(S, 256), (unsigned)Hk, (unsigned)B);
     hipLaunchKernelGGL(h2o_accum_kernel, grid, dim3(256), 0, st, a.scores, a.ml, (int)Hq, G, (int)S, h2o_acc,
                        h2o_sb, h2o_sh);
@@ -1171,4 +1278,53 @@ extern "C" int hc_decode_attn_h2o(int dtype, int64_t B, int64_t Hq, int64_t Hk, 
   return decode_impl(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss, nullptr, 0, 0,
                      nullptr, 0, 0, nullptr, 0, 0, nullptr, scaling, 0.0, out, o_sb, o_sh, nullptr, nullptr, workspace,
                      workspace_bytes, num_splits, stream, nullptr, acc, a_sb, a_sh);
+}
+
+extern "C" int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                                        const void* q, int64_t q_sb, int64_t q_sh,
+                                        const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                                        const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                        double scaling,
+                                        void* out, int64_t o_sb, int64_t o_sh,
+                                        const float* acc, int64_t a_sb, int64_t a_sh,
+                                        int64_t window, int64_t budget,
+                                        void* k_dst, int64_t kd_sb, int64_t kd_sh, int64_t kd_ss,
+                                        void* v_dst, int64_t vd_sb, int64_t vd_sh, int64_t vd_ss,
+                                        float* acc_dst, int64_t ad_sb, int64_t ad_sh,
+                                        void* workspace, int64_t workspace_bytes, int64_t num_splits,
+                                        void* stream) {
+  HC_REQUIRE(acc != nullptr && acc_dst != nullptr && k_dst != nullptr && v_dst != nullptr,
+             "decode_h2o_evict: acc, acc_dst, k_dst and v_dst are required");
+  HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16,
+             "decode_h2o_evict: bad dtype %d", dtype);
+  HC_REQUIRE(window >= 0 && budget >= 0, "decode_h2o_evict: negative window or budget");
+  // keep_index's counts (scoring.py:118-120): exactly one prefix row goes.
+  const int64_t win = window < S ? window : S;
+  const int64_t prefix = S - win;
+  int64_t kp = budget - win < prefix ? budget - win : prefix;
+  if (kp < 0) kp = 0;
+  HC_REQUIRE(prefix - kp == 1, "decode_h2o_evict: S=%lld, window=%lld, budget=%lld drop %lld rows, not one",
+             (long long)S, (long long)window, (long long)budget, (long long)(prefix - kp));
+  HC_REQUIRE(S <= kEvictMaxKeys, "decode_h2o_evict: S=%lld above %d", (long long)S, kEvictMaxKeys);
+  HC_REQUIRE(acc != acc_dst && k != k_dst && v != v_dst, "decode_h2o_evict: destinations must not alias sources");
+  const int es = dtype_size(dtype);
+  const int64_t rowb = D * es;
+  HC_REQUIRE(rowb % 16 == 0 && rowb <= 8192, "decode_h2o_evict: row bytes %lld must be a multiple of 16, <= 8192",
+             (long long)rowb);
+  HC_REQUIRE(((uintptr_t)k_dst % 16 == 0) && ((uintptr_t)v_dst % 16 == 0) && (kd_sb * es) % 16 == 0 &&
+                 (kd_sh * es) % 16 == 0 && (kd_ss * es) % 16 == 0 && (vd_sb * es) % 16 == 0 &&
+                 (vd_sh * es) % 16 == 0 && (vd_ss * es) % 16 == 0 && kd_ss >= D && vd_ss >= D,
+             "decode_h2o_evict: k_dst / v_dst rows must be 16-byte aligned with row stride >= D");
+  H2OEvictArgs ev;
+  ev.k = reinterpret_cast<const char*>(k); ev.k_sb = k_sb * es; ev.k_sh = k_sh * es; ev.k_ss = k_ss * es;
+  ev.v = reinterpret_cast<const char*>(v); ev.v_sb = v_sb * es; ev.v_sh = v_sh * es; ev.v_ss = v_ss * es;
+  ev.kd = reinterpret_cast<char*>(k_dst); ev.kd_sb = kd_sb * es; ev.kd_sh = kd_sh * es; ev.kd_ss = kd_ss * es;
+  ev.vd = reinterpret_cast<char*>(v_dst); ev.vd_sb = vd_sb * es; ev.vd_sh = vd_sh * es; ev.vd_ss = vd_ss * es;
+  ev.acc_dst = acc_dst; ev.ad_sb = ad_sb; ev.ad_sh = ad_sh;
+  ev.prefix = (int)prefix;
+  ev.rowb = (int)rowb;
+  ev.rows_per_wg = (int)std::min<int64_t>(256, 512 / (rowb / 16));
+  return decode_impl(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss, nullptr, 0, 0,
+                     nullptr, 0, 0, nullptr, 0, 0, nullptr, scaling, 0.0, out, o_sb, o_sh, nullptr, nullptr, workspace,
+                     workspace_bytes, num_splits, stream, nullptr, const_cast<float*>(acc), a_sb, a_sh, &ev);
 }

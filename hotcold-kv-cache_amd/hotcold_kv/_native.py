@@ -87,6 +87,19 @@ SIGNATURES = {
         _vp, _i64, _i64,
         _vp, _i64, _i64,
         _vp, _i64, _i64, _vp]),
+    "hc_decode_attn_h2o_evict": (_int, [
+        _int, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _dbl,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64,
+        _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64, _vp]),
     "hc_snapkv_score_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i64]),
     "hc_snapkv_score": (_int, [
         _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,

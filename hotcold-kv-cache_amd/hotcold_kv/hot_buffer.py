@@ -122,23 +122,37 @@ class HotBuffer:
         self.n = 0
         self.append(k, v, pre, pos)
 
+    def spare(self):
+        """The second storage (same capacity), which out-of-place compactions
+        write into before adopt_spare makes it current."""
+        if self._spare is None or self._spare["k"].shape[2] != self.held + self.cap:
+            self._spare = self._new_storage(self.cap)
+        return self._spare
+
+    def spare_rows(self, name):
+        """Hot rows (from row `held` on, full capacity) of the second storage."""
+        return self.spare()[name][:, :, self.held:]
+
+    def adopt_spare(self, n):
+        """Make the second storage current with n hot rows (written there out
+        of place); the held slot travels with the buffer."""
+        dst = self.spare()
+        if self.held:
+            ops.append_rows(0, self.st["k"][:, :, :self.held], dst["k"], self.st["v"][:, :, :self.held], dst["v"])
+        self._spare, self.st = self.st, dst
+        self.n = int(n)
+
     def compact(self, keep):
         """Keep rows keep (B,H,n) per head or (B,n) shared, in that order."""
         n_keep = int(keep.shape[-1])
-        if self._spare is None or self._spare["k"].shape[2] != self.held + self.cap:
-            self._spare = self._new_storage(self.cap)
-        dst = self._spare
+        dst = self.spare()
         pairs = [(self.keys, dst["k"]), (self.values, dst["v"])]
         if self.with_pre:
             pairs.append((self.pre_keys, dst["p"]))
         ops.gather_rows(keep, pairs, dst_row0=self.held,
                         pos_src=self.positions if self.with_pos else None,
                         pos_dst=dst["pos"] if self.with_pos else None)
-        if self.held:
-            # the held slot travels with the buffer
-            ops.append_rows(0, self.st["k"][:, :, :self.held], dst["k"], self.st["v"][:, :, :self.held], dst["v"])
-        self._spare, self.st = self.st, dst
-        self.n = n_keep
+        self.adopt_spare(n_keep)
 
     def gather_from(self, k, v, keep, pre=None, pos=None):
         """Fill the hot rows with rows keep of external tensors (B,H,S,D)."""

@@ -284,6 +284,84 @@ def decode_attention_h2o(q, k, v, scaling, acc, out=None, num_splits=0):
     return out
 
 
+H2O_EVICT_MAX_KEYS = 8192
+
+
+def h2o_evicts_one(S, window_size, budget):
+    """True when keep_index(scores of S keys, window_size, budget) drops
+    exactly one row and S fits the fused eviction (S <= 8192)."""
+    _, prefix, kp = keep_counts(S, window_size, budget)
+    return prefix - kp == 1 and S <= H2O_EVICT_MAX_KEYS
+
+
+def decode_attention_h2o_evict(q, k, v, scaling, acc, window_size, budget, k_dst, v_dst, acc_dst, out=None,
+                               num_splits=0):
+    """One H2O decode step whose append put the cache one row over budget
+    (layer_state.py:102-114 then _compress, :68-79): attends q over k/v
+    (B,Hk,S,D), forms the updated scores acc + this step's G-mean
+    probabilities (key S-1 from zero), and writes the S-1 rows that
+    keep_index(updated, window_size, budget) keeps -- all but the lowest
+    prefix score, the highest index among equal ones -- in order into k_dst,
+    v_dst (B,Hk,>=S-1,D) and acc_dst (B,Hk,>=S-1) fp32.  acc is only read.
+    Equals decode_attention_h2o + keep_index + gather_rows bit for bit.
+    Returns out (B,Hq,D).  Called every decode step: shapes and strides are
+    read once per tensor."""
+    _require_device(q, k, v, acc, k_dst, v_dst, acc_dst)
+    lib = N.lib()
+    if q.dim() == 4:
+        if q.shape[2] != 1:
+            raise RuntimeError(f"decode_attention_h2o_evict: expected one query token, got q {tuple(q.shape)}")
+        q = q[:, :, 0, :]
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    k = _rows4(k, "key")
+    v = _rows4(v, "value")
+    B, Hq, D = q.shape
+    ks, vs = tuple(k.shape), tuple(v.shape)
+    _, Hk, S, _ = ks
+    dt = q.dtype
+    if vs != ks or ks[0] != B or ks[3] != D or k.dtype != dt or v.dtype != dt:
+        raise RuntimeError("decode_attention_h2o_evict: q, k, v shapes / dtypes do not match")
+    st = {}
+    for name, t, rows in (("acc", acc, S), ("acc_dst", acc_dst, S - 1)):
+        sh, sd = tuple(t.shape), t.stride()
+        if t.dtype != torch.float32 or len(sh) != 3 or sh[:2] != (B, Hk) or sh[2] < rows or sd[2] != 1:
+            raise RuntimeError(f"decode_attention_h2o_evict: {name} must be (B,Hk,>={rows}) fp32 with unit last "
+                               f"stride; got {sh} {t.dtype}")
+        st[name] = sd
+    for name, t in (("k_dst", k_dst), ("v_dst", v_dst)):
+        sh, sd = tuple(t.shape), t.stride()
+        if len(sh) != 4 or sh[:2] != (B, Hk) or sh[2] < S - 1 or sh[3] != D or t.dtype != dt or sd[3] != 1:
+            raise RuntimeError(f"decode_attention_h2o_evict: {name} must be (B,Hk,>={S - 1},D) {dt} rows; "
+                               f"got {sh} {t.dtype}")
+        st[name] = sd
+    if not h2o_evicts_one(S, window_size, budget):
+        raise RuntimeError(f"decode_attention_h2o_evict: S={S}, window {window_size}, budget {budget} does not "
+                           f"drop exactly one row (or S > {H2O_EVICT_MAX_KEYS})")
+    if out is None:
+        out = torch.empty((B, Hq, D), dtype=dt, device=q.device)
+    nbytes = lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, 1)
+    ws = _workspace("decode", q.device, nbytes)
+    qs, kss, vss, os_ = q.stride(), k.stride(), v.stride(), out.stride()
+    sa, sad, skd, svd = st["acc"], st["acc_dst"], st["k_dst"], st["v_dst"]
+    rc = lib.hc_decode_attn_h2o_evict(
+        N.dtype_code(dt), B, Hq, Hk, D, S,
+        _ptr(q), qs[0], qs[1],
+        _ptr(k), kss[0], kss[1], kss[2],
+        _ptr(v), vss[0], vss[1], vss[2],
+        float(scaling),
+        _ptr(out), os_[0], os_[1],
+        _ptr(acc), sa[0], sa[1],
+        int(window_size), int(budget),
+        _ptr(k_dst), skd[0], skd[1], skd[2],
+        _ptr(v_dst), svd[0], svd[1], svd[2],
+        _ptr(acc_dst), sad[0], sad[1],
+        _ptr(ws), ws.numel(), int(num_splits),
+        _stream_handle(q.device))
+    N.check(rc, "hc_decode_attn_h2o_evict")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # SnapKV compaction
 # ---------------------------------------------------------------------------

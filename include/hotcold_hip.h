@@ -139,6 +139,34 @@ int hc_decode_attn_h2o(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
                        void* workspace, int64_t workspace_bytes, int64_t num_splits, void* stream);
 
 /*
+ * H2O decode step with the re-eviction fused (layer_state.py:102-114 followed
+ * by _compress, :68-79, when the append put the cache one row over budget).
+ * Attends as hc_decode_attn_h2o, forms the updated scores
+ * acc'[s] = acc[s] + (G-mean probability of key s) (key S-1 from zero), and
+ * drops the one prefix row keep_index(acc', window, budget) (scoring.py:110-132)
+ * leaves out: the lowest score, the highest index among equal scores.  The
+ * S-1 surviving rows of K, V and acc', in their order, are written to
+ * k_dst / v_dst ([B][Hk][>=S-1][D], dtype) and acc_dst ([B][Hk][>=S-1] fp32);
+ * acc is not modified.  Equals hc_decode_attn_h2o + hc_topk_keep +
+ * hc_gather_rows bit for bit.  Requires keep_index to drop exactly one row
+ * (S - min(window, S) - max(0, min(budget - min(window, S), prefix)) == 1),
+ * S <= 8192, destinations distinct from the sources, D * elem_bytes a
+ * multiple of 16.  The workspace is that of hc_decode_attn_h2o.
+ */
+int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                             const void* q, int64_t q_sb, int64_t q_sh,
+                             const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                             const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                             double scaling,
+                             void* out, int64_t o_sb, int64_t o_sh,
+                             const float* acc, int64_t a_sb, int64_t a_sh,
+                             int64_t window, int64_t budget,
+                             void* k_dst, int64_t kd_sb, int64_t kd_sh, int64_t kd_ss,
+                             void* v_dst, int64_t vd_sb, int64_t vd_sh, int64_t vd_ss,
+                             float* acc_dst, int64_t ad_sb, int64_t ad_sh,
+                             void* workspace, int64_t workspace_bytes, int64_t num_splits, void* stream);
+
+/*
  * Window importance scores per KV head, fp32 [B][Hk][S] (row stride S).
  * Replaces snapkv_importance (scoring.py:50-79) with _group_query_to_kv
  * (scoring.py:17-26) and pool1d (scoring.py:40-47) in HC_SCORE_SNAPKV mode,

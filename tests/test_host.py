@@ -363,6 +363,18 @@ def test_press_config_checks():
         PressLayerState("streaming", 64, 16, 7, "maxpool")
 
 
+def test_h2o_fused_eviction_applies_exactly_when_one_row_goes():
+    """The fused H2O step runs only where keep_index drops exactly one row:
+    the step after the cache reaches the budget, with the window inside it."""
+    for S, window, budget in [(513, 32, 512), (65, 16, 64), (2, 1, 1), (8192, 64, 8191)]:
+        assert ops.h2o_evicts_one(S, window, budget)
+        w, prefix, kp = ref.keep_counts(S, window, budget)
+        assert prefix - kp == 1 and kp + w == S - 1
+    for S, window, budget in [(512, 32, 512), (514, 32, 512), (513, 513, 512), (100, 200, 99),
+                              (8193, 64, 8192), (40, 8, 0)]:
+        assert not ops.h2o_evicts_one(S, window, budget), (S, window, budget)
+
+
 def test_gqa_reduction_shapes():
     q = torch.randn(1, 8, 5, 16)
     assert scoring._group_query_to_kv(q, 2).shape == (1, 2, 5, 16)

@@ -412,6 +412,91 @@ def test_decode_attention_h2o_accumulates_group_mean_probs(dtype, splits):
     assert torch.equal(got[:, :, S:], acc0[:, :, S:].double())   # rows past S untouched
 
 
+H2O_EVICT_CASES = [
+    # B, Hq, Hk, S, D, window, dtype, splits, tie
+    (1, 32, 8, 513, 128, 32, torch.float16, 0, None),      # 8k/budget-512 layer, one step past the budget
+    (2, 32, 8, 513, 128, 32, torch.bfloat16, 5, "low"),
+    (2, 8, 2, 65, 16, 16, torch.float32, 1, "high"),       # reference test geometry (test_baselines.py:46)
+    (1, 16, 4, 700, 64, 64, torch.float16, 0, "zero"),
+    (3, 8, 8, 100, 256, 1, torch.bfloat16, 0, "nan"),
+    (1, 32, 8, 4097, 128, 64, torch.float16, 0, "low"),    # budget 4096
+    (1, 4, 1, 2, 32, 1, torch.float32, 0, None),           # one prefix key, one window key
+]
+
+
+@pytest.mark.parametrize("B,Hq,Hk,S,D,window,dtype,splits,tie", H2O_EVICT_CASES)
+def test_decode_attention_h2o_evict_equals_unfused(B, Hq, Hk, S, D, window, dtype, splits, tie):
+    """The fused step (attend, update scores, drop one row) against
+    decode_attention_h2o + keep_index + gather_rows: output, K, V and scores
+    bit for bit into strided destination views, acc unchanged, rows past S-1
+    untouched; the dropped row is the oracle's keep_index complement.  Tie
+    cases plant equal keys with equal old scores so the updated scores tie
+    exactly at the minimum (the highest index must go), at index 0 or the
+    prefix end, or NaN scores (never dropped)."""
+    budget = S - 1
+    prefix = S - min(window, S)
+    q, k, v = _randn((B, Hq, 1, D), 61, dtype), _randn((B, Hk, S, D), 62, dtype), _randn((B, Hk, S, D), 63, dtype)
+    acc0 = torch.rand((B, Hk, S + 3), generator=torch.Generator().manual_seed(64)) * 10
+    if tie is not None:
+        rows = {"low": [2, 7, prefix // 2, prefix - 1], "high": [0, 3, 5], "zero": [0, prefix // 3],
+                "nan": [1, 4]}[tie]
+        rows = sorted(set(r for r in rows if r < prefix))
+        k[:, :, rows] = k[:, :, rows[:1]]
+        acc0[:, :, rows] = -5.0 if tie != "nan" else float("nan")
+    kd, vd = (torch.full((B, Hk, S + 4, D + 8), 7.0, dtype=dtype, device=DEV) for _ in range(2))
+    ad = torch.full((B, Hk, S + 5), 3.0, device=DEV)
+    k_dst, v_dst, a_dst = kd[:, :, 1:S, :D], vd[:, :, 2:S + 1, 8:], ad[:, :, :S - 1]
+
+    qd, kdv, vdv = q.to(DEV), k.to(DEV), v.to(DEV)
+    acc_a = acc0.to(DEV)
+    out_a = ops.decode_attention_h2o(qd, kdv, vdv, 0.09, acc_a[:, :, :S], num_splits=splits)
+    keep = ops.keep_index(acc_a[:, :, :S], window, budget)
+    assert torch.equal(keep.cpu(), ref.keep_index(acc_a[:, :, :S].cpu(), window, budget))
+    acc_b = acc0.to(DEV)
+    out_b = ops.decode_attention_h2o_evict(qd, kdv, vdv, 0.09, acc_b[:, :, :S], window, budget,
+                                           k_dst, v_dst, a_dst, num_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(out_a.cpu(), out_b.cpu())
+    assert torch.equal(acc_b.cpu().view(torch.int32), acc0.view(torch.int32))
+    kc = keep.cpu()
+    assert torch.equal(k_dst.cpu(), ref.gather_kv(k, kc))
+    assert torch.equal(v_dst.cpu(), ref.gather_kv(v, kc))
+    want_sc = acc_a[:, :, :S].cpu().gather(2, kc)
+    assert torch.equal(a_dst.cpu().contiguous().view(torch.int32), want_sc.view(torch.int32))
+    # nothing outside the S-1 destination rows is written
+    assert bool((kd[:, :, 0] == 7).all() and (kd[:, :, S:] == 7).all() and (kd[..., D:] == 7).all())
+    assert bool((vd[:, :, :2] == 7).all() and (vd[:, :, S + 1:] == 7).all() and (vd[..., :8] == 7).all())
+    assert bool((ad[:, :, S - 1:] == 3).all())
+    if tie in ("low", "high", "zero"):
+        dropped = set(range(S)) - set(kc[0, 0].tolist())
+        assert dropped == {rows[-1]}
+
+
+def test_decode_attention_h2o_evict_argument_errors():
+    B, Hq, Hk, S, D = 1, 8, 2, 40, 64
+    q, k, v = (torch.zeros(s, dtype=torch.float16, device=DEV) for s in ((B, Hq, D), (B, Hk, S, D), (B, Hk, S, D)))
+    acc = torch.zeros(B, Hk, S, device=DEV)
+    kd, vd, ad = torch.empty_like(k), torch.empty_like(v), torch.empty_like(acc)
+    with pytest.raises(RuntimeError, match="exactly one row"):
+        ops.decode_attention_h2o_evict(q, k, v, 0.1, acc, 8, S - 2, kd, vd, ad)   # two rows over budget
+    with pytest.raises(RuntimeError, match="exactly one row"):
+        ops.decode_attention_h2o_evict(q, k, v, 0.1, acc, 8, S, kd, vd, ad)       # within budget
+    with pytest.raises(RuntimeError, match="exactly one row"):
+        ops.decode_attention_h2o_evict(q, k, v, 0.1, acc, S, S - 1, kd, vd, ad)   # window covers the cache
+    with pytest.raises(RuntimeError, match="acc_dst"):
+        ops.decode_attention_h2o_evict(q, k, v, 0.1, acc, 8, S - 1, kd, vd, ad[:, :, :S - 2])
+    lib = ops.N.lib()
+    ws = torch.empty(1 << 20, dtype=torch.uint8, device=DEV)
+    ptr = ops._ptr
+    rc = lib.hc_decode_attn_h2o_evict(
+        ops.N.dtype_code(q.dtype), B, Hq, Hk, D, S, ptr(q), q.stride(0), q.stride(1),
+        ptr(k), k.stride(0), k.stride(1), k.stride(2), ptr(v), v.stride(0), v.stride(1), v.stride(2), 0.1,
+        ptr(q), q.stride(0), q.stride(1), ptr(acc), acc.stride(0), acc.stride(1), 8, S - 1,
+        ptr(k), k.stride(0), k.stride(1), k.stride(2), ptr(vd), vd.stride(0), vd.stride(1), vd.stride(2),
+        ptr(ad), ad.stride(0), ad.stride(1), ptr(ws), ws.numel(), 0, ops._stream_handle(q.device))
+    assert rc != 0 and "alias" in lib.hc_last_error().decode()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("to_host", [False, True])
 def test_gather_evict_upcast_and_stage(dtype, to_host):
