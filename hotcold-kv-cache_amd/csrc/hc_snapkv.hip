@@ -178,11 +178,19 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
   __shared__ float red[4][kRowBlk];
   const int nrb = wpad / kRowBlk;
-  // last row block first: with a window as long as the prompt, later rows
-  // attend more keys, and dispatching the heavy workgroups first keeps the
-  // last round from being all heavy ones
-  const int rb = nrb - 1 - (int)(blockIdx.y % nrb);
-  const int h = blockIdx.y / nrb;
+  // Workgroup -> (row block, key range, head), row block fastest.  The
+  // hardware hands consecutive workgroups to the eight XCDs in turn; with a
+  // window as long as the prompt, a key range's work grows with the row
+  // block (the causal skip), so a key range fixed per XCD (key range
+  // fastest) loads the XCDs unevenly -- 6.6x between the first and the last
+  // of four ranges at an 8k prompt.  Row blocks in turn spread every range
+  // over all XCDs.  Heavy workgroups go first (last row block, last key
+  // range) so the last round is not all heavy ones.
+  const int nx = (int)gridDim.x;
+  const int f = (int)blockIdx.x + nx * (int)blockIdx.y;
+  const int rb = nrb - 1 - f % nrb;
+  const int xr = nx - 1 - (f / nrb) % nx;
+  const int h = f / (nrb * nx);
   const int b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, kk = lane >> 4;
@@ -212,7 +220,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   // rows whose position is at least s - 270): a workgroup wholly past that
   // line has nothing to do, and one wholly past its rows' positions has
   // nothing to multiply (no q block to stage).
-  const int wg_key0 = blockIdx.x * (kChunkM * cpw);
+  const int wg_key0 = xr * (kChunkM * cpw);
   if constexpr (MODE == HC_SCORE_SNAPKV)
     if (wg_key0 > qpos0 + nw - 1 + kNeverRead) return;  // workgroup-uniform
   const bool stage = MODE != HC_SCORE_SNAPKV || wg_key0 <= qpos0 + nw - 1;
