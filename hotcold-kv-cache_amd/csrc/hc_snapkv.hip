@@ -475,6 +475,70 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const float* __restrict__ l
 // row's max and 1/l_w are wave-uniform: they come through scalar loads into
 // SGPRs, with no LDS staging and no per-row branch.
 constexpr int kImpRows = 8;
+// Windows from this many rows on take the mirrored-pair importance kernel
+// when there is no pooling (chain lengths then differ by up to W rows).
+constexpr int kMirrorMinW = 1024;
+
+// One key's importance: the fma chain over rows [wbeg, W) of the logits
+// column at byte offset `base` (kOob for a lane without a key).  Rows are
+// streamed kImpRows at a time with the next group in flight; a group's
+// logits and (scalar) row statistics are issued one group ahead.  Groups
+// start at multiples of kImpRows and the statistics are padded to kStatPad
+// (a multiple of 2 * kImpRows) rows.
+template <int MODE>
+__device__ __forceinline__ double imp_chain(__amdgpu_buffer_rsrc_t rs, uint32_t base, uint32_t rowb,
+                                            const RowStat* st, int wst, int W, int wbeg, const DetExp& dexp) {
+  static_assert(kStatPad % (2 * kImpRows) == 0, "statistics padding covers whole row pairs");
+  auto load = [&](uint32_t (&dst)[kImpRows], RowStat (&sdst)[kImpRows], int w0) {
+#pragma unroll
+    for (int r = 0; r < kImpRows; ++r) {
+      const int w = w0 + r;
+      bload<4>(rs, base + (w < W ? (uint32_t)w * rowb : kOob), &dst[r]);
+    }
+    if constexpr (MODE == HC_SCORE_SNAPKV) {
+      // the look-ahead past the last group re-reads the last group (unused)
+      const RowStat* g = st + min(w0, wst - kImpRows);
+#pragma unroll
+      for (int r = 0; r < kImpRows; ++r) sdst[r] = g[r];
+    }
+  };
+  double acc = 0.0;
+  // rows [w0, w0 + kImpRows); rows past W add an exact zero: their padding
+  // statistics are {+inf, 0}, so x = -inf, e = 0 and fma(0, 0, acc) = acc
+  // (acc >= +0)
+  auto chain = [&](const uint32_t (&x)[kImpRows], const RowStat (&sx)[kImpRows], int w0) {
+#pragma unroll
+    for (int r = 0; r < kImpRows; ++r) {
+      const int w = w0 + r;
+      const float L = __uint_as_float(x[r]);
+      if constexpr (MODE == HC_SCORE_SNAPKV) {
+        acc = __builtin_fma(dexp((double)L - sx[r].m), sx[r].inv, acc);
+      } else {
+        acc = acc + (w < W ? (double)L : 0.0);
+      }
+    }
+  };
+  uint32_t xa[kImpRows], xb[kImpRows];
+  RowStat sa[kImpRows], sb[kImpRows];
+  load(xa, sa, wbeg);
+  for (int w0 = wbeg; w0 < W; w0 += 2 * kImpRows) {
+    load(xb, sb, w0 + kImpRows);
+    chain(xa, sa, w0);
+    load(xa, sa, w0 + 2 * kImpRows);
+    chain(xb, sb, w0 + kImpRows);
+  }
+  return acc;
+}
+
+// First row a chain over keys from kmin on must start at: key s is masked in
+// the rows w < s - (S - W) (their position precedes s), which add exact zeros
+// to acc (starting at +0), so the chain starts at the first row kmin attends,
+// rounded down to a row pair.  The logits it then reads lie at most
+// 255 + 2 * kImpRows - 1 = 270 keys past a row's position for a workgroup's
+// 256 keys, inside what the logits kernel writes.
+__device__ __forceinline__ int imp_first_row(int kmin, int S, int W) {
+  return max(0, kmin - (S - W)) / (2 * kImpRows) * (2 * kImpRows);
+}
 
 template <int MODE>
 __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__ logits,
@@ -495,58 +559,10 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
   // the others, whose result is discarded).
   const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + bh * W * S, (uint32_t)((int64_t)W * S * 4));
   const uint32_t base = sv ? (uint32_t)s * 4u : kOob;
-  const uint32_t rowb = (uint32_t)S * 4u;
   const int wst = (int)cdiv(W, kStatPad) * kStatPad;
-  const RowStat* st = rstat + bh * wst;
-  // a group's logits and (scalar) row statistics are issued one group ahead;
-  // groups start at multiples of kImpRows, and the statistics are padded to
-  // kStatPad (a multiple of 2 * kImpRows) rows
-  static_assert(kStatPad % (2 * kImpRows) == 0, "statistics padding covers whole row pairs");
-  auto load = [&](uint32_t (&dst)[kImpRows], RowStat (&sdst)[kImpRows], int w0) {
-#pragma unroll
-    for (int r = 0; r < kImpRows; ++r) {
-      const int w = w0 + r;
-      bload<4>(rs, base + (w < W ? (uint32_t)w * rowb : kOob), &dst[r]);
-    }
-    if constexpr (MODE == HC_SCORE_SNAPKV) {
-      // the look-ahead past the last group re-reads the last group (unused)
-      const RowStat* g = st + min(w0, wst - kImpRows);
-#pragma unroll
-      for (int r = 0; r < kImpRows; ++r) sdst[r] = g[r];
-    }
-  };
-  double acc = 0.0;
   const DetExp dexp = DetExp::load();
-  // rows [w0, w0 + kImpRows); rows past W add an exact zero: their padding
-  // statistics are {+inf, 0}, so x = -inf, e = 0 and fma(0, 0, acc) = acc
-  // (acc >= +0)
-  auto chain = [&](const uint32_t (&x)[kImpRows], const RowStat (&sx)[kImpRows], int w0) {
-#pragma unroll
-    for (int r = 0; r < kImpRows; ++r) {
-      const int w = w0 + r;
-      const float L = __uint_as_float(x[r]);
-      if constexpr (MODE == HC_SCORE_SNAPKV) {
-        acc = __builtin_fma(dexp((double)L - sx[r].m), sx[r].inv, acc);
-      } else {
-        acc = acc + (w < W ? (double)L : 0.0);
-      }
-    }
-  };
-  // Key s is masked in the rows w < s - (S - W) (their position precedes s),
-  // which add exact zeros to acc (starting at +0): the chain starts at the
-  // first row the workgroup's smallest key attends, rounded down to a row
-  // pair (every row for a short window).
-  int wbeg = 0;
-  if constexpr (MODE == HC_SCORE_SNAPKV) wbeg = max(0, c0 - P - (S - W)) / (2 * kImpRows) * (2 * kImpRows);
-  uint32_t xa[kImpRows], xb[kImpRows];
-  RowStat sa[kImpRows], sb[kImpRows];
-  load(xa, sa, wbeg);
-  for (int w0 = wbeg; w0 < W; w0 += 2 * kImpRows) {
-    load(xb, sb, w0 + kImpRows);
-    chain(xa, sa, w0);
-    load(xa, sa, w0 + 2 * kImpRows);
-    chain(xb, sb, w0 + kImpRows);
-  }
+  const int wbeg = MODE == HC_SCORE_SNAPKV ? imp_first_row(c0 - P, S, W) : 0;
+  const double acc = imp_chain<MODE>(rs, base, (uint32_t)S * 4u, rstat + bh * wst, wst, W, wbeg, dexp);
   sm_imp[threadIdx.x] = sv ? (float)acc : 0.f;
   __syncthreads();
   const int t = threadIdx.x;
@@ -569,6 +585,39 @@ __global__ __launch_bounds__(256) void imp_pool_kernel(const float* __restrict__
     out = (float)(sum / (double)ksize);
   }
   scores[bh * S + s] = out;
+}
+
+// Importance without pooling for long windows, keys in mirrored pairs.
+// With a window as long as the prompt (H2O) key s's chain covers the S - s
+// rows at or after its position, so one thread per key leaves the first
+// keys' threads with thousands of rows and the last keys' with a few, and
+// every chain must stay in one thread (its order is part of the scores).
+// Here thread t of workgroup x owns keys a = 256x + t and S - 1 - a: every
+// thread's two chains together cover about S + 1 rows.  The chains and the
+// fp32 result are those of imp_pool_kernel with P = 0, bit for bit.
+// grid (ceil(ceil(S / 2) / 256), Hk, B), block 256.
+__global__ __launch_bounds__(256) void imp_mirror_kernel(const float* __restrict__ logits,
+                                                         const RowStat* __restrict__ rstat, int Hk, int S, int W,
+                                                         float* __restrict__ scores) {
+  const int h = blockIdx.y, b = blockIdx.z;
+  const int64_t bh = (int64_t)b * Hk + h;
+  const int c0 = blockIdx.x * 256;
+  const int a = c0 + (int)threadIdx.x;
+  const int m = S - 1 - a;                 // the mirrored key
+  const bool av = a <= m, mv = a < m;      // the middle key of an odd S once
+  const __amdgpu_buffer_rsrc_t rs = make_rsrc(logits + bh * W * S, (uint32_t)((int64_t)W * S * 4));
+  const uint32_t rowb = (uint32_t)S * 4u;
+  const int wst = (int)cdiv(W, kStatPad) * kStatPad;
+  const RowStat* st = rstat + bh * wst;
+  const DetExp dexp = DetExp::load();
+  const double acc_a = imp_chain<HC_SCORE_SNAPKV>(rs, av ? (uint32_t)a * 4u : kOob, rowb, st, wst, W,
+                                                  imp_first_row(c0, S, W), dexp);
+  // the workgroup's mirrored keys are S - 1 - c0 - 255 .. S - 1 - c0
+  const double acc_m = imp_chain<HC_SCORE_SNAPKV>(rs, mv ? (uint32_t)m * 4u : kOob, rowb, st, wst, W,
+                                                  imp_first_row(max(0, S - 1 - c0 - 255), S, W), dexp);
+  float* out = scores + bh * S;
+  if (av) out[a] = (float)acc_a;
+  if (mv) out[m] = (float)acc_m;
 }
 
 // out[b][s] = (float)((sum_h (double)x[b][h][s]) / H), h ascending.
@@ -626,6 +675,12 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
     else
       hipLaunchKernelGGL(rowsum_kernel<false>, g, dim3(256), 0, st, (const float*)logits, (const uint32_t*)rmax,
                          (int)Hk, (int)S, (int)W, nsplit, rstat);
+  }
+  if (mode == HC_SCORE_SNAPKV && P == 0 && W >= kMirrorMinW) {
+    const dim3 gm((unsigned)cdiv(cdiv(S, 2), 256), (unsigned)Hk, (unsigned)B);
+    hipLaunchKernelGGL(imp_mirror_kernel, gm, dim3(256), 0, st, (const float*)logits, (const RowStat*)rstat,
+                       (int)Hk, (int)S, (int)W, scores);
+    return;
   }
   const dim3 gi((unsigned)cdiv(S, 256 - 2 * P), (unsigned)Hk, (unsigned)B);
   if (mode == HC_SCORE_SNAPKV)

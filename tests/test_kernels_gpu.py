@@ -262,6 +262,9 @@ SCORE_CASES = [
     (1, 8, 2, 3001, 128, 7, torch.bfloat16, 5, "avgpool"),   # S % 4 != 0 (scalar row loads)
     # enough rows and keys for several 128-key chunks per logits workgroup
     (8, 32, 8, 4160, 128, 32, torch.float16, 7, "maxpool"),
+    # a long window without pooling: importance over mirrored key pairs
+    (1, 4, 2, 2500, 64, 1100, torch.float16, 1, "maxpool"),
+    (2, 2, 2, 1301, 32, 1301, torch.float32, 1, "maxpool"),
 ]
 
 
@@ -376,6 +379,9 @@ H2O_CASES = [
     (2, 8, 2, 200, 16, torch.float16),
     (1, 32, 8, 333, 64, torch.float16),
     (1, 8, 8, 97, 128, torch.bfloat16),
+    # windows of 1024 rows or more: importance over mirrored key pairs
+    (1, 4, 2, 1500, 64, torch.float16),
+    (1, 2, 1, 2049, 32, torch.bfloat16),     # odd S: the middle key once
 ]
 
 
