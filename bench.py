@@ -37,9 +37,11 @@ Reported:
   decode launch per layer, as a model's layer loop issues them), warm-cache
   figures, the reference's torch-CPU path on a bounded sample, and
   other_workloads: decode / compaction / inject figures of the 16k, 32k and
-  64k workloads (secondary; --no-other-configs skips them).
+  64k workloads, and h2o: H2O prefill scores and decode steps on one layer
+  (secondary; --no-other-configs skips them).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+                    [--no-cpu-baseline] [--no-other-configs] [--h2o-only]
 """
 
 import argparse
@@ -475,6 +477,61 @@ def measure_config(w, dev, flush, reps=24):
     return out
 
 
+def measure_h2o(w, dev, reps=5, steps=96):
+    """H2O (secondary, not the headline) on one layer of the workload's
+    geometry: the prefill scores (the whole prompt as the window under the
+    fp64 exact-score contract, causal half only) and decode steps at the
+    budget through PressLayerState (append, then attention, score update and
+    the one-row eviction in one call; one layer per step, so the step is
+    bound by its two calls from Python).  Inputs are N(0,1), generated on the
+    device."""
+    import torch
+    from hotcold_kv import ops
+    from hotcold_kv.baselines.layer_state import PressLayerState
+
+    g = torch.Generator(device=dev).manual_seed(9)
+    dt, D, Hk, Hq, S = w.dtype, w.head_dim, w.hk, w.hq, w.seq_len
+    q = torch.randn((1, Hq, S, D), generator=g, device=dev, dtype=dt)
+    k = torch.randn((1, Hk, S, D), generator=g, device=dev, dtype=dt)
+    v = torch.randn((1, Hk, S, D), generator=g, device=dev, dtype=dt)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ops.h2o_prefill_scores(q, k, w.scaling)
+    ts = []
+    for _ in range(reps):
+        e0.record()
+        ops.h2o_prefill_scores(q, k, w.scaling)
+        e1.record()
+        torch.cuda.synchronize()
+        ts.append(e0.elapsed_time(e1))
+    pre_ms = statistics.median(ts)
+    flops = 2.0 * Hq * D * S * (S + 1) / 2        # causal (row, key) pairs of every query head
+    st = PressLayerState("h2o", budget=w.budget, window_size=w.window, kernel_size=w.pool, pooling="maxpool")
+    st.prefill(q, k, v, Hq // Hk, w.scaling)
+    del q, k, v
+    qs = torch.randn((steps, 1, Hq, 1, D), generator=g, device=dev, dtype=dt)
+    ks = torch.randn((steps, 1, Hk, 1, D), generator=g, device=dev, dtype=dt)
+    vs = torch.randn((steps, 1, Hk, 1, D), generator=g, device=dev, dtype=dt)
+    for t in range(8):
+        st.decode(qs[t], ks[t], vs[t], Hq // Hk, w.scaling)
+    torch.cuda.synchronize()
+    e0.record()
+    for t in range(steps):
+        st.decode(qs[t], ks[t], vs[t], Hq // Hk, w.scaling)
+    e1.record()
+    torch.cuda.synchronize()
+    step_us = e0.elapsed_time(e1) * 1e3 / steps
+    out = {"workload": f"one layer of {w.name}: {Hq} query / {Hk} KV heads, {S} tokens, budget {w.budget}, "
+                       f"window {w.window}",
+           "prefill_scores_ms": round(pre_ms, 3),
+           "prefill_scores_tflops_fp64": round(flops / (pre_ms * 1e-3) / 1e12, 2),
+           "decode_step_us": round(step_us, 2), "decode_steps": steps,
+           "decode_hot_rows": st.get_seq_length()}
+    del st, qs, ks, vs
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(w, sample_seconds, n_layers=4):
     """The reference's torch-CPU path (snapkv_importance -> keep_index ->
     gather_kv, then per decode step cat + repeat_kv + SDPA) on a bounded
@@ -534,7 +591,9 @@ def main():
     ap.add_argument("--cpu-sample-seconds", type=float, default=15.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-other-configs", action="store_true",
-                    help="skip the secondary figures of the 16k/32k/64k workloads")
+                    help="skip the secondary figures of the 16k/32k/64k workloads and H2O")
+    ap.add_argument("--h2o-only", action="store_true",
+                    help="only the H2O figures of one layer (one JSON object; for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; the hot tier shards by batch and KV head "
@@ -551,6 +610,9 @@ def main():
     w = synthetic.WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.h2o_only:
+        print(json.dumps({"h2o": measure_h2o(w, dev)}), flush=True)
+        return
     log(f"workload {w.name}: generating inputs on {torch.cuda.get_device_name(dev)}")
     stream = stream_rates(dev)
     log(f"device read sweep {stream['read_GBps']:.0f} GB/s, copy {stream['copy_GBps']:.0f} GB/s")
@@ -602,6 +664,13 @@ def main():
             others.append(r)
         del flush
 
+    h2o = None
+    if not args.no_other_configs and args.workload == "llama8b_8k_b512":
+        log("H2O on one layer ...")
+        h2o = measure_h2o(w, dev)
+        log(f"  prefill scores {h2o['prefill_scores_ms']} ms ({h2o['prefill_scores_tflops_fp64']} TFLOP/s fp64), "
+            f"decode step {h2o['decode_step_us']} us at {h2o['decode_hot_rows']} hot rows")
+
     cpu = None
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
@@ -650,6 +719,7 @@ def main():
                                 "bytes_per_job": int(cbytes)},
         "device_stream": stream,
         "other_workloads": others,
+        "h2o": h2o,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
