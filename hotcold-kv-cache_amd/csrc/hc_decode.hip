@@ -506,13 +506,14 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       for (int j = 0; j < DPL; ++j) st.acc[g][j] = 0.f;
   }
 
-  // Wave w streams the contiguous keys [wbeg, wend): equal counts per wave,
-  // so no wave of the workgroup waits on a longer one at the final barrier.
-  const int kpw = (key_end - key_begin + NW - 1) / NW;
-  const int wbeg = key_begin + wave * kpw;
-  const int wend = min(key_end, wbeg + kpw);
-  const int first = wbeg;
-  const int nt = wbeg < wend ? (wend - wbeg + 15) / 16 : 0;
+  // Wave w takes the 16-key tiles w, w + NW, w + 2 NW, ... of the split's
+  // range, so the waves of a workgroup read neighbouring tiles at any
+  // moment.  Contiguous per-wave ranges measured 13% slower at 72 MB per
+  // launch (16.9 against 14.7 us): the last waves to receive their rows held
+  // the workgroup at its final barrier.  Tile counts differ by at most one.
+  const int first = key_begin + wave * 16;
+  const int wend = key_end;
+  const int nt = first < key_end ? (key_end - first + 16 * NW - 1) / (16 * NW) : 0;
   {
     QFrag<T, D> qf;
     const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
@@ -524,7 +525,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     TileRegs<T, D> r[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i)
-      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * 16, key_begin, wend, col, grp, nullptr);
+      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * 16 * NW, key_begin, wend, col, grp, nullptr);
 
     // Fused append: the last wave of the last split attends the new token as
     // a one-key tile and copies the token's K/V (and pre-RoPE key and
@@ -582,7 +583,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
-      for (int i = 0; i < NBUF - 1; ++i) r[i].keep &= tile_keep_bits(first + i * 16, key_begin, grp, sm_bits);
+      for (int i = 0; i < NBUF - 1; ++i) r[i].keep &= tile_keep_bits(first + i * 16 * NW, key_begin, grp, sm_bits);
     }
     const uint32_t* bits = use_bits ? sm_bits : nullptr;
     float* srow = EVICT ? a.scores + ((int64_t)b * a.Hq + hk * G + min(col, G - 1)) * a.S : nullptr;
@@ -592,13 +593,13 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
 #define HC_RING_GROUP(g0)                                                                                  \
   _Pragma("unroll") for (int j = 0; j < NBUF; ++j) {                                                       \
     const int t = (g0) + j;                                                                                \
-    load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * 16,       \
+    load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * 16 * NW,  \
                     key_begin, wend, col, grp, bits);                                                      \
     if (t < nt) {                                                                                          \
       if constexpr (MX)                                                                                    \
-        process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow); \
+        process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16 * NW, wend, col, grp, srow); \
       else                                                                                                 \
-        process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16, wend, col, grp, srow); \
+        process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16 * NW, wend, col, grp, srow); \
     }                                                                                                      \
   }
     int g_start = 0;
