@@ -705,7 +705,7 @@ def main():
         "decode_launch_us_warm_last_step": round(warm_dec_ms * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(w.name),
-                     "kernel": "decode_attn_kernel (fused append, + decode_combine_kernel)",
+                     "kernel": "decode_attn_kernel (fused append; unsplit at this size, so no merge kernel)",
                      "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3),
                      "launch_timing": "events around [cache sweep; decode] minus events around [cache sweep]"},
         # the exact-score contract computes the window logits in fp64 on the
