@@ -66,7 +66,12 @@ __device__ __forceinline__ void find_digit(const uint32_t* hist, uint32_t krem, 
   }
   if (lane == 63) sm_scan[wave] = incl;
   __syncthreads();
-  for (int w = 0; w < wave; ++w) incl += sm_scan[w];
+  // all wave totals read at once (a loop bounded by `wave` issues its LDS
+  // reads one after another)
+  uint32_t before = 0;
+#pragma unroll
+  for (int w = 0; w < kTopkWaves; ++w) before += w < wave ? sm_scan[w] : 0u;
+  incl += before;
   const uint32_t excl = incl - v;
   if (excl < krem && excl + c0 >= krem) {
     *sm_digit = (uint32_t)(kDigitBins - 1 - 2 * t);
