@@ -385,6 +385,25 @@ H2O_CASES = [
 ]
 
 
+def test_h2o_prefill_scores_8k_properties():
+    """The full 8k prompt (too long for the oracle): every causal row's
+    probabilities sum to one, so each KV head's scores (group means) sum to
+    S; key 0 is all of row 0's mass, so its score is at least 1; scores are
+    non-negative; and equal keys give the harmonic tail sum_{i>=j} 1/(i+1)
+    exactly up to fp32 rounding."""
+    S, D = 8192, 128
+    q, k = _randn((1, 8, S, D), 47, torch.float16), _randn((1, 2, S, D), 48, torch.float16)
+    sc = ops.h2o_prefill_scores(q.to(DEV), k.to(DEV), D ** -0.5).double().cpu()
+    assert sc.shape == (1, 2, S) and bool((sc >= 0).all())
+    assert torch.allclose(sc.sum(-1), torch.full((1, 2), float(S), dtype=torch.float64), rtol=1e-5)
+    assert bool((sc[..., 0] >= 1.0 - 1e-6).all())
+    # equal keys: row i spreads 1/(i+1) over keys 0..i, so key j gets sum_{i>=j} 1/(i+1)
+    keq = torch.ones((1, 1, S, D), dtype=torch.float16)
+    sce = ops.h2o_prefill_scores(q[:, :4].to(DEV), keq.to(DEV), D ** -0.5).double().cpu()[0, 0]
+    tail = torch.flip(torch.cumsum(torch.flip(1.0 / torch.arange(1, S + 1, dtype=torch.float64), [0]), 0), [0])
+    assert torch.allclose(sce, tail, rtol=2e-5, atol=1e-6)
+
+
 @pytest.mark.parametrize("B,Hq,Hk,S,D,dtype", H2O_CASES)
 def test_h2o_prefill_scores_bit_exact(B, Hq, Hk, S, D, dtype):
     q, k = _randn((B, Hq, S, D), 41, dtype), _randn((B, Hk, S, D), 42, dtype)
