@@ -375,14 +375,10 @@ extern "C" int hc_topk_keep(int64_t B, int64_t H, int64_t S, const float* scores
   if (kp > prefix) kp = prefix;
   if (kp < 0) kp = 0;
   const size_t lds = (kp > 0 && prefix <= kTopkCache) ? (size_t)prefix * 4 : 0;
-  if (lds > 65536) {
-    static bool attr_set = false;
-    if (!attr_set) {
-      (void)hipFuncSetAttribute((const void*)topk_keep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                kTopkCache * 4);
-      attr_set = true;
-    }
-  }
+  // set on every call: the attribute is per device, and a process may drive several
+  if (lds > 65536 && hipFuncSetAttribute((const void*)topk_keep_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                         kTopkCache * 4) != hipSuccess)
+    return set_error(HC_ERR_HIP, "topk: cannot raise the dynamic LDS limit to %d bytes", kTopkCache * 4);
   hipLaunchKernelGGL(topk_keep_kernel, dim3((unsigned)H, (unsigned)B), dim3(kTopkThreads), lds,
                      reinterpret_cast<hipStream_t>(stream), scores, s_sb, s_sh, (int)H, (int)prefix, (int)kp,
                      (int)win, keep, evicted);
