@@ -466,12 +466,14 @@ struct DecodeState<bf16_t, D, GM> {
 
 // grid (splits, Hk, B), block 64*NW (NW waves).  Wave w streams a
 // contiguous key range through a ring of NBUF register tiles.
-enum DecodeMode { kPlain = 0, kEvict = 1, kAppend = 2 };
+// Mode bits: kEvict keeps every head's log2 logits (eviction score, H2O);
+// kAppend attends and writes this step's token from k_new / v_new.
+enum DecodeMode { kPlain = 0, kEvict = 1, kAppend = 2, kAppendEvict = 3 };
 
 template <typename T, int D, int GM, int NW, int NBUF, int MINW, int MODE>
 __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a) {
-  constexpr bool EVICT = MODE == kEvict;
-  constexpr bool APPEND = MODE == kAppend;
+  constexpr bool EVICT = (MODE & kEvict) != 0;
+  constexpr bool APPEND = (MODE & kAppend) != 0;
   constexpr int DPL = D / 16;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -606,10 +608,12 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     if constexpr (APPEND) {
       HC_RING_GROUP(0)
       g_start = NBUF;
+      // the token is key S-1; with EVICT its logit is kept like every key's
+      // (only the owning wave's row 0 falls inside [S-1, key_end))
       if constexpr (MX)
-        process_tile_mx<T, D, false>(rn, qf, st, G, a.scale_log2, 0, 0, col, grp, nullptr);
+        process_tile_mx<T, D, EVICT>(rn, qf, st, G, a.scale_log2, a.S - 1, tok ? a.S : 0, col, grp, srow);
       else
-        process_tile<T, D, GM, false>(rn, qf, st, G, a.scale_log2, 0, 0, col, grp, nullptr);
+        process_tile<T, D, GM, EVICT>(rn, qf, st, G, a.scale_log2, a.S - 1, tok ? a.S : 0, col, grp, srow);
     }
     for (int g0 = g_start; g0 < nt; g0 += NBUF) {
       HC_RING_GROUP(g0)
@@ -1017,7 +1021,9 @@ static DecodeLayout decode_layout(int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
 template <typename T, int D, int GM, int NW, int NBUF, int MINW>
 static void launch_decode(const DecodeArgs& a, hipStream_t st) {
   dim3 grid(a.splits, a.Hk, a.B);
-  if (a.scores)
+  if (a.scores && a.k_new)
+    hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, kAppendEvict>), grid, dim3(64 * NW), 0, st, a);
+  else if (a.scores)
     hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, kEvict>), grid, dim3(64 * NW), 0, st, a);
   else if (a.k_new)
     hipLaunchKernelGGL((decode_attn_kernel<T, D, GM, NW, NBUF, MINW, kAppend>), grid, dim3(64 * NW), 0, st, a);
@@ -1147,7 +1153,8 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
                      (long long)workspace_bytes);
   HC_REQUIRE(((uintptr_t)workspace % 256) == 0, "decode: workspace must be 256-byte aligned");
   HC_REQUIRE((evict_loss == nullptr) == (evict_idx == nullptr), "decode: evict_loss and evict_idx go together");
-  HC_REQUIRE(!(h2o_acc && (evict_loss || ap)), "decode: H2O accumulation runs alone");
+  HC_REQUIRE(!(h2o_acc && evict_loss), "decode: H2O accumulation and the eviction score are exclusive");
+  HC_REQUIRE(!(evict_loss && ap), "decode: the eviction score is not computed with a fused append");
 
   DecodeArgs a;
   a.q = q; a.q_sb = q_sb; a.q_sh = q_sh;
@@ -1285,6 +1292,8 @@ extern "C" int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_
                                         const void* q, int64_t q_sb, int64_t q_sh,
                                         const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
                                         const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                        const void* k_new, int64_t kn_sb, int64_t kn_sh,
+                                        const void* v_new, int64_t vn_sb, int64_t vn_sh,
                                         double scaling,
                                         void* out, int64_t o_sb, int64_t o_sh,
                                         const float* acc, int64_t a_sb, int64_t a_sh,
@@ -1325,7 +1334,12 @@ extern "C" int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_
   ev.prefix = (int)prefix;
   ev.rowb = (int)rowb;
   ev.rows_per_wg = (int)std::min<int64_t>(256, 512 / (rowb / 16));
+  HC_REQUIRE((k_new == nullptr) == (v_new == nullptr), "decode_h2o_evict: k_new and v_new go together");
+  DecodeArgs ap{};
+  ap.k_new = k_new; ap.kn_sb = kn_sb; ap.kn_sh = kn_sh;
+  ap.v_new = v_new; ap.vn_sb = vn_sb; ap.vn_sh = vn_sh;
   return decode_impl(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss, nullptr, 0, 0,
                      nullptr, 0, 0, nullptr, 0, 0, nullptr, scaling, 0.0, out, o_sb, o_sh, nullptr, nullptr, workspace,
-                     workspace_bytes, num_splits, stream, nullptr, const_cast<float*>(acc), a_sb, a_sh, &ev);
+                     workspace_bytes, num_splits, stream, k_new ? &ap : nullptr, const_cast<float*>(acc), a_sb, a_sh,
+                     &ev);
 }

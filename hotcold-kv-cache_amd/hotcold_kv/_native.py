@@ -92,6 +92,8 @@ SIGNATURES = {
         _vp, _i64, _i64,
         _vp, _i64, _i64, _i64,
         _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64,
         _dbl,
         _vp, _i64, _i64,
         _vp, _i64, _i64,

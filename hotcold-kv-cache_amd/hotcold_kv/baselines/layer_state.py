@@ -128,20 +128,25 @@ class PressLayerState:
         its score, then keep the budget by score (window kept) when over it."""
         if k_post.shape[2] != 1:
             raise RuntimeError("H2O decode takes one token per step")
-        self.buf.append(k_post, v)
-        self._h2o_storage()
-        n = self.buf.n
+        n = self.buf.n + 1
         if (n > self.budget and not self.buf.with_pre and not self.buf.with_pos
                 and ops.h2o_evicts_one(n, self.window_size, self.budget)):
-            # one row over budget: attention, score update and the one-row
-            # eviction in one call, written into the second buffers
-            out = ops.decode_attention_h2o_evict(q_post, self.buf.keys, self.buf.values, scaling,
+            # one row over budget: append, attention, score update and the
+            # one-row eviction in one call, written into the second buffers
+            self.buf.ensure(n)
+            self._h2o_storage()
+            lo = self.buf.held
+            out = ops.decode_attention_h2o_evict(q_post, self.buf.st["k"][:, :, lo:lo + n],
+                                                 self.buf.st["v"][:, :, lo:lo + n], scaling,
                                                  self._h2o[:, :, :n], self.window_size, self.budget,
                                                  self.buf.spare_rows("k"), self.buf.spare_rows("v"),
-                                                 self._h2o_spare)
+                                                 self._h2o_spare, k_new=k_post, v_new=v)
             self.buf.adopt_spare(n - 1)
             self._h2o, self._h2o_spare = self._h2o_spare, self._h2o
             return out.unsqueeze(2)  # (B,Hq,1,D)
+        self.buf.append(k_post, v)
+        self._h2o_storage()
+        n = self.buf.n
         out = ops.decode_attention_h2o(q_post, self.buf.keys, self.buf.values, scaling, self._h2o[:, :, :n])
         if n > self.budget:
             keep = ops.keep_index(self._h2o[:, :, :n], self.window_size, self.budget)

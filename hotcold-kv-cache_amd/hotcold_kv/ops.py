@@ -295,7 +295,7 @@ def h2o_evicts_one(S, window_size, budget):
 
 
 def decode_attention_h2o_evict(q, k, v, scaling, acc, window_size, budget, k_dst, v_dst, acc_dst, out=None,
-                               num_splits=0):
+                               num_splits=0, k_new=None, v_new=None):
     """One H2O decode step whose append put the cache one row over budget
     (layer_state.py:102-114 then _compress, :68-79): attends q over k/v
     (B,Hk,S,D), forms the updated scores acc + this step's G-mean
@@ -304,9 +304,11 @@ def decode_attention_h2o_evict(q, k, v, scaling, acc, window_size, budget, k_dst
     prefix score, the highest index among equal ones -- in order into k_dst,
     v_dst (B,Hk,>=S-1,D) and acc_dst (B,Hk,>=S-1) fp32.  acc is only read.
     Equals decode_attention_h2o + keep_index + gather_rows bit for bit.
-    Returns out (B,Hq,D).  Called every decode step: shapes and strides are
-    read once per tensor."""
-    _require_device(q, k, v, acc, k_dst, v_dst, acc_dst)
+    With k_new, v_new (B,Hk,D) or (B,Hk,1,D) the step's token is appended in
+    the same launch (decode_attention_append): row S-1 of k/v is the free row
+    it is written into.  Returns out (B,Hq,D).  Called every decode step:
+    shapes and strides are read once per tensor."""
+    _require_device(q, k, v, acc, k_dst, v_dst, acc_dst, k_new, v_new)
     lib = N.lib()
     if q.dim() == 4:
         if q.shape[2] != 1:
@@ -338,6 +340,19 @@ def decode_attention_h2o_evict(q, k, v, scaling, acc, window_size, budget, k_dst
     if not h2o_evicts_one(S, window_size, budget):
         raise RuntimeError(f"decode_attention_h2o_evict: S={S}, window {window_size}, budget {budget} does not "
                            f"drop exactly one row (or S > {H2O_EVICT_MAX_KEYS})")
+    if (k_new is None) != (v_new is None):
+        raise RuntimeError("decode_attention_h2o_evict: k_new and v_new go together")
+    if k_new is not None:
+        k_new, v_new = (x[:, :, 0, :] if x.dim() == 4 else x for x in (k_new, v_new))
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            if tuple(t.shape) != (B, Hk, D) or t.dtype != dt:
+                raise RuntimeError(f"decode_attention_h2o_evict: {name} must be (B,Hk,D)=({B},{Hk},{D}) {dt}; "
+                                   f"got {tuple(t.shape)} {t.dtype}")
+        k_new = k_new if k_new.stride(-1) == 1 else k_new.contiguous()
+        v_new = v_new if v_new.stride(-1) == 1 else v_new.contiguous()
+        kns, vns = k_new.stride(), v_new.stride()
+    else:
+        kns = vns = (0, 0)
     if out is None:
         out = torch.empty((B, Hq, D), dtype=dt, device=q.device)
     nbytes = lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, 1)
@@ -349,6 +364,8 @@ def decode_attention_h2o_evict(q, k, v, scaling, acc, window_size, budget, k_dst
         _ptr(q), qs[0], qs[1],
         _ptr(k), kss[0], kss[1], kss[2],
         _ptr(v), vss[0], vss[1], vss[2],
+        _ptr(k_new), kns[0], kns[1],
+        _ptr(v_new), vns[0], vns[1],
         float(scaling),
         _ptr(out), os_[0], os_[1],
         _ptr(acc), sa[0], sa[1],

@@ -152,11 +152,18 @@ int hc_decode_attn_h2o(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
  * (S - min(window, S) - max(0, min(budget - min(window, S), prefix)) == 1),
  * S <= 8192, destinations distinct from the sources, D * elem_bytes a
  * multiple of 16.  The workspace is that of hc_decode_attn_h2o.
+ * With k_new / v_new ([B][Hk][D], 16-byte aligned rows) the step's token is
+ * appended in the same launch, as hc_decode_attn_append does: it is attended
+ * from k_new / v_new and written into row S-1 of k / v (which must then be
+ * writable) before the eviction copies the rows; NULL means row S-1 already
+ * holds it.  Both forms give the same bits.
  */
 int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
                              const void* q, int64_t q_sb, int64_t q_sh,
                              const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
                              const void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                             const void* k_new, int64_t kn_sb, int64_t kn_sh,
+                             const void* v_new, int64_t vn_sb, int64_t vn_sh,
                              double scaling,
                              void* out, int64_t o_sb, int64_t o_sh,
                              const float* acc, int64_t a_sb, int64_t a_sh,

@@ -497,6 +497,54 @@ def test_decode_attention_h2o_evict_equals_unfused(B, Hq, Hk, S, D, window, dtyp
         assert dropped == {rows[-1]}
 
 
+@pytest.mark.parametrize("dtype,splits", [(torch.float16, 0), (torch.bfloat16, 3), (torch.float32, 1)])
+def test_decode_attention_h2o_evict_with_fused_append(dtype, splits):
+    """The token appended inside the fused step (attended from k_new / v_new,
+    written into row S-1, its logit kept as key S-1's): the token row lands in
+    place; the output and the kept rows' updated scores are within the
+    tolerances of the fp64 oracle (acc + group-mean probabilities); the
+    dropped row is a prefix minimiser of the oracle's updated scores up to
+    that tolerance; and K, V are the bit-exact gather of every other row."""
+    B, Hq, Hk, S, D, window = 2, 32, 8, 513, 128, 32
+    budget, prefix = S - 1, S - window
+    q = _randn((B, Hq, 1, D), 71, dtype)
+    k, v = _randn((B, Hk, S, D), 72, dtype), _randn((B, Hk, S, D), 73, dtype)
+    acc0 = torch.rand((B, Hk, S), generator=torch.Generator().manual_seed(76)) * 10
+    acc0[:, :, S - 1] = 0
+    kd, vd = k.to(DEV), v.to(DEV)
+    kd[:, :, S - 1] = 0
+    vd[:, :, S - 1] = 0
+    k_dst, v_dst = torch.empty_like(kd), torch.empty_like(vd)
+    a_dst = torch.empty((B, Hk, S), device=DEV)
+    out = ops.decode_attention_h2o_evict(q.to(DEV), kd, vd, 0.09, acc0.to(DEV), window, budget, k_dst, v_dst, a_dst,
+                                         num_splits=splits, k_new=k[:, :, S - 1:].to(DEV),
+                                         v_new=v[:, :, S - 1:].to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(kd.cpu(), k) and torch.equal(vd.cpu(), v)          # the token row written in place
+    assert np.abs(out.float().cpu().numpy() - ref.decode_attention(q, k, v, 0.09)).max() <= TOL[dtype]
+    want = acc0.double() + ref.h2o_decode_probs(q, k, 0.09)
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    got_k = k_dst[:, :, :S - 1].cpu()
+    for b in range(B):
+        for h in range(Hk):
+            kept = [i for i in range(S) if i != _dropped_row(got_k[b, h], k[b, h])]
+            assert len(kept) == S - 1
+            e = (set(range(S)) - set(kept)).pop()
+            assert e < prefix
+            assert float(want[b, h, e]) <= float(want[b, h, :prefix].min()) + tol * 10, (b, h, e)
+            assert torch.equal(got_k[b, h], k[b, h, kept]) and torch.equal(v_dst[b, h, :S - 1].cpu(), v[b, h, kept])
+            assert torch.allclose(a_dst[b, h, :S - 1].cpu().double(), want[b, h, kept], rtol=tol, atol=tol * 1e-2)
+
+
+def _dropped_row(kept_rows, rows):
+    """Index of the one row of rows (S,D) missing from kept_rows (S-1,D), kept in order."""
+    n = kept_rows.shape[0]
+    for i in range(n):
+        if not torch.equal(kept_rows[i], rows[i]):
+            return i
+    return n
+
+
 def test_decode_attention_h2o_evict_argument_errors():
     B, Hq, Hk, S, D = 1, 8, 2, 40, 64
     q, k, v = (torch.zeros(s, dtype=torch.float16, device=DEV) for s in ((B, Hq, D), (B, Hk, S, D), (B, Hk, S, D)))
@@ -515,7 +563,8 @@ def test_decode_attention_h2o_evict_argument_errors():
     ptr = ops._ptr
     rc = lib.hc_decode_attn_h2o_evict(
         ops.N.dtype_code(q.dtype), B, Hq, Hk, D, S, ptr(q), q.stride(0), q.stride(1),
-        ptr(k), k.stride(0), k.stride(1), k.stride(2), ptr(v), v.stride(0), v.stride(1), v.stride(2), 0.1,
+        ptr(k), k.stride(0), k.stride(1), k.stride(2), ptr(v), v.stride(0), v.stride(1), v.stride(2),
+        None, 0, 0, None, 0, 0, 0.1,
         ptr(q), q.stride(0), q.stride(1), ptr(acc), acc.stride(0), acc.stride(1), 8, S - 1,
         ptr(k), k.stride(0), k.stride(1), k.stride(2), ptr(vd), vd.stride(0), vd.stride(1), vd.stride(2),
         ptr(ad), ad.stride(0), ad.stride(1), ptr(ws), ws.numel(), 0, ops._stream_handle(q.device))
