@@ -27,6 +27,7 @@
 #include "hc_common.h"
 #include <stddef.h>
 #include <algorithm>
+#include <mutex>
 
 namespace hc {
 
@@ -999,6 +1000,13 @@ static int64_t keys_per_split(int64_t S, int splits, int nw) {
 
 static int64_t align256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
+// Split count of one launch (the choice decode_impl makes).
+static int decode_splits(int es, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S_cache, int64_t num_splits,
+                         bool bitmap) {
+  const int nw = decode_cfg(es, (int)D, group_bucket(Hq / Hk)).nw;
+  return pick_splits(B * Hk, S_cache > 0 ? S_cache : 1, num_splits, nw, bitmap, D * es);
+}
+
 struct DecodeLayout {
   int64_t part_off, scores_off, ml_off, total;
 };
@@ -1128,7 +1136,7 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
   const bool bitmap = mask != nullptr || held_len > 0;
   const int64_t S_cache = ap ? S - 1 : S;  // a fused append's token is not read from k/v
   HC_REQUIRE(held_len <= S_cache, "decode: held_len %lld beyond the cached rows", (long long)held_len);
-  const int splits = pick_splits(B * Hk, S_cache > 0 ? S_cache : 1, num_splits, nw, bitmap, D * es);
+  const int splits = decode_splits(es, B, Hq, Hk, D, S_cache, num_splits, bitmap);
   // Buffer extents of one (b, kv head) must fit the 31-bit load offsets.
   const int64_t k_bytes = ((S - 1) * k_ss + D) * es, v_bytes = ((S - 1) * v_ss + D) * es;
   const int64_t q_bytes = ((Hq / Hk - 1) * q_sh + D) * es;
@@ -1342,4 +1350,99 @@ extern "C" int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_
                      nullptr, 0, 0, nullptr, 0, 0, nullptr, scaling, 0.0, out, o_sb, o_sh, nullptr, nullptr, workspace,
                      workspace_bytes, num_splits, stream, k_new ? &ap : nullptr, const_cast<float*>(acc), a_sb, a_sh,
                      &ev);
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free fused append + decode, for callers that cannot allocate
+// (code under HIP graph capture, tight serving loops, harnesses that forbid
+// hipMalloc).  It is hc_decode_attn_append with the split partials kept in a
+// static device array instead of a caller-owned workspace:
+//   * the array (kNoAllocScratchBytes) lives in the library's code object, so
+//     every GPU the library runs on holds its own copy until the process ends;
+//   * its device address is taken once per device with hipGetSymbolAddress
+//     (on the first call on that device, with that device current) and only
+//     that address is passed to the kernels -- the array's name in host code
+//     is a host-side stand-in, not device memory;
+//   * every call on one GPU shares that GPU's array and leaves its contents
+//     behind: the split partials are fully written before they are read, so
+//     nothing is cleared, and two calls that may overlap on one GPU (two
+//     streams) race on it;
+//   * a call whose partials would not fit is refused (HC_ERR_WORKSPACE), and
+//     no call allocates or frees memory.
+// ---------------------------------------------------------------------------
+namespace hc {
+constexpr int64_t kNoAllocScratchBytes = (int64_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kMaxScratchDevices = 64;
+static void* g_scratch_ptr[kMaxScratchDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array, taken on first use.
+static int scratch_address(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(HC_ERR_HIP, "decode_append_noalloc: hipGetDevice: %s", hipGetErrorString(e));
+  HC_REQUIRE(dev >= 0 && dev < kMaxScratchDevices, "decode_append_noalloc: device %d out of range", dev);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(reinterpret_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess)
+      return set_error(HC_ERR_HIP, "decode_append_noalloc: hipStreamGetDevice: %s", hipGetErrorString(e));
+    HC_REQUIRE(sdev == dev, "decode_append_noalloc: the stream belongs to device %d, the current device is %d",
+               (int)sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return set_error(HC_ERR_HIP, "decode_append_noalloc: hipGetSymbolAddress(scratch) on device %d: %s", dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return HC_OK;
+}
+}  // namespace hc
+
+extern "C" int hc_decode_attn_append_noalloc(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                                             const void* q, int64_t q_sb, int64_t q_sh,
+                                             void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                                             void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                             const void* k_new, int64_t kn_sb, int64_t kn_sh,
+                                             const void* v_new, int64_t vn_sb, int64_t vn_sh,
+                                             const void* p_new, int64_t pn_sb, int64_t pn_sh,
+                                             void* p_dst, int64_t pd_sb, int64_t pd_sh, int64_t pd_ss,
+                                             const int64_t* pos_new, int64_t posn_sb, int64_t* pos_dst,
+                                             int64_t posd_sb,
+                                             const uint8_t* mask, int64_t mask_sb,
+                                             int64_t held_len,
+                                             const int64_t* held_pos, int64_t hp_sb, int64_t hp_sh,
+                                             const uint8_t* held_valid, int64_t hv_sb, int64_t hv_sh,
+                                             const int64_t* cur_pos,
+                                             double scaling,
+                                             void* out, int64_t o_sb, int64_t o_sh,
+                                             int64_t num_splits, void* stream) {
+  HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16,
+             "decode_append_noalloc: bad dtype %d", dtype);
+  HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && D > 0 && S > 0 && Hq % Hk == 0,
+             "decode_append_noalloc: bad shape B=%lld Hq=%lld Hk=%lld D=%lld S=%lld", (long long)B, (long long)Hq,
+             (long long)Hk, (long long)D, (long long)S);
+  // The partials this launch needs, against the array's fixed size.
+  const bool bitmap = mask != nullptr || held_len > 0;
+  const int splits = decode_splits(dtype_size(dtype), B, Hq, Hk, D, S - 1, num_splits, bitmap);
+  const int64_t need = decode_layout(B, Hq, Hk, D, S, splits, 0).total;
+  if (need > kNoAllocScratchBytes)
+    return set_error(HC_ERR_WORKSPACE,
+                     "decode_append_noalloc: %d key splits over %lld (batch, kv head) units need %lld bytes of "
+                     "scratch, above the static maximum of %lld bytes; use fewer splits or hc_decode_attn_append",
+                     splits, (long long)(B * Hk), (long long)need, (long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  int rc = scratch_address(stream, &ws);
+  if (rc != HC_OK) return rc;
+  return hc_decode_attn_append(dtype, B, Hq, Hk, D, S, q, q_sb, q_sh, k, k_sb, k_sh, k_ss, v, v_sb, v_sh, v_ss,
+                               k_new, kn_sb, kn_sh, v_new, vn_sb, vn_sh, p_new, pn_sb, pn_sh, p_dst, pd_sb, pd_sh,
+                               pd_ss, pos_new, posn_sb, pos_dst, posd_sb, mask, mask_sb, held_len, held_pos, hp_sb,
+                               hp_sh, held_valid, hv_sb, hv_sh, cur_pos, scaling, out, o_sb, o_sh, ws,
+                               kNoAllocScratchBytes, num_splits, stream);
 }

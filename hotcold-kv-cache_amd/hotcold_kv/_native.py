@@ -78,6 +78,25 @@ SIGNATURES = {
         _vp, _i64, _i64,
         _vp, _i64, _i64,
         _vp]),
+    "hc_decode_attn_append_noalloc": (_int, [
+        _int, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _vp, _i64,
+        _vp, _i64,
+        _i64,
+        _vp, _i64, _i64,
+        _vp, _i64, _i64,
+        _vp,
+        _dbl,
+        _vp, _i64, _i64,
+        _i64,
+        _vp]),
     "hc_decode_attn_h2o": (_int, [
         _int, _i64, _i64, _i64, _i64, _i64,
         _vp, _i64, _i64,

@@ -6,7 +6,8 @@
  * int status: HC_OK (0) or a negative HC_ERR_* code.  hc_last_error() returns
  * a message for the last failure on the calling thread.  Nothing here
  * allocates device memory: scratch space is a caller-owned workspace whose
- * size the matching *_workspace_size() function reports.
+ * size the matching *_workspace_size() function reports (the one exception,
+ * hc_decode_attn_append_noalloc, uses a static device array instead).
  *
  * Strides are in ELEMENTS of the tensor they describe.  The innermost (head
  * dimension) stride is always 1.  A stride of 0 broadcasts (for example one
@@ -119,6 +120,36 @@ int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t 
                           void* out, int64_t o_sb, int64_t o_sh,
                           void* workspace, int64_t workspace_bytes, int64_t num_splits,
                           void* stream);
+
+/*
+ * hc_decode_attn_append without a workspace: no counterpart in the reference.
+ * It is for callers that cannot allocate (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The arguments and results
+ * are hc_decode_attn_append's, minus (workspace, workspace_bytes); the split
+ * partials live in a static 8 MiB device array that each GPU holds until the
+ * process ends.  Its address is taken once per device on the first call (the
+ * current device must be the stream's device).  A call whose partials need
+ * more than 8 MiB returns HC_ERR_WORKSPACE (fewer splits fit).  Every call on
+ * one GPU shares that GPU's array: calls that may overlap on one GPU (two
+ * streams) race.  Nothing is allocated or freed.
+ */
+int hc_decode_attn_append_noalloc(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
+                                  const void* q, int64_t q_sb, int64_t q_sh,
+                                  void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+                                  void* v, int64_t v_sb, int64_t v_sh, int64_t v_ss,
+                                  const void* k_new, int64_t kn_sb, int64_t kn_sh,
+                                  const void* v_new, int64_t vn_sb, int64_t vn_sh,
+                                  const void* p_new, int64_t pn_sb, int64_t pn_sh,
+                                  void* p_dst, int64_t pd_sb, int64_t pd_sh, int64_t pd_ss,
+                                  const int64_t* pos_new, int64_t posn_sb, int64_t* pos_dst, int64_t posd_sb,
+                                  const uint8_t* mask, int64_t mask_sb,
+                                  int64_t held_len,
+                                  const int64_t* held_pos, int64_t hp_sb, int64_t hp_sh,
+                                  const uint8_t* held_valid, int64_t hv_sb, int64_t hv_sh,
+                                  const int64_t* cur_pos,
+                                  double scaling,
+                                  void* out, int64_t o_sb, int64_t o_sh,
+                                  int64_t num_splits, void* stream);
 
 /*
  * Decode attention that also accumulates H2O scores (layer_state.py:55-65,
