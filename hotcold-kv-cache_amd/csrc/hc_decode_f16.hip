@@ -1,0 +1,8 @@
+// Decode attention kernel instances for f16 K/V (templates in hc_decode_kernels.h).
+#include "hc_decode_kernels.h"
+
+namespace hc {
+int decode_dispatch_f16(int64_t D, const DecodeArgs& a, int nw, hipStream_t st) {
+  return dispatch_d<half_t>(D, a, nw, st);
+}
+}  // namespace hc

@@ -33,8 +33,15 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
+# Leading bytes of a decode workspace that must be zero before its first
+# launch (the in-kernel split merge's arrival counters; launches leave them
+# zero).  The rest of every workspace needs no initialisation.
+DECODE_COUNTER_BYTES = 16384
+
+
 def _workspace(kind, device, nbytes):
-    """A zero-initialised uint8 workspace of at least nbytes for this stream."""
+    """A uint8 workspace of at least nbytes for this stream, allocated once and
+    grown geometrically; a new decode workspace gets its counter block zeroed."""
     key = (kind, device.index if device.index is not None else torch.cuda.current_device(),
            _stream_handle(device))
     with _ws_lock:
@@ -43,7 +50,9 @@ def _workspace(kind, device, nbytes):
             size = max(nbytes, 256)
             if ws is not None:
                 size = max(size, int(ws.numel() * 1.5))
-            ws = torch.zeros(size, dtype=torch.uint8, device=device)
+            ws = torch.empty(size, dtype=torch.uint8, device=device)
+            if kind == "decode":
+                ws[:DECODE_COUNTER_BYTES].zero_()
             _ws_cache[key] = ws
         return ws
 

@@ -63,10 +63,15 @@ const char* hc_last_error(void);
  *   evict_loss / evict_idx (may be NULL): the per-token eviction score
  *     mean_h(mean_d|p v| / l) rounded to dtype, [B][S] float, and its
  *     first-index argmin [B] int64 (kernels.py:66-67, 134-136).
- *   num_splits <= 0 picks a split count; with more than one split the
- *     partial results are merged by a second kernel.  The workspace must hold
+ *   num_splits <= 0 picks the launch shape (few short units are spread over
+ *     many workgroups); with more than one split the partial results are
+ *     merged inside the launch by the last workgroup of each (b, kv head) to
+ *     finish (by a second kernel above 4096 units).  The workspace must hold
  *     hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, with_evict)
- *     bytes; one workspace must not be used by two launches that may overlap.
+ *     bytes.  Its first 16384 bytes (the merge's arrival counters) must be
+ *     zero before the first launch on it, and every launch leaves them zero;
+ *     the rest needs no initialisation.  One workspace must not be used by
+ *     two launches that may overlap.
  *   dropout must be 0.0.
  */
 int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hk, int64_t D,
@@ -126,8 +131,9 @@ int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t 
  * It is for callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The arguments and results
  * are hc_decode_attn_append's, minus (workspace, workspace_bytes); the split
- * partials live in a static 8 MiB device array that each GPU holds until the
- * process ends.  Its address is taken once per device on the first call (the
+ * partials and merge counters live in a static 8 MiB device array (zero at
+ * load) that each GPU holds until the process ends.  Its address is taken
+ * once per device on the first call (the
  * current device must be the stream's device).  A call whose partials need
  * more than 8 MiB returns HC_ERR_WORKSPACE (fewer splits fit).  Every call on
  * one GPU shares that GPU's array: calls that may overlap on one GPU (two

@@ -68,6 +68,33 @@ def test_decode_matches_oracle(B, Hq, Hk, S, D, dtype, splits):
     assert np.abs(got - want).max() <= TOL[dtype], np.abs(got - want).max()
 
 
+@pytest.mark.parametrize("B,S,splits", [
+    (1, 2431, 16),    # 128 workgroups: merged in the kernel by the last split to finish
+    (2, 575, 0),      # one layer at a small batch: the default spreads it over many workgroups
+    (16, 2431, 8),    # 1024 workgroups: merged by a second kernel
+])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_decode_split_merge_paths(B, S, splits, dtype):
+    Hq, Hk, D = 32, 8, 128
+    q = _randn((B, Hq, 1, D), 21, dtype)
+    k = _randn((B, Hk, S, D), 22, dtype)
+    v = _randn((B, Hk, S, D), 23, dtype)
+    sc = 1.0 / math.sqrt(D)
+    want = ref.decode_attention(q, k, v, sc)
+    for rep in range(3):    # repeated launches on one workspace: the counters must come back to zero
+        out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), sc, num_splits=splits)
+        assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype], rep
+    # the fused append through the same shapes: rows 0..S-2 cached, the token attended as key S-1
+    kd, vd = k.to(DEV).clone(), v.to(DEV).clone()
+    out = ops.decode_attention_append(q.to(DEV), kd, vd, k[:, :, S - 1].to(DEV), v[:, :, S - 1].to(DEV), sc,
+                                      num_splits=splits)
+    assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype]
+    torch.cuda.synchronize()
+    for key, ws in ops._ws_cache.items():
+        if key[0] == "decode":
+            assert int(ws[:ops.DECODE_COUNTER_BYTES].count_nonzero()) == 0
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 def test_decode_mask_and_held_slot(dtype):
     B, Hq, Hk, R, n, D = 2, 32, 8, 64, 300, 128

@@ -87,7 +87,7 @@ def _run_pair(t, num_splits):
         a = _args(c, out)
         if which == "workspace":
             nbytes = lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, t["S"], num_splits, 0)
-            ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device="cuda")
+            ws = torch.zeros(max(nbytes, 256), dtype=torch.uint8, device="cuda")  # counter block zero
             rc = lib.hc_decode_attn_append(*a, ws.data_ptr(), ws.numel(), num_splits, stream)
             N.check(rc, "hc_decode_attn_append")
         else:
