@@ -212,6 +212,65 @@ class Setup:
         torch.cuda.synchronize()
 
 
+def dropin_compaction(s, flush, reps=5):
+    """The 32-layer compaction through the drop-in's PressLayerState objects
+    (compact_prompt, the compression half of prefill), on the workload's
+    per-layer prompt tensors:
+      deferred   every layer joins one DeferredCompaction, which runs them
+                 together after the last layer (PressCache's default): one
+                 scoring launch set over per-layer row tables, one top-k, one
+                 gather into every layer's hot buffer;
+      per_layer  each layer compacted as its prefill returns.
+    Two figures per path, medians over reps:
+      gpu   events around the sequence on the launch stream, with the host
+            enqueueing it while the GPU is still busy with cache sweeps (as
+            the last layer's own work keeps it busy in a model's prefill):
+            the GPU time of the compaction alone;
+      wall  host time from an idle GPU until the stream is done (Python,
+            launches and buffer allocation included)."""
+    import torch
+    from hotcold_kv.baselines.layer_state import DeferredCompaction, PressLayerState
+
+    w, B = s.w, s.w.batch
+    layers = [(s.q_post[l * B:(l + 1) * B], s.k_post[l * B:(l + 1) * B], s.v[l * B:(l + 1) * B])
+              for l in range(w.layers)]
+
+    states = [PressLayerState("snapkv", w.budget, w.window, w.pool, "maxpool") for _ in layers]
+
+    def run(deferred):
+        dc = DeferredCompaction() if deferred else None
+        for st, (q, k, v) in zip(states, layers):
+            st.compact_prompt(q, k, v, w.scaling, dc)
+        if dc is not None:
+            dc.flush()
+        return states
+
+    out = {}
+    with torch.cuda.stream(s.stream):
+        for name, deferred in (("deferred", True), ("per_layer", False)):
+            run(deferred)
+            gpu, wall = [], []
+            for _ in range(reps):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                s.stream.synchronize()
+                for _ in range(40):     # ~6 ms of GPU work queued ahead of the timed sequence
+                    flush()
+                e0.record(s.stream)
+                states = run(deferred)
+                e1.record(s.stream)
+                s.stream.synchronize()
+                gpu.append(e0.elapsed_time(e1))
+                flush()
+                s.stream.synchronize()
+                t0 = time.perf_counter()
+                states = run(deferred)
+                s.stream.synchronize()
+                wall.append((time.perf_counter() - t0) * 1e3)
+            out[name] = (statistics.median(gpu), statistics.median(wall))
+            out[name + "_rows"] = states[0].get_seq_length()
+    return out
+
+
 def run_steps(s, steps, flush):
     """Run `steps` whole jobs; return (wall ms/step, compaction ms list,
     decode ms (differential), decode ms (event-bracketed)).
@@ -650,6 +709,10 @@ def main():
         f"{pl_cold_ms * 1e3 / w.layers:.2f} us/layer, warm {pl_warm_ms * 1e3 / w.layers:.2f} us/layer")
     cpl_ms = time_graph(s.g_cpl, s.stream, 10, flush)
     log(f"compaction as one launch set per layer: {cpl_ms:.3f} ms for {w.layers} layers")
+    dro = dropin_compaction(s, flush)
+    log(f"drop-in compaction (PressLayerState.compact_prompt, {w.layers} layers): deferred "
+        f"{dro['deferred'][0]:.3f} ms GPU / {dro['deferred'][1]:.3f} ms wall, one layer at a time "
+        f"{dro['per_layer'][0]:.3f} ms GPU / {dro['per_layer'][1]:.3f} ms wall")
     del flush
 
     others = []
@@ -697,6 +760,12 @@ def main():
                                "Infinity Cache flushed before decode"},
         "compact_ms_32_layers": round(comp_ms, 4),
         "compact_ms_32_layers_per_layer_launches": round(cpl_ms, 4),
+        "compact_ms_32_layers_dropin": {
+            "deferred_gpu_ms": round(dro["deferred"][0], 4), "deferred_wall_ms": round(dro["deferred"][1], 4),
+            "per_layer_gpu_ms": round(dro["per_layer"][0], 4), "per_layer_wall_ms": round(dro["per_layer"][1], 4),
+            "hot_rows_per_layer": dro["deferred_rows"],
+            "path": "PressLayerState.compact_prompt on every layer; deferred = one DeferredCompaction "
+                    "(PressCache default), per_layer = compacted as each prefill returns"},
         "decode_us_per_layer_step": round(dec_us_layer, 4),
         "decode_launch_us_differential": round(dec_ms * 1e3, 3),
         "decode_launch_us_event_bracketed": round(dec_br_ms * 1e3, 3),

@@ -218,6 +218,11 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
 struct RowCopy {
   const char* src[3];
   char* dst[3];
+  // Optional per-row tables (row b of tensor t starts at src_tab[t][b] /
+  // dst_tab[t][b]; the b strides are then unused): rows that live in
+  // separate allocations, e.g. the layers of a model.
+  const char* const* src_tab[3];
+  char* const* dst_tab[3];
   int64_t s_sb[3], s_sh[3], s_ss[3];
   int64_t d_sb[3], d_sh[3], d_ss[3];
   int ntensor;
@@ -255,9 +260,11 @@ __global__ __launch_bounds__(256) void row_copy_kernel(RowCopy c) {
   const int eb = c.elem_bytes;
 #pragma unroll
   for (int t = 0; t < 3; ++t) {
-    if (t < c.ntensor && c.src[t]) {
-      const char* sp = c.src[t] + (b * c.s_sb[t] + h * c.s_sh[t] + si * c.s_ss[t]) * eb + (int64_t)v * VW;
-      char* dp = c.dst[t] + (b * c.d_sb[t] + h * c.d_sh[t] + di * c.d_ss[t]) * eb + (int64_t)v * VW;
+    if (t < c.ntensor && (c.src[t] || c.src_tab[t])) {
+      const char* sb = c.src_tab[t] ? c.src_tab[t][b] : c.src[t] + b * c.s_sb[t] * eb;
+      char* db = c.dst_tab[t] ? c.dst_tab[t][b] : c.dst[t] + b * c.d_sb[t] * eb;
+      const char* sp = sb + (h * c.s_sh[t] + si * c.s_ss[t]) * eb + (int64_t)v * VW;
+      char* dp = db + (h * c.d_sh[t] + di * c.d_ss[t]) * eb + (int64_t)v * VW;
       if constexpr (VW == 16) {
         st16(dp, ld16(sp));
       } else if constexpr (VW == 8) {
@@ -277,8 +284,9 @@ static int pick_vw(const RowCopy& c) {
     if (c.row_bytes % vw) continue;
     bool ok = true;
     for (int t = 0; t < c.ntensor; ++t) {
-      if (!c.src[t]) continue;
+      if (!c.src[t] && !c.src_tab[t]) continue;
       const int64_t eb = c.elem_bytes;
+      // table rows: the caller guarantees 16-byte aligned row starts
       if (((uintptr_t)c.src[t] % vw) || ((uintptr_t)c.dst[t] % vw)) ok = false;
       if ((c.s_sb[t] * eb) % vw || (c.s_sh[t] * eb) % vw || (c.s_ss[t] * eb) % vw) ok = false;
       if ((c.d_sb[t] * eb) % vw || (c.d_sh[t] * eb) % vw || (c.d_ss[t] * eb) % vw) ok = false;
@@ -417,6 +425,36 @@ extern "C" int hc_gather_rows(int64_t B, int64_t H, int64_t n, int64_t D, int64_
   c.row_bytes = (int)(D * elem_bytes);
   c.elem_bytes = (int)elem_bytes;
   return launch_row_copy(c, reinterpret_cast<hipStream_t>(stream), "gather_rows");
+}
+
+extern "C" int hc_gather_rows_tab(int64_t R, int64_t H, int64_t n, int64_t D, int64_t elem_bytes,
+                                  const int64_t* idx, int64_t i_sb, int64_t i_sh, int64_t src_rows, int64_t dst_row0,
+                                  const void* const* src1_rows, int64_t s1_sh, int64_t s1_ss,
+                                  void* const* dst1_rows, int64_t d1_sh, int64_t d1_ss,
+                                  const void* const* src2_rows, int64_t s2_sh, int64_t s2_ss,
+                                  void* const* dst2_rows, int64_t d2_sh, int64_t d2_ss, void* stream) {
+  HC_REQUIRE(R > 0 && H > 0 && n >= 0 && D > 0, "gather_tab: bad shape");
+  HC_REQUIRE(R <= 65535, "gather_tab: too many rows");
+  HC_REQUIRE(elem_bytes == 1 || elem_bytes == 2 || elem_bytes == 4 || elem_bytes == 8, "gather_tab: bad elem_bytes");
+  HC_REQUIRE(idx != nullptr, "gather_tab: null index");
+  HC_REQUIRE(src1_rows && dst1_rows, "gather_tab: first tensor tables required");
+  HC_REQUIRE((src2_rows == nullptr) == (dst2_rows == nullptr), "gather_tab: src/dst tables must both be set");
+  HC_REQUIRE(D * elem_bytes % 2 == 0, "gather_tab: odd row size");
+  if (n == 0) return HC_OK;
+  RowCopy c{};
+  c.src_tab[0] = reinterpret_cast<const char* const*>(src1_rows);
+  c.dst_tab[0] = reinterpret_cast<char* const*>(dst1_rows);
+  c.src_tab[1] = reinterpret_cast<const char* const*>(src2_rows);
+  c.dst_tab[1] = reinterpret_cast<char* const*>(dst2_rows);
+  c.s_sh[0] = s1_sh; c.s_ss[0] = s1_ss; c.d_sh[0] = d1_sh; c.d_ss[0] = d1_ss;
+  c.s_sh[1] = s2_sh; c.s_ss[1] = s2_ss; c.d_sh[1] = d2_sh; c.d_ss[1] = d2_ss;
+  c.ntensor = 2;
+  c.idx = idx; c.i_sb = i_sb; c.i_sh = i_sh;
+  c.src_rows = src_rows; c.src_row0 = 0; c.dst_row0 = dst_row0;
+  c.B = (int)R; c.H = (int)H; c.n = (int)n;
+  c.row_bytes = (int)(D * elem_bytes);
+  c.elem_bytes = (int)elem_bytes;
+  return launch_row_copy(c, reinterpret_cast<hipStream_t>(stream), "gather_rows_tab");
 }
 
 extern "C" int hc_append_rows(int dtype, int64_t B, int64_t H, int64_t T, int64_t D, int64_t row, const void* k_src,

@@ -59,10 +59,11 @@ static ScoreLayout score_layout(int64_t B, int64_t Hk, int64_t S, int64_t D, int
 // qf[b][h][w][d] for w < wpad (zero rows past W).  grid (wpad, Hk, B), block D.
 // Also resets the row-max keys (to the key of -inf) that the logits kernel
 // accumulates into, and writes the padding rows of the row statistics.
+// q_rows (may be NULL): row b's queries start at q_rows[b] instead of q + b*q_sb.
 template <typename T>
-__global__ void qmean_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_row0,
-                             int Hq, int Hk, int W, int wpad, int D, double* __restrict__ qf,
-                             uint32_t* __restrict__ rmax, RowStat* __restrict__ rstat) {
+__global__ void qmean_kernel(const T* __restrict__ q, const T* const* __restrict__ q_rows, int64_t q_sb,
+                             int64_t q_sh, int64_t q_ss, int64_t q_row0, int Hq, int Hk, int W, int wpad, int D,
+                             double* __restrict__ qf, uint32_t* __restrict__ rmax, RowStat* __restrict__ rstat) {
   const int w = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
   const int d = threadIdx.x;
   const int wst = (int)cdiv(W, kStatPad) * kStatPad;  // wst <= wpad
@@ -82,7 +83,7 @@ __global__ void qmean_kernel(const T* __restrict__ q, int64_t q_sb, int64_t q_sh
     G = Hq;
     g0 = 0;
   }
-  const T* src = q + b * q_sb + (q_row0 + w) * q_ss + d;
+  const T* src = (q_rows ? q_rows[b] : q + b * q_sb) + (q_row0 + w) * q_ss + d;
   double sum = to_f64(src[(int64_t)g0 * q_sh]);
   for (int g = 1; g < G; ++g) sum = sum + to_f64(src[(int64_t)(g0 + g) * q_sh]);
   *dst = sum / (double)G;
@@ -171,9 +172,9 @@ constexpr int kKRing = 4;
 
 template <typename T, int MODE, int DC>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void logits_kernel(
-    const T* __restrict__ k, int64_t k_sb, int64_t k_sh, int64_t k_ss, uint32_t k_bytes,
-    const double* __restrict__ qf, int Hk, int S, int Drt, int W, int wpad, double scaling, int cpw,
-    float* __restrict__ logits, uint32_t* __restrict__ rmax) {
+    const T* __restrict__ k, const T* const* __restrict__ k_rows, int64_t k_sb, int64_t k_sh, int64_t k_ss,
+    uint32_t k_bytes, const double* __restrict__ qf, int Hk, int S, int Drt, int W, int wpad, double scaling,
+    int cpw, float* __restrict__ logits, uint32_t* __restrict__ rmax) {
   const int D = DC > 0 ? DC : Drt;
   extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
   __shared__ float red[4][kRowBlk];
@@ -198,7 +199,9 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const int nw = min(kRowBlk, W - w0);
   const int64_t bh = (int64_t)b * Hk + h;
   const int ld = D + 1;
-  const __amdgpu_buffer_rsrc_t krs = make_rsrc(k + b * k_sb + h * k_sh, k_bytes);
+  // k_rows (may be NULL): row b's keys start at k_rows[b] instead of k + b*k_sb
+  const T* krow = k_rows ? k_rows[b] : k + b * k_sb;
+  const __amdgpu_buffer_rsrc_t krs = make_rsrc(krow + h * k_sh, k_bytes);
   const uint32_t rowb = (uint32_t)(k_ss * (int64_t)sizeof(T));
   constexpr int DS = KOperand<T>::DSTEP;
   const int qpos0 = S - W + w0;
@@ -632,16 +635,18 @@ __global__ void head_mean_kernel(const float* __restrict__ x, int H, int S, floa
 
 template <typename T>
 static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, int64_t Hq, int64_t Hk, int64_t S,
-                         int64_t D, int64_t W, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss,
-                         int64_t q_row0, const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss, double scal,
-                         int P, int pooling, int ksize, float* scores, hipStream_t st) {
+                         int64_t D, int64_t W, const void* q, const void* const* q_rows, int64_t q_sb, int64_t q_sh,
+                         int64_t q_ss, int64_t q_row0, const void* k, const void* const* k_rows, int64_t k_sb,
+                         int64_t k_sh, int64_t k_ss, double scal, int P, int pooling, int ksize, float* scores,
+                         hipStream_t st) {
   double* qf = reinterpret_cast<double*>(ws + lay.qf_off);
   float* logits = reinterpret_cast<float*>(ws + lay.logits_off);
   uint32_t* rmax = reinterpret_cast<uint32_t*>(ws + lay.rmax_off);
   RowStat* rstat = reinterpret_cast<RowStat*>(ws + lay.rstat_off);
   const int nrb = (int)(lay.wpad / kRowBlk);
   hipLaunchKernelGGL(qmean_kernel<T>, dim3((unsigned)lay.wpad, (unsigned)Hk, (unsigned)B),
-                     dim3((unsigned)(D < 64 ? 64 : D)), 0, st, (const T*)q, q_sb, q_sh, q_ss, q_row0, (int)Hq,
+                     dim3((unsigned)(D < 64 ? 64 : D)), 0, st, (const T*)q, (const T* const*)q_rows, q_sb, q_sh,
+                     q_ss, q_row0, (int)Hq,
                      (int)Hk, (int)W, (int)lay.wpad, (int)D, qf, rmax, rstat);
   const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
   const uint32_t k_bytes = (uint32_t)(((S - 1) * k_ss + D) * (int64_t)sizeof(T));
@@ -651,7 +656,8 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
   auto launch = [&](auto kern) {
     if (lds > 48 * 1024)
       (void)hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const T*)k, k_sb, k_sh, k_ss, k_bytes, (const double*)qf,
+    hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, (const T*)k, (const T* const*)k_rows, k_sb, k_sh, k_ss,
+                       k_bytes, (const double*)qf,
                        (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, cpw, logits, rmax);
   };
   if (mode == HC_SCORE_SNAPKV) {
@@ -703,11 +709,11 @@ extern "C" int64_t hc_snapkv_score_workspace_size(int64_t B, int64_t Hk, int64_t
   return score_layout(B, Hk, S, D, W).total;
 }
 
-extern "C" int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64_t Hk, int64_t S, int64_t D,
-                               int64_t W, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_row0,
-                               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss, double scaling,
-                               int64_t kernel_size, int pooling, float* scores, void* workspace,
-                               int64_t workspace_bytes, void* stream) {
+static int score_impl(int dtype, int mode, int64_t B, int64_t Hq, int64_t Hk, int64_t S, int64_t D, int64_t W,
+                      const void* q, const void* const* q_rows, int64_t q_sb, int64_t q_sh, int64_t q_ss,
+                      int64_t q_row0, const void* k, const void* const* k_rows, int64_t k_sb, int64_t k_sh,
+                      int64_t k_ss, double scaling, int64_t kernel_size, int pooling, float* scores, void* workspace,
+                      int64_t workspace_bytes, void* stream) {
   HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16, "score: bad dtype %d", dtype);
   HC_REQUIRE(mode == HC_SCORE_SNAPKV || mode == HC_SCORE_RAWSUM, "score: bad mode %d", mode);
   HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && S > 0 && D > 0 && W > 0, "score: empty shape");
@@ -718,7 +724,7 @@ extern "C" int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64
   HC_REQUIRE(S <= ((int64_t)1 << 19), "score: S %lld above 2^19 (fixed-point normaliser range)", (long long)S);
   HC_REQUIRE(B <= 65535 && Hk * cdiv(W, kRowBlk) <= 65535, "score: grid too large");
   HC_REQUIRE(q_row0 >= 0, "score: negative q_row0");
-  HC_REQUIRE(q && k && scores, "score: null pointer");
+  HC_REQUIRE((q || q_rows) && (k || k_rows) && scores, "score: null pointer");
   const int es = dtype_size(dtype);
   HC_REQUIRE(k_ss >= D && ((S - 1) * k_ss + D) * es < ((int64_t)1 << 31),
              "score: one (batch, kv head) key extent must be below 2 GiB with row stride >= D");
@@ -742,15 +748,35 @@ extern "C" int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   char* ws = reinterpret_cast<char*>(workspace);
   if (dtype == HC_DTYPE_F16)
-    launch_score<half_t>(lay, ws, mode, B, Hq, Hk, S, D, W, q, q_sb, q_sh, q_ss, q_row0, k, k_sb, k_sh, k_ss, scal,
-                         P, pooling, (int)kernel_size, scores, st);
+    launch_score<half_t>(lay, ws, mode, B, Hq, Hk, S, D, W, q, q_rows, q_sb, q_sh, q_ss, q_row0, k, k_rows, k_sb,
+                         k_sh, k_ss, scal, P, pooling, (int)kernel_size, scores, st);
   else if (dtype == HC_DTYPE_BF16)
-    launch_score<bf16_t>(lay, ws, mode, B, Hq, Hk, S, D, W, q, q_sb, q_sh, q_ss, q_row0, k, k_sb, k_sh, k_ss, scal,
-                         P, pooling, (int)kernel_size, scores, st);
+    launch_score<bf16_t>(lay, ws, mode, B, Hq, Hk, S, D, W, q, q_rows, q_sb, q_sh, q_ss, q_row0, k, k_rows, k_sb,
+                         k_sh, k_ss, scal, P, pooling, (int)kernel_size, scores, st);
   else
-    launch_score<float>(lay, ws, mode, B, Hq, Hk, S, D, W, q, q_sb, q_sh, q_ss, q_row0, k, k_sb, k_sh, k_ss, scal,
-                        P, pooling, (int)kernel_size, scores, st);
+    launch_score<float>(lay, ws, mode, B, Hq, Hk, S, D, W, q, q_rows, q_sb, q_sh, q_ss, q_row0, k, k_rows, k_sb,
+                        k_sh, k_ss, scal, P, pooling, (int)kernel_size, scores, st);
   return check_launch("snapkv_score");
+}
+
+extern "C" int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64_t Hk, int64_t S, int64_t D,
+                               int64_t W, const void* q, int64_t q_sb, int64_t q_sh, int64_t q_ss, int64_t q_row0,
+                               const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss, double scaling,
+                               int64_t kernel_size, int pooling, float* scores, void* workspace,
+                               int64_t workspace_bytes, void* stream) {
+  HC_REQUIRE(q && k, "score: null pointer");
+  return score_impl(dtype, mode, B, Hq, Hk, S, D, W, q, nullptr, q_sb, q_sh, q_ss, q_row0, k, nullptr, k_sb, k_sh,
+                    k_ss, scaling, kernel_size, pooling, scores, workspace, workspace_bytes, stream);
+}
+
+extern "C" int hc_snapkv_score_rows(int dtype, int mode, int64_t R, int64_t Hq, int64_t Hk, int64_t S, int64_t D,
+                                    int64_t W, const void* const* q_rows, int64_t q_sh, int64_t q_ss,
+                                    int64_t q_row0, const void* const* k_rows, int64_t k_sh, int64_t k_ss,
+                                    double scaling, int64_t kernel_size, int pooling, float* scores,
+                                    void* workspace, int64_t workspace_bytes, void* stream) {
+  HC_REQUIRE(q_rows && k_rows, "score_rows: null row table");
+  return score_impl(dtype, mode, R, Hq, Hk, S, D, W, nullptr, q_rows, 0, q_sh, q_ss, q_row0, nullptr, k_rows, 0,
+                    k_sh, k_ss, scaling, kernel_size, pooling, scores, workspace, workspace_bytes, stream);
 }
 
 extern "C" int hc_head_mean(int64_t B, int64_t H, int64_t S, const float* scores, float* out, void* stream) {

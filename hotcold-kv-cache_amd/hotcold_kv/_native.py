@@ -129,6 +129,13 @@ SIGNATURES = {
         _dbl, _i64, _int,
         _vp,
         _vp, _i64, _vp]),
+    "hc_snapkv_score_rows": (_int, [
+        _int, _int, _i64, _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64,
+        _dbl, _i64, _int,
+        _vp,
+        _vp, _i64, _vp]),
     "hc_head_mean": (_int, [_i64, _i64, _i64, _vp, _vp, _vp]),
     "hc_topk_keep": (_int, [_i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
     "hc_gather_rows": (_int, [
@@ -138,6 +145,12 @@ SIGNATURES = {
         _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
         _vp, _i64, _i64, _i64, _vp, _i64, _i64, _i64,
         _vp, _i64, _vp, _i64,
+        _vp]),
+    "hc_gather_rows_tab": (_int, [
+        _i64, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _vp, _i64, _i64,
+        _vp, _i64, _i64, _vp, _i64, _i64,
         _vp]),
     "hc_append_rows": (_int, [
         _int, _i64, _i64, _i64, _i64, _i64,

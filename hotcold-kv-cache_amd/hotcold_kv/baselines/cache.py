@@ -12,7 +12,7 @@ state.get_seq_length().
 from transformers.cache_utils import Cache, CacheLayerMixin
 
 from .config import PressConfig, pyramid_layer_budget
-from .layer_state import PressLayerState
+from .layer_state import DeferredCompaction, PressLayerState
 
 
 class PressCacheLayer(CacheLayerMixin):
@@ -21,10 +21,11 @@ class PressCacheLayer(CacheLayerMixin):
 
     is_compileable = False
 
-    def __init__(self, cfg: PressConfig, layer_idx: int):
+    def __init__(self, cfg: PressConfig, layer_idx: int, deferred: DeferredCompaction = None):
         super().__init__()
         self.cfg = cfg
         self.layer_idx = layer_idx
+        self.deferred = deferred
         if cfg.method == "pyramidkv":
             budget = pyramid_layer_budget(layer_idx, cfg.num_layers, cfg.max_capacity, cfg.pyramid_beta)
         else:
@@ -35,9 +36,11 @@ class PressCacheLayer(CacheLayerMixin):
         self.seen_tokens = 0
 
     def prefill(self, q_post, k_post, v, n_rep, scaling):
-        out = self.state.prefill(q_post, k_post, v, n_rep, scaling)
+        out = self.state.prefill(q_post, k_post, v, n_rep, scaling, deferred=self.deferred)
         self.seen_tokens = int(k_post.shape[2])
         self.is_initialized = True
+        if self.deferred is not None and self.layer_idx == self.cfg.num_layers - 1:
+            self.deferred.flush()   # the prompt has passed every layer
         return out
 
     def decode(self, q_post, k_post, v, n_rep, scaling):
@@ -67,6 +70,10 @@ class PressCacheLayer(CacheLayerMixin):
 
 
 def build_press_cache(model, cfg: PressConfig) -> Cache:
+    """One PressCacheLayer per decoder layer.  With cfg.defer_compaction the
+    layers' prompt compactions run together after the last layer's prefill
+    (DeferredCompaction), with the same kept indices."""
     n_layers = int(model.config.num_hidden_layers)
     cfg.num_layers = n_layers
-    return Cache(layers=[PressCacheLayer(cfg, layer_idx=i) for i in range(n_layers)])
+    deferred = DeferredCompaction(cfg.defer_max_bytes) if cfg.defer_compaction else None
+    return Cache(layers=[PressCacheLayer(cfg, layer_idx=i, deferred=deferred) for i in range(n_layers)])

@@ -15,6 +15,10 @@ class PressConfig:
     window_size: observation window; also the recent window that is kept.
     kernel_size, pooling: 1-D pooling of the importance ("maxpool"/"avgpool").
     pyramid_beta: spread of the PyramidKV budgets.
+    defer_compaction: compact every layer's prompt together after the last
+        layer's prefill, in one launch set, instead of one layer at a time
+        (same kept indices; prompt K/V stay alive until then, up to
+        defer_max_bytes).  Not a knob of the reference.
     """
 
     method: str = "snapkv"
@@ -24,6 +28,8 @@ class PressConfig:
     pooling: str = "maxpool"
     pyramid_beta: int = 20
     num_layers: int = 32
+    defer_compaction: bool = True
+    defer_max_bytes: int = 16 << 30
 
     def __post_init__(self):
         assert self.method in ("snapkv", "pyramidkv", "h2o"), f"unknown method {self.method}"

@@ -20,6 +20,70 @@ from ..hot_buffer import HotBuffer
 from .scoring import repeat_kv
 
 
+class DeferredCompaction:
+    """The prompt compactions of many layers, run together in one launch set.
+
+    A model's prefill visits its layers in turn, and each layer's SnapKV /
+    PyramidKV compaction (layer_state.py:82-94) depends only on that layer's
+    own prompt queries and keys; no prompt attention reads a compacted cache.
+    So a layer's compaction can wait until the prompt has passed every layer,
+    and all pending layers then compact together: one scoring launch set over
+    every layer's keys (per-layer row tables, no copies), one top-k launch and
+    one gather into every layer's hot buffer per budget.  The kept indices are
+    the ones each layer would get on its own, bit for bit.
+
+    Pending layers keep their whole prompt K/V alive until then; past
+    max_pending_bytes the pending layers are compacted early.
+    """
+
+    def __init__(self, max_pending_bytes=16 << 30):
+        self.max_pending_bytes = int(max_pending_bytes)
+        self.pending = []
+        self.pending_bytes = 0
+
+    def add(self, state, q_post, k_post, v, scaling):
+        """Hold one layer's prompt (the query tensor is kept as is: its window
+        rows are read in place) until flush."""
+        self.pending.append((state, q_post, k_post, v, float(scaling)))
+        self.pending_bytes += sum(t.numel() * t.element_size() for t in (q_post, k_post, v))
+        state._deferred = self
+        if self.pending_bytes > self.max_pending_bytes:
+            self.flush()
+
+    def flush(self):
+        """Compact every pending layer: per group of layers with one shape and
+        knob set, one hot storage for all of them, one copy of every row
+        table, and the scoring, top-k and gather launches."""
+        pending, self.pending, self.pending_bytes = self.pending, [], 0
+        groups = {}
+        for item in pending:
+            st, q, k, v, sc = item
+            key = (k.device, k.dtype, tuple(q.shape), q.stride()[1:], tuple(k.shape), k.stride()[1:],
+                   tuple(v.shape), v.stride()[1:], st.window_size, st.kernel_size, st.pooling, st.budget, sc)
+            groups.setdefault(key, []).append(item)
+        for items in groups.values():
+            st0, q0, k0, _, sc = items[0]
+            B, Hk, S, D = k0.shape
+            window, _, keep_prefix = ops.keep_counts(S, st0.window_size, st0.budget)
+            n = keep_prefix + window
+            cap = n + st0.decode_reserve
+            kst = torch.empty((len(items), B, Hk, cap, D), dtype=k0.dtype, device=k0.device)
+            vst = torch.empty_like(kst)
+            for i, it in enumerate(items):
+                it[0].buf = HotBuffer(B, Hk, D, k0.dtype, k0.device, cap, storage=(kst[i], vst[i]))
+            qs, ks, vs = [it[1] for it in items], [it[2] for it in items], [it[3] for it in items]
+            kd, vd = [it[0].buf.st["k"] for it in items], [it[0].buf.st["v"] for it in items]
+            q_t, k_t, v_t, kd_t, vd_t = ops.device_tables(*[ops.row_addresses(x) for x in (qs, ks, vs, kd, vd)],
+                                                          device=k0.device)
+            scores = ops.snapkv_scores_rows(qs, ks, st0.window_size, sc, st0.kernel_size, st0.pooling,
+                                            tables=(q_t, k_t))
+            keep = ops.keep_index(scores, st0.window_size, st0.budget)
+            ops.gather_rows_tab(keep, ks, vs, kd, vd, dst_row0=0, tables=(k_t, v_t, kd_t, vd_t))
+            for it in items:
+                it[0].buf.n = n
+                it[0]._deferred = None
+
+
 class PressLayerState:
     def __init__(self, method: str, budget: int, window_size: int, kernel_size: int, pooling: str,
                  decode_reserve: int = 256):
@@ -34,14 +98,22 @@ class PressLayerState:
         self.buf = None
         self._h2o = None        # H2O scores [B][Hk][buffer capacity] fp32, aligned with the hot rows
         self._h2o_spare = None
+        self._deferred = None   # the DeferredCompaction holding this layer's prompt, until it runs
+
+    def _settle(self):
+        """Run this layer's deferred compaction (with every other pending layer)."""
+        if self._deferred is not None:
+            self._deferred.flush()
 
     # -- introspection -------------------------------------------------------
     @property
     def keys(self):
+        self._settle()
         return None if self.buf is None else self.buf.keys
 
     @property
     def values(self):
+        self._settle()
         return None if self.buf is None else self.buf.values
 
     @property
@@ -53,6 +125,7 @@ class PressLayerState:
         return self._h2o[:, :, : self.buf.n]
 
     def get_seq_length(self) -> int:
+        self._settle()
         return 0 if self.buf is None else self.buf.n
 
     # -- attention -------------------------------------------------------------
@@ -86,11 +159,24 @@ class PressLayerState:
         self._h2o, self._h2o_spare = self._h2o_spare, self._h2o
 
     # -- forward paths -----------------------------------------------------------
-    def prefill(self, q_post, k_post, v, n_rep, scaling):
-        """Attend over the full prompt, then compress the prompt KV to the budget."""
+    def prefill(self, q_post, k_post, v, n_rep, scaling, deferred=None):
+        """Attend over the full prompt, then compress the prompt KV to the budget
+        -- or, with a DeferredCompaction, leave the compression to it."""
         out = self._attn(q_post, k_post, v, n_rep, scaling, causal=True)
+        self.compact_prompt(q_post, k_post, v, scaling, deferred)
+        return out
+
+    def compact_prompt(self, q_post, k_post, v, scaling, deferred=None):
+        """The compression half of prefill (layer_state.py:82-94 after the
+        attention): score the prompt, keep the budget, gather it into the hot
+        buffer.  With a DeferredCompaction (SnapKV / PyramidKV over budget)
+        the layer joins it and is compacted when it runs."""
         S = int(k_post.shape[2])
         h2o = self.method == "h2o"
+        if deferred is not None and not h2o and S > self.budget:
+            self.buf = None
+            deferred.add(self, q_post, k_post, v, scaling)
+            return
         scores = ops.h2o_prefill_scores(q_post, k_post, scaling) if h2o else None
         if S <= self.budget:
             self._new_buffer(k_post, S)
@@ -98,7 +184,7 @@ class PressLayerState:
             if h2o:
                 self._h2o_storage()
                 self._h2o[:, :, :S].copy_(scores)
-            return out
+            return
         if not h2o:
             scores = ops.snapkv_scores(q_post, k_post, self.window_size, scaling, self.kernel_size, self.pooling)
         keep = ops.keep_index(scores, self.window_size, self.budget)
@@ -106,11 +192,11 @@ class PressLayerState:
         self.buf.gather_from(k_post, v, keep)
         if h2o:
             self._h2o_keep(scores, keep)
-        return out
 
     def decode(self, q_post, k_post, v, n_rep, scaling):
         """Single-token decode: append, then attend over the compressed cache
         (one fused launch for one token)."""
+        self._settle()
         if self.buf is None:
             raise RuntimeError("decode before prefill")
         if self.method == "h2o":

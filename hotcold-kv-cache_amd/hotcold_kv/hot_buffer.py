@@ -16,24 +16,43 @@ from . import ops
 
 
 class HotBuffer:
-    def __init__(self, batch, heads, head_dim, dtype, device, capacity, held=0, with_pre=False, with_pos=False):
+    def __init__(self, batch, heads, head_dim, dtype, device, capacity, held=0, with_pre=False, with_pos=False,
+                 storage=None):
+        """storage: optional (k, v) tensors (B,H,held+capacity,D) to use as the
+        buffer's rows instead of allocating them (e.g. views of one allocation
+        shared by many layers)."""
         self.B, self.H, self.D = int(batch), int(heads), int(head_dim)
         self.dtype, self.device = dtype, torch.device(device)
         self.held = int(held)
         self.with_pre, self.with_pos = with_pre, with_pos
         self.n = 0
-        self._alloc(max(1, int(capacity)))
+        if storage is not None:
+            if with_pre or with_pos or held:
+                raise ValueError("HotBuffer: external storage holds K and V rows only")
+            k, v = storage
+            self.cap = int(k.shape[2])
+            self.st = {"k": k, "v": v}
+        else:
+            self._alloc(max(1, int(capacity)))
         self._spare = None
 
     # -- storage --------------------------------------------------------------
     def _new_storage(self, cap):
+        # Hot rows are written before any read (decode reads rows below
+        # held + n only), so only the held slot -- attended masked until an
+        # inject fills it, and a masked row still enters the P.V product with
+        # weight 0 -- is zero-filled.
         shape = (self.B, self.H, self.held + cap, self.D)
         st = {
-            "k": torch.zeros(shape, dtype=self.dtype, device=self.device),
-            "v": torch.zeros(shape, dtype=self.dtype, device=self.device),
+            "k": torch.empty(shape, dtype=self.dtype, device=self.device),
+            "v": torch.empty(shape, dtype=self.dtype, device=self.device),
         }
         if self.with_pre:
-            st["p"] = torch.zeros(shape, dtype=self.dtype, device=self.device)
+            st["p"] = torch.empty(shape, dtype=self.dtype, device=self.device)
+        if self.held:
+            for name in ("k", "v", "p"):
+                if name in st:
+                    st[name][:, :, :self.held].zero_()
         if self.with_pos:
             st["pos"] = torch.zeros((self.B, self.held + cap), dtype=torch.int64, device=self.device)
         return st

@@ -440,6 +440,114 @@ def snapkv_scores(q_post, keys, window_size, scaling, kernel_size=7, pooling="ma
     return scores
 
 
+def row_addresses(tensors):
+    """Base address of every batch row of every tensor, in order (tensor 0
+    rows 0..B-1, tensor 1 rows 0..B-1, ...)."""
+    ptrs = []
+    for t in tensors:
+        base, step = t.data_ptr(), t.stride(0) * t.element_size()
+        ptrs.extend(base + b * step for b in range(t.shape[0]))
+    return ptrs
+
+
+def device_tables(*lists, device=None):
+    """One device int64 array per list of addresses, all sent with a single
+    copy from pinned host memory (to `device`, default the current one)."""
+    flat = [p for x in lists for p in x]
+    dev = device if device is not None else torch.cuda.current_device()
+    tab = torch.tensor(flat, dtype=torch.int64, pin_memory=True).to(dev, non_blocking=True)
+    out, o = [], 0
+    for x in lists:
+        out.append(tab[o:o + len(x)])
+        o += len(x)
+    return out
+
+
+
+
+def _same_layout(tensors, what):
+    t0 = tensors[0]
+    for t in tensors[1:]:
+        if t.shape != t0.shape or t.stride()[1:] != t0.stride()[1:] or t.dtype != t0.dtype or t.device != t0.device:
+            raise RuntimeError(f"{what}: every tensor must share shape, dtype, device and head/row strides")
+
+
+def snapkv_scores_rows(q_list, k_list, window_size, scaling, kernel_size=7, pooling="maxpool", tables=None):
+    """snapkv_scores for several (queries, keys) pairs at once -- the layers of
+    a model, each in its own allocation -- in one launch set.
+
+    q_list[i] (B,Hq,T,D) holds at least the window (its last min(window, S)
+    rows are the window queries, at prompt positions S-W..S-1); k_list[i]
+    (B,Hk,S,D).  Returns (len * B, Hk, S) float32: the rows of pair i are
+    i*B .. i*B+B-1, each bit-equal to snapkv_scores on that pair.  tables:
+    optional device (q, k) row-address tables already built for the lists.
+    """
+    if not q_list or len(q_list) != len(k_list):
+        raise ValueError("snapkv_scores_rows: one query tensor per key tensor, at least one")
+    _require_device(*q_list, *k_list)
+    _same_layout(q_list, "snapkv_scores_rows (queries)")
+    _same_layout(k_list, "snapkv_scores_rows (keys)")
+    q0, k0 = q_list[0], k_list[0]
+    if q0.dim() != 4 or k0.dim() != 4 or q0.stride(-1) != 1 or k0.stride(-1) != 1:
+        raise RuntimeError("snapkv_scores_rows: 4D tensors with contiguous rows required")
+    if k0.dtype != q0.dtype:
+        raise RuntimeError("snapkv_scores_rows: q and keys must share a dtype")
+    B, Hq, T, D = q0.shape
+    _, Hk, S, _ = k0.shape
+    W = min(int(window_size), S)
+    if T < W:
+        raise RuntimeError(f"snapkv_scores_rows: {T} query rows hold less than the window {W}")
+    R = len(k_list) * B
+    pool = N.HC_POOL_AVG if pooling == "avgpool" else N.HC_POOL_MAX
+    qt, kt = tables if tables is not None else device_tables(row_addresses(q_list), row_addresses(k_list),
+                                                             device=k0.device)
+    scores = torch.empty((R, Hk, S), dtype=torch.float32, device=k0.device)
+    lib = N.lib()
+    ws = _workspace("score", k0.device, lib.hc_snapkv_score_workspace_size(R, Hk, S, D, W))
+    rc = lib.hc_snapkv_score_rows(
+        N.dtype_code(k0.dtype), N.HC_SCORE_SNAPKV, R, Hq, Hk, S, D, W,
+        _ptr(qt), q0.stride(1), q0.stride(2), T - W,
+        _ptr(kt), k0.stride(1), k0.stride(2),
+        float(scaling), int(kernel_size or 1), pool,
+        _ptr(scores), _ptr(ws), ws.numel(), _stream_handle(k0.device))
+    N.check(rc, "hc_snapkv_score_rows")
+    return scores
+
+
+def gather_rows_tab(idx, k_src, v_src, k_dst, v_dst, dst_row0=0, tables=None):
+    """gather_rows of K and V for several tensors at once (the layers of a
+    model): k_dst[i][b,h,dst_row0+j] = k_src[i][b,h,idx[i*B+b,h,j]], same for
+    V, in one launch.  idx is (len * B, H, n) int64.  tables: optional device
+    row-address tables of (k_src, v_src, k_dst, v_dst) already built."""
+    lists = (k_src, v_src, k_dst, v_dst)
+    if not k_src or any(len(x) != len(k_src) for x in lists):
+        raise ValueError("gather_rows_tab: four lists of equal, non-zero length")
+    for x in lists:
+        _same_layout(x, "gather_rows_tab")
+    _require_device(idx, *k_src, *v_src, *k_dst, *v_dst)
+    s0, d0 = k_src[0], k_dst[0]
+    B, H, S, D = s0.shape
+    R = len(k_src) * B
+    if idx.dim() != 3 or idx.shape[0] != R or idx.shape[1] != H or idx.stride(-1) != 1:
+        raise RuntimeError(f"gather_rows_tab: index {tuple(idx.shape)} must be ({R},{H},n) with unit last stride")
+    n = idx.shape[2]
+    for s, d in ((k_src[0], k_dst[0]), (v_src[0], v_dst[0])):
+        if s.dtype != s0.dtype or d.dtype != s0.dtype or s.shape[:2] != (B, H) or d.shape[:2] != (B, H) \
+                or s.shape[3] != D or d.shape[3] != D or s.stride(-1) != 1 or d.stride(-1) != 1:
+            raise RuntimeError("gather_rows_tab: K/V sources and destinations do not match")
+        if d.shape[2] < dst_row0 + n:
+            raise RuntimeError(f"gather_rows_tab: destination holds {d.shape[2]} rows, needs {dst_row0 + n}")
+    dev = s0.device
+    tabs = tables if tables is not None else device_tables(*[row_addresses(x) for x in lists], device=dev)
+    vs, vd = v_src[0], v_dst[0]
+    rc = N.lib().hc_gather_rows_tab(
+        R, H, n, D, s0.element_size(), _ptr(idx), idx.stride(0), idx.stride(1), S, int(dst_row0),
+        _ptr(tabs[0]), s0.stride(1), s0.stride(2), _ptr(tabs[2]), d0.stride(1), d0.stride(2),
+        _ptr(tabs[1]), vs.stride(1), vs.stride(2), _ptr(tabs[3]), vd.stride(1), vd.stride(2),
+        _stream_handle(dev))
+    N.check(rc, "hc_gather_rows_tab")
+
+
 def h2o_prefill_scores(q_post, keys, scaling, max_workspace_bytes=10 << 30):
     """H2O accumulated attention of the whole prompt per KV head, fp32
     (B,Hk,S) (scoring.py:82-107): for every key, the causal softmax

@@ -235,6 +235,24 @@ int hc_snapkv_score(int dtype, int mode, int64_t B, int64_t Hq, int64_t Hk, int6
                     float* scores,
                     void* workspace, int64_t workspace_bytes, void* stream);
 
+/*
+ * hc_snapkv_score over R rows whose queries and keys live in separate
+ * allocations -- the layers of a model, compacted together once the prompt
+ * has passed every layer (layer_state.py:82-94 runs once per layer; the kept
+ * indices do not depend on when it runs).  Row r's queries start at
+ * q_rows[r] and its keys at k_rows[r] (device arrays of R pointers, each
+ * 16-byte aligned); the head and row strides are shared by all rows.  The
+ * scores [R][Hk][S] and the workspace (hc_snapkv_score_workspace_size(R, ..))
+ * are as in hc_snapkv_score with B = R, and so are the bits of every score.
+ */
+int hc_snapkv_score_rows(int dtype, int mode, int64_t R, int64_t Hq, int64_t Hk, int64_t S,
+                         int64_t D, int64_t W,
+                         const void* const* q_rows, int64_t q_sh, int64_t q_ss, int64_t q_row0,
+                         const void* const* k_rows, int64_t k_sh, int64_t k_ss,
+                         double scaling, int64_t kernel_size, int pooling,
+                         float* scores,
+                         void* workspace, int64_t workspace_bytes, void* stream);
+
 /* Mean over KV heads of fp32 scores [B][H][S] -> [B][S] (cache.py:69 ".mean(dim=1)"). */
 int hc_head_mean(int64_t B, int64_t H, int64_t S, const float* scores, float* out, void* stream);
 
@@ -273,6 +291,23 @@ int hc_gather_rows(int64_t B, int64_t H, int64_t n, int64_t D, int64_t elem_byte
                    void* dst3, int64_t d3_sb, int64_t d3_sh, int64_t d3_ss,
                    const int64_t* pos_src, int64_t ps_sb, int64_t* pos_dst, int64_t pd_sb,
                    void* stream);
+
+/*
+ * hc_gather_rows of two tensors (K and V) over R rows that live in separate
+ * allocations: row r of tensor t is read from src<t>_rows[r] and written to
+ * dst<t>_rows[r] (device arrays of R pointers, each 16-byte aligned), with
+ * the head and row strides shared by all rows.  It gathers the kept rows of
+ * every layer of a model into each layer's own hot buffer in one launch
+ * (gather_kv, scoring.py:135-139, run for all layers at once).
+ */
+int hc_gather_rows_tab(int64_t R, int64_t H, int64_t n, int64_t D, int64_t elem_bytes,
+                       const int64_t* idx, int64_t i_sb, int64_t i_sh, int64_t src_rows,
+                       int64_t dst_row0,
+                       const void* const* src1_rows, int64_t s1_sh, int64_t s1_ss,
+                       void* const* dst1_rows, int64_t d1_sh, int64_t d1_ss,
+                       const void* const* src2_rows, int64_t s2_sh, int64_t s2_ss,
+                       void* const* dst2_rows, int64_t d2_sh, int64_t d2_ss,
+                       void* stream);
 
 /*
  * Eviction gather with fp32 upcast (replaces the per-batch gather, .float()

@@ -338,6 +338,32 @@ def test_press_patch_matches_stock_without_compression(model_and_ref, method):
     assert d < TOL[dtype] and agree >= len(fed) - 1, (d, agree)
 
 
+@pytest.mark.parametrize("method", ["snapkv", "pyramidkv"])
+def test_press_patch_deferred_compaction_equals_per_layer(model_and_ref, method):
+    """All layers compacted together after the last prefill (the default)
+    store exactly the rows of one compaction per layer, and decode gives the
+    same logits bit for bit."""
+    model, ids, (_, _, fed), dtype = model_and_ref
+    runs = []
+    for defer in (True, False):
+        install_press_patch()
+        try:
+            cache = build_press_cache(model, PressConfig(method=method, max_capacity=64, window_size=16,
+                                                         defer_compaction=defer))
+            set_active_press_cache(cache)
+            with torch.inference_mode():
+                prefill, logits, _ = decode_trace(model, ids, cache, 4, forced=fed[:4])
+        finally:
+            uninstall_press_patch()
+            set_active_press_cache(None)
+        runs.append((prefill, logits, [(l.state.keys.clone(), l.state.values.clone()) for l in cache.layers]))
+    (p1, l1, kv1), (p2, l2, kv2) = runs
+    assert torch.equal(p1, p2)
+    assert all(torch.equal(a, b) for a, b in zip(l1, l2))
+    for (k1, v1), (k2, v2) in zip(kv1, kv2):
+        assert torch.equal(k1, k2) and torch.equal(v1, v2)
+
+
 def test_press_patch_compresses_to_budget(model_and_ref):
     model, ids, (ref_prefill, _, fed), dtype = model_and_ref
     install_press_patch()

@@ -657,3 +657,37 @@ def test_inject_rerope_matches_model_rotation(dtype, per_head):
     bound = 4 * torch.finfo(dtype).eps * (k16.abs() + partner.abs())
     diff = (got.float() - want.float()).abs()
     assert (diff <= bound).all(), (diff - bound).max()
+
+
+# ---------------------------------------------------------------------------
+# Several layers' compaction in one launch set (row tables)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype,pooling", [(torch.float16, "maxpool"), (torch.bfloat16, "avgpool"),
+                                           (torch.float32, "maxpool")])
+def test_scores_and_gather_over_row_tables_equal_per_layer(dtype, pooling):
+    """snapkv_scores_rows / gather_rows_tab over separately allocated layers
+    give exactly the bits of one snapkv_scores / gather_rows call per layer;
+    the keys use the model's (B,S,H,D)-transposed layout."""
+    L, B, Hq, Hk, S, D, W, budget = 3, 2, 8, 2, 700, 64, 16, 96
+    qs, ks, vs = [], [], []
+    for l in range(L):
+        qs.append(_randn((B, Hq, S, D), 100 + l, dtype).to(DEV))
+        ks.append(_randn((B, S, Hk, D), 200 + l, dtype).to(DEV).transpose(1, 2))   # strided rows
+        vs.append(_randn((B, S, Hk, D), 300 + l, dtype).to(DEV).transpose(1, 2))
+    sc = 1.0 / math.sqrt(D)
+    q_win = [q[:, :, S - W:].contiguous() for q in qs]
+    rows = ops.snapkv_scores_rows(q_win, ks, W, sc, 7, pooling)
+    keep_all = ops.keep_index(rows, W, budget)
+    n = keep_all.shape[-1]
+    kd = [torch.full((B, Hk, n + 5, D), float("nan"), dtype=dtype, device=DEV) for _ in range(L)]
+    vd = [torch.full((B, Hk, n + 5, D), float("nan"), dtype=dtype, device=DEV) for _ in range(L)]
+    ops.gather_rows_tab(keep_all, ks, vs, kd, vd, dst_row0=2)
+    for l in range(L):
+        one = ops.snapkv_scores(qs[l], ks[l], W, sc, 7, pooling)
+        assert torch.equal(rows[l * B:(l + 1) * B], one), l
+        keep = ops.keep_index(one, W, budget)
+        assert torch.equal(keep_all[l * B:(l + 1) * B], keep), l
+        assert torch.equal(keep.cpu(), ref.keep_index(ref.window_scores(qs[l].cpu(), ks[l].cpu(), W, sc, 7, pooling),
+                                                      W, budget)), l
+        assert torch.equal(kd[l][:, :, 2:2 + n], ops.gather_kv(ks[l], keep)), l
+        assert torch.equal(vd[l][:, :, 2:2 + n], ops.gather_kv(vs[l], keep)), l
