@@ -591,6 +591,100 @@ def measure_h2o(w, dev, reps=5, steps=96):
     return out
 
 
+class _Rotary:
+    """The rotary module the inject path reads (default RoPE, no scaling)."""
+
+    def __init__(self, w, dev):
+        from hotcold_kv import synthetic
+        self.inv_freq = synthetic.inv_freq(w.head_dim, w.theta, dev)
+        self.attention_scaling = 1.0
+
+
+def hotcold_pipeline(w, dev, profile_steps=None):
+    """The hot/cold engine's own loop at a held-slot workload, through
+    hotcold_attention (the patched attention's body between RoPE and o_proj):
+      prefill  every layer's prompt appended to its HotColdLayer and
+               compressed to the budget (cache.py:37-128: raw-logit scores of
+               the recent queries, KV-head mean, top-k + recent window); the
+               evicted prompt tokens go to the native cold store;
+      decode   w.decode_steps steps over all layers: per-KV-head retrieval of
+               w.held tokens every w.retrieve_every steps on a host thread,
+               the pinned copy on the side stream, re-RoPE inject into the
+               held slot, and the fused append + held decode.
+    Knobs: max_capacity_prompt = budget + decode steps and topk_ratio giving
+    budget - window prefix tokens, so the prompt is cut to the budget once and
+    decode appends without re-compression.  The prompt's own attention (torch
+    SDPA in the patch) is not run: it is not part of the hot tier.  Inputs are
+    the workload's synthetic tokens, generated on the device beforehand."""
+    import torch
+    from hotcold_kv import KVController, synthetic
+    from hotcold_kv import patch as hp
+    from hotcold_kv.cache import HotColdLayer
+
+    L, B, G = w.layers, w.batch, w.group
+    cap = w.budget + w.decode_steps
+    topk = w.budget - w.window
+    ctrl = KVController(max_capacity_prompt=cap, topk_ratio=(topk + 0.5) / cap, recent_size=w.window,
+                        cpu_buffer_size=w.seq_len, faiss_dim=w.head_dim, window_size=w.retrieve_every,
+                        query_pool_size=4, lookahead_k=w.held, hold_retrieved=True, per_head_retrieval=True,
+                        profile_overlap=True, enable_asserts=False)
+    hp.set_active_rotary_emb(_Rotary(w, dev))
+    layers = [HotColdLayer(ctrl) for _ in range(L)]
+    steps = w.decode_steps if profile_steps is None else profile_steps
+    toks = [[synthetic.make_decode_token(w, l, t, seed=0, device=dev) for l in range(L)] for t in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for l in range(L):
+        p = synthetic.make_prompt(w, layer=l, seed=0, device=dev)
+        if l == 0:
+            ctrl._lazy_init(p["k_pre"], n_layers=L)
+        layers[l].set_last_query_post(p["q_post"][:, :, -w.window:, :].contiguous())
+        layers[l].update(key_states=p["k_post"], value_states=p["v"], layer_idx=l,
+                         cache_kwargs={"pre_key_states": p["k_pre"], "positions": p["positions"]})
+        del p
+    torch.cuda.synchronize()
+    prefill_s = time.perf_counter() - t0
+    step_ms = []
+    torch.cuda.synchronize()
+    t_all = time.perf_counter()
+    for t in range(steps):
+        ts = time.perf_counter()
+        for l in range(L):
+            k = toks[t][l]
+            hp.hotcold_attention(ctrl, layers[l], l, k["q_pre"], k["k_pre"], k["v"], k["q_post"], k["k_post"],
+                                 k["position"], G, w.scaling)
+        step_ms.append((time.perf_counter() - ts) * 1e3)
+    torch.cuda.synchronize()
+    total_ms = (time.perf_counter() - t_all) * 1e3
+    for l in range(L):
+        ctrl.wait_for_retrieval(l)
+    d = ctrl.dbg
+    retr_steps = [t for t in range(steps) if (t + 1) % w.retrieve_every in (0, 1)]
+    other = [step_ms[t] for t in range(steps) if t not in retr_steps]
+    out = {
+        "workload": w.name, "layers": L, "batch": B, "prompt": w.seq_len, "budget": w.budget, "held": w.held,
+        "retrieve_every": w.retrieve_every, "decode_steps": steps,
+        "prefill_compress_evict_s": round(prefill_s, 3),
+        "cold_tokens_per_layer": ctrl.cold_size(0),
+        "hot_rows_per_layer_end": layers[0].hot_length(),
+        "step_us_wall_mean": round(total_ms * 1e3 / steps, 1),
+        "step_us_wall_median": round(statistics.median(step_ms) * 1e3, 1),
+        "step_us_wall_without_retrieval_median": round(statistics.median(other) * 1e3, 1) if other else None,
+        "layer_us_wall_mean": round(total_ms * 1e3 / steps / L, 2),
+        "retrievals": d["retrieval_launched"], "prefetch_launched": d["prefetch_launched"],
+        "prefetch_ready": d["prefetch_ready"],
+        "ready_rate": round(d["prefetch_ready"] / max(1, d["prefetch_launched"]), 4),
+        "prefetch_not_ready_checks": d["prefetch_not_ready_checks"],
+        "injections": d["injection_new"], "held_decodes": d["injection_used"],
+        "copy_ms_mean": round(d["prefetch_copy_ms_sum"] / max(1, d["prefetch_copy_ms_count"]), 4),
+        "h2d_bytes_per_copy": 2 * B * w.hk * w.held * w.head_dim * 4 + 2 * B * w.hk * w.held * 8,
+    }
+    del layers, ctrl, toks
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def cpu_baseline(w, sample_seconds, n_layers=4):
     """The reference's torch-CPU path (snapkv_importance -> keep_index ->
     gather_kv, then per decode step cat + repeat_kv + SDPA) on a bounded
@@ -653,6 +747,8 @@ def main():
                     help="skip the secondary figures of the 16k/32k/64k workloads and H2O")
     ap.add_argument("--h2o-only", action="store_true",
                     help="only the H2O figures of one layer (one JSON object; for profiling)")
+    ap.add_argument("--pipeline-only", action="store_true",
+                    help="only the hot/cold pipeline of the 16k held-slot workload (one JSON object)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; the hot tier shards by batch and KV head "
@@ -671,6 +767,10 @@ def main():
     torch.cuda.set_device(dev)
     if args.h2o_only:
         print(json.dumps({"h2o": measure_h2o(w, dev)}), flush=True)
+        return
+    if args.pipeline_only:
+        print(json.dumps({"hotcold_pipeline": hotcold_pipeline(synthetic.WORKLOADS["llama8b_16k_b1024_held64"],
+                                                               dev)}), flush=True)
         return
     log(f"workload {w.name}: generating inputs on {torch.cuda.get_device_name(dev)}")
     stream = stream_rates(dev)
@@ -726,6 +826,14 @@ def main():
                 f"{r['inject']['rerope_us_all_layers']} us, H2D {r['inject']['h2d_GBps']} GB/s")
             others.append(r)
         del flush
+
+    pipe = None
+    if not args.no_other_configs and args.workload == "llama8b_8k_b512":
+        pw = synthetic.WORKLOADS["llama8b_16k_b1024_held64"]
+        log(f"hot/cold pipeline: {pw.name} ...")
+        pipe = hotcold_pipeline(pw, dev)
+        log(f"  step {pipe['step_us_wall_mean']} us wall ({pipe['layer_us_wall_mean']} us/layer), ready_rate "
+            f"{pipe['ready_rate']}, {pipe['retrievals']} retrievals, copy {pipe['copy_ms_mean']} ms")
 
     h2o = None
     if not args.no_other_configs and args.workload == "llama8b_8k_b512":
@@ -788,6 +896,7 @@ def main():
                                 "bytes_per_job": int(cbytes)},
         "device_stream": stream,
         "other_workloads": others,
+        "hotcold_pipeline": pipe,
         "h2o": h2o,
         "cpu_baseline": cpu,
     }

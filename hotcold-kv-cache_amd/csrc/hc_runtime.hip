@@ -98,6 +98,11 @@ extern "C" int hc_event_query(void* event) {
   return hip_rc(e, "hipEventQuery");
 }
 
+extern "C" int hc_event_synchronize(void* event) {
+  HC_REQUIRE(event != nullptr, "hc_event_synchronize: null event");
+  return hip_rc(hipEventSynchronize(reinterpret_cast<hipEvent_t>(event)), "hipEventSynchronize");
+}
+
 extern "C" int hc_event_elapsed_ms(void* start, void* end, float* ms_out) {
   HC_REQUIRE(start && end && ms_out, "hc_event_elapsed_ms: null argument");
   return hip_rc(hipEventElapsedTime(ms_out, reinterpret_cast<hipEvent_t>(start), reinterpret_cast<hipEvent_t>(end)),

@@ -174,6 +174,7 @@ SIGNATURES = {
     "hc_event_destroy": (_int, [_vp]),
     "hc_event_record": (_int, [_vp, _vp]),
     "hc_event_query": (_int, [_vp]),
+    "hc_event_synchronize": (_int, [_vp]),
     "hc_event_elapsed_ms": (_int, [_vp, _vp, ctypes.POINTER(ctypes.c_float)]),
     "hc_stream_wait_event": (_int, [_vp, _vp]),
     "hc_memcpy_h2d_async": (_int, [_vp, _vp, _i64, _vp]),

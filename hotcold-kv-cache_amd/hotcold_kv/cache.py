@@ -101,6 +101,30 @@ class HotColdLayer(CacheLayerMixin):
         self._compress_if_needed(layer_idx if layer_idx is not None else 0)
         return self.buf.keys, self.buf.values
 
+    # -- one-token decode: append and attend in one launch -------------------------------------
+    def decode_fusable(self) -> bool:
+        """True when this step's one-token append cannot trigger a compression
+        (cache.py:44): the append can then run inside the decode launch."""
+        return self.buf is not None and (self._last_q_post is None
+                                         or self.buf.n + 1 <= self.kvctrl.max_capacity_prompt)
+
+    def append_attend(self, q_post, k_post, v, k_pre, positions, scaling, held=None):
+        """update() of one token (cache.py:130-151) fused with the decode
+        attention over [held slot | hot rows | the token] (patch.py:241-305):
+        one launch writes the token's post-RoPE key, value, pre-RoPE key and
+        position into the next hot row and attends.  held = (pos, valid, R)
+        of the held retrieved slot, or None.  Returns (B,Hq,D)."""
+        buf = self.buf
+        buf.ensure(buf.n + 1)
+        R = int(held[2]) if held is not None else 0
+        lo = buf.held - R
+        out = ops.decode_append_rows(q_post, buf.st, lo, R + buf.n + 1, k_post, v, scaling, p_new=k_pre,
+                                     pos_new=positions, held=held if R else None,
+                                     cur_pos=positions[0, -1:] if R else None)
+        buf.n += 1
+        self.seen_tokens += 1
+        return out
+
     # -- compression (cache.py:37-128) ------------------------------------------------------
     def _compress_if_needed(self, layer_idx):
         ctrl = self.kvctrl

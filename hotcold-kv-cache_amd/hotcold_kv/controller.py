@@ -13,17 +13,24 @@ threads.  Logical order is oldest first; the search ranks by inner product
 per_head_retrieval=True the search runs per KV head (one vector per token
 and head) and positions become (B,Hk,R).
 
-Staging (controller.py:344-442).  A retrieval result lives in pinned host
-buffers; maybe_prefetch_to_gpu copies them with hipMemcpyAsync on a
-library-owned non-blocking side stream (default priority) and records an
-event; poll_staged_gpu queries the event without blocking, and once it has
-completed orders the caller's stream after it (hipStreamWaitEvent) before
-handing the device buffers to the inject kernel.  Host buffers stay
-referenced until their copy is known complete.
+Staging (controller.py:344-442).  Each layer owns a few reusable staging
+slots (pinned host buffers, device buffers and events, allocated once): the
+retrieval worker fills a free slot's host buffers; maybe_prefetch_to_gpu
+copies them with hipMemcpyAsync on a library-owned non-blocking side stream
+(default priority) and records the slot's event; poll_staged_gpu queries the
+event without blocking, and once it has completed orders the caller's stream
+after it (hipStreamWaitEvent) before the inject kernel reads the slot.  A
+slot whose data the held slot still uses is not refilled: when a newer
+retrieval is injected, an event recorded on the consumer stream marks the
+old slot free, and the side stream waits for it before copying into it
+again.  A staging superseded before it was polled is recycled once its copy
+is known complete; nothing waits on the host.
 """
 
+import concurrent.futures
 import ctypes
 import math
+import os
 import threading
 from collections import deque
 
@@ -32,6 +39,7 @@ import torch
 
 from . import _native as N
 from .datatypes import EvictedKV, RetrievedKV, _canon_br_2d, _canon_kv_4d
+from .ops import stream_handle as ops_stream
 
 
 class _Ring:
@@ -92,7 +100,56 @@ class _Ring:
         return d
 
 
+class _Slot:
+    """One reusable staging slot of a layer: pinned host buffers (k_pre, v,
+    pos, valid), their device twins, and the events of its copy."""
+
+    FREE, FILLING, RETRIEVED, COPYING, STAGED, HELD = range(6)
+
+    def __init__(self, host):
+        self.host = host            # (kpre, v, pos, valid) pinned host tensors
+        self.qhost = None           # pinned pooled query of the search it serves
+        self.q_ready = None         # event behind the query's copy
+        self.dev = None             # device twins, allocated on the first copy
+        self.state = _Slot.FREE
+        self.ready = None           # event recorded behind the copy
+        self.copied = False         # ready has been recorded (a copy was issued)
+        self.t0 = self.t1 = None    # timing events (profile_overlap)
+        self.free_after = None      # consumer-stream event: the slot's last reader is done
+        self.released = False       # free_after has been recorded
+
+
+class _Task:
+    """A scheduled search on the controller's worker pool (the handle the
+    reference keeps as a threading.Thread)."""
+
+    def __init__(self, future):
+        self.future = future
+
+    def is_alive(self):
+        return not self.future.done()
+
+    def join(self, timeout=None):
+        try:
+            self.future.result(timeout)
+        except concurrent.futures.TimeoutError:
+            pass
+
+
+_NOT_READY = RetrievedKV(k_pre=torch.empty(0), v=torch.empty(0), pos=torch.empty(0, dtype=torch.long),
+                         valid=torch.empty(0, dtype=torch.bool), ready=False)
+
+
 class KVController:
+    # staging slots per layer: one held, one in copy, one retrieved, one filling
+    MAX_SLOTS = 4
+    # Scheduled searches run on a small pool of worker threads (no thread per
+    # search), each native search on SEARCH_THREADS host threads: every layer
+    # searches in the same decode step, and together they keep to about half
+    # of the cores, so the decode thread is not starved of CPU.
+    SEARCH_THREADS = 2
+    MAX_SEARCH_WORKERS = 4
+
     def __init__(
         self,
         max_capacity_prompt: int = 128,
@@ -141,7 +198,10 @@ class KVController:
         self._retrieval_ready_cpu = []
         self._stage_lock = []
         self._staged = []
+        self._slots = []
+        self._held_slot = []
         self._stream = None
+        self._pool = None
         self._evict_dev = None
         self._evict_host = None
         self.last_injected_len = 0
@@ -165,6 +225,8 @@ class KVController:
             "prefetch_copy_ms_sum": 0.0,
             "prefetch_copy_ms_count": 0,
             "prefetch_not_ready_checks": 0,
+            "retrieval_skipped_no_slot": 0,
+            "prefetch_superseded": 0,
             "main_waited_for_prefetch": 0,
             "triton_decode_calls": 0,
             "triton_prefill_fallback": 0,
@@ -187,17 +249,34 @@ class KVController:
         self._retrieval_ready_cpu = [None] * L
         self._stage_lock = [threading.Lock() for _ in range(L)]
         self._staged = [None] * L
+        self._slots = [[] for _ in range(L)]
+        self._held_slot = [None] * L
         self.held_mem = [None] * L
         if k_pre.is_cuda:
             stream = ctypes.c_void_p()
             N.check(N.lib().hc_stream_create(ctypes.byref(stream)), "hc_stream_create")
             self._stream = stream.value
         self._inited = True
+        if k_pre.is_cuda and self.lookahead_k > 0:
+            # two staging slots per layer up front (one held, one in flight):
+            # pinned allocations are slow and would otherwise land in decode steps
+            for li in range(L):
+                with self._retrieval_lock[li]:
+                    for _ in range(2):
+                        self._take_slot(li).state = _Slot.FREE
 
     def __del__(self):
         try:
+            if self._pool is not None:
+                self._pool.shutdown(wait=True)
+            lib = N.lib()
+            for slots in self._slots:
+                for sl in slots:
+                    for ev in (sl.ready, sl.t0, sl.t1, sl.free_after):
+                        if ev is not None:
+                            lib.hc_event_destroy(ev)
             if self._stream is not None:
-                N.lib().hc_stream_destroy(self._stream)
+                lib.hc_stream_destroy(self._stream)
         except Exception:
             pass
 
@@ -303,36 +382,93 @@ class KVController:
     def update_query_window(self, layer_idx, q_pre):
         self.query_window[int(layer_idx)].append(q_pre.detach())
 
+    def _pooled_query_dev(self, layer_idx):
+        """The pooled recent pre-RoPE query on the device, fp32: (B,D), or
+        (B,Hk,D) per KV head (the means of _q_to_vecs_np before pad/crop and
+        normalisation)."""
+        q = torch.cat(list(self.query_window[int(layer_idx)]), dim=2)
+        if self.per_head_retrieval:
+            B, Hq, T, D = q.shape
+            return q.float().view(B, self.Hk, Hq // self.Hk, T, D).mean(dim=(2, 3))
+        return q.mean(dim=1).mean(dim=1).float()
+
+    def _stage_query(self, layer_idx, slot):
+        """Copy the pooled query into the slot's pinned buffer behind an event
+        on the current stream (no host wait)."""
+        qd = self._pooled_query_dev(layer_idx)
+        if slot.qhost is None or tuple(slot.qhost.shape) != tuple(qd.shape):
+            slot.qhost = torch.empty(qd.shape, dtype=torch.float32, pin_memory=True)
+        slot.qhost.copy_(qd, non_blocking=True)
+        if slot.q_ready is None:
+            slot.q_ready = self._event(0)
+        N.check(N.lib().hc_event_record(slot.q_ready, ops_stream(qd.device)), "hc_event_record")
+
+    def _wait_event(self, ev):
+        N.check(N.lib().hc_event_synchronize(ev), "hc_event_synchronize")
+
     def _pooled_query_np(self, layer_idx):
         qwin = self.query_window[int(layer_idx)]
         if len(qwin) == 0:
             return None
         return self._q_to_vecs_np(torch.cat(list(qwin), dim=2))
 
-    def _retrieval_worker(self, layer_idx, q_vecs):
-        """Top-lookahead_k tokens per batch row (or per KV head) into pinned
-        host buffers (controller.py:250-293), one native call over all rows."""
+    # -- staging slots ------------------------------------------------------------------
+    def _slot_shapes(self):
+        B, Hk, D, R = self.B, self.Hk, self.D, self.lookahead_k
+        pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
+        return ((B, Hk, R, D), torch.float32), ((B, Hk, R, D), torch.float32), (pshape, torch.int64), \
+            (pshape, torch.bool)
+
+    def _take_slot(self, li):
+        """A free slot of layer li whose last copy has completed (its host
+        buffers may be overwritten), marked FILLING; None if all are busy.
+        Called with the layer's retrieval lock held."""
+        for sl in self._slots[li]:
+            if sl.state == _Slot.FREE and (not sl.copied or self._event_done(sl.ready)):
+                sl.state = _Slot.FILLING
+                return sl
+        if len(self._slots[li]) >= self.MAX_SLOTS:
+            return None
+        pin = torch.cuda.is_available()
+        sl = _Slot(tuple(torch.empty(shape, dtype=dt, pin_memory=pin) for shape, dt in self._slot_shapes()))
+        sl.state = _Slot.FILLING
+        self._slots[li].append(sl)
+        return sl
+
+    def _retrieval_worker(self, layer_idx, q_vecs, slot=None, nthreads=0):
+        """Top-lookahead_k tokens per batch row (or per KV head) into a slot's
+        pinned host buffers (controller.py:250-293), one native call over all
+        rows.  q_vecs None: the slot's pooled query is still being copied to
+        the host; wait for it here, on this thread, then normalise it."""
         li = int(layer_idx)
         if not self._inited:
             return
-        B, Hk, D, R = self.B, self.Hk, self.D, self.lookahead_k
-        pin = torch.cuda.is_available()
-        kpre = torch.empty((B, Hk, R, D), dtype=torch.float32, pin_memory=pin)
-        vv = torch.empty((B, Hk, R, D), dtype=torch.float32, pin_memory=pin)
-        pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
-        pos = torch.empty(pshape, dtype=torch.int64, pin_memory=pin)
-        valid = torch.empty(pshape, dtype=torch.bool, pin_memory=pin)
+        if slot is None:
+            with self._retrieval_lock[li]:
+                slot = self._take_slot(li)
+            if slot is None:
+                self.dbg["retrieval_skipped_no_slot"] += 1
+                return
+        if q_vecs is None:
+            self._wait_event(slot.q_ready)
+            q_vecs = self._normalize(self._pad_or_crop(slot.qhost.numpy()))
+        B, R = self.B, self.lookahead_k
+        kpre, vv, pos, valid = slot.host
         q = np.ascontiguousarray(q_vecs, dtype=np.float32).reshape(B, -1, self.faiss_dim)
         stores = (ctypes.c_void_p * B)(*[self.rings[li][b].handle for b in range(B)])
         N.check(N.lib().hc_cold_retrieve(stores, B, q.ctypes.data, q.shape[1] * self.faiss_dim, self.faiss_dim, R,
                                          int(self.per_head_retrieval), kpre.data_ptr(), vv.data_ptr(),
-                                         pos.data_ptr(), valid.data_ptr(), 0), "hc_cold_retrieve")
+                                         pos.data_ptr(), valid.data_ptr(), int(nthreads)), "hc_cold_retrieve")
         with self._retrieval_lock[li]:
             if not bool(valid.any()):
-                self._retrieval_ready_cpu[li] = None
+                slot.state = _Slot.FREE
                 self.dbg["retrieval_ready_empty"] += 1
                 return
-            self._retrieval_ready_cpu[li] = (kpre, vv, pos, valid)
+            old = self._retrieval_ready_cpu[li]
+            if old is not None:        # a newer result replaces one never copied
+                old.state = _Slot.FREE
+            self._retrieval_ready_cpu[li] = slot
+            slot.state = _Slot.RETRIEVED
             self.dbg["retrieval_ready_cpu"] += 1
 
     def launch_retrieval_now(self, layer_idx, q_pre):
@@ -349,7 +485,9 @@ class KVController:
 
     def maybe_launch_async_retrieval(self, layer_idx):
         """Every window_size calls, start a background search with the pooled
-        recent queries (controller.py:314-342)."""
+        recent queries (controller.py:314-342).  Skipped while the layer's
+        previous search still runs (controller.py:333-335) or when every
+        staging slot is in use."""
         if self.lookahead_k <= 0:
             return
         li = int(layer_idx)
@@ -361,17 +499,35 @@ class KVController:
         if self.cold_size(li) == 0:
             self.dbg["retrieval_skipped_no_cold"] += 1
             return
-        q_vecs = self._pooled_query_np(li)
-        if q_vecs is None:
+        if len(self.query_window[li]) == 0:
             return
         with self._retrieval_lock[li]:
             th = self._retrieval_thread[li]
             if th is not None and th.is_alive():
                 return
-            th = threading.Thread(target=self._retrieval_worker, args=(li, q_vecs), daemon=True)
+            slot = self._take_slot(li)
+            if slot is None:
+                self.dbg["retrieval_skipped_no_slot"] += 1
+                return
+        if self._stream is not None and self.query_window[li][0].is_cuda:
+            # pooled on the device; the worker waits for the host copy, the
+            # decode thread does not
+            self._stage_query(li, slot)
+            q_vecs = None
+        else:
+            q_vecs = self._pooled_query_np(li)
+        with self._retrieval_lock[li]:
+            th = self._spawn(self._retrieval_worker, (li, q_vecs, slot, self.SEARCH_THREADS))
             self._retrieval_thread[li] = th
-            th.start()
             self.dbg["retrieval_launched"] += 1
+
+    def _spawn(self, fn, args):
+        if self._pool is None:
+            cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 4)
+            workers = max(1, min(self.MAX_SEARCH_WORKERS, cores // (2 * self.SEARCH_THREADS)))
+            self._pool = concurrent.futures.ThreadPoolExecutor(max_workers=workers,
+                                                               thread_name_prefix="hotcold-search")
+        return _Task(self._pool.submit(fn, *args))
 
     def wait_for_retrieval(self, layer_idx, timeout=None):
         """Join the layer's background search, if any (test and shutdown helper)."""
@@ -380,11 +536,63 @@ class KVController:
             th.join(timeout)
 
     # -- staging ------------------------------------------------------------------------------
+    # The device-side primitives are methods so that tests can run the
+    # staging state machine without a GPU.
     def _event(self, timing):
         ev = ctypes.c_void_p()
         N.check(N.lib().hc_event_create(ctypes.byref(ev), int(timing)), "hc_event_create")
         return ev.value
 
+    def _event_done(self, ev):
+        done = N.lib().hc_event_query(ev)
+        if done < 0:
+            N.check(done, "hc_event_query")
+        return done == 1
+
+    def _alloc_dev(self, slot, device):
+        slot.dev = tuple(torch.empty(t.shape, dtype=t.dtype, device=device) for t in slot.host)
+
+    def _copy_to_device(self, slot):
+        """The slot's host-to-device copies on the side stream, after the
+        consumer stream has released the slot's previous contents; its ready
+        event recorded behind them."""
+        lib = N.lib()
+        if slot.ready is None:
+            slot.ready = self._event(0)
+            if self.profile_overlap:
+                slot.t0, slot.t1 = self._event(1), self._event(1)
+        if slot.released:
+            N.check(lib.hc_stream_wait_event(self._stream, slot.free_after), "hc_stream_wait_event")
+        if slot.t0 is not None:
+            N.check(lib.hc_event_record(slot.t0, self._stream), "hc_event_record")
+        for d, h in zip(slot.dev, slot.host):
+            N.check(lib.hc_memcpy_h2d_async(d.data_ptr(), h.data_ptr(), h.numel() * h.element_size(), self._stream),
+                    "hc_memcpy_h2d_async")
+        if slot.t1 is not None:
+            N.check(lib.hc_event_record(slot.t1, self._stream), "hc_event_record")
+        N.check(lib.hc_event_record(slot.ready, self._stream), "hc_event_record")
+        slot.copied = True
+
+    def _order_after(self, slot):
+        """Order the consumer stream after the slot's copy."""
+        N.check(N.lib().hc_stream_wait_event(ops_stream(slot.dev[0].device), slot.ready), "hc_stream_wait_event")
+
+    def _mark_released(self, slot):
+        """Record on the consumer stream that the slot's last reader has been
+        issued; its next copy waits for this point."""
+        lib = N.lib()
+        if slot.free_after is None:
+            slot.free_after = self._event(0)
+        N.check(lib.hc_event_record(slot.free_after, ops_stream(slot.dev[0].device)), "hc_event_record")
+        slot.released = True
+
+    def _copy_ms(self, slot):
+        ms = ctypes.c_float()
+        if N.lib().hc_event_elapsed_ms(slot.t0, slot.t1, ctypes.byref(ms)) == 0:
+            return float(ms.value)
+        return None
+
+    # -- staging state machine (controller.py:344-442) ------------------------------------------
     def maybe_prefetch_to_gpu(self, layer_idx, device, dtype=None):
         """Start the host-to-device copy of a finished retrieval on the side
         stream (controller.py:344-380).  dtype is accepted for compatibility:
@@ -394,79 +602,88 @@ class KVController:
         if device.type != "cuda" or self._stream is None:
             return
         with self._retrieval_lock[li]:
-            pack = self._retrieval_ready_cpu[li]
+            slot = self._retrieval_ready_cpu[li]
             self._retrieval_ready_cpu[li] = None
-        if pack is None:
-            return
-        kpre, vv, pos, valid = pack
-        lib = N.lib()
-        dev = [torch.empty(t.shape, dtype=t.dtype, device=device) for t in pack]
-        t0 = self._event(1) if self.profile_overlap else None
-        t1 = self._event(1) if self.profile_overlap else None
-        ready = self._event(0)
-        if t0 is not None:
-            N.check(lib.hc_event_record(t0, self._stream), "hc_event_record")
-        for d, h in zip(dev, pack):
-            N.check(lib.hc_memcpy_h2d_async(d.data_ptr(), h.data_ptr(), h.numel() * h.element_size(), self._stream),
-                    "hc_memcpy_h2d_async")
-        if t1 is not None:
-            N.check(lib.hc_event_record(t1, self._stream), "hc_event_record")
-        N.check(lib.hc_event_record(ready, self._stream), "hc_event_record")
+            if slot is None:
+                return
+            slot.state = _Slot.COPYING
+        if slot.dev is None:
+            self._alloc_dev(slot, device)
+        self._copy_to_device(slot)
         with self._stage_lock[li]:
             old = self._staged[li]
-            self._staged[li] = dict(dev=dev, host=pack, ready=ready, t0=t0, t1=t1)
+            self._staged[li] = slot
             self.dbg["prefetch_launched"] += 1
         if old is not None:
-            self._release(old, wait=True)
-
-    def _release(self, st, wait=False):
-        lib = N.lib()
-        if wait:
-            while lib.hc_event_query(st["ready"]) == 0:
-                pass
-        for key in ("ready", "t0", "t1"):
-            if st.get(key) is not None:
-                lib.hc_event_destroy(st[key])
-                st[key] = None
+            # superseded before it was polled: free once its copy completes
+            # (_take_slot checks the event), no wait here
+            with self._retrieval_lock[li]:
+                old.state = _Slot.FREE
+            self.dbg["prefetch_superseded"] += 1
 
     def poll_staged_gpu(self, layer_idx) -> RetrievedKV:
         """Non-blocking check for a staged retrieval (controller.py:382-442)."""
         li = int(layer_idx)
-        empty = RetrievedKV(k_pre=torch.empty(0), v=torch.empty(0), pos=torch.empty(0, dtype=torch.long),
-                            valid=torch.empty(0, dtype=torch.bool), ready=False)
         if not self._inited or self._stream is None:
-            return empty
-        lib = N.lib()
+            return _NOT_READY
         with self._stage_lock[li]:
-            st = self._staged[li]
-            if st is None:
-                return empty
-            done = lib.hc_event_query(st["ready"])
-            if done < 0:
-                N.check(done, "hc_event_query")
-            if done == 0:
+            slot = self._staged[li]
+            if slot is None:
+                return _NOT_READY
+            if not self._event_done(slot.ready):
                 self.dbg["prefetch_not_ready_checks"] += 1
                 if not self.force_wait_for_prefetch_diagnostic:
-                    return empty
+                    return _NOT_READY
                 self.dbg["main_waited_for_prefetch"] += 1
-                while lib.hc_event_query(st["ready"]) == 0:
+                while not self._event_done(slot.ready):
                     pass
             self._staged[li] = None
+            slot.state = _Slot.STAGED
             self.dbg["prefetch_ready"] += 1
         # the copy has completed; order the consumer stream after it anyway
-        cur = torch.cuda.current_stream(st["dev"][0].device).cuda_stream
-        N.check(lib.hc_stream_wait_event(cur, st["ready"]), "hc_stream_wait_event")
-        if self.profile_overlap and st["t0"] is not None:
-            ms = ctypes.c_float()
-            if lib.hc_event_elapsed_ms(st["t0"], st["t1"], ctypes.byref(ms)) == 0:
-                self.dbg["prefetch_copy_ms_sum"] += float(ms.value)
+        self._order_after(slot)
+        if self.profile_overlap and slot.t0 is not None:
+            ms = self._copy_ms(slot)
+            if ms is not None:
+                self.dbg["prefetch_copy_ms_sum"] += ms
                 self.dbg["prefetch_copy_ms_count"] += 1
-        self._release(st)
-        kpre, vv, pos, valid = st["dev"]
-        valid = valid.view(torch.bool)
+        kpre, vv, pos, valid = slot.dev
         kpre = _canon_kv_4d(kpre, "staged.k_pre")
         vv = _canon_kv_4d(vv, "staged.v")
         if not self.per_head_retrieval:
             pos = _canon_br_2d(pos, "staged.pos")
             valid = _canon_br_2d(valid, "staged.valid")
         return RetrievedKV(k_pre=kpre, v=vv, pos=pos, valid=valid, ready=True)
+
+    def staged_consumed(self, layer_idx):
+        """The staging just returned by poll_staged_gpu has been injected on
+        the consumer stream: it becomes the layer's held slot (its positions
+        and valid flags stay in use), and the previous held slot is released
+        behind this point of the consumer stream."""
+        li = int(layer_idx)
+        with self._retrieval_lock[li]:
+            new = next((sl for sl in self._slots[li] if sl.state == _Slot.STAGED), None)
+            if new is None:
+                return
+            old, self._held_slot[li] = self._held_slot[li], new
+            new.state = _Slot.HELD
+            if old is not None and old is not new:
+                self._mark_released(old)
+                old.state = _Slot.FREE
+
+    def resolve_held(self, layer_idx, injected):
+        """The held slot this step attends (patch.py:241-291): the retrieval
+        injected this step, else (hold_retrieved) the last one injected --
+        a copy not ready yet leaves it in place -- else none."""
+        li = int(layer_idx)
+        if injected is not None:
+            if self.hold_retrieved:
+                self.held_mem[li] = injected
+                self.dbg["injection_new"] += 1
+            held = injected
+        else:
+            held = self.held_mem[li] if self.hold_retrieved else None
+        if held is not None:
+            self.last_injected_len = held[2]
+            self.dbg["injection_used"] += 1
+        return held

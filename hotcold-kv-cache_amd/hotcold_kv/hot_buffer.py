@@ -128,11 +128,8 @@ class HotBuffer:
         """Append one token (k, v, pre (B,H,1,D), pos (B,1)) and attend q over
         the hot rows plus the token, in one launch.  Returns (B,Hq,D)."""
         self.ensure(self.n + 1)
-        lo, hi = self.held, self.held + self.n + 1
-        out = ops.decode_attention_append(
-            q, self._rows("k", lo, hi), self._rows("v", lo, hi), k, v, scaling,
-            pre=(pre, self._rows("p", lo, hi)) if self.with_pre and pre is not None else None,
-            pos=(pos, self._rows("pos", lo, hi)) if self.with_pos and pos is not None else None)
+        out = ops.decode_append_rows(q, self.st, self.held, self.n + 1, k, v, scaling,
+                                     p_new=pre if self.with_pre else None, pos_new=pos if self.with_pos else None)
         self.n += 1
         return out
 

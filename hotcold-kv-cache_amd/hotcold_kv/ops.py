@@ -25,8 +25,18 @@ def _require_device(*tensors):
                 f"(got a tensor on {t.device})")
 
 
-def _stream_handle(device):
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def stream_handle(device):
+    """The raw handle of torch's current stream on `device` (hipStream_t as an int)."""
+    if _raw_stream is not None:
+        idx = device.index if device.index is not None else torch.cuda.current_device()
+        return _raw_stream(idx)
     return torch.cuda.current_stream(device).cuda_stream
+
+
+_stream_handle = stream_handle
 
 
 def _ptr(t):
@@ -246,6 +256,77 @@ def decode_attention_append(q, k, v, k_new, v_new, scaling, pre=None, pos=None, 
         _ptr(out), out.stride(0), out.stride(1),
         _ptr(ws), ws.numel(), int(num_splits),
         _stream_handle(q3.device))
+    N.check(rc, "hc_decode_attn_append")
+    return out
+
+
+def decode_append_rows(q, st, lo, S, k_new, v_new, scaling, p_new=None, pos_new=None, held=None, cur_pos=None):
+    """decode_attention_append over rows lo .. lo+S-1 of a hot buffer's
+    storage, addressed by offset instead of through tensor views (the
+    per-layer decode call of the drop-in; same launch, less host work).
+
+    st: {"k", "v"[, "p", "pos"]} -- (B,Hk,cap,D) K/V/pre-RoPE rows and
+    (B,cap) int64 positions.  Row lo+S-1 receives k_new / v_new (and p_new,
+    pos_new (B,1)).  held = (pos, valid, R): the first R attended rows are the
+    held slot, masked with valid & (pos <= cur_pos).  Returns out (B,Hq,D)."""
+    k, v = st["k"], st["v"]
+    B, Hk, cap, D = k.shape
+    q3 = q[:, :, 0, :] if q.dim() == 4 else q
+    kn = k_new[:, :, 0, :] if k_new.dim() == 4 else k_new
+    vn = v_new[:, :, 0, :] if v_new.dim() == 4 else v_new
+    if not q3.is_cuda or q3.shape[0] != B or q3.shape[2] != D or tuple(kn.shape) != (B, Hk, D) \
+            or tuple(vn.shape) != (B, Hk, D) or q3.dtype != k.dtype or kn.dtype != k.dtype or vn.dtype != k.dtype \
+            or q3.stride(-1) != 1 or kn.stride(-1) != 1 or vn.stride(-1) != 1:
+        raise RuntimeError("decode_append_rows: q (B,Hq,D), k_new / v_new (B,Hk,D) device rows in the buffer's "
+                           "dtype required")
+    if lo < 0 or S < 1 or lo + S > cap:
+        raise RuntimeError(f"decode_append_rows: rows {lo}..{lo + S - 1} outside the buffer's {cap}")
+    Hq = q3.shape[1]
+    es = k.element_size()
+    ks, vs = k.stride(), v.stride()
+    pn_args = [None, 0, 0, None, 0, 0, 0]
+    if p_new is not None:
+        pst = st["p"]
+        pn = p_new[:, :, 0, :] if p_new.dim() == 4 else p_new
+        if tuple(pn.shape) != (B, Hk, D) or pn.stride(-1) != 1 or pn.dtype != k.dtype:
+            raise RuntimeError("decode_append_rows: p_new must be (B,Hk,D) in the buffer's dtype")
+        ps = pst.stride()
+        pn_args = [pn.data_ptr(), pn.stride(0), pn.stride(1), pst.data_ptr() + lo * ps[2] * es, ps[0], ps[1], ps[2]]
+    pos_args = [None, 0, None, 0]
+    if pos_new is not None:
+        posst = st["pos"]
+        if pos_new.dtype != torch.int64 or pos_new.shape[0] != B:
+            raise RuntimeError("decode_append_rows: pos_new must be (B,1) int64")
+        pos_args = [pos_new.data_ptr(), pos_new.stride(0), posst.data_ptr() + lo * 8, posst.stride(0)]
+    held_args = [0, None, 0, 0, None, 0, 0, None]
+    if held is not None and int(held[2]) > 0:
+        hp, hv, R = held
+        if hv.dtype == torch.bool:
+            hv = hv.view(torch.uint8)
+        if hp.dtype != torch.int64 or int(R) > S - 1 or hp.shape[0] != B or hv.shape[0] != B \
+                or hp.shape[-1] < R or hv.shape[-1] < R or hp.stride(-1) != 1 or hv.stride(-1) != 1 \
+                or (hp.dim() == 3 and hp.shape[1] != Hk) or (hv.dim() == 3 and hv.shape[1] != Hk):
+            raise RuntimeError("decode_append_rows: held = (pos (B,R)|(B,Hk,R) int64, valid, R <= S-1)")
+        held_args = [int(R), hp.data_ptr(), hp.stride(0), hp.stride(1) if hp.dim() == 3 else 0,
+                     hv.data_ptr(), hv.stride(0), hv.stride(1) if hv.dim() == 3 else 0,
+                     None if cur_pos is None else cur_pos.data_ptr()]
+    out = torch.empty((B, Hq, D), dtype=k.dtype, device=k.device)
+    lib = N.lib()
+    ws = _workspace("decode", k.device, lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, S, 0, 0))
+    rc = lib.hc_decode_attn_append(
+        N.dtype_code(k.dtype), B, Hq, Hk, D, S,
+        q3.data_ptr(), q3.stride(0), q3.stride(1),
+        k.data_ptr() + lo * ks[2] * es, ks[0], ks[1], ks[2],
+        v.data_ptr() + lo * vs[2] * es, vs[0], vs[1], vs[2],
+        kn.data_ptr(), kn.stride(0), kn.stride(1),
+        vn.data_ptr(), vn.stride(0), vn.stride(1),
+        *pn_args, *pos_args,
+        None, 0,
+        *held_args,
+        float(scaling),
+        out.data_ptr(), out.stride(0), out.stride(1),
+        ws.data_ptr(), ws.numel(), 0,
+        stream_handle(k.device))
     N.check(rc, "hc_decode_attn_append")
     return out
 

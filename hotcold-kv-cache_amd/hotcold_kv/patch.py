@@ -63,6 +63,82 @@ def _rotate_k_with_pos(k_pre, pos_ids, head_dim=None):
     return out_k
 
 
+def hotcold_attention(kvctrl, layer, li, q_pre, k_pre, v, q_post, k_post, pos_new, n_rep, scaling,
+                      attention_mask=None, past_key_values=None):
+    """One layer's attention on the hot/cold engine: the body of the patched
+    LlamaAttention.forward between RoPE and o_proj (patch.py:152-337), on
+    (B,H,T,D) q_pre/k_pre/v/q_post/k_post and absolute positions pos_new
+    (B,T).  layer is the layer's HotColdLayer (None: plain cache in
+    past_key_values, or none).  Returns (B,Hq,T,D).
+
+    A one-token step whose append cannot trigger a compression appends inside
+    the decode launch (HotColdLayer.append_attend); other steps append
+    through HotColdLayer.update (which may compress and evict), then attend."""
+    q_len = int(q_pre.shape[2])
+    device = q_pre.device
+
+    # retrieval pipeline (patch.py:164-172)
+    if q_len == 1 or kvctrl.query_pool_size >= kvctrl.window_size:
+        kvctrl.update_query_window(li, q_pre)
+    kvctrl.maybe_launch_async_retrieval(li)
+    kvctrl.maybe_prefetch_to_gpu(li, device=device, dtype=q_pre.dtype)
+
+    fused = q_len == 1 and layer is not None and layer.decode_fusable()
+    k_cur, v_cur = k_post, v
+    if layer is not None:
+        r = kvctrl.recent_size
+        layer.set_last_query_post(q_post if q_len <= r else q_post[:, :, -r:, :].clone())
+        if not fused:
+            layer.update(key_states=k_post, value_states=v, layer_idx=li,
+                         cache_kwargs={"pre_key_states": k_pre, "positions": pos_new})
+    elif past_key_values is not None:
+        past_key_values.update(k_post, v, li)
+
+    if q_len > 1 and kvctrl.retrieve_after_prefill:
+        kvctrl.launch_retrieval_now(li, q_pre[:, :, -kvctrl.query_pool_size:, :])
+        kvctrl.maybe_prefetch_to_gpu(li, device=device, dtype=q_pre.dtype)
+
+    kvctrl.last_injected_len = 0
+
+    if q_len == 1 and layer is not None:
+        injected = None
+        rr = kvctrl.poll_staged_gpu(li)
+        if rr.ready:
+            kbuf, vbuf = layer.buf.held_storage()
+            R = int(rr.k_pre.shape[2])
+            inv, ascale = _rope_params(device)
+            ops.inject_rerope(rr.k_pre, rr.v, rr.pos, inv, ascale, kbuf, vbuf)
+            kvctrl.staged_consumed(li)
+            injected = (rr.pos, rr.valid, R)
+        held = kvctrl.resolve_held(li, injected)
+        if fused:
+            out = layer.append_attend(q_post, k_post, v, k_pre, pos_new, scaling, held)
+        elif held is not None:
+            pos_h, valid_h, R = held
+            k_att, v_att = layer.buf.attended(with_held=True)
+            k_att = k_att[:, :, layer.buf.held - R:]
+            v_att = v_att[:, :, layer.buf.held - R:]
+            out = ops.decode_attention(q_post, k_att, v_att, scaling, held_len=R, held_pos=pos_h,
+                                       held_valid=valid_h, cur_pos=pos_new[0, -1:])
+        else:
+            k_att, v_att = layer.buf.attended(with_held=False)
+            out = ops.decode_attention(q_post, k_att, v_att, scaling)
+        kvctrl.dbg["triton_decode_calls"] += 1
+        return out.unsqueeze(2)                                           # (B,Hq,1,D)
+    if q_len == 1:
+        # no hot/cold layer: attend over this step's cache entry only
+        return ops.decode_attention(q_post, k_cur, v_cur, scaling).unsqueeze(2)
+    kvctrl.dbg["triton_prefill_fallback"] += 1
+    prev = layer.get_seq_length() - q_len if layer is not None else 0
+    if prev > 0:
+        raise NotImplementedError("multi-token forward on a non-empty hot cache (chunked prefill) "
+                                  "is not supported by the hot/cold patch")
+    k_rep = modeling_llama.repeat_kv(k_cur, n_rep) if n_rep > 1 else k_cur
+    v_rep = modeling_llama.repeat_kv(v_cur, n_rep) if n_rep > 1 else v_cur
+    return F.scaled_dot_product_attention(q_post, k_rep, v_rep, attn_mask=attention_mask,
+                                          dropout_p=0.0, is_causal=attention_mask is None)
+
+
 _ORIG = None
 
 
@@ -102,12 +178,6 @@ def install_monkeypatch(enable_debug: bool = True):
         cos, sin = position_embeddings
         q_post, k_post = modeling_llama.apply_rotary_pos_emb(q_pre, k_pre, cos, sin)
 
-        # retrieval pipeline (patch.py:164-172)
-        if q_len == 1 or kvctrl.query_pool_size >= kvctrl.window_size:
-            kvctrl.update_query_window(li, q_pre)
-        kvctrl.maybe_launch_async_retrieval(li)
-        kvctrl.maybe_prefetch_to_gpu(li, device=device, dtype=hidden_states.dtype)
-
         layer = None
         if isinstance(past_key_values, Cache) and isinstance(past_key_values.layers[li], HotColdLayer):
             layer = past_key_values.layers[li]
@@ -124,65 +194,10 @@ def install_monkeypatch(enable_debug: bool = True):
             pos_new = torch.arange(prev, prev + q_len, device=device, dtype=torch.long).unsqueeze(0).expand(bsz, -1)
         pos_new = pos_new.contiguous()
 
-        k_cur, v_cur = k_post, v
-        if layer is not None:
-            r = kvctrl.recent_size
-            layer.set_last_query_post(q_post if q_len <= r else q_post[:, :, -r:, :].clone())
-            layer.update(key_states=k_post, value_states=v, layer_idx=li,
-                         cache_kwargs={"pre_key_states": k_pre, "positions": pos_new})
-        elif past_key_values is not None:
-            past_key_values.update(k_post, v, li)
-
-        if q_len > 1 and kvctrl.retrieve_after_prefill:
-            kvctrl.launch_retrieval_now(li, q_pre[:, :, -kvctrl.query_pool_size:, :])
-            kvctrl.maybe_prefetch_to_gpu(li, device=device, dtype=hidden_states.dtype)
-
-        kvctrl.last_injected_len = 0
-        n_rep = num_heads // num_kv_heads
-        scaling = 1.0 / math.sqrt(head_dim)
-
-        if q_len == 1 and layer is not None:
-            held = None
-            rr = kvctrl.poll_staged_gpu(li)
-            if rr.ready:
-                kbuf, vbuf = layer.buf.held_storage()
-                R = int(rr.k_pre.shape[2])
-                inv, ascale = _rope_params(device)
-                ops.inject_rerope(rr.k_pre, rr.v, rr.pos, inv, ascale, kbuf, vbuf)
-                held = (rr.pos, rr.valid, R)
-                if kvctrl.hold_retrieved:
-                    kvctrl.held_mem[li] = held
-                    kvctrl.dbg["injection_new"] += 1
-            elif kvctrl.hold_retrieved:
-                held = kvctrl.held_mem[li]
-            if held is not None:
-                pos_h, valid_h, R = held
-                kvctrl.last_injected_len = R
-                kvctrl.dbg["injection_used"] += 1
-                k_att, v_att = layer.buf.attended(with_held=True)
-                k_att = k_att[:, :, layer.buf.held - R:]
-                v_att = v_att[:, :, layer.buf.held - R:]
-                out = ops.decode_attention(q_post, k_att, v_att, scaling, held_len=R, held_pos=pos_h,
-                                           held_valid=valid_h, cur_pos=pos_new[0, -1:])
-            else:
-                k_att, v_att = layer.buf.attended(with_held=False)
-                out = ops.decode_attention(q_post, k_att, v_att, scaling)
-            kvctrl.dbg["triton_decode_calls"] += 1
-            attn_out = out.unsqueeze(2)                                    # (B,Hq,1,D)
-        elif q_len == 1:
-            # no hot/cold layer: attend over this step's cache entry only
-            out = ops.decode_attention(q_post, k_cur, v_cur, scaling)
-            attn_out = out.unsqueeze(2)
-        else:
-            kvctrl.dbg["triton_prefill_fallback"] += 1
-            if prev > 0:
-                raise NotImplementedError("multi-token forward on a non-empty hot cache (chunked prefill) "
-                                          "is not supported by the hot/cold patch")
-            k_rep = modeling_llama.repeat_kv(k_cur, n_rep) if n_rep > 1 else k_cur
-            v_rep = modeling_llama.repeat_kv(v_cur, n_rep) if n_rep > 1 else v_cur
-            attn_out = F.scaled_dot_product_attention(q_post, k_rep, v_rep, attn_mask=attention_mask,
-                                                      dropout_p=0.0, is_causal=attention_mask is None)
-
+        attn_out = hotcold_attention(kvctrl, layer, li, q_pre, k_pre, v, q_post, k_post, pos_new,
+                                     num_heads // num_kv_heads, 1.0 / math.sqrt(head_dim),
+                                     attention_mask=attention_mask,
+                                     past_key_values=past_key_values if layer is None else None)
         attn_out = attn_out.transpose(1, 2).contiguous().view(bsz, q_len, -1)
         attn_out = self.o_proj(attn_out)
 

@@ -375,6 +375,9 @@ int hc_event_create(void** event_out, int timing);
 int hc_event_destroy(void* event);
 int hc_event_record(void* event, void* stream);
 int hc_event_query(void* event);            /* 1 = complete, 0 = pending, <0 = error */
+/* Block the calling host thread until the event completes (the retrieval
+ * worker waits for its query vector; the decode thread never calls it). */
+int hc_event_synchronize(void* event);
 int hc_event_elapsed_ms(void* start, void* end, float* ms_out);
 int hc_stream_wait_event(void* stream, void* event);
 int hc_memcpy_h2d_async(void* dst, const void* src, int64_t bytes, void* stream);

@@ -146,7 +146,7 @@ def _evict(ctrl, keys, positions, idx=None):
 def _top1(ctrl, key):
     q = ctrl._k_token_to_vec_np(key)[None, :]
     ctrl._retrieval_worker(0, q)
-    kpre, v, pos, valid = ctrl._retrieval_ready_cpu[0]
+    kpre, v, pos, valid = ctrl._retrieval_ready_cpu[0].host
     assert bool(valid[0, 0])
     return int(pos[0, 0]), kpre[0, :, 0, :], v[0, :, 0, :], pos[0][valid[0]].tolist()
 
@@ -197,7 +197,7 @@ def test_cold_store_skips_padding_and_ranks_by_inner_product():
     assert ctrl.cold_size(0) == 4
     q = ctrl._k_token_to_vec_np(keys[3])
     ctrl._retrieval_worker(0, q[None, :])
-    _, _, pos, valid = ctrl._retrieval_ready_cpu[0]
+    _, _, pos, valid = ctrl._retrieval_ready_cpu[0].host
     got = pos[0][valid[0]].tolist()
     snap = ctrl.rings[0][0].export()
     ip = np.zeros(len(snap["pos"]))
@@ -213,7 +213,7 @@ def test_cold_store_ties_go_to_the_older_token():
     _evict(ctrl, torch.cat([k, k, k]), [10, 11, 12])
     q = ctrl._k_token_to_vec_np(k[0])
     ctrl._retrieval_worker(0, q[None, :])
-    _, _, pos, valid = ctrl._retrieval_ready_cpu[0]
+    _, _, pos, valid = ctrl._retrieval_ready_cpu[0].host
     assert pos[0].tolist() == [10, 11] and valid.all()
 
 
@@ -225,7 +225,7 @@ def test_cold_store_per_head_retrieval():
     q = np.stack([ctrl._normalize(ctrl._pad_or_crop(keys[2, 0].numpy())),
                   ctrl._normalize(ctrl._pad_or_crop(keys[7, 1].numpy()))])[None]
     ctrl._retrieval_worker(0, q)
-    kpre, v, pos, valid = ctrl._retrieval_ready_cpu[0]
+    kpre, v, pos, valid = ctrl._retrieval_ready_cpu[0].host
     assert pos.shape == (1, HK, 2) and valid.dtype == torch.bool
     assert int(pos[0, 0, 0]) == 52 and int(pos[0, 1, 0]) == 57
     assert torch.equal(kpre[0, 0, 0], keys[2, 0]) and torch.equal(kpre[0, 1, 0], keys[7, 1])
@@ -296,7 +296,7 @@ def test_native_retrieve_matches_per_row_search(per_head):
     q = np.stack([np.stack([orcs[0].token_vecs(torch.randn(H, Dm, generator=g).numpy())[h % vh]
                             for h in range(vh)]) for _ in range(B)])
     ctrl._retrieval_worker(0, q if per_head else q[:, 0])
-    kpre, vv, p, valid = ctrl._retrieval_ready_cpu[0]
+    kpre, vv, p, valid = ctrl._retrieval_ready_cpu[0].host
     for b in range(B):
         for h in range(vh):
             hits = orcs[b].search(q[b, h], R, h)

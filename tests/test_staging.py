@@ -1,0 +1,220 @@
+"""CPU tests of the retrieval feed's degrade paths and staging-slot reuse.
+
+The reference degrades without failing when a copy is late (no inject; the
+held slot stays, controller.py:401-412), when the previous search still runs
+(no launch, controller.py:333-335) and when the cold store is empty (no
+search, controller.py:324-326, 307-309).  KVController's device primitives
+(event query, host-to-device copy, stream ordering, device buffers) are
+replaced here by host stand-ins, so the state machine runs without a GPU and
+a copy can be held "not ready" for as long as a test wants.
+"""
+
+import torch
+
+from hotcold_kv.controller import KVController, _Slot
+from hotcold_kv.datatypes import EvictedKV
+
+HK, D = 2, 16
+
+
+class _Event:
+    """Completes after `polls` queries (never when polls is None)."""
+
+    def __init__(self, polls=0):
+        self.polls = polls
+
+    def done(self):
+        if self.polls is None:
+            return False
+        if self.polls > 0:
+            self.polls -= 1
+            return False
+        return True
+
+
+class HostCtrl(KVController):
+    """KVController with host stand-ins for its device primitives."""
+
+    def __init__(self, **kw):
+        kw.setdefault("profile_overlap", False)
+        super().__init__(**kw)
+        self.copy_polls = 0          # queries each new copy needs before it completes
+        self.log = []
+
+    def _event_done(self, ev):
+        return ev.done()
+
+    def _alloc_dev(self, slot, device):
+        slot.dev = tuple(t.clone() for t in slot.host)
+
+    def _copy_to_device(self, slot):
+        if slot.released:
+            self.log.append(("wait_free", id(slot)))
+        for d, h in zip(slot.dev, slot.host):
+            d.copy_(h)
+        slot.ready = _Event(self.copy_polls)
+        slot.copied = True
+        self.log.append(("copy", id(slot)))
+
+    def _order_after(self, slot):
+        self.log.append(("order", id(slot)))
+
+    def _mark_released(self, slot):
+        slot.free_after = _Event(0)
+        slot.released = True
+        self.log.append(("released", id(slot)))
+
+
+def _ctrl(**kw):
+    args = dict(cpu_buffer_size=64, faiss_dim=D, lookahead_k=4, window_size=4, hold_retrieved=True)
+    args.update(kw)
+    ctrl = HostCtrl(**args)
+    ctrl._lazy_init(torch.zeros(1, HK, 1, D), n_layers=1)
+    ctrl._stream = "side"            # a stream handle: enables the staging path
+    return ctrl
+
+
+def _fill(ctrl, n=12, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    keys = torch.randn(n, HK, D, generator=g)
+    ctrl.add_evicted_to_cold_store(0, EvictedKV(
+        k_pre_cpu=keys.permute(1, 0, 2).unsqueeze(0).contiguous(),
+        v_cpu=(-keys).permute(1, 0, 2).unsqueeze(0).contiguous(),
+        pos_cpu=torch.arange(100, 100 + n, dtype=torch.long).unsqueeze(0),
+        evicted_idx=torch.arange(n, dtype=torch.long).unsqueeze(0)))
+
+
+def _window(ctrl):
+    """Run one retrieval period (window_size scheduled calls); the search
+    runs synchronously."""
+    ctrl.update_query_window(0, torch.randn(1, 4, 1, D))
+    for _ in range(ctrl.window_size):
+        ctrl.maybe_launch_async_retrieval(0)
+        ctrl.wait_for_retrieval(0)
+
+
+def _step(ctrl):
+    """One decode step of the patched attention's feed: copy a finished
+    retrieval, poll, inject (here: nothing to write), resolve the held slot."""
+    ctrl.maybe_prefetch_to_gpu(0, "cuda")
+    rr = ctrl.poll_staged_gpu(0)
+    injected = None
+    if rr.ready:
+        ctrl.staged_consumed(0)
+        injected = (rr.pos, rr.valid, int(rr.k_pre.shape[2]))
+    return rr, ctrl.resolve_held(0, injected)
+
+
+def test_empty_store_skips_retrieval():
+    ctrl = _ctrl()
+    _window(ctrl)
+    assert ctrl.dbg["retrieval_skipped_no_cold"] == 1
+    assert ctrl.dbg["retrieval_launched"] == 0
+    rr, held = _step(ctrl)
+    assert not rr.ready and held is None
+    ctrl.launch_retrieval_now(0, torch.randn(1, 4, 1, D))     # the prefill-time search too
+    assert ctrl.dbg["retrieval_skipped_no_cold"] == 2
+
+
+def test_live_worker_skips_launch():
+    ctrl = _ctrl()
+    _fill(ctrl)
+
+    class Alive:
+        def is_alive(self):
+            return True
+
+        def join(self, timeout=None):
+            pass
+
+    ctrl._retrieval_thread[0] = Alive()
+    _window(ctrl)
+    assert ctrl.dbg["retrieval_launched"] == 0          # the running search is not doubled
+    ctrl._retrieval_thread[0] = None
+    _window(ctrl)
+    assert ctrl.dbg["retrieval_launched"] == 1
+    assert ctrl._retrieval_ready_cpu[0] is not None
+
+
+def test_late_copy_keeps_the_previous_held_slot():
+    ctrl = _ctrl()
+    _fill(ctrl)
+    _window(ctrl)
+    rr, held = _step(ctrl)                    # first retrieval lands at once
+    assert rr.ready and held is not None
+    first = held
+    assert ctrl.held_mem[0] is first and ctrl.last_injected_len == 4
+
+    ctrl.copy_polls = None                    # the next copy never completes
+    _window(ctrl)
+    for i in range(3):
+        rr, held = _step(ctrl)
+        assert not rr.ready
+        assert held is first                  # decode keeps attending the previous slot
+        assert ctrl.dbg["prefetch_not_ready_checks"] == i + 1
+    assert ctrl.dbg["injection_new"] == 1
+    assert ctrl.dbg["injection_used"] == 4
+
+
+def test_no_hold_attends_a_retrieval_only_when_it_lands():
+    ctrl = _ctrl(hold_retrieved=False)
+    _fill(ctrl)
+    _window(ctrl)
+    rr, held = _step(ctrl)
+    assert rr.ready and held is not None
+    rr, held = _step(ctrl)
+    assert not rr.ready and held is None
+
+
+def test_superseded_copy_is_recycled_without_waiting():
+    ctrl = _ctrl()
+    _fill(ctrl)
+    ctrl.copy_polls = None                    # copies never complete
+    _window(ctrl)
+    ctrl.maybe_prefetch_to_gpu(0, "cuda")
+    first = ctrl._staged[0]
+    _window(ctrl)
+    ctrl.maybe_prefetch_to_gpu(0, "cuda")     # supersedes the first, which was never polled
+    assert ctrl.dbg["prefetch_superseded"] == 1
+    assert ctrl._staged[0] is not first and first.state == _Slot.FREE
+    # its copy is still running: a new search must not take its host buffers
+    with ctrl._retrieval_lock[0]:
+        taken = ctrl._take_slot(0)
+    assert taken is not first
+    taken.state = _Slot.FREE
+    first.ready = _Event(0)                   # now the old copy completes
+    with ctrl._retrieval_lock[0]:
+        assert ctrl._take_slot(0) is first
+
+
+def test_slots_are_reused_and_a_held_slot_is_released_before_its_next_copy():
+    ctrl = _ctrl()
+    _fill(ctrl)
+    seen = set()
+    for period in range(6):
+        _window(ctrl)
+        rr, held = _step(ctrl)
+        assert rr.ready
+        seen.add(id(ctrl._held_slot[0]))
+    assert len(ctrl._slots[0]) <= 2           # held + the one in flight, allocated once
+    assert len(seen) == 2
+    # every copy into a slot that was held before waited for its release
+    released = set()
+    for kind, sid in ctrl.log:
+        if kind == "released":
+            released.add(sid)
+        if kind == "copy" and sid in released:
+            assert ("wait_free", sid) in ctrl.log
+
+
+def test_busy_slots_skip_the_search():
+    ctrl = _ctrl()
+    _fill(ctrl)
+    ctrl.copy_polls = None
+    for sl in range(KVController.MAX_SLOTS):
+        _window(ctrl)
+        ctrl.maybe_prefetch_to_gpu(0, "cuda")
+    before = ctrl.dbg["retrieval_launched"]
+    _window(ctrl)                             # every slot has a copy in flight
+    assert ctrl.dbg["retrieval_skipped_no_slot"] == 1
+    assert ctrl.dbg["retrieval_launched"] == before
