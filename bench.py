@@ -463,21 +463,27 @@ def measure_config(w, dev, flush, reps=24):
                      "frac": round(gbps / HBM_PEAK_GBS, 4), "layers_per_launch": w.layers}
 
     # -- inject: staged fp32 held slot of every layer -> re-RoPE into the hot buffers --------
-    inv = synthetic.inv_freq(D, w.theta).to(dev)
+    # (rotary tables at the held positions in the cache dtype, as the search
+    # thread ships them with a retrieval)
+    inv = synthetic.inv_freq(D, w.theta)
     kp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).pin_memory()
     vp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).pin_memory()
     kp_dev = torch.empty_like(kp_host, device=dev)
     vp_dev = torch.empty_like(vp_host, device=dev)
     kp_dev.copy_(kp_host)
     vp_dev.copy_(vp_host)
+    cos_t, sin_t = ops.rope_tables(held_pos.cpu().reshape(-1, R), inv, 1.0, dt)
+    cos_t = cos_t.reshape(LB, Hk, R, D // 2).to(dev)
+    sin_t = sin_t.reshape(LB, Hk, R, D // 2).to(dev)
 
     def inject(i):
-        ops.inject_rerope(kp_dev, vp_dev, held_pos, inv, 1.0, k_hot, v_hot)
+        ops.inject_rerope_tab(kp_dev, vp_dev, cos_t, sin_t, k_hot, v_hot)
 
     with torch.cuda.stream(st):
         inject(0)
     inj_ms = differential_ms(st, flush, inject, reps)
-    inj_bytes = 2 * LB * Hk * R * D * (4 + es) + LB * Hk * R * 8
+    # staged K and V read in fp32, both tables read, K and V written in the cache dtype
+    inj_bytes = 2 * LB * Hk * R * D * 4 + LB * Hk * R * D * es + 2 * LB * Hk * R * D * es
     side = torch.cuda.Stream(dev)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -501,6 +507,7 @@ def measure_config(w, dev, flush, reps=24):
     torch.cuda.synchronize()
     out["inject"] = {"rerope_us_all_layers": round(inj_ms * 1e3, 2), "rerope_bytes": int(inj_bytes),
                      "rerope_GBps": round(inj_bytes / (inj_ms * 1e-3) / 1e9, 1),
+                     "rerope_frac": round(inj_bytes / (inj_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
                      "h2d_us_all_layers": round(h2d_ms * 1e3, 1), "h2d_bytes": int(h2d_bytes),
                      "h2d_GBps": round(h2d_bytes / (h2d_ms * 1e-3) / 1e9, 1),
                      "decode_launch_us_with_concurrent_h2d": round(ov_ms * 1e3, 2)}

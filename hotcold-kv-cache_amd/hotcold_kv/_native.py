@@ -168,6 +168,14 @@ SIGNATURES = {
         _vp, _i64, _i64, _i64,
         _vp, _i64, _i64, _i64,
         _vp]),
+    "hc_inject_rerope_tab": (_int, [
+        _int, _i64, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp, _i64, _i64, _i64,
+        _vp]),
     "hc_stream_create": (_int, [ctypes.POINTER(_vp)]),
     "hc_stream_destroy": (_int, [_vp]),
     "hc_event_create": (_int, [ctypes.POINTER(_vp), _int]),

@@ -39,6 +39,7 @@ import torch
 
 from . import _native as N
 from .datatypes import EvictedKV, RetrievedKV, _canon_br_2d, _canon_kv_4d
+from .ops import rope_tables as ops_rope_tables
 from .ops import stream_handle as ops_stream
 
 
@@ -108,6 +109,9 @@ class _Slot:
 
     def __init__(self, host):
         self.host = host            # (kpre, v, pos, valid) pinned host tensors
+        self.tab_host = None        # pinned rotary tables (cos, sin) at pos, cache dtype
+        self.tab_dev = None
+        self.has_tab = False        # the tables were computed for this retrieval
         self.qhost = None           # pinned pooled query of the search it serves
         self.q_ready = None         # event behind the query's copy
         self.dev = None             # device twins, allocated on the first copy
@@ -190,6 +194,8 @@ class KVController:
 
         self._inited = False
         self.B = self.Hk = self.D = self.n_layers = None
+        self.dtype = None
+        self._rope = None           # (inv_freq fp32 CPU, attention_scaling) of the model's rotary module
         self.rings = []
         self.step_count = []
         self.query_window = []
@@ -238,6 +244,7 @@ class KVController:
             return
         B, Hk, _, D = k_pre.shape
         self.B, self.Hk, self.D = int(B), int(Hk), int(D)
+        self.dtype = k_pre.dtype
         self.n_layers = L = int(n_layers)
         vec_heads = self.Hk if self.per_head_retrieval else 1
         self.rings = [[_Ring(self.cpu_buffer_size, self.Hk, self.D, self.faiss_dim, vec_heads,
@@ -279,6 +286,13 @@ class KVController:
                 lib.hc_stream_destroy(self._stream)
         except Exception:
             pass
+
+    def set_rope(self, inv_freq, attention_scaling):
+        """The model's rotary parameters (LlamaRotaryEmbedding.inv_freq and
+        attention_scaling): with them every retrieval carries the rotary
+        tables of its positions, computed on the search thread, and the inject
+        writes apply_rotary_pos_emb's exact bits."""
+        self._rope = (inv_freq.detach().float().cpu().contiguous(), float(attention_scaling))
 
     def evict_staging(self, device, B, H, te, D):
         """Device and pinned host staging blocks of at least
@@ -431,6 +445,9 @@ class KVController:
             return None
         pin = torch.cuda.is_available()
         sl = _Slot(tuple(torch.empty(shape, dtype=dt, pin_memory=pin) for shape, dt in self._slot_shapes()))
+        hc = self.Hk if self.per_head_retrieval else 1
+        tshape = (self.B, hc, self.lookahead_k, self.D // 2)
+        sl.tab_host = tuple(torch.empty(tshape, dtype=self.dtype, pin_memory=pin) for _ in range(2))
         sl.state = _Slot.FILLING
         self._slots[li].append(sl)
         return sl
@@ -459,6 +476,14 @@ class KVController:
         N.check(N.lib().hc_cold_retrieve(stores, B, q.ctypes.data, q.shape[1] * self.faiss_dim, self.faiss_dim, R,
                                          int(self.per_head_retrieval), kpre.data_ptr(), vv.data_ptr(),
                                          pos.data_ptr(), valid.data_ptr(), int(nthreads)), "hc_cold_retrieve")
+        rope = self._rope
+        slot.has_tab = rope is not None
+        if rope is not None:
+            # the tables of LlamaRotaryEmbedding.forward at the retrieved
+            # positions (rows past the hits hold position 0 and stay masked)
+            cos, sin = ops_rope_tables(pos.reshape(-1, R), rope[0], rope[1], self.dtype)
+            slot.tab_host[0].view(-1, R, self.D // 2).copy_(cos)
+            slot.tab_host[1].view(-1, R, self.D // 2).copy_(sin)
         with self._retrieval_lock[li]:
             if not bool(valid.any()):
                 slot.state = _Slot.FREE
@@ -551,6 +576,7 @@ class KVController:
 
     def _alloc_dev(self, slot, device):
         slot.dev = tuple(torch.empty(t.shape, dtype=t.dtype, device=device) for t in slot.host)
+        slot.tab_dev = tuple(torch.empty(t.shape, dtype=t.dtype, device=device) for t in slot.tab_host)
 
     def _copy_to_device(self, slot):
         """The slot's host-to-device copies on the side stream, after the
@@ -565,7 +591,10 @@ class KVController:
             N.check(lib.hc_stream_wait_event(self._stream, slot.free_after), "hc_stream_wait_event")
         if slot.t0 is not None:
             N.check(lib.hc_event_record(slot.t0, self._stream), "hc_event_record")
-        for d, h in zip(slot.dev, slot.host):
+        pairs = list(zip(slot.dev, slot.host))
+        if slot.has_tab:
+            pairs += list(zip(slot.tab_dev, slot.tab_host))
+        for d, h in pairs:
             N.check(lib.hc_memcpy_h2d_async(d.data_ptr(), h.data_ptr(), h.numel() * h.element_size(), self._stream),
                     "hc_memcpy_h2d_async")
         if slot.t1 is not None:
@@ -650,10 +679,15 @@ class KVController:
         kpre, vv, pos, valid = slot.dev
         kpre = _canon_kv_4d(kpre, "staged.k_pre")
         vv = _canon_kv_4d(vv, "staged.v")
+        cos = sin = None
+        if slot.has_tab:
+            cos, sin = slot.tab_dev
+            if not self.per_head_retrieval:
+                cos, sin = cos[:, 0], sin[:, 0]
         if not self.per_head_retrieval:
             pos = _canon_br_2d(pos, "staged.pos")
             valid = _canon_br_2d(valid, "staged.valid")
-        return RetrievedKV(k_pre=kpre, v=vv, pos=pos, valid=valid, ready=True)
+        return RetrievedKV(k_pre=kpre, v=vv, pos=pos, valid=valid, ready=True, cos=cos, sin=sin)
 
     def staged_consumed(self, layer_idx):
         """The staging just returned by poll_staged_gpu has been injected on

@@ -44,6 +44,11 @@ class RetrievedKV:
     pos: torch.Tensor
     valid: torch.Tensor
     ready: bool = False
+    # rotary tables at pos, first D/2 dims in the cache dtype ((B,R,D/2) or
+    # (B,Hk,R,D/2)), computed with the retrieval when the rotary parameters
+    # are known; None otherwise (not fields of the reference)
+    cos: torch.Tensor = None
+    sin: torch.Tensor = None
 
 
 @dataclass

@@ -872,5 +872,58 @@ def inject_rerope(k_pre_f32, v_f32, pos, inv_freq, attention_scaling, k_dst, v_d
     N.check(rc, "hc_inject_rerope")
 
 
+def rope_tables(pos, inv_freq, attention_scaling, dtype):
+    """The rotary tables of LlamaRotaryEmbedding.forward at positions pos
+    (N,R) int64, computed as it does (inv_freq @ pos in fp32, cos/sin of the
+    duplicated frequencies, times attention_scaling, rounded to dtype) on the
+    tensors' device; returns the first halves (N,R,D/2) of cos and sin."""
+    pos = pos.long()
+    inv = inv_freq.float()
+    inv_exp = inv[None, :, None].expand(pos.shape[0], -1, 1)
+    freqs = (inv_exp @ pos[:, None, :].float()).transpose(1, 2)
+    emb = torch.cat((freqs, freqs), dim=-1)
+    half = inv.numel()
+    cos = (emb.cos() * attention_scaling).to(dtype)
+    sin = (emb.sin() * attention_scaling).to(dtype)
+    return cos[..., :half], sin[..., :half]
+
+
+def inject_rerope_tab(k_pre_f32, v_f32, cos_t, sin_t, k_dst, v_dst):
+    """inject_rerope with the rotary tables supplied: cos_t / sin_t (B,R,D/2)
+    (one table per batch row) or (B,Hk,R,D/2), in k_dst's dtype (rope_tables).
+    Writes the rotated keys and the values into rows 0..R-1 of k_dst / v_dst
+    (B,Hk,cap,D); the keys are apply_rotary_pos_emb's bits."""
+    _require_device(k_pre_f32, v_f32, cos_t, sin_t, k_dst, v_dst)
+    B, Hk, R, D = k_pre_f32.shape
+    if k_pre_f32.dtype != torch.float32 or v_f32.dtype != torch.float32:
+        raise RuntimeError("inject_rerope_tab: staged k_pre/v must be float32")
+    if cos_t.dtype != k_dst.dtype or sin_t.dtype != k_dst.dtype or cos_t.shape != sin_t.shape \
+            or cos_t.stride() != sin_t.stride():
+        raise RuntimeError("inject_rerope_tab: cos/sin tables must share shape, strides and the cache dtype")
+    if cos_t.dim() == 3 and tuple(cos_t.shape) == (B, R, D // 2):
+        cs_sb, cs_sh, cs_ss = cos_t.stride(0), 0, cos_t.stride(1)
+    elif cos_t.dim() == 4 and tuple(cos_t.shape) == (B, Hk, R, D // 2):
+        cs_sb, cs_sh, cs_ss = cos_t.stride(0), cos_t.stride(1), cos_t.stride(2)
+    else:
+        raise RuntimeError(f"inject_rerope_tab: tables {tuple(cos_t.shape)} must be (B,R,D/2) or (B,Hk,R,D/2)")
+    if cos_t.stride(-1) != 1:
+        raise RuntimeError("inject_rerope_tab: tables need a unit last stride")
+    for d, name in ((k_dst, "k_dst"), (v_dst, "v_dst")):
+        if d.dim() != 4 or d.shape[0] != B or d.shape[1] != Hk or d.shape[2] < R or d.shape[3] != D \
+                or d.stride(-1) != 1:
+            raise RuntimeError(f"inject_rerope_tab: {name} {tuple(d.shape)} cannot hold {R} rows of ({B},{Hk},*,{D})")
+    if tuple(v_f32.shape) != (B, Hk, R, D) or k_pre_f32.stride(-1) != 1 or v_f32.stride(-1) != 1:
+        raise RuntimeError("inject_rerope_tab: staged k_pre/v must be (B,Hk,R,D) with unit last stride")
+    rc = N.lib().hc_inject_rerope_tab(
+        N.dtype_code(k_dst.dtype), B, Hk, R, D,
+        _ptr(k_pre_f32), *_strides3(k_pre_f32),
+        _ptr(v_f32), *_strides3(v_f32),
+        _ptr(cos_t), _ptr(sin_t), cs_sb, cs_sh, cs_ss,
+        _ptr(k_dst), *_strides3(k_dst),
+        _ptr(v_dst), *_strides3(v_dst),
+        stream_handle(k_dst.device))
+    N.check(rc, "hc_inject_rerope_tab")
+
+
 def default_scaling(head_dim):
     return 1.0 / math.sqrt(head_dim)

@@ -56,10 +56,13 @@ def _rotate_k_with_pos(k_pre, pos_ids, head_dim=None):
     k_pre = _canon_kv_4d(k_pre, "k_pre")
     B, Hk, R, D = k_pre.shape
     inv, scale = _rope_params(k_pre.device)
+    pos = pos_ids.long()
+    cos, sin = ops.rope_tables(pos.reshape(-1, R), inv, scale, k_pre.dtype)    # the rotary module's tables
+    shape = (B, Hk, R, D // 2) if pos.dim() == 3 else (B, R, D // 2)
     out_k = torch.empty((B, Hk, R, D), dtype=k_pre.dtype, device=k_pre.device)
     out_v = torch.empty_like(out_k)
-    ops.inject_rerope(k_pre.float(), torch.zeros_like(k_pre, dtype=torch.float32), pos_ids.long(), inv, scale,
-                      out_k, out_v)
+    ops.inject_rerope_tab(k_pre.float().contiguous(), torch.zeros_like(k_pre, dtype=torch.float32),
+                          cos.reshape(shape).contiguous(), sin.reshape(shape).contiguous(), out_k, out_v)
     return out_k
 
 
@@ -76,6 +79,8 @@ def hotcold_attention(kvctrl, layer, li, q_pre, k_pre, v, q_post, k_post, pos_ne
     through HotColdLayer.update (which may compress and evict), then attend."""
     q_len = int(q_pre.shape[2])
     device = q_pre.device
+    if kvctrl._rope is None and ACTIVE_ROTARY_EMB is not None:
+        kvctrl.set_rope(ACTIVE_ROTARY_EMB.inv_freq, getattr(ACTIVE_ROTARY_EMB, "attention_scaling", 1.0))
 
     # retrieval pipeline (patch.py:164-172)
     if q_len == 1 or kvctrl.query_pool_size >= kvctrl.window_size:
@@ -106,8 +111,11 @@ def hotcold_attention(kvctrl, layer, li, q_pre, k_pre, v, q_post, k_post, pos_ne
         if rr.ready:
             kbuf, vbuf = layer.buf.held_storage()
             R = int(rr.k_pre.shape[2])
-            inv, ascale = _rope_params(device)
-            ops.inject_rerope(rr.k_pre, rr.v, rr.pos, inv, ascale, kbuf, vbuf)
+            if rr.cos is not None:
+                ops.inject_rerope_tab(rr.k_pre, rr.v, rr.cos, rr.sin, kbuf, vbuf)
+            else:
+                inv, ascale = _rope_params(device)
+                ops.inject_rerope(rr.k_pre, rr.v, rr.pos, inv, ascale, kbuf, vbuf)
             kvctrl.staged_consumed(li)
             injected = (rr.pos, rr.valid, R)
         held = kvctrl.resolve_held(li, injected)

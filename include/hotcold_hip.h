@@ -364,6 +364,24 @@ int hc_inject_rerope(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D,
                      void* stream);
 
 /*
+ * hc_inject_rerope with the rotary tables supplied: cos_t / sin_t hold
+ * dtype(fp32(cos/sin(angle)) * scaling) -- what the model's rotary module
+ * returns for the held positions (_rope_cos_sin_for_positions,
+ * patch.py:76-91) -- for the first D/2 dims (the second half repeats them),
+ * as [B][Hk or 1][R][D/2] in dtype with element strides (cs_sb, cs_sh, cs_ss);
+ * cs_sh = 0 shares one table across the KV heads of a batch row.  With the
+ * tables given, every written key is apply_rotary_pos_emb's bits
+ * (patch.py:94-102).  Staged rows 16-byte aligned, D a multiple of 8.
+ */
+int hc_inject_rerope_tab(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D,
+                         const float* k_pre, int64_t kp_sb, int64_t kp_sh, int64_t kp_ss,
+                         const float* v, int64_t vp_sb, int64_t vp_sh, int64_t vp_ss,
+                         const void* cos_t, const void* sin_t, int64_t cs_sb, int64_t cs_sh, int64_t cs_ss,
+                         void* k_dst, int64_t kd_sb, int64_t kd_sh, int64_t kd_ss,
+                         void* v_dst, int64_t vd_sb, int64_t vd_sh, int64_t vd_ss,
+                         void* stream);
+
+/*
  * Staging primitives for the inject feed (controller.py:344-442): a library
  * side stream created hipStreamNonBlocking at default priority, pinned
  * host->device copies on it, and events that the consumer polls (never waits

@@ -401,3 +401,22 @@ def test_canon_shapes():
         _canon_br_2d(torch.zeros(2, 3, 4), "pos")
     with pytest.raises(RuntimeError):
         _canon_br_2d([1, 2], "pos")
+
+
+# ---------------------------------------------------------------------------
+# Rotary tables shipped with a retrieval (the inject's cos/sin)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+def test_rope_tables_are_the_rotary_modules_tables(dtype):
+    """ops.rope_tables (run on the search thread) gives the first halves of
+    LlamaRotaryEmbedding.forward's cos/sin (the oracle restates it), llama3
+    frequencies and an attention scaling included."""
+    g = torch.Generator().manual_seed(5)
+    pos = torch.randint(0, 1 << 17, (6, 40), generator=g)
+    for inv, scale in ((ref.default_inv_freq(128, 500000.0), 1.0),
+                       (ref.default_inv_freq(64, 10000.0) * 0.25, 1.0625)):
+        cos, sin = ops.rope_tables(pos, inv, scale, dtype)
+        wc, ws = ref.rotary_cos_sin(inv, scale, pos, dtype)
+        half = inv.numel()
+        assert torch.equal(cos, wc[..., :half]) and torch.equal(sin, ws[..., :half])
+        assert torch.equal(wc[..., :half], wc[..., half:])      # the second half repeats the first

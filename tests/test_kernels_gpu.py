@@ -633,6 +633,27 @@ def test_gather_evict_upcast_and_stage(dtype, to_host):
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("per_head", [False, True])
+def test_inject_rerope_tab_is_bit_exact(dtype, per_head):
+    """With the rotary tables computed as the model's rotary module computes
+    them (ops.rope_tables), the inject writes apply_rotary_pos_emb's bits."""
+    B, Hk, R, D, cap = 2, 8, 64, 128, 100
+    k_pre = _randn((B, Hk, R, D), 71, torch.float32, scale=3.0)
+    v = _randn((B, Hk, R, D), 72, torch.float32)
+    g = torch.Generator().manual_seed(73)
+    pos = torch.randint(0, 1 << 17, (B, Hk, R) if per_head else (B, R), generator=g)
+    inv = ref.default_inv_freq(D, 500000.0)
+    cos, sin = ops.rope_tables(pos.reshape(-1, R), inv, 1.0, dtype)       # on the host, like the search thread
+    shape = (B, Hk, R, D // 2) if per_head else (B, R, D // 2)
+    kd = torch.zeros((B, Hk, cap, D), dtype=dtype, device=DEV)
+    vd = torch.zeros_like(kd)
+    ops.inject_rerope_tab(k_pre.to(DEV), v.to(DEV), cos.reshape(shape).to(DEV), sin.reshape(shape).to(DEV), kd, vd)
+    assert torch.equal(kd[:, :, :R].cpu(), ref.rerope(k_pre, pos, inv, 1.0, dtype))
+    assert torch.equal(vd[:, :, :R].cpu(), v.to(dtype))
+    assert torch.count_nonzero(kd[:, :, R:]) == 0 and torch.count_nonzero(vd[:, :, R:]) == 0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("per_head", [False, True])
 def test_inject_rerope_matches_model_rotation(dtype, per_head):
     B, Hk, R, D, cap = 2, 8, 64, 128, 100
     k_pre = _randn((B, Hk, R, D), 61, torch.float32)
