@@ -388,6 +388,27 @@ def profiled_traffic(workload):
     return int(m.group(1)) if m else None
 
 
+def read_floor_ms(dev, nbytes, st, flush, reps=24):
+    """ms of a plain streaming read of nbytes (hc_read_bytes: 16-byte loads
+    over 1024 workgroups) after the same cache sweep, differential timing:
+    what a kernel that only reads the decode's bytes takes here."""
+    import torch
+    from hotcold_kv import _native as N
+    nbytes = (int(nbytes) + 15) // 16 * 16
+    buf = torch.ones(nbytes // 2, dtype=torch.float16, device=dev)
+    lib = N.lib()
+
+    def read(i):
+        N.check(lib.hc_read_bytes(buf.data_ptr(), nbytes, None, torch.cuda.current_stream(dev).cuda_stream),
+                "hc_read_bytes")
+
+    with torch.cuda.stream(st):
+        read(0)
+    ms = differential_ms(st, flush, read, reps)
+    del buf
+    return ms
+
+
 def differential_ms(st, flush, fn, reps, warmup=3):
     """ms of fn() measured as events around [sweep; fn] minus events around
     [sweep] alone (see run_steps), as the difference of the two medians
@@ -807,6 +828,10 @@ def main():
     log(f"decode {nbytes / 1e6:.1f} MB/launch -> {achieved:.0f} GB/s; compaction {cbytes / 1e6:.0f} MB -> "
         f"{c_achieved:.0f} GB/s, scoring {sflops / (comp_ms * 1e-3) / 1e12:.2f} TFLOP/s fp64")
 
+    floor_ms = read_floor_ms(dev, nbytes, s.stream, flush)
+    log(f"plain read of the same {nbytes / 1e6:.1f} MB after the same sweep: {floor_ms * 1e3:.2f} us "
+        f"({nbytes / (floor_ms * 1e-3) / 1e9:.0f} GB/s); decode at {floor_ms / dec_ms:.3f} of it")
+
     # warm-cache decode and the per-layer-launch schedule (last decode step)
     warm_dec_ms = time_graph(s.g_dec20, s.stream, 5) / 20
     pl_cold_ms = time_graph(s.g_pl, s.stream, 20, flush)
@@ -891,7 +916,11 @@ def main():
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(w.name),
                      "kernel": "decode_attn_kernel (fused append; unsplit at this size, so no merge kernel)",
                      "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3),
-                     "launch_timing": "events around [cache sweep; decode] minus events around [cache sweep]"},
+                     "launch_timing": "events around [cache sweep; decode] minus events around [cache sweep]",
+                     "read_floor_us": round(floor_ms * 1e3, 3),
+                     "read_floor_frac": round(nbytes / (floor_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "frac_of_read_floor": round(floor_ms / dec_ms, 4),
+                     "read_floor": "hc_read_bytes over the same byte count after the same sweep, same timing"},
         # the exact-score contract computes the window logits in fp64 on the
         # matrix cores: compaction is bound by the fp64 MFMA rate, not by HBM
         "roofline_compaction": {"bound": "mfma", "dtype": "f64",

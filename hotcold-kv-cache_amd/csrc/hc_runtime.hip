@@ -9,6 +9,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+
 #include "hc_common.h"
 
 namespace hc {
@@ -43,9 +45,31 @@ static int hip_rc(hipError_t e, const char* what) {
   return set_error(HC_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+// Calibration read: every 16-byte piece of [p, p + 16*n16) loaded once by a
+// grid-stride loop and folded into a value that is never written unless it
+// equals an arbitrary constant (so the loads cannot be removed).
+__global__ __launch_bounds__(256) void read_bytes_kernel(const u32x4* __restrict__ p, int64_t n16,
+                                                         uint32_t* __restrict__ sink) {
+  u32x4 acc = {0u, 0u, 0u, 0u};
+  const int64_t step = (int64_t)gridDim.x * 256;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += step) acc ^= p[i];
+  if ((acc[0] ^ acc[1] ^ acc[2] ^ acc[3]) == 0x9e3779b9u && sink != nullptr) sink[threadIdx.x] = acc[0];
+}
+
 }  // namespace hc
 
 using namespace hc;
+
+extern "C" int hc_read_bytes(const void* p, int64_t bytes, uint32_t* sink, void* stream) {
+  HC_REQUIRE(p && bytes >= 0 && bytes % 16 == 0 && ((uintptr_t)p % 16) == 0,
+             "read_bytes: 16-byte aligned pointer and size required");
+  if (bytes == 0) return HC_OK;
+  const int64_t n16 = bytes / 16;
+  const int64_t blocks = std::min<int64_t>(1024, cdiv(n16, (int64_t)256));
+  hipLaunchKernelGGL(read_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, reinterpret_cast<hipStream_t>(stream),
+                     reinterpret_cast<const u32x4*>(p), n16, sink);
+  return check_launch("read_bytes");
+}
 
 extern "C" int hc_abi_version(void) { return 1; }
 

@@ -43,6 +43,7 @@ _dbl = ctypes.c_double
 SIGNATURES = {
     "hc_abi_version": (_int, []),
     "hc_last_error": (ctypes.c_char_p, []),
+    "hc_read_bytes": (_int, [_vp, _i64, _vp, _vp]),
     "hc_decode_attn_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i64, _i64, _int]),
     "hc_decode_attn": (_int, [
         _int, _i64, _i64, _i64, _i64, _i64,

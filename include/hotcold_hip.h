@@ -48,6 +48,13 @@ extern "C" {
 int hc_abi_version(void);
 const char* hc_last_error(void);
 
+/* Calibration read (no counterpart in the reference): stream `bytes` (a
+ * multiple of 16) from the 16-byte aligned device pointer p once, with
+ * 16-byte loads over up to 1024 workgroups, writing nothing (sink may be
+ * NULL).  The benchmark times it on the decode's byte count as the plain-read
+ * floor the decode kernel is compared with. */
+int hc_read_bytes(const void* p, int64_t bytes, uint32_t* sink, void* stream);
+
 /*
  * GQA decode attention over the hot buffer (+ held retrieved slot), split-K.
  * Replaces evict_fwd_kernel + triton_evict_attention_forward
