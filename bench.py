@@ -687,6 +687,7 @@ def hotcold_pipeline(w, dev, profile_steps=None):
     for l in range(L):
         ctrl.wait_for_retrieval(l)
     d = ctrl.dbg
+    sl = ctrl._slots[0][0]
     retr_steps = [t for t in range(steps) if (t + 1) % w.retrieve_every in (0, 1)]
     other = [step_ms[t] for t in range(steps) if t not in retr_steps]
     out = {
@@ -705,7 +706,9 @@ def hotcold_pipeline(w, dev, profile_steps=None):
         "prefetch_not_ready_checks": d["prefetch_not_ready_checks"],
         "injections": d["injection_new"], "held_decodes": d["injection_used"],
         "copy_ms_mean": round(d["prefetch_copy_ms_sum"] / max(1, d["prefetch_copy_ms_count"]), 4),
-        "h2d_bytes_per_copy": 2 * B * w.hk * w.held * w.head_dim * 4 + 2 * B * w.hk * w.held * 8,
+        "h2d_bytes_per_copy": sl.nbytes[1] if sl.has_tab else sl.nbytes[0],
+        "h2d_copy": "one hipMemcpyAsync per retrieval from the slot's pinned block: fp32 k_pre and v, "
+                    "int64 positions, valid flags, the rotary tables at the positions",
     }
     del layers, ctrl, toks
     torch.cuda.synchronize()
@@ -713,53 +716,86 @@ def hotcold_pipeline(w, dev, profile_steps=None):
     return out
 
 
+def cpu_model():
+    """The host CPU's model string (/proc/cpuinfo), or the platform's name."""
+    import platform
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
 def cpu_baseline(w, sample_seconds, n_layers=4):
     """The reference's torch-CPU path (snapkv_importance -> keep_index ->
     gather_kv, then per decode step cat + repeat_kv + SDPA) on a bounded
     sample of the same workload: whole single-layer jobs (compaction of the
-    8k prompt + the decode steps) over the first n_layers layers' inputs,
-    fp32-upcast, repeated until sample_seconds of CPU time have been spent."""
+    prompt + the decode steps) over the first n_layers layers' inputs,
+    repeated until the variant's share of sample_seconds has been spent.
+    Two variants, as the reference's path could run on the CPU: the
+    workload's own dtype (fp16/bf16 CPU matmul, scoring.py:70 as written)
+    and the fp32 upcast.  `value` is the first.
+
+    Threads: os.cpu_count() is recorded, and at most 16 are used -- the
+    host share of one GPU on a shared multi-GPU node."""
     import torch
     from hotcold_kv import synthetic
     from oracle import reference as ref
 
     threads = max(1, min(16, os.cpu_count() or 1))
     torch.set_num_threads(threads)
-    layers = []
+    raw = []
     for l in range(min(n_layers, w.layers)):
         p = synthetic.make_prompt(w, layer=l, seed=0, device="cpu")
         toks = [synthetic.make_decode_token(w, l, t, seed=0, device="cpu") for t in range(w.decode_steps)]
-        layers.append((p["q_post"].float(), p["k_post"].float(), p["v"].float(),
-                       [(t["q_post"].float(), t["k_post"].float(), t["v"].float()) for t in toks]))
-    q, k, v, _ = layers[0]
-    ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)  # warm-up
-    comp, dec = [], []
-    jobs = 0
-    t_end = time.perf_counter() + sample_seconds
-    while jobs < 2 or time.perf_counter() < t_end:
-        q, k, v, toks = layers[jobs % len(layers)]
-        t0 = time.perf_counter()
-        keys, vals = ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)
-        comp.append(time.perf_counter() - t0)
-        for qt, kt, vt in toks:
+        raw.append((p, toks))
+
+    def run(dtype, seconds):
+        layers = [(p["q_post"].to(dtype), p["k_post"].to(dtype), p["v"].to(dtype),
+                   [(t["q_post"].to(dtype), t["k_post"].to(dtype), t["v"].to(dtype)) for t in toks])
+                  for p, toks in raw]
+        q, k, v, _ = layers[0]
+        ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)  # warm-up
+        comp, dec = [], []
+        jobs = 0
+        t_end = time.perf_counter() + seconds
+        while jobs < 2 or time.perf_counter() < t_end:
+            q, k, v, toks = layers[jobs % len(layers)]
             t0 = time.perf_counter()
-            _, keys, vals = ref.press_decode_torch(qt, keys, vals, kt, vt, w.scaling)
-            dec.append(time.perf_counter() - t0)
-        jobs += 1
-    comp_ms_layer = statistics.median(comp) * 1e3
-    dec_us = statistics.median(dec) * 1e6
-    spent = sum(comp) + sum(dec)
+            keys, vals = ref.press_compress_torch(q, k, v, w.window, w.budget, w.scaling, w.pool)
+            comp.append(time.perf_counter() - t0)
+            for qt, kt, vt in toks:
+                t0 = time.perf_counter()
+                _, keys, vals = ref.press_decode_torch(qt, keys, vals, kt, vt, w.scaling)
+                dec.append(time.perf_counter() - t0)
+            jobs += 1
+        comp_ms = statistics.median(comp) * 1e3
+        return {"decode_us_per_layer_step": round(statistics.median(dec) * 1e6, 2),
+                "compact_ms_per_layer": round(comp_ms, 3),
+                "compact_ms_32_layers": round(comp_ms * w.layers, 2),
+                "jobs": jobs, "cpu_seconds": round(sum(comp) + sum(dec), 1)}
+
+    lit_name = str(w.dtype).replace("torch.", "")
+    lit = run(w.dtype, sample_seconds / 2)
+    up = run(torch.float32, sample_seconds / 2)
     return {
-        "value": round(dec_us, 2),
+        "value": lit["decode_us_per_layer_step"],
         "unit": "us/layer-step",
         "cores": threads,
         "kind": "port",
-        "sample": (f"{jobs} single-layer jobs of {w.name} cycling over layers 0-{len(layers) - 1} "
-                   f"({spent:.1f} s of CPU time): each an {w.seq_len}-token SnapKV compaction "
-                   f"(median {comp_ms_layer:.2f} ms; x{w.layers} layers = {comp_ms_layer * w.layers:.1f} ms) and "
-                   f"{w.decode_steps} decode steps (append + SDPA, median value above); fp32-upcast torch CPU "
-                   f"restating scoring.py / layer_state.py"),
-        "compact_ms_32_layers": round(comp_ms_layer * w.layers, 2),
+        "sample": (f"single-layer jobs of {w.name} cycling over layers 0-{len(raw) - 1}: each an "
+                   f"{w.seq_len}-token SnapKV compaction and {w.decode_steps} decode steps (append + SDPA); "
+                   f"median per decode step, {lit_name} torch CPU as the workload's dtype "
+                   f"({lit['jobs']} jobs, {lit['cpu_seconds']} s); compaction x{w.layers} layers "
+                   f"= {lit['compact_ms_32_layers']} ms; the fp32 upcast under variants"),
+        "compact_ms_32_layers": lit["compact_ms_32_layers"],
+        "variants": {f"{lit_name} (workload dtype)": lit, "fp32 upcast": up},
+        "cpu_model": cpu_model(),
+        "os_cpu_count": os.cpu_count(),
+        "threads": threads,
     }
 
 
@@ -878,7 +914,9 @@ def main():
     if not args.no_cpu_baseline:
         log("cpu baseline ...")
         cpu = cpu_baseline(w, args.cpu_sample_seconds)
-        log(f"cpu baseline: {cpu['value']} us/layer-step, compaction {cpu['compact_ms_32_layers']} ms")
+        for name, v in cpu["variants"].items():
+            log(f"cpu baseline {name}: {v['decode_us_per_layer_step']} us/layer-step, compaction "
+                f"{v['compact_ms_32_layers']} ms ({cpu['threads']} threads of {cpu['os_cpu_count']}, {cpu['cpu_model']})")
 
     result = {
         "metric": METRIC,

@@ -101,20 +101,50 @@ class _Ring:
         return d
 
 
+def _block_layout(specs, align=256):
+    """Byte offsets of tensors of the given (shape, dtype) packed into one
+    block, each start aligned to `align`; returns (offsets, (bytes without
+    the last two, total bytes))."""
+    offs, off = [], 0
+    ends = []
+    for shape, dt in specs:
+        off = (off + align - 1) // align * align
+        offs.append(off)
+        off += int(np.prod(shape)) * torch.empty((), dtype=dt).element_size()
+        ends.append(off)
+    return offs, (ends[-3], ends[-1])
+
+
+def _carve(block, specs):
+    """Views of the given (shape, dtype) into a uint8 block laid out by
+    _block_layout."""
+    offs, _ = _block_layout(specs)
+    out = []
+    for (shape, dt), off in zip(specs, offs):
+        n = int(np.prod(shape)) * torch.empty((), dtype=dt).element_size()
+        out.append(block[off:off + n].view(dt).view(shape))
+    return tuple(out)
+
+
 class _Slot:
     """One reusable staging slot of a layer: pinned host buffers (k_pre, v,
-    pos, valid), their device twins, and the events of its copy."""
+    pos, valid, and the rotary tables cos, sin), all views of one pinned
+    block so that a retrieval goes over in one copy; its device twin block;
+    the events of its copy."""
 
     FREE, FILLING, RETRIEVED, COPYING, STAGED, HELD = range(6)
 
-    def __init__(self, host):
+    def __init__(self, host, tab_host=None, block=None, nbytes=(0, 0)):
         self.host = host            # (kpre, v, pos, valid) pinned host tensors
-        self.tab_host = None        # pinned rotary tables (cos, sin) at pos, cache dtype
+        self.tab_host = tab_host    # pinned rotary tables (cos, sin) at pos, cache dtype
+        self.block = block          # the one pinned allocation host and tab_host are views of
+        self.nbytes = nbytes        # bytes of the block without / with the tables
         self.tab_dev = None
         self.has_tab = False        # the tables were computed for this retrieval
         self.qhost = None           # pinned pooled query of the search it serves
         self.q_ready = None         # event behind the query's copy
         self.dev = None             # device twins, allocated on the first copy
+        self.dev_block = None       # the device allocation they are views of
         self.state = _Slot.FREE
         self.ready = None           # event recorded behind the copy
         self.copied = False         # ready has been recorded (a copy was issued)
@@ -264,13 +294,18 @@ class KVController:
             N.check(N.lib().hc_stream_create(ctypes.byref(stream)), "hc_stream_create")
             self._stream = stream.value
         self._inited = True
-        if k_pre.is_cuda and self.lookahead_k > 0:
-            # two staging slots per layer up front (one held, one in flight):
-            # pinned allocations are slow and would otherwise land in decode steps
-            for li in range(L):
-                with self._retrieval_lock[li]:
-                    for _ in range(2):
-                        self._take_slot(li).state = _Slot.FREE
+        if k_pre.is_cuda:
+            self._preallocate_slots()
+
+    def _preallocate_slots(self, n=2):
+        """n staging slots per layer up front (one held, one in flight):
+        pinned allocations are slow and would otherwise land in decode steps."""
+        if self.lookahead_k <= 0:
+            return
+        for li in range(self.n_layers):
+            with self._retrieval_lock[li]:
+                for sl in [self._take_slot(li) for _ in range(n - len(self._slots[li]))]:
+                    sl.state = _Slot.FREE
 
     def __del__(self):
         try:
@@ -427,11 +462,15 @@ class KVController:
         return self._q_to_vecs_np(torch.cat(list(qwin), dim=2))
 
     # -- staging slots ------------------------------------------------------------------
-    def _slot_shapes(self):
+    def _slot_specs(self):
+        """(shape, dtype) of a slot's k_pre, v, pos, valid, cos, sin: the
+        order of their views in the slot's one block (tables last, so a
+        retrieval without them copies a prefix of the block)."""
         B, Hk, D, R = self.B, self.Hk, self.D, self.lookahead_k
         pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
-        return ((B, Hk, R, D), torch.float32), ((B, Hk, R, D), torch.float32), (pshape, torch.int64), \
-            (pshape, torch.bool)
+        tshape = (B, Hk if self.per_head_retrieval else 1, R, D // 2)
+        return (((B, Hk, R, D), torch.float32), ((B, Hk, R, D), torch.float32), (pshape, torch.int64),
+                (pshape, torch.bool), (tshape, self.dtype), (tshape, self.dtype))
 
     def _take_slot(self, li):
         """A free slot of layer li whose last copy has completed (its host
@@ -443,11 +482,11 @@ class KVController:
                 return sl
         if len(self._slots[li]) >= self.MAX_SLOTS:
             return None
-        pin = torch.cuda.is_available()
-        sl = _Slot(tuple(torch.empty(shape, dtype=dt, pin_memory=pin) for shape, dt in self._slot_shapes()))
-        hc = self.Hk if self.per_head_retrieval else 1
-        tshape = (self.B, hc, self.lookahead_k, self.D // 2)
-        sl.tab_host = tuple(torch.empty(tshape, dtype=self.dtype, pin_memory=pin) for _ in range(2))
+        specs = self._slot_specs()
+        nbytes = _block_layout(specs)[1]
+        block = torch.empty(nbytes[1], dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+        views = _carve(block, specs)
+        sl = _Slot(views[:4], views[4:], block, nbytes)
         sl.state = _Slot.FILLING
         self._slots[li].append(sl)
         return sl
@@ -456,16 +495,17 @@ class KVController:
         """Top-lookahead_k tokens per batch row (or per KV head) into a slot's
         pinned host buffers (controller.py:250-293), one native call over all
         rows.  q_vecs None: the slot's pooled query is still being copied to
-        the host; wait for it here, on this thread, then normalise it."""
+        the host; wait for it here, on this thread, then normalise it.
+        Returns False when no search ran (no free slot, not initialised)."""
         li = int(layer_idx)
         if not self._inited:
-            return
+            return False
         if slot is None:
             with self._retrieval_lock[li]:
                 slot = self._take_slot(li)
             if slot is None:
                 self.dbg["retrieval_skipped_no_slot"] += 1
-                return
+                return False
         if q_vecs is None:
             self._wait_event(slot.q_ready)
             q_vecs = self._normalize(self._pad_or_crop(slot.qhost.numpy()))
@@ -488,13 +528,14 @@ class KVController:
             if not bool(valid.any()):
                 slot.state = _Slot.FREE
                 self.dbg["retrieval_ready_empty"] += 1
-                return
+                return True
             old = self._retrieval_ready_cpu[li]
             if old is not None:        # a newer result replaces one never copied
                 old.state = _Slot.FREE
             self._retrieval_ready_cpu[li] = slot
             slot.state = _Slot.RETRIEVED
             self.dbg["retrieval_ready_cpu"] += 1
+        return True
 
     def launch_retrieval_now(self, layer_idx, q_pre):
         """One synchronous retrieval outside the schedule (controller.py:295-312)."""
@@ -504,9 +545,9 @@ class KVController:
         if self.cold_size(li) == 0:
             self.dbg["retrieval_skipped_no_cold"] += 1
             return
-        self._retrieval_worker(li, self._q_to_vecs_np(q_pre))
-        self.dbg["retrieval_launched"] += 1
-        self.dbg["retrieval_launched_prefill"] += 1
+        if self._retrieval_worker(li, self._q_to_vecs_np(q_pre)):
+            self.dbg["retrieval_launched"] += 1
+            self.dbg["retrieval_launched_prefill"] += 1
 
     def maybe_launch_async_retrieval(self, layer_idx):
         """Every window_size calls, start a background search with the pooled
@@ -575,8 +616,9 @@ class KVController:
         return done == 1
 
     def _alloc_dev(self, slot, device):
-        slot.dev = tuple(torch.empty(t.shape, dtype=t.dtype, device=device) for t in slot.host)
-        slot.tab_dev = tuple(torch.empty(t.shape, dtype=t.dtype, device=device) for t in slot.tab_host)
+        slot.dev_block = torch.empty(slot.block.numel(), dtype=torch.uint8, device=device)
+        views = _carve(slot.dev_block, self._slot_specs())
+        slot.dev, slot.tab_dev = views[:4], views[4:]
 
     def _copy_to_device(self, slot):
         """The slot's host-to-device copies on the side stream, after the
@@ -591,12 +633,9 @@ class KVController:
             N.check(lib.hc_stream_wait_event(self._stream, slot.free_after), "hc_stream_wait_event")
         if slot.t0 is not None:
             N.check(lib.hc_event_record(slot.t0, self._stream), "hc_event_record")
-        pairs = list(zip(slot.dev, slot.host))
-        if slot.has_tab:
-            pairs += list(zip(slot.tab_dev, slot.tab_host))
-        for d, h in pairs:
-            N.check(lib.hc_memcpy_h2d_async(d.data_ptr(), h.data_ptr(), h.numel() * h.element_size(), self._stream),
-                    "hc_memcpy_h2d_async")
+        nbytes = slot.nbytes[1] if slot.has_tab else slot.nbytes[0]
+        N.check(lib.hc_memcpy_h2d_async(slot.dev_block.data_ptr(), slot.block.data_ptr(), nbytes, self._stream),
+                "hc_memcpy_h2d_async")
         if slot.t1 is not None:
             N.check(lib.hc_event_record(slot.t1, self._stream), "hc_event_record")
         N.check(lib.hc_event_record(slot.ready, self._stream), "hc_event_record")

@@ -27,6 +27,7 @@ import ctypes
 import math
 import os
 import subprocess
+import threading
 
 import numpy as np
 import torch
@@ -34,6 +35,7 @@ import torch
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "_build", "libhc_oracle.so")
 _lib = None
+_lib_lock = threading.Lock()
 
 
 def build():
@@ -43,7 +45,11 @@ def build():
 
 def _clib():
     global _lib
-    if _lib is None:
+    if _lib is not None:
+        return _lib
+    with _lib_lock:                     # tests call the oracle from several threads
+        if _lib is not None:
+            return _lib
         if not os.path.exists(_LIB_PATH):
             build()
         lib = ctypes.CDLL(_LIB_PATH)
@@ -72,13 +78,13 @@ def _f64(t):
 # ---------------------------------------------------------------------------
 # Window scores: the bit-defined contract (C)
 # ---------------------------------------------------------------------------
-def window_scores(q, k, window, scaling, kernel_size=7, pooling="maxpool", mode="snapkv"):
+def window_scores(q, k, window, scaling, kernel_size=7, pooling="maxpool", mode="snapkv", q_is_window=False):
     """Importance (B,Hk,S) float32 under the bit-defined contract.
 
     mode "snapkv" follows snapkv_importance (scoring.py:50-79): window rows are
-    the last min(window,S) rows of q (T == S).  mode "rawsum" follows
-    cache.py:55-69 before the head mean: the last min(window,T) rows of q, no
-    mask, no softmax, no pooling.
+    the last min(window,S) rows of q (T == S; with q_is_window, q holds only
+    those rows).  mode "rawsum" follows cache.py:55-69 before the head mean:
+    the last min(window,T) rows of q, no mask, no softmax, no pooling.
     """
     qn, kn = _f64(q), _f64(k)
     B, Hq, T, D = qn.shape
@@ -86,6 +92,10 @@ def window_scores(q, k, window, scaling, kernel_size=7, pooling="maxpool", mode=
     if mode == "snapkv":
         W = min(int(window), S)
         q_row0 = S - W
+        if q_is_window:
+            if T != W:
+                raise ValueError("q_is_window: q must hold exactly the last min(window, S) rows")
+            q_row0 = 0
         m = 0
     else:
         W = min(int(window), T)
@@ -481,6 +491,44 @@ class ColdStore:
         ip = self.inner_products(q_vec, head)
         order = np.argsort(-ip, kind="stable")[: min(r, n)]
         return [int(i) for i in order]
+
+
+def cold_topk(kpre, q_vec, r, head=0, per_head=False, dim=None, normalize=True):
+    """ColdStore's search over a whole store at once: kpre (n,H,D) fp32 in
+    logical order (oldest first), q_vec (dim,) fp32 -> logical indices of the
+    top-r inner products (controller.py:190-238, 250-293 under ColdStore's
+    contract).  The same per-token arithmetic as ColdStore.token_vecs and
+    ColdStore.inner_products -- fp64 head sums in head order, squares and
+    products accumulated in dimension order, one rounding to fp32 per vector
+    -- applied to all tokens as arrays, for stores of workload size."""
+    kp = np.asarray(kpre, dtype=np.float32)
+    n, H, D = kp.shape
+    dim = D if dim is None else int(dim)
+    if n == 0 or r <= 0:
+        return np.zeros((0,), dtype=np.int64)
+    if per_head:
+        x = kp[:, head, :].astype(np.float64)
+    else:
+        x = np.zeros((n, D), dtype=np.float64)
+        for h in range(H):
+            x = x + kp[:, h, :].astype(np.float64)
+        x = x / float(H)
+    if D > dim:
+        x = x[:, :dim]
+    elif D < dim:
+        x = np.concatenate([x, np.zeros((n, dim - D))], axis=1)
+    den = np.ones((n,), dtype=np.float64)
+    if normalize:
+        ss = np.zeros((n,), dtype=np.float64)
+        for d in range(dim):
+            ss = ss + x[:, d] * x[:, d]
+        den = np.maximum(np.sqrt(ss), 1e-12)
+    vec = (x / den[:, None]).astype(np.float32).astype(np.float64)
+    q = np.asarray(q_vec, dtype=np.float32).astype(np.float64)
+    ip = np.zeros((n,), dtype=np.float64)
+    for d in range(dim):
+        ip = ip + vec[:, d] * q[d]
+    return np.argsort(-ip, kind="stable")[: min(int(r), n)].astype(np.int64)
 
 
 # ---------------------------------------------------------------------------

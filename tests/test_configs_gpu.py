@@ -8,6 +8,9 @@ attention within the dtype tolerance, re-rotated keys within a few rounding
 steps of the model's rotation.
 """
 
+import concurrent.futures
+import os
+
 import numpy as np
 import pytest
 import torch
@@ -44,6 +47,147 @@ def test_compaction_bit_exact_one_layer(name, layer):
             assert set(p["needles"][0, h].tolist()) <= set(want_keep[0, h].tolist())
     assert torch.equal(ops.gather_kv(k.to(DEV), keep).cpu(), ref.gather_kv(k, want_keep))
     assert torch.equal(ops.gather_kv(v.to(DEV), keep).cpu(), ref.gather_kv(v, want_keep))
+
+
+def _per_sequence(fn, n):
+    """[fn(b) for b in range(n)] on host threads: the oracle's C calls
+    release the GIL, so sequences are checked side by side."""
+    workers = max(1, min(16, os.cpu_count() or 1, n))
+    with concurrent.futures.ThreadPoolExecutor(workers) as ex:
+        return list(ex.map(fn, range(n)))
+
+
+def test_compaction_bit_exact_all_sequences_32k():
+    """The 32k workload's batched compaction of one sampled layer, all 16
+    sequences (independent seeds) in one launch set: scores, kept indices,
+    planted needles and the compacted K/V rows against the oracle."""
+    w = synthetic.WORKLOADS["b16_32k_b2048_held128"]
+    print(f"[case] {w.name} layer 19, batch {w.batch}", flush=True)
+    p = synthetic.make_prompt(w, layer=19, seed=0, device=DEV)
+    W = min(w.window, w.seq_len)
+    k, v = p["k_post"], p["v"]
+    scores = ops.snapkv_scores(p["q_post"], k, w.window, w.scaling, w.pool, "maxpool")
+    keep = ops.keep_index(scores, w.window, w.budget)
+    kk, vv = ops.gather_kv(k, keep).cpu(), ops.gather_kv(v, keep).cpu()
+    q_tail = p["q_post"][:, :, -W:].contiguous().cpu()
+    needles = p["needles"].cpu()
+    del p
+    k_cpu, v_cpu = k.cpu(), v.cpu()
+    scores, keep = scores.cpu(), keep.cpu()
+
+    def oracle(b):
+        sc = ref.window_scores(q_tail[b:b + 1], k_cpu[b:b + 1], w.window, w.scaling, w.pool, "maxpool",
+                               q_is_window=True)
+        return sc, ref.keep_index(sc, w.window, w.budget)
+
+    res = _per_sequence(oracle, w.batch)
+    for b, (sc, kp) in enumerate(res):
+        assert torch.equal(scores[b:b + 1], sc), b
+        assert torch.equal(keep[b:b + 1], kp), b
+        for h in range(w.hk):
+            assert set(needles[b, h].tolist()) <= set(kp[0, h].tolist()), (b, h)
+    want_keep = torch.cat([kp for _, kp in res])
+    assert torch.equal(kk, ref.gather_kv(k_cpu, want_keep))
+    assert torch.equal(vv, ref.gather_kv(v_cpu, want_keep))
+
+
+def test_prefill_retrieval_to_held_decode_at_64k():
+    """The 64k bf16 workload (batch 4, budget 4096, window 64, heavy-tailed
+    keys), one layer through the hot/cold engine: the prompt is compressed
+    to the budget and the rest evicted to the cold store; the prefill-time
+    synchronous retrieval (controller.py:295-312) fetches the top-256 tokens
+    per KV head; the first decode step (hotcold_attention) injects them into
+    the held slot and attends [held | hot rows | token] in the fused launch.
+    Checked: the kept rows (oracle compression), the store's contents, each
+    (sequence, KV head)'s retrieved positions (oracle search over the store),
+    the held keys bit for bit (the model's rotation of the stored pre-RoPE
+    keys), and the attention output within the bf16 tolerance."""
+    from hotcold_kv import KVController
+    from hotcold_kv import patch as hp
+    from hotcold_kv.cache import HotColdLayer
+
+    w = synthetic.WORKLOADS["bf16_b4_64k_b4096_held256"]
+    B, Hk, G, D, R = w.batch, w.hk, w.group, w.head_dim, w.prefill_retrieval
+    print(f"[case] {w.name} layer 3, batch {B}, retrieval {R}", flush=True)
+    cap = w.budget + w.decode_steps
+    topk = w.budget - w.window
+    ratio = (topk + 0.5) / cap
+    ctrl = KVController(max_capacity_prompt=cap, topk_ratio=ratio, recent_size=w.window, cpu_buffer_size=w.seq_len,
+                        faiss_dim=D, window_size=w.retrieve_every, query_pool_size=4, lookahead_k=R,
+                        hold_retrieved=True, per_head_retrieval=True, retrieve_after_prefill=True,
+                        force_wait_for_prefetch_diagnostic=True, profile_overlap=False, enable_asserts=True)
+    p = synthetic.make_prompt(w, layer=3, seed=0, device=DEV)
+    inv = synthetic.inv_freq(D, w.theta)
+    ctrl._lazy_init(p["k_pre"], n_layers=1)
+    ctrl.set_rope(inv, 1.0)
+    layer = HotColdLayer(ctrl)
+    q_last = p["q_post"][:, :, -w.window:, :].contiguous()
+    qwin = p["q_pre"][:, :, -ctrl.query_pool_size:, :].contiguous()
+    k_post, v, k_pre, positions = p["k_post"].cpu(), p["v"].cpu(), p["k_pre"].cpu(), p["positions"].cpu()
+    # prefill (patch.py:152-172 without the prompt's own attention)
+    layer.set_last_query_post(q_last)
+    layer.update(key_states=p["k_post"], value_states=p["v"], layer_idx=0,
+                 cache_kwargs={"pre_key_states": p["k_pre"], "positions": p["positions"]})
+    del p
+    ctrl.launch_retrieval_now(0, qwin)
+    ctrl.maybe_prefetch_to_gpu(0, device=DEV)
+    assert ctrl.dbg["retrieval_launched_prefill"] == 1
+    # first decode step
+    tok = synthetic.make_decode_token(w, 3, 0, seed=0, device=DEV)
+    out = hp.hotcold_attention(ctrl, layer, 0, tok["q_pre"], tok["k_pre"], tok["v"], tok["q_post"], tok["k_post"],
+                               tok["position"], G, w.scaling)
+    torch.cuda.synchronize()
+    assert ctrl.dbg["injection_new"] == 1 and ctrl.dbg["prefetch_ready"] == 1
+    n = w.budget + 1
+
+    # kept rows: the oracle's compression, sequence by sequence
+    q_last_cpu = q_last.cpu()
+    res = _per_sequence(lambda b: ref.hotcold_compress(k_post[b:b + 1], v[b:b + 1], k_pre[b:b + 1],
+                                                       positions[b:b + 1], q_last_cpu[b:b + 1], cap, w.window,
+                                                       ratio), B)
+    hot_k, hot_v, hot_pos = layer.keys.cpu(), layer.values.cpu(), layer.positions.cpu()
+    assert hot_k.shape[2] == n
+    for b, want in enumerate(res):
+        assert torch.equal(hot_pos[b, :w.budget], want["positions"][0]), b
+        assert torch.equal(hot_k[b:b + 1, :, :w.budget], want["keys"]), b
+        assert torch.equal(hot_v[b:b + 1, :, :w.budget], want["values"]), b
+
+    # the store holds exactly the evicted tokens, oldest first
+    qvec = ctrl._q_to_vecs_np(qwin)                                      # (B,Hk,D) the search's queries
+    qf = qwin.double().cpu().view(B, Hk, G, -1, D).mean(dim=(2, 3))
+    qf = qf / qf.norm(dim=-1, keepdim=True)
+    assert np.abs(qvec - qf.numpy()).max() < 1e-6
+    held_pos, held_valid, r = ctrl.held_mem[0]
+    assert r == R and bool(held_valid.all())
+    held_pos = held_pos.cpu()
+    kbuf, vbuf = layer.buf.held_storage()
+    lo = layer.buf.held - R
+    got_k, got_v = kbuf[:, :, lo:layer.buf.held].cpu(), vbuf[:, :, lo:layer.buf.held].cpu()
+    want_k = torch.empty((B, Hk, R, D), dtype=torch.float32)
+    want_v = torch.empty((B, Hk, R, D), dtype=torch.float32)
+    for b in range(B):
+        ev = res[b]["evicted_idx"][0]
+        snap = ctrl.rings[0][b].export()
+        assert snap["pos"].tolist() == positions[b, ev].tolist(), b
+        assert torch.equal(torch.from_numpy(snap["kpre"]), k_pre[b][:, ev].permute(1, 0, 2).float()), b
+        for h in range(Hk):
+            idx = ref.cold_topk(snap["kpre"], qvec[b, h], R, head=h, per_head=True, dim=D)
+            assert held_pos[b, h].tolist() == snap["pos"][idx].tolist(), (b, h)
+            want_k[b, h] = torch.from_numpy(snap["kpre"][idx, h])
+            want_v[b, h] = torch.from_numpy(snap["v"][idx, h])
+    assert torch.equal(got_k, ref.rerope(want_k, held_pos, inv, 1.0, w.dtype))
+    assert torch.equal(got_v, want_v.to(w.dtype))
+
+    # the decode over [held | hot rows | token]
+    cur = tok["position"][0, -1:].cpu()
+    K = torch.cat([got_k, hot_k], 2)
+    V = torch.cat([got_v, hot_v], 2)
+    q1 = tok["q_post"].cpu()
+    o = out[:, :, 0].float().cpu().numpy()
+    for h in range(Hk):
+        m = torch.cat([held_valid[:, h].cpu() & (held_pos[:, h] <= cur), torch.ones((B, n), dtype=torch.bool)], 1)
+        want = ref.decode_attention(q1[:, h * G:(h + 1) * G], K[:, h:h + 1], V[:, h:h + 1], w.scaling, m)
+        assert np.abs(o[:, h * G:(h + 1) * G] - want).max() <= TOL[w.dtype], h
 
 
 def test_compaction_full_8k_job_layers_batched():

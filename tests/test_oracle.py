@@ -91,6 +91,18 @@ def test_window_scores_brute_force_tiny():
         assert np.allclose(got[0, h].double().numpy(), imp, rtol=1e-6, atol=1e-9)
 
 
+def test_window_scores_from_the_window_rows_only():
+    """q_is_window: the last W query rows alone give the same scores."""
+    g = torch.Generator().manual_seed(5)
+    q = torch.randn(2, 8, 300, 32, generator=g)
+    k = torch.randn(2, 2, 300, 32, generator=g)
+    full = ref.window_scores(q, k, 16, 0.2, 7, "maxpool")
+    tail = ref.window_scores(q[:, :, -16:].contiguous(), k, 16, 0.2, 7, "maxpool", q_is_window=True)
+    assert torch.equal(full, tail)
+    with pytest.raises(ValueError):
+        ref.window_scores(q[:, :, -8:].contiguous(), k, 16, 0.2, 7, "maxpool", q_is_window=True)
+
+
 def test_window_scores_causal_mask():
     # a key after a window row's own position must get no weight from that row:
     # make the last key dominate; only the last window row may see it
@@ -358,6 +370,32 @@ def load_golden():
         cases[case] = (q, k, W, pool, budget, float(data[f"{case}__scaling"]),
                        torch.from_numpy(data[f"{case}__scores"]), torch.from_numpy(data[f"{case}__keep"]))
     return cases
+
+
+@pytest.mark.parametrize("per_head,dim,normalize", [(False, 16, True), (True, 16, True), (False, 24, True),
+                                                    (True, 8, True), (False, 16, False)])
+def test_cold_topk_equals_cold_store_search(per_head, dim, normalize):
+    """The array form ranks exactly like ColdStore.search, including exact
+    ties (duplicated tokens), a wrapped ring, padding and cropping."""
+    g = np.random.default_rng(dim + 3 * per_head + 7 * normalize)
+    H, D = 3, 16
+    store = ref.ColdStore(capacity=50, dim=dim, normalize=normalize, per_head=per_head)
+    k = g.standard_normal((70, H, D)).astype(np.float32)
+    k[40:45] = k[10:15]                        # duplicates: exact ties
+    store.add(k, -k, np.arange(70))            # drops the 20 oldest
+    kept = np.stack(store.kpre)
+    for head in range(H if per_head else 1):
+        for trial in range(3):
+            q = g.standard_normal(dim).astype(np.float32)
+            q /= np.linalg.norm(q)
+            want = store.search(q, 17, head=head)
+            got = ref.cold_topk(kept, q, 17, head=head, per_head=per_head, dim=dim, normalize=normalize)
+            assert got.tolist() == want
+    if normalize:
+        # unit vectors: a stored vector used as the query ranks its own token
+        # first (Cauchy-Schwarz; the kept store holds no duplicate of it)
+        vec = store.vec[30][0]
+        assert int(ref.cold_topk(kept, vec, 1, per_head=per_head, dim=dim)[0]) == 30
 
 
 def test_golden_fixtures_reproduce():

@@ -11,7 +11,7 @@ a copy can be held "not ready" for as long as a test wants.
 
 import torch
 
-from hotcold_kv.controller import KVController, _Slot
+from hotcold_kv.controller import KVController, _Slot, _block_layout
 from hotcold_kv.datatypes import EvictedKV
 
 HK, D = 2, 16
@@ -218,3 +218,37 @@ def test_busy_slots_skip_the_search():
     _window(ctrl)                             # every slot has a copy in flight
     assert ctrl.dbg["retrieval_skipped_no_slot"] == 1
     assert ctrl.dbg["retrieval_launched"] == before
+
+
+def test_two_slots_per_layer_are_preallocated():
+    ctrl = _ctrl()
+    ctrl._preallocate_slots()
+    slots = ctrl._slots[0]
+    assert len(slots) == 2 and slots[0] is not slots[1]
+    assert all(sl.state == _Slot.FREE for sl in slots)
+    ctrl._preallocate_slots()                 # idempotent
+    assert len(ctrl._slots[0]) == 2
+
+
+def test_slot_buffers_are_views_of_one_block():
+    """k_pre, v, pos, valid, cos, sin carved from one block in that order,
+    256-byte aligned and disjoint; one copy of nbytes[0] carries a retrieval
+    without tables, nbytes[1] one with them."""
+    ctrl = _ctrl(per_head_retrieval=True)
+    with ctrl._retrieval_lock[0]:
+        sl = ctrl._take_slot(0)
+    views = list(sl.host) + list(sl.tab_host)
+    base = sl.block.data_ptr()
+    offs, nbytes = _block_layout(ctrl._slot_specs())
+    spans = []
+    for t, off, (shape, dt) in zip(views, offs, ctrl._slot_specs()):
+        assert t.data_ptr() - base == off and off % 256 == 0
+        assert tuple(t.shape) == tuple(shape) and t.dtype == dt and t.is_contiguous()
+        spans.append((off, off + t.numel() * t.element_size()))
+    for (a0, a1), (b0, b1) in zip(spans, spans[1:]):
+        assert a1 <= b0
+    assert nbytes == (spans[3][1], spans[5][1]) == sl.nbytes
+    assert sl.block.numel() == nbytes[1]
+    # writes through the views land in the block
+    sl.host[2].fill_(7)
+    assert sl.block[offs[2]:offs[2] + 8].view(torch.int64).item() == 7
