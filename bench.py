@@ -268,7 +268,36 @@ def dropin_compaction(s, flush, reps=5):
                 wall.append((time.perf_counter() - t0) * 1e3)
             out[name] = (statistics.median(gpu), statistics.median(wall))
             out[name + "_rows"] = states[0].get_seq_length()
+    out["states"] = states
     return out
+
+
+def dropin_decode(s, states, reps=3):
+    """The decode steps through the drop-in's PressLayerState.decode, one
+    call per layer per step, issued eagerly from Python as a model's layer
+    loop issues them (no graph): the workload's decode tokens over the
+    compacted caches `states` leaves behind.  Host time from an idle GPU
+    until the stream is done, per layer-step (median over reps of the whole
+    job; each rep restarts from the compacted caches)."""
+    import torch
+
+    w, B, G = s.w, s.w.batch, s.w.group
+    toks = [[(s.q_new[t][l * B:(l + 1) * B], s.k_new[t][l * B:(l + 1) * B], s.v_new[t][l * B:(l + 1) * B])
+             for l in range(w.layers)] for t in range(w.decode_steps)]
+    n0 = [st.get_seq_length() for st in states]
+    walls = []
+    with torch.cuda.stream(s.stream):
+        for _ in range(reps + 1):
+            for st, n in zip(states, n0):
+                st.buf.n = n                      # back to the compacted prompt
+            s.stream.synchronize()
+            t0 = time.perf_counter()
+            for t in range(w.decode_steps):
+                for st, (q, k, v) in zip(states, toks[t]):
+                    st.decode(q, k, v, G, w.scaling)
+            s.stream.synchronize()
+            walls.append((time.perf_counter() - t0) * 1e6 / (w.decode_steps * w.layers))
+    return statistics.median(walls[1:])
 
 
 def run_steps(s, steps, flush):
@@ -881,6 +910,8 @@ def main():
     log(f"drop-in compaction (PressLayerState.compact_prompt, {w.layers} layers): deferred "
         f"{dro['deferred'][0]:.3f} ms GPU / {dro['deferred'][1]:.3f} ms wall, one layer at a time "
         f"{dro['per_layer'][0]:.3f} ms GPU / {dro['per_layer'][1]:.3f} ms wall")
+    eager_us = dropin_decode(s, dro.pop("states"))
+    log(f"drop-in decode (PressLayerState.decode per layer, eager from Python): {eager_us:.2f} us/layer-step wall")
     del flush
 
     others = []
@@ -948,6 +979,7 @@ def main():
         "decode_launch_us_differential": round(dec_ms * 1e3, 3),
         "decode_launch_us_event_bracketed": round(dec_br_ms * 1e3, 3),
         "decode_us_per_layer_launch_cold": round(pl_cold_ms * 1e3 / w.layers, 3),
+        "decode_us_per_layer_dropin_eager_wall": round(eager_us, 2),
         "decode_us_per_layer_launch_warm": round(pl_warm_ms * 1e3 / w.layers, 3),
         "decode_launch_us_warm_last_step": round(warm_dec_ms * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",

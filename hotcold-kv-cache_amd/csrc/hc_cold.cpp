@@ -128,12 +128,20 @@ struct ColdStore {
 
   // Inner products of query q with the vectors of head vh over physical
   // slots [s0, s1): fp64, dimensions in order.
+  // Blocked over slots so a block's sums stay in L1 while the dimensions
+  // stream past; every sum still adds its products in dimension order.
   void scan(const float* q, int64_t vh, int64_t s0, int64_t s1, double* ip) const {
-    for (int64_t s = s0; s < s1; ++s) ip[s] = 0.0;
-    for (int64_t d = 0; d < VD; ++d) {
-      const double qd = (double)q[d];
-      const float* col = &vec[((size_t)vh * VD + d) * cap];
-      for (int64_t s = s0; s < s1; ++s) ip[s] += (double)col[s] * qd;
+    constexpr int64_t kBlock = 512;
+    double acc[kBlock];
+    for (int64_t b0 = s0; b0 < s1; b0 += kBlock) {
+      const int64_t n = std::min(kBlock, s1 - b0);
+      for (int64_t i = 0; i < n; ++i) acc[i] = 0.0;
+      for (int64_t d = 0; d < VD; ++d) {
+        const double qd = (double)q[d];
+        const float* col = &vec[((size_t)vh * VD + d) * cap + b0];
+        for (int64_t i = 0; i < n; ++i) acc[i] += (double)col[i] * qd;
+      }
+      memcpy(ip + b0, acc, sizeof(double) * n);
     }
   }
 
@@ -282,16 +290,20 @@ extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t*
 }
 
 extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
-                                int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
-                                uint8_t* valid_out, int64_t nthreads) {
-  if (B <= 0 || R <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out)
+                                int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
+                                float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                                int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing,
+                                int64_t nthreads) {
+  if (B <= 0 || R <= 0 || q_dim <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out)
     return set_error(HC_ERR_INVALID, "cold_retrieve: bad arguments");
+  if (tab && (tab_rows <= 0 || tab_row_bytes <= 0 || !tab_out))
+    return set_error(HC_ERR_INVALID, "cold_retrieve: table rows need a size and an output");
   const ColdStore* s0 = reinterpret_cast<const ColdStore*>(stores[0]);
   if (!s0) return set_error(HC_ERR_INVALID, "cold_retrieve: null store");
-  const int64_t H = s0->H, D = s0->D;
+  const int64_t H = s0->H, D = s0->D, VD = s0->VD;
   for (int64_t b = 0; b < B; ++b) {
     const ColdStore* s = reinterpret_cast<const ColdStore*>(stores[b]);
-    if (!s || s->H != H || s->D != D || s->VD != s0->VD || s->VH != (per_head ? H : 1))
+    if (!s || s->H != H || s->D != D || s->VD != VD || s->VH != (per_head ? H : 1))
       return set_error(HC_ERR_INVALID, "cold_retrieve: store %lld does not match (per_head=%d)", (long long)b,
                        per_head);
   }
@@ -301,28 +313,59 @@ extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, 
   memset(v_out, 0, sizeof(float) * B * H * R * D);
   memset(pos_out, 0, sizeof(int64_t) * B * VH * R);
   memset(valid_out, 0, (size_t)(B * VH * R));
+  std::atomic<int64_t> missing{0};
   const int64_t tasks = B * VH;
   parallel_for(tasks, threads_for(nthreads, tasks), [&](int64_t task) {
     const int64_t b = task / VH, h = task % VH;
     const ColdStore* s = reinterpret_cast<const ColdStore*>(stores[b]);
-    std::shared_lock<std::shared_mutex> lk(s->mu);
-    if (s->size == 0) return;
-    std::vector<double> ip((size_t)s->size);
-    std::vector<int64_t> hits((size_t)R);
-    s->scan(q + b * q_sb + h * q_sh, h, 0, s->size, ip.data());
-    const int64_t m = s->select(ip.data(), R, hits.data());
-    for (int64_t j = 0; j < m; ++j) {
-      const int64_t p = s->physical(hits[j]);
-      const float* kp = &s->kpre[(size_t)p * H * D];
-      const float* vp = &s->v[(size_t)p * H * D];
-      const int64_t h0 = per_head ? h : 0, h1 = per_head ? h + 1 : H;
-      for (int64_t hh = h0; hh < h1; ++hh) {
-        memcpy(kpre_out + ((b * H + hh) * R + j) * D, kp + hh * D, sizeof(float) * D);
-        memcpy(v_out + ((b * H + hh) * R + j) * D, vp + hh * D, sizeof(float) * D);
+    // the query: cropped or zero-padded to the vector width, then (normalize_q)
+    // divided by max(||x||, 1e-12) with the squares summed in dimension order
+    // in fp64 and the quotient rounded to fp32, as the stored vectors are
+    std::vector<float> qv((size_t)VD, 0.0f);
+    const float* qs = q + b * q_sb + h * q_sh;
+    double den = 1.0;
+    if (normalize_q) {
+      double ss = 0.0;
+      for (int64_t d = 0; d < VD; ++d) {
+        const double x = d < q_dim ? (double)qs[d] : 0.0;
+        ss += x * x;
       }
-      pos_out[(b * VH + h) * R + j] = s->pos[p];
-      valid_out[(b * VH + h) * R + j] = 1;
+      den = std::max(std::sqrt(ss), 1e-12);
+    }
+    for (int64_t d = 0; d < std::min(VD, q_dim); ++d) qv[d] = normalize_q ? (float)((double)qs[d] / den) : qs[d];
+    int64_t m = 0;
+    std::vector<int64_t> hits((size_t)R);
+    {
+      std::shared_lock<std::shared_mutex> lk(s->mu);
+      if (s->size > 0) {
+        std::vector<double> ip((size_t)s->size);
+        s->scan(qv.data(), h, 0, s->size, ip.data());
+        m = s->select(ip.data(), R, hits.data());
+        for (int64_t j = 0; j < m; ++j) {
+          const int64_t p = s->physical(hits[j]);
+          const float* kp = &s->kpre[(size_t)p * H * D];
+          const float* vp = &s->v[(size_t)p * H * D];
+          const int64_t h0 = per_head ? h : 0, h1 = per_head ? h + 1 : H;
+          for (int64_t hh = h0; hh < h1; ++hh) {
+            memcpy(kpre_out + ((b * H + hh) * R + j) * D, kp + hh * D, sizeof(float) * D);
+            memcpy(v_out + ((b * H + hh) * R + j) * D, vp + hh * D, sizeof(float) * D);
+          }
+          pos_out[(b * VH + h) * R + j] = s->pos[p];
+          valid_out[(b * VH + h) * R + j] = 1;
+        }
+      }
+    }
+    if (tab) {
+      // rows of the caller's table (one per position) at the retrieved
+      // positions; rows past the hits take position 0
+      for (int64_t j = 0; j < R; ++j) {
+        const int64_t p = pos_out[(b * VH + h) * R + j];
+        uint8_t* dst = tab_out + ((b * VH + h) * R + j) * tab_row_bytes;
+        if (p >= 0 && p < tab_rows) memcpy(dst, tab + p * tab_row_bytes, (size_t)tab_row_bytes);
+        else { memset(dst, 0, (size_t)tab_row_bytes); missing.fetch_add(1); }
+      }
     }
   });
+  if (tab_missing) *tab_missing = missing.load();
   return HC_OK;
 }

@@ -479,6 +479,22 @@ extern "C" int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t H
                      o_sh, nullptr, nullptr, workspace, workspace_bytes, num_splits, stream, &ap);
 }
 
+extern "C" int hc_decode_attn_append_packed(const hc_decode_append_args* a, void* stream) {
+  HC_REQUIRE(a != nullptr, "decode_append_packed: null argument struct");
+  HC_REQUIRE(a->dtype >= INT32_MIN && a->dtype <= INT32_MAX, "decode_append_packed: bad dtype");
+  return hc_decode_attn_append((int)a->dtype, a->B, a->Hq, a->Hk, a->D, a->S, a->q, a->q_sb, a->q_sh, a->k, a->k_sb,
+                               a->k_sh, a->k_ss, a->v, a->v_sb, a->v_sh, a->v_ss, a->k_new, a->kn_sb, a->kn_sh,
+                               a->v_new, a->vn_sb, a->vn_sh, a->p_new, a->pn_sb, a->pn_sh, a->p_dst, a->pd_sb,
+                               a->pd_sh, a->pd_ss, a->pos_new, a->posn_sb, a->pos_dst, a->posd_sb, a->mask,
+                               a->mask_sb, a->held_len, a->held_pos, a->hp_sb, a->hp_sh, a->held_valid, a->hv_sb,
+                               a->hv_sh, a->cur_pos, a->scaling, a->out, a->o_sb, a->o_sh, a->workspace,
+                               a->workspace_bytes, a->num_splits, stream);
+}
+
+extern "C" int64_t hc_decode_append_args_size(void) { return (int64_t)sizeof(hc_decode_append_args); }
+
+static_assert(sizeof(hc_decode_append_args) == 51 * 8, "hc_decode_append_args: every field is 8 bytes, no padding");
+
 extern "C" int hc_decode_attn_h2o(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
                                   const void* q, int64_t q_sb, int64_t q_sh,
                                   const void* k, int64_t k_sb, int64_t k_sh, int64_t k_ss,

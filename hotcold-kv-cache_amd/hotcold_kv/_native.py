@@ -79,6 +79,8 @@ SIGNATURES = {
         _vp, _i64, _i64,
         _vp, _i64, _i64,
         _vp]),
+    "hc_decode_attn_append_packed": (_int, [_vp, _vp]),
+    "hc_decode_append_args_size": (_i64, []),
     "hc_decode_attn_append_noalloc": (_int, [
         _int, _i64, _i64, _i64, _i64, _i64,
         _vp, _i64, _i64,
@@ -198,8 +200,22 @@ SIGNATURES = {
     "hc_cold_add": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp]),
     "hc_cold_search": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "hc_cold_export": (_int, [_vp, _vp, _vp, _vp, _vp]),
-    "hc_cold_retrieve": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _vp, _vp, _vp, _vp, _i64]),
+    "hc_cold_retrieve": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _i64, _int, _vp, _vp, _vp, _vp,
+                                _vp, _i64, _i64, _vp, _vp, _i64]),
 }
+
+
+class DecodeAppendArgs(ctypes.Structure):
+    """ctypes mirror of hc_decode_append_args (include/hotcold_hip.h): every
+    field 8 bytes, in the header's order."""
+    _fields_ = [(n, t) for names, t in (
+        ("dtype B Hq Hk D S", _i64), ("q", _vp), ("q_sb q_sh", _i64), ("k", _vp), ("k_sb k_sh k_ss", _i64),
+        ("v", _vp), ("v_sb v_sh v_ss", _i64), ("k_new", _vp), ("kn_sb kn_sh", _i64), ("v_new", _vp),
+        ("vn_sb vn_sh", _i64), ("p_new", _vp), ("pn_sb pn_sh", _i64), ("p_dst", _vp), ("pd_sb pd_sh pd_ss", _i64),
+        ("pos_new", _vp), ("posn_sb", _i64), ("pos_dst", _vp), ("posd_sb", _i64), ("mask", _vp), ("mask_sb", _i64),
+        ("held_len", _i64), ("held_pos", _vp), ("hp_sb hp_sh", _i64), ("held_valid", _vp), ("hv_sb hv_sh", _i64),
+        ("cur_pos", _vp), ("scaling", _dbl), ("out", _vp), ("o_sb o_sh", _i64), ("workspace", _vp),
+        ("workspace_bytes num_splits", _i64)) for n in names.split()]
 
 
 def library_path():
@@ -223,6 +239,8 @@ def lib():
             fn = getattr(handle, name)
             fn.restype = res
             fn.argtypes = args
+        if handle.hc_decode_append_args_size() != ctypes.sizeof(DecodeAppendArgs):
+            raise RuntimeError("hotcold_kv: hc_decode_append_args layout differs between the library and the binding")
         _lib = handle
     return _lib
 

@@ -202,10 +202,9 @@ class PressLayerState:
         if self.method == "h2o":
             return self._decode_h2o(q_post, k_post, v, scaling)
         if k_post.shape[2] == 1:
-            out = self.buf.append_attend(q_post, k_post, v, scaling)
-        else:
-            self.buf.append(k_post, v)
-            out = ops.decode_attention(q_post, self.buf.keys, self.buf.values, scaling)
+            return self.buf.append_attend(q_post, k_post, v, scaling, keepdim=True)     # (B,Hq,1,D)
+        self.buf.append(k_post, v)
+        out = ops.decode_attention(q_post, self.buf.keys, self.buf.values, scaling)
         return out.unsqueeze(2)  # (B,Hq,1,D)
 
     def _decode_h2o(self, q_post, k_post, v, scaling):

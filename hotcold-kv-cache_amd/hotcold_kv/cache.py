@@ -113,14 +113,18 @@ class HotColdLayer(CacheLayerMixin):
         attention over [held slot | hot rows | the token] (patch.py:241-305):
         one launch writes the token's post-RoPE key, value, pre-RoPE key and
         position into the next hot row and attends.  held = (pos, valid, R)
-        of the held retrieved slot, or None.  Returns (B,Hq,D)."""
+        of the held retrieved slot, or None.  Returns (B,Hq,1,D)."""
         buf = self.buf
+        if positions.shape[-1] != 1:
+            raise RuntimeError("HotColdLayer.append_attend: one token per step, positions (B,1)")
         buf.ensure(buf.n + 1)
         R = int(held[2]) if held is not None else 0
         lo = buf.held - R
+        # one-token step: positions is (B,1), so its first element is the
+        # current position the held-slot mask compares against
         out = ops.decode_append_rows(q_post, buf.st, lo, R + buf.n + 1, k_post, v, scaling, p_new=k_pre,
                                      pos_new=positions, held=held if R else None,
-                                     cur_pos=positions[0, -1:] if R else None)
+                                     cur_pos=positions if R else None, keepdim=True)
         buf.n += 1
         self.seen_tokens += 1
         return out

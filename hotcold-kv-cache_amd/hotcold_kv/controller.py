@@ -104,7 +104,7 @@ class _Ring:
 def _block_layout(specs, align=256):
     """Byte offsets of tensors of the given (shape, dtype) packed into one
     block, each start aligned to `align`; returns (offsets, (bytes without
-    the last two, total bytes))."""
+    the last one, total bytes))."""
     offs, off = [], 0
     ends = []
     for shape, dt in specs:
@@ -112,7 +112,7 @@ def _block_layout(specs, align=256):
         offs.append(off)
         off += int(np.prod(shape)) * torch.empty((), dtype=dt).element_size()
         ends.append(off)
-    return offs, (ends[-3], ends[-1])
+    return offs, (ends[-2], ends[-1])
 
 
 def _carve(block, specs):
@@ -128,15 +128,16 @@ def _carve(block, specs):
 
 class _Slot:
     """One reusable staging slot of a layer: pinned host buffers (k_pre, v,
-    pos, valid, and the rotary tables cos, sin), all views of one pinned
-    block so that a retrieval goes over in one copy; its device twin block;
-    the events of its copy."""
+    pos, valid, and the rotary tables: per row cos then sin), all views of
+    one pinned block so that a retrieval goes over in one copy; its device
+    twin block; the events of its copy."""
 
     FREE, FILLING, RETRIEVED, COPYING, STAGED, HELD = range(6)
 
-    def __init__(self, host, tab_host=None, block=None, nbytes=(0, 0)):
+    def __init__(self, host, tab=None, block=None, nbytes=(0, 0)):
         self.host = host            # (kpre, v, pos, valid) pinned host tensors
-        self.tab_host = tab_host    # pinned rotary tables (cos, sin) at pos, cache dtype
+        self.tab = tab              # pinned rotary tables at pos, (B,Hc,R,2,D/2) cache dtype: [..., 0, :] cos, 1 sin
+        self.tab_host = None if tab is None else (tab[..., 0, :], tab[..., 1, :])
         self.block = block          # the one pinned allocation host and tab_host are views of
         self.nbytes = nbytes        # bytes of the block without / with the tables
         self.tab_dev = None
@@ -226,6 +227,8 @@ class KVController:
         self.B = self.Hk = self.D = self.n_layers = None
         self.dtype = None
         self._rope = None           # (inv_freq fp32 CPU, attention_scaling) of the model's rotary module
+        self._rope_tab = None       # byte rows [position][cos | sin] of the rotary tables (_rope_rows)
+        self._max_pos = 0           # largest position in any cold store
         self.rings = []
         self.step_count = []
         self.query_window = []
@@ -260,6 +263,7 @@ class KVController:
             "injection_skipped_no_valid": 0,
             "prefetch_copy_ms_sum": 0.0,
             "prefetch_copy_ms_count": 0,
+            "rope_rows_direct": 0,
             "prefetch_not_ready_checks": 0,
             "retrieval_skipped_no_slot": 0,
             "prefetch_superseded": 0,
@@ -279,6 +283,7 @@ class KVController:
         vec_heads = self.Hk if self.per_head_retrieval else 1
         self.rings = [[_Ring(self.cpu_buffer_size, self.Hk, self.D, self.faiss_dim, vec_heads,
                              self.normalize_for_ip) for _ in range(B)] for _ in range(L)]
+        self._store_ptrs = [(ctypes.c_void_p * B)(*[r.handle for r in rings]) for rings in self.rings]
         self.step_count = [0] * L
         self.query_window = [deque(maxlen=self.query_pool_size) for _ in range(L)]
         self._retrieval_thread = [None] * L
@@ -328,6 +333,27 @@ class KVController:
         tables of its positions, computed on the search thread, and the inject
         writes apply_rotary_pos_emb's exact bits."""
         self._rope = (inv_freq.detach().float().cpu().contiguous(), float(attention_scaling))
+        self._rope_tab = None
+
+    def _rope_rows(self):
+        """The rotary tables of every position up to the largest one in the
+        cold store, as byte rows [position][cos | sin] (D/2 values each, the
+        cache dtype), or None without set_rope.  Computed on the calling
+        (decode) thread as LlamaRotaryEmbedding.forward computes them, and
+        regrown by doubling when the store reaches past them; the search
+        threads only gather rows."""
+        if self._rope is None or self.dtype is None:
+            return None
+        need = self._max_pos + 1
+        if self._rope_tab is None or self._rope_tab.shape[0] < need:
+            rows = max(4096, 2 * (self._rope_tab.shape[0] if self._rope_tab is not None else 0))
+            while rows < need:
+                rows *= 2
+            cos, sin = ops_rope_tables(torch.arange(rows, dtype=torch.int64).view(1, rows), self._rope[0],
+                                       self._rope[1], self.dtype)
+            tab = torch.stack([cos[0], sin[0]], dim=1).contiguous()                 # (rows, 2, D/2)
+            self._rope_tab = tab.view(torch.uint8).numpy().reshape(rows, -1)
+        return self._rope_tab
 
     def evict_staging(self, device, B, H, te, D):
         """Device and pinned host staging blocks of at least
@@ -366,10 +392,17 @@ class KVController:
         return x
 
     def _normalize(self, x):
+        """x / max(||x||, 1e-12) over the last axis, the squares summed in
+        fp64 in dimension order and the quotient rounded to fp32: the
+        arithmetic of the stored vectors and of hc_cold_retrieve's query
+        normalisation."""
         if not self.normalize_for_ip:
             return x
-        n = np.sqrt((x.astype(np.float64) ** 2).sum(axis=-1, keepdims=True))
-        return (x / np.maximum(n, 1e-12)).astype(np.float32)
+        x64 = np.asarray(x, dtype=np.float64)
+        ss = np.zeros(x64.shape[:-1], dtype=np.float64)
+        for d in range(x64.shape[-1]):
+            ss = ss + x64[..., d] * x64[..., d]
+        return (x64 / np.maximum(np.sqrt(ss), 1e-12)[..., None]).astype(np.float32)
 
     def _k_token_to_vec_np(self, kpre_token):
         """(Hk,D) pre-RoPE key of one token -> its search vector(s), computed
@@ -418,6 +451,8 @@ class KVController:
         vv = ev.v_cpu.detach().cpu().float().contiguous().numpy()
         pos = ev.pos_cpu.detach().cpu().contiguous().numpy().astype(np.int64)
         idx = ev.evicted_idx.detach().cpu().contiguous().numpy().astype(np.int64)
+        if pos.size:
+            self._max_pos = max(self._max_pos, int(pos.max()))
         for b in range(kpre.shape[0]):
             kept = int((idx[b] >= 0).sum())
             if kept == 0:
@@ -463,14 +498,14 @@ class KVController:
 
     # -- staging slots ------------------------------------------------------------------
     def _slot_specs(self):
-        """(shape, dtype) of a slot's k_pre, v, pos, valid, cos, sin: the
-        order of their views in the slot's one block (tables last, so a
-        retrieval without them copies a prefix of the block)."""
+        """(shape, dtype) of a slot's k_pre, v, pos, valid and rotary tables:
+        the order of their views in the slot's one block (the tables last,
+        so a retrieval without them copies a prefix of the block)."""
         B, Hk, D, R = self.B, self.Hk, self.D, self.lookahead_k
         pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
-        tshape = (B, Hk if self.per_head_retrieval else 1, R, D // 2)
+        tshape = (B, Hk if self.per_head_retrieval else 1, R, 2, D // 2)
         return (((B, Hk, R, D), torch.float32), ((B, Hk, R, D), torch.float32), (pshape, torch.int64),
-                (pshape, torch.bool), (tshape, self.dtype), (tshape, self.dtype))
+                (pshape, torch.bool), (tshape, self.dtype))
 
     def _take_slot(self, li):
         """A free slot of layer li whose last copy has completed (its host
@@ -486,17 +521,19 @@ class KVController:
         nbytes = _block_layout(specs)[1]
         block = torch.empty(nbytes[1], dtype=torch.uint8, pin_memory=torch.cuda.is_available())
         views = _carve(block, specs)
-        sl = _Slot(views[:4], views[4:], block, nbytes)
+        sl = _Slot(views[:4], views[4], block, nbytes)
         sl.state = _Slot.FILLING
         self._slots[li].append(sl)
         return sl
 
-    def _retrieval_worker(self, layer_idx, q_vecs, slot=None, nthreads=0):
+    def _retrieval_worker(self, layer_idx, q_vecs, slot=None, nthreads=0, table=None):
         """Top-lookahead_k tokens per batch row (or per KV head) into a slot's
         pinned host buffers (controller.py:250-293), one native call over all
         rows.  q_vecs None: the slot's pooled query is still being copied to
-        the host; wait for it here, on this thread, then normalise it.
-        Returns False when no search ran (no free slot, not initialised)."""
+        the host; wait for it here, on this thread, then normalise it.  table:
+        the rotary tables by position (_rope_rows), gathered into the slot for
+        the inject.  Returns False when no search ran (no free slot, not
+        initialised)."""
         li = int(layer_idx)
         if not self._inited:
             return False
@@ -506,24 +543,39 @@ class KVController:
             if slot is None:
                 self.dbg["retrieval_skipped_no_slot"] += 1
                 return False
-        if q_vecs is None:
-            self._wait_event(slot.q_ready)
-            q_vecs = self._normalize(self._pad_or_crop(slot.qhost.numpy()))
         B, R = self.B, self.lookahead_k
         kpre, vv, pos, valid = slot.host
-        q = np.ascontiguousarray(q_vecs, dtype=np.float32).reshape(B, -1, self.faiss_dim)
-        stores = (ctypes.c_void_p * B)(*[self.rings[li][b].handle for b in range(B)])
-        N.check(N.lib().hc_cold_retrieve(stores, B, q.ctypes.data, q.shape[1] * self.faiss_dim, self.faiss_dim, R,
+        if q_vecs is None:
+            # pooled on the device: raw (B,D) or (B,Hk,D) fp32, cropped or
+            # padded and normalised inside the native call
+            self._wait_event(slot.q_ready)
+            q = slot.qhost
+            q_ptr, q_dim, norm = q.data_ptr(), q.shape[-1], int(self.normalize_for_ip)
+            q_sb, q_sh = q.stride(0), (q.stride(1) if q.dim() == 3 else 0)
+        else:
+            q = np.ascontiguousarray(q_vecs, dtype=np.float32).reshape(B, -1, self.faiss_dim)
+            q_ptr, q_dim, norm = q.ctypes.data, self.faiss_dim, 0
+            q_sb, q_sh = q.shape[1] * self.faiss_dim, self.faiss_dim
+        # the rows of LlamaRotaryEmbedding.forward's tables at the retrieved
+        # positions (rows past the hits hold position 0 and stay masked),
+        # gathered in the same native call from the table the decode thread
+        # computed
+        tab = table is not None and self._rope is not None
+        missing = ctypes.c_int64(0)
+        N.check(N.lib().hc_cold_retrieve(self._store_ptrs[li], B, q_ptr, q_sb, q_sh, q_dim, norm, R,
                                          int(self.per_head_retrieval), kpre.data_ptr(), vv.data_ptr(),
-                                         pos.data_ptr(), valid.data_ptr(), int(nthreads)), "hc_cold_retrieve")
-        rope = self._rope
-        slot.has_tab = rope is not None
-        if rope is not None:
-            # the tables of LlamaRotaryEmbedding.forward at the retrieved
-            # positions (rows past the hits hold position 0 and stay masked)
-            cos, sin = ops_rope_tables(pos.reshape(-1, R), rope[0], rope[1], self.dtype)
+                                         pos.data_ptr(), valid.data_ptr(),
+                                         table.ctypes.data if tab else None, table.shape[0] if tab else 0,
+                                         table.shape[1] if tab else 0, slot.tab.data_ptr() if tab else None,
+                                         ctypes.byref(missing), int(nthreads)), "hc_cold_retrieve")
+        slot.has_tab = tab
+        if tab and missing.value:
+            # a token evicted after the search was scheduled lies past the
+            # table: compute this retrieval's rows directly
+            cos, sin = ops_rope_tables(pos.reshape(-1, R), self._rope[0], self._rope[1], self.dtype)
             slot.tab_host[0].view(-1, R, self.D // 2).copy_(cos)
             slot.tab_host[1].view(-1, R, self.D // 2).copy_(sin)
+            self.dbg["rope_rows_direct"] += 1
         with self._retrieval_lock[li]:
             if not bool(valid.any()):
                 slot.state = _Slot.FREE
@@ -545,7 +597,7 @@ class KVController:
         if self.cold_size(li) == 0:
             self.dbg["retrieval_skipped_no_cold"] += 1
             return
-        if self._retrieval_worker(li, self._q_to_vecs_np(q_pre)):
+        if self._retrieval_worker(li, self._q_to_vecs_np(q_pre), table=self._rope_rows()):
             self.dbg["retrieval_launched"] += 1
             self.dbg["retrieval_launched_prefill"] += 1
 
@@ -583,7 +635,7 @@ class KVController:
         else:
             q_vecs = self._pooled_query_np(li)
         with self._retrieval_lock[li]:
-            th = self._spawn(self._retrieval_worker, (li, q_vecs, slot, self.SEARCH_THREADS))
+            th = self._spawn(self._retrieval_worker, (li, q_vecs, slot, self.SEARCH_THREADS, self._rope_rows()))
             self._retrieval_thread[li] = th
             self.dbg["retrieval_launched"] += 1
 
@@ -618,7 +670,7 @@ class KVController:
     def _alloc_dev(self, slot, device):
         slot.dev_block = torch.empty(slot.block.numel(), dtype=torch.uint8, device=device)
         views = _carve(slot.dev_block, self._slot_specs())
-        slot.dev, slot.tab_dev = views[:4], views[4:]
+        slot.dev, slot.tab_dev = views[:4], (views[4][..., 0, :], views[4][..., 1, :])
 
     def _copy_to_device(self, slot):
         """The slot's host-to-device copies on the side stream, after the
@@ -666,8 +718,10 @@ class KVController:
         stream (controller.py:344-380).  dtype is accepted for compatibility:
         staged buffers stay fp32 and the inject kernel converts."""
         li = int(layer_idx)
+        if self._stream is None or not self._inited or self._retrieval_ready_cpu[li] is None:
+            return                       # nothing retrieved (a result landing now is taken next step)
         device = torch.device(device)
-        if device.type != "cuda" or self._stream is None:
+        if device.type != "cuda":
             return
         with self._retrieval_lock[li]:
             slot = self._retrieval_ready_cpu[li]
@@ -692,7 +746,7 @@ class KVController:
     def poll_staged_gpu(self, layer_idx) -> RetrievedKV:
         """Non-blocking check for a staged retrieval (controller.py:382-442)."""
         li = int(layer_idx)
-        if not self._inited or self._stream is None:
+        if not self._inited or self._stream is None or self._staged[li] is None:
             return _NOT_READY
         with self._stage_lock[li]:
             slot = self._staged[li]

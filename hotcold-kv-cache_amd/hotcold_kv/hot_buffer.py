@@ -124,12 +124,14 @@ class HotBuffer:
                         pos_src=pos if self.with_pos else None, pos_dst=self.st["pos"] if self.with_pos else None)
         self.n += T
 
-    def append_attend(self, q, k, v, scaling, pre=None, pos=None):
+    def append_attend(self, q, k, v, scaling, pre=None, pos=None, keepdim=False):
         """Append one token (k, v, pre (B,H,1,D), pos (B,1)) and attend q over
-        the hot rows plus the token, in one launch.  Returns (B,Hq,D)."""
+        the hot rows plus the token, in one launch.  Returns (B,Hq,D), or
+        (B,Hq,1,D) with keepdim."""
         self.ensure(self.n + 1)
         out = ops.decode_append_rows(q, self.st, self.held, self.n + 1, k, v, scaling,
-                                     p_new=pre if self.with_pre else None, pos_new=pos if self.with_pos else None)
+                                     p_new=pre if self.with_pre else None, pos_new=pos if self.with_pos else None,
+                                     keepdim=keepdim)
         self.n += 1
         return out
 

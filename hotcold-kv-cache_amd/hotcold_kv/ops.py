@@ -6,6 +6,7 @@ there is no CPU path.  Workspaces are cached per (device, stream) and grown on
 demand; torch's caching allocator owns all memory.
 """
 
+import ctypes
 import math
 import threading
 
@@ -260,75 +261,134 @@ def decode_attention_append(q, k, v, k_new, v_new, scaling, pre=None, pos=None, 
     return out
 
 
-def decode_append_rows(q, st, lo, S, k_new, v_new, scaling, p_new=None, pos_new=None, held=None, cur_pos=None):
+class _AppendPlan:
+    """hc_decode_attn_append_packed arguments of one hot-buffer storage (a
+    `st` dict): the shape, the buffers' base pointers and strides, the dtype
+    and the stream's workspace are filled in once; a call validates its
+    inputs and rewrites only the per-step fields."""
+
+    def __init__(self, st, Hq):
+        k, v = st["k"], st["v"]
+        if k.dim() != 4 or v.shape != k.shape or v.dtype != k.dtype or k.stride(-1) != 1 or v.stride(-1) != 1 \
+                or not k.is_cuda:
+            raise RuntimeError("decode_append_rows: hot-buffer K/V storage must be matching 4D device tensors")
+        B, Hk, cap, D = k.shape
+        self.tensors = (k, v, st.get("p"), st.get("pos"))     # the storage the pointers below belong to
+        self.B, self.Hq, self.Hk, self.cap, self.D = B, int(Hq), Hk, cap, D
+        self.dtype, self.dev, self.es = k.dtype, k.device, k.element_size()
+        self.qshape, self.tshape = (B, self.Hq, D), (B, Hk, D)
+        a = self.a = N.DecodeAppendArgs()
+        a.dtype, a.B, a.Hq, a.Hk, a.D = N.dtype_code(k.dtype), B, self.Hq, Hk, D
+        ks, vs = k.stride(), v.stride()
+        a.k_sb, a.k_sh, a.k_ss = ks[0], ks[1], ks[2]
+        a.v_sb, a.v_sh, a.v_ss = vs[0], vs[1], vs[2]
+        self.k0, self.v0, self.krow, self.vrow = k.data_ptr(), v.data_ptr(), ks[2] * self.es, vs[2] * self.es
+        self.p = st.get("p")
+        if self.p is not None:
+            ps = self.p.stride()
+            a.pd_sb, a.pd_sh, a.pd_ss = ps[0], ps[1], ps[2]
+            self.p0, self.prow = self.p.data_ptr(), ps[2] * self.es
+        self.pos = st.get("pos")
+        if self.pos is not None:
+            a.posd_sb = self.pos.stride(0)
+            self.pos0 = self.pos.data_ptr()
+        a.o_sb, a.o_sh = self.Hq * D, D
+        self.stream, self.ws = None, None
+        self.lib = N.lib()
+
+    def _bind_stream(self, stream, S):
+        need = self.lib.hc_decode_attn_workspace_size(self.B, self.Hq, self.Hk, self.D, max(S, self.cap), 0, 0)
+        self.ws = _workspace("decode", self.dev, need)
+        self.a.workspace, self.a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
+        self.stream = stream
+
+    def run(self, q, lo, S, k_new, v_new, scaling, p_new, pos_new, held, cur_pos, keepdim):
+        B, Hk, D = self.B, self.Hk, self.D
+        q3 = q[:, :, 0, :] if q.dim() == 4 else q
+        kn = k_new[:, :, 0, :] if k_new.dim() == 4 else k_new
+        vn = v_new[:, :, 0, :] if v_new.dim() == 4 else v_new
+        if q3.shape != self.qshape or kn.shape != self.tshape or vn.shape != self.tshape or q3.dtype != self.dtype \
+                or kn.dtype != self.dtype or vn.dtype != self.dtype or q3.device != self.dev \
+                or kn.device != self.dev or vn.device != self.dev \
+                or q3.stride(-1) != 1 or kn.stride(-1) != 1 or vn.stride(-1) != 1:
+            raise RuntimeError("decode_append_rows: q (B,Hq,D), k_new / v_new (B,Hk,D) device rows in the buffer's "
+                               "dtype required")
+        if lo < 0 or S < 1 or lo + S > self.cap:
+            raise RuntimeError(f"decode_append_rows: rows {lo}..{lo + S - 1} outside the buffer's {self.cap}")
+        a = self.a
+        a.S = S
+        a.q, (a.q_sb, a.q_sh) = q3.data_ptr(), q3.stride()[:2]
+        a.k, a.v = self.k0 + lo * self.krow, self.v0 + lo * self.vrow
+        a.k_new, (a.kn_sb, a.kn_sh) = kn.data_ptr(), kn.stride()[:2]
+        a.v_new, (a.vn_sb, a.vn_sh) = vn.data_ptr(), vn.stride()[:2]
+        if p_new is not None:
+            if self.p is None:
+                raise RuntimeError("decode_append_rows: p_new given but the buffer keeps no pre-RoPE keys")
+            pn = p_new[:, :, 0, :] if p_new.dim() == 4 else p_new
+            if pn.shape != self.tshape or pn.stride(-1) != 1 or pn.dtype != self.dtype or pn.device != self.dev:
+                raise RuntimeError("decode_append_rows: p_new must be (B,Hk,D) in the buffer's dtype")
+            a.p_new, (a.pn_sb, a.pn_sh) = pn.data_ptr(), pn.stride()[:2]
+            a.p_dst = self.p0 + lo * self.prow
+        else:
+            a.p_new = a.p_dst = None
+        if pos_new is not None:
+            if self.pos is None:
+                raise RuntimeError("decode_append_rows: pos_new given but the buffer keeps no positions")
+            if pos_new.dtype != torch.int64 or pos_new.shape[0] != B or pos_new.device != self.dev:
+                raise RuntimeError("decode_append_rows: pos_new must be (B,1) int64")
+            a.pos_new, a.posn_sb = pos_new.data_ptr(), pos_new.stride(0)
+            a.pos_dst = self.pos0 + lo * 8
+        else:
+            a.pos_new = a.pos_dst = None
+        if held is not None and int(held[2]) > 0:
+            hp, hv, R = held
+            if hv.dtype == torch.bool:
+                hv = hv.view(torch.uint8)
+            if hp.dtype != torch.int64 or int(R) > S - 1 or hp.shape[0] != B or hv.shape[0] != B \
+                    or hp.shape[-1] < R or hv.shape[-1] < R or hp.stride(-1) != 1 or hv.stride(-1) != 1 \
+                    or (hp.dim() == 3 and hp.shape[1] != Hk) or (hv.dim() == 3 and hv.shape[1] != Hk) \
+                    or hp.device != self.dev or hv.device != self.dev \
+                    or (cur_pos is not None and (cur_pos.dtype != torch.int64 or cur_pos.device != self.dev)):
+                raise RuntimeError("decode_append_rows: held = (pos (B,R)|(B,Hk,R) int64, valid, R <= S-1)")
+            a.held_len = int(R)
+            a.held_pos, a.hp_sb, a.hp_sh = hp.data_ptr(), hp.stride(0), hp.stride(1) if hp.dim() == 3 else 0
+            a.held_valid, a.hv_sb, a.hv_sh = hv.data_ptr(), hv.stride(0), hv.stride(1) if hv.dim() == 3 else 0
+            a.cur_pos = None if cur_pos is None else cur_pos.data_ptr()
+        else:
+            a.held_len, a.held_pos, a.held_valid, a.cur_pos = 0, None, None, None
+        a.scaling = scaling
+        out = torch.empty((B, self.Hq, 1, D) if keepdim else (B, self.Hq, D), dtype=self.dtype, device=self.dev)
+        a.out = out.data_ptr()
+        stream = stream_handle(self.dev)
+        if stream != self.stream:
+            self._bind_stream(stream, S)
+        rc = self.lib.hc_decode_attn_append_packed(ctypes.addressof(a), stream)
+        if rc == N.HC_ERR_WORKSPACE:
+            self._bind_stream(stream, S)        # a longer buffer than the one the workspace was sized for
+            rc = self.lib.hc_decode_attn_append_packed(ctypes.addressof(a), stream)
+        N.check(rc, "hc_decode_attn_append")
+        return out
+
+
+def decode_append_rows(q, st, lo, S, k_new, v_new, scaling, p_new=None, pos_new=None, held=None, cur_pos=None,
+                       keepdim=False):
     """decode_attention_append over rows lo .. lo+S-1 of a hot buffer's
     storage, addressed by offset instead of through tensor views (the
-    per-layer decode call of the drop-in; same launch, less host work).
+    per-layer decode call of the drop-in; same launch, less host work: the
+    storage's packed argument struct is kept in st and only the per-step
+    fields are rewritten).
 
     st: {"k", "v"[, "p", "pos"]} -- (B,Hk,cap,D) K/V/pre-RoPE rows and
     (B,cap) int64 positions.  Row lo+S-1 receives k_new / v_new (and p_new,
     pos_new (B,1)).  held = (pos, valid, R): the first R attended rows are the
-    held slot, masked with valid & (pos <= cur_pos).  Returns out (B,Hq,D)."""
-    k, v = st["k"], st["v"]
-    B, Hk, cap, D = k.shape
-    q3 = q[:, :, 0, :] if q.dim() == 4 else q
-    kn = k_new[:, :, 0, :] if k_new.dim() == 4 else k_new
-    vn = v_new[:, :, 0, :] if v_new.dim() == 4 else v_new
-    if not q3.is_cuda or q3.shape[0] != B or q3.shape[2] != D or tuple(kn.shape) != (B, Hk, D) \
-            or tuple(vn.shape) != (B, Hk, D) or q3.dtype != k.dtype or kn.dtype != k.dtype or vn.dtype != k.dtype \
-            or q3.stride(-1) != 1 or kn.stride(-1) != 1 or vn.stride(-1) != 1:
-        raise RuntimeError("decode_append_rows: q (B,Hq,D), k_new / v_new (B,Hk,D) device rows in the buffer's "
-                           "dtype required")
-    if lo < 0 or S < 1 or lo + S > cap:
-        raise RuntimeError(f"decode_append_rows: rows {lo}..{lo + S - 1} outside the buffer's {cap}")
-    Hq = q3.shape[1]
-    es = k.element_size()
-    ks, vs = k.stride(), v.stride()
-    pn_args = [None, 0, 0, None, 0, 0, 0]
-    if p_new is not None:
-        pst = st["p"]
-        pn = p_new[:, :, 0, :] if p_new.dim() == 4 else p_new
-        if tuple(pn.shape) != (B, Hk, D) or pn.stride(-1) != 1 or pn.dtype != k.dtype:
-            raise RuntimeError("decode_append_rows: p_new must be (B,Hk,D) in the buffer's dtype")
-        ps = pst.stride()
-        pn_args = [pn.data_ptr(), pn.stride(0), pn.stride(1), pst.data_ptr() + lo * ps[2] * es, ps[0], ps[1], ps[2]]
-    pos_args = [None, 0, None, 0]
-    if pos_new is not None:
-        posst = st["pos"]
-        if pos_new.dtype != torch.int64 or pos_new.shape[0] != B:
-            raise RuntimeError("decode_append_rows: pos_new must be (B,1) int64")
-        pos_args = [pos_new.data_ptr(), pos_new.stride(0), posst.data_ptr() + lo * 8, posst.stride(0)]
-    held_args = [0, None, 0, 0, None, 0, 0, None]
-    if held is not None and int(held[2]) > 0:
-        hp, hv, R = held
-        if hv.dtype == torch.bool:
-            hv = hv.view(torch.uint8)
-        if hp.dtype != torch.int64 or int(R) > S - 1 or hp.shape[0] != B or hv.shape[0] != B \
-                or hp.shape[-1] < R or hv.shape[-1] < R or hp.stride(-1) != 1 or hv.stride(-1) != 1 \
-                or (hp.dim() == 3 and hp.shape[1] != Hk) or (hv.dim() == 3 and hv.shape[1] != Hk):
-            raise RuntimeError("decode_append_rows: held = (pos (B,R)|(B,Hk,R) int64, valid, R <= S-1)")
-        held_args = [int(R), hp.data_ptr(), hp.stride(0), hp.stride(1) if hp.dim() == 3 else 0,
-                     hv.data_ptr(), hv.stride(0), hv.stride(1) if hv.dim() == 3 else 0,
-                     None if cur_pos is None else cur_pos.data_ptr()]
-    out = torch.empty((B, Hq, D), dtype=k.dtype, device=k.device)
-    lib = N.lib()
-    ws = _workspace("decode", k.device, lib.hc_decode_attn_workspace_size(B, Hq, Hk, D, S, 0, 0))
-    rc = lib.hc_decode_attn_append(
-        N.dtype_code(k.dtype), B, Hq, Hk, D, S,
-        q3.data_ptr(), q3.stride(0), q3.stride(1),
-        k.data_ptr() + lo * ks[2] * es, ks[0], ks[1], ks[2],
-        v.data_ptr() + lo * vs[2] * es, vs[0], vs[1], vs[2],
-        kn.data_ptr(), kn.stride(0), kn.stride(1),
-        vn.data_ptr(), vn.stride(0), vn.stride(1),
-        *pn_args, *pos_args,
-        None, 0,
-        *held_args,
-        float(scaling),
-        out.data_ptr(), out.stride(0), out.stride(1),
-        ws.data_ptr(), ws.numel(), 0,
-        stream_handle(k.device))
-    N.check(rc, "hc_decode_attn_append")
-    return out
+    held slot, masked with valid & (pos <= cur_pos).  Returns out (B,Hq,D),
+    or (B,Hq,1,D) with keepdim."""
+    Hq = q.shape[1]
+    plan = st.get("_plan")
+    if plan is None or plan.Hq != Hq or plan.tensors[0] is not st["k"] or plan.tensors[1] is not st["v"] \
+            or plan.tensors[2] is not st.get("p") or plan.tensors[3] is not st.get("pos"):
+        plan = st["_plan"] = _AppendPlan(st, Hq)
+    return plan.run(q, int(lo), int(S), k_new, v_new, float(scaling), p_new, pos_new, held, cur_pos, keepdim)
 
 
 def decode_attention_h2o(q, k, v, scaling, acc, out=None, num_splits=0):

@@ -121,7 +121,9 @@ def hotcold_attention(kvctrl, layer, li, q_pre, k_pre, v, q_post, k_post, pos_ne
         held = kvctrl.resolve_held(li, injected)
         if fused:
             out = layer.append_attend(q_post, k_post, v, k_pre, pos_new, scaling, held)
-        elif held is not None:
+            kvctrl.dbg["triton_decode_calls"] += 1
+            return out                                                    # (B,Hq,1,D)
+        if held is not None:
             pos_h, valid_h, R = held
             k_att, v_att = layer.buf.attended(with_held=True)
             k_att = k_att[:, :, layer.buf.held - R:]

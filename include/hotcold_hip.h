@@ -134,6 +134,41 @@ int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t 
                           void* stream);
 
 /*
+ * hc_decode_attn_append with its arguments in one struct: the same launch,
+ * checks and results; a per-layer decode loop keeps one struct per hot
+ * buffer and rewrites only the fields that change from step to step (q, the
+ * token's rows, S, the held slot, out), which saves the host the marshalling
+ * of 48 scalar arguments per call.  Replaces the same reference interface as
+ * hc_decode_attn_append (kernels.py:77-137, call site patch.py:295-305).
+ * Every field is 8 bytes wide (sizes, strides and the dtype code as int64,
+ * pointers, scaling as double), so the layout has no padding;
+ * hc_decode_append_args_size() returns sizeof for a binding to check.
+ */
+typedef struct hc_decode_append_args {
+  int64_t dtype, B, Hq, Hk, D, S;
+  const void* q; int64_t q_sb, q_sh;
+  void* k; int64_t k_sb, k_sh, k_ss;
+  void* v; int64_t v_sb, v_sh, v_ss;
+  const void* k_new; int64_t kn_sb, kn_sh;
+  const void* v_new; int64_t vn_sb, vn_sh;
+  const void* p_new; int64_t pn_sb, pn_sh;
+  void* p_dst; int64_t pd_sb, pd_sh, pd_ss;
+  const int64_t* pos_new; int64_t posn_sb;
+  int64_t* pos_dst; int64_t posd_sb;
+  const uint8_t* mask; int64_t mask_sb;
+  int64_t held_len;
+  const int64_t* held_pos; int64_t hp_sb, hp_sh;
+  const uint8_t* held_valid; int64_t hv_sb, hv_sh;
+  const int64_t* cur_pos;
+  double scaling;
+  void* out; int64_t o_sb, o_sh;
+  void* workspace; int64_t workspace_bytes, num_splits;
+} hc_decode_append_args;
+
+int hc_decode_attn_append_packed(const hc_decode_append_args* args, void* stream);
+int64_t hc_decode_append_args_size(void);
+
+/*
  * hc_decode_attn_append without a workspace: no counterpart in the reference.
  * It is for callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The arguments and results
@@ -446,10 +481,20 @@ int hc_cold_export(const void* store, float* kpre, float* v, int64_t* pos, float
  * head-mean vectors; outputs pos/valid [B][R]) or per (batch row, head)
  * (per_head = 1: q[b][h]; pos/valid [B][heads][R]).  kpre/v out are
  * [B][heads][R][head_dim]; rows past the hits are zero with valid = 0.  q has
- * element strides (q_sb, q_sh).  nthreads <= 0 picks min(cores, 16). */
-int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh, int64_t R,
-                     int per_head, float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out,
-                     int64_t nthreads);
+ * q_dim floats per query, element strides (q_sb, q_sh); it is cropped or
+ * zero-padded to vec_dim and, with normalize_q, divided by max(||q||, 1e-12)
+ * as the stored vectors are (squares summed in fp64 in dimension order,
+ * quotient rounded to fp32).  tab (may be NULL): a table of tab_rows rows of
+ * tab_row_bytes bytes indexed by position; the row of every retrieved
+ * position (position 0 past the hits) is copied to tab_out, laid out like
+ * pos_out, and *tab_missing (may be NULL) counts positions beyond the table
+ * (their rows are zero).  This carries the rotary tables of the retrieved
+ * positions (controller.py:365-373 re-rotates them).  nthreads <= 0 picks
+ * min(cores, 16). */
+int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh, int64_t q_dim,
+                     int normalize_q, int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
+                     uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes,
+                     uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads);
 
 #ifdef __cplusplus
 }

@@ -6,6 +6,7 @@ the bit-defined contract; attention outputs within max-abs 2e-3 (fp16),
 the model's own rotation (and equal in at least 99.9% of elements).
 """
 
+import contextlib
 import math
 
 import numpy as np
@@ -256,6 +257,73 @@ def test_decode_append_held_slot_mask_pre_and_pos(per_head):
         m = torch.cat([held & mask, torch.ones((B, 1), dtype=torch.bool)], 1)
         want = ref.decode_attention(q[:, h * G:(h + 1) * G], kw[:, h:h + 1, :n + 1], vw[:, h:h + 1, :n + 1], 0.088, m)
         assert np.abs(out[:, h * G:(h + 1) * G] - want).max() <= 2e-3, h
+
+
+def test_packed_append_rows_equal_the_scalar_entry():
+    """decode_append_rows (hc_decode_attn_append_packed over a reused argument
+    struct) and decode_attention_append (hc_decode_attn_append) on twin
+    buffers: identical outputs and rows, step after step, across a held slot
+    with per-head positions, growth of the buffer (a new storage, so a new
+    struct), a stream switch (the workspace follows the stream) and a second
+    query-head count on the same storage."""
+    from hotcold_kv.hot_buffer import HotBuffer
+    B, Hq, Hk, D, R, n0 = 2, 32, 8, 128, 16, 300
+    dtype = torch.float16
+    g = torch.Generator().manual_seed(7)
+    bufs = [HotBuffer(B, Hk, D, dtype, DEV, n0 + 8, held=R, with_pre=True, with_pos=True) for _ in range(2)]
+    k0, v0, p0 = (torch.randn((B, Hk, n0, D), generator=g).to(dtype).to(DEV) for _ in range(3))
+    pos0 = torch.arange(n0, device=DEV).view(1, -1).expand(B, -1).contiguous()
+    hk, hv = torch.randn((B, Hk, R, D), generator=g).to(dtype), torch.randn((B, Hk, R, D), generator=g).to(dtype)
+    for b in bufs:
+        b.append(k0, v0, p0, pos0)
+        kb, vb = b.held_storage()
+        kb[:, :, :R], vb[:, :, :R] = hk.to(DEV), hv.to(DEV)
+    hpos = torch.randint(0, n0 + 40, (B, Hk, R), generator=g).to(DEV)
+    hval = (torch.rand((B, Hk, R), generator=g) < 0.8).to(DEV)
+    side = torch.cuda.Stream(device=DEV)
+    for step in range(24):                                   # grows past n0 + 8 on step 8
+        q = torch.randn((B, Hq, 1, D), generator=g).to(dtype).to(DEV)
+        kn, vn, pn = (torch.randn((B, Hk, 1, D), generator=g).to(dtype).to(DEV) for _ in range(3))
+        posn = torch.full((B, 1), n0 + step, dtype=torch.int64, device=DEV)
+        held = (hpos, hval, R) if step % 3 else None
+        on_side = step in (5, 6, 15)
+        if on_side:
+            side.wait_stream(torch.cuda.current_stream(DEV))
+        with torch.cuda.stream(side) if on_side else contextlib.nullcontext():
+            outs = []
+            for i, b in enumerate(bufs):
+                b.ensure(b.n + 1)
+                r = R if held else 0
+                lo, S = b.held - r, r + b.n + 1
+                if i == 0:
+                    o = ops.decode_append_rows(q, b.st, lo, S, kn, vn, 0.088, p_new=pn, pos_new=posn, held=held,
+                                               cur_pos=posn if held else None, keepdim=True)
+                else:
+                    st = b.st
+                    o = ops.decode_attention_append(
+                        q, st["k"][:, :, lo:lo + S], st["v"][:, :, lo:lo + S], kn, vn, 0.088,
+                        pre=(pn, st["p"][:, :, lo:]), pos=(posn, st["pos"][:, lo:]), held_len=r,
+                        held_pos=hpos if held else None, held_valid=hval if held else None,
+                        cur_pos=posn[0] if held else None).unsqueeze(2)
+                b.n += 1
+                outs.append(o)
+        torch.cuda.current_stream(DEV).wait_stream(side)
+        assert torch.equal(outs[0], outs[1]), step
+    torch.cuda.synchronize()
+    rows = bufs[0].held + bufs[0].n
+    assert bufs[1].held + bufs[1].n == rows and bufs[0].cap > n0 + 8
+    for name in ("k", "v", "p"):
+        assert torch.equal(bufs[0].st[name][:, :, :rows], bufs[1].st[name][:, :, :rows]), name
+    assert torch.equal(bufs[0].st["pos"][:, :rows], bufs[1].st["pos"][:, :rows])
+    # a second query-head count on the same storage gets its own struct
+    q8 = torch.randn((B, 8, 1, D), generator=g).to(dtype).to(DEV)
+    kn, vn = (torch.randn((B, Hk, 1, D), generator=g).to(dtype).to(DEV) for _ in range(2))
+    b0 = bufs[0]
+    b0.ensure(b0.n + 1)
+    o8 = ops.decode_append_rows(q8, b0.st, b0.held, b0.n + 1, kn, vn, 0.088)
+    want = ref.decode_attention(q8.cpu(), b0.st["k"][:, :, b0.held:b0.held + b0.n + 1].cpu(),
+                                b0.st["v"][:, :, b0.held:b0.held + b0.n + 1].cpu(), 0.088)
+    assert np.abs(o8.float().cpu().numpy() - want).max() <= 2e-3
 
 
 def test_decode_append_argument_errors():

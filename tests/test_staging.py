@@ -11,6 +11,7 @@ a copy can be held "not ready" for as long as a test wants.
 
 import torch
 
+from hotcold_kv import ops
 from hotcold_kv.controller import KVController, _Slot, _block_layout
 from hotcold_kv.datatypes import EvictedKV
 
@@ -231,13 +232,14 @@ def test_two_slots_per_layer_are_preallocated():
 
 
 def test_slot_buffers_are_views_of_one_block():
-    """k_pre, v, pos, valid, cos, sin carved from one block in that order,
-    256-byte aligned and disjoint; one copy of nbytes[0] carries a retrieval
-    without tables, nbytes[1] one with them."""
+    """k_pre, v, pos, valid and the rotary tables carved from one block in
+    that order, 256-byte aligned and disjoint; one copy of nbytes[0] carries
+    a retrieval without tables, nbytes[1] one with them; cos and sin are the
+    two halves of each table row."""
     ctrl = _ctrl(per_head_retrieval=True)
     with ctrl._retrieval_lock[0]:
         sl = ctrl._take_slot(0)
-    views = list(sl.host) + list(sl.tab_host)
+    views = list(sl.host) + [sl.tab]
     base = sl.block.data_ptr()
     offs, nbytes = _block_layout(ctrl._slot_specs())
     spans = []
@@ -247,8 +249,86 @@ def test_slot_buffers_are_views_of_one_block():
         spans.append((off, off + t.numel() * t.element_size()))
     for (a0, a1), (b0, b1) in zip(spans, spans[1:]):
         assert a1 <= b0
-    assert nbytes == (spans[3][1], spans[5][1]) == sl.nbytes
+    assert nbytes == (spans[3][1], spans[4][1]) == sl.nbytes
     assert sl.block.numel() == nbytes[1]
+    cos, sin = sl.tab_host
+    assert cos.data_ptr() == sl.tab.data_ptr() and sin.data_ptr() == cos.data_ptr() + (D // 2) * cos.element_size()
+    assert cos.stride() == sin.stride() and cos.shape == (1, HK, 4, D // 2)
     # writes through the views land in the block
     sl.host[2].fill_(7)
     assert sl.block[offs[2]:offs[2] + 8].view(torch.int64).item() == 7
+
+
+def _rope_ctrl(dtype=torch.float16):
+    ctrl = HostCtrl(cpu_buffer_size=64, faiss_dim=D, lookahead_k=4, window_size=4, hold_retrieved=True,
+                    per_head_retrieval=True)
+    ctrl._lazy_init(torch.zeros(1, HK, 1, D, dtype=dtype), n_layers=1)
+    ctrl._stream = "side"
+    inv = 1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D))
+    ctrl.set_rope(inv, 1.0)
+    return ctrl, inv
+
+
+def test_retrieval_carries_the_rotary_rows_of_its_positions():
+    """The search thread gathers the rows of the table computed on the decode
+    thread: equal to the rotary module's tables at the retrieved positions."""
+    for dtype in (torch.float16, torch.bfloat16, torch.float32):
+        ctrl, inv = _rope_ctrl(dtype)
+        _fill(ctrl)
+        _window(ctrl)
+        sl = ctrl._retrieval_ready_cpu[0]
+        assert sl.has_tab and ctrl.dbg["rope_rows_direct"] == 0
+        pos = sl.host[2]
+        cos, sin = ops.rope_tables(pos.reshape(-1, 4), inv, 1.0, dtype)
+        assert torch.equal(sl.tab_host[0].reshape(cos.shape), cos)
+        assert torch.equal(sl.tab_host[1].reshape(sin.shape), sin)
+        assert ctrl._rope_tab.shape[0] >= 112
+
+
+def test_positions_past_the_table_are_computed_directly():
+    ctrl, inv = _rope_ctrl()
+    _fill(ctrl)
+    small = ctrl._rope_rows()[:50]               # a table from before the evictions reached position 100
+    ctrl._rope_rows = lambda: small
+    _window(ctrl)
+    sl = ctrl._retrieval_ready_cpu[0]
+    assert sl.has_tab and ctrl.dbg["rope_rows_direct"] == 1
+    cos, sin = ops.rope_tables(sl.host[2].reshape(-1, 4), inv, 1.0, torch.float16)
+    assert torch.equal(sl.tab_host[0].reshape(cos.shape), cos)
+    assert torch.equal(sl.tab_host[1].reshape(sin.shape), sin)
+
+
+def test_native_query_normalisation_equals_the_host_one():
+    """A query pooled on the device reaches the native call raw and is
+    cropped / padded and normalised there; a host-pooled one is normalised
+    by _normalize first.  Both retrieve the same tokens, and _normalize is
+    the dimension-order fp64 formula."""
+    import math
+
+    import numpy as np
+    for dim in (D, 12, 20):                        # as is, cropped, padded
+        ctrl = _ctrl(per_head_retrieval=True, faiss_dim=dim)
+        ctrl._wait_event = lambda ev: None
+        _fill(ctrl, n=40)
+        g = torch.Generator().manual_seed(dim)
+        for trial in range(4):
+            raw = torch.randn(1, HK, D, generator=g)
+            got = []
+            for host_side in (True, False):
+                with ctrl._retrieval_lock[0]:
+                    sl = ctrl._take_slot(0)
+                if host_side:
+                    assert ctrl._retrieval_worker(0, ctrl._normalize(ctrl._pad_or_crop(raw.numpy())), slot=sl)
+                else:
+                    sl.qhost = raw.clone()
+                    assert ctrl._retrieval_worker(0, None, slot=sl)
+                got.append((sl.host[2].clone(), sl.host[0].clone()))
+                ctrl._retrieval_ready_cpu[0] = None
+                sl.state = _Slot.FREE
+            assert torch.equal(got[0][0], got[1][0]) and torch.equal(got[0][1], got[1][1]), (dim, trial)
+        x = ctrl._pad_or_crop(raw.numpy())[0, 1].astype(np.float64)
+        ss = 0.0
+        for t in x.tolist():
+            ss += t * t
+        want = (x / max(math.sqrt(ss), 1e-12)).astype(np.float32)
+        assert np.array_equal(ctrl._normalize(ctrl._pad_or_crop(raw.numpy()))[0, 1], want)
