@@ -685,7 +685,9 @@ def hotcold_pipeline(w, dev, profile_steps=None):
                         cpu_buffer_size=w.seq_len, faiss_dim=w.head_dim, window_size=w.retrieve_every,
                         query_pool_size=4, lookahead_k=w.held, hold_retrieved=True, per_head_retrieval=True,
                         profile_overlap=True, enable_asserts=False)
-    hp.set_active_rotary_emb(_Rotary(w, dev))
+    rot = _Rotary(w, dev)
+    hp.set_active_rotary_emb(rot)
+    ctrl.set_rope(rot.inv_freq, rot.attention_scaling)     # as the patched prefill does before its update
     layers = [HotColdLayer(ctrl) for _ in range(L)]
     steps = w.decode_steps if profile_steps is None else profile_steps
     toks = [[synthetic.make_decode_token(w, l, t, seed=0, device=dev) for l in range(L)] for t in range(steps)]
@@ -729,7 +731,11 @@ def hotcold_pipeline(w, dev, profile_steps=None):
         "step_us_wall_median": round(statistics.median(step_ms) * 1e3, 1),
         "step_us_wall_without_retrieval_median": round(statistics.median(other) * 1e3, 1) if other else None,
         "layer_us_wall_mean": round(total_ms * 1e3 / steps / L, 2),
-        "retrievals": d["retrieval_launched"], "prefetch_launched": d["prefetch_launched"],
+        "retrievals": d["retrieval_launched"],
+        "retrievals_scheduled": L * (steps // w.retrieve_every),
+        "retrievals_skipped_search_running": L * (steps // w.retrieve_every) - d["retrieval_launched"]
+        - d["retrieval_skipped_no_slot"] - d["retrieval_skipped_no_cold"],
+        "prefetch_launched": d["prefetch_launched"],
         "prefetch_ready": d["prefetch_ready"],
         "ready_rate": round(d["prefetch_ready"] / max(1, d["prefetch_launched"]), 4),
         "prefetch_not_ready_checks": d["prefetch_not_ready_checks"],

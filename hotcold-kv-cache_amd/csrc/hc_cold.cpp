@@ -20,8 +20,9 @@
 //
 // Storage is one uninitialised allocation per array at full capacity, so host
 // pages are touched only as tokens arrive and never copied on growth.  Search
-// vectors are kept dimension-major ([vec_head][dim][slot]) so the scan over
-// slots is a contiguous, vectorisable loop per dimension.  Large adds fill
+// vectors are kept in 16-slot tiles ([vec_head][slot/16][dim][16]), so a
+// tile's sums stay in registers while its dimensions stream past
+// contiguously.  Large adds fill
 // their (distinct) slots on host threads.  Each store has a reader/writer
 // lock: adds exclude searches, searches run concurrently.
 
@@ -29,9 +30,13 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <immintrin.h>
+
 #include <algorithm>
 #include <atomic>
 #include <cmath>
+#include <condition_variable>
+#include <deque>
 #include <mutex>
 #include <shared_mutex>
 #include <thread>
@@ -65,14 +70,20 @@ struct ColdStore {
   int64_t head = 0;  // physical slot of the next write once full
   RawArray<float> kpre, v;  // [slot][H][D]
   RawArray<int64_t> pos;    // [slot]
-  RawArray<float> vec;      // [VH][VD][cap]
+  RawArray<float> vec;      // [VH][cap/16][VD][16]: 16-slot tiles, each dimension's 16 values together
+  int64_t capT = 0;         // cap rounded up to a whole tile
+
+  size_t vidx(int64_t vh, int64_t d, int64_t slot) const {
+    return (size_t)vh * VD * capT + (size_t)(slot >> 4) * VD * 16 + (size_t)d * 16 + (slot & 15);
+  }
   mutable std::shared_mutex mu;
 
   bool allocate() {
     kpre.reset((size_t)cap * H * D);
     v.reset((size_t)cap * H * D);
     pos.reset((size_t)cap);
-    vec.reset((size_t)VH * VD * cap);
+    capT = (cap + 15) / 16 * 16;
+    vec.reset((size_t)VH * VD * capT);
     return kpre.p && v.p && pos.p && vec.p;
   }
 
@@ -102,8 +113,7 @@ struct ColdStore {
         for (int64_t d = 0; d < VD; ++d) ss += x[d] * x[d];
         den = std::max(std::sqrt(ss), 1e-12);
       }
-      float* col = &vec[(size_t)vh * VD * cap + slot];
-      for (int64_t d = 0; d < VD; ++d) col[(size_t)d * cap] = (float)(x[d] / den);
+      for (int64_t d = 0; d < VD; ++d) vec[vidx(vh, d, slot)] = (float)(x[d] / den);
     }
   }
 
@@ -127,38 +137,75 @@ struct ColdStore {
   }
 
   // Inner products of query q with the vectors of head vh over physical
-  // slots [s0, s1): fp64, dimensions in order.
-  // Blocked over slots so a block's sums stay in L1 while the dimensions
-  // stream past; every sum still adds its products in dimension order.
+  // slots [s0, s1): fp64, dimensions in order.  A whole 16-slot tile (its
+  // 16 x VD floats contiguous) keeps its sums in four AVX2 registers across
+  // all dimensions; every sum still adds its exact fp32 x fp32 products in
+  // dimension order, so the bits are those of a scalar loop.
   void scan(const float* q, int64_t vh, int64_t s0, int64_t s1, double* ip) const {
-    constexpr int64_t kBlock = 512;
-    double acc[kBlock];
-    for (int64_t b0 = s0; b0 < s1; b0 += kBlock) {
-      const int64_t n = std::min(kBlock, s1 - b0);
-      for (int64_t i = 0; i < n; ++i) acc[i] = 0.0;
-      for (int64_t d = 0; d < VD; ++d) {
-        const double qd = (double)q[d];
-        const float* col = &vec[((size_t)vh * VD + d) * cap + b0];
-        for (int64_t i = 0; i < n; ++i) acc[i] += (double)col[i] * qd;
+    double qd[4096];
+    for (int64_t d = 0; d < VD; ++d) qd[d] = (double)q[d];
+    int64_t s = s0;
+    for (; s < s1 && (s & 15); ++s) ip[s] = scan_one(qd, vh, s);
+    for (; s + 16 <= s1; s += 16) {
+      __m256d a0 = _mm256_setzero_pd(), a1 = _mm256_setzero_pd(), a2 = _mm256_setzero_pd(),
+              a3 = _mm256_setzero_pd();
+      const float* col = &vec[vidx(vh, 0, s)];
+      for (int64_t d = 0; d < VD; ++d, col += 16) {
+        const __m256d x = _mm256_set1_pd(qd[d]);
+        a0 = _mm256_add_pd(a0, _mm256_mul_pd(_mm256_cvtps_pd(_mm_loadu_ps(col)), x));
+        a1 = _mm256_add_pd(a1, _mm256_mul_pd(_mm256_cvtps_pd(_mm_loadu_ps(col + 4)), x));
+        a2 = _mm256_add_pd(a2, _mm256_mul_pd(_mm256_cvtps_pd(_mm_loadu_ps(col + 8)), x));
+        a3 = _mm256_add_pd(a3, _mm256_mul_pd(_mm256_cvtps_pd(_mm_loadu_ps(col + 12)), x));
       }
-      memcpy(ip + b0, acc, sizeof(double) * n);
+      _mm256_storeu_pd(ip + s, a0);
+      _mm256_storeu_pd(ip + s + 4, a1);
+      _mm256_storeu_pd(ip + s + 8, a2);
+      _mm256_storeu_pd(ip + s + 12, a3);
     }
+    for (; s < s1; ++s) ip[s] = scan_one(qd, vh, s);
   }
 
-  // Top-r logical indices by (ip desc, logical asc).
+  double scan_one(const double* qd, int64_t vh, int64_t slot) const {
+    double acc = 0.0;
+    for (int64_t d = 0; d < VD; ++d) acc += (double)vec[vidx(vh, d, slot)] * qd[d];
+    return acc;
+  }
+
+  // Top-r logical indices by (ip desc, logical asc).  One pass in logical
+  // order keeps the r best in a heap whose top is the worst kept; a token
+  // replaces it only if strictly better, so among equal inner products the
+  // older token stays.  The kept tokens are then sorted best first.
   int64_t select(const double* ip, int64_t r, int64_t* out) const {
     const int64_t n = size;
     r = std::min(r, n);
     if (r <= 0) return 0;
-    std::vector<int64_t> idx((size_t)n);
-    for (int64_t i = 0; i < n; ++i) idx[i] = i;
-    const auto better = [&](int64_t a, int64_t b) {
-      const double x = ip[physical(a)], y = ip[physical(b)];
-      return x > y || (x == y && a < b);
+    struct Cand {
+      double v;
+      int64_t i;
     };
-    if (r < n) std::nth_element(idx.begin(), idx.begin() + r, idx.end(), better);
-    std::sort(idx.begin(), idx.begin() + r, better);
-    memcpy(out, idx.data(), sizeof(int64_t) * r);
+    // a before b: a is better (larger value, then older)
+    const auto better = [](const Cand& a, const Cand& b) { return a.v > b.v || (a.v == b.v && a.i < b.i); };
+    std::vector<Cand> heap;
+    heap.reserve((size_t)r);
+    const int64_t start = size < cap ? 0 : head;  // physical slot of logical 0
+    int64_t logical = 0;
+    const auto visit = [&](int64_t p0, int64_t p1) {
+      for (int64_t p = p0; p < p1; ++p, ++logical) {
+        const Cand c{ip[p], logical};
+        if ((int64_t)heap.size() < r) {
+          heap.push_back(c);
+          std::push_heap(heap.begin(), heap.end(), better);  // top: the worst kept
+        } else if (better(c, heap.front())) {
+          std::pop_heap(heap.begin(), heap.end(), better);
+          heap.back() = c;
+          std::push_heap(heap.begin(), heap.end(), better);
+        }
+      }
+    };
+    visit(start, std::min(start + n, cap));
+    if (start + n > cap) visit(0, start + n - cap);
+    std::sort(heap.begin(), heap.end(), better);
+    for (int64_t j = 0; j < r; ++j) out[j] = heap[(size_t)j].i;
     return r;
   }
 };
@@ -284,7 +331,7 @@ extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t*
     if (vec)
       for (int64_t h = 0; h < s->VH; ++h)
         for (int64_t d = 0; d < s->VD; ++d)
-          vec[(i * s->VH + h) * s->VD + d] = s->vec[((size_t)h * s->VD + d) * s->cap + p];
+          vec[(i * s->VH + h) * s->VD + d] = s->vec[s->vidx(h, d, p)];
   }
   return HC_OK;
 }
@@ -368,4 +415,149 @@ extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, 
   });
   if (tab_missing) *tab_missing = missing.load();
   return HC_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Retrievals as jobs on the library's own worker threads.  The decode thread
+// submits a job and later polls it; a worker waits for the job's event (the
+// pooled query's device-to-host copy), runs hc_cold_retrieve, counts the
+// valid rows, and marks the job done.  No Python runs on the workers, so a
+// search never contends for the interpreter lock with the decode loop.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct RetrieveJob {
+  std::vector<void*> stores;
+  int64_t B = 0, q_sb = 0, q_sh = 0, q_dim = 0, R = 0, tab_rows = 0, tab_row_bytes = 0, nthreads = 0;
+  int64_t n_flags = 0;  // valid_out entries: B * R, or B * heads * R per KV head
+  int normalize_q = 0, per_head = 0;
+  const float* q = nullptr;
+  float* kpre_out = nullptr;
+  float* v_out = nullptr;
+  int64_t* pos_out = nullptr;
+  uint8_t* valid_out = nullptr;
+  const uint8_t* tab = nullptr;
+  uint8_t* tab_out = nullptr;
+  void* wait_event = nullptr;
+  std::mutex mu;
+  std::condition_variable cv;
+  bool done = false;
+  int rc = HC_OK;
+  int64_t n_valid = 0, tab_missing = 0;
+  char msg[512] = "";
+};
+
+class JobQueue {
+ public:
+  void push(RetrieveJob* j, int64_t workers) {
+    std::lock_guard<std::mutex> lk(mu_);
+    const int64_t want = std::max<int64_t>(1, std::min<int64_t>(workers, 16));
+    while ((int64_t)started_ < want) {
+      std::thread(&JobQueue::run, this).detach();  // lives until the process ends
+      ++started_;
+    }
+    jobs_.push_back(j);
+    cv_.notify_one();
+  }
+
+ private:
+  void run() {
+    for (;;) {
+      RetrieveJob* j;
+      {
+        std::unique_lock<std::mutex> lk(mu_);
+        cv_.wait(lk, [&] { return !jobs_.empty(); });
+        j = jobs_.front();
+        jobs_.pop_front();
+      }
+      execute(j);
+    }
+  }
+
+  static void execute(RetrieveJob* j) {
+    int rc = HC_OK;
+    if (j->wait_event) rc = hc_event_synchronize(j->wait_event);
+    int64_t missing = 0, nv = 0;
+    if (rc == HC_OK)
+      rc = hc_cold_retrieve(j->stores.data(), j->B, j->q, j->q_sb, j->q_sh, j->q_dim, j->normalize_q, j->R,
+                            j->per_head, j->kpre_out, j->v_out, j->pos_out, j->valid_out, j->tab, j->tab_rows,
+                            j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
+    if (rc == HC_OK)
+      for (int64_t i = 0; i < j->n_flags; ++i) nv += j->valid_out[i] != 0;
+    std::lock_guard<std::mutex> lk(j->mu);
+    if (rc != HC_OK) snprintf(j->msg, sizeof(j->msg), "%s", hc_last_error());
+    j->rc = rc;
+    j->n_valid = nv;
+    j->tab_missing = missing;
+    j->done = true;
+    j->cv.notify_all();
+  }
+
+  std::mutex mu_;
+  std::condition_variable cv_;
+  std::deque<RetrieveJob*> jobs_;
+  int started_ = 0;
+};
+
+JobQueue& job_queue() {
+  static JobQueue* q = new JobQueue();  // never destroyed: its threads outlive static destruction
+  return *q;
+}
+
+}  // namespace
+
+extern "C" void* hc_cold_retrieve_async(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
+                                        int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
+                                        float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                                        int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
+                                        int64_t nthreads, void* wait_event, int64_t workers) {
+  if (B <= 0 || R <= 0 || q_dim <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out) {
+    set_error(HC_ERR_INVALID, "cold_retrieve_async: bad arguments");
+    return nullptr;
+  }
+  if (tab && (tab_rows <= 0 || tab_row_bytes <= 0 || !tab_out)) {
+    set_error(HC_ERR_INVALID, "cold_retrieve_async: table rows need a size and an output");
+    return nullptr;
+  }
+  for (int64_t b = 0; b < B; ++b)
+    if (!stores[b]) {
+      set_error(HC_ERR_INVALID, "cold_retrieve_async: null store %lld", (long long)b);
+      return nullptr;
+    }
+  RetrieveJob* j = new (std::nothrow) RetrieveJob();
+  if (!j) {
+    set_error(HC_ERR_INVALID, "cold_retrieve_async: out of host memory");
+    return nullptr;
+  }
+  const ColdStore* s0 = as_store(stores[0]);
+  j->stores.assign(stores, stores + B);
+  j->B = B; j->q = q; j->q_sb = q_sb; j->q_sh = q_sh; j->q_dim = q_dim; j->normalize_q = normalize_q;
+  j->R = R; j->per_head = per_head; j->kpre_out = kpre_out; j->v_out = v_out; j->pos_out = pos_out;
+  j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows; j->tab_row_bytes = tab_row_bytes;
+  j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
+  j->n_flags = B * R * (per_head ? s0->H : 1);
+  job_queue().push(j, workers);
+  return j;
+}
+
+extern "C" int hc_cold_job_poll(void* job, int wait, int64_t* n_valid, int64_t* tab_missing) {
+  RetrieveJob* j = reinterpret_cast<RetrieveJob*>(job);
+  if (!j) return set_error(HC_ERR_INVALID, "cold_job_poll: null job");
+  std::unique_lock<std::mutex> lk(j->mu);
+  if (wait) j->cv.wait(lk, [&] { return j->done; });
+  if (!j->done) return 0;
+  if (n_valid) *n_valid = j->n_valid;
+  if (tab_missing) *tab_missing = j->tab_missing;
+  if (j->rc != HC_OK) return set_error(j->rc, "cold_retrieve (worker): %s", j->msg);
+  return 1;
+}
+
+extern "C" void hc_cold_job_free(void* job) {
+  RetrieveJob* j = reinterpret_cast<RetrieveJob*>(job);
+  if (!j) return;
+  {
+    std::unique_lock<std::mutex> lk(j->mu);
+    j->cv.wait(lk, [&] { return j->done; });  // never free a job a worker still holds
+  }
+  delete j;
 }

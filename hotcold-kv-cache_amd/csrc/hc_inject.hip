@@ -148,9 +148,89 @@ __global__ __launch_bounds__(256) void inject_rerope_tab_kernel(InjectTab a) {
   Vec4<T>::store(vout + half + i, w1);
 }
 
+// Pooled retrieval query: out[b][vh][d] = (sum over the window's T query
+// tensors, then over the heads of KV head vh's group -- or over all Hq heads
+// when there is one vector per batch row -- of q[b][h][d]) / (T * heads), in
+// fp32 with the additions in that fixed order.
+constexpr int kMaxPoolRows = 16;
+struct PoolQueryArgs {
+  const void* q[kMaxPoolRows];
+  int64_t sb[kMaxPoolRows];
+  int64_t sh[kMaxPoolRows];
+  int T, Hq, G, D, per_head;
+  float* out;
+};
+
+template <typename T>
+__global__ void pool_query_kernel(PoolQueryArgs a) {
+#pragma clang fp contract(off)
+  const int b = blockIdx.x, vh = blockIdx.y, nvh = gridDim.y;
+  const int h0 = a.per_head ? vh * a.G : 0, nh = a.per_head ? a.G : a.Hq;
+  const float inv = 1.0f / (float)(a.T * nh);
+  for (int d = threadIdx.x; d < a.D; d += blockDim.x) {
+    float acc = 0.0f;
+    // the window rows by constant index (a runtime index into the argument
+    // arrays would copy them to scratch); 8 head loads in flight per batch,
+    // then their adds in order
+#pragma unroll
+    for (int t = 0; t < kMaxPoolRows; ++t) {
+      if (t < a.T) {
+        const T* q = reinterpret_cast<const T*>(a.q[t]) + b * a.sb[t] + d;
+        const int64_t sh = a.sh[t];
+        for (int hb = 0; hb < nh; hb += 8) {
+          float v[8];
+#pragma unroll
+          for (int u = 0; u < 8; ++u) v[u] = hb + u < nh ? to_f32(q[(int64_t)(h0 + min(hb + u, nh - 1)) * sh]) : 0.0f;
+#pragma unroll
+          for (int u = 0; u < 8; ++u)
+            if (hb + u < nh) acc += v[u];
+        }
+      }
+    }
+    a.out[((int64_t)b * nvh + vh) * a.D + d] = acc * inv;
+  }
+}
+
 }  // namespace hc
 
 using namespace hc;
+
+extern "C" int hc_retrieval_query(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t T,
+                                  const void* const* q, const int64_t* q_sb, const int64_t* q_sh, int per_head,
+                                  float* dev_out, float* host_out, void* event, void* stream) {
+  HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16, "retrieval_query: bad dtype");
+  HC_REQUIRE(B > 0 && Hq > 0 && Hk > 0 && D > 0 && T > 0 && Hq % Hk == 0, "retrieval_query: bad shape");
+  HC_REQUIRE(T <= kMaxPoolRows, "retrieval_query: at most %d window rows", kMaxPoolRows);
+  HC_REQUIRE(B <= 65535 && Hk <= 65535, "retrieval_query: B or Hk too large for the grid");
+  HC_REQUIRE(q && q_sb && q_sh && dev_out, "retrieval_query: null pointer");
+  PoolQueryArgs a{};
+  for (int64_t t = 0; t < T; ++t) {
+    HC_REQUIRE(q[t] != nullptr, "retrieval_query: null query row %lld", (long long)t);
+    a.q[t] = q[t];
+    a.sb[t] = q_sb[t];
+    a.sh[t] = q_sh[t];
+  }
+  a.T = (int)T; a.Hq = (int)Hq; a.G = (int)(Hq / Hk); a.D = (int)D; a.per_head = per_head ? 1 : 0;
+  a.out = dev_out;
+  const int nvh = per_head ? (int)Hk : 1;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const dim3 grid((unsigned)B, (unsigned)nvh);
+  const int threads = D >= 256 ? 256 : (D >= 128 ? 128 : 64);
+  if (dtype == HC_DTYPE_F16) hipLaunchKernelGGL(pool_query_kernel<half_t>, grid, dim3(threads), 0, st, a);
+  else if (dtype == HC_DTYPE_BF16) hipLaunchKernelGGL(pool_query_kernel<bf16_t>, grid, dim3(threads), 0, st, a);
+  else hipLaunchKernelGGL(pool_query_kernel<float>, grid, dim3(threads), 0, st, a);
+  int rc = check_launch("pool_query");
+  if (rc != HC_OK) return rc;
+  if (host_out) {
+    const hipError_t e = hipMemcpyAsync(host_out, dev_out, sizeof(float) * B * nvh * D, hipMemcpyDeviceToHost, st);
+    if (e != hipSuccess) return set_error(HC_ERR_HIP, "retrieval_query: hipMemcpyAsync: %s", hipGetErrorString(e));
+  }
+  if (event) {
+    const hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(event), st);
+    if (e != hipSuccess) return set_error(HC_ERR_HIP, "retrieval_query: hipEventRecord: %s", hipGetErrorString(e));
+  }
+  return HC_OK;
+}
 
 extern "C" int hc_inject_rerope_tab(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D, const float* k_pre,
                                     int64_t kp_sb, int64_t kp_sh, int64_t kp_ss, const float* v, int64_t vp_sb,

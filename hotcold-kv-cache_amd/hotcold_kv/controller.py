@@ -27,7 +27,6 @@ again.  A staging superseded before it was polled is recycled once its copy
 is known complete; nothing waits on the host.
 """
 
-import concurrent.futures
 import ctypes
 import math
 import os
@@ -103,8 +102,8 @@ class _Ring:
 
 def _block_layout(specs, align=256):
     """Byte offsets of tensors of the given (shape, dtype) packed into one
-    block, each start aligned to `align`; returns (offsets, (bytes without
-    the last one, total bytes))."""
+    block, each start aligned to `align`; returns (offsets, ends): the byte
+    just past each tensor."""
     offs, off = [], 0
     ends = []
     for shape, dt in specs:
@@ -112,7 +111,7 @@ def _block_layout(specs, align=256):
         offs.append(off)
         off += int(np.prod(shape)) * torch.empty((), dtype=dt).element_size()
         ends.append(off)
-    return offs, (ends[-2], ends[-1])
+    return offs, ends
 
 
 def _carve(block, specs):
@@ -134,7 +133,7 @@ class _Slot:
 
     FREE, FILLING, RETRIEVED, COPYING, STAGED, HELD = range(6)
 
-    def __init__(self, host, tab=None, block=None, nbytes=(0, 0)):
+    def __init__(self, host, tab=None, block=None, nbytes=(0, 0), qhost=None):
         self.host = host            # (kpre, v, pos, valid) pinned host tensors
         self.tab = tab              # pinned rotary tables at pos, (B,Hc,R,2,D/2) cache dtype: [..., 0, :] cos, 1 sin
         self.tab_host = None if tab is None else (tab[..., 0, :], tab[..., 1, :])
@@ -142,7 +141,8 @@ class _Slot:
         self.nbytes = nbytes        # bytes of the block without / with the tables
         self.tab_dev = None
         self.has_tab = False        # the tables were computed for this retrieval
-        self.qhost = None           # pinned pooled query of the search it serves
+        self.qhost = qhost          # pinned pooled query of the search it serves, (B,VH,D) fp32
+        self.qdev = None            # its device twin, written by the pooling kernel
         self.q_ready = None         # event behind the query's copy
         self.dev = None             # device twins, allocated on the first copy
         self.dev_block = None       # the device allocation they are views of
@@ -154,21 +154,42 @@ class _Slot:
         self.released = False       # free_after has been recorded
 
 
-class _Task:
-    """A scheduled search on the controller's worker pool (the handle the
-    reference keeps as a threading.Thread)."""
+class _Job:
+    """A search running on the library's native worker threads
+    (hc_cold_retrieve_async): the handle the reference keeps as a
+    threading.Thread.  It holds the buffers the search reads and writes until
+    the decode thread collects it."""
 
-    def __init__(self, future):
-        self.future = future
+    def __init__(self, handle, slot, has_tab, keep):
+        self.handle, self.slot, self.has_tab, self.keep = handle, slot, has_tab, keep
+        self.result = None          # (n_valid, positions past the table) once done
+        self.error = None           # (status, message) if the search failed
+
+    def poll(self, wait=False):
+        """True once the search is done (or failed: see error)."""
+        if self.result is None:
+            nv, miss = ctypes.c_int64(0), ctypes.c_int64(0)
+            lib = N.lib()
+            rc = lib.hc_cold_job_poll(self.handle, int(wait), ctypes.byref(nv), ctypes.byref(miss))
+            if rc == 0:
+                return False
+            if rc < 0:
+                self.error = (rc, lib.hc_last_error().decode(errors="replace"))
+            lib.hc_cold_job_free(self.handle)
+            self.handle = None
+            self.result = (nv.value, miss.value)
+        return True
 
     def is_alive(self):
-        return not self.future.done()
+        return not self.poll()
 
     def join(self, timeout=None):
-        try:
-            self.future.result(timeout)
-        except concurrent.futures.TimeoutError:
-            pass
+        self.poll(wait=True)
+
+    def __del__(self):
+        h, self.handle = getattr(self, "handle", None), None
+        if h:
+            N.lib().hc_cold_job_free(h)       # waits for the worker to finish with the buffers
 
 
 _NOT_READY = RetrievedKV(k_pre=torch.empty(0), v=torch.empty(0), pos=torch.empty(0, dtype=torch.long),
@@ -178,10 +199,10 @@ _NOT_READY = RetrievedKV(k_pre=torch.empty(0), v=torch.empty(0), pos=torch.empty
 class KVController:
     # staging slots per layer: one held, one in copy, one retrieved, one filling
     MAX_SLOTS = 4
-    # Scheduled searches run on a small pool of worker threads (no thread per
-    # search), each native search on SEARCH_THREADS host threads: every layer
-    # searches in the same decode step, and together they keep to about half
-    # of the cores, so the decode thread is not starved of CPU.
+    # Scheduled searches run as jobs on the library's native worker threads
+    # (no Python, no thread per search), each on SEARCH_THREADS host threads:
+    # every layer searches in the same decode step, and together they keep to
+    # about half of the cores, so the decode thread is not starved of CPU.
     SEARCH_THREADS = 2
     MAX_SEARCH_WORKERS = 4
 
@@ -226,6 +247,7 @@ class KVController:
         self._inited = False
         self.B = self.Hk = self.D = self.n_layers = None
         self.dtype = None
+        self._device = None         # the device of the hot tier (from the first k_pre)
         self._rope = None           # (inv_freq fp32 CPU, attention_scaling) of the model's rotary module
         self._rope_tab = None       # byte rows [position][cos | sin] of the rotary tables (_rope_rows)
         self._max_pos = 0           # largest position in any cold store
@@ -240,7 +262,6 @@ class KVController:
         self._slots = []
         self._held_slot = []
         self._stream = None
-        self._pool = None
         self._evict_dev = None
         self._evict_host = None
         self.last_injected_len = 0
@@ -279,6 +300,7 @@ class KVController:
         B, Hk, _, D = k_pre.shape
         self.B, self.Hk, self.D = int(B), int(Hk), int(D)
         self.dtype = k_pre.dtype
+        self._device = k_pre.device
         self.n_layers = L = int(n_layers)
         vec_heads = self.Hk if self.per_head_retrieval else 1
         self.rings = [[_Ring(self.cpu_buffer_size, self.Hk, self.D, self.faiss_dim, vec_heads,
@@ -314,8 +336,9 @@ class KVController:
 
     def __del__(self):
         try:
-            if self._pool is not None:
-                self._pool.shutdown(wait=True)
+            for th in self._retrieval_thread:
+                if isinstance(th, _Job):
+                    th.join()                   # a search still writing into a slot's buffers
             lib = N.lib()
             for slots in self._slots:
                 for sl in slots:
@@ -453,6 +476,8 @@ class KVController:
         idx = ev.evicted_idx.detach().cpu().contiguous().numpy().astype(np.int64)
         if pos.size:
             self._max_pos = max(self._max_pos, int(pos.max()))
+            if self._rope is not None:
+                self._rope_rows()       # extend the rotary tables now (prefill), not in a decode step
         for b in range(kpre.shape[0]):
             kept = int((idx[b] >= 0).sum())
             if kept == 0:
@@ -477,15 +502,34 @@ class KVController:
         return q.mean(dim=1).mean(dim=1).float()
 
     def _stage_query(self, layer_idx, slot):
-        """Copy the pooled query into the slot's pinned buffer behind an event
-        on the current stream (no host wait)."""
-        qd = self._pooled_query_dev(layer_idx)
-        if slot.qhost is None or tuple(slot.qhost.shape) != tuple(qd.shape):
-            slot.qhost = torch.empty(qd.shape, dtype=torch.float32, pin_memory=True)
-        slot.qhost.copy_(qd, non_blocking=True)
+        """Pool the window's queries on the device into the slot's pinned
+        buffer (hc_retrieval_query: the pooling kernel, the device-to-host
+        copy and the slot's event, on the current stream, no host wait).
+        Windows of more than 64 query rows, or of mixed dtypes, are pooled by
+        torch (_pooled_query_dev) instead."""
+        win = list(self.query_window[int(layer_idx)])
+        q0 = win[0]
+        B, Hq, _, D = q0.shape
+        if slot.qdev is None:
+            self._alloc_dev(slot, q0.device)
         if slot.q_ready is None:
             slot.q_ready = self._event(0)
-        N.check(N.lib().hc_event_record(slot.q_ready, ops_stream(qd.device)), "hc_event_record")
+        stream = ops_stream(q0.device)
+        rows = [(t, r) for t in win for r in range(t.shape[2])]
+        if len(rows) <= 64 and all(t.dtype == q0.dtype and t.shape[:2] == q0.shape[:2] and t.shape[3] == D
+                                   and t.stride(3) == 1 and t.is_cuda for t in win):
+            es = q0.element_size()
+            n = len(rows)
+            ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() + r * t.stride(2) * es for t, r in rows])
+            sb = (ctypes.c_int64 * n)(*[t.stride(0) for t, _ in rows])
+            sh = (ctypes.c_int64 * n)(*[t.stride(1) for t, _ in rows])
+            N.check(N.lib().hc_retrieval_query(N.dtype_code(q0.dtype), B, Hq, self.Hk, D, n, ptrs, sb, sh,
+                                               int(self.per_head_retrieval), slot.qdev.data_ptr(),
+                                               slot.qhost.data_ptr(), slot.q_ready, stream), "hc_retrieval_query")
+            return
+        qd = self._pooled_query_dev(layer_idx).reshape(B, vh, D)
+        slot.qhost.copy_(qd, non_blocking=True)
+        N.check(N.lib().hc_event_record(slot.q_ready, stream), "hc_event_record")
 
     def _wait_event(self, ev):
         N.check(N.lib().hc_event_synchronize(ev), "hc_event_synchronize")
@@ -498,14 +542,17 @@ class KVController:
 
     # -- staging slots ------------------------------------------------------------------
     def _slot_specs(self):
-        """(shape, dtype) of a slot's k_pre, v, pos, valid and rotary tables:
-        the order of their views in the slot's one block (the tables last,
-        so a retrieval without them copies a prefix of the block)."""
+        """(shape, dtype) of a slot's k_pre, v, pos, valid, rotary tables and
+        pooled query: the order of their views in the slot's one block.  A
+        retrieval copies a prefix of the block: through the flags without
+        tables, through the tables with them; the pooled query, last, only
+        travels device to host."""
         B, Hk, D, R = self.B, self.Hk, self.D, self.lookahead_k
+        vh = Hk if self.per_head_retrieval else 1
         pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
-        tshape = (B, Hk if self.per_head_retrieval else 1, R, 2, D // 2)
+        tshape = (B, vh, R, 2, D // 2)
         return (((B, Hk, R, D), torch.float32), ((B, Hk, R, D), torch.float32), (pshape, torch.int64),
-                (pshape, torch.bool), (tshape, self.dtype))
+                (pshape, torch.bool), (tshape, self.dtype), ((B, vh, D), torch.float32))
 
     def _take_slot(self, li):
         """A free slot of layer li whose last copy has completed (its host
@@ -518,10 +565,12 @@ class KVController:
         if len(self._slots[li]) >= self.MAX_SLOTS:
             return None
         specs = self._slot_specs()
-        nbytes = _block_layout(specs)[1]
-        block = torch.empty(nbytes[1], dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+        ends = _block_layout(specs)[1]
+        block = torch.empty(ends[-1], dtype=torch.uint8, pin_memory=torch.cuda.is_available())
         views = _carve(block, specs)
-        sl = _Slot(views[:4], views[4], block, nbytes)
+        sl = _Slot(views[:4], views[4], block, (ends[3], ends[4]), views[5])
+        if self._device is not None and self._device.type == "cuda":
+            self._alloc_dev(sl, self._device)
         sl.state = _Slot.FILLING
         self._slots[li].append(sl)
         return sl
@@ -529,11 +578,11 @@ class KVController:
     def _retrieval_worker(self, layer_idx, q_vecs, slot=None, nthreads=0, table=None):
         """Top-lookahead_k tokens per batch row (or per KV head) into a slot's
         pinned host buffers (controller.py:250-293), one native call over all
-        rows.  q_vecs None: the slot's pooled query is still being copied to
-        the host; wait for it here, on this thread, then normalise it.  table:
-        the rotary tables by position (_rope_rows), gathered into the slot for
-        the inject.  Returns False when no search ran (no free slot, not
-        initialised)."""
+        rows, on the calling thread.  q_vecs None: the slot's pooled query is
+        still being copied to the host; wait for it here, and normalise it in
+        the native call.  table: the rotary tables by position (_rope_rows),
+        gathered into the slot for the inject.  Returns False when no search
+        ran (no free slot, not initialised)."""
         li = int(layer_idx)
         if not self._inited:
             return False
@@ -543,12 +592,23 @@ class KVController:
             if slot is None:
                 self.dbg["retrieval_skipped_no_slot"] += 1
                 return False
+        if q_vecs is None:
+            self._wait_event(slot.q_ready)
+        args, keep, tab = self._search_args(li, slot, q_vecs, table, nthreads)
+        missing = ctypes.c_int64(0)
+        N.check(N.lib().hc_cold_retrieve(*args[:-1], ctypes.byref(missing), args[-1]), "hc_cold_retrieve")
+        self._finish_retrieval(li, slot, tab, int(slot.host[3].sum()), missing.value)
+        return True
+
+    def _search_args(self, li, slot, q_vecs, table, nthreads):
+        """hc_cold_retrieve's arguments for a search of layer li into `slot`
+        (without tab_missing), the arrays they point into, and whether the
+        rotary rows are gathered.  q_vecs None: the slot's pooled query, raw
+        (B,VH,D) fp32, cropped or padded and normalised inside the native
+        call; else host vectors already in search form."""
         B, R = self.B, self.lookahead_k
         kpre, vv, pos, valid = slot.host
         if q_vecs is None:
-            # pooled on the device: raw (B,D) or (B,Hk,D) fp32, cropped or
-            # padded and normalised inside the native call
-            self._wait_event(slot.q_ready)
             q = slot.qhost
             q_ptr, q_dim, norm = q.data_ptr(), q.shape[-1], int(self.normalize_for_ip)
             q_sb, q_sh = q.stride(0), (q.stride(1) if q.dim() == 3 else 0)
@@ -561,33 +621,46 @@ class KVController:
         # gathered in the same native call from the table the decode thread
         # computed
         tab = table is not None and self._rope is not None
-        missing = ctypes.c_int64(0)
-        N.check(N.lib().hc_cold_retrieve(self._store_ptrs[li], B, q_ptr, q_sb, q_sh, q_dim, norm, R,
-                                         int(self.per_head_retrieval), kpre.data_ptr(), vv.data_ptr(),
-                                         pos.data_ptr(), valid.data_ptr(),
-                                         table.ctypes.data if tab else None, table.shape[0] if tab else 0,
-                                         table.shape[1] if tab else 0, slot.tab.data_ptr() if tab else None,
-                                         ctypes.byref(missing), int(nthreads)), "hc_cold_retrieve")
-        slot.has_tab = tab
-        if tab and missing.value:
+        args = (self._store_ptrs[li], B, q_ptr, q_sb, q_sh, q_dim, norm, R, int(self.per_head_retrieval),
+                kpre.data_ptr(), vv.data_ptr(), pos.data_ptr(), valid.data_ptr(),
+                table.ctypes.data if tab else None, table.shape[0] if tab else 0, table.shape[1] if tab else 0,
+                slot.tab.data_ptr() if tab else None, int(nthreads))
+        return args, (q, table), tab
+
+    def _finish_retrieval(self, li, slot, has_tab, n_valid, missing):
+        """A search into `slot` is done: hand the slot on for its copy, or
+        free it when nothing valid was found."""
+        slot.has_tab = has_tab
+        if has_tab and missing:
             # a token evicted after the search was scheduled lies past the
             # table: compute this retrieval's rows directly
-            cos, sin = ops_rope_tables(pos.reshape(-1, R), self._rope[0], self._rope[1], self.dtype)
+            R = self.lookahead_k
+            cos, sin = ops_rope_tables(slot.host[2].reshape(-1, R), self._rope[0], self._rope[1], self.dtype)
             slot.tab_host[0].view(-1, R, self.D // 2).copy_(cos)
             slot.tab_host[1].view(-1, R, self.D // 2).copy_(sin)
             self.dbg["rope_rows_direct"] += 1
         with self._retrieval_lock[li]:
-            if not bool(valid.any()):
+            if n_valid == 0:
                 slot.state = _Slot.FREE
                 self.dbg["retrieval_ready_empty"] += 1
-                return True
+                return
             old = self._retrieval_ready_cpu[li]
             if old is not None:        # a newer result replaces one never copied
                 old.state = _Slot.FREE
             self._retrieval_ready_cpu[li] = slot
             slot.state = _Slot.RETRIEVED
             self.dbg["retrieval_ready_cpu"] += 1
-        return True
+
+    def _collect(self, li):
+        """Take in the layer's finished native search, if any (decode thread)."""
+        job = self._retrieval_thread[li]
+        if isinstance(job, _Job) and job.poll():
+            self._retrieval_thread[li] = None
+            if job.error is not None:
+                with self._retrieval_lock[li]:
+                    job.slot.state = _Slot.FREE
+                raise N.HotColdError(f"hc_cold_retrieve (search thread): {job.error[1]} (status {job.error[0]})")
+            self._finish_retrieval(li, job.slot, job.has_tab, *job.result)
 
     def launch_retrieval_now(self, layer_idx, q_pre):
         """One synchronous retrieval outside the schedule (controller.py:295-312)."""
@@ -619,6 +692,7 @@ class KVController:
             return
         if len(self.query_window[li]) == 0:
             return
+        self._collect(li)
         with self._retrieval_lock[li]:
             th = self._retrieval_thread[li]
             if th is not None and th.is_alive():
@@ -628,30 +702,34 @@ class KVController:
                 self.dbg["retrieval_skipped_no_slot"] += 1
                 return
         if self._stream is not None and self.query_window[li][0].is_cuda:
-            # pooled on the device; the worker waits for the host copy, the
-            # decode thread does not
+            # pooled on the device; the search thread waits for the host
+            # copy, the decode thread does not
             self._stage_query(li, slot)
-            q_vecs = None
+            q_vecs, event = None, slot.q_ready
         else:
-            q_vecs = self._pooled_query_np(li)
+            q_vecs, event = self._pooled_query_np(li), None
+        args, keep, tab = self._search_args(li, slot, q_vecs, self._rope_rows(), self.SEARCH_THREADS)
+        handle = N.lib().hc_cold_retrieve_async(*args, event, self._search_workers())
+        if not handle:
+            with self._retrieval_lock[li]:
+                slot.state = _Slot.FREE
+            N.check(N.HC_ERR_INVALID, "hc_cold_retrieve_async")
         with self._retrieval_lock[li]:
-            th = self._spawn(self._retrieval_worker, (li, q_vecs, slot, self.SEARCH_THREADS, self._rope_rows()))
-            self._retrieval_thread[li] = th
+            self._retrieval_thread[li] = _Job(handle, slot, tab, keep)
             self.dbg["retrieval_launched"] += 1
 
-    def _spawn(self, fn, args):
-        if self._pool is None:
-            cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 4)
-            workers = max(1, min(self.MAX_SEARCH_WORKERS, cores // (2 * self.SEARCH_THREADS)))
-            self._pool = concurrent.futures.ThreadPoolExecutor(max_workers=workers,
-                                                               thread_name_prefix="hotcold-search")
-        return _Task(self._pool.submit(fn, *args))
+    def _search_workers(self):
+        """Native search threads: about half of this process's cores, at most
+        MAX_SEARCH_WORKERS searches at once."""
+        cores = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 4)
+        return max(1, min(self.MAX_SEARCH_WORKERS, cores // (2 * self.SEARCH_THREADS)))
 
     def wait_for_retrieval(self, layer_idx, timeout=None):
         """Join the layer's background search, if any (test and shutdown helper)."""
         th = self._retrieval_thread[int(layer_idx)] if self._inited else None
         if th is not None:
             th.join(timeout)
+            self._collect(int(layer_idx))
 
     # -- staging ------------------------------------------------------------------------------
     # The device-side primitives are methods so that tests can run the
@@ -671,6 +749,7 @@ class KVController:
         slot.dev_block = torch.empty(slot.block.numel(), dtype=torch.uint8, device=device)
         views = _carve(slot.dev_block, self._slot_specs())
         slot.dev, slot.tab_dev = views[:4], (views[4][..., 0, :], views[4][..., 1, :])
+        slot.qdev = views[5]
 
     def _copy_to_device(self, slot):
         """The slot's host-to-device copies on the side stream, after the
@@ -718,8 +797,12 @@ class KVController:
         stream (controller.py:344-380).  dtype is accepted for compatibility:
         staged buffers stay fp32 and the inject kernel converts."""
         li = int(layer_idx)
-        if self._stream is None or not self._inited or self._retrieval_ready_cpu[li] is None:
-            return                       # nothing retrieved (a result landing now is taken next step)
+        if self._stream is None or not self._inited:
+            return
+        if self._retrieval_thread[li] is not None:
+            self._collect(li)
+        if self._retrieval_ready_cpu[li] is None:
+            return                       # nothing retrieved (a search finishing now is taken next step)
         device = torch.device(device)
         if device.type != "cuda":
             return

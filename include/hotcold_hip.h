@@ -134,6 +134,21 @@ int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t 
                           void* stream);
 
 /*
+ * The pooled retrieval query on the device: the mean of the window's T query
+ * tensors q[t] [B][Hq][D] (element strides q_sb[t], q_sh[t]; T <= 16) over
+ * the rows and over the heads -- of each KV head's group (per_head: out
+ * [B][Hk][D]) or of all Hq heads (out [B][1][D]) -- in fp32, added in
+ * window-then-head order.  Replaces the torch.cat + means of _pooled_query_np
+ * / _q_to_vecs_np (controller.py:240-248, which pool in the cache dtype).
+ * The result goes to dev_out; then, on the same stream, to host_out (pinned,
+ * may be NULL) by hipMemcpyAsync, and `event` (may be NULL) is recorded
+ * behind the copy, for a search thread to wait on.
+ */
+int hc_retrieval_query(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t T, const void* const* q,
+                       const int64_t* q_sb, const int64_t* q_sh, int per_head, float* dev_out, float* host_out,
+                       void* event, void* stream);
+
+/*
  * hc_decode_attn_append with its arguments in one struct: the same launch,
  * checks and results; a per-layer decode loop keeps one struct per hot
  * buffer and rewrites only the fields that change from step to step (q, the
@@ -495,6 +510,25 @@ int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_s
                      int normalize_q, int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
                      uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes,
                      uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads);
+/* hc_cold_retrieve as a job on the library's own worker threads, in place of
+ * the reference's threading.Thread per search (controller.py:336-342).  Up to
+ * `workers` threads (at most 16) are started on first use and kept until the
+ * process ends.  The worker first synchronises on wait_event (may be NULL),
+ * the event behind the pooled query's copy, then runs the retrieval and
+ * counts the valid rows.  The caller keeps every buffer alive until the job
+ * is done.  Returns the job, or NULL on a bad argument (hc_last_error). */
+void* hc_cold_retrieve_async(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
+                             int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
+                             float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                             int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t nthreads,
+                             void* wait_event, int64_t workers);
+/* 0 while the job runs (wait = 0); 1 when it is done, with the number of
+ * valid rows and of positions past the table; a negative HC_ERR_* code if
+ * the retrieval failed (its message in hc_last_error on the calling thread).
+ * wait != 0 blocks until the job is done. */
+int hc_cold_job_poll(void* job, int wait, int64_t* n_valid, int64_t* tab_missing);
+/* Frees a job, first waiting for it if a worker still runs it. */
+void hc_cold_job_free(void* job);
 
 #ifdef __cplusplus
 }

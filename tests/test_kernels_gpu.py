@@ -780,3 +780,47 @@ def test_scores_and_gather_over_row_tables_equal_per_layer(dtype, pooling):
                                                       W, budget)), l
         assert torch.equal(kd[l][:, :, 2:2 + n], ops.gather_kv(ks[l], keep)), l
         assert torch.equal(vd[l][:, :, 2:2 + n], ops.gather_kv(vs[l], keep)), l
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("per_head", [False, True])
+def test_retrieval_query_pooling(dtype, per_head):
+    """hc_retrieval_query: the window's query rows (strided views, as the
+    model's projections hand them over) summed in fp32 in window-then-head
+    order and divided by the count -- equal to that sum computed on the
+    CPU -- copied to pinned memory behind the event."""
+    import ctypes
+
+    from hotcold_kv import _native as N
+    B, Hq, Hk, D, T = 2, 32, 8, 128, 4
+    g = torch.Generator().manual_seed(3 + per_head)
+    rows = [torch.randn((B, 1, Hq, D), generator=g).to(dtype) for _ in range(T)]
+    qs = [r.to(DEV).transpose(1, 2) for r in rows]                 # (B,Hq,1,D) views, head stride D
+    vh = Hk if per_head else 1
+    nh = Hq // Hk if per_head else Hq
+    dev = torch.empty((B, vh, D), dtype=torch.float32, device=DEV)
+    host = torch.empty((B, vh, D), dtype=torch.float32, pin_memory=True)
+    lib = N.lib()
+    ev = ctypes.c_void_p()
+    N.check(lib.hc_event_create(ctypes.byref(ev), 0), "hc_event_create")
+    ptrs = (ctypes.c_void_p * T)(*[q.data_ptr() for q in qs])
+    sb = (ctypes.c_int64 * T)(*[q.stride(0) for q in qs])
+    sh = (ctypes.c_int64 * T)(*[q.stride(1) for q in qs])
+    N.check(lib.hc_retrieval_query(N.dtype_code(dtype), B, Hq, Hk, D, T, ptrs, sb, sh, int(per_head),
+                                   dev.data_ptr(), host.data_ptr(), ev.value,
+                                   torch.cuda.current_stream().cuda_stream), "hc_retrieval_query")
+    N.check(lib.hc_event_synchronize(ev.value), "hc_event_synchronize")
+    lib.hc_event_destroy(ev.value)
+    x = torch.stack([r[:, 0].float() for r in rows])               # (T,B,Hq,D)
+    want = torch.empty((B, vh, D), dtype=torch.float32)
+    inv = torch.tensor(1.0, dtype=torch.float32) / torch.tensor(float(T * nh), dtype=torch.float32)
+    for v in range(vh):
+        acc = torch.zeros((B, D), dtype=torch.float32)
+        for t in range(T):
+            for h in range(v * nh, (v + 1) * nh):
+                acc = acc + x[t, :, h]
+        want[:, v] = acc * inv
+    assert torch.equal(host, want)
+    assert torch.equal(dev.cpu(), want)
+    ref_mean = x.permute(1, 2, 0, 3).reshape(B, vh, nh * T, D).double().mean(dim=2)
+    assert (host.double() - ref_mean).abs().max() < 1e-5

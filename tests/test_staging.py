@@ -9,6 +9,7 @@ replaced here by host stand-ins, so the state machine runs without a GPU and
 a copy can be held "not ready" for as long as a test wants.
 """
 
+import pytest
 import torch
 
 from hotcold_kv import ops
@@ -232,16 +233,17 @@ def test_two_slots_per_layer_are_preallocated():
 
 
 def test_slot_buffers_are_views_of_one_block():
-    """k_pre, v, pos, valid and the rotary tables carved from one block in
-    that order, 256-byte aligned and disjoint; one copy of nbytes[0] carries
-    a retrieval without tables, nbytes[1] one with them; cos and sin are the
-    two halves of each table row."""
+    """k_pre, v, pos, valid, the rotary tables and the pooled query carved
+    from one block in that order, 256-byte aligned and disjoint; one copy of
+    nbytes[0] carries a retrieval without tables, nbytes[1] one with them,
+    and the pooled query lies past both; cos and sin are the two halves of
+    each table row."""
     ctrl = _ctrl(per_head_retrieval=True)
     with ctrl._retrieval_lock[0]:
         sl = ctrl._take_slot(0)
-    views = list(sl.host) + [sl.tab]
+    views = list(sl.host) + [sl.tab, sl.qhost]
     base = sl.block.data_ptr()
-    offs, nbytes = _block_layout(ctrl._slot_specs())
+    offs, ends = _block_layout(ctrl._slot_specs())
     spans = []
     for t, off, (shape, dt) in zip(views, offs, ctrl._slot_specs()):
         assert t.data_ptr() - base == off and off % 256 == 0
@@ -249,8 +251,9 @@ def test_slot_buffers_are_views_of_one_block():
         spans.append((off, off + t.numel() * t.element_size()))
     for (a0, a1), (b0, b1) in zip(spans, spans[1:]):
         assert a1 <= b0
-    assert nbytes == (spans[3][1], spans[4][1]) == sl.nbytes
-    assert sl.block.numel() == nbytes[1]
+    assert [e for _, e in spans] == ends
+    assert sl.nbytes == (spans[3][1], spans[4][1])
+    assert sl.block.numel() == spans[5][1] and tuple(sl.qhost.shape) == (1, HK, D)
     cos, sin = sl.tab_host
     assert cos.data_ptr() == sl.tab.data_ptr() and sin.data_ptr() == cos.data_ptr() + (D // 2) * cos.element_size()
     assert cos.stride() == sin.stride() and cos.shape == (1, HK, 4, D // 2)
@@ -332,3 +335,83 @@ def test_native_query_normalisation_equals_the_host_one():
             ss += t * t
         want = (x / max(math.sqrt(ss), 1e-12)).astype(np.float32)
         assert np.array_equal(ctrl._normalize(ctrl._pad_or_crop(raw.numpy()))[0, 1], want)
+
+
+def test_native_search_jobs_equal_the_synchronous_search():
+    """Searches scheduled on the library's worker threads (several layers at
+    once) write what the synchronous call writes: positions, keys, values,
+    valid flags and rotary rows."""
+    L = 3
+    ctrl = HostCtrl(cpu_buffer_size=64, faiss_dim=D, lookahead_k=4, window_size=1, hold_retrieved=True,
+                    per_head_retrieval=True)
+    ctrl._lazy_init(torch.zeros(1, HK, 1, D, dtype=torch.float16), n_layers=L)
+    ctrl._stream = "side"
+    ctrl.set_rope(1.0 / (500000.0 ** (torch.arange(0, D, 2, dtype=torch.float32) / D)), 1.0)
+    g = torch.Generator().manual_seed(5)
+    for li in range(L):
+        keys = torch.randn(30, HK, D, generator=g)
+        ctrl.add_evicted_to_cold_store(li, EvictedKV(
+            k_pre_cpu=keys.permute(1, 0, 2).unsqueeze(0).contiguous(),
+            v_cpu=(2 * keys).permute(1, 0, 2).unsqueeze(0).contiguous(),
+            pos_cpu=torch.arange(50 * li, 50 * li + 30, dtype=torch.long).unsqueeze(0),
+            evicted_idx=torch.arange(30, dtype=torch.long).unsqueeze(0)))
+    qs = [torch.randn(1, 4, 1, D, generator=g) for _ in range(L)]
+    for li in range(L):                         # all layers' searches in flight together
+        ctrl.update_query_window(li, qs[li])
+        ctrl.maybe_launch_async_retrieval(li)
+    assert ctrl.dbg["retrieval_launched"] == L
+    got = []
+    for li in range(L):
+        ctrl.wait_for_retrieval(li)
+        sl = ctrl._retrieval_ready_cpu[li]
+        assert sl is not None and sl.has_tab and ctrl._retrieval_thread[li] is None
+        got.append([t.clone() for t in sl.host] + [sl.tab.clone()])
+        ctrl._retrieval_ready_cpu[li] = None
+        sl.state = _Slot.FREE
+    for li in range(L):
+        with ctrl._retrieval_lock[li]:
+            sl = ctrl._take_slot(li)
+        assert ctrl._retrieval_worker(li, ctrl._q_to_vecs_np(qs[li]), slot=sl, table=ctrl._rope_rows())
+        for a, b in zip(got[li], list(sl.host) + [sl.tab]):
+            assert torch.equal(a, b), li
+        assert int(got[li][2].min()) >= 50 * li
+
+
+def test_a_refused_native_search_raises_on_the_decode_thread():
+    """Arguments the library refuses at submission raise on the decode thread
+    (here: a zero batch); the slot is not left in flight."""
+    ctrl = _ctrl()
+    _fill(ctrl)
+    real = ctrl._search_args
+
+    def bad(*a, **k):
+        args, keep, tab = real(*a, **k)
+        return (args[0], 0) + args[2:], keep, tab
+
+    ctrl._search_args = bad
+    with pytest.raises(RuntimeError, match="cold_retrieve_async"):
+        _window(ctrl)
+    assert ctrl._retrieval_thread[0] is None
+    assert all(sl.state == _Slot.FREE for sl in ctrl._slots[0])
+
+
+def test_a_search_failing_on_its_worker_raises_once_and_frees_its_slot():
+    """A retrieval that fails on the worker thread (here: the per-head flag
+    does not match the store) is reported by the next collection on the
+    decode thread; the slot is freed and the next search runs."""
+    ctrl = _ctrl()
+    _fill(ctrl)
+    real = ctrl._search_args
+
+    def mismatched(*a, **k):
+        args, keep, tab = real(*a, **k)
+        return args[:8] + (1,) + args[9:], keep, tab
+
+    ctrl._search_args = mismatched
+    with pytest.raises(RuntimeError, match="does not match"):
+        _window(ctrl)
+    assert ctrl._retrieval_thread[0] is None
+    assert all(sl.state == _Slot.FREE for sl in ctrl._slots[0])
+    ctrl._search_args = real
+    _window(ctrl)
+    assert ctrl._retrieval_ready_cpu[0] is not None
