@@ -77,6 +77,24 @@ struct ColdStore {
     return (size_t)vh * VD * capT + (size_t)(slot >> 4) * VD * 16 + (size_t)d * 16 + (slot & 15);
   }
   mutable std::shared_mutex mu;
+  // Search jobs submitted but not finished that read this store; destroying
+  // the store waits for them.
+  mutable std::mutex jobs_mu;
+  mutable std::condition_variable jobs_cv;
+  mutable int64_t jobs_in_flight = 0;
+
+  void pin() const {
+    std::lock_guard<std::mutex> lk(jobs_mu);
+    ++jobs_in_flight;
+  }
+  void unpin() const {
+    std::lock_guard<std::mutex> lk(jobs_mu);
+    if (--jobs_in_flight == 0) jobs_cv.notify_all();
+  }
+  void wait_unpinned() const {
+    std::unique_lock<std::mutex> lk(jobs_mu);
+    jobs_cv.wait(lk, [&] { return jobs_in_flight == 0; });
+  }
 
   bool allocate() {
     kpre.reset((size_t)cap * H * D);
@@ -268,7 +286,12 @@ extern "C" void* hc_cold_create(int64_t capacity, int64_t heads, int64_t head_di
   return s;
 }
 
-extern "C" void hc_cold_destroy(void* store) { delete as_store(store); }
+extern "C" void hc_cold_destroy(void* store) {
+  ColdStore* s = as_store(store);
+  if (!s) return;
+  s->wait_unpinned();  // a search job still reading the store finishes first
+  delete s;
+}
 
 extern "C" int64_t hc_cold_size(const void* store) {
   const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
@@ -484,6 +507,7 @@ class JobQueue {
                             j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
     if (rc == HC_OK)
       for (int64_t i = 0; i < j->n_flags; ++i) nv += j->valid_out[i] != 0;
+    for (void* st : j->stores) as_store(st)->unpin();
     std::lock_guard<std::mutex> lk(j->mu);
     if (rc != HC_OK) snprintf(j->msg, sizeof(j->msg), "%s", hc_last_error());
     j->rc = rc;
@@ -536,6 +560,7 @@ extern "C" void* hc_cold_retrieve_async(void* const* stores, int64_t B, const fl
   j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows; j->tab_row_bytes = tab_row_bytes;
   j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
   j->n_flags = B * R * (per_head ? s0->H : 1);
+  for (int64_t b = 0; b < B; ++b) as_store(stores[b])->pin();
   job_queue().push(j, workers);
   return j;
 }

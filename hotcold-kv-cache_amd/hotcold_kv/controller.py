@@ -375,6 +375,7 @@ class KVController:
             cos, sin = ops_rope_tables(torch.arange(rows, dtype=torch.int64).view(1, rows), self._rope[0],
                                        self._rope[1], self.dtype)
             tab = torch.stack([cos[0], sin[0]], dim=1).contiguous()                 # (rows, 2, D/2)
+            self._rope_tab_t = tab                                                  # owns the bytes below
             self._rope_tab = tab.view(torch.uint8).numpy().reshape(rows, -1)
         return self._rope_tab
 

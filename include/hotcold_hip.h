@@ -479,6 +479,7 @@ int hc_memcpy_d2h_async(void* dst, const void* src, int64_t bytes, void* stream)
  */
 void* hc_cold_create(int64_t capacity, int64_t heads, int64_t head_dim, int64_t vec_dim, int64_t vec_heads,
                      int normalize);
+/* Frees a store, first waiting for any submitted search job that reads it. */
 void hc_cold_destroy(void* store);
 int64_t hc_cold_size(const void* store);
 /* Tokens t < te with evicted_idx[t] >= 0 (evicted_idx may be NULL: all), from

@@ -415,3 +415,25 @@ def test_a_search_failing_on_its_worker_raises_once_and_frees_its_slot():
     ctrl._search_args = real
     _window(ctrl)
     assert ctrl._retrieval_ready_cpu[0] is not None
+
+
+def test_destroying_a_store_waits_for_its_search():
+    """A store freed while a search job reads it (a controller collected with
+    a search in flight) is freed only after the job has finished."""
+    from hotcold_kv import _native as N
+    ctrl = HostCtrl(cpu_buffer_size=20000, faiss_dim=D, lookahead_k=4, window_size=1, hold_retrieved=True)
+    ctrl._lazy_init(torch.zeros(1, HK, 1, D), n_layers=1)
+    ctrl._stream = "side"
+    g = torch.Generator().manual_seed(9)
+    keys = torch.randn(20000, HK, D, generator=g)
+    ctrl.add_evicted_to_cold_store(0, EvictedKV(
+        k_pre_cpu=keys.permute(1, 0, 2).unsqueeze(0).contiguous(), v_cpu=keys.permute(1, 0, 2).unsqueeze(0).contiguous(),
+        pos_cpu=torch.arange(20000, dtype=torch.long).unsqueeze(0),
+        evicted_idx=torch.arange(20000, dtype=torch.long).unsqueeze(0)))
+    ctrl.update_query_window(0, torch.randn(1, 4, 1, D, generator=g))
+    ctrl.maybe_launch_async_retrieval(0)
+    job = ctrl._retrieval_thread[0]
+    ring = ctrl.rings[0][0]
+    handle, ring.handle = ring.handle, None
+    N.lib().hc_cold_destroy(handle)                 # returns once the search no longer reads the store
+    assert job.poll(wait=True) and job.error is None and job.result[0] == 4
