@@ -465,13 +465,14 @@ def differential_ms(st, flush, fn, reps, warmup=3):
     return statistics.median(a.elapsed_time(b) for a, b in pr) - statistics.median(a.elapsed_time(b) for a, b in sw)
 
 
-def measure_config(w, dev, flush, reps=24):
+def measure_config(w, dev, flush, reps=24, cpu=False):
     """Secondary figures of a larger workload (not the headline): the fused
     append+decode over all layers' hot buffers with the held slot active, one
     layer's compaction at the full batch, and the inject path (re-RoPE of a
     full held slot, its pinned H2D copy, and decode with that copy running
     concurrently on a side stream).  Inputs are N(0,1) of the workload's
-    shapes, generated on the device."""
+    shapes, generated on the device.  cpu: also time the reference's
+    torch-CPU path on one layer of the same inputs (cpu_baseline_config)."""
     import torch
     from hotcold_kv import ops, synthetic
 
@@ -587,10 +588,56 @@ def measure_config(w, dev, flush, reps=24):
                          "frac": round(cg / HBM_PEAK_GBS, 4),
                          "scoring_tflops_fp64": round(sflops / (comp_ms * 1e-3) / 1e12, 2),
                          "scoring_mfma_frac": round(sflops / (comp_ms * 1e-3) / 1e12 / FP64_MFMA_PEAK_TFLOPS, 4)}
+    if cpu:
+        out["cpu_baseline"] = cpu_baseline_config(w, q_post[:, :, S - W:].cpu(), k_post.cpu(), v.cpu())
     del q_post, k_post, v
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return out
+
+
+def cpu_baseline_config(w, q_win, k, v, decode_sample=8, max_batch=16):
+    """The reference's torch-CPU path on one layer of a larger workload, in
+    the workload's dtype (fp16/bf16 CPU matmul, as scoring.py:70 runs it):
+    the compaction of the layer's prompt (snapkv_importance -> keep_index ->
+    gather_kv) and decode_sample decode steps (append + SDPA) over the held
+    slot and the kept rows.  One layer of at most max_batch sequences is
+    timed; the figures are scaled to the full batch and to all layers (the
+    work is linear in both), as `sample` states."""
+    import torch
+    from oracle import reference as ref
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+    B_full = k.shape[0]
+    if B_full > max_batch:
+        q_win, k, v = q_win[:max_batch], k[:max_batch], v[:max_batch]
+    scale = B_full / k.shape[0]
+    B, Hk, S, D = k.shape
+    t0 = time.perf_counter()
+    keys, vals = ref.press_compress_torch(q_win, k, v, w.window, w.budget, w.scaling, w.pool, q_is_window=True)
+    comp_ms = (time.perf_counter() - t0) * 1e3 * scale
+    g = torch.Generator().manual_seed(0)
+    if w.held:
+        keys = torch.cat([torch.randn((B, Hk, w.held, D), generator=g).to(k.dtype), keys], 2)
+        vals = torch.cat([torch.randn((B, Hk, w.held, D), generator=g).to(k.dtype), vals], 2)
+    dec = []
+    for _ in range(decode_sample + 1):
+        qt = torch.randn((B, w.hq, 1, D), generator=g).to(k.dtype)
+        kt, vt = (torch.randn((B, Hk, 1, D), generator=g).to(k.dtype) for _ in range(2))
+        t0 = time.perf_counter()
+        _, keys, vals = ref.press_decode_torch(qt, keys, vals, kt, vt, w.scaling)
+        dec.append((time.perf_counter() - t0) * 1e6)
+    dec_us = statistics.median(dec[1:]) * scale
+    name = str(k.dtype).replace("torch.", "")
+    part = f"{B} of its {B_full} sequences, scaled x{scale:g}; " if scale != 1 else ""
+    return {"dtype": name, "threads": threads, "kind": "port",
+            "compact_ms_per_layer": round(comp_ms, 2),
+            "compact_ms_32_layers": round(comp_ms * w.layers, 1),
+            "decode_us_per_layer_step": round(dec_us, 1),
+            "sample": (f"one layer timed ({part}x{w.layers} for all layers): one compaction of a {S}-token "
+                       f"prompt to {w.budget} rows, then {decode_sample} decode steps (median) over {w.held} held "
+                       f"+ {w.budget} kept rows, torch CPU in {name}, {threads} threads")}
 
 
 def measure_h2o(w, dev, reps=5, steps=96):
@@ -925,10 +972,14 @@ def main():
         flush = CacheSweep(dev)
         for name in ("llama8b_16k_b1024_held64", "b16_32k_b2048_held128", "bf16_b4_64k_b4096_held256"):
             log(f"secondary figures: {name} ...")
-            r = measure_config(synthetic.WORKLOADS[name], dev, flush)
+            r = measure_config(synthetic.WORKLOADS[name], dev, flush, cpu=not args.no_cpu_baseline)
             log(f"  decode {r['decode']['us_per_layer_step']} us/layer-step ({r['decode']['frac'] * 100:.1f}% of "
                 f"HBM peak), compaction {r['compaction']['ms_per_layer']} ms/layer, re-RoPE "
                 f"{r['inject']['rerope_us_all_layers']} us, H2D {r['inject']['h2d_GBps']} GB/s")
+            if "cpu_baseline" in r:
+                c = r["cpu_baseline"]
+                log(f"  cpu baseline ({c['dtype']}, {c['threads']} threads): compaction {c['compact_ms_per_layer']} "
+                    f"ms/layer, decode {c['decode_us_per_layer_step']} us/layer-step")
             others.append(r)
         del flush
 

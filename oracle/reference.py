@@ -193,16 +193,19 @@ def pool1d(x, kernel_size, pooling):
     return torch.nn.functional.max_pool1d(x, kernel_size=kernel_size, stride=1, padding=pad)
 
 
-def snapkv_importance_torch(q_post, keys, window_size, scaling, kernel_size, pooling, dtype=torch.float32):
+def snapkv_importance_torch(q_post, keys, window_size, scaling, kernel_size, pooling, dtype=torch.float32,
+                            q_is_window=False):
     """scoring.py:50-79 on CPU with inputs upcast to `dtype` (the reference's
     own op sequence: GQA mean, matmul, causal masked_fill, fp32 softmax, sum
-    over the window, pooling)."""
+    over the window, pooling).  q_is_window: q_post holds only the last
+    min(window, S) query rows."""
     q_post = q_post.detach().cpu().to(dtype)
     keys = keys.detach().cpu().to(dtype)
-    B, Hq, S, D = q_post.shape
+    B, Hq, _, D = q_post.shape
+    S = keys.shape[2]
     Hk = keys.shape[1]
     W = min(window_size, S)
-    q_for = group_query_to_kv(q_post[:, :, S - W:, :], Hk)
+    q_for = group_query_to_kv(q_post if q_is_window else q_post[:, :, S - W:, :], Hk)
     logits = torch.matmul(q_for, keys.transpose(2, 3)) * scaling
     qpos = torch.arange(S - W, S).view(1, 1, W, 1)
     kpos = torch.arange(S).view(1, 1, 1, S)
@@ -548,10 +551,12 @@ def keep_index_torch(scores, window_size, budget):
     return torch.cat([top, recent], dim=-1)
 
 
-def press_compress_torch(q_post, keys, values, window_size, budget, scaling, kernel_size=7, pooling="maxpool"):
+def press_compress_torch(q_post, keys, values, window_size, budget, scaling, kernel_size=7, pooling="maxpool",
+                         q_is_window=False):
     """PressLayerState._compress after prefill scoring (layer_state.py:68-94)
     on the CPU: snapkv_importance -> keep_index -> gather_kv x2."""
-    imp = snapkv_importance_torch(q_post, keys, window_size, scaling, kernel_size, pooling, dtype=keys.dtype)
+    imp = snapkv_importance_torch(q_post, keys, window_size, scaling, kernel_size, pooling, dtype=keys.dtype,
+                                  q_is_window=q_is_window)
     keep = keep_index_torch(imp, window_size, budget)
     B, H, _, D = keys.shape
     idx = keep.unsqueeze(-1).expand(B, H, keep.shape[-1], D)

@@ -103,6 +103,15 @@ def test_window_scores_from_the_window_rows_only():
         ref.window_scores(q[:, :, -8:].contiguous(), k, 16, 0.2, 7, "maxpool", q_is_window=True)
 
 
+def test_torch_importance_from_the_window_rows_only():
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(1, 8, 200, 16, generator=g)
+    k = torch.randn(1, 2, 200, 16, generator=g)
+    full = ref.snapkv_importance_torch(q, k, 24, 0.25, 7, "maxpool")
+    tail = ref.snapkv_importance_torch(q[:, :, -24:].contiguous(), k, 24, 0.25, 7, "maxpool", q_is_window=True)
+    assert torch.equal(full, tail)
+
+
 def test_window_scores_causal_mask():
     # a key after a window row's own position must get no weight from that row:
     # make the last key dominate; only the last window row may see it
