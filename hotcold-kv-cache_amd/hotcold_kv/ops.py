@@ -265,7 +265,13 @@ class _AppendPlan:
     """hc_decode_attn_append_packed arguments of one hot-buffer storage (a
     `st` dict): the shape, the buffers' base pointers and strides, the dtype
     and the stream's workspace are filled in once; a call validates its
-    inputs and rewrites only the per-step fields."""
+    inputs and rewrites only the per-step fields.
+
+    The per-call host work is kept to attribute reads and field writes: the
+    (B,H,1,D) rows are addressed through their data pointer and first two
+    strides (no views), dtypes compare by identity, and a held slot's
+    tensors are validated once per (pos, valid, R) triple, which stays the
+    same between injections."""
 
     def __init__(self, st, Hq):
         k, v = st["k"], st["v"]
@@ -276,7 +282,9 @@ class _AppendPlan:
         self.tensors = (k, v, st.get("p"), st.get("pos"))     # the storage the pointers below belong to
         self.B, self.Hq, self.Hk, self.cap, self.D = B, int(Hq), Hk, cap, D
         self.dtype, self.dev, self.es = k.dtype, k.device, k.element_size()
-        self.qshape, self.tshape = (B, self.Hq, D), (B, Hk, D)
+        self.devidx = k.get_device()
+        self.qshapes = ((B, self.Hq, D), (B, self.Hq, 1, D))
+        self.tshapes = ((B, Hk, D), (B, Hk, 1, D))
         a = self.a = N.DecodeAppendArgs()
         a.dtype, a.B, a.Hq, a.Hk, a.D = N.dtype_code(k.dtype), B, self.Hq, Hk, D
         ks, vs = k.stride(), v.stride()
@@ -294,7 +302,12 @@ class _AppendPlan:
             self.pos0 = self.pos.data_ptr()
         a.o_sb, a.o_sh = self.Hq * D, D
         self.stream, self.ws = None, None
+        self.lo = None                  # the row offset the k / v / p_dst / pos_dst pointers are set for
+        self.held_key = None            # (pos, valid, R) the held fields are set for
+        self.scaling = None
         self.lib = N.lib()
+        self.fn = self.lib.hc_decode_attn_append_packed
+        self.addr = ctypes.addressof(a)
 
     def _bind_stream(self, stream, S):
         need = self.lib.hc_decode_attn_workspace_size(self.B, self.Hq, self.Hk, self.D, max(S, self.cap), 0, 0)
@@ -302,70 +315,88 @@ class _AppendPlan:
         self.a.workspace, self.a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
         self.stream = stream
 
+    def _row(self, t, shapes, what):
+        """data_ptr and (batch, head) strides of a (B,H,D) / (B,H,1,D) row
+        tensor on the buffer's device, in its dtype, with a unit last stride."""
+        sh = t.shape
+        if (sh != shapes[0] and sh != shapes[1]) or t.dtype is not self.dtype or t.get_device() != self.devidx:
+            raise RuntimeError(f"decode_append_rows: {what} must be {shapes[0]} or {shapes[1]} device rows in the "
+                               f"buffer's dtype {self.dtype}; got {tuple(sh)} {t.dtype} on {t.device}")
+        st = t.stride()
+        if st[-1] != 1:
+            raise RuntimeError(f"decode_append_rows: {what} needs a unit last stride")
+        return t.data_ptr(), st[0], st[1]
+
+    def _set_held(self, held, cur_pos, S):
+        hp, hv, R = held
+        R = int(R)
+        if hv.dtype == torch.bool:
+            hv = hv.view(torch.uint8)
+        B, Hk = self.B, self.Hk
+        if hp.dtype != torch.int64 or R > S - 1 or hp.shape[0] != B or hv.shape[0] != B \
+                or hp.shape[-1] < R or hv.shape[-1] < R or hp.stride(-1) != 1 or hv.stride(-1) != 1 \
+                or (hp.dim() == 3 and hp.shape[1] != Hk) or (hv.dim() == 3 and hv.shape[1] != Hk) \
+                or hp.get_device() != self.devidx or hv.get_device() != self.devidx:
+            raise RuntimeError("decode_append_rows: held = (pos (B,R)|(B,Hk,R) int64, valid, R <= S-1)")
+        a = self.a
+        a.held_len = R
+        a.held_pos, a.hp_sb, a.hp_sh = hp.data_ptr(), hp.stride(0), hp.stride(1) if hp.dim() == 3 else 0
+        a.held_valid, a.hv_sb, a.hv_sh = hv.data_ptr(), hv.stride(0), hv.stride(1) if hv.dim() == 3 else 0
+
     def run(self, q, lo, S, k_new, v_new, scaling, p_new, pos_new, held, cur_pos, keepdim):
-        B, Hk, D = self.B, self.Hk, self.D
-        q3 = q[:, :, 0, :] if q.dim() == 4 else q
-        kn = k_new[:, :, 0, :] if k_new.dim() == 4 else k_new
-        vn = v_new[:, :, 0, :] if v_new.dim() == 4 else v_new
-        if q3.shape != self.qshape or kn.shape != self.tshape or vn.shape != self.tshape or q3.dtype != self.dtype \
-                or kn.dtype != self.dtype or vn.dtype != self.dtype or q3.device != self.dev \
-                or kn.device != self.dev or vn.device != self.dev \
-                or q3.stride(-1) != 1 or kn.stride(-1) != 1 or vn.stride(-1) != 1:
-            raise RuntimeError("decode_append_rows: q (B,Hq,D), k_new / v_new (B,Hk,D) device rows in the buffer's "
-                               "dtype required")
+        a = self.a
         if lo < 0 or S < 1 or lo + S > self.cap:
             raise RuntimeError(f"decode_append_rows: rows {lo}..{lo + S - 1} outside the buffer's {self.cap}")
-        a = self.a
+        a.q, a.q_sb, a.q_sh = self._row(q, self.qshapes, "q")
+        a.k_new, a.kn_sb, a.kn_sh = self._row(k_new, self.tshapes, "k_new")
+        a.v_new, a.vn_sb, a.vn_sh = self._row(v_new, self.tshapes, "v_new")
         a.S = S
-        a.q, (a.q_sb, a.q_sh) = q3.data_ptr(), q3.stride()[:2]
-        a.k, a.v = self.k0 + lo * self.krow, self.v0 + lo * self.vrow
-        a.k_new, (a.kn_sb, a.kn_sh) = kn.data_ptr(), kn.stride()[:2]
-        a.v_new, (a.vn_sb, a.vn_sh) = vn.data_ptr(), vn.stride()[:2]
+        if lo != self.lo:
+            a.k, a.v = self.k0 + lo * self.krow, self.v0 + lo * self.vrow
+            if self.p is not None:
+                self.p_dst = self.p0 + lo * self.prow
+            if self.pos is not None:
+                self.pos_dst = self.pos0 + lo * 8
+            self.lo = lo
         if p_new is not None:
             if self.p is None:
                 raise RuntimeError("decode_append_rows: p_new given but the buffer keeps no pre-RoPE keys")
-            pn = p_new[:, :, 0, :] if p_new.dim() == 4 else p_new
-            if pn.shape != self.tshape or pn.stride(-1) != 1 or pn.dtype != self.dtype or pn.device != self.dev:
-                raise RuntimeError("decode_append_rows: p_new must be (B,Hk,D) in the buffer's dtype")
-            a.p_new, (a.pn_sb, a.pn_sh) = pn.data_ptr(), pn.stride()[:2]
-            a.p_dst = self.p0 + lo * self.prow
+            a.p_new, a.pn_sb, a.pn_sh = self._row(p_new, self.tshapes, "p_new")
+            a.p_dst = self.p_dst
         else:
             a.p_new = a.p_dst = None
         if pos_new is not None:
             if self.pos is None:
                 raise RuntimeError("decode_append_rows: pos_new given but the buffer keeps no positions")
-            if pos_new.dtype != torch.int64 or pos_new.shape[0] != B or pos_new.device != self.dev:
+            if pos_new.dtype is not torch.int64 or pos_new.shape[0] != self.B or pos_new.get_device() != self.devidx:
                 raise RuntimeError("decode_append_rows: pos_new must be (B,1) int64")
             a.pos_new, a.posn_sb = pos_new.data_ptr(), pos_new.stride(0)
-            a.pos_dst = self.pos0 + lo * 8
+            a.pos_dst = self.pos_dst
         else:
             a.pos_new = a.pos_dst = None
-        if held is not None and int(held[2]) > 0:
-            hp, hv, R = held
-            if hv.dtype == torch.bool:
-                hv = hv.view(torch.uint8)
-            if hp.dtype != torch.int64 or int(R) > S - 1 or hp.shape[0] != B or hv.shape[0] != B \
-                    or hp.shape[-1] < R or hv.shape[-1] < R or hp.stride(-1) != 1 or hv.stride(-1) != 1 \
-                    or (hp.dim() == 3 and hp.shape[1] != Hk) or (hv.dim() == 3 and hv.shape[1] != Hk) \
-                    or hp.device != self.dev or hv.device != self.dev \
-                    or (cur_pos is not None and (cur_pos.dtype != torch.int64 or cur_pos.device != self.dev)):
+        if held is not None and held[2] > 0:
+            if cur_pos is not None and (cur_pos.dtype is not torch.int64 or cur_pos.get_device() != self.devidx):
                 raise RuntimeError("decode_append_rows: held = (pos (B,R)|(B,Hk,R) int64, valid, R <= S-1)")
-            a.held_len = int(R)
-            a.held_pos, a.hp_sb, a.hp_sh = hp.data_ptr(), hp.stride(0), hp.stride(1) if hp.dim() == 3 else 0
-            a.held_valid, a.hv_sb, a.hv_sh = hv.data_ptr(), hv.stride(0), hv.stride(1) if hv.dim() == 3 else 0
+            key = self.held_key
+            if key is None or held[0] is not key[0] or held[1] is not key[1] or held[2] != key[2] or held[2] > S - 1:
+                self._set_held(held, cur_pos, S)
+                self.held_key = (held[0], held[1], held[2])
             a.cur_pos = None if cur_pos is None else cur_pos.data_ptr()
-        else:
+        elif self.held_key is not None:
             a.held_len, a.held_pos, a.held_valid, a.cur_pos = 0, None, None, None
-        a.scaling = scaling
-        out = torch.empty((B, self.Hq, 1, D) if keepdim else (B, self.Hq, D), dtype=self.dtype, device=self.dev)
+            self.held_key = None
+        if scaling != self.scaling:
+            a.scaling = self.scaling = scaling
+        out = torch.empty((self.B, self.Hq, 1, self.D) if keepdim else (self.B, self.Hq, self.D), dtype=self.dtype,
+                          device=self.dev)
         a.out = out.data_ptr()
-        stream = stream_handle(self.dev)
+        stream = _raw_stream(self.devidx) if _raw_stream is not None else stream_handle(self.dev)
         if stream != self.stream:
             self._bind_stream(stream, S)
-        rc = self.lib.hc_decode_attn_append_packed(ctypes.addressof(a), stream)
+        rc = self.fn(self.addr, stream)
         if rc == N.HC_ERR_WORKSPACE:
             self._bind_stream(stream, S)        # a longer buffer than the one the workspace was sized for
-            rc = self.lib.hc_decode_attn_append_packed(ctypes.addressof(a), stream)
+            rc = self.fn(self.addr, stream)
         N.check(rc, "hc_decode_attn_append")
         return out
 

@@ -280,12 +280,17 @@ def test_packed_append_rows_equal_the_scalar_entry():
         kb[:, :, :R], vb[:, :, :R] = hk.to(DEV), hv.to(DEV)
     hpos = torch.randint(0, n0 + 40, (B, Hk, R), generator=g).to(DEV)
     hval = (torch.rand((B, Hk, R), generator=g) < 0.8).to(DEV)
+    # a second held slot (new tensors, as an injection makes) from step 12 on,
+    # and a shorter one from step 18 on: the struct's held fields follow
+    hpos2 = torch.randint(0, n0 + 40, (B, Hk, R), generator=g).to(DEV)
+    hval2 = (torch.rand((B, Hk, R), generator=g) < 0.5).to(DEV)
     side = torch.cuda.Stream(device=DEV)
     for step in range(24):                                   # grows past n0 + 8 on step 8
         q = torch.randn((B, Hq, 1, D), generator=g).to(dtype).to(DEV)
         kn, vn, pn = (torch.randn((B, Hk, 1, D), generator=g).to(dtype).to(DEV) for _ in range(3))
         posn = torch.full((B, 1), n0 + step, dtype=torch.int64, device=DEV)
-        held = (hpos, hval, R) if step % 3 else None
+        hp_, hv_, R_ = (hpos, hval, R) if step < 12 else ((hpos2, hval2, R) if step < 18 else (hpos2, hval2, R // 2))
+        held = (hp_, hv_, R_) if step % 3 else None
         on_side = step in (5, 6, 15)
         if on_side:
             side.wait_stream(torch.cuda.current_stream(DEV))
@@ -293,7 +298,7 @@ def test_packed_append_rows_equal_the_scalar_entry():
             outs = []
             for i, b in enumerate(bufs):
                 b.ensure(b.n + 1)
-                r = R if held else 0
+                r = R_ if held else 0
                 lo, S = b.held - r, r + b.n + 1
                 if i == 0:
                     o = ops.decode_append_rows(q, b.st, lo, S, kn, vn, 0.088, p_new=pn, pos_new=posn, held=held,
@@ -303,7 +308,7 @@ def test_packed_append_rows_equal_the_scalar_entry():
                     o = ops.decode_attention_append(
                         q, st["k"][:, :, lo:lo + S], st["v"][:, :, lo:lo + S], kn, vn, 0.088,
                         pre=(pn, st["p"][:, :, lo:]), pos=(posn, st["pos"][:, lo:]), held_len=r,
-                        held_pos=hpos if held else None, held_valid=hval if held else None,
+                        held_pos=hp_ if held else None, held_valid=hv_ if held else None,
                         cur_pos=posn[0] if held else None).unsqueeze(2)
                 b.n += 1
                 outs.append(o)
@@ -324,6 +329,39 @@ def test_packed_append_rows_equal_the_scalar_entry():
     want = ref.decode_attention(q8.cpu(), b0.st["k"][:, :, b0.held:b0.held + b0.n + 1].cpu(),
                                 b0.st["v"][:, :, b0.held:b0.held + b0.n + 1].cpu(), 0.088)
     assert np.abs(o8.float().cpu().numpy() - want).max() <= 2e-3
+
+
+def test_packed_append_rows_argument_errors():
+    """decode_append_rows rejects, before any launch, rows of the wrong shape,
+    dtype or device, a held slot that reaches the token's row, and pre-RoPE /
+    position rows for a buffer that keeps none."""
+    from hotcold_kv.hot_buffer import HotBuffer
+    B, Hq, Hk, D = 1, 8, 2, 64
+    b = HotBuffer(B, Hk, D, torch.float16, DEV, 32, held=4)
+    b.append(*(torch.zeros((B, Hk, 8, D), dtype=torch.float16, device=DEV) for _ in range(2)))
+    q = torch.zeros((B, Hq, 1, D), dtype=torch.float16, device=DEV)
+    kn = torch.zeros((B, Hk, 1, D), dtype=torch.float16, device=DEV)
+    lo, S = b.held, b.n + 1
+    ops.decode_append_rows(q, b.st, lo, S, kn, kn, 0.1)      # the valid call
+    with pytest.raises(RuntimeError, match="q must be"):
+        ops.decode_append_rows(torch.zeros((B, Hq, 2, D), dtype=torch.float16, device=DEV), b.st, lo, S, kn, kn, 0.1)
+    with pytest.raises(RuntimeError, match="k_new must be"):
+        ops.decode_append_rows(q, b.st, lo, S, kn.float(), kn, 0.1)
+    with pytest.raises(RuntimeError, match="v_new must be"):
+        ops.decode_append_rows(q, b.st, lo, S, kn, kn.cpu(), 0.1)
+    with pytest.raises(RuntimeError, match="unit last stride"):
+        ops.decode_append_rows(q, b.st, lo, S, kn, torch.zeros((B, Hk, 1, 2 * D), dtype=torch.float16,
+                                                                device=DEV)[..., ::2], 0.1)
+    with pytest.raises(RuntimeError, match="outside the buffer"):
+        ops.decode_append_rows(q, b.st, lo, 10 ** 6, kn, kn, 0.1)
+    with pytest.raises(RuntimeError, match="pre-RoPE"):
+        ops.decode_append_rows(q, b.st, lo, S, kn, kn, 0.1, p_new=kn)
+    hp = torch.zeros((B, Hk, 4), dtype=torch.int64, device=DEV)
+    hv = torch.ones((B, Hk, 4), dtype=torch.bool, device=DEV)
+    with pytest.raises(RuntimeError, match="held"):
+        ops.decode_append_rows(q, b.st, 0, 4, kn, kn, 0.1, held=(hp, hv, 4), cur_pos=hp[0, 0, :1])
+    o = ops.decode_append_rows(q, b.st, 0, 4 + S, kn, kn, 0.1, held=(hp, hv, 4), cur_pos=hp[0, 0, :1])
+    assert o.shape == (B, Hq, D) and torch.isfinite(o.float()).all()
 
 
 def test_decode_append_argument_errors():
