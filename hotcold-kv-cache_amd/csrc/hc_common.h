@@ -262,6 +262,15 @@ __device__ __forceinline__ void bload(__amdgpu_buffer_rsrc_t r, uint32_t off, ui
   }
 }
 
+// A 16-byte raw buffer load with a scalar (wave-uniform) offset added to the
+// lane's offset.
+template <int BYTES>
+__device__ __forceinline__ void bload_so(__amdgpu_buffer_rsrc_t r, uint32_t off, uint32_t soff, uint32_t* w) {
+  static_assert(BYTES == 16, "bload_so: 16-byte loads");
+  const u32x4 x = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
+  w[0] = x[0]; w[1] = x[1]; w[2] = x[2]; w[3] = x[3];
+}
+
 // Raw buffer stores: a store whose offset is past the extent is dropped.
 template <int BYTES>
 __device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, uint32_t off, const uint32_t* w) {

@@ -104,9 +104,11 @@ struct KOperand<half_t> {
   static constexpr int DSTEP = 8;  // dims per load
   uint32_t w[4];
   __device__ static uint32_t sel(int kk) { return 0x0c0c0000u | ((uint32_t)(2 * kk + 1) << 8) | (uint32_t)(2 * kk); }
+  // The dim offset is the load's scalar offset: no select and no add per load
+  // (kOob stays past the extent, and a valid row's 16 bytes stay in the row).
   __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int d0, int kk) {
     (void)kk;
-    bload<16>(r, row_off == kOob ? kOob : row_off + (uint32_t)(d0 * 2), w);
+    bload_so<16>(r, row_off, (uint32_t)(d0 * 2), w);
   }
   __device__ double elem(int half, uint32_t sl) const {
     const uint32_t bits = half ? __builtin_amdgcn_perm(w[3], w[2], sl) : __builtin_amdgcn_perm(w[1], w[0], sl);
@@ -120,9 +122,11 @@ struct KOperand<bf16_t> {
   uint32_t w[4];
   // the element's two bytes land in the high half: the fp32 of the bf16
   __device__ static uint32_t sel(int kk) { return ((uint32_t)(2 * kk + 1) << 24) | ((uint32_t)(2 * kk) << 16) | 0x0c0cu; }
+  // The dim offset is the load's scalar offset: no select and no add per load
+  // (kOob stays past the extent, and a valid row's 16 bytes stay in the row).
   __device__ void load(__amdgpu_buffer_rsrc_t r, uint32_t row_off, int d0, int kk) {
     (void)kk;
-    bload<16>(r, row_off == kOob ? kOob : row_off + (uint32_t)(d0 * 2), w);
+    bload_so<16>(r, row_off, (uint32_t)(d0 * 2), w);
   }
   __device__ double elem(int half, uint32_t sl) const {
     const uint32_t bits = half ? __builtin_amdgcn_perm(w[3], w[2], sl) : __builtin_amdgcn_perm(w[1], w[0], sl);
