@@ -565,6 +565,22 @@ extern "C" int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_
                      &ev);
 }
 
+extern "C" int hc_decode_attn_h2o_evict_packed(const hc_decode_h2o_evict_args* a, void* stream) {
+  HC_REQUIRE(a != nullptr, "decode_h2o_evict_packed: null argument struct");
+  HC_REQUIRE(a->dtype >= INT32_MIN && a->dtype <= INT32_MAX, "decode_h2o_evict_packed: bad dtype");
+  return hc_decode_attn_h2o_evict((int)a->dtype, a->B, a->Hq, a->Hk, a->D, a->S, a->q, a->q_sb, a->q_sh, a->k,
+                                  a->k_sb, a->k_sh, a->k_ss, a->v, a->v_sb, a->v_sh, a->v_ss, a->k_new, a->kn_sb,
+                                  a->kn_sh, a->v_new, a->vn_sb, a->vn_sh, a->scaling, a->out, a->o_sb, a->o_sh, a->acc,
+                                  a->a_sb, a->a_sh, a->window, a->budget, a->k_dst, a->kd_sb, a->kd_sh, a->kd_ss,
+                                  a->v_dst, a->vd_sb, a->vd_sh, a->vd_ss, a->acc_dst, a->ad_sb, a->ad_sh, a->workspace,
+                                  a->workspace_bytes, a->num_splits, stream);
+}
+
+extern "C" int64_t hc_decode_h2o_evict_args_size(void) { return (int64_t)sizeof(hc_decode_h2o_evict_args); }
+
+static_assert(sizeof(hc_decode_h2o_evict_args) == 46 * 8,
+              "hc_decode_h2o_evict_args: every field is 8 bytes, no padding");
+
 // ---------------------------------------------------------------------------
 // Allocation-free fused append + decode, for callers that cannot allocate
 // (code under HIP graph capture, tight serving loops, harnesses that forbid

@@ -81,6 +81,8 @@ SIGNATURES = {
         _vp]),
     "hc_decode_attn_append_packed": (_int, [_vp, _vp]),
     "hc_decode_append_args_size": (_i64, []),
+    "hc_decode_attn_h2o_evict_packed": (_int, [_vp, _vp]),
+    "hc_decode_h2o_evict_args_size": (_i64, []),
     "hc_decode_attn_append_noalloc": (_int, [
         _int, _i64, _i64, _i64, _i64, _i64,
         _vp, _i64, _i64,
@@ -223,6 +225,18 @@ class DecodeAppendArgs(ctypes.Structure):
         ("workspace_bytes num_splits", _i64)) for n in names.split()]
 
 
+class DecodeH2OEvictArgs(ctypes.Structure):
+    """ctypes mirror of hc_decode_h2o_evict_args (include/hotcold_hip.h):
+    every field 8 bytes, in the header's order."""
+    _fields_ = [(n, t) for names, t in (
+        ("dtype B Hq Hk D S", _i64), ("q", _vp), ("q_sb q_sh", _i64), ("k", _vp), ("k_sb k_sh k_ss", _i64),
+        ("v", _vp), ("v_sb v_sh v_ss", _i64), ("k_new", _vp), ("kn_sb kn_sh", _i64), ("v_new", _vp),
+        ("vn_sb vn_sh", _i64), ("scaling", _dbl), ("out", _vp), ("o_sb o_sh", _i64), ("acc", _vp),
+        ("a_sb a_sh window budget", _i64), ("k_dst", _vp), ("kd_sb kd_sh kd_ss", _i64), ("v_dst", _vp),
+        ("vd_sb vd_sh vd_ss", _i64), ("acc_dst", _vp), ("ad_sb ad_sh", _i64), ("workspace", _vp),
+        ("workspace_bytes num_splits", _i64)) for n in names.split()]
+
+
 def library_path():
     return _LIB_PATH
 
@@ -246,6 +260,8 @@ def lib():
             fn.argtypes = args
         if handle.hc_decode_append_args_size() != ctypes.sizeof(DecodeAppendArgs):
             raise RuntimeError("hotcold_kv: hc_decode_append_args layout differs between the library and the binding")
+        if handle.hc_decode_h2o_evict_args_size() != ctypes.sizeof(DecodeH2OEvictArgs):
+            raise RuntimeError("hotcold_kv: hc_decode_h2o_evict_args layout differs between the library and the binding")
         _lib = handle
     return _lib
 

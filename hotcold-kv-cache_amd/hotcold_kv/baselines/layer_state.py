@@ -218,17 +218,15 @@ class PressLayerState:
                 and ops.h2o_evicts_one(n, self.window_size, self.budget)):
             # one row over budget: append, attention, score update and the
             # one-row eviction in one call, written into the second buffers
+            # (rows addressed by offset in the two storages: no views per step)
             self.buf.ensure(n)
             self._h2o_storage()
             lo = self.buf.held
-            out = ops.decode_attention_h2o_evict(q_post, self.buf.st["k"][:, :, lo:lo + n],
-                                                 self.buf.st["v"][:, :, lo:lo + n], scaling,
-                                                 self._h2o[:, :, :n], self.window_size, self.budget,
-                                                 self.buf.spare_rows("k"), self.buf.spare_rows("v"),
-                                                 self._h2o_spare, k_new=k_post, v_new=v)
+            out = ops.decode_h2o_evict_rows(q_post, self.buf.st, lo, n, k_post, v, scaling, self._h2o,
+                                            self.window_size, self.budget, self.buf.spare(), self._h2o_spare, lo)
             self.buf.adopt_spare(n - 1)
             self._h2o, self._h2o_spare = self._h2o_spare, self._h2o
-            return out.unsqueeze(2)  # (B,Hq,1,D)
+            return out  # (B,Hq,1,D)
         self.buf.append(k_post, v)
         self._h2o_storage()
         n = self.buf.n

@@ -422,6 +422,122 @@ def decode_append_rows(q, st, lo, S, k_new, v_new, scaling, p_new=None, pos_new=
     return plan.run(q, int(lo), int(S), k_new, v_new, float(scaling), p_new, pos_new, held, cur_pos, keepdim)
 
 
+class _H2OEvictPlan:
+    """hc_decode_attn_h2o_evict_packed arguments of one (source storage,
+    destination storage, scores, destination scores) quadruple: everything
+    but q, the token's rows, S and out is filled in once.  An H2O layer at
+    budget alternates between two such plans (its storages swap every step)."""
+
+    def __init__(self, st, Hq, acc, dst, acc_dst, dst_lo, window, budget):
+        k, v, kd, vd = st["k"], st["v"], dst["k"], dst["v"]
+        for t in (v, kd, vd):
+            if t.dim() != 4 or t.shape[0] != k.shape[0] or t.shape[1] != k.shape[1] or t.shape[3] != k.shape[3] \
+                    or t.dtype != k.dtype or t.stride(-1) != 1 or t.get_device() != k.get_device():
+                raise RuntimeError("decode_h2o_evict_rows: source and destination K/V storages must be matching "
+                                   "(B,Hk,cap,D) device tensors")
+        if k.dim() != 4 or k.stride(-1) != 1 or not k.is_cuda:
+            raise RuntimeError("decode_h2o_evict_rows: hot-buffer K/V storage must be 4D device tensors")
+        B, Hk, cap, D = k.shape
+        for name, t in (("acc", acc), ("acc_dst", acc_dst)):
+            if t.dtype != torch.float32 or t.dim() != 3 or tuple(t.shape[:2]) != (B, Hk) or t.stride(2) != 1 \
+                    or t.get_device() != k.get_device():
+                raise RuntimeError(f"decode_h2o_evict_rows: {name} must be (B,Hk,n) fp32 with unit last stride")
+        self.tensors = (k, v, kd, vd, acc, acc_dst)
+        self.Hq, self.dst_lo, self.window, self.budget = int(Hq), int(dst_lo), int(window), int(budget)
+        self.B, self.Hk, self.cap, self.D = B, Hk, cap, D
+        self.acc_cap, self.acc_dst_cap, self.dst_cap = acc.shape[2], acc_dst.shape[2], kd.shape[2] - int(dst_lo)
+        self.dtype, self.dev, self.devidx, self.es = k.dtype, k.device, k.get_device(), k.element_size()
+        self.qshapes = ((B, self.Hq, D), (B, self.Hq, 1, D))
+        self.tshapes = ((B, Hk, D), (B, Hk, 1, D))
+        a = self.a = N.DecodeH2OEvictArgs()
+        a.dtype, a.B, a.Hq, a.Hk, a.D = N.dtype_code(k.dtype), B, self.Hq, Hk, D
+        ks, vs, kds, vds = k.stride(), v.stride(), kd.stride(), vd.stride()
+        a.k_sb, a.k_sh, a.k_ss = ks[0], ks[1], ks[2]
+        a.v_sb, a.v_sh, a.v_ss = vs[0], vs[1], vs[2]
+        a.kd_sb, a.kd_sh, a.kd_ss = kds[0], kds[1], kds[2]
+        a.vd_sb, a.vd_sh, a.vd_ss = vds[0], vds[1], vds[2]
+        a.k_dst = kd.data_ptr() + self.dst_lo * kds[2] * self.es
+        a.v_dst = vd.data_ptr() + self.dst_lo * vds[2] * self.es
+        self.k0, self.v0, self.krow, self.vrow = k.data_ptr(), v.data_ptr(), ks[2] * self.es, vs[2] * self.es
+        acs, ads = acc.stride(), acc_dst.stride()
+        a.acc, a.a_sb, a.a_sh = acc.data_ptr(), acs[0], acs[1]
+        a.acc_dst, a.ad_sb, a.ad_sh = acc_dst.data_ptr(), ads[0], ads[1]
+        a.window, a.budget = self.window, self.budget
+        a.o_sb, a.o_sh = self.Hq * D, D
+        self.stream, self.ws, self.lo, self.scaling = None, None, None, None
+        self.lib = N.lib()
+        self.fn = self.lib.hc_decode_attn_h2o_evict_packed
+        self.addr = ctypes.addressof(a)
+
+    def matches(self, st, Hq, acc, dst, acc_dst, dst_lo, window, budget):
+        t = self.tensors
+        return (t[0] is st["k"] and t[1] is st["v"] and t[2] is dst["k"] and t[3] is dst["v"] and t[4] is acc
+                and t[5] is acc_dst and self.Hq == Hq and self.dst_lo == dst_lo and self.window == window
+                and self.budget == budget)
+
+    def _bind_stream(self, stream, S):
+        need = self.lib.hc_decode_attn_workspace_size(self.B, self.Hq, self.Hk, self.D, max(S, self.cap), 0, 1)
+        self.ws = _workspace("decode", self.dev, need)
+        self.a.workspace, self.a.workspace_bytes = self.ws.data_ptr(), self.ws.numel()
+        self.stream = stream
+
+    def run(self, q, lo, S, k_new, v_new, scaling):
+        a = self.a
+        if lo < 0 or S < 2 or lo + S > self.cap or S > self.acc_cap or S - 1 > self.dst_cap \
+                or S - 1 > self.acc_dst_cap:
+            raise RuntimeError(f"decode_h2o_evict_rows: rows {lo}..{lo + S - 1} (kept {S - 1}) outside the "
+                               f"buffers ({self.cap} rows, scores {self.acc_cap}, destination {self.dst_cap})")
+        a.q, a.q_sb, a.q_sh = _row_args(q, self.qshapes, self.dtype, self.devidx, "q")
+        a.k_new, a.kn_sb, a.kn_sh = _row_args(k_new, self.tshapes, self.dtype, self.devidx, "k_new")
+        a.v_new, a.vn_sb, a.vn_sh = _row_args(v_new, self.tshapes, self.dtype, self.devidx, "v_new")
+        a.S = S
+        if lo != self.lo:
+            a.k, a.v = self.k0 + lo * self.krow, self.v0 + lo * self.vrow
+            self.lo = lo
+        if scaling != self.scaling:
+            a.scaling = self.scaling = scaling
+        out = torch.empty((self.B, self.Hq, 1, self.D), dtype=self.dtype, device=self.dev)
+        a.out = out.data_ptr()
+        stream = _raw_stream(self.devidx) if _raw_stream is not None else stream_handle(self.dev)
+        if stream != self.stream:
+            self._bind_stream(stream, S)
+        rc = self.fn(self.addr, stream)
+        if rc == N.HC_ERR_WORKSPACE:
+            self._bind_stream(stream, S)
+            rc = self.fn(self.addr, stream)
+        N.check(rc, "hc_decode_attn_h2o_evict")
+        return out
+
+
+def _row_args(t, shapes, dtype, devidx, what):
+    """data_ptr and (batch, head) strides of a (B,H,D) / (B,H,1,D) row tensor
+    on device devidx, in dtype, with a unit last stride (no view is made)."""
+    sh = t.shape
+    if (sh != shapes[0] and sh != shapes[1]) or t.dtype is not dtype or t.get_device() != devidx:
+        raise RuntimeError(f"decode_h2o_evict_rows: {what} must be {shapes[0]} or {shapes[1]} device rows in "
+                           f"{dtype}; got {tuple(sh)} {t.dtype} on {t.device}")
+    st = t.stride()
+    if st[-1] != 1:
+        raise RuntimeError(f"decode_h2o_evict_rows: {what} needs a unit last stride")
+    return t.data_ptr(), st[0], st[1]
+
+
+def decode_h2o_evict_rows(q, st, lo, S, k_new, v_new, scaling, acc, window_size, budget, dst, acc_dst, dst_lo=0):
+    """decode_attention_h2o_evict over rows lo .. lo+S-1 of a hot buffer's
+    storage st ({"k", "v"} (B,Hk,cap,D)), addressed by offset instead of
+    through views (the H2O decode step of the drop-in at budget; same launch,
+    less host work): row lo+S-1 receives k_new / v_new, acc (B,Hk,>=S) fp32
+    holds the scores of rows lo.. (column i: row lo+i), and the S-1 kept rows
+    and their updated scores go to rows dst_lo.. of the storage dst and to
+    acc_dst (B,Hk,>=S-1).  The packed argument struct of the quadruple is kept in st.
+    Returns out (B,Hq,1,D)."""
+    Hq = q.shape[1]
+    plan = st.get("_h2o_plan")
+    if plan is None or not plan.matches(st, Hq, acc, dst, acc_dst, dst_lo, window_size, budget):
+        plan = st["_h2o_plan"] = _H2OEvictPlan(st, Hq, acc, dst, acc_dst, dst_lo, window_size, budget)
+    return plan.run(q, int(lo), int(S), k_new, v_new, float(scaling))
+
+
 def decode_attention_h2o(q, k, v, scaling, acc, out=None, num_splits=0):
     """Decode attention of q (B,Hq,D) or (B,Hq,1,D) over k/v (B,Hk,S,D) that
     adds each key's attention probability, averaged over the query heads of

@@ -268,6 +268,36 @@ int hc_decode_attn_h2o_evict(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64
                              void* workspace, int64_t workspace_bytes, int64_t num_splits, void* stream);
 
 /*
+ * hc_decode_attn_h2o_evict with its arguments in one struct: the same launch
+ * and results (layer_state.py:102-114 then _compress, :68-79), for callers
+ * that run it every decode step.  A caller fills the fields that stay fixed
+ * (shape, the source and destination rows, the score buffers, window, budget,
+ * workspace) once per pair of storages and rewrites only q, the token's rows,
+ * S and out per step.  Every field is 8 bytes (int64 / pointer / double), so
+ * the layout has no padding; hc_decode_h2o_evict_args_size() returns sizeof
+ * for a binding to check.
+ */
+typedef struct hc_decode_h2o_evict_args {
+  int64_t dtype, B, Hq, Hk, D, S;
+  const void* q; int64_t q_sb, q_sh;
+  const void* k; int64_t k_sb, k_sh, k_ss;
+  const void* v; int64_t v_sb, v_sh, v_ss;
+  const void* k_new; int64_t kn_sb, kn_sh;
+  const void* v_new; int64_t vn_sb, vn_sh;
+  double scaling;
+  void* out; int64_t o_sb, o_sh;
+  const float* acc; int64_t a_sb, a_sh;
+  int64_t window, budget;
+  void* k_dst; int64_t kd_sb, kd_sh, kd_ss;
+  void* v_dst; int64_t vd_sb, vd_sh, vd_ss;
+  float* acc_dst; int64_t ad_sb, ad_sh;
+  void* workspace; int64_t workspace_bytes, num_splits;
+} hc_decode_h2o_evict_args;
+
+int hc_decode_attn_h2o_evict_packed(const hc_decode_h2o_evict_args* args, void* stream);
+int64_t hc_decode_h2o_evict_args_size(void);
+
+/*
  * Window importance scores per KV head, fp32 [B][Hk][S] (row stride S).
  * Replaces snapkv_importance (scoring.py:50-79) with _group_query_to_kv
  * (scoring.py:17-26) and pool1d (scoring.py:40-47) in HC_SCORE_SNAPKV mode,

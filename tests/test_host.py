@@ -49,22 +49,28 @@ def test_library_exports_every_header_symbol():
     assert lib.hc_abi_version() == 1
 
 
-def test_packed_decode_args_mirror_the_header_struct():
-    """The ctypes mirror of hc_decode_append_args: the header's field names in
-    order, 8 bytes each, and the library's sizeof."""
+@pytest.mark.parametrize("struct,mirror,size_fn", [
+    ("hc_decode_append_args", "DecodeAppendArgs", "hc_decode_append_args_size"),
+    ("hc_decode_h2o_evict_args", "DecodeH2OEvictArgs", "hc_decode_h2o_evict_args_size"),
+])
+def test_packed_decode_args_mirror_the_header_struct(struct, mirror, size_fn):
+    """The ctypes mirrors of the packed argument structs: the header's field
+    names in order, 8 bytes each, and the library's sizeof."""
     text = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
-    body = re.search(r"typedef struct hc_decode_append_args \{(.*?)\} hc_decode_append_args;", text, re.S).group(1)
+    body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
     names = [n.strip().lstrip("*") for decl in body.split(";") if decl.strip()
              for n in re.sub(r"^\s*(const\s+)?\w+\s*\**", "", decl.strip()).split(",")]
-    fields = [f[0] for f in N.DecodeAppendArgs._fields_]
+    cls = getattr(N, mirror)
+    fields = [f[0] for f in cls._fields_]
     assert fields == names
     for i, f in enumerate(fields):
-        assert getattr(N.DecodeAppendArgs, f).offset == 8 * i, f
-    assert N.lib().hc_decode_append_args_size() == ctypes.sizeof(N.DecodeAppendArgs) == 8 * len(fields)
+        assert getattr(cls, f).offset == 8 * i, f
+    assert getattr(N.lib(), size_fn)() == ctypes.sizeof(cls) == 8 * len(fields)
 
 
 def test_packed_decode_rejects_a_null_struct():
     assert N.lib().hc_decode_attn_append_packed(None, None) == N.HC_ERR_INVALID
+    assert N.lib().hc_decode_attn_h2o_evict_packed(None, None) == N.HC_ERR_INVALID
 
 
 def test_abi_constants_match_header():

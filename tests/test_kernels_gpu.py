@@ -704,6 +704,67 @@ def test_decode_attention_h2o_evict_argument_errors():
     assert rc != 0 and "alias" in lib.hc_last_error().decode()
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_packed_h2o_evict_rows_equal_the_scalar_entry(dtype):
+    """decode_h2o_evict_rows (hc_decode_attn_h2o_evict_packed over argument
+    structs kept per storage pair) and decode_attention_h2o_evict
+    (hc_decode_attn_h2o_evict) on twin buffers at budget: identical outputs,
+    kept rows and scores step after step, while the two storages and score
+    buffers swap every step and a few steps run on a side stream."""
+    from hotcold_kv.hot_buffer import HotBuffer
+    B, Hq, Hk, D, budget, W = 2, 32, 8, 128, 300, 32
+    g = torch.Generator().manual_seed(11)
+    cap = budget + 16
+    bufs = [HotBuffer(B, Hk, D, dtype, DEV, cap) for _ in range(2)]
+    k0, v0 = (torch.randn((B, Hk, budget, D), generator=g).to(dtype).to(DEV) for _ in range(2))
+    acc0 = torch.rand((B, Hk, budget), generator=g).to(DEV)
+    accs = []
+    for b in bufs:
+        b.append(k0, v0)
+        a = torch.zeros((B, Hk, cap), device=DEV)
+        a[:, :, :budget] = acc0
+        accs.append([a, torch.empty_like(a)])
+    side = torch.cuda.Stream(device=DEV)
+    for step in range(40):
+        q = torch.randn((B, Hq, 1, D), generator=g).to(dtype).to(DEV)
+        kn, vn = (torch.randn((B, Hk, 1, D), generator=g).to(dtype).to(DEV) for _ in range(2))
+        on_side = step in (7, 8, 21)
+        if on_side:
+            side.wait_stream(torch.cuda.current_stream(DEV))
+        with torch.cuda.stream(side) if on_side else contextlib.nullcontext():
+            outs = []
+            for i, b in enumerate(bufs):
+                n = b.n + 1
+                b.ensure(n)
+                acc, acc_sp = accs[i]
+                if i == 0:
+                    o = ops.decode_h2o_evict_rows(q, b.st, b.held, n, kn, vn, 0.088, acc, W, budget, b.spare(),
+                                                  acc_sp, b.held)
+                else:
+                    o = ops.decode_attention_h2o_evict(q, b.st["k"][:, :, :n], b.st["v"][:, :, :n], 0.088,
+                                                       acc[:, :, :n], W, budget, b.spare_rows("k"),
+                                                       b.spare_rows("v"), acc_sp, k_new=kn, v_new=vn).unsqueeze(2)
+                b.adopt_spare(n - 1)
+                accs[i] = [acc_sp, acc]
+                outs.append(o)
+        torch.cuda.current_stream(DEV).wait_stream(side)
+        assert torch.equal(outs[0], outs[1]), step
+    torch.cuda.synchronize()
+    for name in ("k", "v"):
+        assert torch.equal(bufs[0].st[name][:, :, :budget], bufs[1].st[name][:, :, :budget]), name
+    assert torch.equal(accs[0][0][:, :, :budget], accs[1][0][:, :, :budget])
+    # argument errors, before any launch (rows, shapes) and from the library (not one row over budget)
+    b, (acc, acc_sp) = bufs[0], accs[0]
+    q = torch.zeros((B, Hq, 1, D), dtype=dtype, device=DEV)
+    kn = torch.zeros((B, Hk, 1, D), dtype=dtype, device=DEV)
+    with pytest.raises(RuntimeError, match="outside the buffers"):
+        ops.decode_h2o_evict_rows(q, b.st, 0, cap + 1, kn, kn, 0.088, acc, W, budget, b.spare(), acc_sp)
+    with pytest.raises(RuntimeError, match="q must be"):
+        ops.decode_h2o_evict_rows(q[..., :64], b.st, 0, budget + 1, kn, kn, 0.088, acc, W, budget, b.spare(), acc_sp)
+    with pytest.raises(RuntimeError, match="not one"):
+        ops.decode_h2o_evict_rows(q, b.st, 0, budget, kn, kn, 0.088, acc, W, budget, b.spare(), acc_sp)
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("to_host", [False, True])
 def test_gather_evict_upcast_and_stage(dtype, to_host):
