@@ -738,18 +738,21 @@ def hotcold_pipeline(w, dev, profile_steps=None):
     layers = [HotColdLayer(ctrl) for _ in range(L)]
     steps = w.decode_steps if profile_steps is None else profile_steps
     toks = [[synthetic.make_decode_token(w, l, t, seed=0, device=dev) for l in range(L)] for t in range(steps)]
+    prompts = [synthetic.make_prompt(w, layer=l, seed=0, device=dev) for l in range(L)]   # inputs, not timed
+    ctrl._lazy_init(prompts[0]["k_pre"], n_layers=L)
+    windows = [p["q_post"][:, :, -w.window:, :].contiguous() for p in prompts]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for l in range(L):
-        p = synthetic.make_prompt(w, layer=l, seed=0, device=dev)
-        if l == 0:
-            ctrl._lazy_init(p["k_pre"], n_layers=L)
-        layers[l].set_last_query_post(p["q_post"][:, :, -w.window:, :].contiguous())
+        p = prompts[l]
+        layers[l].set_last_query_post(windows[l])
         layers[l].update(key_states=p["k_post"], value_states=p["v"], layer_idx=l,
                          cache_kwargs={"pre_key_states": p["k_pre"], "positions": p["positions"]})
-        del p
     torch.cuda.synchronize()
     prefill_s = time.perf_counter() - t0
+    ctrl.wait_cold_adds()
+    prefill_store_s = time.perf_counter() - t0
+    del prompts, windows, p
     step_ms = []
     torch.cuda.synchronize()
     t_all = time.perf_counter()
@@ -772,6 +775,10 @@ def hotcold_pipeline(w, dev, profile_steps=None):
         "workload": w.name, "layers": L, "batch": B, "prompt": w.seq_len, "budget": w.budget, "held": w.held,
         "retrieve_every": w.retrieve_every, "decode_steps": steps,
         "prefill_compress_evict_s": round(prefill_s, 3),
+        "prefill_cold_store_filled_s": round(prefill_store_s, 3),
+        "prefill_timing": "32 layers' compaction + eviction through HotColdLayer.update, decode thread's wall "
+                          "time (cold-store adds still running on the library's workers), then until every add "
+                          "is applied; prompt generation not timed",
         "cold_tokens_per_layer": ctrl.cold_size(0),
         "hot_rows_per_layer_end": layers[0].hot_length(),
         "step_us_wall_mean": round(total_ms * 1e3 / steps, 1),

@@ -95,6 +95,30 @@ struct ColdStore {
     std::unique_lock<std::mutex> lk(jobs_mu);
     jobs_cv.wait(lk, [&] { return jobs_in_flight == 0; });
   }
+  // Asynchronous adds take a ticket when submitted and are applied in ticket
+  // order.  add_served counts the applied ones.  A reader waits for the adds
+  // submitted before it: wait_adds(ticket) returns once every add with a
+  // smaller ticket has been applied.
+  mutable int64_t add_next = 0, add_served = 0;
+  int64_t take_ticket() const {
+    std::lock_guard<std::mutex> lk(jobs_mu);
+    return add_next++;
+  }
+  int64_t tickets() const {
+    std::lock_guard<std::mutex> lk(jobs_mu);
+    return add_next;
+  }
+  void wait_adds(int64_t ticket) const {
+    std::unique_lock<std::mutex> lk(jobs_mu);
+    jobs_cv.wait(lk, [&] { return add_served >= ticket; });
+  }
+  void serve_ticket() const {
+    std::lock_guard<std::mutex> lk(jobs_mu);
+    ++add_served;
+    jobs_cv.notify_all();
+  }
+  // every add submitted so far has been applied
+  void wait_all_adds() const { wait_adds(tickets()); }
 
   bool allocate() {
     kpre.reset((size_t)cap * H * D);
@@ -112,8 +136,8 @@ struct ColdStore {
   // Search vector(s) of the token in `slot` (its key already stored).
   void set_vec(int64_t slot) {
     const float* kp = &kpre[(size_t)slot * H * D];
-    double x[4096];
     const int64_t n = std::min(D, VD);
+    double x[4096];
     for (int64_t vh = 0; vh < VH; ++vh) {
       if (VH == 1) {
         // head mean: fp64, heads added in order (vectorised across dims)
@@ -296,16 +320,16 @@ extern "C" void hc_cold_destroy(void* store) {
 extern "C" int64_t hc_cold_size(const void* store) {
   const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
   if (!s) return 0;
+  s->wait_all_adds();
   std::shared_lock<std::shared_mutex> lk(s->mu);
   return s->size;
 }
 
-extern "C" int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
-                           const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos,
-                           const int64_t* evicted_idx) {
-  ColdStore* s = as_store(store);
-  if (!s) return set_error(HC_ERR_INVALID, "cold_add: null store");
-  if (te < 0 || (te > 0 && (!kpre || !v || !pos))) return set_error(HC_ERR_INVALID, "cold_add: bad arguments");
+namespace {
+
+// The add itself (arguments checked by the caller, earlier adds applied).
+int add_impl(ColdStore* s, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st, const float* v, int64_t v_sh,
+             int64_t v_st, const int64_t* pos, const int64_t* evicted_idx, int64_t nthreads) {
   // tokens kept: evicted_idx[t] >= 0 (datatypes.py:58-63 pads with -1)
   std::vector<int64_t> sel;
   sel.reserve((size_t)te);
@@ -319,7 +343,7 @@ extern "C" int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k
   // distinct slots: the copies and search vectors run on host threads
   constexpr int64_t kChunk = 256;
   const int64_t nchunks = (m - first + kChunk - 1) / kChunk;
-  parallel_for(nchunks, threads_for(0, nchunks), [&](int64_t c) {
+  parallel_for(nchunks, threads_for(nthreads, nchunks), [&](int64_t c) {
     const int64_t i1 = std::min(m, first + (c + 1) * kChunk);
     for (int64_t i = first + c * kChunk; i < i1; ++i) {
       const int64_t t = sel[i];
@@ -329,11 +353,24 @@ extern "C" int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k
   return HC_OK;
 }
 
+}  // namespace
+
+extern "C" int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
+                           const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos,
+                           const int64_t* evicted_idx) {
+  ColdStore* s = as_store(store);
+  if (!s) return set_error(HC_ERR_INVALID, "cold_add: null store");
+  if (te < 0 || (te > 0 && (!kpre || !v || !pos))) return set_error(HC_ERR_INVALID, "cold_add: bad arguments");
+  s->wait_all_adds();  // after the asynchronous adds submitted before it
+  return add_impl(s, te, kpre, k_sh, k_st, v, v_sh, v_st, pos, evicted_idx, 0);
+}
+
 extern "C" int hc_cold_search(const void* store, const float* q, int64_t r, int64_t head, int64_t* out,
                               int64_t* n_out) {
   const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
   if (!s || !q || !out || !n_out) return set_error(HC_ERR_INVALID, "cold_search: null argument");
   if (head < 0 || head >= s->VH) return set_error(HC_ERR_INVALID, "cold_search: head %lld out of range", (long long)head);
+  s->wait_all_adds();
   std::shared_lock<std::shared_mutex> lk(s->mu);
   std::vector<double> ip((size_t)std::max<int64_t>(s->size, 1));
   s->scan(q, head, 0, s->size, ip.data());
@@ -344,6 +381,7 @@ extern "C" int hc_cold_search(const void* store, const float* q, int64_t r, int6
 extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t* pos, float* vec) {
   const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
   if (!s) return set_error(HC_ERR_INVALID, "cold_export: null store");
+  s->wait_all_adds();
   std::shared_lock<std::shared_mutex> lk(s->mu);
   const int64_t HD = s->H * s->D;
   for (int64_t i = 0; i < s->size; ++i) {
@@ -359,11 +397,13 @@ extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t*
   return HC_OK;
 }
 
-extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
-                                int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
-                                float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
-                                int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing,
-                                int64_t nthreads) {
+namespace {
+
+// The search itself (every add the caller must see already applied).
+int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh, int64_t q_dim,
+                  int normalize_q, int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
+                  uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
+                  int64_t* tab_missing, int64_t nthreads) {
   if (B <= 0 || R <= 0 || q_dim <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out)
     return set_error(HC_ERR_INVALID, "cold_retrieve: bad arguments");
   if (tab && (tab_rows <= 0 || tab_row_bytes <= 0 || !tab_out))
@@ -440,6 +480,20 @@ extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, 
   return HC_OK;
 }
 
+}  // namespace
+
+extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
+                                int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
+                                float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                                int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing,
+                                int64_t nthreads) {
+  if (B > 0 && stores)
+    for (int64_t b = 0; b < B; ++b)
+      if (stores[b]) as_store(stores[b])->wait_all_adds();  // after the adds submitted before it
+  return retrieve_impl(stores, B, q, q_sb, q_sh, q_dim, normalize_q, R, per_head, kpre_out, v_out, pos_out, valid_out,
+                       tab, tab_rows, tab_row_bytes, tab_out, tab_missing, nthreads);
+}
+
 // ---------------------------------------------------------------------------
 // Retrievals as jobs on the library's own worker threads.  The decode thread
 // submits a job and later polls it; a worker waits for the job's event (the
@@ -450,7 +504,15 @@ extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, 
 namespace {
 
 struct RetrieveJob {
+  bool is_add = false;           // an asynchronous add instead of a search
   std::vector<void*> stores;
+  std::vector<int64_t> tickets;  // per store: the adds submitted before this search
+  // add arguments (is_add)
+  int64_t add_te = 0, add_k_sh = 0, add_k_st = 0, add_v_sh = 0, add_v_st = 0, add_ticket = 0, add_threads = 0;
+  const float* add_kpre = nullptr;
+  const float* add_v = nullptr;
+  const int64_t* add_pos = nullptr;
+  const int64_t* add_idx = nullptr;
   int64_t B = 0, q_sb = 0, q_sh = 0, q_dim = 0, R = 0, tab_rows = 0, tab_row_bytes = 0, nthreads = 0;
   int64_t n_flags = 0;  // valid_out entries: B * R, or B * heads * R per KV head
   int normalize_q = 0, per_head = 0;
@@ -501,12 +563,24 @@ class JobQueue {
     int rc = HC_OK;
     if (j->wait_event) rc = hc_event_synchronize(j->wait_event);
     int64_t missing = 0, nv = 0;
-    if (rc == HC_OK)
-      rc = hc_cold_retrieve(j->stores.data(), j->B, j->q, j->q_sb, j->q_sh, j->q_dim, j->normalize_q, j->R,
-                            j->per_head, j->kpre_out, j->v_out, j->pos_out, j->valid_out, j->tab, j->tab_rows,
-                            j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
-    if (rc == HC_OK)
-      for (int64_t i = 0; i < j->n_flags; ++i) nv += j->valid_out[i] != 0;
+    if (j->is_add) {
+      // after the store's earlier adds (the queue hands jobs out in order, so
+      // those are running or done); the ticket is served even on failure
+      ColdStore* s = as_store(j->stores[0]);
+      s->wait_adds(j->add_ticket);
+      if (rc == HC_OK)
+        rc = add_impl(s, j->add_te, j->add_kpre, j->add_k_sh, j->add_k_st, j->add_v, j->add_v_sh, j->add_v_st,
+                      j->add_pos, j->add_idx, j->add_threads);
+      s->serve_ticket();
+    } else {
+      for (size_t b = 0; b < j->stores.size(); ++b) as_store(j->stores[b])->wait_adds(j->tickets[b]);
+      if (rc == HC_OK)
+        rc = retrieve_impl(j->stores.data(), j->B, j->q, j->q_sb, j->q_sh, j->q_dim, j->normalize_q, j->R,
+                           j->per_head, j->kpre_out, j->v_out, j->pos_out, j->valid_out, j->tab, j->tab_rows,
+                           j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
+      if (rc == HC_OK)
+        for (int64_t i = 0; i < j->n_flags; ++i) nv += j->valid_out[i] != 0;
+    }
     for (void* st : j->stores) as_store(st)->unpin();
     std::lock_guard<std::mutex> lk(j->mu);
     if (rc != HC_OK) snprintf(j->msg, sizeof(j->msg), "%s", hc_last_error());
@@ -560,7 +634,35 @@ extern "C" void* hc_cold_retrieve_async(void* const* stores, int64_t B, const fl
   j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows; j->tab_row_bytes = tab_row_bytes;
   j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
   j->n_flags = B * R * (per_head ? s0->H : 1);
-  for (int64_t b = 0; b < B; ++b) as_store(stores[b])->pin();
+  for (int64_t b = 0; b < B; ++b) {
+    as_store(stores[b])->pin();
+    j->tickets.push_back(as_store(stores[b])->tickets());
+  }
+  job_queue().push(j, workers);
+  return j;
+}
+
+extern "C" void* hc_cold_add_async(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
+                                   const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos,
+                                   const int64_t* evicted_idx, void* wait_event, int64_t nthreads,
+                                   int64_t workers) {
+  ColdStore* s = as_store(store);
+  if (!s || te < 0 || (te > 0 && (!kpre || !v || !pos))) {
+    set_error(HC_ERR_INVALID, "cold_add_async: bad arguments");
+    return nullptr;
+  }
+  RetrieveJob* j = new (std::nothrow) RetrieveJob();
+  if (!j) {
+    set_error(HC_ERR_INVALID, "cold_add_async: out of host memory");
+    return nullptr;
+  }
+  j->is_add = true;
+  j->stores.assign(1, store);
+  j->add_te = te; j->add_kpre = kpre; j->add_k_sh = k_sh; j->add_k_st = k_st; j->add_v = v; j->add_v_sh = v_sh;
+  j->add_v_st = v_st; j->add_pos = pos; j->add_idx = evicted_idx; j->wait_event = wait_event;
+  j->add_threads = nthreads;
+  s->pin();
+  j->add_ticket = s->take_ticket();
   job_queue().push(j, workers);
   return j;
 }

@@ -159,15 +159,16 @@ class HotColdLayer(CacheLayerMixin):
         ctrl = self.kvctrl
         B, Hk, D = self.buf.B, self.buf.H, self.buf.D
         te = int(evicted.shape[-1])
-        dev_buf, host_buf = ctrl.evict_staging(self.buf.keys.device, B, Hk, te, D)
+        stage = ctrl.evict_stage(self.buf.keys.device, B, Hk, te, D)
         kp_cpu, v_cpu, pos_cpu = ops.gather_evict(evicted, self.buf.pre_keys, self.buf.values, self.buf.positions,
-                                                  dev_out=dev_buf, host_out=host_buf)
+                                                  dev_out=stage.dev, host_out=stage.host)
         idx_cpu = evicted.to("cpu")  # synchronising copy: the staged block is complete after it
         ctrl.dbg["compress_calls"] += 1
         ctrl.dbg["evicted_tokens"] += int(B * te)
-        # the cold store copies the tokens before returning; the staging is reused
+        # the cold store copies the tokens on the library's worker threads while
+        # the prefill goes on; the stage is reused once those adds are done
         ctrl.add_evicted_to_cold_store(layer_idx, EvictedKV(k_pre_cpu=kp_cpu, v_cpu=v_cpu, pos_cpu=pos_cpu,
-                                                            evicted_idx=idx_cpu))
+                                                            evicted_idx=idx_cpu), stage=stage)
 
     # -- transformers cache interface -------------------------------------------------------
     def get_mask_sizes(self, query_length):

@@ -79,6 +79,23 @@ class _Ring:
                                    None if idx is None else idx.ctypes.data)
         N.check(rc, "hc_cold_add")
 
+    def add_async(self, kpre, v, pos, evicted_idx=None, nthreads=0, workers=4):
+        """add() as a job on the library's worker threads (hc_cold_add_async):
+        returns a _Job once submitted.  Adds apply in submission order, and
+        size, searches and later adds wait for the ones submitted before them.
+        The job keeps the arrays it reads alive until it is collected."""
+        kpre = np.ascontiguousarray(kpre, dtype=np.float32)
+        v = np.ascontiguousarray(v, dtype=np.float32)
+        pos = np.ascontiguousarray(pos, dtype=np.int64)
+        te = int(kpre.shape[1])
+        idx = None if evicted_idx is None else np.ascontiguousarray(evicted_idx, dtype=np.int64)
+        h = self._lib.hc_cold_add_async(self.handle, te, kpre.ctypes.data, te * self.D, self.D,
+                                        v.ctypes.data, te * self.D, self.D, pos.ctypes.data,
+                                        None if idx is None else idx.ctypes.data, None, int(nthreads), int(workers))
+        if not h:
+            N.check(N.HC_ERR_INVALID, "hc_cold_add_async")
+        return _Job(h, None, False, (kpre, v, pos, idx))
+
     def search(self, q, r, head=0):
         """Logical indices of the top-r inner products with q (descending,
         ties to the older token)."""
@@ -196,9 +213,34 @@ _NOT_READY = RetrievedKV(k_pre=torch.empty(0), v=torch.empty(0), pos=torch.empty
                          valid=torch.empty(0, dtype=torch.bool), ready=False)
 
 
+class _EvictStage:
+    """One eviction's device and pinned host staging blocks, and the cold-store
+    add jobs still reading the host block."""
+
+    def __init__(self, dev, host):
+        self.dev, self.host, self.jobs = dev, host, []
+
+    def done(self, wait=False):
+        """True once no add reads the host block; a failed add raises here."""
+        pending, err = [], None
+        for j in self.jobs:
+            if not j.poll(wait=wait):
+                pending.append(j)
+            elif j.error is not None and err is None:
+                err = j.error
+        self.jobs = pending
+        if err is not None:
+            raise N.HotColdError(f"hc_cold_add (worker): {err[1]} (status {err[0]})")
+        return not pending
+
+
 class KVController:
     # staging slots per layer: one held, one in copy, one retrieved, one filling
     MAX_SLOTS = 4
+    # Eviction staging blocks: the prefill's cold-store adds run as native jobs
+    # while the next layer proceeds; a third eviction waits for the oldest.
+    MAX_EVICT_STAGES = 2
+    ADD_THREADS = 8
     # Scheduled searches run as jobs on the library's native worker threads
     # (no Python, no thread per search), each on SEARCH_THREADS host threads:
     # every layer searches in the same decode step, and together they keep to
@@ -262,8 +304,7 @@ class KVController:
         self._slots = []
         self._held_slot = []
         self._stream = None
-        self._evict_dev = None
-        self._evict_host = None
+        self._evict_stages = []
         self.last_injected_len = 0
         self.held_mem = []
 
@@ -339,6 +380,9 @@ class KVController:
             for th in self._retrieval_thread:
                 if isinstance(th, _Job):
                     th.join()                   # a search still writing into a slot's buffers
+            for st in getattr(self, "_evict_stages", ()):
+                for j in st.jobs:
+                    j.join()                    # an add still reading a stage's host block
             lib = N.lib()
             for slots in self._slots:
                 for sl in slots:
@@ -379,16 +423,43 @@ class KVController:
             self._rope_tab = tab.view(torch.uint8).numpy().reshape(rows, -1)
         return self._rope_tab
 
-    def evict_staging(self, device, B, H, te, D):
-        """Device and pinned host staging blocks of at least
-        hc_gather_evict_bytes(B, H, te, D) bytes for one eviction; grown on
-        demand and reused (evictions run one at a time on the main thread)."""
+    def evict_stage(self, device, B, H, te, D):
+        """A staging stage (device and pinned host blocks of at least
+        hc_gather_evict_bytes(B, H, te, D) bytes) that no cold-store add is
+        reading: a free one, a new one while there are fewer than
+        MAX_EVICT_STAGES, else the least recently handed out once its adds are
+        done (grown if needed)."""
         nbytes = int(N.lib().hc_gather_evict_bytes(B, H, te, D))
-        if self._evict_dev is None or self._evict_dev.numel() < nbytes or self._evict_dev.device != device:
-            size = max(nbytes, 2 * (self._evict_dev.numel() if self._evict_dev is not None else 0))
-            self._evict_dev = torch.empty((size,), dtype=torch.uint8, device=device)
-            self._evict_host = torch.empty((size,), dtype=torch.uint8, pin_memory=True)
-        return self._evict_dev, self._evict_host
+        device = torch.device(device)
+        for st in self._evict_stages:
+            if st.dev.device == device and st.dev.numel() >= nbytes and st.done():
+                self._evict_stages.remove(st)
+                self._evict_stages.append(st)
+                return st
+        if len(self._evict_stages) < self.MAX_EVICT_STAGES:
+            st = _EvictStage(*self._stage_blocks(device, nbytes))
+        else:
+            st = self._evict_stages.pop(0)
+            st.done(wait=True)
+            if st.dev.device != device or st.dev.numel() < nbytes:
+                st.dev, st.host = self._stage_blocks(device, max(nbytes, 2 * st.dev.numel()))
+        self._evict_stages.append(st)
+        return st
+
+    def _stage_blocks(self, device, nbytes):
+        """A device block and a pinned host block of nbytes each."""
+        return (torch.empty((nbytes,), dtype=torch.uint8, device=device),
+                torch.empty((nbytes,), dtype=torch.uint8, pin_memory=True))
+
+    def evict_staging(self, device, B, H, te, D):
+        """(device, pinned host) blocks of a free staging stage (evict_stage)."""
+        st = self.evict_stage(device, B, H, te, D)
+        return st.dev, st.host
+
+    def wait_cold_adds(self):
+        """Wait for every cold-store add still running (raises a failed one's error)."""
+        for st in self._evict_stages:
+            st.done(wait=True)
 
     @property
     def cpu_kpre_ring(self):
@@ -467,7 +538,11 @@ class KVController:
         return self._normalize(self._pad_or_crop(qn))
 
     # -- cold store -------------------------------------------------------------------------
-    def add_evicted_to_cold_store(self, layer_idx, ev: EvictedKV):
+    def add_evicted_to_cold_store(self, layer_idx, ev: EvictedKV, stage=None):
+        """Add one eviction's tokens to the layer's cold stores
+        (controller.py:178-188).  With stage (the _EvictStage whose host block
+        ev's tensors view) the adds run as native jobs and the stage stays
+        busy until they are done; without, they complete before returning."""
         if not self._inited:
             raise RuntimeError("KVController not initialized")
         li = int(layer_idx)
@@ -483,7 +558,12 @@ class KVController:
             kept = int((idx[b] >= 0).sum())
             if kept == 0:
                 continue
-            self.rings[li][b].add(kpre[b], vv[b], pos[b], idx[b])
+            if stage is None:
+                self.rings[li][b].add(kpre[b], vv[b], pos[b], idx[b])
+            else:
+                stage.jobs.append(self.rings[li][b].add_async(kpre[b], vv[b], pos[b], idx[b],
+                                                              nthreads=self.ADD_THREADS,
+                                                              workers=self._search_workers()))
             self.dbg["faiss_add"] += min(kept, self.cpu_buffer_size)
             if self.enable_asserts:
                 assert len(self.rings[li][b]) <= self.cpu_buffer_size

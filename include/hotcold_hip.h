@@ -509,14 +509,29 @@ int hc_memcpy_d2h_async(void* dst, const void* src, int64_t bytes, void* stream)
  */
 void* hc_cold_create(int64_t capacity, int64_t heads, int64_t head_dim, int64_t vec_dim, int64_t vec_heads,
                      int normalize);
-/* Frees a store, first waiting for any submitted search job that reads it. */
+/* Frees a store, first waiting for any submitted job (search or add) that
+ * uses it. */
 void hc_cold_destroy(void* store);
+/* Tokens held, after every add submitted to the store so far. */
 int64_t hc_cold_size(const void* store);
 /* Tokens t < te with evicted_idx[t] >= 0 (evicted_idx may be NULL: all), from
  * kpre/v [heads][te][head_dim] with element strides (k_sh, k_st), (v_sh, v_st)
  * and pos[te] -- one batch row of EvictedKV (datatypes.py:58-63). */
 int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
                 const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos, const int64_t* evicted_idx);
+/* hc_cold_add as a job on the library's worker threads (the reference adds
+ * the evicted tokens to its index inline, controller.py:178-188): the
+ * prefill's eviction returns while the store is filled.  Adds to one store are
+ * applied in submission order; a synchronous call on the store (add, size,
+ * search, export, retrieve) first waits for the adds submitted before it, and
+ * a search job waits for the adds submitted before the search was.  The
+ * worker first synchronises on wait_event (may be NULL).  nthreads <= 0 picks
+ * min(cores, 16) for the copy.  The caller keeps kpre, v, pos and evicted_idx
+ * alive until the job is done (hc_cold_job_poll / hc_cold_job_free, as for a
+ * search job).  Returns the job, or NULL on a bad argument (hc_last_error). */
+void* hc_cold_add_async(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
+                        const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos, const int64_t* evicted_idx,
+                        void* wait_event, int64_t nthreads, int64_t workers);
 /* Top-r logical indices for query q [vec_dim] against search vector `head`;
  * *n_out = min(r, size). */
 int hc_cold_search(const void* store, const float* q, int64_t r, int64_t head, int64_t* out, int64_t* n_out);
@@ -554,8 +569,9 @@ void* hc_cold_retrieve_async(void* const* stores, int64_t B, const float* q, int
                              int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t nthreads,
                              void* wait_event, int64_t workers);
 /* 0 while the job runs (wait = 0); 1 when it is done, with the number of
- * valid rows and of positions past the table; a negative HC_ERR_* code if
- * the retrieval failed (its message in hc_last_error on the calling thread).
+ * valid rows and of positions past the table (0 for an add); a negative
+ * HC_ERR_* code if the job failed (its message in hc_last_error on the
+ * calling thread).
  * wait != 0 blocks until the job is done. */
 int hc_cold_job_poll(void* job, int wait, int64_t* n_valid, int64_t* tab_missing);
 /* Frees a job, first waiting for it if a worker still runs it. */

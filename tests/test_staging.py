@@ -66,6 +66,9 @@ class HostCtrl(KVController):
         slot.released = True
         self.log.append(("released", id(slot)))
 
+    def _stage_blocks(self, device, nbytes):
+        return torch.empty((nbytes,), dtype=torch.uint8), torch.empty((nbytes,), dtype=torch.uint8)
+
 
 def _ctrl(**kw):
     args = dict(cpu_buffer_size=64, faiss_dim=D, lookahead_k=4, window_size=4, hold_retrieved=True)
@@ -437,3 +440,130 @@ def test_destroying_a_store_waits_for_its_search():
     handle, ring.handle = ring.handle, None
     N.lib().hc_cold_destroy(handle)                 # returns once the search no longer reads the store
     assert job.poll(wait=True) and job.error is None and job.result[0] == 4
+
+
+# ---------------------------------------------------------------------------
+# Cold-store adds as native jobs (the prefill's eviction returns while the
+# store is filled)
+# ---------------------------------------------------------------------------
+def _tokens(rng, te, i):
+    import numpy as np
+    kpre = rng.standard_normal((HK, te, D), dtype=np.float32)
+    v = rng.standard_normal((HK, te, D), dtype=np.float32)
+    pos = np.arange(1000 * i, 1000 * i + te, dtype=np.int64)
+    idx = np.arange(te, dtype=np.int64)
+    idx[::5] = -1                                   # padding rows are skipped
+    return kpre, v, pos, idx
+
+
+@pytest.mark.parametrize("vec_heads", [1, HK])
+def test_async_adds_equal_synchronous_adds(vec_heads):
+    """Adds submitted as jobs apply in submission order, over a ring that
+    wraps several times: size, searches and the store's contents equal those
+    of synchronous adds, bit for bit.  Size and search, called right after the
+    submissions, wait for the adds submitted before them."""
+    import numpy as np
+    from hotcold_kv.controller import _Ring
+    a, b = _Ring(40, HK, D, D, vec_heads), _Ring(40, HK, D, D, vec_heads)
+    rng = np.random.default_rng(3)
+    jobs = []
+    for i in range(7):
+        kpre, v, pos, idx = _tokens(rng, 17 + 3 * i, i)
+        a.add(kpre, v, pos, idx)
+        jobs.append(b.add_async(kpre, v, pos, idx, nthreads=2, workers=4))
+    assert len(b) == len(a) == 40
+    q = rng.standard_normal(D).astype(np.float32)
+    for h in range(vec_heads):
+        assert np.array_equal(a.search(q, 9, head=h), b.search(q, 9, head=h))
+    for j in jobs:
+        assert j.poll(wait=True) and j.error is None
+    ea, eb = a.export(), b.export()
+    for k in ("kpre", "v", "pos", "vec"):
+        assert np.array_equal(ea[k], eb[k]), k
+
+
+def test_a_search_job_waits_for_the_adds_submitted_before_it():
+    """A search job submitted right after async adds sees them: its result
+    equals the synchronous retrieval over the synchronously filled store."""
+    import numpy as np
+    L = 2
+    ctrls = []
+    for mode in ("sync", "async"):
+        ctrl = HostCtrl(cpu_buffer_size=64, faiss_dim=D, lookahead_k=4, window_size=1, hold_retrieved=True,
+                        per_head_retrieval=True)
+        ctrl._lazy_init(torch.zeros(1, HK, 1, D), n_layers=L)
+        ctrl._stream = "side"
+        g = torch.Generator().manual_seed(8)
+        for li in range(L):
+            keys = torch.randn(50, HK, D, generator=g)
+            ev = EvictedKV(k_pre_cpu=keys.permute(1, 0, 2).unsqueeze(0).contiguous(),
+                           v_cpu=(3 * keys).permute(1, 0, 2).unsqueeze(0).contiguous(),
+                           pos_cpu=torch.arange(100 * li, 100 * li + 50, dtype=torch.long).unsqueeze(0),
+                           evicted_idx=torch.arange(50, dtype=torch.long).unsqueeze(0))
+            if mode == "sync":
+                ctrl.add_evicted_to_cold_store(li, ev)
+            else:
+                st = ctrl.evict_stage("cpu", 1, HK, 50, D)
+                ctrl.add_evicted_to_cold_store(li, ev, stage=st)
+                assert ctrl.dbg["faiss_add"] == 50 * (li + 1)
+        qs = [torch.randn(1, 4, 1, D, generator=g) for _ in range(L)]
+        for li in range(L):
+            ctrl.update_query_window(li, qs[li])
+            ctrl.maybe_launch_async_retrieval(li)
+        got = []
+        for li in range(L):
+            ctrl.wait_for_retrieval(li)
+            sl = ctrl._retrieval_ready_cpu[li]
+            got.append([t.clone() for t in sl.host])
+        ctrl.wait_cold_adds()
+        ctrls.append(got)
+    for li in range(L):
+        for x, y in zip(ctrls[0][li], ctrls[1][li]):
+            assert torch.equal(x, y), li
+
+
+def test_eviction_stages_are_reused_only_after_their_adds():
+    """Two staging stages: a third eviction reuses the least recently handed
+    out one after its adds are done, never one an add still reads."""
+    ctrl = _ctrl()
+
+    class _Pending:                 # a job that finishes after `polls` polls
+        def __init__(self, polls):
+            self.polls, self.error, self.waited = polls, None, False
+
+        def poll(self, wait=False):
+            if wait:
+                self.waited, self.polls = True, 0
+            if self.polls > 0:
+                self.polls -= 1
+                return False
+            return True
+
+    j1, j2 = _Pending(10 ** 9), _Pending(10 ** 9)
+    s1 = ctrl.evict_stage("cpu", 1, HK, 8, D)
+    assert ctrl.evict_stage("cpu", 1, HK, 8, D) is s1  # free: handed out again
+    s1.jobs.append(j1)
+    s2 = ctrl.evict_stage("cpu", 1, HK, 8, D)       # s1 busy: a second stage
+    assert s2 is not s1
+    s2.jobs.append(j2)
+    s3 = ctrl.evict_stage("cpu", 1, HK, 8, D)       # both busy: the oldest, after waiting for it
+    assert s3 is s1 and j1.waited and not j2.waited and not s3.jobs
+    s2.jobs.clear()
+    assert ctrl.evict_stage("cpu", 1, HK, 8, D) is s2  # free: reused without waiting
+    big = ctrl.evict_stage("cpu", 1, HK, 4000, D)    # larger: the oldest, grown
+    assert big.host.numel() >= ops.N.lib().hc_gather_evict_bytes(1, HK, 4000, D)
+
+
+def test_destroying_a_store_waits_for_its_adds():
+    """A store freed while adds run on the worker threads is freed only after
+    them (they read the caller's buffers and write the store)."""
+    import numpy as np
+    from hotcold_kv import _native as N
+    from hotcold_kv.controller import _Ring
+    r = _Ring(20000, HK, D, D, HK)
+    rng = np.random.default_rng(4)
+    jobs = [r.add_async(*_tokens(rng, 6000, i), nthreads=1, workers=2) for i in range(3)]
+    handle, r.handle = r.handle, None
+    N.lib().hc_cold_destroy(handle)
+    for j in jobs:
+        assert j.poll(wait=True) and j.error is None
