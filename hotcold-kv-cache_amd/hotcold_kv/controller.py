@@ -244,9 +244,12 @@ class KVController:
     # Scheduled searches run as jobs on the library's native worker threads
     # (no Python, no thread per search), each on SEARCH_THREADS host threads:
     # every layer searches in the same decode step, and together they keep to
-    # about half of the cores, so the decode thread is not starved of CPU.
+    # about half of the cores (at most 12 threads, within a 16-core share), so
+    # the decode thread is not starved of CPU.  With 4 workers a 32-layer 16k
+    # loop at 0.6 ms per step skipped 1-8 of 256 searches whose predecessor
+    # was still running; with 6, 0-3.
     SEARCH_THREADS = 2
-    MAX_SEARCH_WORKERS = 4
+    MAX_SEARCH_WORKERS = 6
 
     def __init__(
         self,
