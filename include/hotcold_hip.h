@@ -577,6 +577,39 @@ int hc_cold_job_poll(void* job, int wait, int64_t* n_valid, int64_t* tab_missing
 /* Frees a job, first waiting for it if a worker still runs it. */
 void hc_cold_job_free(void* job);
 
+/*
+ * Device search index of the cold stores of one layer: the search vectors of
+ * B stores kept in HBM as vec [B][VH][VD][capT] fp32 (capT >= the stores'
+ * capacity), with the same arithmetic as hc_cold_add / hc_cold_search, so the
+ * hits are the host store's, bit for bit.  It replaces the reference's CPU
+ * faiss.IndexFlatIP scan (controller.py:223-232, 274-293) where a host scan
+ * cannot keep up (a layer of 16 rows x 8 heads x 30 720 tokens is 2 GB of
+ * vectors).  The key/value rows stay in the host store.
+ *
+ * hc_index_add: the vectors of tokens t < te of kpre (fp32 on the device; row
+ * b, head h, token t at kpre[b*k_sb + h*k_sh + t*k_st], head_dim D elements)
+ * into the physical slots slot_of[b][t] (int32 on the device; < 0: not
+ * stored), as hc_cold_add would place them: the head mean (VH = 1) or each
+ * head (VH = H), cropped or zero-padded to VD, normalised when normalize.
+ */
+int hc_index_add(int64_t B, int64_t H, int64_t D, int64_t VH, int64_t VD, int normalize,
+                 const float* kpre, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t te,
+                 const int32_t* slot_of, float* vec, int64_t capT, void* stream);
+/*
+ * hc_index_search: for every row b < B (B <= 64) and head h < VH, the query
+ * q[b*q_sb + h*q_sh .. + q_dim) (fp32 on the device; cropped or zero-padded to
+ * VD <= 1024 and, with normalize_q, normalised as hc_cold_retrieve does) against
+ * the row's sizes[b] stored vectors (ring of capacity cap whose oldest token is
+ * in slot heads[b] once full; sizes and heads are host arrays).  Writes the
+ * top R <= 1024 logical indices (oldest token = 0) in rank order -- inner
+ * product descending, ties to the older token -- to hits [B][VH][R] (int64 on
+ * the device), -1 past min(R, size).  keys: device scratch of B*VH*capT
+ * uint64.
+ */
+int hc_index_search(int64_t B, int64_t VH, int64_t VD, int64_t cap, const float* q, int64_t q_sb, int64_t q_sh,
+                    int64_t q_dim, int normalize_q, const float* vec, int64_t capT, const int64_t* sizes,
+                    const int64_t* heads, int64_t R, uint64_t* keys, int64_t* hits, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

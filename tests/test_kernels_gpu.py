@@ -923,3 +923,60 @@ def test_retrieval_query_pooling(dtype, per_head):
     assert torch.equal(dev.cpu(), want)
     ref_mean = x.permute(1, 2, 0, 3).reshape(B, vh, nh * T, D).double().mean(dim=2)
     assert (host.double() - ref_mean).abs().max() < 1e-5
+
+
+# ---------------------------------------------------------------------------
+# Device search index of the cold stores
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("vec_heads,VD", [(1, 128), (4, 128), (4, 96), (1, 160)])
+def test_device_index_equals_the_host_store(vec_heads, VD):
+    """DeviceIndex (hc_index_add / hc_index_search) against the host stores
+    filled with the same tokens: the same search vectors slot for slot, and the
+    same top-R logical indices in the same order for random queries, planted
+    exact ties (duplicate tokens) included, over rings that wrap and rows in
+    different fill states."""
+    from hotcold_kv.controller import _Ring
+    from hotcold_kv.device_index import DeviceIndex
+    B, H, D, cap = 3, 4, 128, 300
+    rng = np.random.default_rng(12)
+    rings = [_Ring(cap, H, D, VD, vec_heads) for _ in range(B)]
+    dix = DeviceIndex(B, H, D, VD, vec_heads, cap, DEV)
+    for i, te in enumerate((120, 250, 90, 400)):
+        kpre = rng.standard_normal((B, H, te, D), dtype=np.float32)
+        kpre[:, :, 5] = kpre[:, :, 7]                      # exact ties: a token repeated
+        v = rng.standard_normal((B, H, te, D), dtype=np.float32)
+        pos = np.arange(1000 * i, 1000 * i + te, dtype=np.int64)
+        idx = np.tile(np.arange(te, dtype=np.int64), (B, 1))
+        idx[0, ::3] = -1                                   # padding rows of row 0
+        if i == 1:
+            idx[2, :] = -1                                 # row 2 skips this eviction
+        for b in range(B):
+            rings[b].add(kpre[b], v[b], pos, idx[b])
+        dix.add(torch.from_numpy(kpre).to(DEV), idx)
+    torch.cuda.synchronize()
+    for b in range(B):
+        assert len(rings[b]) == int(dix.size[b])
+        ex = rings[b].export()
+        slots = [dix.physical(b, l) for l in range(len(rings[b]))]
+        got = dix.vec[b][:, :, slots].permute(2, 0, 1).cpu().numpy()     # (n, VH, VD)
+        assert np.array_equal(got, ex["vec"]), b
+    R = 64
+    hits = torch.empty((B, vec_heads, R), dtype=torch.int64, device=DEV)
+    for trial in range(6):
+        q = rng.standard_normal((B, vec_heads, D), dtype=np.float32)
+        if trial == 0:
+            q[:, :] = ex["kpre"][5, :vec_heads] if vec_heads > 1 else ex["kpre"][5].mean(0)  # hits a tie
+        dix.search(torch.from_numpy(q).to(DEV), R, hits)
+        h_dev = hits.cpu().numpy()
+        for b in range(B):
+            for h in range(vec_heads):
+                qq = np.zeros(VD, np.float32)
+                qq[:min(D, VD)] = q[b, h, :min(D, VD)]
+                ss = 0.0
+                for x in qq.astype(np.float64):                   # squares summed in dimension order
+                    ss += x * x
+                nrm = max(math.sqrt(ss), 1e-12)
+                want = rings[b].search((qq.astype(np.float64) / nrm).astype(np.float32), R, head=h)
+                got = h_dev[b, h]
+                assert np.array_equal(got[:len(want)], want), (trial, b, h)
+                assert (got[len(want):] == -1).all()
