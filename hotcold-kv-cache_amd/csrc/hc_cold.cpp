@@ -399,6 +399,39 @@ extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t*
 
 namespace {
 
+// Copy the rows of hits[0..m) (logical indices of store s, rank order) into
+// output row (b, h) of a retrieval: kpre/v [B][H][R][D] (one head, or every
+// head with a head-mean vector), pos/valid [B][VH][R].  The caller holds the
+// store's read lock and has zero-filled the outputs.
+void emit_hits(const ColdStore* s, int64_t b, int64_t h, int per_head, int64_t R, const int64_t* hits, int64_t m,
+               float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out) {
+  const int64_t H = s->H, D = s->D, VH = per_head ? H : 1;
+  for (int64_t j = 0; j < m; ++j) {
+    const int64_t p = s->physical(hits[j]);
+    const float* kp = &s->kpre[(size_t)p * H * D];
+    const float* vp = &s->v[(size_t)p * H * D];
+    const int64_t h0 = per_head ? h : 0, h1 = per_head ? h + 1 : H;
+    for (int64_t hh = h0; hh < h1; ++hh) {
+      memcpy(kpre_out + ((b * H + hh) * R + j) * D, kp + hh * D, sizeof(float) * D);
+      memcpy(v_out + ((b * H + hh) * R + j) * D, vp + hh * D, sizeof(float) * D);
+    }
+    pos_out[(b * VH + h) * R + j] = s->pos[p];
+    valid_out[(b * VH + h) * R + j] = 1;
+  }
+}
+
+// Rows of the caller's table (one per position) at the retrieved positions of
+// output row (b, h); rows past the hits take position 0.
+void emit_tab(int64_t b, int64_t h, int64_t VH, int64_t R, const int64_t* pos_out, const uint8_t* tab,
+              int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, std::atomic<int64_t>& missing) {
+  for (int64_t j = 0; j < R; ++j) {
+    const int64_t p = pos_out[(b * VH + h) * R + j];
+    uint8_t* dst = tab_out + ((b * VH + h) * R + j) * tab_row_bytes;
+    if (p >= 0 && p < tab_rows) memcpy(dst, tab + p * tab_row_bytes, (size_t)tab_row_bytes);
+    else { memset(dst, 0, (size_t)tab_row_bytes); missing.fetch_add(1); }
+  }
+}
+
 // The search itself (every add the caller must see already applied).
 int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh, int64_t q_dim,
                   int normalize_q, int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
@@ -451,36 +484,71 @@ int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, 
         std::vector<double> ip((size_t)s->size);
         s->scan(qv.data(), h, 0, s->size, ip.data());
         m = s->select(ip.data(), R, hits.data());
-        for (int64_t j = 0; j < m; ++j) {
-          const int64_t p = s->physical(hits[j]);
-          const float* kp = &s->kpre[(size_t)p * H * D];
-          const float* vp = &s->v[(size_t)p * H * D];
-          const int64_t h0 = per_head ? h : 0, h1 = per_head ? h + 1 : H;
-          for (int64_t hh = h0; hh < h1; ++hh) {
-            memcpy(kpre_out + ((b * H + hh) * R + j) * D, kp + hh * D, sizeof(float) * D);
-            memcpy(v_out + ((b * H + hh) * R + j) * D, vp + hh * D, sizeof(float) * D);
-          }
-          pos_out[(b * VH + h) * R + j] = s->pos[p];
-          valid_out[(b * VH + h) * R + j] = 1;
-        }
+        emit_hits(s, b, h, per_head, R, hits.data(), m, kpre_out, v_out, pos_out, valid_out);
       }
     }
-    if (tab) {
-      // rows of the caller's table (one per position) at the retrieved
-      // positions; rows past the hits take position 0
-      for (int64_t j = 0; j < R; ++j) {
-        const int64_t p = pos_out[(b * VH + h) * R + j];
-        uint8_t* dst = tab_out + ((b * VH + h) * R + j) * tab_row_bytes;
-        if (p >= 0 && p < tab_rows) memcpy(dst, tab + p * tab_row_bytes, (size_t)tab_row_bytes);
-        else { memset(dst, 0, (size_t)tab_row_bytes); missing.fetch_add(1); }
-      }
-    }
+    if (tab) emit_tab(b, h, VH, R, pos_out, tab, tab_rows, tab_row_bytes, tab_out, missing);
   });
   if (tab_missing) *tab_missing = missing.load();
   return HC_OK;
 }
 
+// The rows of hits found elsewhere (the device search index): hits [B][VH][R]
+// logical indices in rank order, -1 past the hits.
+int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits, float* kpre_out,
+                float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows,
+                int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads) {
+  if (B <= 0 || R <= 0 || !stores || !hits || !kpre_out || !v_out || !pos_out || !valid_out)
+    return set_error(HC_ERR_INVALID, "cold_gather: bad arguments");
+  if (tab && (tab_rows <= 0 || tab_row_bytes <= 0 || !tab_out))
+    return set_error(HC_ERR_INVALID, "cold_gather: table rows need a size and an output");
+  const ColdStore* s0 = reinterpret_cast<const ColdStore*>(stores[0]);
+  if (!s0) return set_error(HC_ERR_INVALID, "cold_gather: null store");
+  const int64_t H = s0->H, D = s0->D;
+  for (int64_t b = 0; b < B; ++b) {
+    const ColdStore* s = reinterpret_cast<const ColdStore*>(stores[b]);
+    if (!s || s->H != H || s->D != D)
+      return set_error(HC_ERR_INVALID, "cold_gather: store %lld does not match", (long long)b);
+  }
+  const int64_t VH = per_head ? H : 1;
+  memset(kpre_out, 0, sizeof(float) * B * H * R * D);
+  memset(v_out, 0, sizeof(float) * B * H * R * D);
+  memset(pos_out, 0, sizeof(int64_t) * B * VH * R);
+  memset(valid_out, 0, (size_t)(B * VH * R));
+  std::atomic<int64_t> missing{0};
+  std::atomic<int> bad{0};
+  const int64_t tasks = B * VH;
+  parallel_for(tasks, threads_for(nthreads, tasks), [&](int64_t task) {
+    const int64_t b = task / VH, h = task % VH;
+    const ColdStore* s = reinterpret_cast<const ColdStore*>(stores[b]);
+    const int64_t* hs = hits + (b * VH + h) * R;
+    {
+      std::shared_lock<std::shared_mutex> lk(s->mu);
+      int64_t m = 0;
+      while (m < R && hs[m] >= 0) ++m;
+      for (int64_t j = 0; j < m; ++j)
+        if (hs[j] >= s->size) bad.store(1);
+      if (!bad.load()) emit_hits(s, b, h, per_head, R, hs, m, kpre_out, v_out, pos_out, valid_out);
+    }
+    if (tab) emit_tab(b, h, VH, R, pos_out, tab, tab_rows, tab_row_bytes, tab_out, missing);
+  });
+  if (bad.load()) return set_error(HC_ERR_INVALID, "cold_gather: a hit beyond its store's tokens");
+  if (tab_missing) *tab_missing = missing.load();
+  return HC_OK;
+}
+
 }  // namespace
+
+extern "C" int hc_cold_gather(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits,
+                              float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                              int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing,
+                              int64_t nthreads) {
+  if (B > 0 && stores)
+    for (int64_t b = 0; b < B; ++b)
+      if (stores[b]) as_store(stores[b])->wait_all_adds();
+  return gather_impl(stores, B, per_head, R, hits, kpre_out, v_out, pos_out, valid_out, tab, tab_rows, tab_row_bytes,
+                     tab_out, tab_missing, nthreads);
+}
 
 extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
                                 int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
@@ -505,6 +573,7 @@ namespace {
 
 struct RetrieveJob {
   bool is_add = false;           // an asynchronous add instead of a search
+  const int64_t* hits = nullptr; // a gather of these hits instead of a search
   std::vector<void*> stores;
   std::vector<int64_t> tickets;  // per store: the adds submitted before this search
   // add arguments (is_add)
@@ -574,7 +643,10 @@ class JobQueue {
       s->serve_ticket();
     } else {
       for (size_t b = 0; b < j->stores.size(); ++b) as_store(j->stores[b])->wait_adds(j->tickets[b]);
-      if (rc == HC_OK)
+      if (rc == HC_OK && j->hits)
+        rc = gather_impl(j->stores.data(), j->B, j->per_head, j->R, j->hits, j->kpre_out, j->v_out, j->pos_out,
+                         j->valid_out, j->tab, j->tab_rows, j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
+      else if (rc == HC_OK)
         rc = retrieve_impl(j->stores.data(), j->B, j->q, j->q_sb, j->q_sh, j->q_dim, j->normalize_q, j->R,
                            j->per_head, j->kpre_out, j->v_out, j->pos_out, j->valid_out, j->tab, j->tab_rows,
                            j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
@@ -631,6 +703,43 @@ extern "C" void* hc_cold_retrieve_async(void* const* stores, int64_t B, const fl
   j->stores.assign(stores, stores + B);
   j->B = B; j->q = q; j->q_sb = q_sb; j->q_sh = q_sh; j->q_dim = q_dim; j->normalize_q = normalize_q;
   j->R = R; j->per_head = per_head; j->kpre_out = kpre_out; j->v_out = v_out; j->pos_out = pos_out;
+  j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows; j->tab_row_bytes = tab_row_bytes;
+  j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
+  j->n_flags = B * R * (per_head ? s0->H : 1);
+  for (int64_t b = 0; b < B; ++b) {
+    as_store(stores[b])->pin();
+    j->tickets.push_back(as_store(stores[b])->tickets());
+  }
+  job_queue().push(j, workers);
+  return j;
+}
+
+extern "C" void* hc_cold_gather_async(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits,
+                                      float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out,
+                                      const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
+                                      int64_t nthreads, void* wait_event, int64_t workers) {
+  if (B <= 0 || R <= 0 || !stores || !hits || !kpre_out || !v_out || !pos_out || !valid_out) {
+    set_error(HC_ERR_INVALID, "cold_gather_async: bad arguments");
+    return nullptr;
+  }
+  if (tab && (tab_rows <= 0 || tab_row_bytes <= 0 || !tab_out)) {
+    set_error(HC_ERR_INVALID, "cold_gather_async: table rows need a size and an output");
+    return nullptr;
+  }
+  for (int64_t b = 0; b < B; ++b)
+    if (!stores[b]) {
+      set_error(HC_ERR_INVALID, "cold_gather_async: null store %lld", (long long)b);
+      return nullptr;
+    }
+  RetrieveJob* j = new (std::nothrow) RetrieveJob();
+  if (!j) {
+    set_error(HC_ERR_INVALID, "cold_gather_async: out of host memory");
+    return nullptr;
+  }
+  const ColdStore* s0 = as_store(stores[0]);
+  j->stores.assign(stores, stores + B);
+  j->hits = hits;
+  j->B = B; j->R = R; j->per_head = per_head; j->kpre_out = kpre_out; j->v_out = v_out; j->pos_out = pos_out;
   j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows; j->tab_row_bytes = tab_row_bytes;
   j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
   j->n_flags = B * R * (per_head ? s0->H : 1);

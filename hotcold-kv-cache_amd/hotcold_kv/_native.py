@@ -207,6 +207,9 @@ SIGNATURES = {
     "hc_cold_retrieve_async": (_vp, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _i64, _int, _vp, _vp, _vp, _vp,
                                      _vp, _i64, _i64, _vp, _i64, _vp, _i64]),
     "hc_cold_add_async": (_vp, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64]),
+    "hc_cold_gather": (_int, [_vp, _i64, _int, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64]),
+    "hc_cold_gather_async": (_vp, [_vp, _i64, _int, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp,
+                                   _i64]),
     "hc_cold_job_poll": (_int, [_vp, _int, _vp, _vp]),
     "hc_cold_job_free": (None, [_vp]),
     "hc_index_add": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),

@@ -568,6 +568,22 @@ void* hc_cold_retrieve_async(void* const* stores, int64_t B, const float* q, int
                              float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
                              int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t nthreads,
                              void* wait_event, int64_t workers);
+/* The rows of hits found by the device search index (hc_index_search): hits
+ * [B][VH][R] (host) holds logical indices of each row's store in rank order,
+ * -1 past the hits.  Writes the outputs as hc_cold_retrieve does for the same
+ * hits (kpre/v, pos/valid, table rows), after the adds submitted before it.
+ * A hit beyond its store's tokens is HC_ERR_INVALID. */
+int hc_cold_gather(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits, float* kpre_out,
+                   float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows,
+                   int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads);
+/* hc_cold_gather as a job on the worker threads: the worker first
+ * synchronises on wait_event (the event behind the hits' device-to-host copy)
+ * and waits for the adds submitted before the job.  Polled and freed like a
+ * search job. */
+void* hc_cold_gather_async(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits,
+                           float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                           int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t nthreads,
+                           void* wait_event, int64_t workers);
 /* 0 while the job runs (wait = 0); 1 when it is done, with the number of
  * valid rows and of positions past the table (0 for an add); a negative
  * HC_ERR_* code if the job failed (its message in hc_last_error on the

@@ -567,3 +567,69 @@ def test_destroying_a_store_waits_for_its_adds():
     N.lib().hc_cold_destroy(handle)
     for j in jobs:
         assert j.poll(wait=True) and j.error is None
+
+
+@pytest.mark.parametrize("per_head", [False, True])
+def test_gathering_given_hits_equals_the_native_retrieval(per_head):
+    """hc_cold_gather (the rows of hits found by the device search index)
+    writes what hc_cold_retrieve writes when given the hits its own search
+    finds: keys, values, positions, valid flags and rotary-table rows, with
+    short rows (fewer tokens than R) padded the same way; and a search job
+    queued behind async adds sees them (hc_cold_gather_async)."""
+    import ctypes
+    import numpy as np
+    from hotcold_kv import _native as N
+    from hotcold_kv.controller import _Ring
+    lib = N.lib()
+    B, H, Dd, R, cap = 3, HK, D, 8, 50
+    VH = H if per_head else 1
+    rng = np.random.default_rng(21)
+    rings = [_Ring(cap, H, Dd, Dd, VH) for _ in range(B)]
+    for b, n in enumerate((70, 5, 30)):                       # wrapped, short, partial
+        kp = rng.standard_normal((H, n, Dd), dtype=np.float32)
+        rings[b].add(kp, rng.standard_normal((H, n, Dd), dtype=np.float32), np.arange(7 * b, 7 * b + n) * 3)
+    stores = (ctypes.c_void_p * B)(*[r.handle for r in rings])
+    q = rng.standard_normal((B, VH, Dd), dtype=np.float32)
+    tab = rng.integers(0, 255, size=(400, 12), dtype=np.uint8)
+
+    def outputs():
+        return (np.zeros((B, H, R, Dd), np.float32), np.zeros((B, H, R, Dd), np.float32),
+                np.zeros((B, VH, R), np.int64), np.zeros((B, VH, R), np.uint8), np.zeros((B, VH, R, 12), np.uint8))
+
+    want, got = outputs(), outputs()
+    miss_w, miss_g = ctypes.c_int64(), ctypes.c_int64()
+    N.check(lib.hc_cold_retrieve(stores, B, q.ctypes.data, VH * Dd, Dd, Dd, 1, R, int(per_head),
+                                 *[x.ctypes.data for x in want[:4]], tab.ctypes.data, 400, 12, want[4].ctypes.data,
+                                 ctypes.byref(miss_w), 2), "hc_cold_retrieve")
+    hits = np.full((B, VH, R), -1, np.int64)
+    for b in range(B):
+        for h in range(VH):
+            x = q[b, h].astype(np.float64)
+            ss = 0.0
+            for e in x:
+                ss += e * e
+            found = rings[b].search((x / max(ss ** 0.5, 1e-12)).astype(np.float32), R, head=h)
+            hits[b, h, :len(found)] = found
+    N.check(lib.hc_cold_gather(stores, B, int(per_head), R, hits.ctypes.data, *[x.ctypes.data for x in got[:4]],
+                               tab.ctypes.data, 400, 12, got[4].ctypes.data, ctypes.byref(miss_g), 2), "hc_cold_gather")
+    for a, b_ in zip(want, got):
+        assert np.array_equal(a, b_)
+    assert miss_w.value == miss_g.value
+    # a hit beyond a store's tokens is refused
+    bad = hits.copy()
+    bad[1, 0, 0] = 40
+    assert lib.hc_cold_gather(stores, B, int(per_head), R, bad.ctypes.data, *[x.ctypes.data for x in got[:4]],
+                              None, 0, 0, None, None, 1) == N.HC_ERR_INVALID
+    # the job form after async adds: it waits for them
+    more = rng.standard_normal((H, 20, Dd), dtype=np.float32)
+    adds = [rings[1].add_async(more, more, np.arange(20), nthreads=1, workers=2)]
+    hits2 = hits.copy()
+    hits2[1, :, :] = np.arange(R)                             # store 1 now holds 25 tokens
+    job = lib.hc_cold_gather_async(stores, B, int(per_head), R, hits2.ctypes.data, *[x.ctypes.data for x in got[:4]],
+                                   None, 0, 0, None, 1, None, 2)
+    nv = ctypes.c_int64()
+    assert lib.hc_cold_job_poll(job, 1, ctypes.byref(nv), None) == 1
+    lib.hc_cold_job_free(job)
+    assert got[3][1].all() and nv.value == int((hits2 >= 0).sum()) * 1
+    for j in adds:
+        assert j.poll(wait=True) and j.error is None
