@@ -704,7 +704,7 @@ class _Rotary:
         self.attention_scaling = 1.0
 
 
-def hotcold_pipeline(w, dev, profile_steps=None):
+def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
     """The hot/cold engine's own loop at a held-slot workload, through
     hotcold_attention (the patched attention's body between RoPE and o_proj):
       prefill  every layer's prompt appended to its HotColdLayer and
@@ -712,7 +712,10 @@ def hotcold_pipeline(w, dev, profile_steps=None):
                the recent queries, KV-head mean, top-k + recent window); the
                evicted prompt tokens go to the native cold store;
       decode   w.decode_steps steps over all layers: per-KV-head retrieval of
-               w.held tokens every w.retrieve_every steps on a host thread,
+               w.held tokens every w.retrieve_every steps (ranked on the
+               layer's device index, rows gathered from the host store on the
+               library's worker threads; device_search=False: searched on the
+               host store),
                the pinned copy on the side stream, re-RoPE inject into the
                held slot, and the fused append + held decode.
     Knobs: max_capacity_prompt = budget + decode steps and topk_ratio giving
@@ -731,7 +734,7 @@ def hotcold_pipeline(w, dev, profile_steps=None):
     ctrl = KVController(max_capacity_prompt=cap, topk_ratio=(topk + 0.5) / cap, recent_size=w.window,
                         cpu_buffer_size=w.seq_len, faiss_dim=w.head_dim, window_size=w.retrieve_every,
                         query_pool_size=4, lookahead_k=w.held, hold_retrieved=True, per_head_retrieval=True,
-                        profile_overlap=True, enable_asserts=False)
+                        profile_overlap=True, enable_asserts=False, device_search=device_search)
     rot = _Rotary(w, dev)
     hp.set_active_rotary_emb(rot)
     ctrl.set_rope(rot.inv_freq, rot.attention_scaling)     # as the patched prefill does before its update
@@ -786,6 +789,7 @@ def hotcold_pipeline(w, dev, profile_steps=None):
         "step_us_wall_without_retrieval_median": round(statistics.median(other) * 1e3, 1) if other else None,
         "layer_us_wall_mean": round(total_ms * 1e3 / steps / L, 2),
         "retrievals": d["retrieval_launched"],
+        "retrievals_on_device_index": d["retrieval_device"],
         "retrievals_scheduled": L * (steps // w.retrieve_every),
         "retrievals_skipped_search_running": L * (steps // w.retrieve_every) - d["retrieval_launched"]
         - d["retrieval_skipped_no_slot"] - d["retrieval_skipped_no_cold"],

@@ -38,6 +38,7 @@ import torch
 
 from . import _native as N
 from .datatypes import EvictedKV, RetrievedKV, _canon_br_2d, _canon_kv_4d
+from .device_index import DeviceIndex
 from .ops import rope_tables as ops_rope_tables
 from .ops import stream_handle as ops_stream
 
@@ -150,7 +151,7 @@ class _Slot:
 
     FREE, FILLING, RETRIEVED, COPYING, STAGED, HELD = range(6)
 
-    def __init__(self, host, tab=None, block=None, nbytes=(0, 0), qhost=None):
+    def __init__(self, host, tab=None, block=None, nbytes=(0, 0), qhost=None, hits_host=None):
         self.host = host            # (kpre, v, pos, valid) pinned host tensors
         self.tab = tab              # pinned rotary tables at pos, (B,Hc,R,2,D/2) cache dtype: [..., 0, :] cos, 1 sin
         self.tab_host = None if tab is None else (tab[..., 0, :], tab[..., 1, :])
@@ -161,6 +162,9 @@ class _Slot:
         self.qhost = qhost          # pinned pooled query of the search it serves, (B,VH,D) fp32
         self.qdev = None            # its device twin, written by the pooling kernel
         self.q_ready = None         # event behind the query's copy
+        self.hits_host = hits_host  # pinned hits of a device search, (B,VH,R) int64 logical indices
+        self.hits_dev = None        # their device twin, written by the search kernel
+        self.hits_ready = None      # event behind the hits' device-to-host copy
         self.dev = None             # device twins, allocated on the first copy
         self.dev_block = None       # the device allocation they are views of
         self.state = _Slot.FREE
@@ -268,6 +272,7 @@ class KVController:
         profile_overlap: bool = True,
         force_wait_for_prefetch_diagnostic: bool = False,
         per_head_retrieval: bool = False,
+        device_search: bool = True,
     ):
         self.max_capacity_prompt = int(max_capacity_prompt)
         self.topk_ratio = float(topk_ratio)
@@ -288,6 +293,12 @@ class KVController:
         self.profile_overlap = bool(profile_overlap)
         self.force_wait_for_prefetch_diagnostic = bool(force_wait_for_prefetch_diagnostic)
         self.per_head_retrieval = bool(per_head_retrieval)
+        # True: with the hot tier on a GPU, each layer's search vectors are
+        # also kept in HBM (DeviceIndex) and the scheduled searches rank them
+        # there; the host stores then only gather the hits' rows.  A layer
+        # whose index cannot follow its store (an add without a staging stage)
+        # goes back to the host search.
+        self.device_search = bool(device_search)
 
         self._inited = False
         self.B = self.Hk = self.D = self.n_layers = None
@@ -308,6 +319,9 @@ class KVController:
         self._held_slot = []
         self._stream = None
         self._evict_stages = []
+        self._dindex = []           # per layer: DeviceIndex, or None (host search)
+        self._search_stream = None  # side stream of the device searches
+        self._search_done = []      # per layer: event behind its last device search
         self.last_injected_len = 0
         self.held_mem = []
 
@@ -317,6 +331,8 @@ class KVController:
             "faiss_add": 0,
             "retrieval_launched": 0,
             "retrieval_launched_prefill": 0,
+            "retrieval_device": 0,
+            "device_index_dropped": 0,
             "retrieval_ready_cpu": 0,
             "retrieval_skipped_no_cold": 0,
             "retrieval_ready_empty": 0,
@@ -360,13 +376,41 @@ class KVController:
         self._slots = [[] for _ in range(L)]
         self._held_slot = [None] * L
         self.held_mem = [None] * L
+        self._dindex = [None] * L
+        self._search_done = [None] * L
         if k_pre.is_cuda:
             stream = ctypes.c_void_p()
             N.check(N.lib().hc_stream_create(ctypes.byref(stream)), "hc_stream_create")
             self._stream = stream.value
+            if self.device_search and self.lookahead_k > 0:
+                self._create_device_indexes()
         self._inited = True
         if k_pre.is_cuda:
             self._preallocate_slots()
+
+    def _create_device_indexes(self):
+        """One DeviceIndex per layer (vectors of every row's store, capacity
+        cpu_buffer_size) and the search stream, or none at all when they do
+        not fit the device's memory or the search kernel's limits."""
+        vh = self.Hk if self.per_head_retrieval else 1
+        if self.B > 64 or self.faiss_dim > 1024 or self.lookahead_k > 1024:
+            return
+        try:
+            self._dindex = [DeviceIndex(self.B, self.Hk, self.D, self.faiss_dim, vh, self.cpu_buffer_size,
+                                        self._device, self.normalize_for_ip) for _ in range(self.n_layers)]
+        except torch.OutOfMemoryError:
+            self._dindex = [None] * self.n_layers
+            return
+        stream = ctypes.c_void_p()
+        N.check(N.lib().hc_stream_create(ctypes.byref(stream)), "hc_stream_create")
+        self._search_stream = stream.value
+
+    def _drop_device_index(self, li):
+        """The layer goes back to the host search (its store took an add the
+        device index did not see)."""
+        if self._dindex and self._dindex[li] is not None:
+            self._dindex[li] = None
+            self.dbg["device_index_dropped"] += 1
 
     def _preallocate_slots(self, n=2):
         """n staging slots per layer up front (one held, one in flight):
@@ -389,11 +433,12 @@ class KVController:
             lib = N.lib()
             for slots in self._slots:
                 for sl in slots:
-                    for ev in (sl.ready, sl.t0, sl.t1, sl.free_after):
+                    for ev in (sl.ready, sl.t0, sl.t1, sl.free_after, sl.q_ready, sl.hits_ready):
                         if ev is not None:
                             lib.hc_event_destroy(ev)
-            if self._stream is not None:
-                lib.hc_stream_destroy(self._stream)
+            for s in (self._stream, self._search_stream):
+                if s is not None:
+                    lib.hc_stream_destroy(s)
         except Exception:
             pass
 
@@ -557,6 +602,8 @@ class KVController:
             self._max_pos = max(self._max_pos, int(pos.max()))
             if self._rope is not None:
                 self._rope_rows()       # extend the rotary tables now (prefill), not in a decode step
+        if self._dindex and self._dindex[li] is not None:
+            self._index_add(li, ev, stage, idx)
         for b in range(kpre.shape[0]):
             kept = int((idx[b] >= 0).sum())
             if kept == 0:
@@ -570,6 +617,23 @@ class KVController:
             self.dbg["faiss_add"] += min(kept, self.cpu_buffer_size)
             if self.enable_asserts:
                 assert len(self.rings[li][b]) <= self.cpu_buffer_size
+
+    def _index_add(self, li, ev, stage, idx):
+        """The eviction's search vectors into the layer's device index, from
+        the stage's device block (the twin of the host block ev's tensors
+        view), on the current stream after the layer's last device search
+        (which may still read the ring slots this add overwrites).  Without
+        such a block the layer goes back to the host search."""
+        B, H, te, D = ev.k_pre_cpu.shape
+        if stage is None or stage.dev.device.type != "cuda" or ev.k_pre_cpu.data_ptr() != stage.host.data_ptr() \
+                or stage.dev.numel() < 4 * B * H * te * D:
+            self._drop_device_index(li)
+            return
+        kdev = stage.dev[:4 * B * H * te * D].view(torch.float32).view(B, H, te, D)
+        stream = ops_stream(kdev.device)
+        if self._search_done[li] is not None:
+            N.check(N.lib().hc_stream_wait_event(stream, self._search_done[li]), "hc_stream_wait_event")
+        self._dindex[li].add(kdev, idx, stream=stream)
 
     # -- query pooling / retrieval -----------------------------------------------------
     def update_query_window(self, layer_idx, q_pre):
@@ -611,8 +675,9 @@ class KVController:
                                                int(self.per_head_retrieval), slot.qdev.data_ptr(),
                                                slot.qhost.data_ptr(), slot.q_ready, stream), "hc_retrieval_query")
             return
-        qd = self._pooled_query_dev(layer_idx).reshape(B, vh, D)
-        slot.qhost.copy_(qd, non_blocking=True)
+        vh = self.Hk if self.per_head_retrieval else 1
+        slot.qdev.copy_(self._pooled_query_dev(layer_idx).reshape(B, vh, D))
+        slot.qhost.copy_(slot.qdev, non_blocking=True)
         N.check(N.lib().hc_event_record(slot.q_ready, stream), "hc_event_record")
 
     def _wait_event(self, ev):
@@ -626,17 +691,17 @@ class KVController:
 
     # -- staging slots ------------------------------------------------------------------
     def _slot_specs(self):
-        """(shape, dtype) of a slot's k_pre, v, pos, valid, rotary tables and
-        pooled query: the order of their views in the slot's one block.  A
-        retrieval copies a prefix of the block: through the flags without
-        tables, through the tables with them; the pooled query, last, only
-        travels device to host."""
+        """(shape, dtype) of a slot's k_pre, v, pos, valid, rotary tables,
+        pooled query and device-search hits: the order of their views in the
+        slot's one block.  A retrieval copies a prefix of the block: through
+        the flags without tables, through the tables with them; the pooled
+        query and the hits, last, only travel device to host."""
         B, Hk, D, R = self.B, self.Hk, self.D, self.lookahead_k
         vh = Hk if self.per_head_retrieval else 1
         pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
         tshape = (B, vh, R, 2, D // 2)
         return (((B, Hk, R, D), torch.float32), ((B, Hk, R, D), torch.float32), (pshape, torch.int64),
-                (pshape, torch.bool), (tshape, self.dtype), ((B, vh, D), torch.float32))
+                (pshape, torch.bool), (tshape, self.dtype), ((B, vh, D), torch.float32), ((B, vh, R), torch.int64))
 
     def _take_slot(self, li):
         """A free slot of layer li whose last copy has completed (its host
@@ -652,7 +717,7 @@ class KVController:
         ends = _block_layout(specs)[1]
         block = torch.empty(ends[-1], dtype=torch.uint8, pin_memory=torch.cuda.is_available())
         views = _carve(block, specs)
-        sl = _Slot(views[:4], views[4], block, (ends[3], ends[4]), views[5])
+        sl = _Slot(views[:4], views[4], block, (ends[3], ends[4]), views[5], views[6])
         if self._device is not None and self._device.type == "cuda":
             self._alloc_dev(sl, self._device)
         sl.state = _Slot.FILLING
@@ -771,7 +836,11 @@ class KVController:
             return
         if not self._inited:
             return
-        if self.cold_size(li) == 0:
+        dindex = self._dindex[li] if self._dindex and self.query_window[li] \
+            and self.query_window[li][0].is_cuda else None
+        # the device index knows its rows' sizes without waiting for the
+        # host stores' adds
+        if (dindex is not None and not dindex.size.any()) or (dindex is None and self.cold_size(li) == 0):
             self.dbg["retrieval_skipped_no_cold"] += 1
             return
         if len(self.query_window[li]) == 0:
@@ -789,6 +858,9 @@ class KVController:
             # pooled on the device; the search thread waits for the host
             # copy, the decode thread does not
             self._stage_query(li, slot)
+            if dindex is not None:
+                self._launch_device_search(li, slot, dindex)
+                return
             q_vecs, event = None, slot.q_ready
         else:
             q_vecs, event = self._pooled_query_np(li), None
@@ -801,6 +873,43 @@ class KVController:
         with self._retrieval_lock[li]:
             self._retrieval_thread[li] = _Job(handle, slot, tab, keep)
             self.dbg["retrieval_launched"] += 1
+
+    def _launch_device_search(self, li, slot, dindex):
+        """A scheduled search on the device index: on the search stream,
+        after the query's pooling, the ranking kernel writes the slot's hits
+        and they are copied to its pinned buffer; a native job then waits for
+        that copy (and for the adds submitted before it) and gathers the
+        hits' rows from the host stores into the slot, as the host search
+        would have (hc_cold_gather).  The decode thread waits for none of it."""
+        lib = N.lib()
+        ss = self._search_stream
+        if slot.hits_ready is None:
+            slot.hits_ready = self._event(0)
+        R = self.lookahead_k
+        try:
+            dindex.search(slot.qdev, R, slot.hits_dev, normalize_q=self.normalize_for_ip, stream=ss,
+                          hits_host=slot.hits_host, wait_event=slot.q_ready, done_event=slot.hits_ready)
+        except Exception:
+            with self._retrieval_lock[li]:
+                slot.state = _Slot.FREE
+            raise
+        self._search_done[li] = slot.hits_ready
+        table = self._rope_rows()
+        tab = table is not None and self._rope is not None
+        kpre, vv, pos, valid = slot.host
+        handle = lib.hc_cold_gather_async(
+            self._store_ptrs[li], self.B, int(self.per_head_retrieval), R, slot.hits_host.data_ptr(),
+            kpre.data_ptr(), vv.data_ptr(), pos.data_ptr(), valid.data_ptr(),
+            table.ctypes.data if tab else None, table.shape[0] if tab else 0, table.shape[1] if tab else 0,
+            slot.tab.data_ptr() if tab else None, self.SEARCH_THREADS, slot.hits_ready, self._search_workers())
+        if not handle:
+            with self._retrieval_lock[li]:
+                slot.state = _Slot.FREE
+            N.check(N.HC_ERR_INVALID, "hc_cold_gather_async")
+        with self._retrieval_lock[li]:
+            self._retrieval_thread[li] = _Job(handle, slot, tab, (slot.hits_host, table))
+            self.dbg["retrieval_launched"] += 1
+            self.dbg["retrieval_device"] += 1
 
     def _search_workers(self):
         """Native search threads: about half of this process's cores, at most
@@ -833,7 +942,7 @@ class KVController:
         slot.dev_block = torch.empty(slot.block.numel(), dtype=torch.uint8, device=device)
         views = _carve(slot.dev_block, self._slot_specs())
         slot.dev, slot.tab_dev = views[:4], (views[4][..., 0, :], views[4][..., 1, :])
-        slot.qdev = views[5]
+        slot.qdev, slot.hits_dev = views[5], views[6]
 
     def _copy_to_device(self, slot):
         """The slot's host-to-device copies on the side stream, after the

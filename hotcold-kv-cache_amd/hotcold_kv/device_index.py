@@ -26,7 +26,8 @@ from . import _native as N
 
 class DeviceIndex:
     """Search vectors of B cold stores (one layer), capacity cap each, in HBM:
-    vec [B][VH][VD][capT] fp32, VH = 1 (head mean) or H (per KV head)."""
+    vec [B][VH][capT/64][VD][64] fp32 (tiles of 64 slots), VH = 1 (head
+    mean) or H (per KV head)."""
 
     def __init__(self, B, H, D, VD, VH, cap, device, normalize=True):
         if VH not in (1, H):
@@ -37,7 +38,8 @@ class DeviceIndex:
         if self.device.type == "cuda" and self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
         self.capT = (self.cap + 63) // 64 * 64
-        self.vec = torch.empty((self.B, self.VH, self.VD, self.capT), dtype=torch.float32, device=self.device)
+        self.vec = torch.empty((self.B, self.VH, self.capT // 64, self.VD, 64), dtype=torch.float32,
+                               device=self.device)
         self.keys = torch.empty((self.B, self.VH, self.capT), dtype=torch.int64, device=self.device)
         self.size = np.zeros(self.B, dtype=np.int64)
         self.head = np.zeros(self.B, dtype=np.int64)
@@ -89,15 +91,20 @@ class DeviceIndex:
                                        self.vec.data_ptr(), self.capT, st), "hc_index_add")
         self._slot_of = slot_of            # kept until the launch has run (the next add replaces it)
 
-    def search(self, q, R, hits, normalize_q=True, stream=None):
+    def search(self, q, R, hits, normalize_q=True, stream=None, hits_host=None, wait_event=None, done_event=None):
         """Top-R logical indices per (row, head) for queries q (B,VH,q_dim)
         fp32 on the device, into hits (B,VH,R) int64 on the device (-1 past
-        each row's size); on the current stream."""
+        each row's size); on `stream` (default: the current stream), after
+        wait_event if given.  hits_host (pinned, like hits): also copied
+        there, done_event recorded behind the copy."""
         if q.dtype != torch.float32 or q.dim() != 3 or q.shape[0] != self.B or q.shape[1] != self.VH \
                 or q.stride(2) != 1 or q.device != self.device:
             raise RuntimeError("DeviceIndex.search: q must be (B,VH,q_dim) fp32 on the index's device")
         if hits.dtype != torch.int64 or tuple(hits.shape) != (self.B, self.VH, int(R)) or not hits.is_contiguous():
             raise RuntimeError("DeviceIndex.search: hits must be a contiguous (B,VH,R) int64 tensor")
+        if hits_host is not None and (hits_host.dtype != torch.int64 or hits_host.shape != hits.shape
+                                      or not hits_host.is_contiguous() or hits_host.is_cuda):
+            raise RuntimeError("DeviceIndex.search: hits_host must be a contiguous host tensor like hits")
         st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
         sizes = np.ascontiguousarray(self.size, dtype=np.int64)
         heads = np.ascontiguousarray(self.head, dtype=np.int64)
@@ -105,8 +112,13 @@ class DeviceIndex:
         N.check(self._lib.hc_index_search(self.B, self.VH, self.VD, self.cap, q.data_ptr(), qs[0], qs[1],
                                           int(q.shape[2]), int(bool(normalize_q)), self.vec.data_ptr(), self.capT,
                                           sizes.ctypes.data, heads.ctypes.data, int(R), self.keys.data_ptr(),
-                                          hits.data_ptr(), st), "hc_index_search")
+                                          hits.data_ptr(), None if hits_host is None else hits_host.data_ptr(),
+                                          wait_event, done_event, st), "hc_index_search")
         return hits
+
+    def vectors(self, b):
+        """Row b's vectors as (VH, VD, capT), slot-indexed (a view over the tiles)."""
+        return self.vec[b].permute(0, 2, 1, 3).reshape(self.VH, self.VD, self.capT)
 
     def physical(self, b, logical):
         """Physical slot of logical index `logical` of row b."""

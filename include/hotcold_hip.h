@@ -595,8 +595,9 @@ void hc_cold_job_free(void* job);
 
 /*
  * Device search index of the cold stores of one layer: the search vectors of
- * B stores kept in HBM as vec [B][VH][VD][capT] fp32 (capT >= the stores'
- * capacity), with the same arithmetic as hc_cold_add / hc_cold_search, so the
+ * B stores kept in HBM as vec [B][VH][capT/64][VD][64] fp32 (tiles of 64
+ * slots; capT >= the stores' capacity, a multiple of 64), with the same
+ * arithmetic as hc_cold_add / hc_cold_search, so the
  * hits are the host store's, bit for bit.  It replaces the reference's CPU
  * faiss.IndexFlatIP scan (controller.py:223-232, 274-293) where a host scan
  * cannot keep up (a layer of 16 rows x 8 heads x 30 720 tokens is 2 GB of
@@ -620,11 +621,14 @@ int hc_index_add(int64_t B, int64_t H, int64_t D, int64_t VH, int64_t VD, int no
  * top R <= 1024 logical indices (oldest token = 0) in rank order -- inner
  * product descending, ties to the older token -- to hits [B][VH][R] (int64 on
  * the device), -1 past min(R, size).  keys: device scratch of B*VH*capT
- * uint64.
+ * uint64.  On `stream`, optionally: first wait for wait_event (the query's
+ * producer), then copy the hits to hits_host (pinned, B*VH*R int64) and
+ * record done_event behind the copy; NULL skips each.
  */
 int hc_index_search(int64_t B, int64_t VH, int64_t VD, int64_t cap, const float* q, int64_t q_sb, int64_t q_sh,
                     int64_t q_dim, int normalize_q, const float* vec, int64_t capT, const int64_t* sizes,
-                    const int64_t* heads, int64_t R, uint64_t* keys, int64_t* hits, void* stream);
+                    const int64_t* heads, int64_t R, uint64_t* keys, int64_t* hits, int64_t* hits_host,
+                    void* wait_event, void* done_event, void* stream);
 
 #ifdef __cplusplus
 }

@@ -958,7 +958,7 @@ def test_device_index_equals_the_host_store(vec_heads, VD):
         assert len(rings[b]) == int(dix.size[b])
         ex = rings[b].export()
         slots = [dix.physical(b, l) for l in range(len(rings[b]))]
-        got = dix.vec[b][:, :, slots].permute(2, 0, 1).cpu().numpy()     # (n, VH, VD)
+        got = dix.vectors(b)[:, :, slots].permute(2, 0, 1).cpu().numpy()     # (n, VH, VD)
         assert np.array_equal(got, ex["vec"]), b
     R = 64
     hits = torch.empty((B, vec_heads, R), dtype=torch.int64, device=DEV)
@@ -980,3 +980,122 @@ def test_device_index_equals_the_host_store(vec_heads, VD):
                 got = h_dev[b, h]
                 assert np.array_equal(got[:len(want)], want), (trial, b, h)
                 assert (got[len(want):] == -1).all()
+
+
+
+def _host_query(q, VD):
+    """q cropped or padded to VD and normalised as the host store does it
+    (squares summed in fp64 in dimension order)."""
+    qq = np.zeros(VD, np.float32)
+    n = min(len(q), VD)
+    qq[:n] = q[:n]
+    ss = 0.0
+    for x in qq.astype(np.float64):
+        ss += x * x
+    return (qq.astype(np.float64) / max(math.sqrt(ss), 1e-12)).astype(np.float32)
+
+
+@pytest.mark.parametrize("copies,R", [(0, 64), (500, 64), (500, 1024), (1200, 64), (1200, 1024), (5000, 256)])
+def test_device_index_selection_with_many_ties(copies, R):
+    """The selection's paths against the host store: candidate sets that fit
+    in LDS or never do (every vector equal), ties at the R-th key fewer than
+    its tie buffer or more (then taken oldest first by the ordered scan), R up
+    to 1024; rings of 5000 slots after 6000 adds, so the oldest token is
+    mid-ring.  The query is the repeated vector, so its copies are the top
+    keys."""
+    from hotcold_kv.controller import _Ring
+    from hotcold_kv.device_index import DeviceIndex
+    B, H, D, cap, te = 2, 2, 16, 5000, 6000
+    rng = np.random.default_rng(copies + R)
+    rings = [_Ring(cap, H, D, D, 1) for _ in range(B)]
+    dix = DeviceIndex(B, H, D, D, 1, cap, DEV)
+    kpre = rng.standard_normal((B, H, te, D), dtype=np.float32)
+    u = rng.standard_normal((H, D), dtype=np.float32)
+    for b in range(B):
+        at = rng.choice(np.arange(1000, te), size=min(copies, te - 1000), replace=False)
+        kpre[b][:, at] = u[:, None, :]
+    v = rng.standard_normal((B, H, te, D), dtype=np.float32)
+    pos = np.arange(te, dtype=np.int64)
+    idx = np.tile(np.arange(te, dtype=np.int64), (B, 1))
+    for half in (slice(0, 3500), slice(3500, te)):
+        for b in range(B):
+            rings[b].add(kpre[b][:, half], v[b][:, half], pos[half], idx[b, half] - half.start)
+        dix.add(torch.from_numpy(np.ascontiguousarray(kpre[:, :, half])).to(DEV), idx[:, half] - half.start)
+    torch.cuda.synchronize()
+    hits = torch.empty((B, 1, R), dtype=torch.int64, device=DEV)
+    for q in (u.mean(0), rng.standard_normal(D).astype(np.float32)):
+        dix.search(torch.from_numpy(np.tile(q, (B, 1, 1))).to(DEV), R, hits)
+        got = hits.cpu().numpy()
+        for b in range(B):
+            want = rings[b].search(_host_query(q, D), R)
+            assert np.array_equal(got[b, 0, :len(want)], want), b
+            assert (got[b, 0, len(want):] == -1).all()
+
+@pytest.mark.parametrize("per_head,faiss_dim", [(False, 32), (True, 64), (True, 96)])
+def test_scheduled_device_search_equals_the_host_search(per_head, faiss_dim):
+    """Two controllers fed the same staged evictions (gather_evict into an
+    eviction stage, as the cache evicts) and the same decode queries: one
+    ranks on its device index and gathers the hits natively
+    (hc_index_search + hc_cold_gather_async), the other searches the host
+    stores (hc_cold_retrieve_async).  Every scheduled retrieval stages the
+    same k_pre, v, positions, valid flags and rotary-table rows, over rings
+    that wrap and planted exact ties; after an add the device index cannot
+    follow (no stage) that layer goes back to the host search, still equal."""
+    from hotcold_kv import KVController
+    from hotcold_kv.datatypes import EvictedKV
+    B, Hk, G, D, S, te, R = 2, 2, 2, 64, 400, 120, 16
+    rng = torch.Generator().manual_seed(5)
+    args = dict(max_capacity_prompt=128, cpu_buffer_size=300, faiss_dim=faiss_dim, window_size=1,
+                query_pool_size=2, lookahead_k=R, hold_retrieved=True, per_head_retrieval=per_head,
+                profile_overlap=False)
+    ctrls = [KVController(device_search=True, **args), KVController(device_search=False, **args)]
+    inv = synthetic.inv_freq(D, 10000.0)
+    for c in ctrls:
+        c._lazy_init(torch.empty((B, Hk, 1, D), dtype=torch.bfloat16, device=DEV), n_layers=1)
+        c.set_rope(inv, 1.0)
+    assert ctrls[0]._dindex[0] is not None and ctrls[1]._dindex[0] is None
+    print(f"[case] per_head {per_head} faiss_dim {faiss_dim}", flush=True)
+    n_dev = 0
+    for rnd in range(6):
+        k = torch.randn((B, Hk, S, D), generator=rng).to(torch.bfloat16)
+        k[:, :, 1::2] = k[:, :, 0::2]                       # exact ties: every token twice
+        v = torch.randn((B, Hk, S, D), generator=rng).to(torch.bfloat16)
+        pos = (torch.arange(S, dtype=torch.int64) + 500 * rnd).repeat(B, 1)
+        idx = torch.stack([torch.randperm(S, generator=rng)[:te].sort().values for _ in range(B)])
+        staged = rnd != 3                                   # round 3: a synchronous add
+        for c in ctrls:
+            kd, vd, pd, id_ = k.to(DEV), v.to(DEV), pos.to(DEV), idx.to(DEV)
+            if staged:
+                st = c.evict_stage(kd.device, B, Hk, te, D)
+                kp, vv, pp = ops.gather_evict(id_, kd, vd, pd, dev_out=st.dev, host_out=st.host)
+                torch.cuda.synchronize()
+                c.add_evicted_to_cold_store(0, EvictedKV(k_pre_cpu=kp, v_cpu=vv, pos_cpu=pp, evicted_idx=idx),
+                                            stage=st)
+            else:
+                st = None
+                kp = k.float().gather(2, idx.view(B, 1, te, 1).expand(B, Hk, te, D))
+                vv = v.float().gather(2, idx.view(B, 1, te, 1).expand(B, Hk, te, D))
+                c.add_evicted_to_cold_store(0, EvictedKV(k_pre_cpu=kp, v_cpu=vv, pos_cpu=pos.gather(1, idx),
+                                                         evicted_idx=idx))
+        for step in range(3):
+            q = torch.randn((B, Hk * G, 1, D), generator=rng).to(torch.bfloat16)
+            if step == 0:
+                q[:, :] = k[:, :1, 2 * rnd:2 * rnd + 1].repeat_interleave(Hk * G, 1)   # aims at a tie
+            slots = []
+            for c in ctrls:
+                c.update_query_window(0, q.to(DEV))
+                c.maybe_launch_async_retrieval(0)
+                c.wait_for_retrieval(0)
+                slots.append(c._retrieval_ready_cpu[0])
+            a, b = slots
+            assert a is not None and b is not None and a is not b
+            for x, y, what in zip(a.host, b.host, ("k_pre", "v", "pos", "valid")):
+                assert torch.equal(x, y), (rnd, step, what)
+            assert a.has_tab and b.has_tab and torch.equal(a.tab, b.tab), (rnd, step)
+            assert bool(a.host[3].any())
+        n_dev = ctrls[0].dbg["retrieval_device"]
+        assert n_dev == (3 * (rnd + 1) if rnd < 3 else 9), rnd
+        assert ctrls[1].dbg["retrieval_device"] == 0
+    assert ctrls[0].dbg["device_index_dropped"] == 1 and ctrls[0]._dindex[0] is None
+    for c in ctrls:
+        c.wait_cold_adds()

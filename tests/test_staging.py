@@ -236,15 +236,15 @@ def test_two_slots_per_layer_are_preallocated():
 
 
 def test_slot_buffers_are_views_of_one_block():
-    """k_pre, v, pos, valid, the rotary tables and the pooled query carved
-    from one block in that order, 256-byte aligned and disjoint; one copy of
-    nbytes[0] carries a retrieval without tables, nbytes[1] one with them,
-    and the pooled query lies past both; cos and sin are the two halves of
-    each table row."""
+    """k_pre, v, pos, valid, the rotary tables, the pooled query and the
+    device-search hits carved from one block in that order, 256-byte aligned
+    and disjoint; one copy of nbytes[0] carries a retrieval without tables,
+    nbytes[1] one with them, and the pooled query and hits lie past both;
+    cos and sin are the two halves of each table row."""
     ctrl = _ctrl(per_head_retrieval=True)
     with ctrl._retrieval_lock[0]:
         sl = ctrl._take_slot(0)
-    views = list(sl.host) + [sl.tab, sl.qhost]
+    views = list(sl.host) + [sl.tab, sl.qhost, sl.hits_host]
     base = sl.block.data_ptr()
     offs, ends = _block_layout(ctrl._slot_specs())
     spans = []
@@ -256,7 +256,8 @@ def test_slot_buffers_are_views_of_one_block():
         assert a1 <= b0
     assert [e for _, e in spans] == ends
     assert sl.nbytes == (spans[3][1], spans[4][1])
-    assert sl.block.numel() == spans[5][1] and tuple(sl.qhost.shape) == (1, HK, D)
+    assert sl.block.numel() == spans[6][1] and tuple(sl.qhost.shape) == (1, HK, D)
+    assert tuple(sl.hits_host.shape) == (1, HK, 4) and sl.hits_host.dtype == torch.int64
     cos, sin = sl.tab_host
     assert cos.data_ptr() == sl.tab.data_ptr() and sin.data_ptr() == cos.data_ptr() + (D // 2) * cos.element_size()
     assert cos.stride() == sin.stride() and cos.shape == (1, HK, 4, D // 2)
