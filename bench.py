@@ -766,8 +766,10 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
             hp.hotcold_attention(ctrl, layers[l], l, k["q_pre"], k["k_pre"], k["v"], k["q_post"], k["k_post"],
                                  k["position"], G, w.scaling)
         step_ms.append((time.perf_counter() - ts) * 1e3)
+    t_issue = time.perf_counter()
     torch.cuda.synchronize()
     total_ms = (time.perf_counter() - t_all) * 1e3
+    drain_ms = (time.perf_counter() - t_issue) * 1e3
     for l in range(L):
         ctrl.wait_for_retrieval(l)
     d = ctrl.dbg
@@ -786,6 +788,8 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
         "hot_rows_per_layer_end": layers[0].hot_length(),
         "step_us_wall_mean": round(total_ms * 1e3 / steps, 1),
         "step_us_wall_median": round(statistics.median(step_ms) * 1e3, 1),
+        "step_us_issue_mean": round(statistics.fmean(step_ms) * 1e3, 1),
+        "gpu_drain_ms_after_loop": round(drain_ms, 2),
         "step_us_wall_without_retrieval_median": round(statistics.median(other) * 1e3, 1) if other else None,
         "layer_us_wall_mean": round(total_ms * 1e3 / steps / L, 2),
         "retrievals": d["retrieval_launched"],

@@ -34,6 +34,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <chrono>
 #include <cmath>
 #include <condition_variable>
 #include <deque>
@@ -628,9 +629,21 @@ class JobQueue {
     }
   }
 
+  // Waits for a device event by polling it, asleep between polls: a worker
+  // blocked in the runtime's own wait spins there and slows the launches the
+  // decode thread issues meanwhile.  Retrievals take milliseconds, so the
+  // polling granularity is immaterial.
+  static int wait_device_event(void* ev) {
+    for (;;) {
+      const int r = hc_event_query(ev);
+      if (r != 0) return r < 0 ? r : HC_OK;
+      std::this_thread::sleep_for(std::chrono::microseconds(20));
+    }
+  }
+
   static void execute(RetrieveJob* j) {
     int rc = HC_OK;
-    if (j->wait_event) rc = hc_event_synchronize(j->wait_event);
+    if (j->wait_event) rc = wait_device_event(j->wait_event);
     int64_t missing = 0, nv = 0;
     if (j->is_add) {
       // after the store's earlier adds (the queue hands jobs out in order, so

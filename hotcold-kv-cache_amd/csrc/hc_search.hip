@@ -124,6 +124,7 @@ struct IndexSearchArgs {
   int64_t capT;
   uint64_t* keys;  // scratch [B][VH][capT]
   int64_t* hits;   // [B][VH][R]: logical indices in rank order, -1 past the hits
+  int64_t* hits_mapped;  // the same, into pinned host memory through its device mapping (or null)
   int B, VH, VD, R, cap, q_dim, normalize_q;
   int size[kIdxMaxB], head[kIdxMaxB];  // ring state of each row's store
 };
@@ -243,7 +244,10 @@ __global__ __launch_bounds__(kIdxThreads) void index_select_kernel(IndexSearchAr
   const uint64_t* kb = a.keys + (int64_t)(b * a.VH + vh) * a.capT;
   const int m = min(a.R, size);
   if (m == 0) {  // uniform per workgroup
-    for (int j = tid; j < a.R; j += kIdxThreads) out[j] = -1;
+    for (int j = tid; j < a.R; j += kIdxThreads) {
+      out[j] = -1;
+      if (a.hits_mapped) a.hits_mapped[(int64_t)(b * a.VH + vh) * a.R + j] = -1;
+    }
     return;
   }
   auto logical = [&](int p) { return full ? (p - head + a.cap) % a.cap : p; };
@@ -394,7 +398,11 @@ __global__ __launch_bounds__(kIdxThreads) void index_select_kernel(IndexSearchAr
       }
       __syncthreads();
     }
-  for (int j = tid; j < a.R; j += kIdxThreads) out[j] = j < m ? (int64_t)wl[j] : -1;
+  for (int j = tid; j < a.R; j += kIdxThreads) {
+    const int64_t h = j < m ? (int64_t)wl[j] : -1;
+    out[j] = h;
+    if (a.hits_mapped) a.hits_mapped[(int64_t)(b * a.VH + vh) * a.R + j] = h;
+  }
 }
 
 }  // namespace hc
@@ -442,6 +450,18 @@ extern "C" int hc_index_search(int64_t B, int64_t VH, int64_t VD, int64_t cap, c
   int max_size = 0;
   for (int64_t b = 0; b < B; ++b) max_size = max(max_size, a.size[b]);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  if (hits_host) {
+    // the kernel writes the host copy itself through the pinned buffer's
+    // device mapping: no copy to issue, and the hits are on the host when the
+    // kernel is done
+    void* mapped = nullptr;
+    const hipError_t e = hipHostGetDevicePointer(&mapped, hits_host, 0);
+    if (e != hipSuccess || mapped == nullptr) {
+      (void)hipGetLastError();
+      return set_error(HC_ERR_INVALID, "index_search: hits_host is not pinned host memory");
+    }
+    a.hits_mapped = reinterpret_cast<int64_t*>(mapped);
+  }
   if (wait_event) {
     const hipError_t e = hipStreamWaitEvent(st, reinterpret_cast<hipEvent_t>(wait_event), 0);
     if (e != hipSuccess) return set_error(HC_ERR_HIP, "index_search: hipStreamWaitEvent: %s", hipGetErrorString(e));
@@ -452,11 +472,6 @@ extern "C" int hc_index_search(int64_t B, int64_t VH, int64_t VD, int64_t cap, c
   hipLaunchKernelGGL(index_select_kernel, dim3((unsigned)VH, (unsigned)B), dim3(kIdxThreads), 0, st, a);
   const int rc = check_launch("index_search");
   if (rc != HC_OK) return rc;
-  if (hits_host) {
-    const hipError_t e = hipMemcpyAsync(hits_host, hits, (size_t)(B * VH * R) * sizeof(int64_t),
-                                        hipMemcpyDeviceToHost, st);
-    if (e != hipSuccess) return set_error(HC_ERR_HIP, "index_search: hipMemcpyAsync: %s", hipGetErrorString(e));
-  }
   if (done_event) {
     const hipError_t e = hipEventRecord(reinterpret_cast<hipEvent_t>(done_event), st);
     if (e != hipSuccess) return set_error(HC_ERR_HIP, "index_search: hipEventRecord: %s", hipGetErrorString(e));

@@ -181,8 +181,9 @@ class _Job:
     threading.Thread.  It holds the buffers the search reads and writes until
     the decode thread collects it."""
 
-    def __init__(self, handle, slot, has_tab, keep):
+    def __init__(self, handle, slot, has_tab, keep, by_hits=False):
         self.handle, self.slot, self.has_tab, self.keep = handle, slot, has_tab, keep
+        self.by_hits = by_hits      # a gather of device-ranked hits (hc_cold_gather_async)
         self.result = None          # (n_valid, positions past the table) once done
         self.error = None           # (status, message) if the search failed
 
@@ -322,6 +323,8 @@ class KVController:
         self._dindex = []           # per layer: DeviceIndex, or None (host search)
         self._search_stream = None  # side stream of the device searches
         self._search_done = []      # per layer: event behind its last device search
+        self._pending_search = []   # (layer, slot, index) of device searches scheduled this step
+        self._flush_event = None    # decode-stream event the step's device searches wait for
         self.last_injected_len = 0
         self.held_mem = []
 
@@ -436,6 +439,8 @@ class KVController:
                     for ev in (sl.ready, sl.t0, sl.t1, sl.free_after, sl.q_ready, sl.hits_ready):
                         if ev is not None:
                             lib.hc_event_destroy(ev)
+            if self._flush_event is not None:
+                lib.hc_event_destroy(self._flush_event)
             for s in (self._stream, self._search_stream):
                 if s is not None:
                     lib.hc_stream_destroy(s)
@@ -622,8 +627,11 @@ class KVController:
         """The eviction's search vectors into the layer's device index, from
         the stage's device block (the twin of the host block ev's tensors
         view), on the current stream after the layer's last device search
-        (which may still read the ring slots this add overwrites).  Without
-        such a block the layer goes back to the host search."""
+        (which may still read the ring slots this add overwrites).  First the
+        layer's device search is settled: its gather addresses the host
+        stores by the logical indices ranked before this add.  Without such a
+        block the layer goes back to the host search."""
+        self._settle_search(li)
         B, H, te, D = ev.k_pre_cpu.shape
         if stage is None or stage.dev.device.type != "cuda" or ev.k_pre_cpu.data_ptr() != stage.host.data_ptr() \
                 or stage.dev.numel() < 4 * B * H * te * D:
@@ -649,18 +657,19 @@ class KVController:
             return q.float().view(B, self.Hk, Hq // self.Hk, T, D).mean(dim=(2, 3))
         return q.mean(dim=1).mean(dim=1).float()
 
-    def _stage_query(self, layer_idx, slot):
-        """Pool the window's queries on the device into the slot's pinned
-        buffer (hc_retrieval_query: the pooling kernel, the device-to-host
-        copy and the slot's event, on the current stream, no host wait).
-        Windows of more than 64 query rows, or of mixed dtypes, are pooled by
-        torch (_pooled_query_dev) instead."""
+    def _stage_query(self, layer_idx, slot, to_host=True):
+        """Pool the window's queries on the device into the slot's query
+        buffer (hc_retrieval_query: the pooling kernel, on the current
+        stream, no host wait); to_host: also copy it to the slot's pinned
+        buffer and record the slot's event behind the copy.  Windows of more
+        than 64 query rows, or of mixed dtypes, are pooled by torch
+        (_pooled_query_dev) instead."""
         win = list(self.query_window[int(layer_idx)])
         q0 = win[0]
         B, Hq, _, D = q0.shape
         if slot.qdev is None:
             self._alloc_dev(slot, q0.device)
-        if slot.q_ready is None:
+        if slot.q_ready is None and to_host:
             slot.q_ready = self._event(0)
         stream = ops_stream(q0.device)
         rows = [(t, r) for t in win for r in range(t.shape[2])]
@@ -673,12 +682,14 @@ class KVController:
             sh = (ctypes.c_int64 * n)(*[t.stride(1) for t, _ in rows])
             N.check(N.lib().hc_retrieval_query(N.dtype_code(q0.dtype), B, Hq, self.Hk, D, n, ptrs, sb, sh,
                                                int(self.per_head_retrieval), slot.qdev.data_ptr(),
-                                               slot.qhost.data_ptr(), slot.q_ready, stream), "hc_retrieval_query")
+                                               slot.qhost.data_ptr() if to_host else None,
+                                               slot.q_ready if to_host else None, stream), "hc_retrieval_query")
             return
         vh = self.Hk if self.per_head_retrieval else 1
         slot.qdev.copy_(self._pooled_query_dev(layer_idx).reshape(B, vh, D))
-        slot.qhost.copy_(slot.qdev, non_blocking=True)
-        N.check(N.lib().hc_event_record(slot.q_ready, stream), "hc_event_record")
+        if to_host:
+            slot.qhost.copy_(slot.qdev, non_blocking=True)
+            N.check(N.lib().hc_event_record(slot.q_ready, stream), "hc_event_record")
 
     def _wait_event(self, ev):
         N.check(N.lib().hc_event_synchronize(ev), "hc_event_synchronize")
@@ -827,10 +838,18 @@ class KVController:
         """Every window_size calls, start a background search with the pooled
         recent queries (controller.py:314-342).  Skipped while the layer's
         previous search still runs (controller.py:333-335) or when every
-        staging slot is in use."""
+        staging slot is in use.  Device searches scheduled in one decode step
+        are launched together after the last layer's call (_flush_searches)."""
+        li = int(layer_idx)
+        if self._pending_search and li <= self._pending_search[-1][0]:
+            self._flush_searches()          # a new step began before the last layer's call
+        self._maybe_launch(li)
+        if self._pending_search and li == self.n_layers - 1:
+            self._flush_searches()
+
+    def _maybe_launch(self, li):
         if self.lookahead_k <= 0:
             return
-        li = int(layer_idx)
         self.step_count[li] += 1
         if self.step_count[li] % self.window_size != 0:
             return
@@ -854,13 +873,17 @@ class KVController:
             if slot is None:
                 self.dbg["retrieval_skipped_no_slot"] += 1
                 return
+        if dindex is not None:
+            # pooled on the device now; ranked on the search stream with the
+            # step's other device searches
+            self._stage_query(li, slot, to_host=False)
+            self._pending_search.append((li, slot, dindex))
+            self.dbg["retrieval_launched"] += 1
+            return
         if self._stream is not None and self.query_window[li][0].is_cuda:
             # pooled on the device; the search thread waits for the host
             # copy, the decode thread does not
             self._stage_query(li, slot)
-            if dindex is not None:
-                self._launch_device_search(li, slot, dindex)
-                return
             q_vecs, event = None, slot.q_ready
         else:
             q_vecs, event = self._pooled_query_np(li), None
@@ -874,11 +897,33 @@ class KVController:
             self._retrieval_thread[li] = _Job(handle, slot, tab, keep)
             self.dbg["retrieval_launched"] += 1
 
-    def _launch_device_search(self, li, slot, dindex):
-        """A scheduled search on the device index: on the search stream,
-        after the query's pooling, the ranking kernel writes the slot's hits
-        and they are copied to its pinned buffer; a native job then waits for
-        that copy (and for the adds submitted before it) and gathers the
+    def _flush_searches(self):
+        """Launch the pending device searches on the search stream, behind one
+        event recorded now on the decode stream (after every pooled query)."""
+        pending, self._pending_search = self._pending_search, []
+        if not pending:
+            return
+        if self._flush_event is None:
+            self._flush_event = self._event(0)
+        N.check(N.lib().hc_event_record(self._flush_event, ops_stream(self._device)), "hc_event_record")
+        for i, (li, slot, dindex) in enumerate(pending):
+            self._launch_device_search(li, slot, dindex, self._flush_event if i == 0 else None)
+
+    def _settle_search(self, li):
+        """Before the layer's store takes new tokens: its pending device search
+        is launched, and its gather job (which addresses the store by the
+        logical indices the device ranked) is waited for."""
+        if any(p[0] == li for p in self._pending_search):
+            self._flush_searches()
+        job = self._retrieval_thread[li] if self._retrieval_thread else None
+        if isinstance(job, _Job) and job.by_hits:
+            job.join()
+
+    def _launch_device_search(self, li, slot, dindex, wait_event):
+        """A scheduled search on the device index: on the search stream, after
+        wait_event, the ranking kernels write the slot's hits (also into its
+        pinned buffer) and its event is recorded; a native job then waits for
+        that event (and for the adds submitted before it) and gathers the
         hits' rows from the host stores into the slot, as the host search
         would have (hc_cold_gather).  The decode thread waits for none of it."""
         lib = N.lib()
@@ -888,7 +933,7 @@ class KVController:
         R = self.lookahead_k
         try:
             dindex.search(slot.qdev, R, slot.hits_dev, normalize_q=self.normalize_for_ip, stream=ss,
-                          hits_host=slot.hits_host, wait_event=slot.q_ready, done_event=slot.hits_ready)
+                          hits_host=slot.hits_host, wait_event=wait_event, done_event=slot.hits_ready)
         except Exception:
             with self._retrieval_lock[li]:
                 slot.state = _Slot.FREE
@@ -907,8 +952,7 @@ class KVController:
                 slot.state = _Slot.FREE
             N.check(N.HC_ERR_INVALID, "hc_cold_gather_async")
         with self._retrieval_lock[li]:
-            self._retrieval_thread[li] = _Job(handle, slot, tab, (slot.hits_host, table))
-            self.dbg["retrieval_launched"] += 1
+            self._retrieval_thread[li] = _Job(handle, slot, tab, (slot.hits_host, table), by_hits=True)
             self.dbg["retrieval_device"] += 1
 
     def _search_workers(self):
@@ -919,6 +963,8 @@ class KVController:
 
     def wait_for_retrieval(self, layer_idx, timeout=None):
         """Join the layer's background search, if any (test and shutdown helper)."""
+        if any(p[0] == int(layer_idx) for p in self._pending_search):
+            self._flush_searches()
         th = self._retrieval_thread[int(layer_idx)] if self._inited else None
         if th is not None:
             th.join(timeout)

@@ -95,8 +95,8 @@ class DeviceIndex:
         """Top-R logical indices per (row, head) for queries q (B,VH,q_dim)
         fp32 on the device, into hits (B,VH,R) int64 on the device (-1 past
         each row's size); on `stream` (default: the current stream), after
-        wait_event if given.  hits_host (pinned, like hits): also copied
-        there, done_event recorded behind the copy."""
+        wait_event if given.  hits_host (pinned, like hits): the kernel
+        writes the hits there too; done_event is recorded behind it."""
         if q.dtype != torch.float32 or q.dim() != 3 or q.shape[0] != self.B or q.shape[1] != self.VH \
                 or q.stride(2) != 1 or q.device != self.device:
             raise RuntimeError("DeviceIndex.search: q must be (B,VH,q_dim) fp32 on the index's device")

@@ -621,9 +621,11 @@ int hc_index_add(int64_t B, int64_t H, int64_t D, int64_t VH, int64_t VD, int no
  * top R <= 1024 logical indices (oldest token = 0) in rank order -- inner
  * product descending, ties to the older token -- to hits [B][VH][R] (int64 on
  * the device), -1 past min(R, size).  keys: device scratch of B*VH*capT
- * uint64.  On `stream`, optionally: first wait for wait_event (the query's
- * producer), then copy the hits to hits_host (pinned, B*VH*R int64) and
- * record done_event behind the copy; NULL skips each.
+ * uint64.  On `stream`, optionally (NULL skips each): first wait for
+ * wait_event (the query's producer); write the hits to hits_host as well
+ * (pinned host memory, B*VH*R int64, written by the kernel through its device
+ * mapping, so they are on the host once the kernel is done; anything else is
+ * HC_ERR_INVALID); record done_event behind the kernels.
  */
 int hc_index_search(int64_t B, int64_t VH, int64_t VD, int64_t cap, const float* q, int64_t q_sb, int64_t q_sh,
                     int64_t q_dim, int normalize_q, const float* vec, int64_t capT, const int64_t* sizes,

@@ -1099,3 +1099,64 @@ def test_scheduled_device_search_equals_the_host_search(per_head, faiss_dim):
     assert ctrls[0].dbg["device_index_dropped"] == 1 and ctrls[0]._dindex[0] is None
     for c in ctrls:
         c.wait_cold_adds()
+
+
+def test_device_searches_of_a_step_launch_together_and_settle_before_adds():
+    """Three layers: the device searches scheduled in a decode step wait
+    until the last layer's call and are then launched together; an eviction
+    into a layer whose search is still pending launches it first and waits for
+    its gather, so the staged rows are those of the store the device ranked.
+    Every layer's staged retrieval equals the host search's."""
+    from hotcold_kv import KVController
+    from hotcold_kv.datatypes import EvictedKV
+    B, Hk, G, D, S, te, R, L = 2, 2, 2, 64, 300, 100, 8, 3
+    rng = torch.Generator().manual_seed(9)
+    args = dict(max_capacity_prompt=128, cpu_buffer_size=150, faiss_dim=D, window_size=1, query_pool_size=1,
+                lookahead_k=R, hold_retrieved=True, per_head_retrieval=True, profile_overlap=False)
+    ctrls = [KVController(device_search=True, **args), KVController(device_search=False, **args)]
+    for c in ctrls:
+        c._lazy_init(torch.empty((B, Hk, 1, D), dtype=torch.float16, device=DEV), n_layers=L)
+
+    def evict(c, li, rnd):
+        g = torch.Generator().manual_seed(100 * rnd + li)
+        k = torch.randn((B, Hk, S, D), generator=g).to(torch.float16).to(DEV)
+        v = torch.randn((B, Hk, S, D), generator=g).to(torch.float16).to(DEV)
+        pos = (torch.arange(S, dtype=torch.int64) + 1000 * rnd).repeat(B, 1).to(DEV)
+        idx = torch.stack([torch.randperm(S, generator=g)[:te].sort().values for _ in range(B)])
+        st = c.evict_stage(k.device, B, Hk, te, D)
+        kp, vv, pp = ops.gather_evict(idx.to(DEV), k, v, pos, dev_out=st.dev, host_out=st.host)
+        torch.cuda.synchronize()
+        c.add_evicted_to_cold_store(li, EvictedKV(k_pre_cpu=kp, v_cpu=vv, pos_cpu=pp, evicted_idx=idx), stage=st)
+
+    for c in ctrls:
+        for li in range(L):
+            evict(c, li, 0)
+    for step in range(4):
+        qs = [torch.randn((B, Hk * G, 1, D), generator=rng).to(torch.float16).to(DEV) for _ in range(L)]
+        for c in ctrls:
+            dev = c.device_search
+            for li in range(L):
+                c.update_query_window(li, qs[li])
+                c.maybe_launch_async_retrieval(li)
+                if dev and li < L - 1 and not (step == 2 and li == 1):
+                    assert [p[0] for p in c._pending_search] == list(range(li + 1))
+                    assert c._retrieval_thread[li] is None
+                if step == 2 and li == 1:
+                    # layer 0's device search is still pending; the host search
+                    # is joined first, so both rank the store before the add
+                    if not dev:
+                        c.wait_for_retrieval(0)
+                    evict(c, 0, 1 + step)
+                    if dev:                     # the pending searches were launched first
+                        assert not c._pending_search and c._retrieval_thread[1] is not None
+            if dev:
+                assert not c._pending_search
+            for li in range(L):
+                c.wait_for_retrieval(li)
+        for li in range(L):
+            a, b = ctrls[0]._retrieval_ready_cpu[li], ctrls[1]._retrieval_ready_cpu[li]
+            for x, y, what in zip(a.host, b.host, ("k_pre", "v", "pos", "valid")):
+                assert torch.equal(x, y), (step, li, what)
+    assert ctrls[0].dbg["retrieval_device"] == 4 * L and ctrls[1].dbg["retrieval_device"] == 0
+    for c in ctrls:
+        c.wait_cold_adds()
