@@ -590,10 +590,41 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
                          "scoring_mfma_frac": round(sflops / (comp_ms * 1e-3) / 1e12 / FP64_MFMA_PEAK_TFLOPS, 4)}
     if cpu:
         out["cpu_baseline"] = cpu_baseline_config(w, q_post[:, :, S - W:].cpu(), k_post.cpu(), v.cpu())
-    del q_post, k_post, v
+    del q_post, k_post, v, kb, vb
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    out["device_search"] = measure_device_search(w, dev, st, flush, g)
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return out
+
+
+def measure_device_search(w, dev, st, flush, g, reps=12):
+    """One layer's device search index at the workload's cold-store size:
+    every sequence's evicted prompt tokens (seq_len - budget of them, N(0,1)
+    pre-RoPE keys) added per KV head, then the top-held search per (sequence,
+    KV head) timed differentially (hc_index_search: the scoring kernel and
+    the select kernel).  Algorithmic bytes: the fp32 vectors read once, the
+    order keys written and read once."""
+    import numpy as np
+    import torch
+    from hotcold_kv.device_index import DeviceIndex
+
+    B, Hk, D, R = w.batch, w.hk, w.head_dim, w.held
+    n = w.seq_len - w.budget
+    dix = DeviceIndex(B, Hk, D, D, Hk, w.seq_len, dev)
+    with torch.cuda.stream(st):
+        kpre = torch.randn((B, Hk, n, D), generator=g, device=dev, dtype=torch.float32)
+        dix.add(kpre, np.tile(np.arange(n, dtype=np.int64), (B, 1)), stream=st.cuda_stream)
+        q = torch.randn((B, Hk, D), generator=g, device=dev, dtype=torch.float32)
+        hits = torch.empty((B, Hk, R), dtype=torch.int64, device=dev)
+    del kpre
+    ms = differential_ms(st, flush, lambda i: dix.search(q, R, hits, stream=st.cuda_stream), reps)
+    nbytes = B * Hk * n * (4 * D + 16)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    return {"tokens_per_store": n, "stores": B, "vector_heads": Hk, "vector_dim": D, "top": R,
+            "search_us": round(ms * 1e3, 1), "bytes": int(nbytes), "achieved_GBps": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline_config(w, q_win, k, v, decode_sample=8, max_batch=16):
@@ -910,6 +941,8 @@ def main():
                     help="only the H2O figures of one layer (one JSON object; for profiling)")
     ap.add_argument("--pipeline-only", action="store_true",
                     help="only the hot/cold pipeline of the 16k held-slot workload (one JSON object)")
+    ap.add_argument("--device-search-only", action="store_true",
+                    help="only the device search index figures of the 16k/32k/64k workloads (one JSON object)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; the hot tier shards by batch and KV head "
@@ -928,6 +961,13 @@ def main():
     torch.cuda.set_device(dev)
     if args.h2o_only:
         print(json.dumps({"h2o": measure_h2o(w, dev)}), flush=True)
+        return
+    if args.device_search_only:
+        st, g = torch.cuda.Stream(dev), torch.Generator(device=dev).manual_seed(5)
+        flush = CacheSweep(dev)
+        print(json.dumps({"device_search": {name: measure_device_search(synthetic.WORKLOADS[name], dev, st, flush, g)
+                                             for name in ("llama8b_16k_b1024_held64", "b16_32k_b2048_held128",
+                                                          "bf16_b4_64k_b4096_held256")}}), flush=True)
         return
     if args.pipeline_only:
         print(json.dumps({"hotcold_pipeline": hotcold_pipeline(synthetic.WORKLOADS["llama8b_16k_b1024_held64"],
@@ -990,7 +1030,8 @@ def main():
             r = measure_config(synthetic.WORKLOADS[name], dev, flush, cpu=not args.no_cpu_baseline)
             log(f"  decode {r['decode']['us_per_layer_step']} us/layer-step ({r['decode']['frac'] * 100:.1f}% of "
                 f"HBM peak), compaction {r['compaction']['ms_per_layer']} ms/layer, re-RoPE "
-                f"{r['inject']['rerope_us_all_layers']} us, H2D {r['inject']['h2d_GBps']} GB/s")
+                f"{r['inject']['rerope_us_all_layers']} us, H2D {r['inject']['h2d_GBps']} GB/s, device search "
+                f"{r['device_search']['search_us']} us ({r['device_search']['frac'] * 100:.1f}% of HBM peak)")
             if "cpu_baseline" in r:
                 c = r["cpu_baseline"]
                 log(f"  cpu baseline ({c['dtype']}, {c['threads']} threads): compaction {c['compact_ms_per_layer']} "
