@@ -513,12 +513,14 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
                      "bytes_per_launch": int(nbytes), "achieved_GBps": round(gbps, 1),
                      "frac": round(gbps / HBM_PEAK_GBS, 4), "layers_per_launch": w.layers}
 
-    # -- inject: staged fp32 held slot of every layer -> re-RoPE into the hot buffers --------
-    # (rotary tables at the held positions in the cache dtype, as the search
-    # thread ships them with a retrieval)
+    # -- inject: staged held slot of every layer -> re-RoPE into the hot buffers --------------
+    # (K/V staged in the cache dtype and the rotary tables at the held
+    # positions, as a retrieval ships them)
     inv = synthetic.inv_freq(D, w.theta)
-    kp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).pin_memory()
-    vp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).pin_memory()
+    kv_dt = dt if dt in (torch.float16, torch.bfloat16) else torch.float32
+    kes = elem_size(kv_dt)
+    kp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).to(kv_dt).pin_memory()
+    vp_host = torch.randn((LB, Hk, R, D), dtype=torch.float32).to(kv_dt).pin_memory()
     kp_dev = torch.empty_like(kp_host, device=dev)
     vp_dev = torch.empty_like(vp_host, device=dev)
     kp_dev.copy_(kp_host)
@@ -533,8 +535,8 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
     with torch.cuda.stream(st):
         inject(0)
     inj_ms = differential_ms(st, flush, inject, reps)
-    # staged K and V read in fp32, both tables read, K and V written in the cache dtype
-    inj_bytes = 2 * LB * Hk * R * D * 4 + LB * Hk * R * D * es + 2 * LB * Hk * R * D * es
+    # staged K and V read, both tables read, K and V written in the cache dtype
+    inj_bytes = 2 * LB * Hk * R * D * kes + LB * Hk * R * D * es + 2 * LB * Hk * R * D * es
     side = torch.cuda.Stream(dev)
     torch.cuda.synchronize()
     e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -545,7 +547,7 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
         e1.record(side)
     torch.cuda.synchronize()
     h2d_ms = e0.elapsed_time(e1)
-    h2d_bytes = 2 * LB * Hk * R * D * 4
+    h2d_bytes = 2 * LB * Hk * R * D * kes
 
     # decode while the side stream copies the staged slot (the inject feed's overlap)
     def decode_overlapped(i):
@@ -835,7 +837,7 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
         "injections": d["injection_new"], "held_decodes": d["injection_used"],
         "copy_ms_mean": round(d["prefetch_copy_ms_sum"] / max(1, d["prefetch_copy_ms_count"]), 4),
         "h2d_bytes_per_copy": sl.nbytes[1] if sl.has_tab else sl.nbytes[0],
-        "h2d_copy": "one hipMemcpyAsync per retrieval from the slot's pinned block: fp32 k_pre and v, "
+        "h2d_copy": "one hipMemcpyAsync per retrieval from the slot's pinned block: k_pre and v in the cache dtype, "
                     "int64 positions, valid flags, the rotary tables at the positions",
     }
     del layers, ctrl, toks

@@ -56,7 +56,7 @@ def hipcc():
 
 # Host C++ (no device code).  AVX2 for the cold-store scans; floating-point
 # contraction off so the fp64 search arithmetic is the written sequence.
-CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-mavx2", "-ffp-contract=off", "-Wall", f"-I{INCLUDE}",
+CXX_FLAGS = ["-O3", "-std=c++17", "-fPIC", "-pthread", "-mavx2", "-mf16c", "-ffp-contract=off", "-Wall", f"-I{INCLUDE}",
              f"-I{CSRC}"]
 
 

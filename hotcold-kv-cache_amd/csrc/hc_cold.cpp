@@ -400,12 +400,54 @@ extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t*
 
 namespace {
 
+// fp32 -> bf16, round to nearest even (NaN stays a quiet NaN): the device's
+// and torch's conversion.
+inline uint16_t bf16_bits(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// n fp32 values to the retrieval's element type (HC_DTYPE_*): fp32 copies;
+// fp16 rounds to nearest even with F16C (subnormal results kept), as the
+// device's and torch's conversions do; bf16 as bf16_bits.
+void convert_row(const float* src, void* dst, int64_t n, int dtype) {
+  if (dtype == HC_DTYPE_F32) {
+    memcpy(dst, src, sizeof(float) * n);
+  } else if (dtype == HC_DTYPE_F16) {
+    uint16_t* o = static_cast<uint16_t*>(dst);
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8)
+      _mm_storeu_si128(reinterpret_cast<__m128i*>(o + i),
+                       _mm256_cvtps_ph(_mm256_loadu_ps(src + i), _MM_FROUND_TO_NEAREST_INT | _MM_FROUND_NO_EXC));
+    for (; i < n; ++i)
+      o[i] = (uint16_t)_mm_extract_epi16(_mm_cvtps_ph(_mm_set_ss(src[i]), _MM_FROUND_TO_NEAREST_INT), 0);
+  } else {
+    uint16_t* o = static_cast<uint16_t*>(dst);
+    for (int64_t i = 0; i < n; ++i) o[i] = bf16_bits(src[i]);
+  }
+}
+
+inline int64_t kv_elem_bytes(int dtype) { return dtype == HC_DTYPE_F32 ? 4 : 2; }
+
+// A retrieval's K/V output: [B][H][R][D] of the element type `dtype`.
+struct KvOut {
+  int dtype;
+  void* k;
+  void* v;
+  void* row(void* base, int64_t i, int64_t D) const {
+    return static_cast<char*>(base) + i * D * kv_elem_bytes(dtype);
+  }
+};
+
 // Copy the rows of hits[0..m) (logical indices of store s, rank order) into
 // output row (b, h) of a retrieval: kpre/v [B][H][R][D] (one head, or every
-// head with a head-mean vector), pos/valid [B][VH][R].  The caller holds the
-// store's read lock and has zero-filled the outputs.
+// head with a head-mean vector) in out.dtype, pos/valid [B][VH][R].  The
+// caller holds the store's read lock and has zero-filled the outputs.
 void emit_hits(const ColdStore* s, int64_t b, int64_t h, int per_head, int64_t R, const int64_t* hits, int64_t m,
-               float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out) {
+               const KvOut& out, int64_t* pos_out, uint8_t* valid_out) {
   const int64_t H = s->H, D = s->D, VH = per_head ? H : 1;
   for (int64_t j = 0; j < m; ++j) {
     const int64_t p = s->physical(hits[j]);
@@ -413,8 +455,8 @@ void emit_hits(const ColdStore* s, int64_t b, int64_t h, int per_head, int64_t R
     const float* vp = &s->v[(size_t)p * H * D];
     const int64_t h0 = per_head ? h : 0, h1 = per_head ? h + 1 : H;
     for (int64_t hh = h0; hh < h1; ++hh) {
-      memcpy(kpre_out + ((b * H + hh) * R + j) * D, kp + hh * D, sizeof(float) * D);
-      memcpy(v_out + ((b * H + hh) * R + j) * D, vp + hh * D, sizeof(float) * D);
+      convert_row(kp + hh * D, out.row(out.k, (b * H + hh) * R + j, D), D, out.dtype);
+      convert_row(vp + hh * D, out.row(out.v, (b * H + hh) * R + j, D), D, out.dtype);
     }
     pos_out[(b * VH + h) * R + j] = s->pos[p];
     valid_out[(b * VH + h) * R + j] = 1;
@@ -435,11 +477,14 @@ void emit_tab(int64_t b, int64_t h, int64_t VH, int64_t R, const int64_t* pos_ou
 
 // The search itself (every add the caller must see already applied).
 int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh, int64_t q_dim,
-                  int normalize_q, int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
-                  uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
-                  int64_t* tab_missing, int64_t nthreads) {
+                  int normalize_q, int64_t R, int per_head, int kv_dtype, void* kpre_out, void* v_out,
+                  int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes,
+                  uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads) {
   if (B <= 0 || R <= 0 || q_dim <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out)
     return set_error(HC_ERR_INVALID, "cold_retrieve: bad arguments");
+  if (kv_dtype != HC_DTYPE_F32 && kv_dtype != HC_DTYPE_F16 && kv_dtype != HC_DTYPE_BF16)
+    return set_error(HC_ERR_INVALID, "cold_retrieve: bad output dtype %d", kv_dtype);
+  const KvOut out{kv_dtype, kpre_out, v_out};
   if (tab && (tab_rows <= 0 || tab_row_bytes <= 0 || !tab_out))
     return set_error(HC_ERR_INVALID, "cold_retrieve: table rows need a size and an output");
   const ColdStore* s0 = reinterpret_cast<const ColdStore*>(stores[0]);
@@ -453,8 +498,8 @@ int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, 
   }
   const int64_t VH = per_head ? H : 1;
   // outputs: kpre/v [B][H][R][D]; pos/valid [B][R] or [B][H][R]; zero-filled
-  memset(kpre_out, 0, sizeof(float) * B * H * R * D);
-  memset(v_out, 0, sizeof(float) * B * H * R * D);
+  memset(kpre_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
+  memset(v_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
   memset(pos_out, 0, sizeof(int64_t) * B * VH * R);
   memset(valid_out, 0, (size_t)(B * VH * R));
   std::atomic<int64_t> missing{0};
@@ -485,7 +530,7 @@ int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, 
         std::vector<double> ip((size_t)s->size);
         s->scan(qv.data(), h, 0, s->size, ip.data());
         m = s->select(ip.data(), R, hits.data());
-        emit_hits(s, b, h, per_head, R, hits.data(), m, kpre_out, v_out, pos_out, valid_out);
+        emit_hits(s, b, h, per_head, R, hits.data(), m, out, pos_out, valid_out);
       }
     }
     if (tab) emit_tab(b, h, VH, R, pos_out, tab, tab_rows, tab_row_bytes, tab_out, missing);
@@ -496,11 +541,14 @@ int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, 
 
 // The rows of hits found elsewhere (the device search index): hits [B][VH][R]
 // logical indices in rank order, -1 past the hits.
-int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits, float* kpre_out,
-                float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows,
-                int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads) {
+int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits, int kv_dtype,
+                void* kpre_out, void* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads) {
   if (B <= 0 || R <= 0 || !stores || !hits || !kpre_out || !v_out || !pos_out || !valid_out)
     return set_error(HC_ERR_INVALID, "cold_gather: bad arguments");
+  if (kv_dtype != HC_DTYPE_F32 && kv_dtype != HC_DTYPE_F16 && kv_dtype != HC_DTYPE_BF16)
+    return set_error(HC_ERR_INVALID, "cold_gather: bad output dtype %d", kv_dtype);
+  const KvOut out{kv_dtype, kpre_out, v_out};
   if (tab && (tab_rows <= 0 || tab_row_bytes <= 0 || !tab_out))
     return set_error(HC_ERR_INVALID, "cold_gather: table rows need a size and an output");
   const ColdStore* s0 = reinterpret_cast<const ColdStore*>(stores[0]);
@@ -512,8 +560,8 @@ int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const i
       return set_error(HC_ERR_INVALID, "cold_gather: store %lld does not match", (long long)b);
   }
   const int64_t VH = per_head ? H : 1;
-  memset(kpre_out, 0, sizeof(float) * B * H * R * D);
-  memset(v_out, 0, sizeof(float) * B * H * R * D);
+  memset(kpre_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
+  memset(v_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
   memset(pos_out, 0, sizeof(int64_t) * B * VH * R);
   memset(valid_out, 0, (size_t)(B * VH * R));
   std::atomic<int64_t> missing{0};
@@ -529,7 +577,7 @@ int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const i
       while (m < R && hs[m] >= 0) ++m;
       for (int64_t j = 0; j < m; ++j)
         if (hs[j] >= s->size) bad.store(1);
-      if (!bad.load()) emit_hits(s, b, h, per_head, R, hs, m, kpre_out, v_out, pos_out, valid_out);
+      if (!bad.load()) emit_hits(s, b, h, per_head, R, hs, m, out, pos_out, valid_out);
     }
     if (tab) emit_tab(b, h, VH, R, pos_out, tab, tab_rows, tab_row_bytes, tab_out, missing);
   });
@@ -541,26 +589,26 @@ int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const i
 }  // namespace
 
 extern "C" int hc_cold_gather(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits,
-                              float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
-                              int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing,
-                              int64_t nthreads) {
+                              int kv_dtype, void* kpre_out, void* v_out, int64_t* pos_out, uint8_t* valid_out,
+                              const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
+                              int64_t* tab_missing, int64_t nthreads) {
   if (B > 0 && stores)
     for (int64_t b = 0; b < B; ++b)
       if (stores[b]) as_store(stores[b])->wait_all_adds();
-  return gather_impl(stores, B, per_head, R, hits, kpre_out, v_out, pos_out, valid_out, tab, tab_rows, tab_row_bytes,
-                     tab_out, tab_missing, nthreads);
+  return gather_impl(stores, B, per_head, R, hits, kv_dtype, kpre_out, v_out, pos_out, valid_out, tab, tab_rows,
+                     tab_row_bytes, tab_out, tab_missing, nthreads);
 }
 
 extern "C" int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
-                                int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
-                                float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                                int64_t q_dim, int normalize_q, int64_t R, int per_head, int kv_dtype,
+                                void* kpre_out, void* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
                                 int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing,
                                 int64_t nthreads) {
   if (B > 0 && stores)
     for (int64_t b = 0; b < B; ++b)
       if (stores[b]) as_store(stores[b])->wait_all_adds();  // after the adds submitted before it
-  return retrieve_impl(stores, B, q, q_sb, q_sh, q_dim, normalize_q, R, per_head, kpre_out, v_out, pos_out, valid_out,
-                       tab, tab_rows, tab_row_bytes, tab_out, tab_missing, nthreads);
+  return retrieve_impl(stores, B, q, q_sb, q_sh, q_dim, normalize_q, R, per_head, kv_dtype, kpre_out, v_out, pos_out,
+                       valid_out, tab, tab_rows, tab_row_bytes, tab_out, tab_missing, nthreads);
 }
 
 // ---------------------------------------------------------------------------
@@ -587,8 +635,9 @@ struct RetrieveJob {
   int64_t n_flags = 0;  // valid_out entries: B * R, or B * heads * R per KV head
   int normalize_q = 0, per_head = 0;
   const float* q = nullptr;
-  float* kpre_out = nullptr;
-  float* v_out = nullptr;
+  int kv_dtype = HC_DTYPE_F32;
+  void* kpre_out = nullptr;
+  void* v_out = nullptr;
   int64_t* pos_out = nullptr;
   uint8_t* valid_out = nullptr;
   const uint8_t* tab = nullptr;
@@ -657,11 +706,12 @@ class JobQueue {
     } else {
       for (size_t b = 0; b < j->stores.size(); ++b) as_store(j->stores[b])->wait_adds(j->tickets[b]);
       if (rc == HC_OK && j->hits)
-        rc = gather_impl(j->stores.data(), j->B, j->per_head, j->R, j->hits, j->kpre_out, j->v_out, j->pos_out,
+        rc = gather_impl(j->stores.data(), j->B, j->per_head, j->R, j->hits, j->kv_dtype, j->kpre_out, j->v_out,
+                         j->pos_out,
                          j->valid_out, j->tab, j->tab_rows, j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
       else if (rc == HC_OK)
         rc = retrieve_impl(j->stores.data(), j->B, j->q, j->q_sb, j->q_sh, j->q_dim, j->normalize_q, j->R,
-                           j->per_head, j->kpre_out, j->v_out, j->pos_out, j->valid_out, j->tab, j->tab_rows,
+                           j->per_head, j->kv_dtype, j->kpre_out, j->v_out, j->pos_out, j->valid_out, j->tab, j->tab_rows,
                            j->tab_row_bytes, j->tab_out, &missing, j->nthreads);
       if (rc == HC_OK)
         for (int64_t i = 0; i < j->n_flags; ++i) nv += j->valid_out[i] != 0;
@@ -690,11 +740,12 @@ JobQueue& job_queue() {
 }  // namespace
 
 extern "C" void* hc_cold_retrieve_async(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
-                                        int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
-                                        float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
-                                        int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
+                                        int64_t q_dim, int normalize_q, int64_t R, int per_head, int kv_dtype,
+                                        void* kpre_out, void* v_out, int64_t* pos_out, uint8_t* valid_out,
+                                        const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
                                         int64_t nthreads, void* wait_event, int64_t workers) {
-  if (B <= 0 || R <= 0 || q_dim <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out) {
+  if (B <= 0 || R <= 0 || q_dim <= 0 || !stores || !q || !kpre_out || !v_out || !pos_out || !valid_out ||
+      (kv_dtype != HC_DTYPE_F32 && kv_dtype != HC_DTYPE_F16 && kv_dtype != HC_DTYPE_BF16)) {
     set_error(HC_ERR_INVALID, "cold_retrieve_async: bad arguments");
     return nullptr;
   }
@@ -715,9 +766,9 @@ extern "C" void* hc_cold_retrieve_async(void* const* stores, int64_t B, const fl
   const ColdStore* s0 = as_store(stores[0]);
   j->stores.assign(stores, stores + B);
   j->B = B; j->q = q; j->q_sb = q_sb; j->q_sh = q_sh; j->q_dim = q_dim; j->normalize_q = normalize_q;
-  j->R = R; j->per_head = per_head; j->kpre_out = kpre_out; j->v_out = v_out; j->pos_out = pos_out;
-  j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows; j->tab_row_bytes = tab_row_bytes;
-  j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
+  j->R = R; j->per_head = per_head; j->kv_dtype = kv_dtype; j->kpre_out = kpre_out; j->v_out = v_out;
+  j->pos_out = pos_out; j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows;
+  j->tab_row_bytes = tab_row_bytes; j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
   j->n_flags = B * R * (per_head ? s0->H : 1);
   for (int64_t b = 0; b < B; ++b) {
     as_store(stores[b])->pin();
@@ -728,10 +779,11 @@ extern "C" void* hc_cold_retrieve_async(void* const* stores, int64_t B, const fl
 }
 
 extern "C" void* hc_cold_gather_async(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits,
-                                      float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out,
-                                      const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
-                                      int64_t nthreads, void* wait_event, int64_t workers) {
-  if (B <= 0 || R <= 0 || !stores || !hits || !kpre_out || !v_out || !pos_out || !valid_out) {
+                                      int kv_dtype, void* kpre_out, void* v_out, int64_t* pos_out,
+                                      uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes,
+                                      uint8_t* tab_out, int64_t nthreads, void* wait_event, int64_t workers) {
+  if (B <= 0 || R <= 0 || !stores || !hits || !kpre_out || !v_out || !pos_out || !valid_out ||
+      (kv_dtype != HC_DTYPE_F32 && kv_dtype != HC_DTYPE_F16 && kv_dtype != HC_DTYPE_BF16)) {
     set_error(HC_ERR_INVALID, "cold_gather_async: bad arguments");
     return nullptr;
   }
@@ -752,8 +804,9 @@ extern "C" void* hc_cold_gather_async(void* const* stores, int64_t B, int per_he
   const ColdStore* s0 = as_store(stores[0]);
   j->stores.assign(stores, stores + B);
   j->hits = hits;
-  j->B = B; j->R = R; j->per_head = per_head; j->kpre_out = kpre_out; j->v_out = v_out; j->pos_out = pos_out;
-  j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows; j->tab_row_bytes = tab_row_bytes;
+  j->B = B; j->R = R; j->per_head = per_head; j->kv_dtype = kv_dtype; j->kpre_out = kpre_out; j->v_out = v_out;
+  j->pos_out = pos_out; j->valid_out = valid_out; j->tab = tab; j->tab_rows = tab_rows;
+  j->tab_row_bytes = tab_row_bytes;
   j->tab_out = tab_out; j->nthreads = nthreads; j->wait_event = wait_event;
   j->n_flags = B * R * (per_head ? s0->H : 1);
   for (int64_t b = 0; b < B; ++b) {

@@ -56,14 +56,15 @@ __global__ void inject_rerope_kernel(const float* __restrict__ kp, int64_t kp_sb
 // Vector form with cos/sin supplied (the model's rotary tables at the held
 // positions, already rounded to the cache dtype, as apply_rotary_pos_emb
 // receives them): every element is then the reference's bits.  A thread
-// takes four dims of each half of one row -- 16-byte loads of the staged
-// fp32 K and V, one 4-wide load of cos and of sin -- so D/8 threads cover a
-// row and a 256-thread workgroup 2048/D rows.  Rows run (b, h, r) with r
-// fastest; a table shared by the KV heads of a batch row has cs_sh = 0.
+// takes four dims of each half of one row -- 4-wide loads of the staged K
+// and V (fp32, or already in the cache dtype), one 4-wide load of cos and of
+// sin -- so D/8 threads cover a row and a 256-thread workgroup 2048/D rows.
+// Rows run (b, h, r) with r fastest; a table shared by the KV heads of a
+// batch row has cs_sh = 0.
 struct InjectTab {
-  const float* kp;
+  const void* kp;
   int64_t kp_sb, kp_sh, kp_ss;
-  const float* vp;
+  const void* vp;
   int64_t vp_sb, vp_sh, vp_ss;
   const void* cs_cos;
   const void* cs_sin;
@@ -105,7 +106,9 @@ struct Vec4 {  // 2-byte types: four values in 8 bytes
   }
 };
 
-template <typename T>
+// T: the cache dtype; KT: the staged rows' type (float, or T itself -- the
+// keys are rounded to T before the rotation either way).
+template <typename T, typename KT>
 __global__ __launch_bounds__(256) void inject_rerope_tab_kernel(InjectTab a) {
 #pragma clang fp contract(off)
   const int half = a.D / 2;
@@ -118,18 +121,18 @@ __global__ __launch_bounds__(256) void inject_rerope_tab_kernel(InjectTab a) {
   const int64_t bh = row / a.R;
   const int h = (int)(bh % a.Hk);
   const int b = (int)(bh / a.Hk);
-  const float* krow = a.kp + b * a.kp_sb + h * a.kp_sh + (int64_t)r * a.kp_ss;
-  const float* vrow = a.vp + b * a.vp_sb + h * a.vp_sh + (int64_t)r * a.vp_ss;
+  const KT* krow = reinterpret_cast<const KT*>(a.kp) + b * a.kp_sb + h * a.kp_sh + (int64_t)r * a.kp_ss;
+  const KT* vrow = reinterpret_cast<const KT*>(a.vp) + b * a.vp_sb + h * a.vp_sh + (int64_t)r * a.vp_ss;
   const int64_t cso = b * a.cs_sb + h * a.cs_sh + (int64_t)r * a.cs_ss + i;
-  const floatx4 k0 = Vec4<float>::load(krow + i), k1 = Vec4<float>::load(krow + half + i);
-  const floatx4 v0 = Vec4<float>::load(vrow + i), v1 = Vec4<float>::load(vrow + half + i);
+  const typename Vec4<KT>::type k0 = Vec4<KT>::load(krow + i), k1 = Vec4<KT>::load(krow + half + i);
+  const typename Vec4<KT>::type v0 = Vec4<KT>::load(vrow + i), v1 = Vec4<KT>::load(vrow + half + i);
   const typename Vec4<T>::type cv = Vec4<T>::load(reinterpret_cast<const T*>(a.cs_cos) + cso);
   const typename Vec4<T>::type sv = Vec4<T>::load(reinterpret_cast<const T*>(a.cs_sin) + cso);
   float o0[4], o1[4], w0[4], w1[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const float c = Vec4<T>::get(cv, j), s = Vec4<T>::get(sv, j);
-    const float ka = to_f32(from_f32<T>(k0[j])), kb = to_f32(from_f32<T>(k1[j]));
+    const float ka = to_f32(from_f32<T>(Vec4<KT>::get(k0, j))), kb = to_f32(from_f32<T>(Vec4<KT>::get(k1, j)));
     // (k * cos) + (rotate_half(k) * sin), each op rounded to T
     const float a1 = to_f32(from_f32<T>(ka * c));
     const float a2 = to_f32(from_f32<T>((-kb) * s));
@@ -137,8 +140,8 @@ __global__ __launch_bounds__(256) void inject_rerope_tab_kernel(InjectTab a) {
     const float b2 = to_f32(from_f32<T>(ka * s));
     o0[j] = a1 + a2;
     o1[j] = b1 + b2;
-    w0[j] = v0[j];
-    w1[j] = v1[j];
+    w0[j] = Vec4<KT>::get(v0, j);
+    w1[j] = Vec4<KT>::get(v1, j);
   }
   T* kout = reinterpret_cast<T*>(a.kd) + b * a.kd_sb + h * a.kd_sh + (int64_t)r * a.kd_ss;
   T* vout = reinterpret_cast<T*>(a.vd) + b * a.vd_sb + h * a.vd_sh + (int64_t)r * a.vd_ss;
@@ -232,24 +235,26 @@ extern "C" int hc_retrieval_query(int dtype, int64_t B, int64_t Hq, int64_t Hk, 
   return HC_OK;
 }
 
-extern "C" int hc_inject_rerope_tab(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D, const float* k_pre,
-                                    int64_t kp_sb, int64_t kp_sh, int64_t kp_ss, const float* v, int64_t vp_sb,
-                                    int64_t vp_sh, int64_t vp_ss, const void* cos_t, const void* sin_t,
+extern "C" int hc_inject_rerope_tab(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D, int kv_dtype,
+                                    const void* k_pre, int64_t kp_sb, int64_t kp_sh, int64_t kp_ss, const void* v,
+                                    int64_t vp_sb, int64_t vp_sh, int64_t vp_ss, const void* cos_t, const void* sin_t,
                                     int64_t cs_sb, int64_t cs_sh, int64_t cs_ss, void* k_dst, int64_t kd_sb,
                                     int64_t kd_sh, int64_t kd_ss, void* v_dst, int64_t vd_sb, int64_t vd_sh,
                                     int64_t vd_ss, void* stream) {
   HC_REQUIRE(dtype == HC_DTYPE_F32 || dtype == HC_DTYPE_F16 || dtype == HC_DTYPE_BF16, "inject_tab: bad dtype %d",
              dtype);
+  HC_REQUIRE(kv_dtype == HC_DTYPE_F32 || kv_dtype == dtype,
+             "inject_tab: staged k_pre / v must be fp32 or the cache dtype (%d, cache %d)", kv_dtype, dtype);
   HC_REQUIRE(B > 0 && Hk > 0 && R >= 0 && D > 0, "inject_tab: bad shape");
   HC_REQUIRE(D % 8 == 0, "inject_tab: head_dim %lld must be a multiple of 8", (long long)D);
   if (R == 0) return HC_OK;
   HC_REQUIRE(k_pre && v && cos_t && sin_t && k_dst && v_dst, "inject_tab: null pointer");
-  const int es = dtype_size(dtype);
+  const int es = dtype_size(dtype), kes = dtype_size(kv_dtype);
   const auto al = [](const void* p, int n) { return ((uintptr_t)p % n) == 0; };
-  // 16-byte fp32 rows, 4-element (8- or 16-byte) table and output pieces
-  HC_REQUIRE(al(k_pre, 16) && al(v, 16) && kp_sb % 4 == 0 && kp_sh % 4 == 0 && kp_ss % 4 == 0 && vp_sb % 4 == 0 &&
-                 vp_sh % 4 == 0 && vp_ss % 4 == 0,
-             "inject_tab: staged k_pre / v rows must be 16-byte aligned");
+  // 4-element pieces of the staged rows, the tables and the outputs
+  HC_REQUIRE(al(k_pre, 4 * kes) && al(v, 4 * kes) && kp_sb % 4 == 0 && kp_sh % 4 == 0 && kp_ss % 4 == 0 &&
+                 vp_sb % 4 == 0 && vp_sh % 4 == 0 && vp_ss % 4 == 0,
+             "inject_tab: staged k_pre / v rows must be aligned to 4 elements");
   HC_REQUIRE(al(cos_t, 4 * es) && al(sin_t, 4 * es) && cs_sb % 4 == 0 && cs_sh % 4 == 0 && cs_ss % 4 == 0 &&
                  al(k_dst, 4 * es) && al(v_dst, 4 * es) && kd_sb % 4 == 0 && kd_sh % 4 == 0 && kd_ss % 4 == 0 &&
                  vd_sb % 4 == 0 && vd_sh % 4 == 0 && vd_ss % 4 == 0,
@@ -266,9 +271,16 @@ extern "C" int hc_inject_rerope_tab(int dtype, int64_t B, int64_t Hk, int64_t R,
   HC_REQUIRE(cdiv(threads, (int64_t)256) <= 0x7fffffff, "inject_tab: grid too large");
   const dim3 grid((unsigned)cdiv(threads, (int64_t)256));
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  if (dtype == HC_DTYPE_F16) hipLaunchKernelGGL(inject_rerope_tab_kernel<half_t>, grid, dim3(256), 0, st, a);
-  else if (dtype == HC_DTYPE_BF16) hipLaunchKernelGGL(inject_rerope_tab_kernel<bf16_t>, grid, dim3(256), 0, st, a);
-  else hipLaunchKernelGGL(inject_rerope_tab_kernel<float>, grid, dim3(256), 0, st, a);
+  const bool f32 = kv_dtype == HC_DTYPE_F32;
+  if (dtype == HC_DTYPE_F16) {
+    if (f32) hipLaunchKernelGGL((inject_rerope_tab_kernel<half_t, float>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((inject_rerope_tab_kernel<half_t, half_t>), grid, dim3(256), 0, st, a);
+  } else if (dtype == HC_DTYPE_BF16) {
+    if (f32) hipLaunchKernelGGL((inject_rerope_tab_kernel<bf16_t, float>), grid, dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((inject_rerope_tab_kernel<bf16_t, bf16_t>), grid, dim3(256), 0, st, a);
+  } else {
+    hipLaunchKernelGGL((inject_rerope_tab_kernel<float, float>), grid, dim3(256), 0, st, a);
+  }
   return check_launch("inject_rerope_tab");
 }
 

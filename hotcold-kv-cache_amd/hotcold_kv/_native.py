@@ -174,7 +174,7 @@ SIGNATURES = {
         _vp, _i64, _i64, _i64,
         _vp]),
     "hc_inject_rerope_tab": (_int, [
-        _int, _i64, _i64, _i64, _i64,
+        _int, _i64, _i64, _i64, _i64, _int,
         _vp, _i64, _i64, _i64,
         _vp, _i64, _i64, _i64,
         _vp, _vp, _i64, _i64, _i64,
@@ -202,14 +202,15 @@ SIGNATURES = {
     "hc_cold_add": (_int, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp]),
     "hc_cold_search": (_int, [_vp, _vp, _i64, _i64, _vp, _vp]),
     "hc_cold_export": (_int, [_vp, _vp, _vp, _vp, _vp]),
-    "hc_cold_retrieve": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _i64, _int, _vp, _vp, _vp, _vp,
+    "hc_cold_retrieve": (_int, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _i64, _int, _int, _vp, _vp, _vp, _vp,
                                 _vp, _i64, _i64, _vp, _vp, _i64]),
-    "hc_cold_retrieve_async": (_vp, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _i64, _int, _vp, _vp, _vp, _vp,
+    "hc_cold_retrieve_async": (_vp, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _i64, _int, _int, _vp, _vp, _vp, _vp,
                                      _vp, _i64, _i64, _vp, _i64, _vp, _i64]),
     "hc_cold_add_async": (_vp, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64]),
-    "hc_cold_gather": (_int, [_vp, _i64, _int, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64]),
-    "hc_cold_gather_async": (_vp, [_vp, _i64, _int, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64, _vp,
-                                   _i64]),
+    "hc_cold_gather": (_int, [_vp, _i64, _int, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp,
+                              _i64]),
+    "hc_cold_gather_async": (_vp, [_vp, _i64, _int, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64,
+                                   _vp, _i64]),
     "hc_cold_job_poll": (_int, [_vp, _int, _vp, _vp]),
     "hc_cold_job_free": (None, [_vp]),
     "hc_index_add": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),

@@ -711,8 +711,16 @@ class KVController:
         vh = Hk if self.per_head_retrieval else 1
         pshape = (B, Hk, R) if self.per_head_retrieval else (B, R)
         tshape = (B, vh, R, 2, D // 2)
-        return (((B, Hk, R, D), torch.float32), ((B, Hk, R, D), torch.float32), (pshape, torch.int64),
+        kv = self._kv_dtype()
+        return (((B, Hk, R, D), kv), ((B, Hk, R, D), kv), (pshape, torch.int64),
                 (pshape, torch.bool), (tshape, self.dtype), ((B, vh, D), torch.float32), ((B, vh, R), torch.int64))
+
+    def _kv_dtype(self):
+        """Element type of the staged k_pre / v: the cache dtype when it is
+        fp16 or bf16 (the reference moves retrieved rows to the model dtype
+        on their copy, controller.py:368-369; the native retrieval rounds
+        them the same way, so the copy carries half the bytes), else fp32."""
+        return self.dtype if self.dtype in (torch.float16, torch.bfloat16) else torch.float32
 
     def _take_slot(self, li):
         """A free slot of layer li whose last copy has completed (its host
@@ -782,7 +790,7 @@ class KVController:
         # computed
         tab = table is not None and self._rope is not None
         args = (self._store_ptrs[li], B, q_ptr, q_sb, q_sh, q_dim, norm, R, int(self.per_head_retrieval),
-                kpre.data_ptr(), vv.data_ptr(), pos.data_ptr(), valid.data_ptr(),
+                N.dtype_code(kpre.dtype), kpre.data_ptr(), vv.data_ptr(), pos.data_ptr(), valid.data_ptr(),
                 table.ctypes.data if tab else None, table.shape[0] if tab else 0, table.shape[1] if tab else 0,
                 slot.tab.data_ptr() if tab else None, int(nthreads))
         return args, (q, table), tab
@@ -944,7 +952,7 @@ class KVController:
         kpre, vv, pos, valid = slot.host
         handle = lib.hc_cold_gather_async(
             self._store_ptrs[li], self.B, int(self.per_head_retrieval), R, slot.hits_host.data_ptr(),
-            kpre.data_ptr(), vv.data_ptr(), pos.data_ptr(), valid.data_ptr(),
+            N.dtype_code(kpre.dtype), kpre.data_ptr(), vv.data_ptr(), pos.data_ptr(), valid.data_ptr(),
             table.ctypes.data if tab else None, table.shape[0] if tab else 0, table.shape[1] if tab else 0,
             slot.tab.data_ptr() if tab else None, self.SEARCH_THREADS, slot.hits_ready, self._search_workers())
         if not handle:

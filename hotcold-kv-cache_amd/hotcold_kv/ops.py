@@ -1095,15 +1095,19 @@ def rope_tables(pos, inv_freq, attention_scaling, dtype):
     return cos[..., :half], sin[..., :half]
 
 
-def inject_rerope_tab(k_pre_f32, v_f32, cos_t, sin_t, k_dst, v_dst):
+def inject_rerope_tab(k_pre, v_staged, cos_t, sin_t, k_dst, v_dst):
     """inject_rerope with the rotary tables supplied: cos_t / sin_t (B,R,D/2)
     (one table per batch row) or (B,Hk,R,D/2), in k_dst's dtype (rope_tables).
-    Writes the rotated keys and the values into rows 0..R-1 of k_dst / v_dst
-    (B,Hk,cap,D); the keys are apply_rotary_pos_emb's bits."""
-    _require_device(k_pre_f32, v_f32, cos_t, sin_t, k_dst, v_dst)
-    B, Hk, R, D = k_pre_f32.shape
-    if k_pre_f32.dtype != torch.float32 or v_f32.dtype != torch.float32:
-        raise RuntimeError("inject_rerope_tab: staged k_pre/v must be float32")
+    The staged k_pre / v (B,Hk,R,D) are float32 or already in k_dst's dtype
+    (the reference moves them to the model dtype before rotating,
+    controller.py:368-369).  Writes the rotated keys and the values into rows
+    0..R-1 of k_dst / v_dst (B,Hk,cap,D); the keys are apply_rotary_pos_emb's
+    bits."""
+    _require_device(k_pre, v_staged, cos_t, sin_t, k_dst, v_dst)
+    B, Hk, R, D = k_pre.shape
+    k_pre_f32, v_f32 = k_pre, v_staged
+    if k_pre.dtype != v_staged.dtype or k_pre.dtype not in (torch.float32, k_dst.dtype):
+        raise RuntimeError("inject_rerope_tab: staged k_pre/v must both be float32 or the cache dtype")
     if cos_t.dtype != k_dst.dtype or sin_t.dtype != k_dst.dtype or cos_t.shape != sin_t.shape \
             or cos_t.stride() != sin_t.stride():
         raise RuntimeError("inject_rerope_tab: cos/sin tables must share shape, strides and the cache dtype")
@@ -1122,7 +1126,7 @@ def inject_rerope_tab(k_pre_f32, v_f32, cos_t, sin_t, k_dst, v_dst):
     if tuple(v_f32.shape) != (B, Hk, R, D) or k_pre_f32.stride(-1) != 1 or v_f32.stride(-1) != 1:
         raise RuntimeError("inject_rerope_tab: staged k_pre/v must be (B,Hk,R,D) with unit last stride")
     rc = N.lib().hc_inject_rerope_tab(
-        N.dtype_code(k_dst.dtype), B, Hk, R, D,
+        N.dtype_code(k_dst.dtype), B, Hk, R, D, N.dtype_code(k_pre.dtype),
         _ptr(k_pre_f32), *_strides3(k_pre_f32),
         _ptr(v_f32), *_strides3(v_f32),
         _ptr(cos_t), _ptr(sin_t), cs_sb, cs_sh, cs_ss,

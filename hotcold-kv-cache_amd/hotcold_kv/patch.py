@@ -115,7 +115,7 @@ def hotcold_attention(kvctrl, layer, li, q_pre, k_pre, v, q_post, k_post, pos_ne
                 ops.inject_rerope_tab(rr.k_pre, rr.v, rr.cos, rr.sin, kbuf, vbuf)
             else:
                 inv, ascale = _rope_params(device)
-                ops.inject_rerope(rr.k_pre, rr.v, rr.pos, inv, ascale, kbuf, vbuf)
+                ops.inject_rerope(rr.k_pre.float(), rr.v.float(), rr.pos, inv, ascale, kbuf, vbuf)
             kvctrl.staged_consumed(li)
             injected = (rr.pos, rr.valid, R)
         held = kvctrl.resolve_held(li, injected)

@@ -458,11 +458,14 @@ int hc_inject_rerope(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D,
  * as [B][Hk or 1][R][D/2] in dtype with element strides (cs_sb, cs_sh, cs_ss);
  * cs_sh = 0 shares one table across the KV heads of a batch row.  With the
  * tables given, every written key is apply_rotary_pos_emb's bits
- * (patch.py:94-102).  Staged rows 16-byte aligned, D a multiple of 8.
+ * (patch.py:94-102).  The staged k_pre / v are kv_dtype: HC_DTYPE_F32, or the
+ * cache dtype itself (the reference moves them to the model dtype before the
+ * rotation, controller.py:368-369; the keys are rounded to it either way).
+ * Staged rows aligned to 4 elements, D a multiple of 8.
  */
-int hc_inject_rerope_tab(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D,
-                         const float* k_pre, int64_t kp_sb, int64_t kp_sh, int64_t kp_ss,
-                         const float* v, int64_t vp_sb, int64_t vp_sh, int64_t vp_ss,
+int hc_inject_rerope_tab(int dtype, int64_t B, int64_t Hk, int64_t R, int64_t D, int kv_dtype,
+                         const void* k_pre, int64_t kp_sb, int64_t kp_sh, int64_t kp_ss,
+                         const void* v, int64_t vp_sb, int64_t vp_sh, int64_t vp_ss,
                          const void* cos_t, const void* sin_t, int64_t cs_sb, int64_t cs_sh, int64_t cs_ss,
                          void* k_dst, int64_t kd_sb, int64_t kd_sh, int64_t kd_ss,
                          void* v_dst, int64_t vd_sb, int64_t vd_sh, int64_t vd_ss,
@@ -541,7 +544,10 @@ int hc_cold_export(const void* store, float* kpre, float* v, int64_t* pos, float
 /* Retrieval of R tokens per batch row (per_head = 0: query q[b] of store b's
  * head-mean vectors; outputs pos/valid [B][R]) or per (batch row, head)
  * (per_head = 1: q[b][h]; pos/valid [B][heads][R]).  kpre/v out are
- * [B][heads][R][head_dim]; rows past the hits are zero with valid = 0.  q has
+ * [B][heads][R][head_dim] of kv_dtype (HC_DTYPE_F32, or HC_DTYPE_F16 /
+ * HC_DTYPE_BF16: the stored fp32 values rounded to nearest even, as the
+ * reference's kpre_cpu.to(device, dtype) rounds them, controller.py:368-369);
+ * rows past the hits are zero with valid = 0.  q has
  * q_dim floats per query, element strides (q_sb, q_sh); it is cropped or
  * zero-padded to vec_dim and, with normalize_q, divided by max(||q||, 1e-12)
  * as the stored vectors are (squares summed in fp64 in dimension order,
@@ -553,9 +559,9 @@ int hc_cold_export(const void* store, float* kpre, float* v, int64_t* pos, float
  * positions (controller.py:365-373 re-rotates them).  nthreads <= 0 picks
  * min(cores, 16). */
 int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh, int64_t q_dim,
-                     int normalize_q, int64_t R, int per_head, float* kpre_out, float* v_out, int64_t* pos_out,
-                     uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes,
-                     uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads);
+                     int normalize_q, int64_t R, int per_head, int kv_dtype, void* kpre_out, void* v_out,
+                     int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows,
+                     int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads);
 /* hc_cold_retrieve as a job on the library's own worker threads, in place of
  * the reference's threading.Thread per search (controller.py:336-342).  Up to
  * `workers` threads (at most 16) are started on first use and kept until the
@@ -564,8 +570,8 @@ int hc_cold_retrieve(void* const* stores, int64_t B, const float* q, int64_t q_s
  * counts the valid rows.  The caller keeps every buffer alive until the job
  * is done.  Returns the job, or NULL on a bad argument (hc_last_error). */
 void* hc_cold_retrieve_async(void* const* stores, int64_t B, const float* q, int64_t q_sb, int64_t q_sh,
-                             int64_t q_dim, int normalize_q, int64_t R, int per_head, float* kpre_out,
-                             float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                             int64_t q_dim, int normalize_q, int64_t R, int per_head, int kv_dtype, void* kpre_out,
+                             void* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
                              int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t nthreads,
                              void* wait_event, int64_t workers);
 /* The rows of hits found by the device search index (hc_index_search): hits
@@ -573,17 +579,17 @@ void* hc_cold_retrieve_async(void* const* stores, int64_t B, const float* q, int
  * -1 past the hits.  Writes the outputs as hc_cold_retrieve does for the same
  * hits (kpre/v, pos/valid, table rows), after the adds submitted before it.
  * A hit beyond its store's tokens is HC_ERR_INVALID. */
-int hc_cold_gather(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits, float* kpre_out,
-                   float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab, int64_t tab_rows,
-                   int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing, int64_t nthreads);
-/* hc_cold_gather as a job on the worker threads: the worker first
- * synchronises on wait_event (the event behind the hits' device-to-host copy)
- * and waits for the adds submitted before the job.  Polled and freed like a
- * search job. */
+int hc_cold_gather(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits, int kv_dtype,
+                   void* kpre_out, void* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
+                   int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t* tab_missing,
+                   int64_t nthreads);
+/* hc_cold_gather as a job on the worker threads: the worker first waits for
+ * wait_event (the event behind the search that wrote the hits) and for the
+ * adds submitted before the job.  Polled and freed like a search job. */
 void* hc_cold_gather_async(void* const* stores, int64_t B, int per_head, int64_t R, const int64_t* hits,
-                           float* kpre_out, float* v_out, int64_t* pos_out, uint8_t* valid_out, const uint8_t* tab,
-                           int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out, int64_t nthreads,
-                           void* wait_event, int64_t workers);
+                           int kv_dtype, void* kpre_out, void* v_out, int64_t* pos_out, uint8_t* valid_out,
+                           const uint8_t* tab, int64_t tab_rows, int64_t tab_row_bytes, uint8_t* tab_out,
+                           int64_t nthreads, void* wait_event, int64_t workers);
 /* 0 while the job runs (wait = 0); 1 when it is done, with the number of
  * valid rows and of positions past the table (0 for an add); a negative
  * HC_ERR_* code if the job failed (its message in hc_last_error on the

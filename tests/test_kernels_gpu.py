@@ -817,6 +817,12 @@ def test_inject_rerope_tab_is_bit_exact(dtype, per_head):
     assert torch.equal(kd[:, :, :R].cpu(), ref.rerope(k_pre, pos, inv, 1.0, dtype))
     assert torch.equal(vd[:, :, :R].cpu(), v.to(dtype))
     assert torch.count_nonzero(kd[:, :, R:]) == 0 and torch.count_nonzero(vd[:, :, R:]) == 0
+    if dtype != torch.float32:
+        # rows staged in the cache dtype (as the reference's copy converts them) give the same bits
+        kd2, vd2 = torch.zeros_like(kd), torch.zeros_like(vd)
+        ops.inject_rerope_tab(k_pre.to(dtype).to(DEV), v.to(dtype).to(DEV), cos.reshape(shape).to(DEV),
+                              sin.reshape(shape).to(DEV), kd2, vd2)
+        assert torch.equal(kd2, kd) and torch.equal(vd2, vd)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])

@@ -599,7 +599,7 @@ def test_gathering_given_hits_equals_the_native_retrieval(per_head):
 
     want, got = outputs(), outputs()
     miss_w, miss_g = ctypes.c_int64(), ctypes.c_int64()
-    N.check(lib.hc_cold_retrieve(stores, B, q.ctypes.data, VH * Dd, Dd, Dd, 1, R, int(per_head),
+    N.check(lib.hc_cold_retrieve(stores, B, q.ctypes.data, VH * Dd, Dd, Dd, 1, R, int(per_head), N.HC_DTYPE_F32,
                                  *[x.ctypes.data for x in want[:4]], tab.ctypes.data, 400, 12, want[4].ctypes.data,
                                  ctypes.byref(miss_w), 2), "hc_cold_retrieve")
     hits = np.full((B, VH, R), -1, np.int64)
@@ -611,26 +611,68 @@ def test_gathering_given_hits_equals_the_native_retrieval(per_head):
                 ss += e * e
             found = rings[b].search((x / max(ss ** 0.5, 1e-12)).astype(np.float32), R, head=h)
             hits[b, h, :len(found)] = found
-    N.check(lib.hc_cold_gather(stores, B, int(per_head), R, hits.ctypes.data, *[x.ctypes.data for x in got[:4]],
-                               tab.ctypes.data, 400, 12, got[4].ctypes.data, ctypes.byref(miss_g), 2), "hc_cold_gather")
+    N.check(lib.hc_cold_gather(stores, B, int(per_head), R, hits.ctypes.data, N.HC_DTYPE_F32,
+                               *[x.ctypes.data for x in got[:4]], tab.ctypes.data, 400, 12, got[4].ctypes.data,
+                               ctypes.byref(miss_g), 2), "hc_cold_gather")
     for a, b_ in zip(want, got):
         assert np.array_equal(a, b_)
     assert miss_w.value == miss_g.value
     # a hit beyond a store's tokens is refused
     bad = hits.copy()
     bad[1, 0, 0] = 40
-    assert lib.hc_cold_gather(stores, B, int(per_head), R, bad.ctypes.data, *[x.ctypes.data for x in got[:4]],
-                              None, 0, 0, None, None, 1) == N.HC_ERR_INVALID
+    assert lib.hc_cold_gather(stores, B, int(per_head), R, bad.ctypes.data, N.HC_DTYPE_F32,
+                              *[x.ctypes.data for x in got[:4]], None, 0, 0, None, None, 1) == N.HC_ERR_INVALID
     # the job form after async adds: it waits for them
     more = rng.standard_normal((H, 20, Dd), dtype=np.float32)
     adds = [rings[1].add_async(more, more, np.arange(20), nthreads=1, workers=2)]
     hits2 = hits.copy()
     hits2[1, :, :] = np.arange(R)                             # store 1 now holds 25 tokens
-    job = lib.hc_cold_gather_async(stores, B, int(per_head), R, hits2.ctypes.data, *[x.ctypes.data for x in got[:4]],
-                                   None, 0, 0, None, 1, None, 2)
+    job = lib.hc_cold_gather_async(stores, B, int(per_head), R, hits2.ctypes.data, N.HC_DTYPE_F32,
+                                   *[x.ctypes.data for x in got[:4]], None, 0, 0, None, 1, None, 2)
     nv = ctypes.c_int64()
     assert lib.hc_cold_job_poll(job, 1, ctypes.byref(nv), None) == 1
     lib.hc_cold_job_free(job)
     assert got[3][1].all() and nv.value == int((hits2 >= 0).sum()) * 1
     for j in adds:
         assert j.poll(wait=True) and j.error is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_retrieved_rows_in_the_cache_dtype_round_as_torch_does(dtype):
+    """A retrieval written in fp16 / bf16 (the staged rows the copy carries)
+    equals torch's conversion of the same rows written in fp32 -- the
+    reference's kpre_cpu.to(device, dtype) (controller.py:368-369): round to
+    nearest even at exact midpoints, subnormal results, overflow to inf,
+    signed zeros and infinities."""
+    import ctypes
+
+    import numpy as np
+
+    from hotcold_kv import _native as N
+    from hotcold_kv.controller import _Ring
+    Dd, H, n = 16, 2, 24
+    rng = np.random.default_rng(3)
+    vals = [1 + 2 ** -11, 1 + 3 * 2 ** -11, 1 + 2 ** -8, 1 + 3 * 2 ** -8, -(1 + 2 ** -11), 3e-6, 1e-7, 6.1e-5,
+            65519.0, 65520.0, 70000.0, 3.39e38, 3.4e38, -0.0, float("inf"), float("-inf"), 2 ** -126, 1e-40]
+    kpre = (rng.standard_normal((H, n, Dd)) * 10.0 ** rng.integers(-9, 6, (H, n, Dd))).astype(np.float32)
+    kpre.reshape(-1)[:len(vals)] = np.array(vals, dtype=np.float32)
+    v = (rng.standard_normal((H, n, Dd)) * 1e3).astype(np.float32)
+    ring = _Ring(32, H, Dd, Dd, H)
+    ring.add(kpre, v, np.arange(n, dtype=np.int64), np.arange(n, dtype=np.int64))
+    stores = (ctypes.c_void_p * 1)(ring.handle)
+    hits = np.tile(np.arange(n, dtype=np.int64), (1, H, 1))
+    lib = N.lib()
+
+    def gather(code, np_dtype):
+        k = np.zeros((1, H, n, Dd), np_dtype)
+        vv = np.zeros((1, H, n, Dd), np_dtype)
+        pos, valid = np.zeros((1, H, n), np.int64), np.zeros((1, H, n), np.uint8)
+        N.check(lib.hc_cold_gather(stores, 1, 1, n, hits.ctypes.data, code, k.ctypes.data, vv.ctypes.data,
+                                   pos.ctypes.data, valid.ctypes.data, None, 0, 0, None, None, 1), "hc_cold_gather")
+        return k, vv
+
+    k32, v32 = gather(N.HC_DTYPE_F32, np.float32)
+    k16, v16 = gather(N.dtype_code(dtype), np.uint16)
+    for w32, w16 in ((k32, k16), (v32, v16)):
+        want = torch.from_numpy(w32).to(dtype).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(w16, want)
