@@ -605,9 +605,14 @@ def measure_device_search(w, dev, st, flush, g, reps=12):
     """One layer's device search index at the workload's cold-store size:
     every sequence's evicted prompt tokens (seq_len - budget of them, N(0,1)
     pre-RoPE keys) added per KV head, then the top-held search per (sequence,
-    KV head) timed differentially (hc_index_search: the scoring kernel and
-    the select kernel).  Algorithmic bytes: the fp32 vectors read once, the
-    order keys written and read once."""
+    KV head) timed differentially (hc_index_search), both ways it runs:
+      search_us        the fp16 pass (fp16 copy scored in fp32, then the
+                       candidates it cannot rule out scored exactly); bytes:
+                       the fp16 vectors read once, 4-byte keys written and
+                       read once (the candidates' exact reads are ~R rows);
+      search_exact_us  the exact fp64 scan alone; bytes: the fp32 vectors
+                       read once, 8-byte keys written and read once.
+    Both give the same hits (tests/test_kernels_gpu.py)."""
     import numpy as np
     import torch
     from hotcold_kv.device_index import DeviceIndex
@@ -622,11 +627,19 @@ def measure_device_search(w, dev, st, flush, g, reps=12):
         hits = torch.empty((B, Hk, R), dtype=torch.int64, device=dev)
     del kpre
     ms = differential_ms(st, flush, lambda i: dix.search(q, R, hits, stream=st.cuda_stream), reps)
-    nbytes = B * Hk * n * (4 * D + 16)
+    ms_exact = differential_ms(st, flush, lambda i: dix.search(q, R, hits, stream=st.cuda_stream, pass16=False),
+                               reps)
+    fp16 = dix.vec16 is not None
+    nbytes = B * Hk * n * ((2 * D + 8) if fp16 else (4 * D + 16))
+    nbytes_exact = B * Hk * n * (4 * D + 16)
     gbs = nbytes / (ms * 1e-3) / 1e9
+    gbs_exact = nbytes_exact / (ms_exact * 1e-3) / 1e9
     return {"tokens_per_store": n, "stores": B, "vector_heads": Hk, "vector_dim": D, "top": R,
+            "path": "fp16 pass + exact re-score" if fp16 else "exact scan",
             "search_us": round(ms * 1e3, 1), "bytes": int(nbytes), "achieved_GBps": round(gbs, 1),
-            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+            "frac": round(gbs / HBM_PEAK_GBS, 4),
+            "search_exact_us": round(ms_exact * 1e3, 1), "bytes_exact": int(nbytes_exact),
+            "frac_exact": round(gbs_exact / HBM_PEAK_GBS, 4)}
 
 
 def cpu_baseline_config(w, q_win, k, v, decode_sample=8, max_batch=16):

@@ -213,9 +213,10 @@ SIGNATURES = {
                                    _vp, _i64]),
     "hc_cold_job_poll": (_int, [_vp, _int, _vp, _vp]),
     "hc_cold_job_free": (None, [_vp]),
-    "hc_index_add": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _i64, _vp]),
-    "hc_index_search": (_int, [_i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp, _i64, _vp, _vp, _i64, _vp,
-                                _vp, _vp, _vp, _vp, _vp]),
+    "hc_index_add": (_int, [_i64, _i64, _i64, _i64, _i64, _int, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64,
+                             _vp]),
+    "hc_index_search": (_int, [_i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp, _vp, _int, _i64, _vp, _vp,
+                                _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
     "hc_retrieval_query": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp, _vp, _vp, _vp]),
 }
 

@@ -396,7 +396,7 @@ class KVController:
         cpu_buffer_size) and the search stream, or none at all when they do
         not fit the device's memory or the search kernel's limits."""
         vh = self.Hk if self.per_head_retrieval else 1
-        if self.B > 64 or self.faiss_dim > 1024 or self.lookahead_k > 1024:
+        if self.B > 64 or self.faiss_dim > 1024 or self.faiss_dim % 4 or self.lookahead_k > 1024:
             return
         try:
             self._dindex = [DeviceIndex(self.B, self.Hk, self.D, self.faiss_dim, vh, self.cpu_buffer_size,

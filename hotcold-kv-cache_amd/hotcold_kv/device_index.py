@@ -26,27 +26,39 @@ from . import _native as N
 
 class DeviceIndex:
     """Search vectors of B cold stores (one layer), capacity cap each, in HBM:
-    vec [B][VH][capT/64][VD][64] fp32 (tiles of 64 slots), VH = 1 (head
-    mean) or H (per KV head)."""
+    vec [B][VH][capT/64][VD/4][64][4] fp32 (tiles of 64 slots, VD a
+    multiple of 4), VH = 1 (head mean) or H (per KV head).  With unit vectors (normalize) and VD a
+    multiple of 8 it also keeps them rounded to fp16 (vec16), and a search
+    with a normalised query first scans that copy, then scores exactly only
+    the slots the fp16 scores cannot rule out (pass16=False: exact scan
+    only).  The hits are the same either way."""
 
-    def __init__(self, B, H, D, VD, VH, cap, device, normalize=True):
+    def __init__(self, B, H, D, VD, VH, cap, device, normalize=True, pass16=True):
         if VH not in (1, H):
             raise ValueError("DeviceIndex: VH must be 1 or H")
+        if VD % 4:
+            raise ValueError("DeviceIndex: the vector width must be a multiple of 4")
         self.B, self.H, self.D, self.VD, self.VH, self.cap = int(B), int(H), int(D), int(VD), int(VH), int(cap)
         self.normalize = bool(normalize)
         self.device = torch.device(device)
         if self.device.type == "cuda" and self.device.index is None:
             self.device = torch.device("cuda", torch.cuda.current_device())
         self.capT = (self.cap + 63) // 64 * 64
-        self.vec = torch.empty((self.B, self.VH, self.capT // 64, self.VD, 64), dtype=torch.float32,
+        self.vec = torch.empty((self.B, self.VH, self.capT // 64, self.VD // 4, 64, 4), dtype=torch.float32,
                                device=self.device)
         self.keys = torch.empty((self.B, self.VH, self.capT), dtype=torch.int64, device=self.device)
+        self.vec16 = self.keys32 = None
+        if pass16 and self.normalize and self.VD % 8 == 0:
+            self.vec16 = torch.empty((self.B, self.VH, self.capT // 64, self.VD // 8, 64, 8), dtype=torch.float16,
+                                     device=self.device)
+            self.keys32 = torch.empty((self.B, self.VH, self.capT), dtype=torch.int32, device=self.device)
         self.size = np.zeros(self.B, dtype=np.int64)
         self.head = np.zeros(self.B, dtype=np.int64)
         self._lib = N.lib()
 
     def nbytes(self):
-        return self.vec.numel() * 4 + self.keys.numel() * 8
+        extra = 0 if self.vec16 is None else self.vec16.numel() * 2 + self.keys32.numel() * 4
+        return self.vec.numel() * 4 + self.keys.numel() * 8 + extra
 
     def _slots(self, idx):
         """Physical slots (B, te) int32 for the tokens of idx (B, te) (>= 0:
@@ -88,15 +100,18 @@ class DeviceIndex:
         st = stream if stream is not None else torch.cuda.current_stream(self.device).cuda_stream
         N.check(self._lib.hc_index_add(self.B, self.H, self.D, self.VH, self.VD, int(self.normalize),
                                        kpre.data_ptr(), ks[0], ks[1], ks[2], te, slot_of.data_ptr(),
-                                       self.vec.data_ptr(), self.capT, st), "hc_index_add")
+                                       self.vec.data_ptr(), None if self.vec16 is None else self.vec16.data_ptr(),
+                                       self.capT, st), "hc_index_add")
         self._slot_of = slot_of            # kept until the launch has run (the next add replaces it)
 
-    def search(self, q, R, hits, normalize_q=True, stream=None, hits_host=None, wait_event=None, done_event=None):
+    def search(self, q, R, hits, normalize_q=True, stream=None, hits_host=None, wait_event=None, done_event=None,
+               pass16=True):
         """Top-R logical indices per (row, head) for queries q (B,VH,q_dim)
         fp32 on the device, into hits (B,VH,R) int64 on the device (-1 past
         each row's size); on `stream` (default: the current stream), after
         wait_event if given.  hits_host (pinned, like hits): the kernel
-        writes the hits there too; done_event is recorded behind it."""
+        writes the hits there too; done_event is recorded behind it.
+        pass16=False: the exact scan even where the fp16 pass applies."""
         if q.dtype != torch.float32 or q.dim() != 3 or q.shape[0] != self.B or q.shape[1] != self.VH \
                 or q.stride(2) != 1 or q.device != self.device:
             raise RuntimeError("DeviceIndex.search: q must be (B,VH,q_dim) fp32 on the index's device")
@@ -109,16 +124,19 @@ class DeviceIndex:
         sizes = np.ascontiguousarray(self.size, dtype=np.int64)
         heads = np.ascontiguousarray(self.head, dtype=np.int64)
         qs = q.stride()
+        v16 = self.vec16 if pass16 else None
         N.check(self._lib.hc_index_search(self.B, self.VH, self.VD, self.cap, q.data_ptr(), qs[0], qs[1],
-                                          int(q.shape[2]), int(bool(normalize_q)), self.vec.data_ptr(), self.capT,
+                                          int(q.shape[2]), int(bool(normalize_q)), self.vec.data_ptr(),
+                                          None if v16 is None else v16.data_ptr(), int(self.normalize), self.capT,
                                           sizes.ctypes.data, heads.ctypes.data, int(R), self.keys.data_ptr(),
-                                          hits.data_ptr(), None if hits_host is None else hits_host.data_ptr(),
+                                          None if v16 is None else self.keys32.data_ptr(), hits.data_ptr(),
+                                          None if hits_host is None else hits_host.data_ptr(),
                                           wait_event, done_event, st), "hc_index_search")
         return hits
 
     def vectors(self, b):
         """Row b's vectors as (VH, VD, capT), slot-indexed (a view over the tiles)."""
-        return self.vec[b].permute(0, 2, 1, 3).reshape(self.VH, self.VD, self.capT)
+        return self.vec[b].permute(0, 2, 4, 1, 3).reshape(self.VH, self.VD, self.capT)
 
     def physical(self, b, logical):
         """Physical slot of logical index `logical` of row b."""

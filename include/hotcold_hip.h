@@ -601,8 +601,9 @@ void hc_cold_job_free(void* job);
 
 /*
  * Device search index of the cold stores of one layer: the search vectors of
- * B stores kept in HBM as vec [B][VH][capT/64][VD][64] fp32 (tiles of 64
- * slots; capT >= the stores' capacity, a multiple of 64), with the same
+ * B stores kept in HBM as vec [B][VH][capT/64][VD/4][64][4] fp32 (tiles of 64
+ * slots, VD a multiple of 4; capT >= the stores' capacity, a multiple of 64),
+ * with the same
  * arithmetic as hc_cold_add / hc_cold_search, so the
  * hits are the host store's, bit for bit.  It replaces the reference's CPU
  * faiss.IndexFlatIP scan (controller.py:223-232, 274-293) where a host scan
@@ -614,10 +615,12 @@ void hc_cold_job_free(void* job);
  * into the physical slots slot_of[b][t] (int32 on the device; < 0: not
  * stored), as hc_cold_add would place them: the head mean (VH = 1) or each
  * head (VH = H), cropped or zero-padded to VD, normalised when normalize.
+ * vec16 (may be NULL; VD a multiple of 8): the same vectors rounded to fp16,
+ * [B][VH][capT/64][VD/8][64][8], for the search's fp16 pass.
  */
 int hc_index_add(int64_t B, int64_t H, int64_t D, int64_t VH, int64_t VD, int normalize,
                  const float* kpre, int64_t k_sb, int64_t k_sh, int64_t k_st, int64_t te,
-                 const int32_t* slot_of, float* vec, int64_t capT, void* stream);
+                 const int32_t* slot_of, float* vec, void* vec16, int64_t capT, void* stream);
 /*
  * hc_index_search: for every row b < B (B <= 64) and head h < VH, the query
  * q[b*q_sb + h*q_sh .. + q_dim) (fp32 on the device; cropped or zero-padded to
@@ -627,16 +630,21 @@ int hc_index_add(int64_t B, int64_t H, int64_t D, int64_t VH, int64_t VD, int no
  * top R <= 1024 logical indices (oldest token = 0) in rank order -- inner
  * product descending, ties to the older token -- to hits [B][VH][R] (int64 on
  * the device), -1 past min(R, size).  keys: device scratch of B*VH*capT
- * uint64.  On `stream`, optionally (NULL skips each): first wait for
+ * uint64.  With vec16 and keys32 (B*VH*capT uint32 scratch) given, unit
+ * vectors (vec_normalized) and a normalised query, the search first scores
+ * the fp16 copy in fp32, then scores exactly only the slots within twice the
+ * bound of the two scores' difference of that pass's R-th score (a superset
+ * of the exact top R, ties included): the same hits, about half the bytes.  On `stream`, optionally (NULL skips each): first wait for
  * wait_event (the query's producer); write the hits to hits_host as well
  * (pinned host memory, B*VH*R int64, written by the kernel through its device
  * mapping, so they are on the host once the kernel is done; anything else is
  * HC_ERR_INVALID); record done_event behind the kernels.
  */
 int hc_index_search(int64_t B, int64_t VH, int64_t VD, int64_t cap, const float* q, int64_t q_sb, int64_t q_sh,
-                    int64_t q_dim, int normalize_q, const float* vec, int64_t capT, const int64_t* sizes,
-                    const int64_t* heads, int64_t R, uint64_t* keys, int64_t* hits, int64_t* hits_host,
-                    void* wait_event, void* done_event, void* stream);
+                    int64_t q_dim, int normalize_q, const float* vec, const void* vec16, int vec_normalized,
+                    int64_t capT, const int64_t* sizes, const int64_t* heads, int64_t R, uint64_t* keys,
+                    uint32_t* keys32, int64_t* hits, int64_t* hits_host, void* wait_event, void* done_event,
+                    void* stream);
 
 #ifdef __cplusplus
 }

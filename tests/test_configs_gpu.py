@@ -9,6 +9,7 @@ steps of the model's rotation.
 """
 
 import concurrent.futures
+import math
 import os
 
 import numpy as np
@@ -281,3 +282,47 @@ def test_pipeline_16k_compaction_then_decode_matches_oracle():
         out = ops.decode_attention(tok["q_post"].to(DEV), kk, vv, w.scaling).float().cpu().numpy()
         want = ref.decode_attention(tok["q_post"], rk, rv, w.scaling)
         assert np.abs(out - want).max() <= TOL[w.dtype], t
+
+
+def test_device_search_at_32k_x16_equals_the_host_store():
+    """The device search index at the 32k x 16 workload's size: 16 stores of
+    30 720 evicted tokens, one 128-float vector per KV head, top-128 per
+    (sequence, KV head).  The hits of three sequences are compared with their
+    host stores' exact search (itself pinned by the oracle) for the
+    workload's pooled-query-like queries: a stored key's direction, and
+    random ones."""
+    from hotcold_kv.controller import _Ring
+    from hotcold_kv.device_index import DeviceIndex
+
+    w = synthetic.WORKLOADS["b16_32k_b2048_held128"]
+    B, Hk, D, R = w.batch, w.hk, w.head_dim, w.held
+    n = w.seq_len - w.budget
+    print(f"[case] {w.name}: device index {B} x {Hk} x {n}, top-{R}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(17)
+    kpre = torch.randn((B, Hk, n, D), generator=g, device=DEV, dtype=torch.float32)
+    dix = DeviceIndex(B, Hk, D, D, Hk, w.seq_len, DEV)
+    dix.add(kpre, np.tile(np.arange(n, dtype=np.int64), (B, 1)))
+    rows = (0, 7, 15)
+    rings = {}
+    for b in rows:
+        k_b = kpre[b].cpu().numpy()
+        rings[b] = _Ring(w.seq_len, Hk, D, D, Hk)
+        rings[b].add(k_b, k_b, np.arange(n, dtype=np.int64), np.arange(n, dtype=np.int64))
+    hits = torch.empty((B, Hk, R), dtype=torch.int64, device=DEV)
+    for trial in range(3):
+        q = torch.randn((B, Hk, D), generator=g, device=DEV, dtype=torch.float32)
+        if trial == 0:
+            q = kpre[:, :, 1234].clone()            # a stored key's direction ranks it first
+        dix.search(q, R, hits)
+        got = hits.cpu().numpy()
+        qc = q.cpu().numpy()
+        for b in rows:
+            for h in range(Hk):
+                x = qc[b, h].astype(np.float64)
+                ss = 0.0
+                for e in x:
+                    ss += e * e
+                want = rings[b].search((x / max(math.sqrt(ss), 1e-12)).astype(np.float32), R, head=h)
+                assert np.array_equal(got[b, h], want), (trial, b, h)
+                if trial == 0:
+                    assert want[0] == 1234

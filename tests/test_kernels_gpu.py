@@ -1037,6 +1037,35 @@ def test_device_index_selection_with_many_ties(copies, R):
             assert np.array_equal(got[b, 0, :len(want)], want), b
             assert (got[b, 0, len(want):] == -1).all()
 
+@pytest.mark.parametrize("R", [16, 64, 512])
+def test_device_index_fp16_pass_equals_the_exact_scan(R):
+    """The fp16 pass (fp32 scores of the fp16 copy, then exact scores of the
+    slots within twice the error bound of its R-th score) returns the exact
+    scan's hits, also where the top of the ranking is crowded with
+    near-duplicates closer than fp16 can tell apart (relative differences of
+    1e-6), where ties are exact, and where more candidates than the pass
+    re-scores survive (then the exact selection runs)."""
+    from hotcold_kv.device_index import DeviceIndex
+    B, H, D, cap, te = 2, 4, 128, 3000, 3500
+    rng = np.random.default_rng(R)
+    kpre = rng.standard_normal((B, H, te, D), dtype=np.float32)
+    base = rng.standard_normal((B, H, D), dtype=np.float32)
+    near = rng.choice(np.arange(600, te), size=300, replace=False)
+    kpre[:, :, near] = base[:, :, None, :] * (1 + 1e-6 * rng.standard_normal((B, H, 300, D))).astype(np.float32)
+    dup = rng.choice(np.setdiff1d(np.arange(600, te), near), size=2500 if R == 512 else 40, replace=False)
+    kpre[1, :, dup] = kpre[1, :, dup[:1]]                     # exact duplicates in row 1
+    dix = DeviceIndex(B, H, D, D, H, cap, DEV)
+    assert dix.vec16 is not None
+    dix.add(torch.from_numpy(kpre).to(DEV), np.tile(np.arange(te, dtype=np.int64), (B, 1)))
+    h16 = torch.empty((B, H, R), dtype=torch.int64, device=DEV)
+    h64 = torch.empty_like(h16)
+    queries = [base, kpre[:, :, dup[0]], rng.standard_normal((B, H, D), dtype=np.float32)]
+    for i, q in enumerate(queries):
+        qd = torch.from_numpy(np.ascontiguousarray(q)).to(DEV)
+        dix.search(qd, R, h16)
+        dix.search(qd, R, h64, pass16=False)
+        assert torch.equal(h16, h64), i
+
 @pytest.mark.parametrize("per_head,faiss_dim", [(False, 32), (True, 64), (True, 96)])
 def test_scheduled_device_search_equals_the_host_search(per_head, faiss_dim):
     """Two controllers fed the same staged evictions (gather_evict into an
