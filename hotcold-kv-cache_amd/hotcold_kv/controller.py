@@ -184,6 +184,7 @@ class _Job:
     def __init__(self, handle, slot, has_tab, keep, by_hits=False):
         self.handle, self.slot, self.has_tab, self.keep = handle, slot, has_tab, keep
         self.by_hits = by_hits      # a gather of device-ranked hits (hc_cold_gather_async)
+        self._lib = N.lib()         # held: __del__ may run after module teardown
         self.result = None          # (n_valid, positions past the table) once done
         self.error = None           # (status, message) if the search failed
 
@@ -191,7 +192,7 @@ class _Job:
         """True once the search is done (or failed: see error)."""
         if self.result is None:
             nv, miss = ctypes.c_int64(0), ctypes.c_int64(0)
-            lib = N.lib()
+            lib = self._lib
             rc = lib.hc_cold_job_poll(self.handle, int(wait), ctypes.byref(nv), ctypes.byref(miss))
             if rc == 0:
                 return False
@@ -211,7 +212,7 @@ class _Job:
     def __del__(self):
         h, self.handle = getattr(self, "handle", None), None
         if h:
-            N.lib().hc_cold_job_free(h)       # waits for the worker to finish with the buffers
+            self._lib.hc_cold_job_free(h)     # waits for the worker to finish with the buffers
 
 
 _NOT_READY = RetrievedKV(k_pre=torch.empty(0), v=torch.empty(0), pos=torch.empty(0, dtype=torch.long),
@@ -393,14 +394,21 @@ class KVController:
 
     def _create_device_indexes(self):
         """One DeviceIndex per layer (vectors of every row's store, capacity
-        cpu_buffer_size) and the search stream, or none at all when they do
-        not fit the device's memory or the search kernel's limits."""
+        cpu_buffer_size, fp32 and an fp16 copy: 6 bytes per dimension per
+        slot) with one key scratch for all (12 bytes per slot), and the
+        search stream; or none at all when they do not fit the device's
+        memory or the search kernels' limits."""
         vh = self.Hk if self.per_head_retrieval else 1
         if self.B > 64 or self.faiss_dim > 1024 or self.faiss_dim % 4 or self.lookahead_k > 1024:
             return
         try:
+            # every search runs on the one search stream, so the layers share
+            # one key scratch
+            capT = (self.cpu_buffer_size + 63) // 64 * 64
+            scratch = DeviceIndex.scratch_for(self.B, vh, capT, self._device)
             self._dindex = [DeviceIndex(self.B, self.Hk, self.D, self.faiss_dim, vh, self.cpu_buffer_size,
-                                        self._device, self.normalize_for_ip) for _ in range(self.n_layers)]
+                                        self._device, self.normalize_for_ip, scratch=scratch)
+                            for _ in range(self.n_layers)]
         except torch.OutOfMemoryError:
             self._dindex = [None] * self.n_layers
             return

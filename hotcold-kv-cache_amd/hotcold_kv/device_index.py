@@ -33,7 +33,7 @@ class DeviceIndex:
     the slots the fp16 scores cannot rule out (pass16=False: exact scan
     only).  The hits are the same either way."""
 
-    def __init__(self, B, H, D, VD, VH, cap, device, normalize=True, pass16=True):
+    def __init__(self, B, H, D, VD, VH, cap, device, normalize=True, pass16=True, scratch=None):
         if VH not in (1, H):
             raise ValueError("DeviceIndex: VH must be 1 or H")
         if VD % 4:
@@ -46,19 +46,30 @@ class DeviceIndex:
         self.capT = (self.cap + 63) // 64 * 64
         self.vec = torch.empty((self.B, self.VH, self.capT // 64, self.VD // 4, 64, 4), dtype=torch.float32,
                                device=self.device)
-        self.keys = torch.empty((self.B, self.VH, self.capT), dtype=torch.int64, device=self.device)
-        self.vec16 = self.keys32 = None
+        self.vec16 = None
         if pass16 and self.normalize and self.VD % 8 == 0:
             self.vec16 = torch.empty((self.B, self.VH, self.capT // 64, self.VD // 8, 64, 8), dtype=torch.float16,
                                      device=self.device)
-            self.keys32 = torch.empty((self.B, self.VH, self.capT), dtype=torch.int32, device=self.device)
+        # the searches' key scratch: B*VH*capT 8-byte and 4-byte keys.  Indexes
+        # whose searches are ordered on one stream may share one (scratch_for)
+        self.keys, self.keys32 = scratch if scratch is not None else self.scratch_for(self.B, self.VH, self.capT,
+                                                                                      self.device)
+        if self.keys.numel() < self.B * self.VH * self.capT or self.keys32.numel() < self.B * self.VH * self.capT:
+            raise ValueError("DeviceIndex: the shared key scratch is too small")
         self.size = np.zeros(self.B, dtype=np.int64)
         self.head = np.zeros(self.B, dtype=np.int64)
         self._lib = N.lib()
 
+    @staticmethod
+    def scratch_for(B, VH, capT, device):
+        """Key scratch for searches of B*VH planes of capT slots."""
+        n = int(B) * int(VH) * int(capT)
+        return (torch.empty((n,), dtype=torch.int64, device=device),
+                torch.empty((n,), dtype=torch.int32, device=device))
+
     def nbytes(self):
-        extra = 0 if self.vec16 is None else self.vec16.numel() * 2 + self.keys32.numel() * 4
-        return self.vec.numel() * 4 + self.keys.numel() * 8 + extra
+        """Bytes of the vectors (fp32 and the fp16 copy), without the key scratch."""
+        return self.vec.numel() * 4 + (0 if self.vec16 is None else self.vec16.numel() * 2)
 
     def _slots(self, idx):
         """Physical slots (B, te) int32 for the tokens of idx (B, te) (>= 0:

@@ -676,3 +676,47 @@ def test_retrieved_rows_in_the_cache_dtype_round_as_torch_does(dtype):
     for w32, w16 in ((k32, k16), (v32, v16)):
         want = torch.from_numpy(w32).to(dtype).view(torch.int16).numpy().view(np.uint16)
         assert np.array_equal(w16, want)
+
+
+def test_device_index_ring_mirrors_the_host_store():
+    """DeviceIndex's slot assignment (host bookkeeping, no kernel): after adds
+    that wrap the ring, rows with padding and a row that skips an add, the
+    token at logical index l of each row sits in physical slot
+    physical(b, l), and the sizes equal the host stores'.  The key scratch
+    can be shared between indexes and is checked for size."""
+    import numpy as np
+
+    from hotcold_kv.controller import _Ring
+    from hotcold_kv.device_index import DeviceIndex
+    B, H, D, cap = 3, 2, 8, 50
+    dix = DeviceIndex(B, H, D, D, H, cap, "cpu")
+    assert dix.capT == 64 and dix.vec16 is not None and dix.keys.numel() == B * H * 64
+    rings = [_Ring(cap, H, D, D, H) for _ in range(B)]
+    where = [dict() for _ in range(B)]            # token id -> physical slot
+    order = [[] for _ in range(B)]                # token ids, oldest first
+    tok = 0
+    rng = np.random.default_rng(1)
+    for te in (20, 45, 7, 60, 33):
+        idx = np.tile(np.arange(te, dtype=np.int64), (B, 1))
+        idx[0, ::4] = -1
+        if te == 7:
+            idx[2, :] = -1
+        slot_of = dix._slots(idx)
+        for b in range(B):
+            kept = np.nonzero(idx[b] >= 0)[0]
+            k = rng.standard_normal((H, te, D), dtype=np.float32)
+            rings[b].add(k, k, np.arange(te, dtype=np.int64), idx[b])
+            for j in kept[-cap:]:
+                where[b][tok + j] = int(slot_of[b, j])
+                order[b].append(tok + j)
+            order[b] = order[b][-cap:]
+            assert (slot_of[b][idx[b] < 0] == -1).all()
+        tok += te
+    for b in range(B):
+        assert int(dix.size[b]) == len(rings[b]) == len(order[b])
+        for l, t in enumerate(order[b]):
+            assert dix.physical(b, l) == where[b][t], (b, l)
+    other = DeviceIndex(B, H, D, D, H, cap, "cpu", scratch=(dix.keys, dix.keys32))
+    assert other.keys.data_ptr() == dix.keys.data_ptr()
+    with pytest.raises(ValueError):
+        DeviceIndex(B, H, D, D, H, 2 * cap, "cpu", scratch=(dix.keys, dix.keys32))
