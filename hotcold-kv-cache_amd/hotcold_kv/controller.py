@@ -256,6 +256,10 @@ class KVController:
     # was still running; with 6, 0-3.
     SEARCH_THREADS = 2
     MAX_SEARCH_WORKERS = 6
+    # The device search indexes are made only when they take at most this
+    # share of the device's free memory (the model's activations need the
+    # rest); otherwise the host stores search.
+    DEVICE_INDEX_MAX_FREE_FRACTION = 0.5
 
     def __init__(
         self,
@@ -337,6 +341,7 @@ class KVController:
             "retrieval_launched_prefill": 0,
             "retrieval_device": 0,
             "device_index_dropped": 0,
+            "device_index_too_large": 0,
             "retrieval_ready_cpu": 0,
             "retrieval_skipped_no_cold": 0,
             "retrieval_ready_empty": 0,
@@ -401,10 +406,15 @@ class KVController:
         vh = self.Hk if self.per_head_retrieval else 1
         if self.B > 64 or self.faiss_dim > 1024 or self.faiss_dim % 4 or self.lookahead_k > 1024:
             return
+        capT = (self.cpu_buffer_size + 63) // 64 * 64
+        need = self.n_layers * self.B * vh * capT * (6 * self.faiss_dim) + self.B * vh * capT * 12
+        free = torch.cuda.mem_get_info(self._device)[0]
+        if need > self.DEVICE_INDEX_MAX_FREE_FRACTION * free:
+            self.dbg["device_index_too_large"] = 1
+            return
         try:
             # every search runs on the one search stream, so the layers share
             # one key scratch
-            capT = (self.cpu_buffer_size + 63) // 64 * 64
             scratch = DeviceIndex.scratch_for(self.B, vh, capT, self._device)
             self._dindex = [DeviceIndex(self.B, self.Hk, self.D, self.faiss_dim, vh, self.cpu_buffer_size,
                                         self._device, self.normalize_for_ip, scratch=scratch)

@@ -1195,3 +1195,17 @@ def test_device_searches_of_a_step_launch_together_and_settle_before_adds():
     assert ctrls[0].dbg["retrieval_device"] == 4 * L and ctrls[1].dbg["retrieval_device"] == 0
     for c in ctrls:
         c.wait_cold_adds()
+
+
+def test_device_index_is_not_made_past_its_memory_share():
+    """With the device indexes' share of free memory set to zero the
+    controller makes none, says so in dbg, and its searches run on the host
+    stores."""
+    from hotcold_kv import KVController
+    c = KVController(cpu_buffer_size=64, faiss_dim=16, lookahead_k=4, window_size=1, per_head_retrieval=True)
+    c.DEVICE_INDEX_MAX_FREE_FRACTION = 0.0
+    c._lazy_init(torch.empty((1, 2, 1, 16), dtype=torch.float16, device=DEV), n_layers=2)
+    assert c._dindex == [None, None] and c.dbg["device_index_too_large"] == 1
+    d = KVController(cpu_buffer_size=64, faiss_dim=16, lookahead_k=4, window_size=1, per_head_retrieval=True)
+    d._lazy_init(torch.empty((1, 2, 1, 16), dtype=torch.float16, device=DEV), n_layers=2)
+    assert all(x is not None for x in d._dindex) and d._dindex[0].keys is d._dindex[1].keys
