@@ -20,6 +20,12 @@
 //     logical index), the top R in rank order (ColdStore::select).
 // So the hits equal the host store's bit for bit.  The key/value rows stay in
 // the host store; only the hits' logical indices go back to the host.
+//
+// With unit vectors, a copy rounded to fp16 halves the scan: its fp32 scores
+// are within a proven bound delta of the exact ones, so only the slots whose
+// fp16-pass score is within 2*delta of the R-th best can be in the exact top
+// R; those are scored exactly and ranked as above (index_score16_kernel,
+// index_select16_kernel).  The hits are the same.
 #include <cmath>
 
 #include "hc_common.h"
