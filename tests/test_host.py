@@ -444,3 +444,39 @@ def test_rope_tables_are_the_rotary_modules_tables(dtype):
         half = inv.numel()
         assert torch.equal(cos, wc[..., :half]) and torch.equal(sin, ws[..., :half])
         assert torch.equal(wc[..., :half], wc[..., half:])      # the second half repeats the first
+
+
+def test_device_index_entries_refuse_bad_arguments_before_any_launch():
+    """hc_index_add / hc_index_search check their arguments on the host and
+    return HC_ERR_INVALID without touching the device: batch rows past 64, a
+    vector width that is not a multiple of 4 (or past 1024), R past 1024, a
+    capacity that is not a multiple of 64, ring states outside the capacity,
+    null pointers, and an fp16 copy with a width not a multiple of 8."""
+    lib = N.lib()
+    fake = ctypes.c_void_p(0x1000)        # never dereferenced: every call below fails its checks first
+    sizes = np.zeros(2, dtype=np.int64)
+    heads = np.zeros(2, dtype=np.int64)
+
+    def search(B=2, VH=1, VD=64, cap=128, R=8, capT=128, sz=sizes, hd=heads, vec=fake, keys=fake):
+        return lib.hc_index_search(B, VH, VD, cap, fake, VD, VD, VD, 1, vec, None, 1, capT, sz.ctypes.data,
+                                   hd.ctypes.data, R, keys, None, fake, None, None, None, None)
+
+    def add(VD=64, vec16=None, capT=128):
+        return lib.hc_index_add(2, 2, 64, 1, VD, 1, fake, 128, 64, 64, 4, fake, fake, vec16, capT, None)
+
+    assert search(B=65) == N.HC_ERR_INVALID
+    assert search(B=0) == N.HC_ERR_INVALID
+    assert search(VD=6) == N.HC_ERR_INVALID
+    assert search(VD=2048) == N.HC_ERR_INVALID
+    assert search(R=1025) == N.HC_ERR_INVALID
+    assert search(capT=100) == N.HC_ERR_INVALID
+    assert search(cap=200) == N.HC_ERR_INVALID                 # capT below the capacity
+    assert search(sz=np.array([0, 129], dtype=np.int64)) == N.HC_ERR_INVALID
+    assert search(hd=np.array([0, 128], dtype=np.int64)) == N.HC_ERR_INVALID
+    assert search(vec=None) == N.HC_ERR_INVALID
+    assert search(keys=None) == N.HC_ERR_INVALID
+    assert "index_search" in lib.hc_last_error().decode()
+    assert add(VD=6) == N.HC_ERR_INVALID
+    assert add(VD=12, vec16=fake) == N.HC_ERR_INVALID
+    assert add(capT=100) == N.HC_ERR_INVALID
+    assert "index_add" in lib.hc_last_error().decode()
