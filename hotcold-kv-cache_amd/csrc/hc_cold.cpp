@@ -73,6 +73,12 @@ struct ColdStore {
   RawArray<int64_t> pos;    // [slot]
   RawArray<float> vec;      // [VH][cap/16][VD][16]: 16-slot tiles, each dimension's 16 values together
   int64_t capT = 0;         // cap rounded up to a whole tile
+  // Deferred search vectors: while defer_vecs, adds store keys, values and
+  // positions only (the caller searches elsewhere, e.g. a device index);
+  // the first host search computes every live token's vectors
+  // (materialize_vecs) and ends the deferral.
+  bool defer_vecs = false;
+  bool vecs_missing = false;
 
   size_t vidx(int64_t vh, int64_t d, int64_t slot) const {
     return (size_t)vh * VD * capT + (size_t)(slot >> 4) * VD * 16 + (size_t)d * 16 + (slot & 15);
@@ -168,8 +174,13 @@ struct ColdStore {
       memcpy(vd + h * D, vv + h * v_sh, sizeof(float) * D);
     }
     pos[slot] = p;
-    set_vec(slot);
+    if (defer_vecs) vecs_missing = true;
+    else set_vec(slot);
   }
+
+  // The vectors of every live token, if adds deferred them; later adds
+  // compute theirs again.  Takes the write lock: call without holding it.
+  void materialize_vecs(int64_t nthreads);
 
   // Slot for the next token (advances the ring).
   int64_t next_slot() {
@@ -280,6 +291,19 @@ void parallel_for(int64_t n, int nthreads, F f) {
   for (auto& th : pool) th.join();
 }
 
+void ColdStore::materialize_vecs(int64_t nthreads) {
+  std::unique_lock<std::shared_mutex> lk(mu);
+  defer_vecs = false;
+  if (!vecs_missing) return;
+  constexpr int64_t kChunk = 256;
+  const int64_t nchunks = (size + kChunk - 1) / kChunk;
+  parallel_for(nchunks, threads_for(nthreads, nchunks), [&](int64_t c) {
+    const int64_t i1 = std::min(size, (c + 1) * kChunk);
+    for (int64_t i = c * kChunk; i < i1; ++i) set_vec(i);  // the live slots are 0..size-1
+  });
+  vecs_missing = false;
+}
+
 }  // namespace
 
 using hc::set_error;
@@ -316,6 +340,19 @@ extern "C" void hc_cold_destroy(void* store) {
   if (!s) return;
   s->wait_unpinned();  // a search job still reading the store finishes first
   delete s;
+}
+
+extern "C" int hc_cold_defer_vectors(void* store, int defer) {
+  ColdStore* s = as_store(store);
+  if (!s) return set_error(HC_ERR_INVALID, "cold_defer_vectors: null store");
+  s->wait_all_adds();
+  if (defer) {
+    std::unique_lock<std::shared_mutex> lk(s->mu);
+    s->defer_vecs = true;
+  } else {
+    s->materialize_vecs(0);
+  }
+  return HC_OK;
 }
 
 extern "C" int64_t hc_cold_size(const void* store) {
@@ -372,6 +409,7 @@ extern "C" int hc_cold_search(const void* store, const float* q, int64_t r, int6
   if (!s || !q || !out || !n_out) return set_error(HC_ERR_INVALID, "cold_search: null argument");
   if (head < 0 || head >= s->VH) return set_error(HC_ERR_INVALID, "cold_search: head %lld out of range", (long long)head);
   s->wait_all_adds();
+  as_store(const_cast<void*>(store))->materialize_vecs(0);
   std::shared_lock<std::shared_mutex> lk(s->mu);
   std::vector<double> ip((size_t)std::max<int64_t>(s->size, 1));
   s->scan(q, head, 0, s->size, ip.data());
@@ -383,6 +421,7 @@ extern "C" int hc_cold_export(const void* store, float* kpre, float* v, int64_t*
   const ColdStore* s = reinterpret_cast<const ColdStore*>(store);
   if (!s) return set_error(HC_ERR_INVALID, "cold_export: null store");
   s->wait_all_adds();
+  if (vec) as_store(const_cast<void*>(store))->materialize_vecs(0);
   std::shared_lock<std::shared_mutex> lk(s->mu);
   const int64_t HD = s->H * s->D;
   for (int64_t i = 0; i < s->size; ++i) {
@@ -496,6 +535,7 @@ int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, 
       return set_error(HC_ERR_INVALID, "cold_retrieve: store %lld does not match (per_head=%d)", (long long)b,
                        per_head);
   }
+  for (int64_t b = 0; b < B; ++b) as_store(stores[b])->materialize_vecs(nthreads);
   const int64_t VH = per_head ? H : 1;
   // outputs: kpre/v [B][H][R][D]; pos/valid [B][R] or [B][H][R]; zero-filled
   memset(kpre_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));

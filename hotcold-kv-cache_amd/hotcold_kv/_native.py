@@ -207,6 +207,7 @@ SIGNATURES = {
     "hc_cold_retrieve_async": (_vp, [_vp, _i64, _vp, _i64, _i64, _i64, _int, _i64, _int, _int, _vp, _vp, _vp, _vp,
                                      _vp, _i64, _i64, _vp, _i64, _vp, _i64]),
     "hc_cold_add_async": (_vp, [_vp, _i64, _vp, _i64, _i64, _vp, _i64, _i64, _vp, _vp, _vp, _i64, _i64]),
+    "hc_cold_defer_vectors": (_int, [_vp, _int]),
     "hc_cold_gather": (_int, [_vp, _i64, _int, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp,
                               _i64]),
     "hc_cold_gather_async": (_vp, [_vp, _i64, _int, _i64, _vp, _int, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _i64,

@@ -425,6 +425,11 @@ class KVController:
         stream = ctypes.c_void_p()
         N.check(N.lib().hc_stream_create(ctypes.byref(stream)), "hc_stream_create")
         self._search_stream = stream.value
+        # the host stores need no search vectors while the device ranks; a
+        # host search (after an index is dropped) computes them first
+        for rings in self.rings:
+            for r in rings:
+                N.check(N.lib().hc_cold_defer_vectors(r.handle, 1), "hc_cold_defer_vectors")
 
     def _drop_device_index(self, li):
         """The layer goes back to the host search (its store took an add the

@@ -535,6 +535,12 @@ int hc_cold_add(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_
 void* hc_cold_add_async(void* store, int64_t te, const float* kpre, int64_t k_sh, int64_t k_st,
                         const float* v, int64_t v_sh, int64_t v_st, const int64_t* pos, const int64_t* evicted_idx,
                         void* wait_event, int64_t nthreads, int64_t workers);
+/* defer != 0: later adds store keys, values and positions but not the
+ * search vectors (the caller ranks elsewhere, e.g. a device search index);
+ * the next host search, retrieval or vector export computes every live
+ * token's vectors first and ends the deferral, so results never change.
+ * defer = 0: compute them now and stop deferring.  Waits for earlier adds. */
+int hc_cold_defer_vectors(void* store, int defer);
 /* Top-r logical indices for query q [vec_dim] against search vector `head`;
  * *n_out = min(r, size). */
 int hc_cold_search(const void* store, const float* q, int64_t r, int64_t head, int64_t* out, int64_t* n_out);

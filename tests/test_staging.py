@@ -720,3 +720,62 @@ def test_device_index_ring_mirrors_the_host_store():
     assert other.keys.data_ptr() == dix.keys.data_ptr()
     with pytest.raises(ValueError):
         DeviceIndex(B, H, D, D, H, 2 * cap, "cpu", scratch=(dix.keys, dix.keys32))
+
+
+@pytest.mark.parametrize("vec_heads", [1, 2])
+def test_deferred_search_vectors_give_the_same_results(vec_heads):
+    """A store whose adds defer the search vectors (hc_cold_defer_vectors, set
+    while a device index ranks) answers searches, retrievals and vector
+    exports exactly as a store that computed them at every add, over adds
+    that wrap the ring, before and after its first host search (which
+    computes the missing vectors and ends the deferral)."""
+    import ctypes
+
+    import numpy as np
+
+    from hotcold_kv import _native as N
+    from hotcold_kv.controller import _Ring
+    H, Dd, cap = 2, 16, 40
+    rng = np.random.default_rng(vec_heads)
+    a, b = _Ring(cap, H, Dd, Dd, vec_heads), _Ring(cap, H, Dd, Dd, vec_heads)
+    assert N.lib().hc_cold_defer_vectors(b.handle, 1) == 0
+
+    def add(te):
+        k = rng.standard_normal((H, te, Dd), dtype=np.float32)
+        v = rng.standard_normal((H, te, Dd), dtype=np.float32)
+        p = rng.integers(0, 10 ** 6, te).astype(np.int64)
+        for r in (a, b):
+            r.add_async(k, v, p, nthreads=2, workers=2).join()
+
+    def same():
+        for h in range(vec_heads):
+            q = rng.standard_normal(Dd).astype(np.float32)
+            q /= np.linalg.norm(q)
+            assert np.array_equal(a.search(q, 12, head=h), b.search(q, 12, head=h))
+
+    add(25)
+    add(30)                                   # wraps
+    same()                                    # b computes its vectors here
+    add(17)                                   # b computes them at the add again
+    same()
+    ea, eb = a.export(), b.export()
+    for key in ("kpre", "v", "pos", "vec"):
+        assert np.array_equal(ea[key], eb[key]), key
+    # a retrieval on a deferring store
+    a2, c = _Ring(cap, H, Dd, Dd, vec_heads), _Ring(cap, H, Dd, Dd, vec_heads)
+    N.lib().hc_cold_defer_vectors(c.handle, 1)
+    k = rng.standard_normal((H, 53, Dd), dtype=np.float32)
+    for r in (a2, c):
+        r.add(k, k, np.arange(53, dtype=np.int64))
+    q = rng.standard_normal((1, vec_heads, Dd)).astype(np.float32)
+    outs = []
+    for r in (a2, c):
+        st = (ctypes.c_void_p * 1)(r.handle)
+        kp, vv = np.zeros((1, H, 8, Dd), np.float32), np.zeros((1, H, 8, Dd), np.float32)
+        pos, valid = np.zeros((1, vec_heads, 8), np.int64), np.zeros((1, vec_heads, 8), np.uint8)
+        N.check(N.lib().hc_cold_retrieve(st, 1, q.ctypes.data, vec_heads * Dd, Dd, Dd, 1, 8, int(vec_heads > 1),
+                                         N.HC_DTYPE_F32, kp.ctypes.data, vv.ctypes.data, pos.ctypes.data,
+                                         valid.ctypes.data, None, 0, 0, None, None, 1), "hc_cold_retrieve")
+        outs.append((kp, vv, pos, valid))
+    for x, y in zip(*outs):
+        assert np.array_equal(x, y)
