@@ -783,12 +783,47 @@ class KVController:
             if slot is None:
                 self.dbg["retrieval_skipped_no_slot"] += 1
                 return False
+        dindex = self._dindex[li] if self._dindex else None
+        if q_vecs is not None and dindex is not None:
+            return self._device_retrieval_now(li, slot, dindex, q_vecs, table, nthreads)
         if q_vecs is None:
             self._wait_event(slot.q_ready)
         args, keep, tab = self._search_args(li, slot, q_vecs, table, nthreads)
         missing = ctypes.c_int64(0)
         N.check(N.lib().hc_cold_retrieve(*args[:-1], ctypes.byref(missing), args[-1]), "hc_cold_retrieve")
         self._finish_retrieval(li, slot, tab, int(slot.host[3].sum()), missing.value)
+        return True
+
+    def _device_retrieval_now(self, li, slot, dindex, q_vecs, table, nthreads):
+        """_retrieval_worker on the layer's device index: the host query
+        vectors (already in search form) ranked by the exact device scan, then
+        the hits' rows gathered from the host stores on the calling thread
+        (hc_cold_gather) -- the rows hc_cold_retrieve would write, and the
+        host stores keep deferring their vectors.  The scan runs on the
+        search stream (the layers share its key scratch), after the current
+        stream's work, and is waited for."""
+        self._settle_search(li)
+        q = torch.from_numpy(np.ascontiguousarray(q_vecs, dtype=np.float32).reshape(self.B, -1, self.faiss_dim))
+        q = q.to(self._device)
+        if self._flush_event is None:
+            self._flush_event = self._event(0)
+        if slot.hits_ready is None:
+            slot.hits_ready = self._event(0)
+        N.check(N.lib().hc_event_record(self._flush_event, ops_stream(self._device)), "hc_event_record")
+        dindex.search(q, self.lookahead_k, slot.hits_dev, normalize_q=False, stream=self._search_stream,
+                      hits_host=slot.hits_host, wait_event=self._flush_event, done_event=slot.hits_ready)
+        self._wait_event(slot.hits_ready)
+        self._search_done[li] = slot.hits_ready
+        kpre, vv, pos, valid = slot.host
+        tab = table is not None and self._rope is not None
+        missing = ctypes.c_int64(0)
+        N.check(N.lib().hc_cold_gather(
+            self._store_ptrs[li], self.B, int(self.per_head_retrieval), self.lookahead_k, slot.hits_host.data_ptr(),
+            N.dtype_code(kpre.dtype), kpre.data_ptr(), vv.data_ptr(), pos.data_ptr(), valid.data_ptr(),
+            table.ctypes.data if tab else None, table.shape[0] if tab else 0, table.shape[1] if tab else 0,
+            slot.tab.data_ptr() if tab else None, ctypes.byref(missing), int(nthreads)), "hc_cold_gather")
+        self.dbg["retrieval_device"] += 1
+        self._finish_retrieval(li, slot, tab, int(valid.sum()), missing.value)
         return True
 
     def _search_args(self, li, slot, q_vecs, table, nthreads):

@@ -96,7 +96,8 @@ def test_prefill_retrieval_to_held_decode_at_64k():
     """The 64k bf16 workload (batch 4, budget 4096, window 64, heavy-tailed
     keys), one layer through the hot/cold engine: the prompt is compressed
     to the budget and the rest evicted to the cold store; the prefill-time
-    synchronous retrieval (controller.py:295-312) fetches the top-256 tokens
+    synchronous retrieval (controller.py:295-312, ranked on the layer's device
+    index) fetches the top-256 tokens
     per KV head; the first decode step (hotcold_attention) injects them into
     the held slot and attends [held | hot rows | token] in the fused launch.
     Checked: the kept rows (oracle compression), the store's contents, each
@@ -133,6 +134,7 @@ def test_prefill_retrieval_to_held_decode_at_64k():
     ctrl.launch_retrieval_now(0, qwin)
     ctrl.maybe_prefetch_to_gpu(0, device=DEV)
     assert ctrl.dbg["retrieval_launched_prefill"] == 1
+    assert ctrl.dbg["retrieval_device"] == 1          # ranked on the layer's device index
     # first decode step
     tok = synthetic.make_decode_token(w, 3, 0, seed=0, device=DEV)
     out = hp.hotcold_attention(ctrl, layer, 0, tok["q_pre"], tok["k_pre"], tok["v"], tok["q_post"], tok["k_post"],
