@@ -285,4 +285,30 @@ __device__ __forceinline__ void bstore(__amdgpu_buffer_rsrc_t r, uint32_t off, c
   }
 }
 
+// Wave-aggregated LDS updates.  Radix-select keys mostly share their leading
+// digits, so plain per-lane atomics on one histogram bin or one append counter
+// serialise across the whole workgroup; here each wave issues one atomic for
+// the lanes that agree with its first active lane.
+__device__ __forceinline__ void hist_add(uint32_t* hist, uint32_t dig, bool active) {
+  const uint64_t todo = __ballot(active);
+  if (!todo) return;
+  const int lane = __lane_id(), leader = __ffsll((unsigned long long)todo) - 1;
+  const uint32_t d0 = (uint32_t)__shfl((int)dig, leader);
+  const uint64_t same = __ballot(active && dig == d0);
+  if (lane == leader) atomicAdd(&hist[d0], (uint32_t)__popcll(same));
+  if (active && dig != d0) atomicAdd(&hist[dig], 1u);
+}
+
+// A slot of an LDS list for each lane with `want` (-1 for the others): one
+// atomic per wave, lanes in lane order.
+__device__ __forceinline__ int append_slot(int* counter, bool want) {
+  const uint64_t m = __ballot(want);
+  if (!m) return -1;
+  const int lane = __lane_id(), leader = __ffsll((unsigned long long)m) - 1;
+  int base = 0;
+  if (lane == leader) base = atomicAdd(counter, __popcll(m));
+  base = __shfl(base, leader);
+  return want ? base + __popcll(m & ((1ull << lane) - 1)) : -1;
+}
+
 }  // namespace hc

@@ -151,7 +151,7 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
 #pragma unroll
         for (int u = 0; u < kTopkU; ++u) {
           const int i = base + u * kTopkThreads + (int)threadIdx.x;
-          if (i < prefix && (ks[u] & pmask) == pbits) atomicAdd(&hist[(ks[u] >> shift) & dmask], 1u);
+          hist_add(hist, (ks[u] >> shift) & dmask, i < prefix && (ks[u] & pmask) == pbits);
         }
       }
       __syncthreads();
