@@ -1066,8 +1066,9 @@ def test_device_index_fp16_pass_equals_the_exact_scan(R):
         dix.search(qd, R, h64, pass16=False)
         assert torch.equal(h16, h64), i
 
-@pytest.mark.parametrize("per_head,faiss_dim", [(False, 32), (True, 64), (True, 96)])
-def test_scheduled_device_search_equals_the_host_search(per_head, faiss_dim):
+@pytest.mark.parametrize("per_head,faiss_dim,normalize", [(False, 32, True), (True, 64, True), (True, 96, True),
+                                                         (True, 64, False)])
+def test_scheduled_device_search_equals_the_host_search(per_head, faiss_dim, normalize):
     """Two controllers fed the same staged evictions (gather_evict into an
     eviction stage, as the cache evicts) and the same decode queries: one
     ranks on its device index and gathers the hits natively
@@ -1082,14 +1083,15 @@ def test_scheduled_device_search_equals_the_host_search(per_head, faiss_dim):
     rng = torch.Generator().manual_seed(5)
     args = dict(max_capacity_prompt=128, cpu_buffer_size=300, faiss_dim=faiss_dim, window_size=1,
                 query_pool_size=2, lookahead_k=R, hold_retrieved=True, per_head_retrieval=per_head,
-                profile_overlap=False)
+                profile_overlap=False, normalize_for_ip=normalize)
     ctrls = [KVController(device_search=True, **args), KVController(device_search=False, **args)]
     inv = synthetic.inv_freq(D, 10000.0)
     for c in ctrls:
         c._lazy_init(torch.empty((B, Hk, 1, D), dtype=torch.bfloat16, device=DEV), n_layers=1)
         c.set_rope(inv, 1.0)
     assert ctrls[0]._dindex[0] is not None and ctrls[1]._dindex[0] is None
-    print(f"[case] per_head {per_head} faiss_dim {faiss_dim}", flush=True)
+    print(f"[case] per_head {per_head} faiss_dim {faiss_dim} normalize {normalize}", flush=True)
+    assert (ctrls[0]._dindex[0].vec16 is not None) == normalize       # the fp16 pass needs unit vectors
     n_dev = 0
     for rnd in range(6):
         k = torch.randn((B, Hk, S, D), generator=rng).to(torch.bfloat16)
