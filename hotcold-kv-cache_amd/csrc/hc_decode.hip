@@ -55,6 +55,8 @@ __global__ __launch_bounds__(256) void h2o_accum_kernel(const float* scores, con
 // grid (cdiv(S, rows_per_wg), Hk, B), block 256; rows are rowb bytes
 // (a multiple of 16), rows_per_wg <= 256 and rows_per_wg * rowb / 16 <= 2 * 256.
 constexpr int kEvictMaxKeys = 8192;
+constexpr int kH2OMaxG = 8;    // query heads per KV head with the batched score loads
+constexpr int kH2OBatch = 4;   // keys per thread whose scores are loaded together
 struct H2OEvictArgs {
   const char* k;
   int64_t k_sb, k_sh, k_ss;  // byte strides
@@ -96,7 +98,46 @@ __global__ __launch_bounds__(256) void h2o_evict_one_kernel(const float* scores,
   }
 
   const float* arow = acc + b * a_sb + hk * a_sh;
-  for (int s = tid; s < S; s += 256) sm_sc[s] = h2o_updated(scores, ml, Hq, G, S, b, hk, s, arow);
+  if (G <= kH2OMaxG) {
+    // h2o_updated with the group's (max, sum) pairs loaded once and the score
+    // loads of kH2OBatch keys issued before any is used (the same operations
+    // in the same order, so the same bits)
+    // (register arrays indexed only by unrolled constants; heads past G are
+    // loaded from head G-1 and not used, so every load is unconditional)
+    float Mg[kH2OMaxG], Lg[kH2OMaxG];
+#pragma unroll
+    for (int g = 0; g < kH2OMaxG; ++g) {
+      const int h = hk * G + min(g, G - 1);
+      Mg[g] = ml[((int64_t)b * Hq + h) * 2 + 0];
+      Lg[g] = ml[((int64_t)b * Hq + h) * 2 + 1];
+    }
+    for (int s0 = tid; s0 < S; s0 += 256 * kH2OBatch) {
+      float sc[kH2OBatch][kH2OMaxG], av[kH2OBatch];
+#pragma unroll
+      for (int j = 0; j < kH2OBatch; ++j) {
+        const int s = min(s0 + 256 * j, S - 1);
+        // the new token (s = S-1) has no accumulated score: its column is
+        // never read, so the load is clamped to the last existing one
+        av[j] = S >= 2 ? arow[min(s, S - 2)] : 0.f;
+#pragma unroll
+        for (int g = 0; g < kH2OMaxG; ++g) sc[j][g] = scores[((int64_t)b * Hq + hk * G + min(g, G - 1)) * S + s];
+      }
+#pragma unroll
+      for (int j = 0; j < kH2OBatch; ++j) {
+        const int s = s0 + 256 * j;
+        if (s < S) {
+          float col = 0.f;
+#pragma unroll
+          for (int g = 0; g < kH2OMaxG; ++g)
+            if (g < G) col += (sc[j][g] == -INFINITY) ? 0.f : exp2f(sc[j][g] - Mg[g]) / Lg[g];
+          col /= (float)G;
+          sm_sc[s] = (s == S - 1 ? 0.f : av[j]) + col;
+        }
+      }
+    }
+  } else {
+    for (int s = tid; s < S; s += 256) sm_sc[s] = h2o_updated(scores, ml, Hq, G, S, b, hk, s, arow);
+  }
   __syncthreads();
 
   // lowest (order key, ~index) over the prefix
