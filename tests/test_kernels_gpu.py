@@ -1099,7 +1099,7 @@ def test_scheduled_device_search_equals_the_host_search(per_head, faiss_dim, nor
         v = torch.randn((B, Hk, S, D), generator=rng).to(torch.bfloat16)
         pos = (torch.arange(S, dtype=torch.int64) + 500 * rnd).repeat(B, 1)
         idx = torch.stack([torch.randperm(S, generator=rng)[:te].sort().values for _ in range(B)])
-        staged = rnd != 3                                   # round 3: a synchronous add
+        staged = rnd != 3                                   # the fourth eviction: a synchronous add
         for c in ctrls:
             kd, vd, pd, id_ = k.to(DEV), v.to(DEV), pos.to(DEV), idx.to(DEV)
             if staged:
