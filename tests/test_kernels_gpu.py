@@ -579,6 +579,8 @@ H2O_EVICT_CASES = [
     (3, 8, 8, 100, 256, 1, torch.bfloat16, 0, "nan"),
     (1, 32, 8, 4097, 128, 64, torch.float16, 0, "low"),    # budget 4096
     (1, 4, 1, 2, 32, 1, torch.float32, 0, None),           # one prefix key, one window key
+    (1, 64, 8, 300, 128, 16, torch.float16, 0, "low"),     # group of 8: the batched score loads' widest group
+    (1, 32, 2, 333, 128, 16, torch.bfloat16, 0, "high"),   # group of 16: scores loaded key by key
 ]
 
 
