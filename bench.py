@@ -750,6 +750,11 @@ class _Rotary:
         self.attention_scaling = 1.0
 
 
+def _mean_us(ms):
+    """Mean of a list of millisecond times in us (None if empty)."""
+    return round(statistics.fmean(ms) * 1e3, 1) if ms else None
+
+
 def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
     """The hot/cold engine's own loop at a held-slot workload, through
     hotcold_attention (the patched attention's body between RoPE and o_proj):
@@ -835,6 +840,14 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
         "step_us_wall_mean": round(total_ms * 1e3 / steps, 1),
         "step_us_wall_median": round(statistics.median(step_ms) * 1e3, 1),
         "step_us_issue_mean": round(statistics.fmean(step_ms) * 1e3, 1),
+        "step_us_issue_first": round(step_ms[0] * 1e3, 1),
+        "step_us_issue_mean_after_first": round(statistics.fmean(step_ms[1:]) * 1e3, 1) if steps > 1 else None,
+        "step_us_issue_p90": round(sorted(step_ms)[(9 * len(step_ms)) // 10] * 1e3, 1),
+        # the step whose layers start their searches, and the step after it
+        # (the searches' copies start; the previous copies are injected)
+        "step_us_issue_search_steps_mean": _mean_us([step_ms[t] for t in retr_steps if (t + 1) % w.retrieve_every == 0]),
+        "step_us_issue_copy_steps_mean": _mean_us([step_ms[t] for t in retr_steps
+                                                   if (t + 1) % w.retrieve_every == 1 and t > 0]),
         "gpu_drain_ms_after_loop": round(drain_ms, 2),
         "step_us_wall_without_retrieval_median": round(statistics.median(other) * 1e3, 1) if other else None,
         "layer_us_wall_mean": round(total_ms * 1e3 / steps / L, 2),
