@@ -56,6 +56,7 @@ __global__ __launch_bounds__(256) void h2o_accum_kernel(const float* scores, con
 // (a multiple of 16), rows_per_wg <= 256 and rows_per_wg * rowb / 16 <= 2 * 256.
 constexpr int kEvictMaxKeys = 8192;
 constexpr int kH2OMaxG = 8;    // query heads per KV head with the batched score loads
+                               // (kernels for groups of up to 4 and up to 8)
 constexpr int kH2OBatch = 4;   // keys per thread whose scores are loaded together
 struct H2OEvictArgs {
   const char* k;
@@ -71,9 +72,11 @@ struct H2OEvictArgs {
   int prefix, rowb, rows_per_wg;
 };
 
+template <int GM>
 __global__ __launch_bounds__(256) void h2o_evict_one_kernel(const float* scores, const float* ml, int Hq, int G,
                                                             int S, const float* acc, int64_t a_sb, int64_t a_sh,
                                                             H2OEvictArgs e) {
+  static_assert(GM >= 1 && GM <= kH2OMaxG, "group bound of the batched score loads");
   __shared__ float sm_sc[kEvictMaxKeys];
   __shared__ uint32_t sm_best[2][4];
   const int hk = blockIdx.y, b = blockIdx.z;
@@ -98,21 +101,22 @@ __global__ __launch_bounds__(256) void h2o_evict_one_kernel(const float* scores,
   }
 
   const float* arow = acc + b * a_sb + hk * a_sh;
-  if (G <= kH2OMaxG) {
+  if (G <= GM) {
     // h2o_updated with the group's (max, sum) pairs loaded once and the score
     // loads of kH2OBatch keys issued before any is used (the same operations
     // in the same order, so the same bits)
-    // (register arrays indexed only by unrolled constants; heads past G are
-    // loaded from head G-1 and not used, so every load is unconditional)
-    float Mg[kH2OMaxG], Lg[kH2OMaxG];
+    // (register arrays indexed only by unrolled constants; heads past G, up to
+    // the kernel's bound GM, are loaded from head G-1 and not used, so every
+    // load is unconditional)
+    float Mg[GM], Lg[GM];
 #pragma unroll
-    for (int g = 0; g < kH2OMaxG; ++g) {
+    for (int g = 0; g < GM; ++g) {
       const int h = hk * G + min(g, G - 1);
       Mg[g] = ml[((int64_t)b * Hq + h) * 2 + 0];
       Lg[g] = ml[((int64_t)b * Hq + h) * 2 + 1];
     }
     for (int s0 = tid; s0 < S; s0 += 256 * kH2OBatch) {
-      float sc[kH2OBatch][kH2OMaxG], av[kH2OBatch];
+      float sc[kH2OBatch][GM], av[kH2OBatch];
 #pragma unroll
       for (int j = 0; j < kH2OBatch; ++j) {
         const int s = min(s0 + 256 * j, S - 1);
@@ -120,7 +124,7 @@ __global__ __launch_bounds__(256) void h2o_evict_one_kernel(const float* scores,
         // never read, so the load is clamped to the last existing one
         av[j] = S >= 2 ? arow[min(s, S - 2)] : 0.f;
 #pragma unroll
-        for (int g = 0; g < kH2OMaxG; ++g) sc[j][g] = scores[((int64_t)b * Hq + hk * G + min(g, G - 1)) * S + s];
+        for (int g = 0; g < GM; ++g) sc[j][g] = scores[((int64_t)b * Hq + hk * G + min(g, G - 1)) * S + s];
       }
 #pragma unroll
       for (int j = 0; j < kH2OBatch; ++j) {
@@ -128,7 +132,7 @@ __global__ __launch_bounds__(256) void h2o_evict_one_kernel(const float* scores,
         if (s < S) {
           float col = 0.f;
 #pragma unroll
-          for (int g = 0; g < kH2OMaxG; ++g)
+          for (int g = 0; g < GM; ++g)
             if (g < G) col += (sc[j][g] == -INFINITY) ? 0.f : exp2f(sc[j][g] - Mg[g]) / Lg[g];
           col /= (float)G;
           sm_sc[s] = (s == S - 1 ? 0.f : av[j]) + col;
@@ -446,8 +450,14 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
 
   if (h2o_acc && h2o_ev) {
     const dim3 grid((unsigned)cdiv(S, h2o_ev->rows_per_wg), (unsigned)Hk, (unsigned)B);
-    hipLaunchKernelGGL(h2o_evict_one_kernel, grid, dim3(256), 0, st, a.scores, a.ml, (int)Hq, G, (int)S, h2o_acc,
-                       h2o_sb, h2o_sh, *h2o_ev);
+    // a group of up to 4 (e.g. 32 query / 8 KV heads) loads only its own
+    // heads' scores; larger groups take the bound-8 kernel (key by key past 8)
+    if (G <= 4)
+      hipLaunchKernelGGL(h2o_evict_one_kernel<4>, grid, dim3(256), 0, st, a.scores, a.ml, (int)Hq, G, (int)S,
+                         h2o_acc, h2o_sb, h2o_sh, *h2o_ev);
+    else
+      hipLaunchKernelGGL(h2o_evict_one_kernel<kH2OMaxG>, grid, dim3(256), 0, st, a.scores, a.ml, (int)Hq, G,
+                         (int)S, h2o_acc, h2o_sb, h2o_sh, *h2o_ev);
     if ((rc = check_launch("h2o_evict_one")) != HC_OK) return rc;
   } else if (h2o_acc) {
     const dim3 grid((unsigned)cdiv(S, 256), (unsigned)Hk, (unsigned)B);
