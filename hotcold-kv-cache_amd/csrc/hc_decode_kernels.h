@@ -14,12 +14,16 @@
 //   * K/V stream through a per-wave ring of register tiles filled by raw
 //     buffer loads (128-bit per lane).  Rows outside the workgroup's key range
 //     are addressed past the buffer's end, so the hardware returns zeros
-//     without touching memory; every load is unconditional, which lets the
-//     compiler keep the whole ring in flight (exact vmcnt waits);
+//     without touching memory; every ring load is unconditional, which lets
+//     the compiler keep the whole ring in flight (exact vmcnt waits).  The
+//     split's rows are dealt out evenly over the waves (whole tiles, then
+//     one partial tile each), so the waves finish together;
 //   * Q.K^T on MFMA: v_mfma_f32_16x16x32_{f16,bf16} with the 16 key rows of a
 //     tile as the A operand and the G (<=16) query heads as the B operand;
 //     fp32 inputs use v_mfma_f32_16x16x4f32;
-//   * online max-stabilised softmax in the log2 domain (exp2), fp32;
+//   * online softmax in the log2 domain (exp2), fp32, with a lazy
+//     reference max: the accumulators are rescaled only when a tile's max
+//     exceeds the reference by more than 2^8;
 //   * P.V on MFMA for f16/bf16 (v_mfma_f32_16x16x16_{f16,bf16}): the Q.K^T
 //     output leaves lane (r, c) holding p for keys 4r..4r+3 of head c, which
 //     is exactly its B-operand share, and its four V rows give the A operand
@@ -30,12 +34,16 @@
 //     evaluated once per workgroup into an LDS bitmap;
 //   * split partials (m, l, acc) are merged by the last workgroup of each
 //     (batch, kv head) to finish, through device-coherent stores, an arrival
-//     counter and device-coherent loads; launches with many workgroups merge
-//     them in a second, one-pass kernel instead.
+//     counter and device-coherent loads issued together; launches with many
+//     workgroups merge them in a second, one-pass kernel instead;
+//   * the fused append's token is loaded, attended and stored by the one
+//     wave that owns it, before the ring, so no other wave spends load slots
+//     or registers on it.
 #pragma once
 #include "hc_common.h"
 #include <stddef.h>
 #include <algorithm>
+#include <type_traits>
 
 
 namespace hc {
@@ -94,6 +102,38 @@ static_assert(offsetof(DecodeArgs, Hq) + sizeof(int) <= 128, "prologue fields mu
 
 // Keys of one split when the keep bitmap is needed (mask or held slot).
 constexpr int kMaxBitmapKeys = 16384;
+
+// Online softmax with a lazy reference: a tile moves the reference (and
+// rescales the accumulators) only when its max exceeds the reference by more
+// than this many log2 units, so the probabilities stay below 2^8 -- well
+// inside the f16/bf16 range of the rounded P -- and most tiles skip the
+// rescale.  The (m, l, acc) partials are exact for whatever reference they
+// carry, so every merge below is unchanged.
+constexpr float kLazyLog2 = 8.0f;
+
+// exp2 on the hardware instruction: every argument here is <= 8 (a logit
+// minus a reference at most 8 below it), where v_exp_f32 needs none of
+// exp2f's range scaling; -inf gives 0.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Reductions over the four 16-lane rows of a wave (lanes c, c+16, c+32,
+// c+48), on gfx950's row-swap permutes instead of LDS-routed shuffles.  With
+// both operands equal, v_permlane16_swap leaves rows (0,1) of the pair
+// holding (r0, r1) and rows (2,3) holding (r2, r3); v_permlane32_swap then
+// pairs the two halves.  Every lane ends with the same value, combined in
+// the same order.
+__device__ __forceinline__ float rows_max(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return fmaxf(__uint_as_float(c[0]), __uint_as_float(c[1]));
+}
+__device__ __forceinline__ float rows_sum(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto c = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(c[0]) + __uint_as_float(c[1]);
+}
 // ---------------------------------------------------------------------------
 // Per-lane registers of one 16-key tile.
 //   K (MFMA A operand): lane l holds key row tile + l%16, 16-byte pieces at
@@ -332,15 +372,14 @@ __device__ __forceinline__ void process_tile(const TileRegs<T, D>& r, const QFra
       }
     }
   }
-  float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-  tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
-  const float m_new = fmaxf(st.m_run, tm);
+  const float tm = rows_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  const bool bump = tm > st.m_run + kLazyLog2;  // false for an all-masked tile
+  const float m_new = bump ? tm : st.m_run;
   const bool dead = (m_new == -INFINITY);
-  const float alpha = dead ? 1.f : exp2f(st.m_run - m_new);
+  const float alpha = bump ? fast_exp2(st.m_run - m_new) : 1.f;
   float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : exp2f(s[i] - m_new);
+  for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : fast_exp2(s[i] - m_new);
   st.l_run = st.l_run * alpha + ((p[0] + p[1]) + (p[2] + p[3]));
   st.m_run = m_new;
 
@@ -435,15 +474,14 @@ __device__ __forceinline__ void process_tile_mx(const TileRegs<T, D>& r, const Q
       }
     }
   }
-  float tm = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
-  tm = fmaxf(tm, __shfl_xor(tm, 16, 64));
-  tm = fmaxf(tm, __shfl_xor(tm, 32, 64));
-  const float m_new = fmaxf(st.m_run, tm);
+  const float tm = rows_max(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])));
+  const bool bump = tm > st.m_run + kLazyLog2;  // false for an all-masked tile
+  const float m_new = bump ? tm : st.m_run;
   const bool dead = (m_new == -INFINITY);
-  const float alpha = dead ? 1.f : exp2f(st.m_run - m_new);
+  const float alpha = bump ? fast_exp2(st.m_run - m_new) : 1.f;
   float p[4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : exp2f(s[i] - m_new);
+  for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : fast_exp2(s[i] - m_new);
   float pr[4];
   const uint32_t b0 = MxOps<T>::pack2(p[0], p[1], pr[0], pr[1]);
   const uint32_t b1 = MxOps<T>::pack2(p[2], p[3], pr[2], pr[3]);
@@ -486,12 +524,16 @@ __device__ __forceinline__ float load_agent(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Merge the split partials (m, l, acc) of unit (b, hk) in one pass over the
-// splits (online rescaling; the loads do not depend on the running values)
-// and write the output rows, plus the final (max, sum) when a.ml is set.
-// Threads tid, tid + nthreads, ... take the unit's G*D output elements.
+// Merge the split partials (m, l, acc) of unit (b, hk) and write the output
+// rows, plus the final (max, sum) when a.ml is set.  The partials of up to
+// eight splits are loaded before any is used, so their loads are in flight
+// together (loaded and used one split at a time, each load had waited for
+// the one before: 1.2 us more per launch at five splits); they are then
+// combined by online rescaling.  Threads tid, tid + nthreads, ... take the
+// unit's G*D output elements.
 template <typename T, bool AGENT>
 __device__ __forceinline__ void merge_partials(const DecodeArgs& a, int b, int hk, int D, int tid, int nthreads) {
+  constexpr int kChunk = 8;
   const int G = a.G;
   const int unit = b * a.Hk + hk;
   const int stride_part = G * D + 2 * G;
@@ -500,18 +542,24 @@ __device__ __forceinline__ void merge_partials(const DecodeArgs& a, int b, int h
   for (int e = tid; e < G * D; e += nthreads) {
     const int g = e / D, d = e - g * D;
     float M = -INFINITY, A = 0.f, L = 0.f;
-#pragma unroll 8
-    for (int s = 0; s < a.splits; ++s) {
-      const float* ps = pu + s * stride_part;
-      const float ms = AGENT ? load_agent(ps + G * D + g) : ps[G * D + g];
-      const float as = AGENT ? load_agent(ps + e) : ps[e];
-      const float ls = AGENT ? load_agent(ps + G * D + G + g) : ps[G * D + G + g];
-      const float Mn = fmaxf(M, ms);
-      if (Mn != -INFINITY) {
-        const float c0 = exp2f(M - Mn), c1 = exp2f(ms - Mn);
-        A = A * c0 + as * c1;
-        L = L * c0 + ls * c1;
-        M = Mn;
+    for (int s0 = 0; s0 < a.splits; s0 += kChunk) {
+      float ms[kChunk], as[kChunk], ls[kChunk];
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        const float* ps = pu + min(s0 + j, a.splits - 1) * stride_part;
+        ms[j] = AGENT ? load_agent(ps + G * D + g) : ps[G * D + g];
+        as[j] = AGENT ? load_agent(ps + e) : ps[e];
+        ls[j] = AGENT ? load_agent(ps + G * D + G + g) : ps[G * D + G + g];
+      }
+#pragma unroll
+      for (int j = 0; j < kChunk; ++j) {
+        const float Mn = fmaxf(M, ms[j]);
+        if (s0 + j < a.splits && Mn != -INFINITY) {
+          const float c0 = fast_exp2(M - Mn), c1 = fast_exp2(ms[j] - Mn);
+          A = A * c0 + as[j] * c1;
+          L = L * c0 + ls[j] * c1;
+          M = Mn;
+        }
       }
     }
     obase[g * a.o_sh + d] = from_f32<T>(A / L);
@@ -566,47 +614,54 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       for (int j = 0; j < DPL; ++j) st.acc[g][j] = 0.f;
   }
 
-  // Wave w takes the 16-key tiles w, w + NW, w + 2 NW, ... of the split's
-  // range, so the waves of a workgroup read neighbouring tiles at any
-  // moment.  Contiguous per-wave ranges measured 13% slower at 72 MB per
-  // launch (16.9 against 14.7 us): the last waves to receive their rows held
-  // the workgroup at its final barrier.  Tile counts differ by at most one.
-  const int first = key_begin + wave * 16;
-  const int wend = key_end;
-  const int nt = first < key_end ? (key_end - first + 16 * NW - 1) / (16 * NW) : 0;
+  // Tile schedule of the split's keys [key_begin, key_end): full rounds of
+  // NW 16-key tiles, wave w taking the w-th tile of each round (so the waves
+  // of a workgroup read neighbouring rows at any moment), then the keys left
+  // over spread evenly over the waves, one partial tile each.  Every wave
+  // thus reads about the same number of rows: with whole tiles in the last
+  // round, half the waves of a 36-tile unit had a tile more to wait for and
+  // held the workgroup at its final barrier.  Tile t of the wave covers rows
+  // [tlo(t), thi(t)); past the wave's last tile the range is empty, so the
+  // ring's extra loads touch no memory.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const int nkeys = max(0, key_end - key_begin);
+  const int full = nkeys / (16 * NW);
+  const int rem = nkeys - full * 16 * NW;
+  const int cw = (rem + NW - 1) / NW;
+  const bool part = wv * cw < rem;
+  const int nt = full + (part ? 1 : 0);
+  const int tail_lo = key_begin + full * 16 * NW + wv * cw;
+  const int tail_hi = min(tail_lo + cw, key_end);
+  auto tlo = [&](int t) { return t < full ? key_begin + (t * NW + wv) * 16 : (t == full && part ? tail_lo : key_end); };
+  auto thi = [&](int t) {
+    return t < full ? key_begin + (t * NW + wv) * 16 + 16 : (t == full && part ? tail_hi : key_end);
+  };
   {
-    QFrag<T, D> qf;
-    const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
-    qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
-
-    // The ring's first NBUF-1 tiles are issued before the keep bitmap is
-    // built, so the bitmap's own loads overlap them; their keep bits are
-    // applied once the bitmap is complete.
+    // The ring's first NBUF-1 tiles are issued first, so their HBM round
+    // trip overlaps everything else the prologue loads; the keep bitmap's
+    // bits are applied to them once it is complete.
     TileRegs<T, D> r[NBUF];
 #pragma unroll
     for (int i = 0; i < NBUF - 1; ++i)
-      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, first + i * 16 * NW, key_begin, wend, col, grp, nullptr);
+      load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, tlo(i), key_begin, thi(i), col, grp, nullptr);
 
-    // Fused append: the last wave of the last split attends the new token as
-    // a one-key tile and copies the token's K/V (and pre-RoPE key and
-    // position) into row S-1.  Its loads are issued right after the ring's
-    // first tiles and it is processed after the wave's first NBUF tiles, by
-    // when they have landed, so it adds no wait; the copies are stored after
-    // the last tile.  Every wave runs
-    // this code with resources of extent 0 where it does not own the token:
-    // no branch around memory operations, so the compiler's load counting
-    // stays exact.
+    // Fused append: the last wave of the last split attends the new token
+    // (key S-1) as a one-key tile and copies its K/V (and pre-RoPE key and
+    // position) into row S-1.  Only that wave loads it, in a wave-uniform
+    // branch ahead of every load the ring waits on, so the other waves issue
+    // nothing for it and the ring's load counting stays exact.  The token is
+    // processed and stored before the ring, which frees its registers.
+    bool tok = false;
+    if constexpr (APPEND) tok = split == a.splits - 1 && wv == NW - 1;
     TileRegs<T, D> rn;
     uint32_t pw[TileRegs<T, D>::KW][4];
     uint32_t pos_w[2];
-    bool tok = false;
-    if constexpr (APPEND) {
-      tok = split == a.splits - 1 && __builtin_amdgcn_readfirstlane(wave) == NW - 1;
+    if (APPEND && tok) {
       constexpr uint32_t rowb = D * sizeof(T);
-      const T* kn = tok ? reinterpret_cast<const T*>(a.k_new) + b * a.kn_sb + hk * a.kn_sh : kbase;
-      const T* vn = tok ? reinterpret_cast<const T*>(a.v_new) + b * a.vn_sb + hk * a.vn_sh : vbase;
-      load_token<T, D>(rn, make_rsrc(kn, tok ? rowb : 0u), make_rsrc(vn, tok ? rowb : 0u), col, grp, tok);
-      const bool tp = tok && a.p_new != nullptr;
+      const T* kn = reinterpret_cast<const T*>(a.k_new) + b * a.kn_sb + hk * a.kn_sh;
+      const T* vn = reinterpret_cast<const T*>(a.v_new) + b * a.vn_sb + hk * a.vn_sh;
+      load_token<T, D>(rn, make_rsrc(kn, rowb), make_rsrc(vn, rowb), col, grp, true);
+      const bool tp = a.p_new != nullptr;
       const T* pn = tp ? reinterpret_cast<const T*>(a.p_new) + b * a.pn_sb + hk * a.pn_sh : kbase;
       const __amdgpu_buffer_rsrc_t pnrs = make_rsrc(pn, tp ? rowb : 0u);
 #pragma unroll
@@ -614,10 +669,14 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
         const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
         bload<16>(pnrs, (col == 0 && d0 < D) ? (uint32_t)(d0 * sizeof(T)) : kOob, pw[t]);
       }
-      const bool tq = tok && a.pos_new != nullptr && hk == 0;
+      const bool tq = a.pos_new != nullptr && hk == 0;
       const int64_t* psrc = tq ? a.pos_new + b * a.posn_sb : reinterpret_cast<const int64_t*>(kbase);
       bload<8>(make_rsrc(psrc, tq ? 8u : 0u), lane == 0 ? 0u : kOob, pos_w);
     }
+
+    QFrag<T, D> qf;
+    const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
+    qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
 
     // Keep bitmap of the split's keys (attention mask and held-slot test
     // valid & pos <= cur), one key per thread, packed by wave ballots.
@@ -626,7 +685,6 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     if (use_bits) {
       const int64_t cur = a.cur_pos ? *a.cur_pos : INT64_MAX;
       const uint8_t* mrow = a.mask ? a.mask + b * a.mask_sb : nullptr;
-      const int nkeys = key_end - key_begin;
       for (int base = 0; base < nkeys; base += 64 * NW) {
         const int rel = base + (int)threadIdx.x;
         const int key = key_begin + rel;
@@ -643,46 +701,19 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
-      for (int i = 0; i < NBUF - 1; ++i) r[i].keep &= tile_keep_bits(first + i * 16 * NW, key_begin, grp, sm_bits);
+      for (int i = 0; i < NBUF - 1; ++i) r[i].keep &= tile_keep_bits(tlo(i), key_begin, grp, sm_bits);
     }
-    const uint32_t* bits = use_bits ? sm_bits : nullptr;
     float* srow = EVICT ? a.scores + ((int64_t)b * a.Hq + hk * G + min(col, G - 1)) * a.S : nullptr;
 
-    // Step t issues the loads of tile t + NBUF - 1 (past the range: no memory
-    // traffic) and then processes tile t, so NBUF-1 tiles stay in flight.
-#define HC_RING_GROUP(g0)                                                                                  \
-  _Pragma("unroll") for (int j = 0; j < NBUF; ++j) {                                                       \
-    const int t = (g0) + j;                                                                                \
-    load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, first + (t + NBUF - 1) * 16 * NW,  \
-                    key_begin, wend, col, grp, bits);                                                      \
-    if (t < nt) {                                                                                          \
-      if constexpr (MX)                                                                                    \
-        process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16 * NW, wend, col, grp, srow); \
-      else                                                                                                 \
-        process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, first + t * 16 * NW, wend, col, grp, srow); \
-    }                                                                                                      \
-  }
-    int g_start = 0;
-    if constexpr (APPEND) {
-      HC_RING_GROUP(0)
-      g_start = NBUF;
-      // the token is key S-1; with EVICT its logit is kept like every key's
-      // (only the owning wave's row 0 falls inside [S-1, key_end))
+    if (APPEND && tok) {
+      // with EVICT the token's logit is kept like every key's
       if constexpr (MX)
-        process_tile_mx<T, D, EVICT>(rn, qf, st, G, a.scale_log2, a.S - 1, tok ? a.S : 0, col, grp, srow);
+        process_tile_mx<T, D, EVICT>(rn, qf, st, G, a.scale_log2, a.S - 1, a.S, col, grp, srow);
       else
-        process_tile<T, D, GM, EVICT>(rn, qf, st, G, a.scale_log2, a.S - 1, tok ? a.S : 0, col, grp, srow);
-    }
-    for (int g0 = g_start; g0 < nt; g0 += NBUF) {
-      HC_RING_GROUP(g0)
-    }
-#undef HC_RING_GROUP
-    if constexpr (APPEND) {
-      // The token's rows.  Stored after the last tile: issued before the
-      // loop instead, they measured slower.
+        process_tile<T, D, GM, EVICT>(rn, qf, st, G, a.scale_log2, a.S - 1, a.S, col, grp, srow);
       const uint32_t row = (uint32_t)(a.S - 1);
-      store_token<T, D>(rn, krs, vrs, row * k_rowb, row * v_rowb, col, grp, tok);
-      const bool tp = tok && a.p_new != nullptr;
+      store_token<T, D>(rn, krs, vrs, row * k_rowb, row * v_rowb, col, grp, true);
+      const bool tp = a.p_new != nullptr;
       T* pd = tp ? reinterpret_cast<T*>(a.p_dst) + b * a.pd_sb + hk * a.pd_sh + (int64_t)row * a.pd_ss
                  : const_cast<T*>(kbase);
       const __amdgpu_buffer_rsrc_t pdrs = make_rsrc(pd, tp ? (uint32_t)(D * sizeof(T)) : 0u);
@@ -691,16 +722,41 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
         const int d0 = (sizeof(T) == 4) ? 16 * t + 4 * grp : 32 * t + 8 * grp;
         bstore<16>(pdrs, (col == 0 && d0 < D) ? (uint32_t)(d0 * sizeof(T)) : kOob, pw[t]);
       }
-      const bool tq = tok && a.pos_new != nullptr && hk == 0;
+      const bool tq = a.pos_new != nullptr && hk == 0;
       int64_t* pdst = tq ? a.pos_dst + b * a.posd_sb + row : reinterpret_cast<int64_t*>(const_cast<T*>(kbase));
       bstore<8>(make_rsrc(pdst, tq ? 8u : 0u), lane == 0 ? 0u : kOob, pos_w);
     }
+
+    // Step t issues the loads of tile t + NBUF - 1 (an empty range past the
+    // wave's tiles: no memory traffic) and then processes tile t, so NBUF-1
+    // tiles stay in flight.  The loop is compiled twice, with and without
+    // the keep bitmap, so launches without one carry no bitmap test per key.
+    auto ring = [&](auto with_bits) {
+      constexpr bool WB = decltype(with_bits)::value;
+      const uint32_t* bits = WB ? sm_bits : nullptr;
+      for (int g0 = 0; g0 < nt; g0 += NBUF) {
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) {
+          const int t = g0 + j;
+          load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, tlo(t + NBUF - 1), key_begin,
+                          thi(t + NBUF - 1), col, grp, bits);
+          if (t < nt) {
+            if constexpr (MX)
+              process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, tlo(t), thi(t), col, grp, srow);
+            else
+              process_tile<T, D, GM, EVICT>(r[j], qf, st, G, a.scale_log2, tlo(t), thi(t), col, grp, srow);
+          }
+        }
+      }
+    };
+    if (use_bits)
+      ring(std::true_type{});
+    else
+      ring(std::false_type{});
   }
 
   // ---- reduce the four row groups of the wave (they share m_run) ----
-  float l_run = st.l_run;
-  l_run += __shfl_xor(l_run, 16, 64);
-  l_run += __shfl_xor(l_run, 32, 64);
+  const float l_run = rows_sum(st.l_run);
   // Partials in LDS, one padding float per 32 (bank-conflict-free writes of
   // the MFMA layout, where the four row groups sit 32 floats apart).
   constexpr int RS = D + D / 32 + 1;
@@ -727,10 +783,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     for (int g = 0; g < GM; ++g)
 #pragma unroll
       for (int j = 0; j < DPL; ++j) {
-        float x = st.acc[g][j];
-        x += __shfl_xor(x, 16, 64);
-        x += __shfl_xor(x, 32, 64);
-        st.acc[g][j] = x;
+        st.acc[g][j] = rows_sum(st.acc[g][j]);
       }
     if (grp == 0) {
 #pragma unroll
@@ -759,7 +812,7 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     if (M != -INFINITY) {
 #pragma unroll
       for (int w = 0; w < NW; ++w) {
-        const float sc = exp2f(sm_m[w][g] - M);
+        const float sc = fast_exp2(sm_m[w][g] - M);
         A = fmaf(sm_acc[w][g][d + (d >> 5)], sc, A);
         L = fmaf(sm_l[w][g], sc, L);
       }
