@@ -113,6 +113,7 @@ class Setup:
     def __init__(self, w, dev):
         import torch
         from hotcold_kv import synthetic
+        from hotcold_kv.hot_buffer import kv_rows
 
         self.w = w
         L, B, S, D = w.layers, w.batch, w.seq_len, w.head_dim
@@ -129,8 +130,11 @@ class Setup:
             self.v[sl] = p["v"]
             del p
         self.cap = w.budget + w.decode_steps
-        self.k_hot = torch.zeros((LB, w.hk, self.cap, D), dtype=dt, device=dev)
-        self.v_hot = torch.zeros_like(self.k_hot)
+        # the hot tier's own layout (hot_buffer.kv_rows): each row's key and
+        # value adjacent, K and V as (LB,Hk,cap,D) views of row stride 2*D
+        self.k_hot, self.v_hot = kv_rows((LB, w.hk), self.cap, D, dt, dev)
+        self.k_hot.zero_()
+        self.v_hot.zero_()
         self.q_new, self.k_new, self.v_new = [], [], []
         for t in range(w.decode_steps):
             qs, ks, vs = [], [], []
@@ -475,6 +479,7 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
     torch-CPU path on one layer of the same inputs (cpu_baseline_config)."""
     import torch
     from hotcold_kv import ops, synthetic
+    from hotcold_kv.hot_buffer import kv_rows
 
     g = torch.Generator(device=dev).manual_seed(5)
     dt, D, Hk, Hq = w.dtype, w.head_dim, w.hk, w.hq
@@ -487,8 +492,9 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
            "held": R, "dtype": {torch.float16: "f16", torch.bfloat16: "bf16", torch.float32: "f32"}[dt]}
 
     # -- decode: hot buffers of every layer, held slot in rows 0..R-1 ------------------------
-    k_hot = torch.randn((LB, Hk, cap, D), generator=g, device=dev, dtype=dt)
-    v_hot = torch.randn((LB, Hk, cap, D), generator=g, device=dev, dtype=dt)
+    k_hot, v_hot = kv_rows((LB, Hk), cap, D, dt, dev)
+    k_hot.copy_(torch.randn((LB, Hk, cap, D), generator=g, device=dev, dtype=dt))
+    v_hot.copy_(torch.randn((LB, Hk, cap, D), generator=g, device=dev, dtype=dt))
     q = torch.randn((LB, Hq, D), generator=g, device=dev, dtype=dt)
     k_new = torch.randn((LB, Hk, 1, D), generator=g, device=dev, dtype=dt)
     v_new = torch.randn((LB, Hk, 1, D), generator=g, device=dev, dtype=dt)

@@ -16,7 +16,7 @@ import torch
 import torch.nn.functional as F
 
 from .. import ops
-from ..hot_buffer import HotBuffer
+from ..hot_buffer import HotBuffer, kv_rows
 from .scoring import repeat_kv
 
 
@@ -67,8 +67,7 @@ class DeferredCompaction:
             window, _, keep_prefix = ops.keep_counts(S, st0.window_size, st0.budget)
             n = keep_prefix + window
             cap = n + st0.decode_reserve
-            kst = torch.empty((len(items), B, Hk, cap, D), dtype=k0.dtype, device=k0.device)
-            vst = torch.empty_like(kst)
+            kst, vst = kv_rows((len(items), B, Hk), cap, D, k0.dtype, k0.device)
             for i, it in enumerate(items):
                 it[0].buf = HotBuffer(B, Hk, D, k0.dtype, k0.device, cap, storage=(kst[i], vst[i]))
             qs, ks, vs = [it[1] for it in items], [it[2] for it in items], [it[3] for it in items]

