@@ -154,8 +154,9 @@ __global__ __launch_bounds__(256) void inject_rerope_tab_kernel(InjectTab a) {
 // Pooled retrieval query: out[b][vh][d] = (sum over the window's T query
 // tensors, then over the heads of KV head vh's group -- or over all Hq heads
 // when there is one vector per batch row -- of q[b][h][d]) / (T * heads), in
-// fp32 with the additions in that fixed order.
-constexpr int kMaxPoolRows = 16;
+// fp32 with the additions in that fixed order.  Up to kMaxPoolRows window
+// rows (hc_retrieval_query_max_rows; the host pools longer windows itself).
+constexpr int kMaxPoolRows = 64;
 struct PoolQueryArgs {
   const void* q[kMaxPoolRows];
   int64_t sb[kMaxPoolRows];
@@ -197,6 +198,8 @@ __global__ void pool_query_kernel(PoolQueryArgs a) {
 }  // namespace hc
 
 using namespace hc;
+
+extern "C" int64_t hc_retrieval_query_max_rows(void) { return kMaxPoolRows; }
 
 extern "C" int hc_retrieval_query(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t T,
                                   const void* const* q, const int64_t* q_sb, const int64_t* q_sh, int per_head,

@@ -218,6 +218,7 @@ SIGNATURES = {
                              _vp]),
     "hc_index_search": (_int, [_i64, _i64, _i64, _i64, _vp, _i64, _i64, _i64, _int, _vp, _vp, _int, _i64, _vp, _vp,
                                 _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "hc_retrieval_query_max_rows": (_i64, []),
     "hc_retrieval_query": (_int, [_int, _i64, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _int, _vp, _vp, _vp, _vp]),
 }
 

@@ -685,8 +685,8 @@ class KVController:
         buffer (hc_retrieval_query: the pooling kernel, on the current
         stream, no host wait); to_host: also copy it to the slot's pinned
         buffer and record the slot's event behind the copy.  Windows of more
-        than 64 query rows, or of mixed dtypes, are pooled by torch
-        (_pooled_query_dev) instead."""
+        query rows than the kernel takes (hc_retrieval_query_max_rows), or of
+        mixed dtypes, are pooled by torch (_pooled_query_dev) instead."""
         win = list(self.query_window[int(layer_idx)])
         q0 = win[0]
         B, Hq, _, D = q0.shape
@@ -696,7 +696,7 @@ class KVController:
             slot.q_ready = self._event(0)
         stream = ops_stream(q0.device)
         rows = [(t, r) for t in win for r in range(t.shape[2])]
-        if len(rows) <= 64 and all(t.dtype == q0.dtype and t.shape[:2] == q0.shape[:2] and t.shape[3] == D
+        if len(rows) <= N.lib().hc_retrieval_query_max_rows() and all(t.dtype == q0.dtype and t.shape[:2] == q0.shape[:2] and t.shape[3] == D
                                    and t.stride(3) == 1 and t.is_cuda for t in win):
             es = q0.element_size()
             n = len(rows)

@@ -111,11 +111,21 @@ def hotcold_attention(kvctrl, layer, li, q_pre, k_pre, v, q_post, k_post, pos_ne
         if rr.ready:
             kbuf, vbuf = layer.buf.held_storage()
             R = int(rr.k_pre.shape[2])
-            if rr.cos is not None:
-                ops.inject_rerope_tab(rr.k_pre, rr.v, rr.cos, rr.sin, kbuf, vbuf)
-            else:
-                inv, ascale = _rope_params(device)
-                ops.inject_rerope(rr.k_pre.float(), rr.v.float(), rr.pos, inv, ascale, kbuf, vbuf)
+            cos_t, sin_t = rr.cos, rr.sin
+            if cos_t is None:
+                # searched before the rotary parameters were known, so no
+                # tables travelled with the rows: build them here from the
+                # staged positions as the rotary module does, so the held keys
+                # are apply_rotary_pos_emb's bits as with shipped tables
+                # (without a rotary module this raises, as patch.py:76-78)
+                inv, ascale = _rope_params(device) if kvctrl._rope is None else \
+                    (kvctrl._rope[0].to(device), kvctrl._rope[1])
+                cos, sin = ops.rope_tables(rr.pos.reshape(-1, R), inv, ascale, kbuf.dtype)
+                B, Hk, _, D = rr.k_pre.shape
+                shape = (B, Hk, R, D // 2) if rr.pos.dim() == 3 else (B, R, D // 2)
+                cos_t, sin_t = cos.reshape(shape).contiguous(), sin.reshape(shape).contiguous()
+                kvctrl.dbg["rope_rows_direct"] += 1
+            ops.inject_rerope_tab(rr.k_pre, rr.v, cos_t, sin_t, kbuf, vbuf)
             kvctrl.staged_consumed(li)
             injected = (rr.pos, rr.valid, R)
         held = kvctrl.resolve_held(li, injected)

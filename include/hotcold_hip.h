@@ -135,7 +135,8 @@ int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t 
 
 /*
  * The pooled retrieval query on the device: the mean of the window's T query
- * tensors q[t] [B][Hq][D] (element strides q_sb[t], q_sh[t]; T <= 16) over
+ * tensors q[t] [B][Hq][D] (element strides q_sb[t], q_sh[t];
+ * T <= hc_retrieval_query_max_rows()) over
  * the rows and over the heads -- of each KV head's group (per_head: out
  * [B][Hk][D]) or of all Hq heads (out [B][1][D]) -- in fp32, added in
  * window-then-head order.  Replaces the torch.cat + means of _pooled_query_np
@@ -144,6 +145,10 @@ int hc_decode_attn_append(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t 
  * may be NULL) by hipMemcpyAsync, and `event` (may be NULL) is recorded
  * behind the copy, for a search thread to wait on.
  */
+/* The largest window (T) hc_retrieval_query accepts: 64.  No counterpart in
+ * the reference; callers pool longer windows themselves. */
+int64_t hc_retrieval_query_max_rows(void);
+
 int hc_retrieval_query(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t T, const void* const* q,
                        const int64_t* q_sb, const int64_t* q_sh, int per_head, float* dev_out, float* host_out,
                        void* event, void* stream);

@@ -193,6 +193,169 @@ def test_prefill_retrieval_to_held_decode_at_64k():
         assert np.abs(o[:, h * G:(h + 1) * G] - want).max() <= TOL[w.dtype], h
 
 
+@pytest.mark.parametrize("name,batch,pool", [
+    ("llama8b_16k_b1024_held64", 1, 4),
+    ("llama8b_16k_b1024_held64", 1, 32),
+    ("b16_32k_b2048_held128", 2, 4),
+])
+def test_scheduled_retrieval_windows(name, batch, pool):
+    """The every-window_size-steps retrieval (controller.py:314-342) at a
+    workload's size: one layer through hotcold_attention for two windows.
+    The prompt is compressed to the budget and the rest evicted to the cold
+    store; every retrieve_every steps the last `pool` pre-RoPE queries are
+    pooled per KV head (pool 32 exceeds the old 16-row kernel bound), the
+    top-R tokens are ranked on the layer's device index, copied on the side
+    stream and re-rotated into the held slot, which later steps attend with
+    valid & pos <= cur (patch.py:241-305).  The test waits for each search
+    after its step, so the next step injects it.  Checked at every
+    injection: each (sequence, KV head)'s positions against the oracle search
+    over the store, the held keys bit for bit (the model's rotation of the
+    stored pre-RoPE keys) and the values; at every step: the output within
+    the dtype tolerance of the fp64 oracle over [held | hot rows | token]."""
+    from hotcold_kv import KVController
+    from hotcold_kv import patch as hp
+    from hotcold_kv.cache import HotColdLayer
+
+    w = synthetic.WORKLOADS[name]
+    B, Hk, G, D, R, E = batch, w.hk, w.group, w.head_dim, w.held, w.retrieve_every
+    lid = 2
+    print(f"[case] {w.name} layer {lid}, batch {B}, pool {pool}, held {R}, every {E}", flush=True)
+    steps = 2 * E + 2
+    cap = w.budget + steps
+    ratio = (w.budget - w.window + 0.5) / cap
+    ctrl = KVController(max_capacity_prompt=cap, topk_ratio=ratio, recent_size=w.window, cpu_buffer_size=w.seq_len,
+                        faiss_dim=D, window_size=E, query_pool_size=pool, lookahead_k=R, hold_retrieved=True,
+                        per_head_retrieval=True, force_wait_for_prefetch_diagnostic=True, profile_overlap=False,
+                        enable_asserts=True)
+    p = synthetic.make_prompt(w, layer=lid, seed=0, device=DEV, batch=B)
+    inv = synthetic.inv_freq(D, w.theta)
+    ctrl._lazy_init(p["k_pre"], n_layers=1)
+    ctrl.set_rope(inv, 1.0)
+    layer = HotColdLayer(ctrl)
+    layer.set_last_query_post(p["q_post"][:, :, -w.window:, :].contiguous())
+    layer.update(key_states=p["k_post"], value_states=p["v"], layer_idx=0,
+                 cache_kwargs={"pre_key_states": p["k_pre"], "positions": p["positions"]})
+    del p
+    ctrl.wait_cold_adds()
+    # decode appends without re-compression, so the store stays as filled
+    snaps = [ctrl.rings[0][b].export() for b in range(B)]
+    assert all(len(s["pos"]) == w.seq_len - w.budget for s in snaps)
+
+    q_hist, launched, windows = [], None, 0
+    for t in range(steps):
+        tok = synthetic.make_decode_token(w, lid, t, seed=0, device=DEV, batch=B)
+        q_hist.append(tok["q_pre"])
+        n_new = ctrl.dbg["injection_new"]
+        out = hp.hotcold_attention(ctrl, layer, 0, tok["q_pre"], tok["k_pre"], tok["v"], tok["q_post"],
+                                   tok["k_post"], tok["position"], G, w.scaling)
+        torch.cuda.synchronize()
+        kbuf, vbuf = layer.buf.held_storage()
+        if ctrl.dbg["injection_new"] != n_new:
+            # a new held slot: the search launched at the end of the last window
+            assert launched is not None and t % E == 0, t
+            windows += 1
+            qvec = ctrl._q_to_vecs_np(launched)                        # (B,Hk,D) the search's queries
+            T = launched.shape[2]
+            qf = launched.double().cpu().view(B, Hk, G, T, D).mean(dim=(2, 3))
+            qf = qf / qf.norm(dim=-1, keepdim=True)
+            assert np.abs(qvec - qf.numpy()).max() < 1e-6
+            held_pos, held_valid, r = ctrl.held_mem[0]
+            assert r == R and bool(held_valid.all())
+            hp_cpu = held_pos.cpu()
+            want_k = torch.empty((B, Hk, R, D), dtype=torch.float32)
+            want_v = torch.empty((B, Hk, R, D), dtype=torch.float32)
+            for b in range(B):
+                for h in range(Hk):
+                    idx = ref.cold_topk(snaps[b]["kpre"], qvec[b, h], R, head=h, per_head=True, dim=D)
+                    assert hp_cpu[b, h].tolist() == snaps[b]["pos"][idx].tolist(), (t, b, h)
+                    want_k[b, h] = torch.from_numpy(snaps[b]["kpre"][idx, h])
+                    want_v[b, h] = torch.from_numpy(snaps[b]["v"][idx, h])
+            lo = layer.buf.held - R
+            assert torch.equal(kbuf[:, :, lo:layer.buf.held].cpu(), ref.rerope(want_k, hp_cpu, inv, 1.0, w.dtype))
+            assert torch.equal(vbuf[:, :, lo:layer.buf.held].cpu(), want_v.to(w.dtype))
+        if (t + 1) % E == 0:
+            launched = torch.cat(q_hist[-pool:], dim=2)              # the layer's query window
+            ctrl.wait_for_retrieval(0)                                 # the next step copies and injects it
+        # this step's output: [held | hot rows (the appended token last)]
+        hot_k, hot_v = layer.keys.cpu(), layer.values.cpu()
+        n = hot_k.shape[2]
+        cur = tok["position"][0, -1:].cpu()
+        held = ctrl.held_mem[0]
+        q1 = tok["q_post"].cpu()
+        o = out[:, :, 0].float().cpu().numpy()
+        for h in range(Hk):
+            if held is not None:
+                lo = layer.buf.held - R
+                K = torch.cat([kbuf[:, h:h + 1, lo:layer.buf.held].cpu(), hot_k[:, h:h + 1]], 2)
+                V = torch.cat([vbuf[:, h:h + 1, lo:layer.buf.held].cpu(), hot_v[:, h:h + 1]], 2)
+                pos_h, valid_h = held[0][:, h].cpu(), held[1][:, h].cpu()
+                m = torch.cat([valid_h & (pos_h <= cur), torch.ones((B, n), dtype=torch.bool)], 1)
+            else:
+                K, V, m = hot_k[:, h:h + 1], hot_v[:, h:h + 1], None
+            want = ref.decode_attention(q1[:, h * G:(h + 1) * G], K, V, w.scaling, m)
+            assert np.abs(o[:, h * G:(h + 1) * G] - want).max() <= TOL[w.dtype], (t, h)
+    assert windows == 2 and ctrl.dbg["retrieval_device"] == 2
+    assert ctrl.dbg["retrieval_skipped_no_slot"] == 0
+
+
+def test_retrieval_searched_without_rotary_tables_injects_exact_keys():
+    """A retrieval searched before the rotary parameters were known carries
+    no rotary tables; the inject then builds them from the staged positions
+    (as the rotary module computes them), so the held keys are still the
+    model's rotation bit for bit (patch.py:76-102 rotates with the module's
+    own cos/sin)."""
+    import types
+
+    from hotcold_kv import KVController
+    from hotcold_kv import patch as hp
+    from hotcold_kv.cache import HotColdLayer
+
+    w = synthetic.WORKLOADS["llama8b_16k_b1024_held64"]
+    B, Hk, G, D, R = 1, w.hk, w.group, w.head_dim, w.held
+    cap = w.budget + 4
+    ratio = (w.budget - w.window + 0.5) / cap
+    ctrl = KVController(max_capacity_prompt=cap, topk_ratio=ratio, recent_size=w.window, cpu_buffer_size=w.seq_len,
+                        faiss_dim=D, window_size=w.retrieve_every, query_pool_size=4, lookahead_k=R,
+                        hold_retrieved=True, per_head_retrieval=True, force_wait_for_prefetch_diagnostic=True,
+                        profile_overlap=False, enable_asserts=True)
+    p = synthetic.make_prompt(w, layer=4, seed=0, device=DEV, batch=B)
+    inv = synthetic.inv_freq(D, w.theta)
+    ctrl._lazy_init(p["k_pre"], n_layers=1)
+    layer = HotColdLayer(ctrl)
+    layer.set_last_query_post(p["q_post"][:, :, -w.window:, :].contiguous())
+    layer.update(key_states=p["k_post"], value_states=p["v"], layer_idx=0,
+                 cache_kwargs={"pre_key_states": p["k_pre"], "positions": p["positions"]})
+    qwin = p["q_pre"][:, :, -4:, :].contiguous()
+    del p
+    ctrl.wait_cold_adds()
+    assert ctrl._rope is None
+    ctrl.launch_retrieval_now(0, qwin)                 # no set_rope yet: no tables travel
+    ctrl.maybe_prefetch_to_gpu(0, device=DEV)
+    assert ctrl.dbg["rope_rows_direct"] == 0
+    hp.set_active_rotary_emb(types.SimpleNamespace(inv_freq=inv.to(DEV), attention_scaling=1.0))
+    try:
+        tok = synthetic.make_decode_token(w, 4, 0, seed=0, device=DEV, batch=B)
+        hp.hotcold_attention(ctrl, layer, 0, tok["q_pre"], tok["k_pre"], tok["v"], tok["q_post"], tok["k_post"],
+                             tok["position"], G, w.scaling)
+        torch.cuda.synchronize()
+    finally:
+        hp.set_active_rotary_emb(None)
+    assert ctrl.dbg["injection_new"] == 1 and ctrl.dbg["rope_rows_direct"] == 1
+    held_pos, held_valid, r = ctrl.held_mem[0]
+    assert r == R and bool(held_valid.all())
+    hp_cpu = held_pos.cpu()
+    snap = ctrl.rings[0][0].export()
+    qvec = ctrl._q_to_vecs_np(qwin)
+    want_k = torch.empty((B, Hk, R, D), dtype=torch.float32)
+    for h in range(Hk):
+        idx = ref.cold_topk(snap["kpre"], qvec[0, h], R, head=h, per_head=True, dim=D)
+        assert hp_cpu[0, h].tolist() == snap["pos"][idx].tolist(), h
+        want_k[0, h] = torch.from_numpy(snap["kpre"][idx, h])
+    kbuf, _ = layer.buf.held_storage()
+    got = kbuf[:, :, layer.buf.held - R:layer.buf.held].cpu()
+    assert torch.equal(got, ref.rerope(want_k, hp_cpu, inv, 1.0, w.dtype))
+
+
 def test_compaction_full_8k_job_layers_batched():
     """The bench's batched launch (layers stacked along the batch axis) keeps
     exactly what the per-layer oracle keeps, for the first and last layer."""
