@@ -5,6 +5,7 @@
 // reference's per-token eviction score run here after the attention.
 #include "hc_decode_kernels.h"
 #include <algorithm>
+#include <atomic>
 #include <mutex>
 
 namespace hc {
@@ -239,11 +240,16 @@ __global__ __launch_bounds__(256) void evict_score_kernel(const float* scores, c
   if (threadIdx.x == 0) idx[b] = si[0];
 }
 
-// The first kCounterBytes of a decode workspace hold the arrival counters of
-// the in-kernel merge, one per (batch, kv head): zero before the first launch
-// on the workspace, and every launch leaves them zero.
+// The first kCounterBytes of a decode workspace hold the in-kernel merge's
+// arrival words, one 64-bit [launch tag | arrivals] per (batch, kv head).
+// They need no initialisation: every launch counts under a tag of its own
+// (kernel comment at the arrival).
 constexpr int64_t kCounterBytes = 16384;
-constexpr int64_t kMaxMergeUnits = kCounterBytes / 4;
+constexpr int64_t kMaxMergeUnits = kCounterBytes / 8;
+
+// Launch tags of the in-kernel merge: consecutive launches get different
+// tags (a 32-bit counter, wrapping after 2^32 launches).
+static std::atomic<uint32_t> g_launch_tag{0};
 // The in-kernel merge is used up to this many workgroups.  Its chain (the
 // partial's device-coherent stores, the arrival count, the last workgroup's
 // loads) costs a few memory round trips on the last workgroup of each unit,
@@ -422,7 +428,8 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
   a.splits = splits;
   a.keys_per_split = (int)shape.kps;
   a.S_cache = (int)S_cache;
-  a.counters = shape.merge_in_kernel ? reinterpret_cast<uint32_t*>(ws) : nullptr;
+  a.counters = shape.merge_in_kernel ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
+  a.epoch = g_launch_tag.fetch_add(1, std::memory_order_relaxed) + 1;
   if (ap) {
     a.k_new = ap->k_new; a.kn_sb = ap->kn_sb; a.kn_sh = ap->kn_sh;
     a.v_new = ap->v_new; a.vn_sb = ap->vn_sb; a.vn_sh = ap->vn_sh;
@@ -635,29 +642,37 @@ static_assert(sizeof(hc_decode_h2o_evict_args) == 46 * 8,
 // ---------------------------------------------------------------------------
 // Allocation-free fused append + decode, for callers that cannot allocate
 // (code under HIP graph capture, tight serving loops, harnesses that forbid
-// hipMalloc).  It is hc_decode_attn_append with the split partials kept in a
-// static device array instead of a caller-owned workspace:
-//   * the array (kNoAllocScratchBytes) lives in the library's code object, so
-//     every GPU the library runs on holds its own copy until the process ends;
+// hipMalloc).  It is hc_decode_attn_append with the split partials and merge
+// words kept in a static device array instead of a caller-owned workspace:
+//   * the array (kNoAllocSlots regions of kNoAllocSlotBytes) lives in the
+//     library's code object, so every GPU the library runs on holds its own
+//     copy until the process ends;
 //   * its device address is taken once per device with hipGetSymbolAddress
 //     (on the first call on that device, with that device current) and only
 //     that address is passed to the kernels -- the array's name in host code
 //     is a host-side stand-in, not device memory;
-//   * every call on one GPU shares that GPU's array and leaves its contents
-//     behind: the split partials are fully written before they are read, so
-//     nothing is cleared, and two calls that may overlap on one GPU (two
-//     streams) race on it;
-//   * a call whose partials would not fit is refused (HC_ERR_WORKSPACE), and
-//     no call allocates or frees memory.
+//   * each region serves one stream: the first call from a stream binds it a
+//     free region for the rest of the process, so calls from different
+//     streams never share partials, and calls from one stream are ordered by
+//     that stream; a call from a stream beyond the regions is refused
+//     (HC_ERR_INVALID).  The partials are fully written before they are read
+//     and the merge words count under per-launch tags, so nothing is cleared;
+//   * a call whose partials would not fit a region is refused
+//     (HC_ERR_WORKSPACE), and no call allocates or frees memory.
 // ---------------------------------------------------------------------------
 namespace hc {
-constexpr int64_t kNoAllocScratchBytes = (int64_t)8 << 20;
-static __device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+constexpr int kNoAllocSlots = 4;
+constexpr int64_t kNoAllocSlotBytes = (int64_t)8 << 20;
+static __device__ __align__(256) unsigned char scratch[kNoAllocSlots * kNoAllocSlotBytes];
 constexpr int kMaxScratchDevices = 64;
 static void* g_scratch_ptr[kMaxScratchDevices];
+static void* g_slot_stream[kMaxScratchDevices][kNoAllocSlots];
+static bool g_slot_bound[kMaxScratchDevices][kNoAllocSlots];
 static std::mutex g_scratch_mu;
 
-// Device address of the current device's scratch array, taken on first use.
+// Device address of the calling stream's region of the current device's
+// scratch array: the array's address is taken on the device's first call,
+// and the stream is bound a free region on its first call.
 static int scratch_address(void* stream, void** out) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
@@ -680,7 +695,21 @@ static int scratch_address(void* stream, void** out) {
                        hipGetErrorString(e));
     g_scratch_ptr[dev] = p;
   }
-  *out = g_scratch_ptr[dev];
+  int slot = -1;
+  for (int i = 0; i < kNoAllocSlots && slot < 0; ++i)
+    if (g_slot_bound[dev][i] && g_slot_stream[dev][i] == stream) slot = i;
+  for (int i = 0; i < kNoAllocSlots && slot < 0; ++i)
+    if (!g_slot_bound[dev][i]) {
+      g_slot_bound[dev][i] = true;
+      g_slot_stream[dev][i] = stream;
+      slot = i;
+    }
+  if (slot < 0)
+    return set_error(HC_ERR_INVALID,
+                     "decode_append_noalloc: the static scratch of device %d serves %d streams and all are bound to "
+                     "other streams (calls from more streams would share partials); use hc_decode_attn_append",
+                     dev, kNoAllocSlots);
+  *out = static_cast<char*>(g_scratch_ptr[dev]) + (int64_t)slot * kNoAllocSlotBytes;
   return HC_OK;
 }
 }  // namespace hc
@@ -712,11 +741,11 @@ extern "C" int hc_decode_attn_append_noalloc(int dtype, int64_t B, int64_t Hq, i
   const bool bitmap = mask != nullptr || held_len > 0;
   const int splits = decode_call_shape(dtype_size(dtype), B, Hq, Hk, D, S - 1, num_splits, bitmap).splits;
   const int64_t need = decode_layout(B, Hq, Hk, D, S, splits, 0).total;
-  if (need > kNoAllocScratchBytes)
+  if (need > kNoAllocSlotBytes)
     return set_error(HC_ERR_WORKSPACE,
                      "decode_append_noalloc: %d key splits over %lld (batch, kv head) units need %lld bytes of "
                      "scratch, above the static maximum of %lld bytes; use fewer splits or hc_decode_attn_append",
-                     splits, (long long)(B * Hk), (long long)need, (long long)kNoAllocScratchBytes);
+                     splits, (long long)(B * Hk), (long long)need, (long long)kNoAllocSlotBytes);
   void* ws = nullptr;
   int rc = scratch_address(stream, &ws);
   if (rc != HC_OK) return rc;
@@ -724,5 +753,5 @@ extern "C" int hc_decode_attn_append_noalloc(int dtype, int64_t B, int64_t Hq, i
                                k_new, kn_sb, kn_sh, v_new, vn_sb, vn_sh, p_new, pn_sb, pn_sh, p_dst, pd_sb, pd_sh,
                                pd_ss, pos_new, posn_sb, pos_dst, posd_sb, mask, mask_sb, held_len, held_pos, hp_sb,
                                hp_sh, held_valid, hv_sb, hv_sh, cur_pos, scaling, out, o_sb, o_sh, ws,
-                               kNoAllocScratchBytes, num_splits, stream);
+                               kNoAllocSlotBytes, num_splits, stream);
 }

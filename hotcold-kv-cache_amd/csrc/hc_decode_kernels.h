@@ -94,9 +94,11 @@ struct DecodeArgs {
   int64_t posn_sb;
   int64_t* pos_dst;
   int64_t posd_sb;
-  // In-kernel merge of the split partials (splits > 1): one arrival counter
-  // per (b, kv head), zero between launches; NULL = a second merge kernel.
-  uint32_t* counters;
+  // In-kernel merge of the split partials (splits > 1): one arrival word
+  // per (b, kv head), [launch tag : 32 | arrivals : 32], any initial
+  // contents; NULL = a second merge kernel.  epoch is this launch's tag.
+  unsigned long long* counters;
+  uint32_t epoch;
 };
 static_assert(offsetof(DecodeArgs, Hq) + sizeof(int) <= 128, "prologue fields must fit the first 128 bytes");
 
@@ -843,17 +845,44 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     // accesses, so no L2 write-back or invalidation is needed: each thread
     // waits until its stores have completed, the workgroup's arrival is
     // counted after that, and the merging workgroup reads only after it has
-    // seen every other arrival.  It leaves the counter at zero again.
+    // seen every other arrival.  (The ordering between the partials and the
+    // count rests on those completed stores, not on release/acquire: an
+    // agent-scope release writes back the whole L2 of the XCD, which had
+    // made one 5-split launch 19-20 us instead of 9.)
+    //
+    // Arrivals are counted under this launch's tag: the upper half of the
+    // unit's word.  An arrival that finds another launch's tag (left by an
+    // earlier launch, or garbage) re-registers with a compare-and-swap as the
+    // tag's first arrival, so no count a launch left behind can make a
+    // workgroup merge early.  Every failed swap means another workgroup of
+    // the unit changed the word (at most twice each), so the loop is bounded
+    // by 2 * splits + 1 rounds.  The merging workgroup leaves (tag, 0), so a
+    // launch replayed with the same tag (a captured graph) counts from zero.
     __shared__ uint32_t sm_last;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (threadIdx.x == 0)
-      sm_last = __hip_atomic_fetch_add(a.counters + unit, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                (uint32_t)(a.splits - 1);
+    unsigned long long* word = a.counters + unit;
+    const unsigned long long tag = (unsigned long long)a.epoch << 32;
+    if (threadIdx.x == 0) {
+      unsigned long long old = __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      unsigned long long mine = old + 1;
+      if ((old & 0xffffffff00000000ull) != tag) {
+        unsigned long long cur = mine;
+        for (int round = 0; round <= 2 * a.splits; ++round) {
+          const unsigned long long want = ((cur & 0xffffffff00000000ull) == tag) ? cur + 1 : (tag | 1ull);
+          if (__hip_atomic_compare_exchange_strong(word, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)) {
+            mine = want;
+            break;
+          }
+        }
+      }
+      sm_last = (uint32_t)mine == (uint32_t)a.splits;
+    }
     __syncthreads();
     if (sm_last) {
       merge_partials<T, true>(a, b, hk, D, threadIdx.x, 64 * NW);
-      if (threadIdx.x == 0) __hip_atomic_store(a.counters + unit, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) __hip_atomic_store(word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

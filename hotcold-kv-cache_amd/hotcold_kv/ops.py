@@ -44,15 +44,15 @@ def _ptr(t):
     return None if t is None else t.data_ptr()
 
 
-# Leading bytes of a decode workspace that must be zero before its first
-# launch (the in-kernel split merge's arrival counters; launches leave them
-# zero).  The rest of every workspace needs no initialisation.
+# Leading bytes of a decode workspace that hold the in-kernel split merge's
+# arrival words.  They need no initialisation (each launch counts under its
+# own tag); a new workspace still starts them at zero.
 DECODE_COUNTER_BYTES = 16384
 
 
 def _workspace(kind, device, nbytes):
     """A uint8 workspace of at least nbytes for this stream, allocated once and
-    grown geometrically; a new decode workspace gets its counter block zeroed."""
+    grown geometrically."""
     key = (kind, device.index if device.index is not None else torch.cuda.current_device(),
            _stream_handle(device))
     with _ws_lock:

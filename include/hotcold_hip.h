@@ -75,10 +75,10 @@ int hc_read_bytes(const void* p, int64_t bytes, uint32_t* sink, void* stream);
  *     merged inside the launch by the last workgroup of each (b, kv head) to
  *     finish (by a second kernel above 4096 units).  The workspace must hold
  *     hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, with_evict)
- *     bytes.  Its first 16384 bytes (the merge's arrival counters) must be
- *     zero before the first launch on it, and every launch leaves them zero;
- *     the rest needs no initialisation.  One workspace must not be used by
- *     two launches that may overlap.
+ *     bytes.  It needs no initialisation: its first 16384 bytes hold the
+ *     merge's arrival words, counted under a tag of each launch's own, so
+ *     whatever a workspace holds cannot trigger an early merge.  One
+ *     workspace must not be used by two launches that may overlap.
  *   dropout must be 0.0.
  */
 int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hk, int64_t D,
@@ -193,13 +193,14 @@ int64_t hc_decode_append_args_size(void);
  * It is for callers that cannot allocate (code under HIP graph capture, tight
  * serving loops, harnesses that forbid hipMalloc).  The arguments and results
  * are hc_decode_attn_append's, minus (workspace, workspace_bytes); the split
- * partials and merge counters live in a static 8 MiB device array (zero at
- * load) that each GPU holds until the process ends.  Its address is taken
- * once per device on the first call (the
- * current device must be the stream's device).  A call whose partials need
- * more than 8 MiB returns HC_ERR_WORKSPACE (fewer splits fit).  Every call on
- * one GPU shares that GPU's array: calls that may overlap on one GPU (two
- * streams) race.  Nothing is allocated or freed.
+ * partials and merge words live in a static 32 MiB device array that each
+ * GPU holds until the process ends: four 8 MiB regions, one per stream.  The
+ * array's address is taken once per device on the first call (the current
+ * device must be the stream's device), and a stream's first call binds it a
+ * free region for the rest of the process, so calls on different streams
+ * never share partials.  A call from a fifth stream of one device returns
+ * HC_ERR_INVALID; a call whose partials need more than 8 MiB returns
+ * HC_ERR_WORKSPACE (fewer splits fit).  Nothing is allocated or freed.
  */
 int hc_decode_attn_append_noalloc(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, int64_t S,
                                   const void* q, int64_t q_sb, int64_t q_sh,

@@ -82,7 +82,7 @@ def test_decode_split_merge_paths(B, S, splits, dtype):
     v = _randn((B, Hk, S, D), 23, dtype)
     sc = 1.0 / math.sqrt(D)
     want = ref.decode_attention(q, k, v, sc)
-    for rep in range(3):    # repeated launches on one workspace: the counters must come back to zero
+    for rep in range(3):    # repeated launches on one workspace: each counts under its own tag
         out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), sc, num_splits=splits)
         assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype], rep
     # the fused append through the same shapes: rows 0..S-2 cached, the token attended as key S-1
@@ -93,7 +93,43 @@ def test_decode_split_merge_paths(B, S, splits, dtype):
     torch.cuda.synchronize()
     for key, ws in ops._ws_cache.items():
         if key[0] == "decode":
-            assert int(ws[:ops.DECODE_COUNTER_BYTES].count_nonzero()) == 0
+            # every merge leaves its unit's word at (tag, 0 arrivals)
+            words = ws[:ops.DECODE_COUNTER_BYTES].view(torch.int64)
+            assert int((words & 0xffffffff).count_nonzero()) == 0
+
+
+@pytest.mark.parametrize("fill", ["random", "ones", "counts_left_behind"])
+def test_decode_split_merge_ignores_stale_counter_words(fill):
+    """The in-kernel merge's arrival words may hold anything before a launch
+    (a launch cut short, a caller's uninitialised workspace): each launch
+    counts under its own tag, so the output is the same bits as on a zeroed
+    block."""
+    B, Hq, Hk, S, D, splits = 1, 32, 8, 2431, 128, 16
+    dtype = torch.float16
+    q = _randn((B, Hq, 1, D), 31, dtype).to(DEV)
+    k = _randn((B, Hk, S, D), 32, dtype).to(DEV)
+    v = _randn((B, Hk, S, D), 33, dtype).to(DEV)
+    sc = 1.0 / math.sqrt(D)
+    ws = ops._workspace("decode", torch.device(DEV), 1)     # the stream's decode workspace
+    ws[:ops.DECODE_COUNTER_BYTES].zero_()
+    clean = ops.decode_attention(q, k, v, sc, num_splits=splits).clone()
+    torch.cuda.synchronize()
+    ws = ops._workspace("decode", torch.device(DEV), 1)
+    words = ws[:ops.DECODE_COUNTER_BYTES].view(torch.int64)
+    g = torch.Generator().manual_seed(34)
+    if fill == "random":
+        words.copy_(torch.randint(-(1 << 62), 1 << 62, words.shape, generator=g))
+    elif fill == "ones":
+        words.fill_(-1)
+    else:
+        # another launch's tag with splits-1 arrivals: a plain counter would
+        # let this launch's first arrival merge alone
+        words.copy_(torch.full(words.shape, (12345 << 32) + splits - 1, dtype=torch.int64))
+    torch.cuda.synchronize()
+    out = ops.decode_attention(q, k, v, sc, num_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(out, clean), fill
+    assert np.abs(out.float().cpu().numpy() - ref.decode_attention(q.cpu(), k.cpu(), v.cpu(), sc)).max() <= TOL[dtype]
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])

@@ -6,7 +6,8 @@ hc_decode_attn_append (the same kernels, the same split choice) on the same
 inputs: the output and the appended rows.  Two calls run back to back, the
 second on a smaller input, so the second reads a scratch array that still
 holds the first call's partials; a call whose partials would exceed the
-array is refused.
+array is refused.  Each stream of a device gets a region of its own, so a
+call on a second stream gives the same bits; a fifth stream is refused.
 """
 
 import pytest
@@ -135,3 +136,43 @@ def test_noalloc_refuses_oversized_partials():
                     None, 0, 0, None, 0, 0, None, 0, 0, None, 0.088, out.data_ptr(), 0, D, 64, stream)
     assert rc == N.HC_ERR_WORKSPACE
     assert "static maximum" in N.lib().hc_last_error().decode()
+
+
+def test_noalloc_streams_get_own_regions_and_a_fifth_is_refused():
+    """Calls on other streams use regions of their own (the same bits as the
+    workspace entry point); once four streams of the device are bound, a
+    call from a fifth is refused.  torch's current stream, which the tests
+    above bound, stays bound, so noalloc calls on it still work after this."""
+    lib = N.lib()
+    t = _case(2, 32, 8, 128, 700, torch.float16, 16, seed=77)
+    (o_ws, k_ws, _, _, _), _ = _run_pair(t, 5)
+    cur = torch.cuda.current_stream()
+    others = [torch.cuda.Stream() for _ in range(4)]
+    results = []
+    refused = None
+    for s in [cur] + others:
+        c = dict(t)
+        for name in ("k", "v", "pd", "posd"):
+            c[name] = t[name].clone()
+        out = torch.full_like(o_ws, float("nan"))
+        torch.cuda.synchronize()
+        rc = _noalloc()(*_args(c, out), 5, s.cuda_stream)
+        torch.cuda.synchronize()
+        if rc != N.HC_OK:
+            refused = (s, rc, lib.hc_last_error().decode())
+            break
+        results.append((out, c["k"]))
+    # the current stream plus three more fit; the fourth new stream does not
+    assert len(results) == 4, refused
+    assert refused is not None and refused[0] is others[-1] and refused[1] == N.HC_ERR_INVALID
+    assert "streams" in refused[2]
+    for out, kk in results:
+        assert torch.equal(out, o_ws) and torch.equal(kk, k_ws)
+    # the bound streams keep working
+    c = dict(t)
+    for name in ("k", "v", "pd", "posd"):
+        c[name] = t[name].clone()
+    out = torch.full_like(o_ws, float("nan"))
+    N.check(_noalloc()(*_args(c, out), 5, others[0].cuda_stream), "hc_decode_attn_append_noalloc")
+    torch.cuda.synchronize()
+    assert torch.equal(out, o_ws)
