@@ -1,6 +1,7 @@
 """Knobs of the compression baselines (src/hotcold_kv/baselines/config.py:4-48)."""
 
 from dataclasses import dataclass
+from typing import Optional
 
 
 @dataclass
@@ -18,7 +19,8 @@ class PressConfig:
     defer_compaction: compact every layer's prompt together after the last
         layer's prefill, in one launch set, instead of one layer at a time
         (same kept indices; prompt K/V stay alive until then, up to
-        defer_max_bytes).  Not a knob of the reference.
+        defer_max_bytes, by default an eighth of the device's memory and at
+        most 16 GiB).  Not a knob of the reference.
     """
 
     method: str = "snapkv"
@@ -29,7 +31,7 @@ class PressConfig:
     pyramid_beta: int = 20
     num_layers: int = 32
     defer_compaction: bool = True
-    defer_max_bytes: int = 16 << 30
+    defer_max_bytes: Optional[int] = None
 
     def __post_init__(self):
         assert self.method in ("snapkv", "pyramidkv", "h2o"), f"unknown method {self.method}"

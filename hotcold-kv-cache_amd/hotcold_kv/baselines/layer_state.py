@@ -32,22 +32,36 @@ class DeferredCompaction:
     one gather into every layer's hot buffer per budget.  The kept indices are
     the ones each layer would get on its own, bit for bit.
 
-    Pending layers keep their whole prompt K/V alive until then; past
-    max_pending_bytes the pending layers are compacted early.
+    Pending layers keep their prompt K/V (and a copy of their window's query
+    rows) alive until then; past max_pending_bytes the pending layers are
+    compacted early.  By default that limit is an eighth of the device's
+    memory, at most 16 GiB, so deferring cannot take a device that fitted the
+    per-layer compaction far past its memory.
     """
 
-    def __init__(self, max_pending_bytes=16 << 30):
-        self.max_pending_bytes = int(max_pending_bytes)
+    DEFAULT_MAX_BYTES = 16 << 30
+
+    def __init__(self, max_pending_bytes=None):
+        self.max_pending_bytes = None if max_pending_bytes is None else int(max_pending_bytes)
         self.pending = []
         self.pending_bytes = 0
 
+    def _limit(self, device):
+        if self.max_pending_bytes is None:
+            total = torch.cuda.get_device_properties(device).total_memory
+            self.max_pending_bytes = min(self.DEFAULT_MAX_BYTES, total // 8)
+        return self.max_pending_bytes
+
     def add(self, state, q_post, k_post, v, scaling):
-        """Hold one layer's prompt (the query tensor is kept as is: its window
-        rows are read in place) until flush."""
-        self.pending.append((state, q_post, k_post, v, float(scaling)))
-        self.pending_bytes += sum(t.numel() * t.element_size() for t in (q_post, k_post, v))
+        """Hold one layer's prompt until flush: its keys and values as they
+        are, and a copy of the query's window rows (the only query rows the
+        scores read)."""
+        W = min(state.window_size, int(q_post.shape[2]))
+        q_win = q_post[:, :, q_post.shape[2] - W:].contiguous()
+        self.pending.append((state, q_win, k_post, v, float(scaling)))
+        self.pending_bytes += sum(t.numel() * t.element_size() for t in (q_win, k_post, v))
         state._deferred = self
-        if self.pending_bytes > self.max_pending_bytes:
+        if self.pending_bytes > self._limit(k_post.device):
             self.flush()
 
     def flush(self):

@@ -965,15 +965,31 @@ class KVController:
 
     def _flush_searches(self):
         """Launch the pending device searches on the search stream, behind one
-        event recorded now on the decode stream (after every pooled query)."""
+        event recorded now on the decode stream (after every pooled query).
+        If a launch fails, the searches not launched yet give their slots back
+        (the failing one frees its own) before the error propagates, so their
+        layers can schedule again."""
         pending, self._pending_search = self._pending_search, []
         if not pending:
             return
+        launched = 0
+        try:
+            self._record_flush_event()
+            for i, (li, slot, dindex) in enumerate(pending):
+                self._launch_device_search(li, slot, dindex, self._flush_event if i == 0 else None)
+                launched = i + 1
+        except BaseException:
+            for li, slot, _ in pending[launched:]:
+                with self._retrieval_lock[li]:
+                    if slot.state == _Slot.FILLING:
+                        slot.state = _Slot.FREE
+            raise
+
+    def _record_flush_event(self):
+        """Record the event the step's device searches wait on, on the decode stream."""
         if self._flush_event is None:
             self._flush_event = self._event(0)
         N.check(N.lib().hc_event_record(self._flush_event, ops_stream(self._device)), "hc_event_record")
-        for i, (li, slot, dindex) in enumerate(pending):
-            self._launch_device_search(li, slot, dindex, self._flush_event if i == 0 else None)
 
     def _settle_search(self, li):
         """Before the layer's store takes new tokens: its pending device search

@@ -421,6 +421,35 @@ def test_a_search_failing_on_its_worker_raises_once_and_frees_its_slot():
     assert ctrl._retrieval_ready_cpu[0] is not None
 
 
+def test_a_failed_device_search_launch_frees_the_searches_after_it():
+    """When one of a step's device searches fails to launch, the searches
+    queued after it give their slots back (the failing one frees its own,
+    the ones already launched stay with their gather jobs) and the error
+    propagates; the layer can schedule again afterwards."""
+    ctrl = _ctrl()
+    _fill(ctrl)
+    slots = [ctrl._take_slot(0) for _ in range(3)]
+    assert all(sl is not None and sl.state == _Slot.FILLING for sl in slots)
+    ctrl._pending_search = [(0, sl, object()) for sl in slots]
+    calls = []
+
+    def launch(li, slot, dindex, wait_event):
+        calls.append(slot)
+        if len(calls) == 2:
+            raise RuntimeError("launch refused")
+
+    ctrl._launch_device_search = launch
+    ctrl._record_flush_event = lambda: None
+    with pytest.raises(RuntimeError, match="launch refused"):
+        ctrl._flush_searches()
+    assert calls == slots[:2]
+    assert slots[0].state == _Slot.FILLING                    # launched: its job owns it
+    assert slots[1].state == _Slot.FREE and slots[2].state == _Slot.FREE
+    assert ctrl._pending_search == []
+    slots[0].state = _Slot.FREE
+    assert ctrl._take_slot(0) is not None
+
+
 def test_destroying_a_store_waits_for_its_search():
     """A store freed while a search job reads it (a controller collected with
     a search in flight) is freed only after the job has finished."""
