@@ -607,6 +607,53 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
     return out
 
 
+def measure_compaction_layer(w, dev, reps=12):
+    """One layer's SnapKV compaction of a workload at its full batch (window
+    scores, kept indices, gather of K and V into the budget), N(0,1) inputs,
+    timed differentially after the cache sweep, median of `reps`.  Printed
+    alone by --compaction-only, for per-kernel profiles of the larger
+    windows."""
+    import torch
+    from hotcold_kv import ops
+    g = torch.Generator(device=dev).manual_seed(11)
+    dt, D, Hk, Hq = w.dtype, w.head_dim, w.hk, w.hq
+    B, S, W = w.batch, w.seq_len, min(w.window, w.seq_len)
+    q_post = torch.randn((B, Hq, S, D), generator=g, device=dev, dtype=dt)
+    k_post = torch.randn((B, Hk, S, D), generator=g, device=dev, dtype=dt)
+    v = torch.randn((B, Hk, S, D), generator=g, device=dev, dtype=dt)
+    kb = torch.empty((B, Hk, w.budget, D), dtype=dt, device=dev)
+    vb = torch.empty_like(kb)
+    st, flush = torch.cuda.Stream(dev), CacheSweep(dev)
+
+    def compact(i):
+        sc = ops.snapkv_scores(q_post, k_post, W, w.scaling, w.pool, "maxpool")
+        keep = ops.keep_index(sc, W, w.budget)
+        ops.gather_rows(keep, [(k_post, kb), (v, vb)])
+
+    with torch.cuda.stream(st):
+        compact(0)
+    ms = differential_ms(st, flush, compact, reps)
+    # one plain read of the keys (a known byte count: the calibration of the
+    # FETCH_SIZE counter in the same run)
+    from hotcold_kv import _native as N
+    kbytes = k_post.numel() * k_post.element_size()
+    N.check(N.lib().hc_read_bytes(k_post.data_ptr(), kbytes, None, torch.cuda.current_stream(dev).cuda_stream),
+            "hc_read_bytes")
+    torch.cuda.synchronize()
+    sflops = 2.0 * B * Hk * W * S * D
+    out = {"workload": w.name, "batch": B, "seq_len": S, "window": W, "budget": w.budget,
+           "calibration_read_bytes": int(kbytes),
+           "ms_per_layer": round(ms, 4), "scoring_flop_per_layer": int(sflops),
+           "scoring_tflops_fp64": round(sflops / (ms * 1e-3) / 1e12, 2),
+           "scoring_mfma_frac": round(sflops / (ms * 1e-3) / 1e12 / FP64_MFMA_PEAK_TFLOPS, 4),
+           "fp64_floor_ms": round(sflops / (FP64_MFMA_PEAK_TFLOPS * 1e12) * 1e3, 4),
+           "bytes_per_layer": int(compaction_bytes(w, B))}
+    del q_post, k_post, v, kb, vb
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def measure_device_search(w, dev, st, flush, g, reps=12):
     """One layer's device search index at the workload's cold-store size:
     every sequence's evicted prompt tokens (seq_len - budget of them, N(0,1)
@@ -977,6 +1024,8 @@ def main():
                     help="only the hot/cold pipeline of the 16k held-slot workload (one JSON object)")
     ap.add_argument("--device-search-only", action="store_true",
                     help="only the device search index figures of the 16k/32k/64k workloads (one JSON object)")
+    ap.add_argument("--compaction-only", metavar="WORKLOAD",
+                    help="only one layer's compaction of WORKLOAD at its full batch (one JSON object; for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py: this build measures one GPU only; the hot tier shards by batch and KV head "
@@ -1002,6 +1051,10 @@ def main():
         print(json.dumps({"device_search": {name: measure_device_search(synthetic.WORKLOADS[name], dev, st, flush, g)
                                              for name in ("llama8b_16k_b1024_held64", "b16_32k_b2048_held128",
                                                           "bf16_b4_64k_b4096_held256")}}), flush=True)
+        return
+    if args.compaction_only:
+        print(json.dumps({"compaction_layer": measure_compaction_layer(synthetic.WORKLOADS[args.compaction_only],
+                                                                       dev)}), flush=True)
         return
     if args.pipeline_only:
         print(json.dumps({"hotcold_pipeline": hotcold_pipeline(synthetic.WORKLOADS["llama8b_16k_b1024_held64"],

@@ -27,7 +27,14 @@
 namespace hc {
 
 constexpr int kChunkM = 128;  // keys per logits workgroup (4 waves x 32 keys)
-constexpr int kRowBlk = 32;   // window rows per logits workgroup (fp64 accumulators)
+constexpr int kRowBlk = 32;   // window rows per logits workgroup up to a window of 32
+constexpr int kRowBlkWide = 64;  // ... and for longer windows
+
+// Window rows per logits workgroup: a window of up to 32 rows in one block
+// of 32; longer windows in blocks of 64, so each key slice is loaded and
+// converted once for twice the matrix work (with blocks of 32 a window of 64
+// read every key twice: 2.4 GB of fetch for 1.07 GB of keys at 32k x 16).
+static int64_t row_block(int64_t W) { return W > kRowBlk ? kRowBlkWide : kRowBlk; }
 constexpr int kMaxPool = 32;  // max half-width of the pooling window
 
 struct ScoreLayout {
@@ -46,7 +53,7 @@ static int64_t al256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 
 static ScoreLayout score_layout(int64_t B, int64_t Hk, int64_t S, int64_t D, int64_t W) {
   ScoreLayout L;
-  L.wpad = cdiv(W, kRowBlk) * kRowBlk;
+  L.wpad = cdiv(W, row_block(W)) * row_block(W);
   L.nchunk_m = cdiv(S, kChunkM);
   L.qf_off = 0;
   L.logits_off = al256(L.qf_off + B * Hk * L.wpad * D * 8);
@@ -152,10 +159,10 @@ struct KOperand<float> {
 //   A (16 rows x 4): lane l supplies qf[w0 + 16*nb + l%16][4t + l/16]
 //   B (4 x 16 keys): lane l supplies k[key0 + 16*mb + l%16][4t + l/16]
 //   D: lane l holds rows w0 + 16*nb + l/16 + 4i, key key0 + 16*mb + l%16
-// grid (ceil(S / (128*cpw)), Hk * nrb, B), block 256.  The 32 x D
-// fp64 query block is staged in LDS once and reused for cpw chunks
-// of 128 keys; per chunk each wave covers 32 keys (two 16-key blocks) x 32
-// window rows (two 16-row blocks).  K loads are unconditional buffer loads
+// grid (ceil(S / (128*cpw)), Hk * nrb, B), block 256.  The ROWS x D
+// fp64 query block (ROWS = 32 or 64 window rows, 16 * NRB) is staged in LDS
+// once and reused for cpw chunks of 128 keys; per chunk each wave covers 32
+// keys (two 16-key blocks) x ROWS window rows (NRB 16-row blocks).  K loads are unconditional buffer loads
 // ahead of use (rows past S read zeros).  With the head dim known at compile
 // time (DC > 0) the dim loop is unrolled over a register ring of kKRing
 // slices, kKRing - 1 of them in flight while one is multiplied, and the ring
@@ -174,15 +181,16 @@ constexpr int kNeverRead = 512;  // > the 256 (rowsum) and 270 (imp_pool) read m
 constexpr int kLogitTargetWg = 1024;
 constexpr int kKRing = 4;
 
-template <typename T, int MODE, int DC>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) void logits_kernel(
+template <typename T, int MODE, int DC, int NRB>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, NRB == 2 ? 4 : 2))) void logits_kernel(
     const T* __restrict__ k, const T* const* __restrict__ k_rows, int64_t k_sb, int64_t k_sh, int64_t k_ss,
     uint32_t k_bytes, const double* __restrict__ qf, int Hk, int S, int Drt, int W, int wpad, double scaling,
     int cpw, float* __restrict__ logits, uint32_t* __restrict__ rmax) {
+  constexpr int ROWS = 16 * NRB;  // window rows of the workgroup: NRB 16-row MFMA blocks
   const int D = DC > 0 ? DC : Drt;
-  extern __shared__ double sq[];  // [32][D + 1] window-row block of qf
-  __shared__ float red[4][kRowBlk];
-  const int nrb = wpad / kRowBlk;
+  extern __shared__ double sq[];  // [ROWS][D + 1] window-row block of qf
+  __shared__ float red[4][ROWS];
+  const int nrb = wpad / ROWS;
   // Workgroup -> (row block, key range, head), row block fastest.  The
   // hardware hands consecutive workgroups to the eight XCDs in turn; with a
   // window as long as the prompt, a key range's work grows with the row
@@ -199,8 +207,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   const int b = blockIdx.z;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int col = lane & 15, kk = lane >> 4;
-  const int w0 = rb * kRowBlk;
-  const int nw = min(kRowBlk, W - w0);
+  const int w0 = rb * ROWS;
+  const int nw = min(ROWS, W - w0);
   const int64_t bh = (int64_t)b * Hk + h;
   const int ld = D + 1;
   // k_rows (may be NULL): row b's keys start at k_rows[b] instead of k + b*k_sb
@@ -210,13 +218,12 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   constexpr int DS = KOperand<T>::DSTEP;
   const int qpos0 = S - W + w0;
   const uint32_t sl = KOperand<T>::sel(kk);
-  const double* q0 = sq + col * ld + kk;         // rows 0..15 of the block
-  const double* q1 = sq + (16 + col) * ld + kk;  // rows 16..31
+  const double* qrow = sq + col * ld + kk;  // row 16 i + col of the block at qrow + 16 i ld
   // this (b, h)'s W x S logits; W * S * 4 < 2^31 is checked by the host
   const __amdgpu_buffer_rsrc_t lrs = make_rsrc(logits + bh * W * S, (uint32_t)((int64_t)W * S * 4));
-  float mrow[8];
+  float mrow[4 * NRB];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) mrow[j] = -INFINITY;
+  for (int j = 0; j < 4 * NRB; ++j) mrow[j] = -INFINITY;
 
   constexpr int NS = DC / DS;  // dim slices per key chunk (compile-time D)
   // the ring runs on into the next chunk: slice s of every chunk must land in
@@ -248,7 +255,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
   }
   const double* qsrc = qf + (bh * wpad + w0) * D;
   if (stage)
-    for (int i = threadIdx.x; i < kRowBlk * D; i += 256) sq[(i / D) * ld + (i % D)] = qsrc[i];
+    for (int i = threadIdx.x; i < ROWS * D; i += 256) sq[(i / D) * ld + (i % D)] = qsrc[i];
   __syncthreads();
 
   // wave-uniform chunk count: short prompts stop at their last chunk
@@ -265,18 +272,22 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     // the q reads repeat for every chunk; keep them inside the loop (hoisted,
     // all D/2 of them would hold 2*D registers for the kernel's lifetime)
     __asm__ volatile("" ::: "memory");
-    doublex4 acc00 = {0.0, 0.0, 0.0, 0.0}, acc01 = acc00, acc10 = acc00, acc11 = acc00;
+    // acc[i][m]: rows 16 i .. of the block against key block m
+    doublex4 acc[NRB][2];
+#pragma unroll
+    for (int i = 0; i < NRB; ++i) acc[i][0] = acc[i][1] = doublex4{0.0, 0.0, 0.0, 0.0};
     auto steps = [&](const KOperand<T>& xa, const KOperand<T>& xb, int d0) {
 #pragma unroll
       for (int hf = 0; hf < DS / 4; ++hf) {  // k-steps t = d0/4 + hf
         const int d = d0 + 4 * hf;
-        const double a0 = q0[d], a1 = q1[d];
         const double b0 = xa.elem(hf, sl);
         const double b1 = xb.elem(hf, sl);
-        acc00 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b0, acc00, 0, 0, 0);
-        acc01 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b0, acc01, 0, 0, 0);
-        acc10 = __builtin_amdgcn_mfma_f64_16x16x4f64(a0, b1, acc10, 0, 0, 0);
-        acc11 = __builtin_amdgcn_mfma_f64_16x16x4f64(a1, b1, acc11, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < NRB; ++i) {
+          const double ai = qrow[16 * i * ld + d];
+          acc[i][0] = __builtin_amdgcn_mfma_f64_16x16x4f64(ai, b0, acc[i][0], 0, 0, 0);
+          acc[i][1] = __builtin_amdgcn_mfma_f64_16x16x4f64(ai, b1, acc[i][1], 0, 0, 0);
+        }
       }
     };
     // ping-pong over pairs of dim chunks (D % 16 == 0); the final pair of
@@ -314,17 +325,13 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     // Epilogue: lane holds rows 16*nbk + kk + 4i for keys 16*mb + col.  The
     // 16 lanes of one row store 64 contiguous bytes and the two key blocks
     // complete the row's 128-byte segment; masked lanes store to kOob.
-    const double r00[4] = {acc00[0], acc00[1], acc00[2], acc00[3]};
-    const double r01[4] = {acc01[0], acc01[1], acc01[2], acc01[3]};
-    const double r10[4] = {acc10[0], acc10[1], acc10[2], acc10[3]};
-    const double r11[4] = {acc11[0], acc11[1], acc11[2], acc11[3]};
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int nbk = 0; nbk < 2; ++nbk) {
+      for (int nbk = 0; nbk < NRB; ++nbk) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
-          const double v = nbk == 0 ? (mb == 0 ? r00[i] : r10[i]) : (mb == 0 ? r01[i] : r11[i]);
+          const double v = acc[nbk][mb][i];
           const int w = 16 * nbk + kk + 4 * i;
           const int key = key0 + 16 * mb + col;
           float L;
@@ -348,7 +355,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int nbk = 0; nbk < 2; ++nbk) {
+      for (int nbk = 0; nbk < NRB; ++nbk) {
 #pragma unroll
         for (int mb = 0; mb < 2; ++mb) {
           const int w = 16 * nbk + kk + 4 * i;
@@ -360,7 +367,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 4))) voi
     key0 += kChunkM;
   }
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {  // row 16*(j/4) + kk + 4*(j%4), max over the 16 key lanes
+  for (int j = 0; j < 4 * NRB; ++j) {  // row 16*(j/4) + kk + 4*(j%4), max over the 16 key lanes
     float m = mrow[j];
     m = fmaxf(m, __shfl_xor(m, 1, 64));
     m = fmaxf(m, __shfl_xor(m, 2, 64));
@@ -647,12 +654,13 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
   float* logits = reinterpret_cast<float*>(ws + lay.logits_off);
   uint32_t* rmax = reinterpret_cast<uint32_t*>(ws + lay.rmax_off);
   RowStat* rstat = reinterpret_cast<RowStat*>(ws + lay.rstat_off);
-  const int nrb = (int)(lay.wpad / kRowBlk);
+  const int rows = (int)row_block(W);
+  const int nrb = (int)(lay.wpad / rows);
   hipLaunchKernelGGL(qmean_kernel<T>, dim3((unsigned)lay.wpad, (unsigned)Hk, (unsigned)B),
                      dim3((unsigned)(D < 64 ? 64 : D)), 0, st, (const T*)q, (const T* const*)q_rows, q_sb, q_sh,
                      q_ss, q_row0, (int)Hq,
                      (int)Hk, (int)W, (int)lay.wpad, (int)D, qf, rmax, rstat);
-  const size_t lds = (size_t)(kRowBlk * (D + 1) * 8);
+  const size_t lds = (size_t)(rows * (D + 1) * 8);
   const uint32_t k_bytes = (uint32_t)(((S - 1) * k_ss + D) * (int64_t)sizeof(T));
   const int64_t wg1 = cdiv(S, (int64_t)kChunkM) * Hk * nrb * B;  // workgroups at one chunk each
   const int cpw = (int)std::max<int64_t>(1, std::min<int64_t>(kLogitChunks, wg1 / kLogitTargetWg));
@@ -665,12 +673,19 @@ static void launch_score(const ScoreLayout& lay, char* ws, int mode, int64_t B, 
                        (int)Hk, (int)S, (int)D, (int)W, (int)lay.wpad, scal, cpw, logits, rmax);
   };
   if (mode == HC_SCORE_SNAPKV) {
-    if (D == 128) launch(logits_kernel<T, HC_SCORE_SNAPKV, 128>);
-    else if (D == 64) launch(logits_kernel<T, HC_SCORE_SNAPKV, 64>);
-    else launch(logits_kernel<T, HC_SCORE_SNAPKV, 0>);
+    if (rows == kRowBlk) {
+      if (D == 128) launch(logits_kernel<T, HC_SCORE_SNAPKV, 128, 2>);
+      else if (D == 64) launch(logits_kernel<T, HC_SCORE_SNAPKV, 64, 2>);
+      else launch(logits_kernel<T, HC_SCORE_SNAPKV, 0, 2>);
+    } else {
+      if (D == 128) launch(logits_kernel<T, HC_SCORE_SNAPKV, 128, 4>);
+      else if (D == 64) launch(logits_kernel<T, HC_SCORE_SNAPKV, 64, 4>);
+      else launch(logits_kernel<T, HC_SCORE_SNAPKV, 0, 4>);
+    }
   } else {
     // the raw sums' fp64 divides leave no registers for the unrolled ring
-    launch(logits_kernel<T, HC_SCORE_RAWSUM, 0>);
+    if (rows == kRowBlk) launch(logits_kernel<T, HC_SCORE_RAWSUM, 0, 2>);
+    else launch(logits_kernel<T, HC_SCORE_RAWSUM, 0, 4>);
   }
   if (mode == HC_SCORE_SNAPKV) {
     // rows split across the waves of a workgroup (1, 2 or 4 per row) when
@@ -726,7 +741,7 @@ static int score_impl(int dtype, int mode, int64_t B, int64_t Hq, int64_t Hk, in
              (long long)W, (long long)S);
   HC_REQUIRE(D % 16 == 0 && D <= 512, "score: head_dim %lld must be a multiple of 16 and <= 512", (long long)D);
   HC_REQUIRE(S <= ((int64_t)1 << 19), "score: S %lld above 2^19 (fixed-point normaliser range)", (long long)S);
-  HC_REQUIRE(B <= 65535 && Hk * cdiv(W, kRowBlk) <= 65535, "score: grid too large");
+  HC_REQUIRE(B <= 65535 && Hk * cdiv(W, row_block(W)) <= 65535, "score: grid too large");
   HC_REQUIRE(q_row0 >= 0, "score: negative q_row0");
   HC_REQUIRE((q || q_rows) && (k || k_rows) && scores, "score: null pointer");
   const int es = dtype_size(dtype);
