@@ -61,6 +61,12 @@ METRIC = "decode µs/layer & SnapKV compact ms (8k→512); % of HBM peak GB/s on
 HBM_PEAK_GBS = 8000.0
 FP64_MFMA_PEAK_TFLOPS = 78.6
 FLUSH_BYTES = 512 << 20
+# Layers of the hot/cold loop at the larger held-slot shapes: the host cold
+# store holds fp32 pre-RoPE keys and values for every prompt position (1 KB
+# per token and KV head), 4.3 GB per layer at 32k x 16 and 2.1 GB at 64k x 4,
+# and half as much again once a host search computes its vectors; these
+# counts keep each run near 70 GB of host memory (105 GB with the vectors).
+PIPELINE_LAYERS = {"b16_32k_b2048_held128": 16, "bf16_b4_64k_b4096_held256": 32}
 
 
 class CacheSweep:
@@ -808,7 +814,7 @@ def _mean_us(ms):
     return round(statistics.fmean(ms) * 1e3, 1) if ms else None
 
 
-def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
+def hotcold_pipeline(w, dev, profile_steps=None, device_search=True, layers=None, step_sync=False):
     """The hot/cold engine's own loop at a held-slot workload, through
     hotcold_attention (the patched attention's body between RoPE and o_proj):
       prefill  every layer's prompt appended to its HotColdLayer and
@@ -826,13 +832,21 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
     budget - window prefix tokens, so the prompt is cut to the budget once and
     decode appends without re-compression.  The prompt's own attention (torch
     SDPA in the patch) is not run: it is not part of the hot tier.  Inputs are
-    the workload's synthetic tokens, generated on the device beforehand."""
+    the workload's synthetic tokens, generated on the device beforehand.
+    layers: how many of the model's layers to run (default all); where the
+    prompts of all of them would take more than a quarter of device memory,
+    each layer's prompt is generated just before its update and freed after
+    it, and the prefill time is the sum of the updates alone.
+    step_sync: end every step by waiting for the decode stream, as a generate
+    loop does when it reads the step's sampled token back to the host; without
+    it the issuing thread runs ahead of the GPU by as many steps as the queue
+    holds, and a search issued in one window may not have run by the next."""
     import torch
     from hotcold_kv import KVController, synthetic
     from hotcold_kv import patch as hp
     from hotcold_kv.cache import HotColdLayer
 
-    L, B, G = w.layers, w.batch, w.group
+    L, B, G = int(layers or w.layers), w.batch, w.group
     cap = w.budget + w.decode_steps
     topk = w.budget - w.window
     ctrl = KVController(max_capacity_prompt=cap, topk_ratio=(topk + 0.5) / cap, recent_size=w.window,
@@ -845,21 +859,41 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
     layers = [HotColdLayer(ctrl) for _ in range(L)]
     steps = w.decode_steps if profile_steps is None else profile_steps
     toks = [[synthetic.make_decode_token(w, l, t, seed=0, device=dev) for l in range(L)] for t in range(steps)]
-    prompts = [synthetic.make_prompt(w, layer=l, seed=0, device=dev) for l in range(L)]   # inputs, not timed
-    ctrl._lazy_init(prompts[0]["k_pre"], n_layers=L)
-    windows = [p["q_post"][:, :, -w.window:, :].contiguous() for p in prompts]
+    esize = torch.empty((), dtype=w.dtype).element_size()
+    prompt_bytes = B * w.seq_len * w.head_dim * esize * (2 * w.hq + 3 * w.hk)
+    lazy = L * prompt_bytes > torch.cuda.get_device_properties(dev).total_memory // 4
+
+    def prompt(l):
+        p = synthetic.make_prompt(w, layer=l, seed=0, device=dev)
+        return p, p["q_post"][:, :, -w.window:, :].contiguous()
+
+    prompts = [] if lazy else [prompt(l) for l in range(L)]      # inputs, not timed
+    first = prompts[0][0] if prompts else prompt(0)[0]
+    ctrl._lazy_init(first["k_pre"], n_layers=L)
+    del first
+    prefill_s = 0.0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for l in range(L):
-        p = prompts[l]
-        layers[l].set_last_query_post(windows[l])
+        if lazy:
+            p, win = prompt(l)
+            torch.cuda.synchronize()
+            tl = time.perf_counter()
+        else:
+            p, win = prompts[l]
+        layers[l].set_last_query_post(win)
         layers[l].update(key_states=p["k_post"], value_states=p["v"], layer_idx=l,
                          cache_kwargs={"pre_key_states": p["k_pre"], "positions": p["positions"]})
+        if lazy:
+            torch.cuda.synchronize()
+            prefill_s += time.perf_counter() - tl
+            del p, win
     torch.cuda.synchronize()
-    prefill_s = time.perf_counter() - t0
+    if not lazy:
+        prefill_s = time.perf_counter() - t0
     ctrl.wait_cold_adds()
     prefill_store_s = time.perf_counter() - t0
-    del prompts, windows, p
+    del prompts
     step_ms = []
     torch.cuda.synchronize()
     t_all = time.perf_counter()
@@ -869,6 +903,8 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
             k = toks[t][l]
             hp.hotcold_attention(ctrl, layers[l], l, k["q_pre"], k["k_pre"], k["v"], k["q_post"], k["k_post"],
                                  k["position"], G, w.scaling)
+        if step_sync:
+            torch.cuda.current_stream().synchronize()
         step_ms.append((time.perf_counter() - ts) * 1e3)
     t_issue = time.perf_counter()
     torch.cuda.synchronize()
@@ -882,14 +918,18 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True):
     other = [step_ms[t] for t in range(steps) if t not in retr_steps]
     out = {
         "workload": w.name, "layers": L, "batch": B, "prompt": w.seq_len, "budget": w.budget, "held": w.held,
-        "retrieve_every": w.retrieve_every, "decode_steps": steps,
+        "retrieve_every": w.retrieve_every, "decode_steps": steps, "step_sync": step_sync,
         "prefill_compress_evict_s": round(prefill_s, 3),
         "prefill_cold_store_filled_s": round(prefill_store_s, 3),
-        "prefill_timing": "32 layers' compaction + eviction through HotColdLayer.update, decode thread's wall "
-                          "time (cold-store adds still running on the library's workers), then until every add "
-                          "is applied; prompt generation not timed",
+        "prefill_timing": (f"{L} layers' compaction + eviction through HotColdLayer.update, decode thread's "
+                           "wall time (cold-store adds still running on the library's workers), then until every "
+                           "add is applied; prompt generation not timed"
+                           + ("; prompts generated per layer, so the first figure sums the updates and the "
+                              "second includes the generation" if lazy else "")),
         "cold_tokens_per_layer": ctrl.cold_size(0),
         "hot_rows_per_layer_end": layers[0].hot_length(),
+        "step_times": ("step_us_wall_mean: the loop's wall time over the steps; the others: each step on the "
+                       "issuing thread" + (", including its wait for the decode stream" if step_sync else "")),
         "step_us_wall_mean": round(total_ms * 1e3 / steps, 1),
         "step_us_wall_median": round(statistics.median(step_ms) * 1e3, 1),
         "step_us_issue_mean": round(statistics.fmean(step_ms) * 1e3, 1),
@@ -1020,8 +1060,13 @@ def main():
                     help="skip the secondary figures of the 16k/32k/64k workloads and H2O")
     ap.add_argument("--h2o-only", action="store_true",
                     help="only the H2O figures of one layer (one JSON object; for profiling)")
-    ap.add_argument("--pipeline-only", action="store_true",
-                    help="only the hot/cold pipeline of the 16k held-slot workload (one JSON object)")
+    ap.add_argument("--pipeline-only", nargs="?", const="llama8b_16k_b1024_held64", metavar="WORKLOAD",
+                    help="only the hot/cold pipeline of a held-slot workload, by default the 16k one "
+                         "(one JSON object)")
+    ap.add_argument("--pipeline-layers", type=int, default=None,
+                    help="layers of the --pipeline-only run (default: the workload's larger-loop layer count)")
+    ap.add_argument("--pipeline-step-sync", action="store_true",
+                    help="--pipeline-only: wait for the decode stream at the end of every step")
     ap.add_argument("--device-search-only", action="store_true",
                     help="only the device search index figures of the 16k/32k/64k workloads (one JSON object)")
     ap.add_argument("--compaction-only", metavar="WORKLOAD",
@@ -1057,8 +1102,10 @@ def main():
                                                                        dev)}), flush=True)
         return
     if args.pipeline_only:
-        print(json.dumps({"hotcold_pipeline": hotcold_pipeline(synthetic.WORKLOADS["llama8b_16k_b1024_held64"],
-                                                               dev)}), flush=True)
+        pl = args.pipeline_layers or PIPELINE_LAYERS.get(args.pipeline_only)
+        print(json.dumps({"hotcold_pipeline": hotcold_pipeline(synthetic.WORKLOADS[args.pipeline_only], dev,
+                                                               layers=pl, step_sync=args.pipeline_step_sync)}),
+              flush=True)
         return
     log(f"workload {w.name}: generating inputs on {torch.cuda.get_device_name(dev)}")
     stream = stream_rates(dev)
@@ -1126,13 +1173,24 @@ def main():
             others.append(r)
         del flush
 
-    pipe = None
+    pipe = pipe_larger = None
     if not args.no_other_configs and args.workload == "llama8b_8k_b512":
         pw = synthetic.WORKLOADS["llama8b_16k_b1024_held64"]
         log(f"hot/cold pipeline: {pw.name} ...")
         pipe = hotcold_pipeline(pw, dev)
         log(f"  step {pipe['step_us_wall_mean']} us wall ({pipe['layer_us_wall_mean']} us/layer), ready_rate "
             f"{pipe['ready_rate']}, {pipe['retrievals']} retrievals, copy {pipe['copy_ms_mean']} ms")
+        pipe_larger = []
+        for name, pl in PIPELINE_LAYERS.items():
+            for sync in (True, False):
+                log(f"hot/cold pipeline: {name}, {pl} layers, "
+                    f"{'each step synchronized' if sync else 'steps issued ahead'} ...")
+                r = hotcold_pipeline(synthetic.WORKLOADS[name], dev, layers=pl, step_sync=sync)
+                log(f"  step {r['step_us_wall_mean']} us wall (median {r['step_us_wall_median']}), searches "
+                    f"{r['retrievals']} run of {r['retrievals_scheduled']} scheduled "
+                    f"({r['retrievals_skipped_search_running']} skipped: search still running), ready_rate "
+                    f"{r['ready_rate']}")
+                pipe_larger.append(r)
 
     h2o = None
     if not args.no_other_configs and args.workload == "llama8b_8k_b512":
@@ -1203,6 +1261,7 @@ def main():
         "device_stream": stream,
         "other_workloads": others,
         "hotcold_pipeline": pipe,
+        "hotcold_pipeline_larger": pipe_larger,
         "h2o": h2o,
         "cpu_baseline": cpu,
     }
