@@ -613,6 +613,126 @@ def measure_config(w, dev, flush, reps=24, cpu=False):
     return out
 
 
+DECODE_LAYOUTS = ("separate", "kv_adjacent", "head_interleaved", "kv_adjacent_head_interleaved")
+
+
+def decode_layout_views(kind, LB, Hk, rows, D, dtype, dev):
+    """(k, v) views (LB, Hk, rows, D) of hot rows in one of four HBM layouts:
+      separate                      K and V each [LB][Hk][rows][D]
+      kv_adjacent                   one [LB][Hk][rows][2][D] (the hot buffer's)
+      head_interleaved              K and V each [LB][rows][Hk][D]
+      kv_adjacent_head_interleaved  one [LB][rows][Hk][2][D]
+    The decode kernel takes row and head strides, so the same launch reads
+    all four."""
+    import torch
+    if kind == "separate":
+        return (torch.empty((LB, Hk, rows, D), dtype=dtype, device=dev),
+                torch.empty((LB, Hk, rows, D), dtype=dtype, device=dev))
+    if kind == "kv_adjacent":
+        kv = torch.empty((LB, Hk, rows, 2, D), dtype=dtype, device=dev)
+        return kv[:, :, :, 0], kv[:, :, :, 1]
+    if kind == "head_interleaved":
+        return (torch.empty((LB, rows, Hk, D), dtype=dtype, device=dev).permute(0, 2, 1, 3),
+                torch.empty((LB, rows, Hk, D), dtype=dtype, device=dev).permute(0, 2, 1, 3))
+    if kind == "kv_adjacent_head_interleaved":
+        kv = torch.empty((LB, rows, Hk, 2, D), dtype=dtype, device=dev)
+        return kv[:, :, :, 0].permute(0, 2, 1, 3), kv[:, :, :, 1].permute(0, 2, 1, 3)
+    raise ValueError(f"unknown layout {kind!r}; one of {DECODE_LAYOUTS}")
+
+
+def measure_decode_layouts(dev, kinds=DECODE_LAYOUTS, launches=("stacked", "layer"), reps=40):
+    """The fused append+decode of the 32-layer 8k->512 hot tier (fp16, 543
+    cached rows + the appended token per (layer, KV head), 71.96 MB per
+    32-layer launch) over each hot-row layout, beside the plain read of the
+    same byte count (hc_read_bytes).  Launches: "stacked" (all 32 layers in
+    one launch) and "layer" (one layer's launch, layers in turn).  Timed
+    differentially after the cache sweep, the layouts round-robin within
+    each repetition, starting one layout later in each repetition, after a
+    discarded launch over buffers of their own (so no layout follows a
+    launch over its own rows; with one layout, no such launch, so that a
+    kernel trace holds that layout's launches only); medians over reps.  Each layout's output is
+    checked against an fp32 torch attention first."""
+    import torch
+    from hotcold_kv import ops, synthetic
+
+    w = synthetic.WORKLOADS["llama8b_8k_b512"]
+    LB, Hk, Hq, D, dt = w.layers * w.batch, w.hk, w.hq, w.head_dim, w.dtype
+    n = w.budget + 32                       # rows per view: 543 cached + the appended token's row
+    g = torch.Generator(device=dev).manual_seed(21)
+    st = torch.cuda.Stream(dev)
+    flush = CacheSweep(dev)
+    q = torch.randn((LB, Hq, D), generator=g, device=dev, dtype=dt)
+    k_new = torch.randn((LB, Hk, 1, D), generator=g, device=dev, dtype=dt)
+    v_new = torch.randn((LB, Hk, 1, D), generator=g, device=dev, dtype=dt)
+    o = torch.empty((LB, Hq, D), dtype=dt, device=dev)
+    src_k = torch.randn((LB, Hk, n, D), generator=g, device=dev, dtype=dt)
+    src_v = torch.randn((LB, Hk, n, D), generator=g, device=dev, dtype=dt)
+    views, out = {}, {}
+    for kind in kinds:
+        k, v = decode_layout_views(kind, LB, Hk, n + 8, D, dt, dev)
+        k[:, :, :n].copy_(src_k)
+        v[:, :, :n].copy_(src_v)
+        views[kind] = (k, v)
+        ops.decode_attention_append(q, k[:, :, :n], v[:, :, :n], k_new, v_new, w.scaling, out=o)
+        kk = torch.cat([src_k[:, :, :n - 1], k_new], 2).float()
+        vv = torch.cat([src_v[:, :, :n - 1], v_new], 2).float()
+        qq = q.float().view(LB, Hk, Hq // Hk, D)
+        ref_o = torch.matmul(torch.softmax(torch.matmul(qq, kk.transpose(2, 3).contiguous()) * w.scaling, -1), vv)
+        err = float((o.float() - ref_o.reshape(LB, Hq, D)).abs().max())
+        if not err < 1e-2:
+            raise RuntimeError(f"decode over layout {kind}: max abs error {err} against fp32 torch")
+        out[kind] = {"k_strides": list(k.stride()), "v_strides": list(v.stride()), "max_abs_err_vs_fp32": err}
+    del src_k, src_v
+    views["_dummy"] = decode_layout_views("separate", LB, Hk, n + 8, D, dt, dev)
+    for t in views["_dummy"]:
+        t.zero_()
+    bytes_stacked = decode_bytes(w, LB, n)
+    bytes_layer = decode_bytes(w, w.batch, n)
+
+    def ev():
+        return torch.cuda.Event(enable_timing=True)
+
+    for launch in launches:
+        sw = {kind: [] for kind in kinds}
+        pr = {kind: [] for kind in kinds}
+        with torch.cuda.stream(st):
+            for r in range(3 + reps):
+                l = r % LB
+                order = ["_dummy"] * (len(kinds) > 1) + [kinds[(r + i) % len(kinds)] for i in range(len(kinds))]
+                for kind in order:
+                    k, v = views[kind]
+                    a0, a1, b0, b1 = ev(), ev(), ev(), ev()
+                    a0.record(st)
+                    flush()
+                    a1.record(st)
+                    b0.record(st)
+                    flush()
+                    if launch == "stacked":
+                        ops.decode_attention_append(q, k[:, :, :n], v[:, :, :n], k_new, v_new, w.scaling, out=o)
+                    else:
+                        ops.decode_attention_append(q[l:l + 1], k[l:l + 1, :, :n], v[l:l + 1, :, :n],
+                                                    k_new[l:l + 1], v_new[l:l + 1], w.scaling, out=o[l:l + 1])
+                    b1.record(st)
+                    if r >= 3 and kind != "_dummy":
+                        sw[kind].append((a0, a1))
+                        pr[kind].append((b0, b1))
+        torch.cuda.synchronize()
+        nb = bytes_stacked if launch == "stacked" else bytes_layer
+        for kind in kinds:
+            ms = (statistics.median(a.elapsed_time(b) for a, b in pr[kind])
+                  - statistics.median(a.elapsed_time(b) for a, b in sw[kind]))
+            out[kind][f"{launch}_us"] = round(ms * 1e3, 3)
+            out[kind][f"{launch}_frac"] = round(nb / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
+    res = {"workload": w.name, "keys_attended": n, "layouts": out}
+    if "stacked" in launches:
+        res["bytes_stacked"] = int(bytes_stacked)
+        res["read_floor_stacked_us"] = round(read_floor_ms(dev, bytes_stacked, st, flush) * 1e3, 3)
+    if "layer" in launches:
+        res["bytes_layer"] = int(bytes_layer)
+        res["read_floor_layer_us"] = round(read_floor_ms(dev, bytes_layer, st, flush) * 1e3, 3)
+    return res
+
+
 def measure_compaction_layer(w, dev, reps=12):
     """One layer's SnapKV compaction of a workload at its full batch (window
     scores, kept indices, gather of K and V into the budget), N(0,1) inputs,
@@ -1063,6 +1183,11 @@ def main():
     ap.add_argument("--pipeline-only", nargs="?", const="llama8b_16k_b1024_held64", metavar="WORKLOAD",
                     help="only the hot/cold pipeline of a held-slot workload, by default the 16k one "
                          "(one JSON object)")
+    ap.add_argument("--decode-layouts", nargs="?", const=",".join(DECODE_LAYOUTS), metavar="LAYOUTS",
+                    help="only the 32-layer 8k decode over hot-row layouts (comma-separated, default all four), "
+                         "beside the plain read of its bytes (one JSON object)")
+    ap.add_argument("--layout-launch", choices=("stacked", "layer", "both"), default="both",
+                    help="--decode-layouts: time the 32-layer launch, one layer's launch, or both")
     ap.add_argument("--pipeline-layers", type=int, default=None,
                     help="layers of the --pipeline-only run (default: the workload's larger-loop layer count)")
     ap.add_argument("--pipeline-step-sync", action="store_true",
@@ -1100,6 +1225,11 @@ def main():
     if args.compaction_only:
         print(json.dumps({"compaction_layer": measure_compaction_layer(synthetic.WORKLOADS[args.compaction_only],
                                                                        dev)}), flush=True)
+        return
+    if args.decode_layouts:
+        launches = ("stacked", "layer") if args.layout_launch == "both" else (args.layout_launch,)
+        print(json.dumps({"decode_layouts": measure_decode_layouts(dev, tuple(args.decode_layouts.split(",")),
+                                                                   launches)}), flush=True)
         return
     if args.pipeline_only:
         pl = args.pipeline_layers or PIPELINE_LAYERS.get(args.pipeline_only)

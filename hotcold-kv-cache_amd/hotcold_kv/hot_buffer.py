@@ -20,11 +20,13 @@ from . import ops
 def kv_rows(prefix, rows, head_dim, dtype, device):
     """Key and value rows with each row's key and value adjacent in memory:
     one allocation [*prefix][rows][2][head_dim], returned as two
-    (*prefix, rows, head_dim) views of row stride 2*head_dim.  Decode then
-    reads each (batch, head) as one stream instead of two: the 32-layer
-    8k-context launch measured 0.46 us faster (15.76 against 16.22 us) and one
-    layer's launch 0.65 us (8.96 against 9.62 us) than with separate K and V
-    tensors.  Every kernel that reads or writes hot rows takes row strides."""
+    (*prefix, rows, head_dim) views of row stride 2*head_dim, so decode reads
+    each (batch, head) as one stream instead of two.  Timed against separate
+    K and V tensors and two head-interleaved layouts, the 32-layer
+    8k-context decode launch differs by less than 0.7 us (15.5-16.2 us for
+    72 MB) and in no consistent order; the layout is kept for its one
+    allocation per layer.  Every kernel that reads or writes hot rows takes
+    row strides."""
     kv = torch.empty((*prefix, rows, 2, head_dim), dtype=dtype, device=device)
     return kv[..., 0, :], kv[..., 1, :]
 
