@@ -241,15 +241,43 @@ __global__ __launch_bounds__(256) void evict_score_kernel(const float* scores, c
 }
 
 // The first kCounterBytes of a decode workspace hold the in-kernel merge's
-// arrival words, one 64-bit [launch tag | arrivals] per (batch, kv head).
-// They need no initialisation: every launch counts under a tag of its own
-// (kernel comment at the arrival).
+// arrival words, one 64-bit [launch tag | done bit, arrivals] per (batch,
+// kv head).  They need no initialisation: every launch counts under a tag
+// of its own (kernel comment at the arrival).
 constexpr int64_t kCounterBytes = 16384;
 constexpr int64_t kMaxMergeUnits = kCounterBytes / 8;
 
 // Launch tags of the in-kernel merge: consecutive launches get different
 // tags (a 32-bit counter, wrapping after 2^32 launches).
 static std::atomic<uint32_t> g_launch_tag{0};
+
+// The tag a workspace's arrival words were last left under: a launch that
+// passes it counts on the words as they are, with one atomic per
+// workgroup; words under any other tag cost its first arrivals a
+// compare-and-swap each.  A direct-mapped table of recent workspaces: a
+// workspace whose entry another one took only costs its next launch those
+// swaps.
+namespace {
+constexpr int kTagSlots = 256;
+struct TagSlot {
+  uintptr_t ws;
+  uint32_t tag;
+};
+TagSlot g_tag_slots[kTagSlots];
+std::mutex g_tag_mu;
+
+// Records tag as the workspace's latest and returns the one before it (or
+// tag itself for a workspace not in the table).
+uint32_t exchange_workspace_tag(const void* ws, uint32_t tag) {
+  const uintptr_t p = reinterpret_cast<uintptr_t>(ws);
+  TagSlot& slot = g_tag_slots[((p >> 8) ^ (p >> 20)) % kTagSlots];
+  std::lock_guard<std::mutex> lk(g_tag_mu);
+  const uint32_t prev = slot.ws == p ? slot.tag : tag;
+  slot.ws = p;
+  slot.tag = tag;
+  return prev;
+}
+}  // namespace
 // The in-kernel merge is used up to this many workgroups.  Its chain (the
 // partial's device-coherent stores, the arrival count, the last workgroup's
 // loads) costs a few memory round trips on the last workgroup of each unit,
@@ -430,6 +458,7 @@ static int decode_impl(int dtype, int64_t B, int64_t Hq, int64_t Hk, int64_t D, 
   a.S_cache = (int)S_cache;
   a.counters = shape.merge_in_kernel ? reinterpret_cast<unsigned long long*>(ws) : nullptr;
   a.epoch = g_launch_tag.fetch_add(1, std::memory_order_relaxed) + 1;
+  a.prev_epoch = a.counters ? exchange_workspace_tag(ws, a.epoch) : a.epoch;
   if (ap) {
     a.k_new = ap->k_new; a.kn_sb = ap->kn_sb; a.kn_sh = ap->kn_sh;
     a.v_new = ap->v_new; a.vn_sb = ap->vn_sb; a.vn_sh = ap->vn_sh;

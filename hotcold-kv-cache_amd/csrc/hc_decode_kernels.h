@@ -95,10 +95,12 @@ struct DecodeArgs {
   int64_t* pos_dst;
   int64_t posd_sb;
   // In-kernel merge of the split partials (splits > 1): one arrival word
-  // per (b, kv head), [launch tag : 32 | arrivals : 32], any initial
-  // contents; NULL = a second merge kernel.  epoch is this launch's tag.
+  // per (b, kv head), [launch tag : 32 | done : 1 | arrivals : 31], any
+  // initial contents; NULL = a second merge kernel.  epoch is this launch's
+  // tag, prev_epoch the tag the words were left under by the workspace's
+  // previous launch (epoch itself if not known).
   unsigned long long* counters;
-  uint32_t epoch;
+  uint32_t epoch, prev_epoch;
 };
 static_assert(offsetof(DecodeArgs, Hq) + sizeof(int) <= 128, "prologue fields must fit the first 128 bytes");
 
@@ -850,26 +852,37 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     // agent-scope release writes back the whole L2 of the XCD, which had
     // made one 5-split launch 19-20 us instead of 9.)
     //
-    // Arrivals are counted under this launch's tag: the upper half of the
-    // unit's word.  An arrival that finds another launch's tag (left by an
-    // earlier launch, or garbage) re-registers with a compare-and-swap as the
-    // tag's first arrival, so no count a launch left behind can make a
-    // workgroup merge early.  Every failed swap means another workgroup of
-    // the unit changed the word (at most twice each), so the loop is bounded
-    // by 2 * splits + 1 rounds.  The merging workgroup leaves (tag, 0), so a
-    // launch replayed with the same tag (a captured graph) counts from zero.
+    // Arrival words.  A merging workgroup leaves its unit's word as
+    // (tag, done, 0).  The next launch on the workspace passes that tag as
+    // prev_epoch, and its arrivals count on the word as it is: one atomic
+    // add each.  Counts are this launch's only in a word under prev_epoch
+    // with the done bit (what a finished launch left), under this launch's
+    // own tag with the done bit (left by this same launch, replayed from a
+    // captured graph), or under its own tag without it (registered by this
+    // launch, below).  An arrival that finds anything else (garbage, a
+    // count an unfinished launch left behind, a tag the host no longer
+    // knows) re-registers the word with a compare-and-swap as (tag, 1), so
+    // no stale count can make a workgroup merge early.  Every failed swap
+    // means another workgroup of the unit changed the word (at most twice
+    // each), so the loop is bounded by 2 * splits + 1 rounds.
     __shared__ uint32_t sm_last;
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     unsigned long long* word = a.counters + unit;
+    constexpr unsigned long long kHi = 0xffffffff00000000ull, kDone = 0x80000000ull;
     const unsigned long long tag = (unsigned long long)a.epoch << 32;
+    const unsigned long long prev = (unsigned long long)a.prev_epoch << 32;
     if (threadIdx.x == 0) {
-      unsigned long long old = __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      const auto counting = [&](unsigned long long w) {
+        return (w & kDone) ? ((w & kHi) == prev || (w & kHi) == tag) : ((w & kHi) == tag);
+      };
+      const unsigned long long old = __hip_atomic_fetch_add(word, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       unsigned long long mine = old + 1;
-      if ((old & 0xffffffff00000000ull) != tag) {
-        unsigned long long cur = mine;
+      if (!counting(old)) {
+        mine = 0;
+        unsigned long long cur = old + 1;
         for (int round = 0; round <= 2 * a.splits; ++round) {
-          const unsigned long long want = ((cur & 0xffffffff00000000ull) == tag) ? cur + 1 : (tag | 1ull);
+          const unsigned long long want = counting(cur) ? cur + 1 : (tag | 1ull);
           if (__hip_atomic_compare_exchange_strong(word, &cur, want, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT)) {
             mine = want;
@@ -877,12 +890,12 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
           }
         }
       }
-      sm_last = (uint32_t)mine == (uint32_t)a.splits;
+      sm_last = (uint32_t)(mine & 0x7fffffffull) == (uint32_t)a.splits;
     }
     __syncthreads();
     if (sm_last) {
       merge_partials<T, true>(a, b, hk, D, threadIdx.x, 64 * NW);
-      if (threadIdx.x == 0) __hip_atomic_store(word, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (threadIdx.x == 0) __hip_atomic_store(word, tag | kDone, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }

@@ -77,8 +77,11 @@ int hc_read_bytes(const void* p, int64_t bytes, uint32_t* sink, void* stream);
  *     hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, with_evict)
  *     bytes.  It needs no initialisation: its first 16384 bytes hold the
  *     merge's arrival words, counted under a tag of each launch's own, so
- *     whatever a workspace holds cannot trigger an early merge.  One
- *     workspace must not be used by two launches that may overlap.
+ *     whatever a workspace holds cannot trigger an early merge.  Words the
+ *     workspace's previous launch left are counted on directly; others
+ *     (a new workspace, one used by another caller in between) cost the
+ *     launch's first arrivals one compare-and-swap each.  One workspace
+ *     must not be used by two launches that may overlap.
  *   dropout must be 0.0.
  */
 int64_t hc_decode_attn_workspace_size(int64_t B, int64_t Hq, int64_t Hk, int64_t D,

@@ -93,17 +93,24 @@ def test_decode_split_merge_paths(B, S, splits, dtype):
     torch.cuda.synchronize()
     for key, ws in ops._ws_cache.items():
         if key[0] == "decode":
-            # every merge leaves its unit's word at (tag, 0 arrivals)
+            # every merge leaves its unit's word at (tag, done, 0 arrivals)
             words = ws[:ops.DECODE_COUNTER_BYTES].view(torch.int64)
-            assert int((words & 0xffffffff).count_nonzero()) == 0
+            assert int((words & 0x7fffffff).count_nonzero()) == 0
 
 
-@pytest.mark.parametrize("fill", ["random", "ones", "counts_left_behind"])
+def _word(tag, low):
+    """An arrival word [tag : 32 | low : 32] as a signed int64."""
+    w = (tag << 32) | low
+    return w - (1 << 64) if w >= 1 << 63 else w
+
+
+@pytest.mark.parametrize("fill", ["random", "ones", "counts_left_behind", "finished_under_another_tag"])
 def test_decode_split_merge_ignores_stale_counter_words(fill):
     """The in-kernel merge's arrival words may hold anything before a launch
     (a launch cut short, a caller's uninitialised workspace): each launch
-    counts under its own tag, so the output is the same bits as on a zeroed
-    block."""
+    counts only on words left by the workspace's previous launch, so the
+    output is the same bits as on a zeroed block, and a second launch on
+    the words the first one left is the same again."""
     B, Hq, Hk, S, D, splits = 1, 32, 8, 2431, 128, 16
     dtype = torch.float16
     q = _randn((B, Hq, 1, D), 31, dtype).to(DEV)
@@ -121,14 +128,20 @@ def test_decode_split_merge_ignores_stale_counter_words(fill):
         words.copy_(torch.randint(-(1 << 62), 1 << 62, words.shape, generator=g))
     elif fill == "ones":
         words.fill_(-1)
-    else:
+    elif fill == "counts_left_behind":
         # another launch's tag with splits-1 arrivals: a plain counter would
         # let this launch's first arrival merge alone
-        words.copy_(torch.full(words.shape, (12345 << 32) + splits - 1, dtype=torch.int64))
+        words.fill_(_word(0xfffffffe, splits - 1))
+    else:
+        # the done bit, as a finished launch leaves it, but under a tag that
+        # is not the workspace's last one, and with splits-1 arrivals
+        words.fill_(_word(0xfffffffe, 0x80000000 | (splits - 1)))
     torch.cuda.synchronize()
     out = ops.decode_attention(q, k, v, sc, num_splits=splits)
+    again = ops.decode_attention(q, k, v, sc, num_splits=splits)
     torch.cuda.synchronize()
     assert torch.equal(out, clean), fill
+    assert torch.equal(again, clean), fill
     assert np.abs(out.float().cpu().numpy() - ref.decode_attention(q.cpu(), k.cpu(), v.cpu(), sc)).max() <= TOL[dtype]
 
 
