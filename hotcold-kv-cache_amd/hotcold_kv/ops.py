@@ -46,7 +46,8 @@ def _ptr(t):
 
 # Leading bytes of a decode workspace that hold the in-kernel split merge's
 # arrival words.  They need no initialisation (each launch counts under its
-# own tag); a new workspace still starts them at zero.
+# own tag), so nothing clears them: a workspace first allocated while a
+# graph is being captured puts no fill kernel into the graph.
 DECODE_COUNTER_BYTES = 16384
 
 
@@ -62,8 +63,6 @@ def _workspace(kind, device, nbytes):
             if ws is not None:
                 size = max(size, int(ws.numel() * 1.5))
             ws = torch.empty(size, dtype=torch.uint8, device=device)
-            if kind == "decode":
-                ws[:DECODE_COUNTER_BYTES].zero_()
             _ws_cache[key] = ws
         return ws
 

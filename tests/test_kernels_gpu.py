@@ -14,6 +14,7 @@ import pytest
 import torch
 
 from hotcold_kv import ops, synthetic
+from hotcold_kv.hot_buffer import kv_rows
 from oracle import reference as ref
 
 pytestmark = pytest.mark.gpu
@@ -91,11 +92,79 @@ def test_decode_split_merge_paths(B, S, splits, dtype):
                                       num_splits=splits)
     assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype]
     torch.cuda.synchronize()
-    for key, ws in ops._ws_cache.items():
-        if key[0] == "decode":
-            # every merge leaves its unit's word at (tag, done, 0 arrivals)
-            words = ws[:ops.DECODE_COUNTER_BYTES].view(torch.int64)
-            assert int((words & 0x7fffffff).count_nonzero()) == 0
+    if B * Hk * max(splits, 1) <= 512:
+        # merged in the kernel: every merge leaves its unit's arrival word at
+        # (tag, done, 0 arrivals)
+        words = ops._workspace("decode", torch.device(DEV), 1)[:ops.DECODE_COUNTER_BYTES].view(torch.int64)
+        assert int((words[:B * Hk] & 0x7fffffff).count_nonzero()) == 0
+        assert int(((words[:B * Hk] >> 31) & 1).sum()) == B * Hk
+
+
+@pytest.mark.parametrize("S", [300, 575, 1200, 2431, 129])
+def test_decode_split_merge_as_the_shape_changes(S):
+    """Launches of different lengths on one workspace, issued back to back
+    (the split count and the partials' addresses change with S; decode of a
+    growing cache crosses such steps): each merges only its own launch's
+    partials."""
+    B, Hq, Hk, D = 1, 32, 8, 128
+    dtype = torch.float16
+    q = _randn((B, Hq, 1, D), 40 + S, dtype)
+    k = _randn((B, Hk, S, D), 41 + S, dtype)
+    v = _randn((B, Hk, S, D), 42 + S, dtype)
+    sc = 1.0 / math.sqrt(D)
+    want = ref.decode_attention(q, k, v, sc)
+    qd, kd, vd = q.to(DEV), k.to(DEV), v.to(DEV)
+    outs = [ops.decode_attention(qd, kd, vd, sc, num_splits=n) for n in (0, 3, 0, 7)]
+    torch.cuda.synchronize()
+    for out in outs:
+        assert np.abs(out.float().cpu().numpy() - want).max() <= TOL[dtype]
+    assert torch.equal(outs[0], outs[2])
+
+
+def test_decode_split_merge_in_a_replayed_graph():
+    """One layer's append+decode (8 KV heads, 545 keys: five splits merged
+    inside the launch) captured in a graph and replayed with new queries
+    and tokens each time: every replay's output equals an eager launch on
+    the same inputs, bit for bit, so no replay merges partials an earlier
+    replay left (a replay repeats the launch's tag: every workgroup's
+    partial has landed before it counts in)."""
+    B, Hq, Hk, D, S = 1, 32, 8, 128, 545
+    dtype = torch.float16
+    dev = torch.device(DEV)
+    g = torch.Generator(device=dev).manual_seed(50)
+    k, v = kv_rows((B, Hk), S + 7, D, dtype, dev)
+    k.copy_(torch.randn((B, Hk, S + 7, D), generator=g, device=dev, dtype=dtype))
+    v.copy_(torch.randn((B, Hk, S + 7, D), generator=g, device=dev, dtype=dtype))
+    q = torch.randn((B, Hq, D), generator=g, device=dev, dtype=dtype)
+    kn = torch.randn((B, Hk, 1, D), generator=g, device=dev, dtype=dtype)
+    vn = torch.randn((B, Hk, 1, D), generator=g, device=dev, dtype=dtype)
+    out = torch.empty((B, Hq, D), device=dev, dtype=dtype)
+    sc = 1.0 / math.sqrt(D)
+    st = torch.cuda.Stream(dev)
+    with torch.cuda.stream(st):
+        ops.decode_attention_append(q, k[:, :, :S], v[:, :, :S], kn, vn, sc, out=out)   # the stream's workspace
+    st.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        ops.decode_attention_append(q, k[:, :, :S], v[:, :, :S], kn, vn, sc, out=out)
+    for rep in range(6):
+        with torch.cuda.stream(st):
+            q.copy_(torch.randn((B, Hq, D), generator=g, device=dev, dtype=dtype))
+            kn.copy_(torch.randn((B, Hk, 1, D), generator=g, device=dev, dtype=dtype))
+            vn.copy_(torch.randn((B, Hk, 1, D), generator=g, device=dev, dtype=dtype))
+        st.synchronize()
+        graph.replay()
+        st.synchronize()
+        got = out.clone()
+        with torch.cuda.stream(st):
+            want = ops.decode_attention_append(q, k[:, :, :S], v[:, :, :S], kn, vn, sc)
+        st.synchronize()
+        assert torch.equal(got, want), rep
+        kk = torch.cat([k[:, :, :S - 1], kn], 2).cpu()
+        vv = torch.cat([v[:, :, :S - 1], vn], 2).cpu()
+        oracle = ref.decode_attention(q[:, :, None].cpu(), kk, vv, sc)
+        assert np.abs(got.float().cpu().numpy().reshape(oracle.shape) - oracle).max() <= TOL[dtype], rep
+    del graph
 
 
 def _word(tag, low):
@@ -125,7 +194,10 @@ def test_decode_split_merge_ignores_stale_counter_words(fill):
     words = ws[:ops.DECODE_COUNTER_BYTES].view(torch.int64)
     g = torch.Generator().manual_seed(34)
     if fill == "random":
+        # arrival words, generations and the split partials' room alike
         words.copy_(torch.randint(-(1 << 62), 1 << 62, words.shape, generator=g))
+        ws[ops.DECODE_COUNTER_BYTES:].copy_(torch.randint(0, 256, (ws.numel() - ops.DECODE_COUNTER_BYTES,),
+                                                          generator=g, dtype=torch.uint8))
     elif fill == "ones":
         words.fill_(-1)
     elif fill == "counts_left_behind":
