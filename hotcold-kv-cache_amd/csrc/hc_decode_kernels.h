@@ -913,8 +913,11 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeArgs a, int D
 //         1: up to 512 with the accumulation registers);
 //   nw    waves per workgroup (8 needs minw 2 and an epilogue of at most
 //         32 KB LDS, nw*gm*D floats).
-// Chosen so that no instance spills (checked with the compiler's
-// kernel-resource-usage report).
+// Chosen so that no f16/bf16 instance spills (checked with the compiler's
+// kernel-resource-usage report).  The fp32 instances keep P.V on the VALU,
+// GM * D / 16 accumulators per lane, and from D = 64 on (D = 128 with
+// groups of 16) they spill 48-968 bytes per lane to scratch; fp32 caches
+// are a correctness path, not a speed one.
 struct DecodeCfg {
   int nbuf, minw, nw;
 };

@@ -658,6 +658,22 @@ def test_h2o_prefill_scores_8k_properties():
     assert torch.allclose(sce, tail, rtol=2e-5, atol=1e-6)
 
 
+def test_h2o_prefill_scores_bit_exact_at_8k():
+    """One KV group of the full 8k prompt (2 query heads, fp16): the H2O
+    prefill scores equal the oracle's bit for bit.  The oracle's fp64
+    contract takes about 20 s per query head on one core, so the two heads
+    run on two threads (the oracle's C call releases the GIL)."""
+    from concurrent.futures import ThreadPoolExecutor
+    S, D, Hq = 8192, 128, 2
+    q, k = _randn((1, Hq, S, D), 49, torch.float16), _randn((1, 1, S, D), 50, torch.float16)
+    sc = D ** -0.5
+    got = ops.h2o_prefill_scores(q.to(DEV), k.to(DEV), sc).cpu()
+    with ThreadPoolExecutor(Hq) as pool:
+        per_q = list(pool.map(lambda h: ref.window_scores(q[:, h:h + 1], k, S, sc, 1, "maxpool"), range(Hq)))
+    want = ref.head_mean(torch.cat(per_q, 1)).reshape(1, 1, S)
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("B,Hq,Hk,S,D,dtype", H2O_CASES)
 def test_h2o_prefill_scores_bit_exact(B, Hq, Hk, S, D, dtype):
     q, k = _randn((B, Hq, S, D), 41, dtype), _randn((B, Hk, S, D), 42, dtype)
