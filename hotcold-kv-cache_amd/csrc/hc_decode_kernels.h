@@ -847,10 +847,14 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     // accesses, so no L2 write-back or invalidation is needed: each thread
     // waits until its stores have completed, the workgroup's arrival is
     // counted after that, and the merging workgroup reads only after it has
-    // seen every other arrival.  (The ordering between the partials and the
-    // count rests on those completed stores, not on release/acquire: an
-    // agent-scope release writes back the whole L2 of the XCD, which had
-    // made one 5-split launch 19-20 us instead of 9.)
+    // seen every other arrival.  The ordering between the partials and the
+    // count rests on those completed stores, not on release/acquire, so it
+    // is outside the HIP memory model's guarantees: it relies on gfx950's
+    // agent-scope stores having reached the device-coherent level once the
+    // vmcnt wait returns, and on agent-scope loads reading that level.  A
+    // release on the count (it writes back the XCD's whole L2) with an
+    // acquire in the merger gives the same outputs and costs 1.5 us per
+    // launch of one 8k layer (7.75 against 9.3 us cold, replayed graph).
     //
     // Arrival words.  A merging workgroup leaves its unit's word as
     // (tag, done, 0).  The next launch on the workspace passes that tag as
