@@ -73,7 +73,8 @@ int hc_read_bytes(const void* p, int64_t bytes, uint32_t* sink, void* stream);
  *   num_splits <= 0 picks the launch shape (few short units are spread over
  *     many workgroups); with more than one split the partial results are
  *     merged inside the launch by the last workgroup of each (b, kv head) to
- *     finish (by a second kernel above 4096 units).  The workspace must hold
+ *     finish (by a second kernel when the launch has more than 512
+ *     workgroups or more than 2048 units).  The workspace must hold
  *     hc_decode_attn_workspace_size(B, Hq, Hk, D, S, num_splits, with_evict)
  *     bytes.  It needs no initialisation: its first 16384 bytes hold the
  *     merge's arrival words, counted under a tag of each launch's own, so
