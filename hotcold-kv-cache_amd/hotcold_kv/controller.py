@@ -696,8 +696,9 @@ class KVController:
             slot.q_ready = self._event(0)
         stream = ops_stream(q0.device)
         rows = [(t, r) for t in win for r in range(t.shape[2])]
-        if len(rows) <= N.lib().hc_retrieval_query_max_rows() and all(t.dtype == q0.dtype and t.shape[:2] == q0.shape[:2] and t.shape[3] == D
-                                   and t.stride(3) == 1 and t.is_cuda for t in win):
+        if len(rows) <= N.lib().hc_retrieval_query_max_rows() and all(
+                t.dtype == q0.dtype and t.shape[:2] == q0.shape[:2] and t.shape[3] == D and t.stride(3) == 1
+                and t.is_cuda for t in win):
             es = q0.element_size()
             n = len(rows)
             ptrs = (ctypes.c_void_p * n)(*[t.data_ptr() + r * t.stride(2) * es for t, r in rows])
