@@ -415,6 +415,18 @@ def stream_rates(dev, nbytes=1 << 30, iters=10):
     return {"read_GBps": round(read, 1), "copy_GBps": round(copy, 1), "copy_bytes_each_way": half * 4}
 
 
+def profiled_launch_us(workload):
+    """The decode launch's average kernel duration (us) over the launches
+    right after the cache sweep, from the committed rocprofv3 kernel-trace
+    summary of this workload, or None if there is none."""
+    import re
+    path = os.path.join(ROOT, "profiles", f"decode_attn_compaction_{workload}_kernel_trace.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^decode_launch_avg_us_after_sweep:\s*([0-9.]+)", open(path).read(), re.M)
+    return float(m.group(1)) if m else None
+
+
 def profiled_traffic(workload):
     """HBM bytes per decode launch from the committed FETCH_SIZE / WRITE_SIZE
     summary of this workload (rocprofv3 --pmc runs, scaled by a known-size
@@ -1372,6 +1384,10 @@ def main():
         "decode_launch_us_warm_last_step": round(warm_dec_ms * 1e3, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": profiled_traffic(w.name),
+                     "profiled_launch_us": profiled_launch_us(w.name),
+                     "profiled_launch": "rocprofv3 average kernel duration of the launches right after the sweep "
+                                        "(committed kernel-trace summary); launch_us exceeds it by the gap between "
+                                        "two dependent kernels",
                      "kernel": "decode_attn_kernel (fused append; unsplit at this size, so no merge kernel)",
                      "bytes_per_launch": int(nbytes), "launch_us": round(dec_ms * 1e3, 3),
                      "launch_timing": "events around [cache sweep; decode] minus events around [cache sweep]",
