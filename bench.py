@@ -999,16 +999,15 @@ def hotcold_pipeline(w, dev, profile_steps=None, device_search=True, layers=None
         p = synthetic.make_prompt(w, layer=l, seed=0, device=dev)
         return p, p["q_post"][:, :, -w.window:, :].contiguous()
 
-    prompts = [] if lazy else [prompt(l) for l in range(L)]      # inputs, not timed
-    first = prompts[0][0] if prompts else prompt(0)[0]
-    ctrl._lazy_init(first["k_pre"], n_layers=L)
-    del first
+    # inputs, not timed; lazily, only layer 0's prompt exists before the loop
+    prompts = [prompt(l) for l in range(1 if lazy else L)]
+    ctrl._lazy_init(prompts[0][0]["k_pre"], n_layers=L)
     prefill_s = 0.0
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for l in range(L):
         if lazy:
-            p, win = prompt(l)
+            p, win = prompts.pop() if l == 0 else prompt(l)
             torch.cuda.synchronize()
             tl = time.perf_counter()
         else:
