@@ -23,7 +23,8 @@
 //     fp32 inputs use v_mfma_f32_16x16x4f32;
 //   * online softmax in the log2 domain (exp2), fp32, with a lazy
 //     reference max: the accumulators are rescaled only when a tile's max
-//     exceeds the reference by more than 2^8;
+//     exceeds the reference by more than 8 in the log2 domain (a factor of
+//     2^8);
 //   * P.V on MFMA for f16/bf16 (v_mfma_f32_16x16x16_{f16,bf16}): the Q.K^T
 //     output leaves lane (r, c) holding p for keys 4r..4r+3 of head c, which
 //     is exactly its B-operand share, and its four V rows give the A operand
