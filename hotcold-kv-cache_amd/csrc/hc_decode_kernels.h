@@ -28,8 +28,9 @@
 //   * P.V on MFMA for f16/bf16 (v_mfma_f32_16x16x16_{f16,bf16}): the Q.K^T
 //     output leaves lane (r, c) holding p for keys 4r..4r+3 of head c, which
 //     is exactly its B-operand share, and its four V rows give the A operand
-//     (a byte permute per register), so no lane exchanges data; P is rounded
-//     to the input type and the softmax sum uses the same rounded values.
+//     (a byte permute per register), so no lane exchanges data; for bf16, P
+//     enters as a high and a low part (two MFMAs per block, a 16-bit
+//     mantissa), for f16 rounded once; the softmax sum uses the same values.
 //     fp32 inputs use the VALU (16 lanes per V row, fp32 FMAs);
 //   * the attention mask and the held slot's valid & (pos <= cur) test are
 //     evaluated once per workgroup into an LDS bitmap;
@@ -435,12 +436,10 @@ struct MxOps<half_t> {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(vec4, u32x2{a0, a1}),
                                                 __builtin_bit_cast(vec4, u32x2{b0, b1}), c, 0, 0, 0);
   }
-  // Round two probabilities to f16; return the packed pair and the rounded values.
-  __device__ static uint32_t pack2(float x, float y, float& rx, float& ry) {
-    const half_t hx = (half_t)x, hy = (half_t)y;
-    rx = (float)hx;
-    ry = (float)hy;
-    return (uint32_t)__builtin_bit_cast(uint16_t, hx) | ((uint32_t)__builtin_bit_cast(uint16_t, hy) << 16);
+  __device__ static uint32_t bits(float x, float& r) {
+    const half_t h = (half_t)x;
+    r = (float)h;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
   }
 };
 
@@ -451,13 +450,43 @@ struct MxOps<bf16_t> {
     return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(vec4, u32x2{a0, a1}),
                                                     __builtin_bit_cast(vec4, u32x2{b0, b1}), c, 0, 0, 0);
   }
-  __device__ static uint32_t pack2(float x, float y, float& rx, float& ry) {
-    const bf16_t hx = (bf16_t)x, hy = (bf16_t)y;
-    rx = (float)hx;
-    ry = (float)hy;
-    return (uint32_t)__builtin_bit_cast(uint16_t, hx) | ((uint32_t)__builtin_bit_cast(uint16_t, hy) << 16);
+  __device__ static uint32_t bits(float x, float& r) {
+    const bf16_t h = (bf16_t)x;
+    r = (float)h;
+    return (uint32_t)__builtin_bit_cast(uint16_t, h);
   }
 };
+
+// Probabilities for the P.V MFMA's B operand, packed in pairs.  For bf16
+// (8-bit mantissa) each p enters as a high and a low part, hi = T(p) and
+// lo = T(p - hi), and V.hi + V.lo (two MFMAs, fp32 accumulation) carry p
+// with a 16-bit mantissa: the output's mean error is then the bf16 rounding
+// of the exact result, where rounding p itself had made it 1.2-1.5 times
+// that.  f16 (11-bit mantissa) rounds p once: its error stays well inside
+// its tolerance, and the second MFMA would cost the 32-layer launch about
+// 2%.  r returns the value each product uses (hi + lo, or the rounded p),
+// for the softmax sum.
+template <typename T>
+struct PSplit {
+  static constexpr bool kTwo = std::is_same<T, bf16_t>::value;
+};
+template <typename T>
+__device__ __forceinline__ void split2(float x, float y, uint32_t& hi, uint32_t& lo, float& rx, float& ry) {
+  float hx, hy;
+  const uint32_t bx = MxOps<T>::bits(x, hx), by = MxOps<T>::bits(y, hy);
+  hi = bx | (by << 16);
+  if constexpr (PSplit<T>::kTwo) {
+    float lx, ly;
+    const uint32_t cx = MxOps<T>::bits(x - hx, lx), cy = MxOps<T>::bits(y - hy, ly);
+    lo = cx | (cy << 16);
+    rx = hx + lx;
+    ry = hy + ly;
+  } else {
+    lo = 0u;
+    rx = hx;
+    ry = hy;
+  }
+}
 
 template <typename T, int D, bool EVICT>
 __device__ __forceinline__ void process_tile_mx(const TileRegs<T, D>& r, const QFrag<T, D>& qf, MxState<D>& st,
@@ -488,8 +517,9 @@ __device__ __forceinline__ void process_tile_mx(const TileRegs<T, D>& r, const Q
 #pragma unroll
   for (int i = 0; i < 4; ++i) p[i] = dead ? 0.f : fast_exp2(s[i] - m_new);
   float pr[4];
-  const uint32_t b0 = MxOps<T>::pack2(p[0], p[1], pr[0], pr[1]);
-  const uint32_t b1 = MxOps<T>::pack2(p[2], p[3], pr[2], pr[3]);
+  uint32_t b0, b1, e0, e1;
+  split2<T>(p[0], p[1], b0, e0, pr[0], pr[1]);
+  split2<T>(p[2], p[3], b1, e1, pr[2], pr[3]);
   st.l_run = st.l_run * alpha + ((pr[0] + pr[1]) + (pr[2] + pr[3]));
   st.m_run = m_new;
   if (__any(alpha != 1.f)) {
@@ -504,6 +534,7 @@ __device__ __forceinline__ void process_tile_mx(const TileRegs<T, D>& r, const Q
     const uint32_t a0 = __builtin_amdgcn_perm(r.v[1][w], r.v[0][w], sel);
     const uint32_t a1 = __builtin_amdgcn_perm(r.v[3][w], r.v[2][w], sel);
     st.acc[j] = MxOps<T>::mma(a0, a1, b0, b1, st.acc[j]);
+    if constexpr (PSplit<T>::kTwo) st.acc[j] = MxOps<T>::mma(a0, a1, e0, e1, st.acc[j]);
   }
 }
 

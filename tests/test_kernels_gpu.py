@@ -167,6 +167,23 @@ def test_decode_split_merge_in_a_replayed_graph():
     del graph
 
 
+@pytest.mark.parametrize("S,splits", [(2431, 0), (2431, 5), (545, 0)])
+def test_decode_bf16_error_is_the_output_rounding(S, splits):
+    """bf16 P.V carries each probability as a high and a low bf16 part, so the
+    output's mean error against the fp64 oracle is the bf16 rounding of the
+    exact result itself (rounding p to bf16 alone had made it 1.3-1.5 times
+    that); V is scaled x3 so that the rounding is well above fp32 noise."""
+    B, Hq, Hk, D = 1, 32, 8, 128
+    dt = torch.bfloat16
+    q, k = _randn((B, Hq, 1, D), 60, dt), _randn((B, Hk, S, D), 61, dt)
+    v = _randn((B, Hk, S, D), 62, dt, scale=3.0)
+    sc = 1.0 / math.sqrt(D)
+    out = ops.decode_attention(q.to(DEV), k.to(DEV), v.to(DEV), sc, num_splits=splits).double().cpu().numpy()
+    want = ref.decode_attention(q, k, v, sc)
+    rounding = np.abs(torch.from_numpy(want).to(dt).double().numpy() - want).mean()
+    assert np.abs(out - want).mean() <= 1.05 * rounding
+
+
 def _word(tag, low):
     """An arrival word [tag : 32 | low : 32] as a signed int64."""
     w = (tag << 32) | low
