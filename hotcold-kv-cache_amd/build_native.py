@@ -97,8 +97,40 @@ def build(jobs=None, verbose=True):
     return out
 
 
+BIND_SRC = os.path.join(CSRC, "bind", "hc_step_bind.cpp")
+BIND_NAME = "hc_step_bind"
+
+
+def build_bind(verbose=True):
+    """The Python extension module of the decode loop's per-step call
+    (csrc/bind/hc_step_bind.cpp: host C++ against torch's headers, linked to
+    libhotcold_hip.so beside it), built into OUT_DIR next to the library.
+    Build the library first."""
+    import torch.utils.cpp_extension as ce
+
+    lib = os.path.join(OUT_DIR, LIB_NAME)
+    if not os.path.exists(lib):
+        raise RuntimeError(f"build the library ({lib}) before its binding")
+    bdir = os.path.join(OBJ_DIR, "bind")
+    os.makedirs(bdir, exist_ok=True)
+    # runpath: the library beside the installed module ($ORIGIN), and from
+    # the build directory (where load() imports it once) the same library;
+    # '$$' is ninja's escape of '$' and '\' the shell's
+    rel = os.path.relpath(OUT_DIR, bdir)
+    ce.load(name=BIND_NAME, sources=[BIND_SRC], build_directory=bdir, extra_cflags=["-O3", f"-I{INCLUDE}"],
+            extra_ldflags=[f"-L{OUT_DIR}", "-lhotcold_hip", f"-Wl,-rpath,\\$$ORIGIN:\\$$ORIGIN/{rel}"],
+            verbose=False)
+    out = os.path.join(OUT_DIR, BIND_NAME + ".so")
+    shutil.copyfile(os.path.join(bdir, BIND_NAME + ".so"), out + ".tmp")
+    os.replace(out + ".tmp", out)
+    if verbose:
+        print(f"[build] {out}")
+    return out
+
+
 if __name__ == "__main__":
     ap = argparse.ArgumentParser()
     ap.add_argument("--jobs", type=int, default=None)
     args = ap.parse_args()
     build(args.jobs)
+    build_bind()

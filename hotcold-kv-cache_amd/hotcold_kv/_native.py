@@ -277,6 +277,33 @@ def lib():
     return _lib
 
 
+_BIND_PATH = os.path.join(os.path.dirname(_LIB_PATH), "hc_step_bind.so")
+_bind = None
+_bind_tried = False
+
+
+def step_bind():
+    """The decode loop's native per-step call (csrc/bind/hc_step_bind.cpp, a
+    Python extension module beside the library), or None where it is not
+    built: the packed decode call then marshals its step from Python through
+    ctypes, into the same library and kernels."""
+    global _bind, _bind_tried
+    if _bind_tried:
+        return _bind
+    if os.path.exists(_BIND_PATH):
+        lib()                                           # the module links against the library (loads under _lock)
+    with _lock:
+        if not _bind_tried:
+            if os.path.exists(_BIND_PATH):
+                import importlib.util
+                spec = importlib.util.spec_from_file_location("hc_step_bind", _BIND_PATH)
+                mod = importlib.util.module_from_spec(spec)
+                spec.loader.exec_module(mod)
+                _bind = mod
+            _bind_tried = True
+    return _bind
+
+
 class HotColdError(RuntimeError):
     pass
 

@@ -306,6 +306,7 @@ class _AppendPlan:
         self.scaling = None
         self.lib = N.lib()
         self.fn = self.lib.hc_decode_attn_append_packed
+        self.bind = N.step_bind()
         self.addr = ctypes.addressof(a)
 
     def _bind_stream(self, stream, S):
@@ -346,9 +347,11 @@ class _AppendPlan:
         a = self.a
         if lo < 0 or S < 1 or lo + S > self.cap:
             raise RuntimeError(f"decode_append_rows: rows {lo}..{lo + S - 1} outside the buffer's {self.cap}")
-        a.q, a.q_sb, a.q_sh = self._row(q, self.qshapes, "q")
-        a.k_new, a.kn_sb, a.kn_sh = self._row(k_new, self.tshapes, "k_new")
-        a.v_new, a.vn_sb, a.vn_sh = self._row(v_new, self.tshapes, "v_new")
+        bind = self.bind
+        if bind is None:
+            a.q, a.q_sb, a.q_sh = self._row(q, self.qshapes, "q")
+            a.k_new, a.kn_sb, a.kn_sh = self._row(k_new, self.tshapes, "k_new")
+            a.v_new, a.vn_sb, a.vn_sh = self._row(v_new, self.tshapes, "v_new")
         a.S = S
         if lo != self.lo:
             a.k, a.v = self.k0 + lo * self.krow, self.v0 + lo * self.vrow
@@ -357,21 +360,26 @@ class _AppendPlan:
             if self.pos is not None:
                 self.pos_dst = self.pos0 + lo * 8
             self.lo = lo
+        # the native step (bind) checks and addresses q, the token's rows,
+        # p_new and pos_new itself, and clears p_dst / pos_dst without them
         if p_new is not None:
             if self.p is None:
                 raise RuntimeError("decode_append_rows: p_new given but the buffer keeps no pre-RoPE keys")
-            a.p_new, a.pn_sb, a.pn_sh = self._row(p_new, self.tshapes, "p_new")
+            if bind is None:
+                a.p_new, a.pn_sb, a.pn_sh = self._row(p_new, self.tshapes, "p_new")
             a.p_dst = self.p_dst
-        else:
+        elif bind is None:
             a.p_new = a.p_dst = None
         if pos_new is not None:
             if self.pos is None:
                 raise RuntimeError("decode_append_rows: pos_new given but the buffer keeps no positions")
-            if pos_new.dtype is not torch.int64 or pos_new.shape[0] != self.B or pos_new.get_device() != self.devidx:
-                raise RuntimeError("decode_append_rows: pos_new must be (B,1) int64")
-            a.pos_new, a.posn_sb = pos_new.data_ptr(), pos_new.stride(0)
+            if bind is None:
+                if pos_new.dtype is not torch.int64 or pos_new.shape[0] != self.B \
+                        or pos_new.get_device() != self.devidx:
+                    raise RuntimeError("decode_append_rows: pos_new must be (B,1) int64")
+                a.pos_new, a.posn_sb = pos_new.data_ptr(), pos_new.stride(0)
             a.pos_dst = self.pos_dst
-        else:
+        elif bind is None:
             a.pos_new = a.pos_dst = None
         if held is not None and held[2] > 0:
             if cur_pos is not None and (cur_pos.dtype is not torch.int64 or cur_pos.get_device() != self.devidx):
@@ -386,13 +394,22 @@ class _AppendPlan:
             self.held_key = None
         if scaling != self.scaling:
             a.scaling = self.scaling = scaling
+        stream = _raw_stream(self.devidx) if _raw_stream is not None else stream_handle(self.dev)
+        if stream != self.stream:
+            self._bind_stream(stream, S)
+        if bind is not None:
+            out, rc = bind.decode_append_step(self.addr, q, k_new, v_new, p_new, pos_new, keepdim, stream,
+                                              self.devidx)
+            if rc == N.HC_ERR_WORKSPACE:
+                self._bind_stream(stream, S)    # a longer buffer than the one the workspace was sized for
+                out, rc = bind.decode_append_step(self.addr, q, k_new, v_new, p_new, pos_new, keepdim, stream,
+                                                  self.devidx)
+            N.check(rc, "hc_decode_attn_append")
+            return out
         # sizes as separate arguments: 0.4 us less per call than a tuple
         out = (torch.empty(self.B, self.Hq, 1, self.D, dtype=self.dtype, device=self.dev) if keepdim
                else torch.empty(self.B, self.Hq, self.D, dtype=self.dtype, device=self.dev))
         a.out = out.data_ptr()
-        stream = _raw_stream(self.devidx) if _raw_stream is not None else stream_handle(self.dev)
-        if stream != self.stream:
-            self._bind_stream(stream, S)
         rc = self.fn(self.addr, stream)
         if rc == N.HC_ERR_WORKSPACE:
             self._bind_stream(stream, S)        # a longer buffer than the one the workspace was sized for
