@@ -673,20 +673,29 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     return t < full ? key_begin + (t * NW + wv) * 16 + 16 : (t == full && part ? tail_hi : key_end);
   };
   {
-    // The ring's first NBUF-1 tiles are issued first, so their HBM round
-    // trip overlaps everything else the prologue loads; the keep bitmap's
-    // bits are applied to them once it is complete.
+    // The ring's first tiles (NBUF-1 of them; the one tile of a depth-1
+    // ring) are issued first, so their HBM round trip overlaps everything
+    // else the prologue loads; the keep bitmap's bits are applied to them
+    // once it is complete.
+    constexpr int PRE = NBUF > 1 ? NBUF - 1 : 1;
     TileRegs<T, D> r[NBUF];
 #pragma unroll
-    for (int i = 0; i < NBUF - 1; ++i)
+    for (int i = 0; i < PRE; ++i)
       load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, tlo(i), key_begin, thi(i), col, grp, nullptr);
 
     // Fused append: the last wave of the last split attends the new token
     // (key S-1) as a one-key tile and copies its K/V (and pre-RoPE key and
     // position) into row S-1.  Only that wave loads it, in a wave-uniform
     // branch ahead of every load the ring waits on, so the other waves issue
-    // nothing for it and the ring's load counting stays exact.  The token is
-    // processed and stored before the ring, which frees its registers.
+    // nothing for it and the ring's load counting stays exact.  With a ring
+    // of depth 2 or more the token is processed and stored before the ring,
+    // which frees its registers.  With a ring of depth 1 (splits of one tile
+    // per wave) it is processed after the wave's tile: the tile, the token
+    // and q then arrive in one round trip, and the token's stores are
+    // acknowledged together with the split's partial stores.  Processed
+    // first, the token had held back the tile's load until after its
+    // stores, whose acknowledgement the tile's wait then included: two
+    // round trips for that wave of the last split.
     bool tok = false;
     if constexpr (APPEND) tok = split == a.splits - 1 && wv == NW - 1;
     TileRegs<T, D> rn;
@@ -737,11 +746,11 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       __builtin_amdgcn_s_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
 #pragma unroll
-      for (int i = 0; i < NBUF - 1; ++i) r[i].keep &= tile_keep_bits(tlo(i), key_begin, grp, sm_bits);
+      for (int i = 0; i < PRE; ++i) r[i].keep &= tile_keep_bits(tlo(i), key_begin, grp, sm_bits);
     }
     float* srow = EVICT ? a.scores + ((int64_t)b * a.Hq + hk * G + min(col, G - 1)) * a.S : nullptr;
 
-    if (APPEND && tok) {
+    auto attend_token = [&]() {
       // with EVICT the token's logit is kept like every key's
       if constexpr (MX)
         process_tile_mx<T, D, EVICT>(rn, qf, st, G, a.scale_log2, a.S - 1, a.S, col, grp, srow);
@@ -761,12 +770,16 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       const bool tq = a.pos_new != nullptr && hk == 0;
       int64_t* pdst = tq ? a.pos_dst + b * a.posd_sb + row : reinterpret_cast<int64_t*>(const_cast<T*>(kbase));
       bstore<8>(make_rsrc(pdst, tq ? 8u : 0u), lane == 0 ? 0u : kOob, pos_w);
-    }
+    };
+    if constexpr (NBUF > 1)
+      if (APPEND && tok) attend_token();
 
     // Step t issues the loads of tile t + NBUF - 1 (an empty range past the
     // wave's tiles: no memory traffic) and then processes tile t, so NBUF-1
-    // tiles stay in flight.  The loop is compiled twice, with and without
-    // the keep bitmap, so launches without one carry no bitmap test per key.
+    // tiles stay in flight.  A ring of depth 1 issued tile 0 in the prologue
+    // and loads tile t at step t > 0.  The loop is compiled twice, with and
+    // without the keep bitmap, so launches without one carry no bitmap test
+    // per key.
     auto ring = [&](auto with_bits) {
       constexpr bool WB = decltype(with_bits)::value;
       const uint32_t* bits = WB ? sm_bits : nullptr;
@@ -774,8 +787,13 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
 #pragma unroll
         for (int j = 0; j < NBUF; ++j) {
           const int t = g0 + j;
-          load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, tlo(t + NBUF - 1), key_begin,
-                          thi(t + NBUF - 1), col, grp, bits);
+          if constexpr (NBUF == 1) {
+            if (t > 0)
+              load_tile<T, D>(r[0], krs, vrs, k_rowb, v_rowb, tlo(t), key_begin, thi(t), col, grp, bits);
+          } else {
+            load_tile<T, D>(r[(j + NBUF - 1) % NBUF], krs, vrs, k_rowb, v_rowb, tlo(t + NBUF - 1), key_begin,
+                            thi(t + NBUF - 1), col, grp, bits);
+          }
           if (t < nt) {
             if constexpr (MX)
               process_tile_mx<T, D, EVICT>(r[j], qf, st, G, a.scale_log2, tlo(t), thi(t), col, grp, srow);
@@ -789,6 +807,8 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       ring(std::true_type{});
     else
       ring(std::false_type{});
+    if constexpr (NBUF == 1)
+      if (APPEND && tok) attend_token();
   }
 
   // ---- reduce the four row groups of the wave (they share m_run) ----
