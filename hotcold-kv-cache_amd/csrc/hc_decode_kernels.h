@@ -39,8 +39,8 @@
 //     counter and device-coherent loads issued together; launches with many
 //     workgroups merge them in a second, one-pass kernel instead;
 //   * the fused append's token is loaded, attended and stored by the one
-//     wave that owns it, before the ring, so no other wave spends load slots
-//     or registers on it.
+//     wave that owns it, so no other wave spends load slots or registers on
+//     it.
 #pragma once
 #include "hc_common.h"
 #include <stddef.h>
@@ -51,9 +51,11 @@
 namespace hc {
 
 struct DecodeArgs {
-  // Fields the kernel's prologue reads come first: they fit the first 128
-  // bytes, two scalar loads issued together, so the first K/V loads wait on
-  // one round trip to the argument memory.
+  // Bytes 0-127 (one 128-byte line of the argument memory): what the first
+  // K/V tile's and q's loads need, so both leave after one batch of scalar
+  // loads.  Bytes 128-255: the rest of the prologue's fields (the fused
+  // append's token rows, the keep bitmap's mask and held length), one more
+  // line.
   const void* q;
   int64_t q_sb, q_sh;
   const void* k;
@@ -67,33 +69,33 @@ struct DecodeArgs {
   float scale_log2;
   int splits, S, Hq;
   int B, Hk;
-  const uint8_t* mask;
-  int64_t mask_sb;
-  const int64_t* held_pos;
-  int64_t hp_sb, hp_sh;
-  const uint8_t* held_valid;
-  int64_t hv_sb, hv_sh;
-  const int64_t* cur_pos;
-  int64_t held_len;
-  void* out;
-  int64_t o_sb, o_sh;
-  float* part;         // [units][splits][G*D + 2*G] split partials (splits > 1)
-  float* scores;       // optional [B][Hq][S] log2-domain logits (eviction score)
-  float* ml;           // optional [B][Hq][2] final (max, sum)
   // Fused append (hc_decode_attn_append): the token at row S-1 comes from
   // k_new / v_new ([B][Hk][D]); the last split's workgroup attends it and
   // writes it (and optionally its pre-RoPE key and position) into row S-1.
-  // Last in the struct: only the append kernels read these.
   const void* k_new;
   int64_t kn_sb, kn_sh;
   const void* v_new;
   int64_t vn_sb, vn_sh;
   const void* p_new;
   int64_t pn_sb, pn_sh;
-  void* p_dst;
-  int64_t pd_sb, pd_sh, pd_ss;
   const int64_t* pos_new;
   int64_t posn_sb;
+  const uint8_t* mask;
+  int64_t mask_sb;
+  int64_t held_len;
+  const int64_t* cur_pos;
+  // Read after the first tile's loads have left.
+  const int64_t* held_pos;
+  int64_t hp_sb, hp_sh;
+  const uint8_t* held_valid;
+  int64_t hv_sb, hv_sh;
+  void* out;
+  int64_t o_sb, o_sh;
+  float* part;         // [units][splits][G*D + 2*G] split partials (splits > 1)
+  float* scores;       // optional [B][Hq][S] log2-domain logits (eviction score)
+  float* ml;           // optional [B][Hq][2] final (max, sum)
+  void* p_dst;         // fused append: the pre-RoPE key's and position's destinations
+  int64_t pd_sb, pd_sh, pd_ss;
   int64_t* pos_dst;
   int64_t posd_sb;
   // In-kernel merge of the split partials (splits > 1): one arrival word
@@ -104,7 +106,9 @@ struct DecodeArgs {
   unsigned long long* counters;
   uint32_t epoch, prev_epoch;
 };
-static_assert(offsetof(DecodeArgs, Hq) + sizeof(int) <= 128, "prologue fields must fit the first 128 bytes");
+static_assert(offsetof(DecodeArgs, Hq) + sizeof(int) <= 128, "the first loads' fields must fit bytes 0-127");
+static_assert(offsetof(DecodeArgs, B) == 128 && offsetof(DecodeArgs, cur_pos) + sizeof(void*) <= 256,
+              "the prologue's other fields must fit bytes 128-255");
 
 // Keys of one split when the keep bitmap is needed (mask or held slot).
 constexpr int kMaxBitmapKeys = 16384;
@@ -683,6 +687,13 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     for (int i = 0; i < PRE; ++i)
       load_tile<T, D>(r[i], krs, vrs, k_rowb, v_rowb, tlo(i), key_begin, thi(i), col, grp, nullptr);
 
+    // q next: its fields share the tile's first argument loads, so its
+    // loads leave in the same round trip (placed after the token's, they
+    // had waited for a second batch of argument loads).
+    QFrag<T, D> qf;
+    const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
+    qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
+
     // Fused append: the last wave of the last split attends the new token
     // (key S-1) as a one-key tile and copies its K/V (and pre-RoPE key and
     // position) into row S-1.  Only that wave loads it, in a wave-uniform
@@ -718,10 +729,6 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       const int64_t* psrc = tq ? a.pos_new + b * a.posn_sb : reinterpret_cast<const int64_t*>(kbase);
       bload<8>(make_rsrc(psrc, tq ? 8u : 0u), lane == 0 ? 0u : kOob, pos_w);
     }
-
-    QFrag<T, D> qf;
-    const T* q0 = reinterpret_cast<const T*>(a.q) + b * a.q_sb + (int64_t)(hk * G) * a.q_sh;
-    qf.load(make_rsrc(q0, a.q_bytes), (uint32_t)(a.q_sh * (int64_t)sizeof(T)), col, grp, G);
 
     // Keep bitmap of the split's keys (attention mask and held-slot test
     // valid & pos <= cur), one key per thread, packed by wave ballots.
