@@ -740,11 +740,20 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
       for (int base = 0; base < nkeys; base += 64 * NW) {
         const int rel = base + (int)threadIdx.x;
         const int key = key_begin + rel;
-        bool kp = rel < nkeys;
-        if (kp && mrow) kp = mrow[key] != 0;
-        if (kp && key < a.held_len)
-          kp = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key] != 0 &&
-               a.held_pos[b * a.hp_sb + hk * a.hp_sh + key] <= cur;
+        const bool in = rel < nkeys;
+        const bool held = in && key < a.held_len;
+        // The mask byte and the held slot's valid byte and position are
+        // each loaded only where they are read, and all of them before any
+        // is tested: one round trip.  (Tested as loaded, the position's load
+        // had waited for the valid byte's.)
+        uint32_t mv = 1, hvv = 1;
+        int64_t hpv = 0;
+        if (in && mrow) mv = mrow[key];
+        if (held) {
+          hvv = a.held_valid[b * a.hv_sb + hk * a.hv_sh + key];
+          hpv = a.held_pos[b * a.hp_sb + hk * a.hp_sh + key];
+        }
+        const bool kp = in && mv != 0 && (!held || (hvv != 0 && hpv <= cur));
         const unsigned long long m = __ballot(kp);
         if (lane < 2) sm_bits[((base + 64 * wave) >> 5) + lane] = lane ? (uint32_t)(m >> 32) : (uint32_t)m;
       }
