@@ -484,7 +484,7 @@ struct KvOut {
 // Copy the rows of hits[0..m) (logical indices of store s, rank order) into
 // output row (b, h) of a retrieval: kpre/v [B][H][R][D] (one head, or every
 // head with a head-mean vector) in out.dtype, pos/valid [B][VH][R].  The
-// caller holds the store's read lock and has zero-filled the outputs.
+// caller holds the store's read lock; zero_tail fills rows [m, R).
 void emit_hits(const ColdStore* s, int64_t b, int64_t h, int per_head, int64_t R, const int64_t* hits, int64_t m,
                const KvOut& out, int64_t* pos_out, uint8_t* valid_out) {
   const int64_t H = s->H, D = s->D, VH = per_head ? H : 1;
@@ -500,6 +500,24 @@ void emit_hits(const ColdStore* s, int64_t b, int64_t h, int per_head, int64_t R
     pos_out[(b * VH + h) * R + j] = s->pos[p];
     valid_out[(b * VH + h) * R + j] = 1;
   }
+}
+
+// Zero rows [from, R) of output row (b, h), the rows emit_hits leaves past
+// the hits.  Each task zeroes only its own rows, on its own thread: zeroing
+// all of the outputs up front was a single-threaded pass over as many bytes
+// as the copies write (8 MB per search at batch 16, 8 KV heads, 128 rows).
+void zero_tail(int64_t b, int64_t h, int per_head, int64_t H, int64_t R, int64_t D, int64_t from, const KvOut& out,
+               int64_t* pos_out, uint8_t* valid_out) {
+  if (from >= R) return;
+  const int64_t VH = per_head ? H : 1;
+  const int64_t h0 = per_head ? h : 0, h1 = per_head ? h + 1 : H;
+  const size_t bytes = (size_t)((R - from) * D * kv_elem_bytes(out.dtype));
+  for (int64_t hh = h0; hh < h1; ++hh) {
+    memset(out.row(out.k, (b * H + hh) * R + from, D), 0, bytes);
+    memset(out.row(out.v, (b * H + hh) * R + from, D), 0, bytes);
+  }
+  memset(pos_out + (b * VH + h) * R + from, 0, sizeof(int64_t) * (size_t)(R - from));
+  memset(valid_out + (b * VH + h) * R + from, 0, (size_t)(R - from));
 }
 
 // Rows of the caller's table (one per position) at the retrieved positions of
@@ -537,11 +555,8 @@ int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, 
   }
   for (int64_t b = 0; b < B; ++b) as_store(stores[b])->materialize_vecs(nthreads);
   const int64_t VH = per_head ? H : 1;
-  // outputs: kpre/v [B][H][R][D]; pos/valid [B][R] or [B][H][R]; zero-filled
-  memset(kpre_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
-  memset(v_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
-  memset(pos_out, 0, sizeof(int64_t) * B * VH * R);
-  memset(valid_out, 0, (size_t)(B * VH * R));
+  // outputs: kpre/v [B][H][R][D]; pos/valid [B][R] or [B][H][R]; rows past
+  // the hits zero-filled
   std::atomic<int64_t> missing{0};
   const int64_t tasks = B * VH;
   parallel_for(tasks, threads_for(nthreads, tasks), [&](int64_t task) {
@@ -573,6 +588,7 @@ int retrieve_impl(void* const* stores, int64_t B, const float* q, int64_t q_sb, 
         emit_hits(s, b, h, per_head, R, hits.data(), m, out, pos_out, valid_out);
       }
     }
+    zero_tail(b, h, per_head, H, R, D, m, out, pos_out, valid_out);
     if (tab) emit_tab(b, h, VH, R, pos_out, tab, tab_rows, tab_row_bytes, tab_out, missing);
   });
   if (tab_missing) *tab_missing = missing.load();
@@ -600,10 +616,6 @@ int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const i
       return set_error(HC_ERR_INVALID, "cold_gather: store %lld does not match", (long long)b);
   }
   const int64_t VH = per_head ? H : 1;
-  memset(kpre_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
-  memset(v_out, 0, (size_t)(kv_elem_bytes(kv_dtype) * B * H * R * D));
-  memset(pos_out, 0, sizeof(int64_t) * B * VH * R);
-  memset(valid_out, 0, (size_t)(B * VH * R));
   std::atomic<int64_t> missing{0};
   std::atomic<int> bad{0};
   const int64_t tasks = B * VH;
@@ -617,7 +629,12 @@ int gather_impl(void* const* stores, int64_t B, int per_head, int64_t R, const i
       while (m < R && hs[m] >= 0) ++m;
       for (int64_t j = 0; j < m; ++j)
         if (hs[j] >= s->size) bad.store(1);
-      if (!bad.load()) emit_hits(s, b, h, per_head, R, hs, m, out, pos_out, valid_out);
+      int64_t filled = 0;
+      if (!bad.load()) {
+        emit_hits(s, b, h, per_head, R, hs, m, out, pos_out, valid_out);
+        filled = m;
+      }
+      zero_tail(b, h, per_head, H, R, D, filled, out, pos_out, valid_out);
     }
     if (tab) emit_tab(b, h, VH, R, pos_out, tab, tab_rows, tab_row_bytes, tab_out, missing);
   });

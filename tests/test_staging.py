@@ -623,8 +623,10 @@ def test_gathering_given_hits_equals_the_native_retrieval(per_head):
     tab = rng.integers(0, 255, size=(400, 12), dtype=np.uint8)
 
     def outputs():
-        return (np.zeros((B, H, R, Dd), np.float32), np.zeros((B, H, R, Dd), np.float32),
-                np.zeros((B, VH, R), np.int64), np.zeros((B, VH, R), np.uint8), np.zeros((B, VH, R, 12), np.uint8))
+        # garbage, as reused staging buffers hold: every row must be written
+        return (np.full((B, H, R, Dd), 7.0, np.float32), np.full((B, H, R, Dd), -3.0, np.float32),
+                np.full((B, VH, R), 123, np.int64), np.full((B, VH, R), 9, np.uint8),
+                np.full((B, VH, R, 12), 77, np.uint8))
 
     want, got = outputs(), outputs()
     miss_w, miss_g = ctypes.c_int64(), ctypes.c_int64()
@@ -646,6 +648,17 @@ def test_gathering_given_hits_equals_the_native_retrieval(per_head):
     for a, b_ in zip(want, got):
         assert np.array_equal(a, b_)
     assert miss_w.value == miss_g.value
+    # rows past the hits: zero keys, values and positions, invalid (store 1
+    # holds 5 tokens, fewer than R)
+    for b in range(B):
+        for h in range(VH):
+            m = int((hits[b, h] >= 0).sum())
+            assert got[3][b, h, :m].all() and not got[3][b, h, m:].any()
+            assert (got[2][b, h, m:] == 0).all()
+            heads = [h] if per_head else range(H)
+            for hh in heads:
+                assert not got[0][b, hh, m:].any() and not got[1][b, hh, m:].any()
+    assert int((hits[1] >= 0).sum(axis=-1).min()) == 5
     # a hit beyond a store's tokens is refused
     bad = hits.copy()
     bad[1, 0, 0] = 40
