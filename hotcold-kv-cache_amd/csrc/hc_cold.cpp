@@ -464,8 +464,21 @@ void convert_row(const float* src, void* dst, int64_t n, int dtype) {
     for (; i < n; ++i)
       o[i] = (uint16_t)_mm_extract_epi16(_mm_cvtps_ph(_mm_set_ss(src[i]), _MM_FROUND_TO_NEAREST_INT), 0);
   } else {
+    // bf16_bits eight at a time (AVX2): equal to it on every fp32 bit pattern
     uint16_t* o = static_cast<uint16_t*>(dst);
-    for (int64_t i = 0; i < n; ++i) o[i] = bf16_bits(src[i]);
+    const __m256i one = _mm256_set1_epi32(1), half = _mm256_set1_epi32(0x7fff), quiet = _mm256_set1_epi32(0x40);
+    const __m256i absm = _mm256_set1_epi32(0x7fffffff), inf = _mm256_set1_epi32(0x7f800000);
+    int64_t i = 0;
+    for (; i + 8 <= n; i += 8) {
+      const __m256i u = _mm256_castps_si256(_mm256_loadu_ps(src + i));
+      const __m256i hi = _mm256_srli_epi32(u, 16);
+      const __m256i rnd = _mm256_srli_epi32(_mm256_add_epi32(u, _mm256_add_epi32(half, _mm256_and_si256(hi, one))), 16);
+      const __m256i nan = _mm256_cmpgt_epi32(_mm256_and_si256(u, absm), inf);
+      const __m256i r = _mm256_blendv_epi8(rnd, _mm256_or_si256(hi, quiet), nan);
+      const __m256i pk = _mm256_permute4x64_epi64(_mm256_packus_epi32(r, r), 0xD8);
+      _mm_storeu_si128(reinterpret_cast<__m128i*>(o + i), _mm256_castsi256_si128(pk));
+    }
+    for (; i < n; ++i) o[i] = bf16_bits(src[i]);
   }
 }
 
