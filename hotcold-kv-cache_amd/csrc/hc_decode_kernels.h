@@ -701,12 +701,11 @@ __global__ __launch_bounds__(64 * NW, MINW) void decode_attn_kernel(DecodeArgs a
     // nothing for it and the ring's load counting stays exact.  With a ring
     // of depth 2 or more the token is processed and stored before the ring,
     // which frees its registers.  With a ring of depth 1 (splits of one tile
-    // per wave) it is processed after the wave's tile: the tile, the token
-    // and q then arrive in one round trip, and the token's stores are
-    // acknowledged together with the split's partial stores.  Processed
-    // first, the token had held back the tile's load until after its
-    // stores, whose acknowledgement the tile's wait then included: two
-    // round trips for that wave of the last split.
+    // per wave) it is processed after the wave's tile, whose loads (and q's)
+    // leave first, and the token's stores are acknowledged together with the
+    // split's partial stores.  Processed first, the token had held back the
+    // tile's load until after its stores, whose acknowledgement the tile's
+    // wait then included: two round trips for that wave of the last split.
     bool tok = false;
     if constexpr (APPEND) tok = split == a.splits - 1 && wv == NW - 1;
     TileRegs<T, D> rn;
