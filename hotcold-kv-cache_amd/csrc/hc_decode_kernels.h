@@ -996,9 +996,13 @@ struct DecodeCfg {
 constexpr DecodeCfg decode_cfg(int es, int D, int gm) {
   int nbuf = 2, minw = 1;
   if (es == 2) {
-    // MFMA P.V: the accumulators do not grow with the group.  One tile in
-    // flight per wave measured fastest (deeper rings add VGPRs, no speed).
-    if (D <= 128) { nbuf = 2; minw = 2; }
+    // MFMA P.V: the accumulators do not grow with the group.  A ring of
+    // depth 1 (each wave's next tile loaded when its last is done; the
+    // workgroup's other waves overlap the loads), with the first tile issued
+    // ahead of q and the token, measured fastest at every launch shape: the
+    // 32-layer 8k launch 15.3 against 15.9 us with depth 2, and 0.6-3% at
+    // the 16k, 32k x 16 and 64k x 4 launches.
+    if (D <= 128) { nbuf = 1; minw = 2; }
   } else if (D <= 32) {
     nbuf = 4; minw = 2;
   } else if (D == 64) {
@@ -1030,9 +1034,8 @@ static void launch_nw(const DecodeArgs& a, int nw, hipStream_t st) {
   constexpr DecodeCfg c = decode_cfg((int)sizeof(T), D, GM);
   (void)nw;  // equals c.nw: the host picked the shape for it
   // Splits of at most one tile per wave (latency-bound launches of a few
-  // units, e.g. one layer at batch 1) run with a ring of depth 1: nothing
-  // follows the tile, and the smaller kernel measured 0.6-0.8 us faster per
-  // launch (9.5 against 10.1 us per f16 layer at 544 keys, 8 KV heads).
+  // units, e.g. one layer at batch 1) run with a ring of depth 1 at every
+  // element type: nothing follows the tile.
   if constexpr (c.nbuf > 1) {
     if (a.keys_per_split <= 16 * c.nw) {
       launch_decode<T, D, GM, c.nw, 1, c.minw>(a, st);
