@@ -44,6 +44,10 @@ DECODE_CASES = [
     (1, 64, 8, 300, 128, torch.float16),    # group of 8
     (1, 8, 1, 1000, 256, torch.bfloat16),   # one KV head, wide head_dim
     (1, 32, 2, 333, 128, torch.float16),    # group of 16
+    # several 16-key tiles per wave at the smaller head dims
+    (2, 16, 4, 3000, 64, torch.float16),
+    (1, 8, 2, 2600, 32, torch.bfloat16),
+    (1, 8, 2, 4100, 16, torch.float16),
 ]
 
 
@@ -327,6 +331,7 @@ APPEND_CASES = [
     (3, 16, 4, 8, 0, 64, torch.float16, 0),         # empty cache: the new token alone
     (1, 64, 8, 300, 250, 128, torch.float16, 0),    # group of 8
     (1, 8, 1, 1000, 900, 256, torch.bfloat16, 0),   # one KV head, wide head_dim
+    (2, 16, 4, 3100, 3000, 64, torch.bfloat16, 0),  # several tiles per wave, head_dim 64
 ]
 
 
