@@ -7,7 +7,6 @@ reductions, pool1d, gather_scores) are plain tensor ops that the kernels
 fuse; they are kept for API compatibility.
 """
 
-import torch
 import torch.nn.functional as F
 
 from .. import ops

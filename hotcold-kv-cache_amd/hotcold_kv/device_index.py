@@ -16,8 +16,6 @@ oldest), so physical slots agree and a hit's logical index addresses the host
 store's row.
 """
 
-import ctypes
-
 import numpy as np
 import torch
 

@@ -768,8 +768,6 @@ def device_tables(*lists, device=None):
     return out
 
 
-
-
 def _same_layout(tensors, what):
     t0 = tensors[0]
     for t in tensors[1:]:

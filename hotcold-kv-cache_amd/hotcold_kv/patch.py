@@ -25,7 +25,7 @@ from transformers.models.llama import modeling_llama
 
 from . import ops
 from .cache import HotColdLayer
-from .datatypes import _canon_br_2d, _canon_kv_4d
+from .datatypes import _canon_kv_4d
 
 ACTIVE_KVCTRL = None
 ACTIVE_ROTARY_EMB = None  # model.model.rotary_emb
