@@ -257,7 +257,9 @@ def keep_counts(S, window_size, budget):
 def keep_index(scores, window_size, budget, return_evicted=False):
     """scoring.py:110-132 with the deterministic tie rule: the keep_prefix
     prefix positions of highest score, ties to the lower index (a stable sort
-    on -score), sorted ascending, then arange(prefix, S)."""
+    on -score), sorted ascending, then arange(prefix, S).  NaN ranks above
+    every number, +inf included, as in torch.topk; NaNs tie with each other,
+    and -0 with +0."""
     sc = scores.detach().cpu().float().numpy()
     squeeze = sc.ndim == 2
     if squeeze:
@@ -270,8 +272,9 @@ def keep_index(scores, window_size, budget, return_evicted=False):
     for b in range(B):
         for h in range(H):
             pre = sc[b, h, :prefix].astype(np.float64)
-            key = np.where(np.isnan(pre), -np.inf, -pre)  # NaN ranks highest, like torch.topk
-            order = np.argsort(key, kind="stable")
+            nan = np.isnan(pre)
+            # stable: NaN first, then descending value (lexsort's last key is the primary)
+            order = np.lexsort((np.where(nan, 0.0, -pre), ~nan))
             top = np.sort(order[:kp])
             keep[b, h, :kp] = top
             keep[b, h, kp:] = recent

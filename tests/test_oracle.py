@@ -152,15 +152,21 @@ def test_rawsum_scores_closed_form():
 # ---------------------------------------------------------------------------
 # keep_index
 # ---------------------------------------------------------------------------
+def _rank(x):
+    # torch.topk's order: NaN above every number; NaNs equal to each other
+    return (1, 0.0) if math.isnan(x) else (0, x)
+
+
 def _brute_keep(vals, window, budget):
     S = len(vals)
     win = min(window, S)
     prefix = S - win
     kp = max(0, min(budget - win, prefix))
+    r = [_rank(x) for x in vals]
     best = None
     for comb in itertools.combinations(range(prefix), kp):
         chosen = set(comb)
-        ok = all(vals[i] > vals[j] or (vals[i] == vals[j] and i < j)
+        ok = all(r[i] > r[j] or (r[i] == r[j] and i < j)
                  for i in chosen for j in range(prefix) if j not in chosen)
         if ok:
             assert best is None, "selection must be unique"
@@ -175,6 +181,34 @@ def test_keep_index_brute_force(seed):
     vals = (torch.randint(0, 4, (1, 1, S), generator=g).float() / 2)  # many ties
     got = ref.keep_index(vals, window, budget)[0, 0].tolist()
     assert got == _brute_keep(vals[0, 0].tolist(), window, budget)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_keep_index_brute_force_special_values(seed):
+    # NaN, +-inf and +-0 among ties: NaN ranks above +inf, -0 ties with +0
+    g = torch.Generator().manual_seed(100 + seed)
+    S, window, budget = 11, 2, 6
+    pool = torch.tensor([float("nan"), float("inf"), -float("inf"), 0.0, -0.0, 1.0])
+    vals = pool[torch.randint(0, len(pool), (1, 1, S), generator=g)]
+    got = ref.keep_index(vals, window, budget)[0, 0].tolist()
+    assert got == _brute_keep(vals[0, 0].tolist(), window, budget)
+    # a keep boundary inside the NaN / +inf group
+    row = [float("inf"), float("nan"), float("inf"), float("nan"), 0.0, -0.0, 1.0, 0.5]
+    for budget in range(1, 7):
+        got = ref.keep_index(torch.tensor([[row]]), 2, budget)[0, 0].tolist()
+        assert got == _brute_keep(row, 2, budget), budget
+
+
+def test_keep_index_nan_above_inf_like_torch_topk():
+    # one NaN and one +inf among distinct values: a unique selection, which
+    # torch.topk makes too (NaN first)
+    s = _randn((1, 2, 300), 13)
+    s[0, 0, 200], s[0, 0, 17] = float("inf"), float("nan")
+    s[0, 1, 5], s[0, 1, 250] = float("inf"), float("nan")
+    for budget in (1, 2, 3, 40):
+        got = ref.keep_index(s, 8, budget + 8)
+        assert torch.equal(got, ref.keep_index_torch(s, 8, budget + 8)), budget
+    assert ref.keep_index(s, 8, 9)[0, 0].tolist()[0] == 17
 
 
 def test_keep_index_reference_invariants():
