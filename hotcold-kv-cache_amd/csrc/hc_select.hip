@@ -214,6 +214,194 @@ __global__ __launch_bounds__(kTopkThreads) void topk_keep_kernel(const float* __
   for (int j = threadIdx.x; j < window; j += kTopkThreads) out[keep_prefix + j] = prefix + j;
 }
 
+// The same selection with each (batch, head) row spread over chunks of
+// kTopkChunk keys, for grids of few long rows (one workgroup per row would
+// leave most CUs idle, each scanning its whole row several times).  A chain
+// of launches on one stream, whose boundaries order the steps:
+//   topk_init   per row: zero the histogram, state = (0, 0, keep_prefix)
+//   3 x topk_hist   per chunk: LDS histogram of the pass's digit over the
+//                   keys that match the row's prefix, added to the row's
+//                   global histogram
+//       topk_digit  per row: the digit of the pass (find_digit), folded into
+//                   the row's prefix; the histogram is left zeroed
+//   topk_count  per chunk: keys above the threshold and equal to it
+//   topk_emit   per chunk: the kept and evicted indices of the chunk, at the
+//               offsets the earlier chunks' counts give
+// The threshold key, the number of ties kept and every output position are
+// those of topk_keep_kernel: the ties kept are still the lowest-index ones.
+constexpr int kTopkChunk = kTopkThreads * kTopkU;  // keys per workgroup
+constexpr int kTopkState = 4;                      // (prefix bits, prefix mask, keys still to take, 0)
+
+__device__ __forceinline__ int pass_shift(int pass) { return pass == 0 ? 21 : pass == 1 ? 10 : 0; }
+__device__ __forceinline__ uint32_t pass_mask(int pass) { return pass == 2 ? 1023u : 2047u; }
+
+__global__ __launch_bounds__(256) void topk_init_kernel(int H, uint32_t keep_prefix, uint32_t* __restrict__ ghist,
+                                                        uint32_t* __restrict__ state) {
+  const int64_t row = (int64_t)blockIdx.y * H + blockIdx.x;
+  for (int i = threadIdx.x; i < kDigitBins; i += 256) ghist[row * kDigitBins + i] = 0;
+  if (threadIdx.x < kTopkState) state[row * kTopkState + threadIdx.x] = threadIdx.x == 2 ? keep_prefix : 0u;
+}
+
+// The order keys of chunk c of a row: kTopkU per thread, loaded together
+// (indices clamped into [k0, k1); the lanes past k1 are masked by the caller).
+__device__ __forceinline__ void chunk_keys(const float* sc, int k0, int k1, uint32_t (&ks)[kTopkU]) {
+  float v[kTopkU];
+#pragma unroll
+  for (int u = 0; u < kTopkU; ++u) v[u] = sc[min(k0 + u * kTopkThreads + (int)threadIdx.x, k1 - 1)];
+#pragma unroll
+  for (int u = 0; u < kTopkU; ++u) ks[u] = order_key(v[u]);
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_hist_kernel(const float* __restrict__ scores, int64_t s_sb,
+                                                                 int64_t s_sh, int H, int prefix, int pass,
+                                                                 uint32_t* __restrict__ ghist,
+                                                                 const uint32_t* __restrict__ state) {
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t row = (int64_t)b * H + h;
+  const float* sc = scores + b * s_sb + h * s_sh;
+  const int k0 = c * kTopkChunk, k1 = min(prefix, k0 + kTopkChunk);
+  const int shift = pass_shift(pass);
+  const uint32_t dmask = pass_mask(pass);
+  const uint32_t pbits = state[row * kTopkState + 0], pmask = state[row * kTopkState + 1];
+  __shared__ uint32_t hist[kDigitBins];
+  for (int i = threadIdx.x; i < kDigitBins; i += kTopkThreads) hist[i] = 0;
+  __syncthreads();
+  uint32_t ks[kTopkU];
+  chunk_keys(sc, k0, k1, ks);
+#pragma unroll
+  for (int u = 0; u < kTopkU; ++u) {
+    const int i = k0 + u * kTopkThreads + (int)threadIdx.x;
+    hist_add(hist, (ks[u] >> shift) & dmask, i < k1 && (ks[u] & pmask) == pbits);
+  }
+  __syncthreads();
+  for (int i = threadIdx.x; i < kDigitBins; i += kTopkThreads) {
+    const uint32_t n = hist[i];
+    if (n) atomicAdd(&ghist[row * kDigitBins + i], n);
+  }
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_digit_kernel(int H, int pass, uint32_t* __restrict__ ghist,
+                                                                  uint32_t* __restrict__ state) {
+  const int64_t row = (int64_t)blockIdx.y * H + blockIdx.x;
+  __shared__ uint32_t hist[kDigitBins];
+  __shared__ uint32_t sm_scan[kTopkWaves];
+  __shared__ uint32_t sm_digit, sm_krem;
+  uint32_t* g = ghist + row * kDigitBins;
+  for (int i = threadIdx.x; i < kDigitBins; i += kTopkThreads) {
+    hist[i] = g[i];
+    g[i] = 0;
+  }
+  const uint32_t krem = state[row * kTopkState + 2];
+  __syncthreads();
+  find_digit(hist, krem, sm_scan, &sm_digit, &sm_krem);
+  if (threadIdx.x == 0) {
+    const int shift = pass_shift(pass);
+    state[row * kTopkState + 0] |= sm_digit << shift;
+    state[row * kTopkState + 1] |= pass_mask(pass) << shift;
+    state[row * kTopkState + 2] = sm_krem;
+  }
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_count_kernel(const float* __restrict__ scores, int64_t s_sb,
+                                                                  int64_t s_sh, int H, int prefix, int nchunk,
+                                                                  const uint32_t* __restrict__ state,
+                                                                  int* __restrict__ counts) {
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t row = (int64_t)b * H + h;
+  const float* sc = scores + b * s_sb + h * s_sh;
+  const int k0 = c * kTopkChunk, k1 = min(prefix, k0 + kTopkChunk);
+  const uint32_t tkey = state[row * kTopkState + 0];
+  __shared__ int sm_wave[kTopkWaves];
+  uint32_t ks[kTopkU];
+  chunk_keys(sc, k0, k1, ks);
+  int n_gt = 0, n_eq = 0;
+#pragma unroll
+  for (int u = 0; u < kTopkU; ++u) {
+    if (k0 + u * kTopkThreads + (int)threadIdx.x < k1) {
+      n_gt += ks[u] > tkey;
+      n_eq += ks[u] == tkey;
+    }
+  }
+  int tot_gt, tot_eq;
+  block_excl_scan(n_gt, sm_wave, &tot_gt);
+  block_excl_scan(n_eq, sm_wave, &tot_eq);
+  if (threadIdx.x == 0) {
+    counts[(row * nchunk + c) * 2 + 0] = tot_gt;
+    counts[(row * nchunk + c) * 2 + 1] = tot_eq;
+  }
+}
+
+__global__ __launch_bounds__(kTopkThreads) void topk_emit_kernel(const float* __restrict__ scores, int64_t s_sb,
+                                                                 int64_t s_sh, int H, int prefix, int nchunk,
+                                                                 int keep_prefix, int window,
+                                                                 const uint32_t* __restrict__ state,
+                                                                 const int* __restrict__ counts,
+                                                                 int64_t* __restrict__ keep,
+                                                                 int64_t* __restrict__ evicted) {
+  const int c = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int64_t row = (int64_t)b * H + h;
+  const float* sc = scores + b * s_sb + h * s_sh;
+  const int k0 = c * kTopkChunk, k1 = min(prefix, k0 + kTopkChunk);
+  const int n_keep = keep_prefix + window;
+  int64_t* out = keep + row * n_keep;
+  int64_t* ev = evicted ? evicted + row * (prefix - keep_prefix) : nullptr;
+  const uint32_t tkey = state[row * kTopkState + 0];
+  const int need_eq = (int)state[row * kTopkState + 2];
+  __shared__ int sm_wave[kTopkWaves];
+  // the earlier chunks: keys above the threshold, and ties
+  int gt_c = 0, eq_c = 0;
+  for (int cc = 0; cc < c; ++cc) {
+    gt_c += counts[(row * nchunk + cc) * 2 + 0];
+    eq_c += counts[(row * nchunk + cc) * 2 + 1];
+  }
+  // each thread owns a contiguous run of the chunk, as in topk_keep_kernel
+  const int len = k1 - k0;
+  const int run = (len + kTopkThreads - 1) / kTopkThreads;
+  const int i0 = k0 + min(len, (int)threadIdx.x * run);
+  const int i1 = k0 + min(len, (int)threadIdx.x * run + run);
+  // a run is at most kTopkU keys (a chunk is kTopkThreads * kTopkU): loaded
+  // once, for the counts and the emit (an empty run, i0 == i1 == k1, reads
+  // key k1 - 1 and uses none)
+  static_assert(kTopkChunk == kTopkThreads * kTopkU, "one load batch per run");
+  uint32_t ks[kTopkU];
+#pragma unroll
+  for (int u = 0; u < kTopkU; ++u) ks[u] = order_key(sc[min(i0 + u, i1 - 1 < i0 ? k1 - 1 : i1 - 1)]);
+  int n_gt = 0, n_eq = 0;
+#pragma unroll
+  for (int u = 0; u < kTopkU; ++u) {
+    if (i0 + u < i1) {
+      n_gt += ks[u] > tkey;
+      n_eq += ks[u] == tkey;
+    }
+  }
+  int tot;
+  // ties before this thread's run over the whole row; the ties it keeps
+  const int eq_before = eq_c + block_excl_scan(n_eq, sm_wave, &tot);
+  const int take_eq = max(0, min(need_eq - eq_before, n_eq));
+  // indices kept before the run: every key above the threshold, and
+  // min(ties before, need_eq) ties
+  const int sel_before = gt_c + min(eq_c, need_eq) + block_excl_scan(n_gt + take_eq, sm_wave, &tot);
+  int pos = sel_before;
+  int epos = i0 - sel_before;
+  int eq_seen = 0;
+#pragma unroll
+  for (int u = 0; u < kTopkU; ++u) {
+    const int j = i0 + u;
+    if (j >= i1) break;
+    bool sel = false;
+    if (ks[u] > tkey) {
+      sel = true;
+    } else if (ks[u] == tkey) {
+      sel = eq_seen < take_eq;
+      ++eq_seen;
+    }
+    if (sel) out[pos++] = j;
+    else if (ev) ev[epos++] = j;
+  }
+  if (c == 0)
+    for (int j = threadIdx.x; j < window; j += kTopkThreads) out[keep_prefix + j] = prefix + j;
+}
+
 // Row copy: thread copies one VW-byte vector of one row of each tensor.
 struct RowCopy {
   const char* src[3];
@@ -391,6 +579,83 @@ extern "C" int hc_topk_keep(int64_t B, int64_t H, int64_t S, const float* scores
                      reinterpret_cast<hipStream_t>(stream), scores, s_sb, s_sh, (int)H, (int)prefix, (int)kp,
                      (int)win, keep, evicted);
   return check_launch("topk_keep");
+}
+
+namespace {
+
+// The chunked selection pays for its chain of launches (about 35 us) where
+// one workgroup per row is slow: rows longer than the kTopkCache keys that
+// workgroup keeps in LDS (it then re-reads them from memory on every pass),
+// in grids of fewer rows than CUs.  At 64k keys x 32 rows the selection took
+// 110 us in one workgroup per row and 51 us chunked; at 32k keys x 128 rows,
+// LDS-cached, 59 us against 64.
+bool topk_chunked(int64_t rows, int64_t prefix, int64_t kp) {
+  return kp > 0 && rows < 256 && prefix > kTopkCache;
+}
+
+struct TopkWs {
+  int64_t state_off, counts_off, total;
+};
+
+TopkWs topk_ws_layout(int64_t rows, int64_t nchunk) {
+  const auto al = [](int64_t x) { return (x + 255) & ~(int64_t)255; };
+  TopkWs w;
+  w.state_off = al(rows * kDigitBins * 4);
+  w.counts_off = w.state_off + al(rows * kTopkState * 4);
+  w.total = w.counts_off + al(rows * nchunk * 2 * 4);
+  return w;
+}
+
+void topk_counts(int64_t S, int64_t window, int64_t budget, int64_t* win, int64_t* prefix, int64_t* kp) {
+  *win = window < S ? window : S;
+  *prefix = S - *win;
+  *kp = budget - *win;
+  if (*kp > *prefix) *kp = *prefix;
+  if (*kp < 0) *kp = 0;
+}
+
+}  // namespace
+
+extern "C" int64_t hc_topk_keep_workspace_size(int64_t B, int64_t H, int64_t S, int64_t window, int64_t budget) {
+  if (B <= 0 || H <= 0 || S <= 0 || window < 0 || budget < 0) return 0;
+  int64_t win, prefix, kp;
+  topk_counts(S, window, budget, &win, &prefix, &kp);
+  if (!topk_chunked(B * H, prefix, kp)) return 0;
+  return topk_ws_layout(B * H, cdiv(prefix, (int64_t)kTopkChunk)).total;
+}
+
+extern "C" int hc_topk_keep_ws(int64_t B, int64_t H, int64_t S, const float* scores, int64_t s_sb, int64_t s_sh,
+                               int64_t window, int64_t budget, int64_t* keep, int64_t* evicted, void* ws,
+                               int64_t ws_bytes, void* stream) {
+  HC_REQUIRE(B > 0 && H > 0 && S > 0, "topk: empty shape");
+  HC_REQUIRE(window >= 0 && budget >= 0, "topk: negative window/budget");
+  HC_REQUIRE(S < ((int64_t)1 << 31), "topk: S too large");
+  HC_REQUIRE(B <= 65535 && H <= 65535, "topk: grid too large");
+  HC_REQUIRE(scores && keep, "topk: null pointer");
+  int64_t win, prefix, kp;
+  topk_counts(S, window, budget, &win, &prefix, &kp);
+  if (ws == nullptr || !topk_chunked(B * H, prefix, kp))
+    return hc_topk_keep(B, H, S, scores, s_sb, s_sh, window, budget, keep, evicted, stream);
+  const int64_t nchunk = cdiv(prefix, (int64_t)kTopkChunk);
+  const TopkWs lay = topk_ws_layout(B * H, nchunk);
+  HC_REQUIRE(ws_bytes >= lay.total, "topk: workspace of %lld bytes given, %lld needed", (long long)ws_bytes,
+             (long long)lay.total);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  uint32_t* ghist = static_cast<uint32_t*>(ws);
+  uint32_t* state = reinterpret_cast<uint32_t*>(static_cast<char*>(ws) + lay.state_off);
+  int* counts = reinterpret_cast<int*>(static_cast<char*>(ws) + lay.counts_off);
+  const dim3 rows((unsigned)H, (unsigned)B), chunks((unsigned)nchunk, (unsigned)H, (unsigned)B);
+  hipLaunchKernelGGL(topk_init_kernel, rows, dim3(256), 0, st, (int)H, (uint32_t)kp, ghist, state);
+  for (int pass = 0; pass < 3; ++pass) {
+    hipLaunchKernelGGL(topk_hist_kernel, chunks, dim3(kTopkThreads), 0, st, scores, s_sb, s_sh, (int)H, (int)prefix,
+                       pass, ghist, (const uint32_t*)state);
+    hipLaunchKernelGGL(topk_digit_kernel, rows, dim3(kTopkThreads), 0, st, (int)H, pass, ghist, state);
+  }
+  hipLaunchKernelGGL(topk_count_kernel, chunks, dim3(kTopkThreads), 0, st, scores, s_sb, s_sh, (int)H,
+                     (int)prefix, (int)nchunk, (const uint32_t*)state, counts);
+  hipLaunchKernelGGL(topk_emit_kernel, chunks, dim3(kTopkThreads), 0, st, scores, s_sb, s_sh, (int)H, (int)prefix,
+                     (int)nchunk, (int)kp, (int)win, (const uint32_t*)state, (const int*)counts, keep, evicted);
+  return check_launch("topk_keep_ws");
 }
 
 extern "C" int hc_gather_rows(int64_t B, int64_t H, int64_t n, int64_t D, int64_t elem_bytes, const int64_t* idx,

@@ -143,6 +143,8 @@ SIGNATURES = {
         _vp, _i64, _vp]),
     "hc_head_mean": (_int, [_i64, _i64, _i64, _vp, _vp, _vp]),
     "hc_topk_keep": (_int, [_i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp]),
+    "hc_topk_keep_workspace_size": (_i64, [_i64, _i64, _i64, _i64, _i64]),
+    "hc_topk_keep_ws": (_int, [_i64, _i64, _i64, _vp, _i64, _i64, _i64, _i64, _vp, _vp, _vp, _i64, _vp]),
     "hc_gather_rows": (_int, [
         _i64, _i64, _i64, _i64, _i64,
         _vp, _i64, _i64, _i64, _i64,

@@ -915,9 +915,12 @@ def keep_index(scores, window_size, budget, return_evicted=False):
     window, prefix, kp = keep_counts(S, window_size, budget)
     keep = torch.empty((B, H, kp + window), dtype=torch.int64, device=scores.device)
     ev = torch.empty((B, H, prefix - kp), dtype=torch.int64, device=scores.device) if return_evicted else None
-    rc = N.lib().hc_topk_keep(B, H, S, _ptr(scores), scores.stride(0), scores.stride(1), int(window_size),
-                              int(budget), _ptr(keep), _ptr(ev), _stream_handle(scores.device))
-    N.check(rc, "hc_topk_keep")
+    # few long rows: the chunked selection, in a workspace the library sizes
+    ws_bytes = N.lib().hc_topk_keep_workspace_size(B, H, S, int(window_size), int(budget))
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=scores.device) if ws_bytes > 0 else None
+    rc = N.lib().hc_topk_keep_ws(B, H, S, _ptr(scores), scores.stride(0), scores.stride(1), int(window_size),
+                                 int(budget), _ptr(keep), _ptr(ev), _ptr(ws), ws_bytes, _stream_handle(scores.device))
+    N.check(rc, "hc_topk_keep_ws")
     if squeeze:
         keep = keep[:, 0]
         ev = ev[:, 0] if ev is not None else None

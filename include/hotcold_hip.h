@@ -368,6 +368,23 @@ int hc_topk_keep(int64_t B, int64_t H, int64_t S, const float* scores, int64_t s
                  int64_t window, int64_t budget, int64_t* keep, int64_t* evicted, void* stream);
 
 /*
+ * hc_topk_keep with a caller-provided device workspace, for the same
+ * replacement of keep_index (scoring.py:110-132) and the top-k of
+ * cache.py:47-95.  Grids of fewer than 256 (batch, head) rows whose prefix
+ * is longer than 32768 keys take a chunked selection that spreads each row
+ * over workgroups of 8192 keys (a chain of launches on `stream`); the
+ * outputs are those of hc_topk_keep, bit for bit.
+ * hc_topk_keep_workspace_size returns the workspace the call needs (0: none, the
+ * call runs hc_topk_keep).  ws == NULL also runs hc_topk_keep; a non-NULL ws
+ * of fewer bytes than needed is HC_ERR_INVALID.  The workspace needs no
+ * clearing and is in use until the stream reaches the end of the call.
+ */
+int64_t hc_topk_keep_workspace_size(int64_t B, int64_t H, int64_t S, int64_t window, int64_t budget);
+int hc_topk_keep_ws(int64_t B, int64_t H, int64_t S, const float* scores, int64_t s_sb, int64_t s_sh,
+                    int64_t window, int64_t budget, int64_t* keep, int64_t* evicted, void* ws, int64_t ws_bytes,
+                    void* stream);
+
+/*
  * Row gather into the hot buffer: dst_i[b][h][j] = src_i[b][h][idx[b][h][j]] for
  * j < n, for up to three tensors that share the index set (K, V, pre-RoPE K).
  * Replaces gather_kv (scoring.py:135-139), _compress (layer_state.py:76-77) and

@@ -614,6 +614,74 @@ def test_keep_index_special_values():
     for budget in range(1, 12):
         got = ops.keep_index(sc.to(DEV), 2, budget).cpu()
         assert torch.equal(got, ref.keep_index(sc, 2, budget)), budget
+    # NaN ranks above +inf (torch.topk's order), NaNs tie with each other
+    sc = torch.tensor([[[float("inf"), float("nan"), 1.0, float("inf"), float("nan"), -0.0, 0.0, float("nan"),
+                         -float("inf"), 2.0, 0.5, 0.25]]])
+    for budget in range(1, 12):
+        got, gev = ops.keep_index(sc.to(DEV), 2, budget, return_evicted=True)
+        want, wev = ref.keep_index(sc, 2, budget, return_evicted=True)
+        assert torch.equal(got.cpu(), want) and torch.equal(gev.cpu(), wev), budget
+
+
+def _chunk_scores(B, H, S, kind, seed):
+    g = torch.Generator().manual_seed(seed)
+    if kind == "coarse":     # many exact ties, like max-pool plateaus
+        return torch.randint(0, 50, (B, H, S), generator=g).float() / 7.0
+    if kind == "equal":
+        return torch.full((B, H, S), 1.5)
+    sc = torch.randn((B, H, S), generator=g)
+    if kind == "special":    # NaN, +-inf and +-0 sprinkled over the row
+        u = torch.rand((B, H, S), generator=g)
+        sc[u < 0.002] = float("nan")
+        sc[(u >= 0.002) & (u < 0.004)] = float("inf")
+        sc[(u >= 0.004) & (u < 0.006)] = -float("inf")
+        sc[(u >= 0.006) & (u < 0.02)] = -0.0
+        sc[(u >= 0.02) & (u < 0.03)] = 0.0
+    return sc
+
+
+# rows < 256 and prefixes longer than 32768 keys: the chunked selection
+@pytest.mark.parametrize("B,H,S,window,budget,kind", [
+    (1, 8, 32768 + 65, 64, 1024, "coarse"),      # a last chunk of one key
+    (2, 4, 40000, 64, 4096, "coarse"),            # a partial last chunk
+    (4, 8, 65536, 64, 4096, "normal"),            # the 64k x 4 layer's rows
+    (1, 1, 40000, 0, 39999, "coarse"),            # all but one key kept
+    (1, 3, 50000, 32, 40, "special"),             # few kept, NaN / inf among them
+    (3, 5, 33000, 7, 32990, "equal"),             # one tie class over the whole row
+    (2, 2, 40960, 0, 1, "special"),               # one key kept, five whole chunks
+])
+def test_keep_index_chunked_matches_oracle(B, H, S, window, budget, kind):
+    from hotcold_kv import _native as N
+    assert N.lib().hc_topk_keep_workspace_size(B, H, S, window, budget) > 0    # the chunked path runs
+    sc = _chunk_scores(B, H, S, kind, S + budget)
+    scd = sc.to(DEV)
+    got, gev = ops.keep_index(scd, window, budget, return_evicted=True)
+    want, wev = ref.keep_index(sc, window, budget, return_evicted=True)
+    assert torch.equal(got.cpu(), want)
+    assert torch.equal(gev.cpu(), wev)
+    # the one-workgroup-per-row kernel, called directly, gives the same outputs
+    one, oev = torch.empty_like(got), torch.empty_like(gev)
+    N.check(N.lib().hc_topk_keep(B, H, S, scd.data_ptr(), scd.stride(0), scd.stride(1), window, budget,
+                                 one.data_ptr(), oev.data_ptr(), ops._stream_handle(scd.device)), "hc_topk_keep")
+    assert torch.equal(one, got) and torch.equal(oev, gev)
+
+
+def test_keep_index_chunked_workspace_reuse_and_size_check():
+    from hotcold_kv import _native as N
+    B, H, S, window, budget = 2, 4, 40000, 16, 500
+    need = N.lib().hc_topk_keep_workspace_size(B, H, S, window, budget)
+    assert need > 0
+    ws = torch.full((need,), 0xA5, dtype=torch.uint8, device=DEV)    # garbage: the call needs no clearing
+    for seed in (1, 2):                                               # the same workspace twice in a row
+        sc = _chunk_scores(B, H, S, "coarse", seed).to(DEV)
+        keep = torch.empty((B, H, budget), dtype=torch.int64, device=DEV)
+        N.check(N.lib().hc_topk_keep_ws(B, H, S, sc.data_ptr(), sc.stride(0), sc.stride(1), window, budget,
+                                        keep.data_ptr(), None, ws.data_ptr(), need,
+                                        ops._stream_handle(sc.device)), "hc_topk_keep_ws")
+        assert torch.equal(keep.cpu(), ref.keep_index(sc.cpu(), window, budget))
+    rc = N.lib().hc_topk_keep_ws(B, H, S, sc.data_ptr(), sc.stride(0), sc.stride(1), window, budget,
+                                 keep.data_ptr(), None, ws.data_ptr(), need - 1, ops._stream_handle(sc.device))
+    assert rc == N.HC_ERR_INVALID
 
 
 def test_gather_shared_index_with_positions():
