@@ -209,13 +209,15 @@ class PressLayerState:
     def decode(self, q_post, k_post, v, n_rep, scaling):
         """Single-token decode: append, then attend over the compressed cache
         (one fused launch for one token)."""
-        self._settle()
-        if self.buf is None:
+        if self._deferred is not None:
+            self._deferred.flush()
+        buf = self.buf
+        if buf is None:
             raise RuntimeError("decode before prefill")
+        if self.method != "h2o" and k_post.shape[2] == 1:                   # the per-step call
+            return buf.append_attend(q_post, k_post, v, scaling, None, None, True)     # (B,Hq,1,D)
         if self.method == "h2o":
             return self._decode_h2o(q_post, k_post, v, scaling)
-        if k_post.shape[2] == 1:
-            return self.buf.append_attend(q_post, k_post, v, scaling, keepdim=True)     # (B,Hq,1,D)
         self.buf.append(k_post, v)
         out = ops.decode_attention(q_post, self.buf.keys, self.buf.values, scaling)
         return out.unsqueeze(2)  # (B,Hq,1,D)

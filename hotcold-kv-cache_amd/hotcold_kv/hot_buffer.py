@@ -142,11 +142,12 @@ class HotBuffer:
         """Append one token (k, v, pre (B,H,1,D), pos (B,1)) and attend q over
         the hot rows plus the token, in one launch.  Returns (B,Hq,D), or
         (B,Hq,1,D) with keepdim."""
-        self.ensure(self.n + 1)
-        out = ops.decode_append_rows(q, self.st, self.held, self.n + 1, k, v, scaling,
-                                     p_new=pre if self.with_pre else None, pos_new=pos if self.with_pos else None,
-                                     keepdim=keepdim)
-        self.n += 1
+        n = self.n + 1
+        if n > self.cap:
+            self.ensure(n)
+        out = ops.decode_append_rows(q, self.st, self.held, n, k, v, scaling, pre if self.with_pre else None,
+                                     pos if self.with_pos else None, None, None, keepdim)
+        self.n = n
         return out
 
     def set_from(self, k, v, pre=None, pos=None):

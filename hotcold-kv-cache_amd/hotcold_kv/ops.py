@@ -400,11 +400,12 @@ class _AppendPlan:
         if bind is not None:
             out, rc = bind.decode_append_step(self.addr, q, k_new, v_new, p_new, pos_new, keepdim, stream,
                                               self.devidx)
-            if rc == N.HC_ERR_WORKSPACE:
-                self._bind_stream(stream, S)    # a longer buffer than the one the workspace was sized for
-                out, rc = bind.decode_append_step(self.addr, q, k_new, v_new, p_new, pos_new, keepdim, stream,
-                                                  self.devidx)
-            N.check(rc, "hc_decode_attn_append")
+            if rc:                              # not HC_OK (0)
+                if rc == N.HC_ERR_WORKSPACE:
+                    self._bind_stream(stream, S)    # a longer buffer than the one the workspace was sized for
+                    out, rc = bind.decode_append_step(self.addr, q, k_new, v_new, p_new, pos_new, keepdim, stream,
+                                                      self.devidx)
+                N.check(rc, "hc_decode_attn_append")
             return out
         # sizes as separate arguments: 0.4 us less per call than a tuple
         out = (torch.empty(self.B, self.Hq, 1, self.D, dtype=self.dtype, device=self.dev) if keepdim
