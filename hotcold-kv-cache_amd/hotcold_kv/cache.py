@@ -117,15 +117,19 @@ class HotColdLayer(CacheLayerMixin):
         buf = self.buf
         if positions.shape[-1] != 1:
             raise RuntimeError("HotColdLayer.append_attend: one token per step, positions (B,1)")
-        buf.ensure(buf.n + 1)
+        n = buf.n + 1
+        if n > buf.cap:
+            buf.ensure(n)
         R = int(held[2]) if held is not None else 0
-        lo = buf.held - R
         # one-token step: positions is (B,1), so its first element is the
         # current position the held-slot mask compares against
-        out = ops.decode_append_rows(q_post, buf.st, lo, R + buf.n + 1, k_post, v, scaling, p_new=k_pre,
-                                     pos_new=positions, held=held if R else None,
-                                     cur_pos=positions if R else None, keepdim=True)
-        buf.n += 1
+        if R:
+            out = ops.decode_append_rows(q_post, buf.st, buf.held - R, R + n, k_post, v, scaling, k_pre, positions,
+                                         held, positions, True)
+        else:
+            out = ops.decode_append_rows(q_post, buf.st, buf.held, n, k_post, v, scaling, k_pre, positions, None,
+                                         None, True)
+        buf.n = n
         self.seen_tokens += 1
         return out
 

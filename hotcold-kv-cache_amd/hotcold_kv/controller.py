@@ -668,7 +668,7 @@ class KVController:
 
     # -- query pooling / retrieval -----------------------------------------------------
     def update_query_window(self, layer_idx, q_pre):
-        self.query_window[int(layer_idx)].append(q_pre.detach())
+        self.query_window[int(layer_idx)].append(q_pre.detach() if q_pre.requires_grad else q_pre)
 
     def _pooled_query_dev(self, layer_idx):
         """The pooled recent pre-RoPE query on the device, fp32: (B,D), or
