@@ -9,6 +9,8 @@
 // lowest-index ties with key == T.  Emitting in index order gives the
 // ascending sort of scoring.py:130 for free, and the result is the exact
 // "value descending, ties to the lower index" set (no nth_element ambiguity).
+// hc_topk_keep_ws makes the same selection for grids of few rows longer than
+// the LDS key cache, each row spread over chunks of 8192 keys (topk_*_kernel).
 //
 // hc_gather_rows / hc_append_rows replace gather_kv (scoring.py:135-139),
 // the gathers of cache.py:79-84 and the torch.cat appends of cache.py:145-148
