@@ -684,6 +684,38 @@ def test_keep_index_chunked_workspace_reuse_and_size_check():
     assert rc == N.HC_ERR_INVALID
 
 
+def test_keep_index_chunked_in_a_replayed_graph():
+    """The chunked selection captured in a graph and replayed over new scores:
+    its workspace, allocated at capture and never cleared by the host, is set
+    up by the chain's own first kernel on every replay (no memset node)."""
+    from hotcold_kv import _native as N
+    B, H, S, window, budget = 2, 4, 40000, 16, 500
+    assert N.lib().hc_topk_keep_workspace_size(B, H, S, window, budget) > 0
+    dev = torch.device(DEV)
+    sc = _chunk_scores(B, H, S, "coarse", 1).to(dev)
+    st = torch.cuda.Stream(dev)
+    with torch.cuda.stream(st):
+        ops.keep_index(sc, window, budget, return_evicted=True)     # outside the capture first
+    st.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        keep, ev = ops.keep_index(sc, window, budget, return_evicted=True)
+    for rep, kind in enumerate(("coarse", "special", "normal", "coarse", "equal")):
+        new = _chunk_scores(B, H, S, kind, 10 + rep)
+        with torch.cuda.stream(st):
+            sc.copy_(new.to(dev))
+        st.synchronize()
+        graph.replay()
+        st.synchronize()
+        want, wev = ref.keep_index(new, window, budget, return_evicted=True)
+        assert torch.equal(keep.cpu(), want), rep
+        assert torch.equal(ev.cpu(), wev), rep
+        with torch.cuda.stream(st):                                  # the program's own work between replays
+            ops.keep_index(sc, window, budget)
+        st.synchronize()
+    del graph
+
+
 def test_gather_shared_index_with_positions():
     B, Hk, S, D, n = 2, 8, 300, 128, 77
     dtype = torch.float16
