@@ -119,6 +119,16 @@ def test_workspace_sizes():
     assert 0 < s1 < s2
     # the fp32 window logits dominate: W*S*4 bytes per KV head
     assert s1 >= 8 * 32 * 8192 * 4
+    # the chunked top-k: only grids of fewer than 256 rows whose prefix passes
+    # the 32768 keys the one-workgroup kernel caches; per row a 2048-bin
+    # histogram, the state and two counts per 8192-key chunk, each part
+    # 256-byte aligned
+    assert lib.hc_topk_keep_workspace_size(4, 8, 65536, 64, 4096) == \
+        32 * 2048 * 4 + 512 + ((32 * 8 * 2 * 4 + 255) // 256) * 256
+    assert lib.hc_topk_keep_workspace_size(32, 8, 8192, 32, 512) == 0       # rows >= 256
+    assert lib.hc_topk_keep_workspace_size(16, 8, 32768, 64, 2048) == 0     # prefix 32704 fits the cache
+    assert lib.hc_topk_keep_workspace_size(1, 1, 40000, 0, 0) == 0          # nothing kept
+    assert lib.hc_topk_keep_workspace_size(1, 1, 32769, 0, 10) > 0
 
 
 def test_ops_refuse_host_tensors():
